@@ -1,0 +1,72 @@
+"""Float64 numpy forward of the decoder, written from the textbook definitions
+(RMSNorm, NeoX half-split RoPE, softmax attention with the interleaved GQA head
+map of attention.rs:415-428, SwiGLU).  Used by tests to pin the C oracle; it
+shares no code with it (matrix softmax instead of the oracle's online softmax)."""
+import numpy as np
+
+
+def weights(model):
+    names = {t[0]: i for i, t in enumerate(model.tensors())}
+    return {n: model.get(i).astype(np.float64) for n, i in names.items()}
+
+
+def rms(x, w, eps):
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w.reshape(-1)
+
+
+def rope(x, pos, theta):
+    # x [S, H, hd]
+    hd = x.shape[-1]
+    half = hd // 2
+    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
+    ang = pos[:, None] * inv[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], -1)
+
+
+def block(W, pre, x, cfg, pos):
+    H, nh, nkv = cfg.hidden_dim, cfg.n_heads, cfg.n_kv_heads
+    hd = H // nh
+    S = x.shape[0]
+    xn = rms(x, W[pre + "norm1.weight"], cfg.norm_eps)
+    q = (xn @ W[pre + "attn.wq.weight"].T).reshape(S, nh, hd)
+    k = (xn @ W[pre + "attn.wk.weight"].T).reshape(S, nkv, hd)
+    v = (xn @ W[pre + "attn.wv.weight"].T).reshape(S, nkv, hd)
+    q, k = rope(q, pos, cfg.rope_theta), rope(k, pos, cfg.rope_theta)
+    out = np.zeros((S, nh, hd))
+    mask = np.tril(np.ones((S, S), bool))
+    for h in range(nh):
+        kh = h % nkv
+        sc = q[:, h] @ k[:, kh].T / np.sqrt(hd)
+        sc = np.where(mask, sc, -np.inf)
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        out[:, h] = p @ v[:, kh]
+    x = x + out.reshape(S, nh * hd) @ W[pre + "attn.wo.weight"].T
+    xn = rms(x, W[pre + "norm2.weight"], cfg.norm_eps)
+    g = xn @ W[pre + "ffn.w_gate.weight"].T
+    u = xn @ W[pre + "ffn.w_up.weight"].T
+    return x + (g / (1 + np.exp(-g)) * u) @ W[pre + "ffn.w_down.weight"].T
+
+
+def forward(W, cfg, ids):
+    """Full (uncached) forward over ids; returns logits [S, V] and normed hidden [S, H]."""
+    E = W["embedding.weight"]
+    x = E[np.asarray(ids, np.int64)]
+    pos = np.arange(len(ids), dtype=np.float64)
+    for l in range(cfg.n_layers):
+        x = block(W, f"blocks.{l}.", x, cfg, pos)
+    hn = rms(x, W["final_norm.weight"], cfg.norm_eps)
+    return hn @ E.T, hn
+
+
+def mtp_head(W, cfg, head, anchor, ids):
+    E = W["embedding.weight"]
+    pre = f"mtp.heads.{head}."
+    loc = [rms(np.asarray(anchor, np.float64), W[pre + "trunk_norm.weight"], cfg.norm_eps)]
+    for t in ids:
+        loc.append(rms(E[int(t)], W[pre + "token_norm.weight"], cfg.norm_eps))
+    x = np.stack(loc)
+    x = block(W, pre + "refine.", x, cfg, np.arange(len(loc), dtype=np.float64))
+    return rms(x[-1], W[pre + "output_norm.weight"], cfg.norm_eps) @ E.T

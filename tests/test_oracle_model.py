@@ -1,0 +1,132 @@
+"""Pins the oracle forward and MTP engine (model.rs, nn/src, mtp_speculative.rs)."""
+import numpy as np
+import pytest
+
+import npref
+import refcpu as R
+
+
+def tiny_cfg(**kw):
+    base = dict(vocab_size=97, hidden_dim=64, ffn_dim=96, n_layers=2, n_heads=4, n_kv_heads=2,
+                max_seq_len=48, num_future_tokens=3)
+    base.update(kw)
+    return R.make_config(**base)
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def test_cached_forward_matches_float64_full_forward():  # model_tests.rs:178-203
+    cfg = tiny_cfg()
+    m = R.Model(cfg, seed=0, std=0.05)
+    W = npref.weights(m)
+    ids = R.synth_tokens(0, 99, 13, cfg.vocab_size)
+    kv = m.kv(cfg.max_seq_len)
+    l1, h1 = kv.forward(ids[:9], 0)
+    l2, h2 = kv.forward(ids[9:], 9)
+    want, hwant = npref.forward(W, cfg, ids)
+    got = np.concatenate([l1, l2])
+    assert rel(got, want) < 1e-5
+    assert rel(np.concatenate([h1, h2]), hwant) < 1e-5
+
+
+def test_gqa_head_map_is_interleaved():
+    # With h % n_kv the result matches; a grouped map (h // rep) would not.
+    cfg = tiny_cfg(n_heads=4, n_kv_heads=2, n_layers=1)
+    m = R.Model(cfg, seed=3, std=0.2)
+    W = npref.weights(m)
+    ids = R.synth_tokens(1, 1, 10, cfg.vocab_size)
+    got, _ = m.kv(cfg.max_seq_len).forward(ids, 0)
+    want, _ = npref.forward(W, cfg, ids)
+    assert rel(got, want) < 1e-5
+
+
+def test_rollback_by_index_overwrites_suffix():  # nn/src/kvcache.rs:380-414
+    cfg = tiny_cfg()
+    m = R.Model(cfg, seed=1, std=0.05)
+    ids = R.synth_tokens(2, 1, 12, cfg.vocab_size)
+    kv = m.kv(cfg.max_seq_len)
+    kv.forward(ids[:8], 0)
+    kv.forward(ids[8:12], 8)
+    assert len(kv) == 12
+    a, _ = kv.forward(ids[10:12], 10)  # rewind to 10 and replay
+    kv2 = m.kv(cfg.max_seq_len)
+    b, _ = kv2.forward(ids[:12], 0)
+    assert rel(a, b[10:]) < 1e-5
+    kv.truncate(4)
+    assert len(kv) == 4
+    with pytest.raises(ValueError):
+        kv.truncate(5)
+
+
+def test_mtp_head_matches_float64():  # mtp.rs:104-114, model.rs:783-817
+    cfg = tiny_cfg()
+    m = R.Model(cfg, seed=2, std=0.05)
+    W = npref.weights(m)
+    anchor = np.random.default_rng(0).normal(0, 1, cfg.hidden_dim).astype(np.float32)
+    for head in (0, 1):
+        ids = R.synth_tokens(3, head, head + 1, cfg.vocab_size)
+        got = m.mtp_head(head, anchor, ids)
+        want = npref.mtp_head(W, cfg, head, anchor, ids)
+        assert rel(got, want) < 1e-5
+    with pytest.raises(ValueError):
+        m.mtp_head(0, anchor, np.array([1, 2], np.uint32))
+
+
+def test_zero_weight_model_picks_last_index():  # F9; speculative.rs:878-904
+    cfg = tiny_cfg()
+    m = R.Model(cfg)  # all linears zero, norms 1
+    prompt = np.array([5, 6, 7], np.uint32)
+    toks, fin, stats, _ = m.mtp_generate(prompt, 6, 3, R.sampler(greedy=True))
+    assert list(toks) == [cfg.vocab_size - 1] * 6 and fin == R.FINISH_MAX_TOKENS
+    assert stats["target_decode_forwards"] == 2 and stats["draft_tokens_accepted"] == 6
+
+
+def test_greedy_mtp_matches_plain_greedy():  # mtp_speculative.rs:438-454
+    cfg = tiny_cfg(vocab_size=64, max_seq_len=64)
+    m = R.Model(cfg, seed=4, std=0.3)
+    prompt = R.synth_tokens(4, 2, 9, cfg.vocab_size)
+    s = R.sampler(greedy=True)
+    plain, fin_p = m.plain_generate(prompt, 30, s)
+    for nd in (2, 3):
+        spec, fin_s, stats, _ = m.mtp_generate(prompt, 30, nd, s)
+        assert list(spec) == list(plain) and fin_s == fin_p
+        assert stats["mtp_head_forwards"] > 0
+        assert stats["draft_tokens_proposed"] == stats["draft_tokens_accepted"] + stats["draft_tokens_rejected"]
+        assert stats["rounds"] <= stats["target_decode_forwards"]
+
+
+def test_context_limit_is_reported():  # speculative.rs:1030-1043
+    cfg = tiny_cfg(max_seq_len=16)
+    m = R.Model(cfg)
+    toks, fin, _, _ = m.mtp_generate(np.array([1, 2, 3, 4, 5], np.uint32), 20, 3, R.sampler(greedy=True))
+    assert len(toks) == 11 and fin == R.FINISH_CONTEXT_LIMIT
+
+
+def test_quantised_weights_only_change_weights():
+    cfg4 = tiny_cfg(hidden_dim=128, ffn_dim=256, n_heads=4, n_kv_heads=2, weight_format=R.W_INT4_G128,
+                    lm_head_format=1)
+    m4 = R.Model(cfg4, seed=5, std=0.02)
+    cfg32 = tiny_cfg(hidden_dim=128, ffn_dim=256, n_heads=4, n_kv_heads=2)
+    m32 = R.Model(cfg32)
+    for i in range(len(m4.tensors())):
+        m32.set(i, m4.get(i))
+    ids = R.synth_tokens(5, 5, 10, cfg4.vocab_size)
+    a, _ = m4.kv(48).forward(ids, 0)
+    b, _ = m32.kv(48).forward(ids, 0)
+    assert np.array_equal(a, b)
+    # the INT4 weights really are the g128 codec applied to the raw synthetic weights
+    raw = R.synth_fill(5, 2, 128 * 128, 0.02)
+    p, sh, zh = R.quantise_i4_f16(raw, 128)
+    assert np.array_equal(m4.get(2).ravel(), R.dequantise_i4_f16(p, raw.size, 128, sh, zh))
+
+
+def test_int8_kv_cache_stays_close_to_f32():
+    kw = dict(hidden_dim=128, ffn_dim=256, n_heads=2, n_kv_heads=1)
+    m8 = R.Model(tiny_cfg(kv_format=R.KV_INT8, **kw), seed=6, std=0.05)
+    m32 = R.Model(tiny_cfg(**kw), seed=6, std=0.05)
+    ids = R.synth_tokens(6, 6, 20, 97)
+    a, _ = m8.kv(48).forward(ids, 0)
+    b, _ = m32.kv(48).forward(ids, 0)
+    assert 0 < rel(a, b) < 2e-2
