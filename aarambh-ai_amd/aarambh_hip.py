@@ -1,0 +1,403 @@
+"""Python host mirror of aarambh-studio's speculative-verify interface over the
+HIP C ABI (include/aarambh_hip.h, libaarambh_hip.so).
+
+The names follow the reference crates so that tests read like the reference's
+own:
+  ModelConfig / MtpConfig          core/src/config.rs:734-776, 275-283
+  Sampler.greedy / top_k_top_p     inference/src/sampler.rs:33-65
+  SpeculativeConfig                inference/src/speculative.rs:14-31
+  SpeculativeStats                 inference/src/speculative.rs:41-90
+  HipModel.forward_with_cache_output / forward_mtp_head
+                                   model/src/model.rs:529-587, 783-817
+  HipModel KV snapshot / restore   inference/src/kvcache.rs:56-69
+  MtpSpeculativeEngine.generate    inference/src/mtp_speculative.rs:86-336
+Errors raise AarambhError subclasses (core/src/error.rs:5-33).  There is no
+CPU fallback: a missing or unloadable library raises immediately.
+"""
+import atexit
+import ctypes as C
+import os
+import weakref
+from dataclasses import dataclass, field
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libaarambh_hip.so")
+
+W_F32, W_BF16, W_INT8_ROW, W_INT4_G128 = 0, 1, 2, 3
+KV_F32, KV_F16, KV_INT8 = 0, 1, 2
+T_NORM, T_LINEAR, T_EMBED = 0, 1, 2
+FLAG_RATIO_NEAR, FLAG_CDF_NEAR = 1, 2
+PROF_NAMES = ["gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down", "gemv_lmhead", "attention", "accept", "other"]
+
+
+class AarambhError(RuntimeError):
+    pass
+
+
+class ConfigError(AarambhError):
+    pass
+
+
+class ShapeError(AarambhError):
+    pass
+
+
+class UnsupportedError(AarambhError):
+    pass
+
+
+class DeviceError(AarambhError):
+    pass
+
+
+_ERRS = {1: ConfigError, 2: ShapeError, 3: UnsupportedError, 4: DeviceError}
+
+
+class _Cfg(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab_size", "hidden_dim", "ffn_dim", "n_layers", "n_heads",
+                                          "n_kv_heads", "max_seq_len")] + \
+               [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
+               [(n, C.c_int32) for n in ("num_future_tokens", "weight_format", "lm_head_format", "kv_format",
+                                          "max_batch", "max_rows")]
+
+
+class _Sampler(C.Structure):
+    _fields_ = [("greedy", C.c_int32), ("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float)]
+
+
+class _Stats(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("rounds", "draft_tokens_proposed", "draft_tokens_accepted",
+                                          "draft_tokens_rejected", "target_decode_forwards",
+                                          "draft_decode_forwards", "mtp_head_forwards")]
+
+
+_lib = None
+_P = C.c_void_p
+
+
+def lib():
+    """Load libaarambh_hip.so; raises if it is missing (no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise DeviceError(f"HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+    L = C.CDLL(LIB_PATH)
+    sig = {
+        "aarh_create": (C.c_int, [C.c_int, C.POINTER(_Cfg), C.POINTER(_P)]),
+        "aarh_destroy": (None, [_P]),
+        "aarh_last_error": (C.c_char_p, [_P]),
+        "aarh_stream": (_P, [_P]),
+        "aarh_sync": (C.c_int, [_P]),
+        "aarh_num_tensors": (C.c_int, [_P]),
+        "aarh_tensor_info": (C.c_int, [_P, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int64),
+                                       C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+        "aarh_load_tensor_f32": (C.c_int, [_P, C.c_int, _P, C.c_int64]),
+        "aarh_load_tensor_int4": (C.c_int, [_P, C.c_int, _P, _P, _P, C.c_int64, C.c_int64, C.c_int32]),
+        "aarh_load_tensor_int8": (C.c_int, [_P, C.c_int, _P, _P, C.c_int64, C.c_int64]),
+        "aarh_init_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float]),
+        "aarh_kv_reset": (C.c_int, [_P, C.c_int]),
+        "aarh_kv_len": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
+        "aarh_kv_rollback": (C.c_int, [_P, C.c_int, C.c_int32]),
+        "aarh_kv_fill_synthetic": (C.c_int, [_P, C.c_int, C.c_int32, C.c_uint64]),
+        "aarh_forward": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _P, _P]),
+        "aarh_last_logits_device": (_P, [_P]),
+        "aarh_last_hidden_device": (_P, [_P]),
+        "aarh_mtp_head": (C.c_int, [_P, C.c_int, _P, _P, C.c_int, _P]),
+        "aarh_accept_sample": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.POINTER(_Sampler), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+        "aarh_mtp_generate": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
+                                        _P, _P, _P, C.POINTER(_Stats)]),
+        "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
+        "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                    C.POINTER(C.c_int64)]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aarh_sync", "aarh_num_tensors",
+            "aarh_tensor_info", "aarh_load_tensor_f32", "aarh_load_tensor_int4", "aarh_load_tensor_int8",
+            "aarh_init_synthetic", "aarh_kv_reset", "aarh_kv_len", "aarh_kv_rollback", "aarh_kv_fill_synthetic",
+            "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
+            "aarh_accept_sample", "aarh_mtp_generate", "aarh_prof_enable", "aarh_prof_get"]
+
+
+def _ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+@dataclass
+class ModelConfig:
+    """ModelConfig subset (core/src/config.rs:734-776) plus MtpConfig.num_future_tokens."""
+    vocab_size: int
+    hidden_dim: int
+    ffn_dim: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    max_seq_len: int
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+    num_future_tokens: int = 0
+    weight_format: int = W_F32
+    lm_head_format: int = 0
+    kv_format: int = KV_F32
+
+    @property
+    def head_dim(self):  # core/src/config.rs:866-868
+        return self.hidden_dim // self.n_heads
+
+
+@dataclass
+class Sampler:
+    """inference/src/sampler.rs:14-65 (device path: no top-k / top-p)."""
+    greedy: bool = True
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 0.0
+    seed: int = 0
+
+    @staticmethod
+    def greedy_sampler():
+        return Sampler(greedy=True)
+
+    @staticmethod
+    def top_k_top_p(temperature, top_k=None, top_p=None, seed=0):
+        if temperature < 0:
+            raise ConfigError("temperature must be non-negative")
+        if top_p is not None and not (0.0 <= top_p <= 1.0):
+            raise ConfigError("top_p must be in [0, 1]")
+        return Sampler(False, temperature, top_k or 0, top_p or 0.0, seed)
+
+    def is_deterministic(self):  # sampler.rs:91-97
+        return self.greedy or self.temperature <= np.finfo(np.float32).eps
+
+    def _c(self):
+        return _Sampler(1 if self.greedy else 0, self.temperature, self.top_k, self.top_p)
+
+
+@dataclass
+class SpeculativeConfig:
+    num_draft_tokens: int = 4
+
+    def __post_init__(self):
+        if self.num_draft_tokens == 0:
+            raise ConfigError("num_draft_tokens must be greater than zero")
+
+
+@dataclass
+class SpeculativeStats:
+    rounds: int = 0
+    draft_tokens_proposed: int = 0
+    draft_tokens_accepted: int = 0
+    draft_tokens_rejected: int = 0
+    target_decode_forwards: int = 0
+    draft_decode_forwards: int = 0
+    mtp_head_forwards: int = 0
+
+    def acceptance_rate(self):
+        return 0.0 if self.draft_tokens_proposed == 0 else self.draft_tokens_accepted / self.draft_tokens_proposed
+
+    def accepted_tokens_per_target_forward(self):
+        return 0.0 if self.target_decode_forwards == 0 else self.draft_tokens_accepted / self.target_decode_forwards
+
+
+@dataclass
+class GenerationOutput:
+    token_ids: list
+    finish_reason: str
+    speculative_stats: SpeculativeStats = field(default_factory=SpeculativeStats)
+
+
+FINISH = {0: "MaxTokens", 1: "EosToken", 2: "ContextLimit"}
+
+
+_LIVE = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_contexts():
+    # Destroy contexts while the HIP runtime is still up (its own teardown runs later).
+    for m in list(_LIVE):
+        m.close()
+
+
+class HipModel:
+    """Device copy of one target model plus its KV cache slots."""
+
+    def __init__(self, cfg: ModelConfig, max_batch=1, max_rows=128, device=0):
+        self.cfg = cfg
+        c = _Cfg(cfg.vocab_size, cfg.hidden_dim, cfg.ffn_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads,
+                 cfg.max_seq_len, cfg.rope_theta, cfg.norm_eps, cfg.num_future_tokens, cfg.weight_format,
+                 cfg.lm_head_format, cfg.kv_format, max_batch, max_rows)
+        h = _P()
+        st = lib().aarh_create(device, C.byref(c), C.byref(h))
+        self.h = h
+        if st:
+            msg = lib().aarh_last_error(h).decode() if h else "aarh_create failed"
+            self.close()
+            raise _ERRS.get(st, AarambhError)(msg)
+        self.max_batch = max_batch
+        self.max_rows = max_rows
+        _LIVE.add(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aarh_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _check(self, st):
+        if st:
+            raise _ERRS.get(st, AarambhError)(lib().aarh_last_error(self.h).decode())
+
+    def tensors(self):
+        out = []
+        name = C.create_string_buffer(128)
+        for i in range(lib().aarh_num_tensors(self.h)):
+            r, c, k = C.c_int64(), C.c_int64(), C.c_int32()
+            self._check(lib().aarh_tensor_info(self.h, i, name, 128, C.byref(r), C.byref(c), C.byref(k)))
+            out.append((name.value.decode(), r.value, c.value, k.value))
+        return out
+
+    def load_f32(self, tid, values):
+        v = np.ascontiguousarray(values, np.float32)
+        self._check(lib().aarh_load_tensor_f32(self.h, tid, _ptr(v), v.size))
+
+    def load_int4(self, tid, packed, scales_f16, zeros_f16, rows, cols, group=128):
+        p = np.ascontiguousarray(packed, np.uint8)
+        s = np.ascontiguousarray(scales_f16, np.uint16)
+        z = np.ascontiguousarray(zeros_f16, np.uint16)
+        self._check(lib().aarh_load_tensor_int4(self.h, tid, _ptr(p), _ptr(s), _ptr(z), rows, cols, group))
+
+    def load_int8(self, tid, codes, scales, rows, cols):
+        q = np.ascontiguousarray(codes, np.int8)
+        s = np.ascontiguousarray(scales, np.float32)
+        self._check(lib().aarh_load_tensor_int8(self.h, tid, _ptr(q), _ptr(s), rows, cols))
+
+    def init_synthetic(self, seed=0, std=0.02):
+        self._check(lib().aarh_init_synthetic(self.h, seed, std))
+
+    # --- KV cache (inference/src/kvcache.rs) ---
+    def kv_len(self, slot=0):
+        v = C.c_int32()
+        self._check(lib().aarh_kv_len(self.h, slot, C.byref(v)))
+        return v.value
+
+    def kv_reset(self, slot=0):
+        self._check(lib().aarh_kv_reset(self.h, slot))
+
+    def snapshot(self, slot=0):
+        return self.kv_len(slot)
+
+    def restore(self, snapshot, slot=0):
+        self._check(lib().aarh_kv_rollback(self.h, slot, snapshot))
+
+    def kv_fill_synthetic(self, slot, length, seed=0):
+        self._check(lib().aarh_kv_fill_synthetic(self.h, slot, length, seed))
+
+    # --- model API ---
+    def forward_with_cache_output(self, ids, offsets, slots=None, want_logits=True, want_hidden=True):
+        """ids [nseq, S]; returns (logits [nseq, S, V], hidden [nseq, S, H])."""
+        ids = np.ascontiguousarray(np.atleast_2d(ids), np.uint32)
+        nseq, S = ids.shape
+        offs = np.ascontiguousarray(np.broadcast_to(np.asarray(offsets, np.int32), (nseq,)), np.int32)
+        sl = np.ascontiguousarray(np.arange(nseq, dtype=np.int32) if slots is None else slots, np.int32)
+        lg = np.empty((nseq, S, self.cfg.vocab_size), np.float32) if want_logits else None
+        hd = np.empty((nseq, S, self.cfg.hidden_dim), np.float32) if want_hidden else None
+        self._check(lib().aarh_forward(self.h, _ptr(ids), _ptr(sl), _ptr(offs), nseq, S, _ptr(lg), _ptr(hd)))
+        return lg, hd
+
+    def forward_mtp_head(self, head, anchor, ids):
+        anchor = np.ascontiguousarray(np.atleast_2d(anchor), np.float32)
+        ids = np.ascontiguousarray(np.atleast_2d(ids), np.uint32)
+        nseq = anchor.shape[0]
+        out = np.empty((nseq, self.cfg.vocab_size), np.float32)
+        self._check(lib().aarh_mtp_head(self.h, head, _ptr(anchor), _ptr(ids), nseq, _ptr(out)))
+        return out
+
+    def sync(self):
+        self._check(lib().aarh_sync(self.h))
+
+    def stream(self):
+        return lib().aarh_stream(self.h)
+
+    def prof_enable(self, on=True):
+        self._check(lib().aarh_prof_enable(self.h, 1 if on else 0))
+
+    def prof_get(self):
+        out = {}
+        for i, n in enumerate(PROF_NAMES):
+            ms, by, cnt = C.c_double(), C.c_double(), C.c_int64()
+            self._check(lib().aarh_prof_get(self.h, i, C.byref(ms), C.byref(by), C.byref(cnt)))
+            out[n] = {"ms": ms.value, "bytes": by.value, "launches": cnt.value}
+        return out
+
+    def accept_sample(self, target, draft, draft_tokens, sampler, bonus, seeds=None, word_offsets=None,
+                      uniforms=None, n_proposals=None):
+        """Acceptance on device tensors (torch cuda tensors).  target [B, Kt, V] f32,
+        draft [B, K, V] f32, draft_tokens [B, K] int32.  Returns a dict of torch tensors."""
+        import torch
+        B, K, V = draft.shape if draft is not None else (target.shape[0], 0, target.shape[2])
+        dev = target.device
+        outs = {k: torch.empty(B, dtype=torch.int32, device=dev)
+                for k in ("accept_len", "token", "flags", "draws", "status")}
+
+        def p(t):
+            return None if t is None else C.c_void_p(t.data_ptr())
+
+        torch.cuda.synchronize(dev)
+        st = lib().aarh_accept_sample(self.h, p(target), target.shape[1], p(draft), p(draft_tokens),
+                                      p(n_proposals), B, K, V, 1 if bonus else 0, C.byref(sampler._c()),
+                                      p(seeds), p(word_offsets), p(uniforms), p(outs["accept_len"]),
+                                      p(outs["token"]), p(outs["flags"]), p(outs["draws"]), p(outs["status"]),
+                                      None)
+        self._check(st)
+        self.sync()
+        return outs
+
+
+class MtpSpeculativeEngine:
+    """inference/src/mtp_speculative.rs:18-336 for a batch of independent requests."""
+
+    def __init__(self, model: HipModel, config: SpeculativeConfig):
+        mtp = model.cfg.num_future_tokens
+        if mtp < 2:
+            raise ConfigError("internal speculative decoding requires model.mtp configuration")
+        if config.num_draft_tokens < 2:
+            raise ConfigError("MTP speculative decoding requires at least two proposal tokens")
+        if config.num_draft_tokens > mtp:
+            raise ConfigError(f"requested {config.num_draft_tokens} MTP proposal tokens but checkpoint horizon is {mtp}")
+        self.model = model
+        self.config = config
+
+    def generate_batch(self, prompts, max_new_tokens, sampler: Sampler, seeds=None):
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.uint32)
+        nseq, plen = prompts.shape
+        sd = np.ascontiguousarray(
+            np.full(nseq, sampler.seed, np.uint64) if seeds is None else seeds, np.uint64)
+        out = np.zeros((nseq, max(max_new_tokens, 1)), np.uint32)
+        n = np.zeros(nseq, np.int32)
+        fin = np.zeros(nseq, np.int32)
+        stats = (_Stats * nseq)()
+        m = self.model
+        m._check(lib().aarh_mtp_generate(m.h, _ptr(prompts), nseq, plen, max_new_tokens,
+                                         self.config.num_draft_tokens, C.byref(sampler._c()), _ptr(sd),
+                                         _ptr(out), _ptr(n), _ptr(fin), stats))
+        res = []
+        for b in range(nseq):
+            st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
+            res.append(GenerationOutput(list(out[b, :n[b]]), FINISH[int(fin[b])], st))
+        return res
+
+    def generate(self, prompt_ids, max_new_tokens, sampler: Sampler):
+        return self.generate_batch(np.asarray(prompt_ids)[None, :], max_new_tokens, sampler)[0]

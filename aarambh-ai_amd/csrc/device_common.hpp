@@ -1,0 +1,273 @@
+// Device-side helpers shared by the gfx950 kernels of libaarambh_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+#define WAVE 64
+
+// f32::total_cmp ordering key: larger key == larger value, NaN above +inf.
+__device__ __forceinline__ int32_t total_key(float f) {
+    int32_t i = __float_as_int(f);
+    return i ^ (int32_t)(((uint32_t)(i >> 31)) >> 1);
+}
+
+// exp rounded to nearest f32: evaluate in f64 and round once.  This matches a
+// correctly rounded libm expf except in the rare cases where the host libm
+// itself misrounds; those show up as flagged near-ties, never silently.
+__device__ __forceinline__ float expf_rn(float x) { return (float)exp((double)x); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// rand 0.8 StdRng (ChaCha12, rand_chacha 0.3.1) seeded by seed_from_u64
+// (rand_core 0.6.4): keystream word n of sequence seed, evaluated on device.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t rotl32(uint32_t v, int n) { return (v << n) | (v >> (32 - n)); }
+
+__device__ inline void rng_key_from_seed(uint64_t state, uint32_t key[8]) {
+    const uint64_t mul = 6364136223846793005ull, inc = 11634580027462260723ull;
+    for (int i = 0; i < 8; i++) {
+        state = state * mul + inc;
+        uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+        uint32_t rot = (uint32_t)(state >> 59);
+        key[i] = (xs >> rot) | (xs << ((32 - rot) & 31));
+    }
+}
+
+#define CHACHA_QR(a, b, c, d)                                                                      \
+    a += b; d ^= a; d = rotl32(d, 16);                                                             \
+    c += d; b ^= c; b = rotl32(b, 12);                                                             \
+    a += b; d ^= a; d = rotl32(d, 8);                                                              \
+    c += d; b ^= c; b = rotl32(b, 7);
+
+__device__ inline uint32_t rng_word(const uint32_t key[8], uint64_t word) {
+    uint32_t in[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
+                       key[0], key[1], key[2], key[3], key[4], key[5], key[6], key[7],
+                       (uint32_t)(word >> 4), (uint32_t)(word >> 36), 0u, 0u};
+    uint32_t x[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) x[i] = in[i];
+    for (int r = 0; r < 12; r += 2) {
+        CHACHA_QR(x[0], x[4], x[8], x[12]);
+        CHACHA_QR(x[1], x[5], x[9], x[13]);
+        CHACHA_QR(x[2], x[6], x[10], x[14]);
+        CHACHA_QR(x[3], x[7], x[11], x[15]);
+        CHACHA_QR(x[0], x[5], x[10], x[15]);
+        CHACHA_QR(x[1], x[6], x[11], x[12]);
+        CHACHA_QR(x[2], x[7], x[8], x[13]);
+        CHACHA_QR(x[3], x[4], x[9], x[14]);
+    }
+    uint32_t idx = (uint32_t)(word & 15);
+    uint32_t out = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        if ((uint32_t)i == idx) out = x[i] + in[i];
+    return out;
+}
+
+// rand 0.8 Standard f32: (next_u32 >> 8) * 2^-24.
+__device__ inline float rng_f32(const uint32_t key[8], uint64_t word) {
+    return (float)(rng_word(key, word) >> 8) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level primitives
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_excl_scan_i32(int v) {
+    const int lane = threadIdx.x & 63;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    return incl - v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Exact sequential f32 summation on one wave.
+//
+// Returns s_{n-1} where s_k = fl(s_{k-1} + v[k]), s_{-1} = 0, for v[k] >= 0,
+// bit-identical to a scalar left-to-right f32 loop (the reference's
+// iter().sum::<f32>() and the running cumulative of sample_from_probs).
+// With u >= 0 it also finds the first k with u <= s_k (inverse CDF).
+//
+// Method: while s stays inside one binade [2^e, 2^(e+1)), every partial sum
+// is an integer multiple of ulp(s), and fl(s + x) = s + ulp * RNE(x / ulp)
+// unless x / ulp has fraction exactly 1/2 (a tie, decided by parity).  So the
+// wave turns 256 elements at a time into integer increments, scans them, and
+// stops at the first element that leaves the binade or ties; that element is
+// added with a real f32 add and the scan restarts after it.
+// ---------------------------------------------------------------------------
+struct SeqSum {
+    float total;
+    int cross;      // first k with u <= s_k (n-1 if none); -1 when u < 0
+    float s_at;     // s_cross
+    float s_before; // s_{cross-1} (0 for cross == 0)
+};
+
+__device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+    int pos = 0;
+    int cross = -1;
+    float s_at = 0.0f, s_before = 0.0f;
+    const bool want = u >= 0.0f;
+    while (pos < n) {
+        const int base = pos + 4 * lane;
+        float x[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) x[k] = (base + k < n) ? v[base + k] : 0.0f;
+
+        if (s == 0.0f) {
+            // Zeros keep s at 0 (0 + 0 = 0); the first non-zero element x gives s = x.
+            int fnz = 4;
+#pragma unroll
+            for (int k = 3; k >= 0; k--)
+                if (base + k < n && x[k] != 0.0f) fnz = k;
+            unsigned long long m = __ballot(fnz < 4);
+            if (want && cross < 0 && u <= 0.0f) {
+                cross = pos;
+                s_at = 0.0f;
+                s_before = 0.0f;
+            }
+            if (m == 0ull) {
+                pos += 256;
+                continue;
+            }
+            int bl = __ffsll((long long)m) - 1;
+            int bk = __shfl(fnz, bl, 64);
+            int t = pos + 4 * bl + bk;
+            float xt = v[t];
+            s = xt;
+            if (want && cross < 0 && u <= s) {
+                cross = t;
+                s_at = s;
+                s_before = 0.0f;
+            }
+            pos = t + 1;
+            continue;
+        }
+        const uint32_t bits = __float_as_uint(s);
+        const int eb = (int)((bits >> 23) & 0xFF);
+        if (eb == 0) {
+            // subnormal running sum: one scalar step
+            float xt = v[pos];
+            float sp = s;
+            s = s + xt;
+            if (want && cross < 0 && u <= s) {
+                cross = pos;
+                s_at = s;
+                s_before = sp;
+            }
+            pos++;
+            continue;
+        }
+        const int sh = 150 - eb;                         // x / ulp(s) == ldexp(x, sh)
+        const int ns = (int)((bits & 0x7FFFFFu) | 0x800000u); // s / ulp(s)
+        int r[4];
+        bool special[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float c = ldexpf(x[k], sh);
+            float a = floorf(c);
+            float f = c - a;
+            special[k] = !(c < 16777216.0f) || (f == 0.5f) || !(x[k] >= 0.0f);
+            r[k] = special[k] ? 16777216 : ((int)a + (f > 0.5f ? 1 : 0));
+        }
+        int lsum = r[0] + r[1] + r[2] + r[3];
+        if (lsum > 16777217) lsum = 16777217;
+        int excl = wave_excl_scan_i32(lsum);
+        int run = ns + excl;
+        int first_bad = 4, first_cross = 4;
+        float cs_at = 0.0f, cs_before = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (first_bad < 4) break;
+            if (base + k >= n) break;
+            int rk = run + r[k];
+            if (special[k] || rk >= 16777216) {
+                first_bad = k;
+                break;
+            }
+            if (want && first_cross == 4) {
+                float sk = ldexpf((float)rk, -sh);
+                if (u <= sk) {
+                    first_cross = k;
+                    cs_at = sk;
+                    cs_before = ldexpf((float)run, -sh);
+                }
+            }
+            run = rk;
+        }
+        unsigned long long badm = __ballot(first_bad < 4);
+        int bad_lane = badm ? (__ffsll((long long)badm) - 1) : 64;
+        unsigned long long lanes_ok = bad_lane >= 64 ? ~0ull : ((1ull << bad_lane) | ((1ull << bad_lane) - 1ull));
+        unsigned long long cm = __ballot(first_cross < 4) & lanes_ok;
+        if (want && cross < 0 && cm) {
+            int cl = __ffsll((long long)cm) - 1;
+            int ck = __shfl(first_cross, cl, 64);
+            cross = pos + 4 * cl + ck;
+            s_at = __shfl(cs_at, cl, 64);
+            s_before = __shfl(cs_before, cl, 64);
+            if (ck == 0 && cl == 0) s_before = s;
+        }
+        if (bad_lane == 64) {
+            int total = __shfl(excl + lsum, 63, 64);
+            s = ldexpf((float)(ns + total), -sh);
+            pos += 256;
+        } else {
+            int run_before = __shfl(run, bad_lane, 64);
+            int tk = __shfl(first_bad, bad_lane, 64);
+            int t = pos + 4 * bad_lane + tk;
+            float sp = ldexpf((float)run_before, -sh);
+            float xt = v[t];
+            s = sp + xt;
+            if (want && cross < 0 && u <= s) {
+                cross = t;
+                s_at = s;
+                s_before = sp;
+            }
+            pos = t + 1;
+        }
+    }
+    if (want && cross < 0) {
+        cross = n - 1;
+        s_at = s;
+        s_before = s;
+    }
+    SeqSum res;
+    res.total = s;
+    res.cross = cross;
+    res.s_at = s_at;
+    res.s_before = s_before;
+    return res;
+}

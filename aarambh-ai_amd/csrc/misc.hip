@@ -1,0 +1,456 @@
+// Small kernels around the verify forward: embedding gather, MTP local
+// sequence preparation, row RMSNorm, weight quantisation / repacking into the
+// tiled GEMV layout, synthetic weights and KV contents, row argmax.
+#include <float.h>
+#include <stdio.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aarh {
+
+static constexpr int MT_THREADS = 256;
+
+static thread_local char g_last_err[256] = "";
+
+int note_error(hipError_t e) {
+    if (e == hipSuccess) return 0;
+    snprintf(g_last_err, sizeof(g_last_err), "%s", hipGetErrorString(e));
+    return 1;
+}
+
+const char* last_launch_error() { return g_last_err; }
+
+__device__ inline float load_table(const void* table, int fmt, size_t idx) {
+    if (fmt == WF_BF16) return bf16_to_f32(((const uint16_t*)table)[idx]);
+    return ((const float*)table)[idx];
+}
+
+__device__ inline float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_sum_f32(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += red[w];
+    return s;
+}
+
+// TokenEmbedding::forward (model/src/embedding.rs:26-28) + split sums of
+// squares over 128-column groups for the first RMSNorm.
+__global__ void embed_kernel(const void* table, int fmt, int H, const uint32_t* ids, float* x,
+                             float* ssq_part, int M) {
+    const int m = blockIdx.x;
+    const size_t base = (size_t)ids[m] * H;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)m * H + k] = load_table(table, fmt, base + k);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int cg = wid; cg < H / 128; cg += nw) {
+        float a = x[(size_t)m * H + cg * 128 + lane], b = x[(size_t)m * H + cg * 128 + 64 + lane];
+        float s = wave_sum_f32(a * a + b * b);
+        if (lane == 0) ssq_part[(size_t)cg * M + m] = s;
+    }
+}
+
+int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x,
+                 float* ssq_part, hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), 0, stream, table, table_fmt, H, ids, x,
+                       ssq_part, M);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// MtpHead::local_sequence (nn/src/mtp.rs:247-293): row 0 = trunk_norm(anchor),
+// rows 1.. = token_norm(embedding(ids)); one workgroup per output row.
+__global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, const void* table, int fmt,
+                                const uint32_t* ids, int ids_stride, int L, int H, const float* trunk_w,
+                                const float* token_w, float eps, float* x, float* ssq_part, int M) {
+    __shared__ float red[MT_THREADS / 64];
+    const int row = blockIdx.x;
+    const int seq = row / L, l = row % L;
+    float* out = x + (size_t)row * H;
+    const float* w = l == 0 ? trunk_w : token_w;
+    for (int k = threadIdx.x; k < H; k += blockDim.x)
+        out[k] = l == 0 ? anchor[(size_t)seq * anchor_stride + k]
+                        : load_table(table, fmt, (size_t)ids[(size_t)seq * ids_stride + l - 1] * H + k);
+    __syncthreads();
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) ss += out[k] * out[k];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    __syncthreads();
+    for (int k = threadIdx.x; k < H; k += blockDim.x) out[k] = out[k] * inv * w[k];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int cg = wid; cg < H / 128; cg += nw) {
+        float a = out[cg * 128 + lane], b = out[cg * 128 + 64 + lane];
+        float s = wave_sum_f32(a * a + b * b);
+        if (lane == 0) ssq_part[(size_t)cg * M + row] = s;
+    }
+}
+
+int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* table, int table_fmt,
+                    const uint32_t* ids, int ids_stride, int nseq, int L, int H, const float* trunk_w,
+                    const float* token_w, float eps, float* x, float* ssq_part, hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(MT_THREADS), 0, stream, anchor, anchor_stride,
+                       table, table_fmt, ids, ids_stride, L, H, trunk_w, token_w, eps, x, ssq_part, nseq * L);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// RMSNorm of selected rows (nn/src/norm.rs:17-19).
+__global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float* w, float eps, float* out) {
+    __shared__ float red[MT_THREADS / 64];
+    const int m = blockIdx.x;
+    const float* r = x + row_off(xmap, m);
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) ss += r[k] * r[k];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) out[(size_t)m * H + k] = r[k] * inv * w[k];
+}
+
+int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, float eps, float* out,
+                     hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), 0, stream, x, xmap, H, w, eps, out);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Destination row of source row n inside a fused matrix.  interleave 1/2 puts
+// gate/up row f at row (f/8)*16 + f%8 (+8 for up) so a 16-row tile holds 8
+// matching gate and up rows.
+__device__ __forceinline__ int dest_row(int n, int row_offset, int interleave) {
+    if (interleave == 0) return row_offset + n;
+    return (n >> 3) * 16 + (n & 7) + (interleave == 2 ? 8 : 0);
+}
+
+// INT4 g128 quantisation (quant/src/int4.rs:7-41, codes from the f32 scale,
+// scale/zero stored fp16) straight into the tiled layout.  One wave per
+// (row, group); lane l holds columns 2l, 2l+1.
+__global__ void quant_int4_kernel(const float* w, int N, int K, uint8_t* tiled, uint32_t* sz,
+                                  int row_offset, int interleave) {
+    const int G = K >> 7;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (wave >= N * G) return;
+    const int lane = threadIdx.x & 63;
+    const int n = wave / G, g = wave % G;
+    const float* src = w + (size_t)n * K + g * 128;
+    float v0 = src[2 * lane], v1 = src[2 * lane + 1];
+    float mn = fminf(v0, v1), mx = fmaxf(v0, v1);
+    for (int d = 32; d >= 1; d >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, d, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+    }
+    float sc = fabsf(mx - mn) <= FLT_EPSILON ? 1.0f : (mx - mn) / 15.0f;
+    float z = roundf(-mn / sc);
+    float q0 = fminf(fmaxf(roundf(v0 / sc + z), 0.0f), 15.0f);
+    float q1 = fminf(fmaxf(roundf(v1 / sc + z), 0.0f), 15.0f);
+    const int dn = dest_row(n, row_offset, interleave);
+    const int nt = dn >> 4, r = dn & 15;
+    const int j = lane >> 4, c2 = lane & 15;  // columns 2*lane = 32*j + 2*c2
+    const size_t tile = (size_t)nt * G + g;
+    tiled[tile * 1024 + 16 * (j * 16 + r) + c2] = (uint8_t)(((int)q0 & 15) | (((int)q1 & 15) << 4));
+    if (lane == 0) {
+        uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
+        uint16_t zh = __builtin_bit_cast(uint16_t, (_Float16)z);
+        sz[tile * 16 + r] = (uint32_t)sh | ((uint32_t)zh << 16);
+    }
+}
+
+// Per-output-row symmetric INT8 (quant/src/qat.rs:155-169), tiled.
+__global__ void quant_int8_kernel(const float* w, int N, int K, uint8_t* tiled, float* rscale, int row_offset,
+                                  int interleave) {
+    __shared__ float red[MT_THREADS / 64];
+    const int n = blockIdx.x;
+    const float* src = w + (size_t)n * K;
+    float mx = 0.f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(src[k]));
+    mx = wave_max_f32(mx);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) red[wid] = mx;
+    __syncthreads();
+    float m = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) m = fmaxf(m, red[i]);
+    float sc = m / 127.0f;
+    if (m <= FLT_EPSILON) sc = 1.0f;
+    const int dn = dest_row(n, row_offset, interleave);
+    const int nt = dn >> 4, r = dn & 15, G = K >> 7;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
+        float q = fminf(fmaxf(roundf(src[k] / sc), -127.0f), 127.0f);
+        tiled[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = (uint8_t)(int8_t)q;
+    }
+    if (threadIdx.x == 0) rscale[dn] = sc;
+}
+
+__global__ void quant_bf16_kernel(const float* w, int N, int K, uint8_t* tiled, int row_offset, int interleave) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * K) return;
+    const int n = (int)(i / K), k = (int)(i % K);
+    const int dn = dest_row(n, row_offset, interleave);
+    const int nt = dn >> 4, r = dn & 15, G = K >> 7;
+    const int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
+    ((uint16_t*)tiled)[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = f32_to_bf16_rne(w[i]);
+}
+
+__global__ void copy_f32_rows_kernel(const float* w, int N, int K, float* dst, int row_offset, int interleave) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * K) return;
+    const int n = (int)(i / K), k = (int)(i % K);
+    dst[(size_t)dest_row(n, row_offset, interleave) * K + k] = w[i];
+}
+
+int launch_quantise_tiled(const float* w, int N, int K, int fmt, uint8_t* tiled, uint32_t* sz, float* rscale,
+                          int row_offset, int N_total, int interleave, hipStream_t stream) {
+    (void)N_total;
+    if (K % 128) return 2;
+    if (fmt == WF_INT4) {
+        const int waves = N * (K / 128);
+        hipLaunchKernelGGL(quant_int4_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, w, N, K, tiled, sz,
+                           row_offset, interleave);
+    } else if (fmt == WF_INT8) {
+        hipLaunchKernelGGL(quant_int8_kernel, dim3(N), dim3(MT_THREADS), 0, stream, w, N, K, tiled, rscale,
+                           row_offset, interleave);
+    } else if (fmt == WF_BF16) {
+        const size_t n = (size_t)N * K;
+        hipLaunchKernelGGL(quant_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, N, K,
+                           tiled, row_offset, interleave);
+    } else {
+        const size_t n = (size_t)N * K;
+        hipLaunchKernelGGL(copy_f32_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, N,
+                           K, (float*)tiled, row_offset, interleave);
+    }
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Reference PackedInt4Tensor layout (row-major, two codes per byte, low
+// nibble = even index, int4.rs:45-53) -> tiled layout.  One thread per byte.
+__global__ void repack_int4_kernel(const uint8_t* packed, const uint16_t* sc, const uint16_t* zr, int N, int K,
+                                   uint8_t* tiled, uint32_t* sz, int row_offset, int interleave) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nbytes = (size_t)N * K / 2;
+    if (i >= nbytes) return;
+    const int n = (int)(i / (K / 2)), kb = (int)(i % (K / 2));
+    const int k = 2 * kb;
+    const int dn = dest_row(n, row_offset, interleave);
+    const int nt = dn >> 4, r = dn & 15, G = K >> 7;
+    const int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
+    const size_t tile = (size_t)nt * G + g;
+    tiled[tile * 1024 + 16 * (j * 16 + r) + (c >> 1)] = packed[i];
+    if (kk == 0) sz[tile * 16 + r] = (uint32_t)sc[(size_t)n * G + g] | ((uint32_t)zr[(size_t)n * G + g] << 16);
+}
+
+int launch_repack_int4(const uint8_t* packed, const uint16_t* sc, const uint16_t* zr, int N, int K, uint8_t* tiled,
+                       uint32_t* sz, int row_offset, int N_total, int interleave, hipStream_t stream) {
+    (void)N_total;
+    const size_t nb = (size_t)N * K / 2;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(repack_int4_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream, packed, sc, zr,
+                       N, K, tiled, sz, row_offset, interleave);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+__global__ void repack_int8_kernel(const int8_t* codes, const float* sc, int N, int K, uint8_t* tiled, float* rscale,
+                                   int row_offset, int interleave) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * K) return;
+    const int n = (int)(i / K), k = (int)(i % K);
+    const int dn = dest_row(n, row_offset, interleave);
+    const int nt = dn >> 4, r = dn & 15, G = K >> 7;
+    const int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
+    tiled[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = (uint8_t)codes[i];
+    if (k == 0) rscale[dn] = sc[n];
+}
+
+int launch_repack_int8(const int8_t* codes, const float* sc, int N, int K, uint8_t* tiled, float* rscale,
+                       int row_offset, int N_total, int interleave, hipStream_t stream) {
+    (void)N_total;
+    const size_t n = (size_t)N * K;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(repack_int8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, codes, sc, N, K,
+                       tiled, rscale, row_offset, interleave);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Build-defined synthetic generator (same formula as the test oracle):
+// splitmix64 counter hash -> Box-Muller in f64.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ float synth_normal(uint64_t seed, uint32_t stream, uint64_t index) {
+    uint64_t base = splitmix64(seed ^ ((uint64_t)stream * 0xD1B54A32D192ED03ull));
+    uint64_t h = splitmix64(base + index);
+    double u1 = ((double)(h >> 40) + 1.0) * (1.0 / 16777216.0);
+    double u2 = (double)((h >> 16) & 0xFFFFFFull) * (1.0 / 16777216.0);
+    return (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+}
+
+__global__ void synth_fill_kernel(float* out, long long n, unsigned long long seed, unsigned stream, float std) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = (float)((double)synth_normal(seed, stream, (uint64_t)i) * (double)std);
+}
+
+int launch_synth_fill(float* out, long long n, unsigned long long seed, unsigned stream_id, float std,
+                      hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(synth_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, out, n, seed,
+                       stream_id, std);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+__global__ void to_bf16_kernel(const float* src, uint16_t* dst, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = f32_to_bf16_rne(src[i]);
+}
+
+int launch_to_bf16(const float* src, uint16_t* dst, long long n, hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, src, dst, n);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Synthetic post-RoPE K/V contents for long-context benchmarks; one wave per
+// (token, kv head, K|V).  Same values as the oracle's ref_kv_fill_synthetic.
+__global__ void kv_fill_kernel(void* kc, void* vc, uint16_t* ks, uint16_t* vs, int kv_fmt, int slot, int n_kv,
+                               int hd, int cap, int len, unsigned long long seed, int layer) {
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (wave >= len * n_kv * 2) return;
+    const int lane = threadIdx.x & 63;
+    const int which = wave & 1;
+    const int th = wave >> 1;
+    const int t = th / n_kv, h = th % n_kv;
+    const uint32_t stream = 0x4B560000u + (uint32_t)(layer * 2 + which);
+    const uint64_t off = ((uint64_t)t * n_kv + h) * hd;
+    float v0 = lane < hd ? synth_normal(seed, stream, off + lane) : 0.f;
+    float v1 = lane + 64 < hd ? synth_normal(seed, stream, off + lane + 64) : 0.f;
+    const size_t hb = (size_t)slot * n_kv + h;
+    if (kv_fmt == KV_INT8) {
+        float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+        float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
+        int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.f), 127.f);
+        int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.f), 127.f);
+        uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
+        if (which == 0) {
+            int8_t* dst = (int8_t*)kc + (hb * cap + t) * hd;
+            if (lane < hd) dst[lane] = q0;
+            if (lane + 64 < hd) dst[lane + 64] = q1;
+            if (lane == 0) ks[hb * cap + t] = sh;
+        } else {
+            int8_t* dst = (int8_t*)vc + hb * hd * cap + t;
+            if (lane < hd) dst[(size_t)lane * cap] = q0;
+            if (lane + 64 < hd) dst[(size_t)(lane + 64) * cap] = q1;
+            if (lane == 0) vs[hb * cap + t] = sh;
+        }
+    } else if (kv_fmt == KV_F16) {
+        if (which == 0) {
+            _Float16* dst = (_Float16*)kc + (hb * cap + t) * hd;
+            if (lane < hd) dst[lane] = (_Float16)v0;
+            if (lane + 64 < hd) dst[lane + 64] = (_Float16)v1;
+        } else {
+            _Float16* dst = (_Float16*)vc + hb * hd * cap + t;
+            if (lane < hd) dst[(size_t)lane * cap] = (_Float16)v0;
+            if (lane + 64 < hd) dst[(size_t)(lane + 64) * cap] = (_Float16)v1;
+        }
+    } else {
+        if (which == 0) {
+            float* dst = (float*)kc + (hb * cap + t) * hd;
+            if (lane < hd) dst[lane] = v0;
+            if (lane + 64 < hd) dst[lane + 64] = v1;
+        } else {
+            float* dst = (float*)vc + hb * hd * cap + t;
+            if (lane < hd) dst[(size_t)lane * cap] = v0;
+            if (lane + 64 < hd) dst[(size_t)(lane + 64) * cap] = v1;
+        }
+    }
+}
+
+int launch_kv_fill_synthetic(void* kc, void* vc, uint16_t* ks, uint16_t* vs, int kv_fmt, int slot, int n_kv, int hd,
+                             int cap, int len, unsigned long long seed, int layer, hipStream_t stream) {
+    const int waves = len * n_kv * 2;
+    if (waves == 0) return 0;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(kv_fill_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, kc, vc, ks, vs, kv_fmt, slot,
+                       n_kv, hd, cap, len, seed, layer);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// argmax under f32::total_cmp keeping the last maximal index (sampler.rs:217-224),
+// plus the top-2 value gap (greedy near-tie measure).
+__global__ void argmax_rows_kernel(const float* x, long long ld, int V, int32_t* out, int out_stride, float* gap) {
+    __shared__ int rk[MT_THREADS / 64], ri[MT_THREADS / 64];
+    __shared__ float r1[MT_THREADS / 64], r2[MT_THREADS / 64];
+    const float* row = x + (size_t)blockIdx.x * ld;
+    int bk = INT_MIN, bi = 0;
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int j = threadIdx.x; j < V; j += blockDim.x) {
+        float v = row[j];
+        int k = total_key(v);
+        if (k >= bk) { bk = k; bi = j; }
+        if (v > t1) { t2 = t1; t1 = v; } else if (v > t2) { t2 = v; }
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
+        if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
+        float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
+        float n1 = fmaxf(t1, o1);
+        float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+        t1 = n1; t2 = n2;
+    }
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) { rk[wid] = bk; ri[wid] = bi; r1[wid] = t1; r2[wid] = t2; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int k0 = rk[0], i0 = ri[0];
+        float a1 = r1[0], a2 = r2[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) {
+            if (rk[w] > k0 || (rk[w] == k0 && ri[w] > i0)) { k0 = rk[w]; i0 = ri[w]; }
+            float n1 = fmaxf(a1, r1[w]);
+            float n2 = fmaxf(fminf(a1, r1[w]), fmaxf(a2, r2[w]));
+            a1 = n1; a2 = n2;
+        }
+        out[(size_t)blockIdx.x * out_stride] = i0;
+        if (gap) gap[blockIdx.x] = a1 - a2;
+    }
+}
+
+int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* out, int out_stride, float* gap,
+                       hipStream_t stream) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(MT_THREADS), 0, stream, x, ld, V, out, out_stride, gap);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Row copies given as device arrays of (src, dst) pointers: one workgroup per row.
+__global__ void copy_rows_kernel(const float* const* src, float* const* dst, int n) {
+    const float* s = src[blockIdx.x];
+    float* d = dst[blockIdx.x];
+    for (int k = threadIdx.x; k < n; k += blockDim.x) d[k] = s[k];
+}
+
+int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream) {
+    if (rows <= 0) return 0;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(rows), dim3(MT_THREADS), 0, stream, src, dst, n);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+__global__ void fill_f32_kernel(float* p, long long n, float v) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+int launch_fill_f32(float* p, long long n, float v, hipStream_t stream) {
+    if (n <= 0) return 0;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, n, v);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+}  // namespace aarh

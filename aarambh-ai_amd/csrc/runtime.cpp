@@ -1,0 +1,1433 @@
+// Host runtime of libaarambh_hip: context, device weights, KV cache, the
+// verify forward (layer loop over the gfx950 kernels), MTP heads, the MTP
+// speculative engine loop, and the C ABI declared in include/aarambh_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/aarambh_hip.h"
+#include "kernels.hpp"
+
+using namespace aarh;
+
+namespace {
+
+struct DevTensor {
+    int fmt = WF_F32;
+    int N = 0, K = 0;
+    uint8_t* w = nullptr;
+    uint32_t* sz = nullptr;
+    float* rscale = nullptr;
+};
+
+struct BlockW {
+    float* norm1 = nullptr;
+    float* norm2 = nullptr;
+    DevTensor qkv, wo, gu, down;
+};
+
+struct HeadW {
+    float* trunk = nullptr;
+    float* token = nullptr;
+    float* out_norm = nullptr;
+    BlockW blk;
+};
+
+// Tensor ids follow the reference checkpoint order (model.rs:82-279): embedding,
+// per layer [norm1, wq, wk, wv, wo, norm2, w_gate, w_up, w_down], final_norm,
+// per MTP head [trunk_norm, token_norm, refine.norm1, wq, wk, wv, wo,
+// refine.norm2, w_gate, w_up, w_down, output_norm].
+enum Part { P_EMBED, P_NORM, P_WQ, P_WK, P_WV, P_WO, P_GATE, P_UP, P_DOWN };
+struct TensorSlot {
+    std::string name;
+    int64_t rows = 0, cols = 0;
+    int kind = AARH_T_NORM;
+    Part part = P_NORM;
+    float** norm_ptr = nullptr;
+    BlockW* blk = nullptr;
+};
+
+struct ProfRec {
+    int cls;
+    hipEvent_t a, b;
+    double bytes;
+};
+
+}  // namespace
+
+struct aarh_ctx {
+    aarh_model_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int hd = 0, QD = 0, KD = 0, F = 0, Fp = 0, H = 0, V = 0, nheads_mtp = 0;
+    std::string err;
+
+    // weights
+    void* embed = nullptr;  // gather table, row-major [V][H] (f32 or bf16)
+    int embed_fmt = WF_F32;
+    DevTensor lm;           // tied LM head
+    std::vector<BlockW> layers;
+    float* final_norm = nullptr;
+    std::vector<HeadW> heads;
+    std::vector<TensorSlot> slots;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float* staging = nullptr;
+    size_t staging_elems = 0;
+
+    // KV cache
+    int cap = 0;
+    std::vector<void*> kc, vc;
+    std::vector<uint16_t*> ksc, vsc;
+    std::vector<int> kv_len;
+    void *mkc = nullptr, *mvc = nullptr;  // MTP local caches (f32)
+    int mcap = 0;
+
+    // scratch
+    int Mmax = 0;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *ssq_a = nullptr, *ssq_b = nullptr;
+    float *hidden = nullptr, *logits = nullptr, *part = nullptr, *apart = nullptr, *hn = nullptr;
+    size_t part_elems = 0, apart_elems = 0;
+    unsigned *gcnt = nullptr, *acnt = nullptr;
+    int32_t *d_pos0 = nullptr, *d_slot = nullptr, *d_zero = nullptr, *d_seqidx = nullptr;
+    uint32_t* d_ids = nullptr;
+    int32_t *h_pos0 = nullptr, *h_slot = nullptr;
+    uint32_t* h_ids = nullptr;
+    // acceptance scratch
+    float *acc_max = nullptr, *acc_sum = nullptr;
+    int32_t* acc_argmax = nullptr;
+    unsigned* acc_cnt = nullptr;
+    int acc_rows_cap = 0, acc_seq_cap = 0;
+
+    // profiling
+    bool prof = false;
+    std::vector<ProfRec> prof_recs;
+    std::vector<hipEvent_t> ev_pool;
+    double prof_ms[AARH_PROF_COUNT] = {0};
+    double prof_bytes[AARH_PROF_COUNT] = {0};
+    int64_t prof_n[AARH_PROF_COUNT] = {0};
+};
+
+namespace {
+
+int fail(aarh_ctx* c, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    return code;
+}
+
+#define HIPCHK(c, call)                                                                        \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess) return fail((c), AARH_ERR_DEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+#define KCHK(c, call)                                                                          \
+    do {                                                                                       \
+        int r_ = (call);                                                                       \
+        if (r_ != 0) return fail((c), r_, "kernel launch failed: %s (code %d: %s)", #call, r_, last_launch_error()); \
+    } while (0)
+
+template <class T>
+int dalloc(aarh_ctx* c, T** p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc((void**)p, bytes);
+    if (e != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return 0;
+}
+
+size_t weight_bytes(int fmt, int64_t N, int64_t K) {
+    switch (fmt) {
+        case WF_INT4: return (size_t)(N * K / 2);
+        case WF_INT8: return (size_t)(N * K);
+        case WF_BF16: return (size_t)(N * K * 2);
+        default: return (size_t)(N * K * 4);
+    }
+}
+
+// Algorithmic bytes a launch must move: quantised weights and their scales.
+double alg_weight_bytes(const DevTensor& t) {
+    double b = (double)weight_bytes(t.fmt, t.N, t.K);
+    if (t.fmt == WF_INT4) b += (double)t.N * (t.K / 128) * 4.0;
+    if (t.fmt == WF_INT8) b += (double)t.N * 4.0;
+    return b;
+}
+
+int alloc_tensor(aarh_ctx* c, DevTensor& t, int fmt, int N, int K) {
+    t.fmt = fmt;
+    t.N = N;
+    t.K = K;
+    if (dalloc(c, &t.w, weight_bytes(fmt, N, K))) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipMemset(t.w, 0, weight_bytes(fmt, N, K)));
+    if (fmt == WF_INT4) {
+        size_t n = (size_t)N / 16 * (K / 128) * 16;
+        if (dalloc(c, &t.sz, n * 4)) return AARH_ERR_DEVICE;
+        // scale 1.0, zero 0 for never-loaded rows (fp16 0x3C00)
+        std::vector<uint32_t> ones(n, 0x3C00u);
+        HIPCHK(c, hipMemcpy(t.sz, ones.data(), n * 4, hipMemcpyHostToDevice));
+    }
+    if (fmt == WF_INT8) {
+        if (dalloc(c, &t.rscale, (size_t)N * 4)) return AARH_ERR_DEVICE;
+        std::vector<float> ones(N, 1.0f);
+        HIPCHK(c, hipMemcpy(t.rscale, ones.data(), (size_t)N * 4, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+void free_tensor(DevTensor& t) {
+    if (t.w) (void)hipFree(t.w);
+    if (t.sz) (void)hipFree(t.sz);
+    if (t.rscale) (void)hipFree(t.rscale);
+    t = DevTensor{};
+}
+
+// k-splits per 128-row group: enough workgroups to cover 256 CUs twice, each
+// with >= 2 K-groups when possible, activation tile within a 64 KiB LDS budget.
+int choose_S(const DevTensor& t, int M, int split) {
+    const int G = t.K / 128, nrg = t.N / 128;
+    int gmax;
+    if (t.fmt == WF_F32) {
+        long long kr = (160LL * 1024 - (long long)M * 516) / (4LL * M);
+        gmax = (int)std::max(1LL, kr / 128);
+    } else {
+        const int MT = split ? (M + 7) / 8 : (M + 15) / 16;
+        long long kr = 65536LL / (MT * 32) - 8;
+        gmax = (int)std::max(1LL, kr / 128);
+    }
+    int s_min = (G + gmax - 1) / gmax;
+    int s_par = (512 + nrg - 1) / nrg;
+    int S = std::max(s_min, std::min(s_par, std::max(1, G / 2)));
+    return std::min(std::max(S, 1), G);
+}
+
+hipEvent_t take_event(aarh_ctx* c) {
+    if (!c->ev_pool.empty()) {
+        hipEvent_t e = c->ev_pool.back();
+        c->ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+struct ProfScope {
+    aarh_ctx* c;
+    int cls;
+    double bytes;
+    hipEvent_t a = nullptr;
+    ProfScope(aarh_ctx* c_, int cls_, double bytes_) : c(c_), cls(cls_), bytes(bytes_) {
+        if (c->prof) {
+            a = take_event(c);
+            (void)hipEventRecord(a, c->stream);
+        }
+    }
+    ~ProfScope() {
+        if (c->prof) {
+            hipEvent_t b = take_event(c);
+            (void)hipEventRecord(b, c->stream);
+            c->prof_recs.push_back({cls, a, b, bytes});
+        }
+    }
+};
+
+int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, const float* norm_w,
+         const float* ssq, float* hidden_out, int epi, float* out, RowMap omap, float* resid, int ldr,
+         float* ssq_out, const QkvEpi* qkv, int cls) {
+    GemvArgs a{};
+    a.fmt = t.fmt;
+    a.w = t.w;
+    a.sz = t.sz;
+    a.rscale = t.rscale;
+    a.N = t.N;
+    a.K = t.K;
+    a.M = M;
+    a.split = t.fmt != WF_F32 ? 1 : 0;  // hi+lo activation rows keep ~22-bit products at any M
+    a.S = choose_S(t, M, a.split);
+    a.x = x;
+    a.xmap = xmap;
+    a.norm_w = norm_w;
+    a.ssq_part = ssq;
+    a.n_ssq = c->H / 128;
+    a.eps = c->cfg.norm_eps;
+    a.hidden_out = hidden_out;
+    a.part = c->part;
+    a.counters = c->gcnt;
+    a.epi = epi;
+    a.out = out;
+    a.omap = omap;
+    a.resid = resid;
+    a.ldr = ldr;
+    a.ssq_out = ssq_out;
+    if (qkv) a.qkv = *qkv;
+    if ((size_t)a.S * M * t.N > c->part_elems)
+        return fail(c, AARH_ERR_SHAPE, "split-K scratch too small (S=%d M=%d N=%d)", a.S, M, t.N);
+    ProfScope ps(c, cls, alg_weight_bytes(t));
+    int r = launch_gemv(a, c->stream);
+    if (r) return fail(c, r, "gemv launch failed (fmt %d N %d K %d M %d S %d): code %d %s", t.fmt, t.N, t.K, M, a.S, r,
+                       last_launch_error());
+    return 0;
+}
+
+RowMap rm(int S, long long seq_stride, long long row_stride) {
+    RowMap r;
+    r.S = S;
+    r.seq_stride = seq_stride;
+    r.row_stride = row_stride;
+    return r;
+}
+
+// One transformer block (block.rs:331-350) over M = nseq * S rows whose
+// residual stream is c->x and whose ssq partials for norm1 are in c->ssq_a.
+int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_pos0, const int32_t* d_slot,
+              int kv_fmt, int cap, void* kc, void* vc, uint16_t* ks, uint16_t* vs, int max_kv_len) {
+    const int M = nseq * S, H = c->H;
+    QkvEpi e{};
+    e.n_heads = c->cfg.n_heads;
+    e.n_kv = c->cfg.n_kv_heads;
+    e.hd = c->hd;
+    e.pos0 = d_pos0;
+    e.slot = d_slot;
+    e.rope_cos = c->rope_cos;
+    e.rope_sin = c->rope_sin;
+    e.q_out = c->q;
+    e.kv_fmt = kv_fmt;
+    e.cap = cap;
+    e.kc = kc;
+    e.vc = vc;
+    e.ks = ks;
+    e.vs = vs;
+    int r;
+    if ((r = gemv(c, w.qkv, M, c->x, rm(M, 0, H), w.norm1, c->ssq_a, nullptr, EPI_QKV, nullptr, rm(S, 0, 0),
+                  nullptr, 0, nullptr, &e, AARH_PROF_GEMV_QKV)))
+        return r;
+    // attention
+    AttnArgs at{};
+    at.nseq = nseq;
+    at.S = S;
+    at.n_heads = c->cfg.n_heads;
+    at.n_kv = c->cfg.n_kv_heads;
+    at.hd = c->hd;
+    at.pos0 = d_pos0;
+    at.slot = d_slot;
+    at.q = c->q;
+    at.kv_fmt = kv_fmt;
+    at.cap = cap;
+    at.kc = kc;
+    at.vc = vc;
+    at.ks = ks;
+    at.vs = vs;
+    at.scale = (float)(1.0 / std::sqrt((double)c->hd));
+    const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
+    const int Rt = S * G;
+    at.rows_per_tile = std::min(32, Rt);
+    at.ntiles = (Rt + at.rows_per_tile - 1) / at.rows_per_tile;
+    const int base = nseq * c->cfg.n_kv_heads * at.ntiles;
+    const int max_chunks = std::max(1, (max_kv_len + 63) / 64);
+    int nch = std::max(1, std::min(max_chunks, (512 + base - 1) / base));
+    int chunk = ((max_kv_len + nch - 1) / nch + 63) / 64 * 64;
+    nch = (max_kv_len + chunk - 1) / chunk;
+    at.chunk = chunk;
+    at.nchunks = nch;
+    size_t need = (size_t)base * nch * 32 * (c->hd + 2);
+    if (need > c->apart_elems) return fail(c, AARH_ERR_SHAPE, "attention scratch too small");
+    at.part = c->apart;
+    at.counters = c->acnt;
+    at.out = c->att;
+    {
+        double kvb = 0;
+        if (kv_fmt == KV_INT8) kvb = (double)max_kv_len * nseq * c->cfg.n_kv_heads * (2.0 * c->hd + 4.0);
+        else kvb = (double)max_kv_len * nseq * c->cfg.n_kv_heads * 2.0 * c->hd * (kv_fmt == KV_F16 ? 2 : 4);
+        ProfScope ps(c, AARH_PROF_ATTENTION, kvb);
+        KCHK(c, launch_attention(at, c->stream));
+    }
+    if ((r = gemv(c, w.wo, M, c->att, rm(M, 0, c->QD), nullptr, nullptr, nullptr, EPI_RESID, nullptr, rm(1, 0, 0),
+                  c->x, H, c->ssq_b, nullptr, AARH_PROF_GEMV_WO)))
+        return r;
+    if ((r = gemv(c, w.gu, M, c->x, rm(M, 0, H), w.norm2, c->ssq_b, nullptr, EPI_SWIGLU, c->h, rm(M, 0, c->Fp),
+                  nullptr, 0, nullptr, nullptr, AARH_PROF_GEMV_GATEUP)))
+        return r;
+    if ((r = gemv(c, w.down, M, c->h, rm(M, 0, c->Fp), nullptr, nullptr, nullptr, EPI_RESID, nullptr, rm(1, 0, 0),
+                  c->x, H, c->ssq_a, nullptr, AARH_PROF_GEMV_DOWN)))
+        return r;
+    return 0;
+}
+
+// forward_with_cache_output on device: ids/pos0/slot are device arrays for
+// nseq sequences x S tokens; logits go to `lout` via `lmap`, normed hidden to
+// `hout` ([M][H]) when non-null.  max_kv_len = max(pos0) + S.
+int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const int32_t* d_slot, int nseq, int S,
+                int max_kv_len, float* lout, RowMap lmap, float* hout) {
+    const int M = nseq * S, H = c->H;
+    if (M > c->Mmax) return fail(c, AARH_ERR_SHAPE, "rows %d exceed max_rows %d", M, c->Mmax);
+    {
+        ProfScope ps(c, AARH_PROF_OTHER, 0);
+        KCHK(c, launch_embed(c->embed, c->embed_fmt, H, d_ids, M, c->x, c->ssq_a, c->stream));
+    }
+    for (int l = 0; l < c->cfg.n_layers; l++) {
+        int r = run_block(c, c->layers[l], nseq, S, d_pos0, d_slot, c->cfg.kv_format, c->cap, c->kc[l], c->vc[l],
+                          c->ksc[l], c->vsc[l], max_kv_len);
+        if (r) return r;
+    }
+    return gemv(c, c->lm, M, c->x, rm(M, 0, H), c->final_norm, c->ssq_a, hout, EPI_STORE, lout, lmap, nullptr, 0,
+                nullptr, nullptr, AARH_PROF_GEMV_LMHEAD);
+}
+
+// forward_mtp_head on device for nseq sequences: anchor rows (stride), ids
+// [nseq][ids_stride] (first head+1 used); logits row of seq j -> lout + j*lstride.
+int mtp_head_dev(aarh_ctx* c, int head, const float* d_anchor, long long anchor_stride, const uint32_t* d_ids,
+                 int ids_stride, int nseq, float* lout, long long lstride) {
+    if (head < 0 || head >= c->nheads_mtp) return fail(c, AARH_ERR_CONFIG, "MTP head index %d is not configured", head);
+    const int L = head + 2, H = c->H;
+    if (nseq * L > c->Mmax) return fail(c, AARH_ERR_SHAPE, "MTP rows exceed max_rows");
+    const HeadW& hw = c->heads[head];
+    {
+        ProfScope ps(c, AARH_PROF_OTHER, 0);
+        KCHK(c, launch_mtp_prep(d_anchor, anchor_stride, c->embed, c->embed_fmt, d_ids, ids_stride, nseq, L, H, hw.trunk,
+                                hw.token, c->cfg.norm_eps, c->x, c->ssq_a, c->stream));
+    }
+    // local cache slots 0..nseq-1 at positions 0..L-1 (no KV cache: mtp.rs:104-114)
+    int r = run_block(c, hw.blk, nseq, L, c->d_zero, c->d_seqidx, KV_F32, c->mcap, c->mkc, c->mvc, nullptr, nullptr, L);
+    if (r) return r;
+    {
+        ProfScope ps(c, AARH_PROF_OTHER, 0);
+        KCHK(c, launch_norm_rows(c->x + (size_t)(L - 1) * H, rm(1, (long long)L * H, 0), nseq, H, hw.out_norm,
+                                 c->cfg.norm_eps, c->hn, c->stream));
+    }
+    // LM head without a norm prologue on the normalised last rows
+    DevTensor lm = c->lm;
+    return gemv(c, lm, nseq, c->hn, rm(nseq, 0, H), nullptr, nullptr, nullptr, EPI_STORE, lout, rm(1, lstride, 0),
+                nullptr, 0, nullptr, nullptr, AARH_PROF_GEMV_LMHEAD);
+}
+
+int sync_stream(aarh_ctx* c) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* aarh_last_error(const aarh_ctx* c) { return c ? c->err.c_str() : "null context"; }
+void* aarh_stream(aarh_ctx* c) { return c ? (void*)c->stream : nullptr; }
+int aarh_sync(aarh_ctx* c) { return sync_stream(c); }
+
+void aarh_destroy(aarh_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    auto F = [](void* p) {
+        if (p) (void)hipFree(p);
+    };
+    F(c->embed);
+    if (c->lm.w != c->embed) free_tensor(c->lm);
+    for (auto& b : c->layers) {
+        F(b.norm1);
+        F(b.norm2);
+        free_tensor(b.qkv);
+        free_tensor(b.wo);
+        free_tensor(b.gu);
+        free_tensor(b.down);
+    }
+    F(c->final_norm);
+    for (auto& h : c->heads) {
+        F(h.trunk);
+        F(h.token);
+        F(h.out_norm);
+        F(h.blk.norm1);
+        F(h.blk.norm2);
+        free_tensor(h.blk.qkv);
+        free_tensor(h.blk.wo);
+        free_tensor(h.blk.gu);
+        free_tensor(h.blk.down);
+    }
+    F(c->rope_cos);
+    F(c->rope_sin);
+    F(c->staging);
+    for (size_t i = 0; i < c->kc.size(); i++) {
+        F(c->kc[i]);
+        F(c->vc[i]);
+        F(c->ksc[i]);
+        F(c->vsc[i]);
+    }
+    F(c->mkc);
+    F(c->mvc);
+    for (void* p : {(void*)c->x, (void*)c->q, (void*)c->att, (void*)c->h, (void*)c->ssq_a, (void*)c->ssq_b,
+                    (void*)c->hidden, (void*)c->logits, (void*)c->part, (void*)c->apart, (void*)c->hn, (void*)c->gcnt,
+                    (void*)c->acnt, (void*)c->d_pos0, (void*)c->d_slot, (void*)c->d_zero, (void*)c->d_seqidx,
+                    (void*)c->d_ids, (void*)c->acc_max, (void*)c->acc_sum, (void*)c->acc_argmax, (void*)c->acc_cnt})
+        F(p);
+    if (c->h_pos0) (void)hipHostFree(c->h_pos0);
+    if (c->h_slot) (void)hipHostFree(c->h_slot);
+    if (c->h_ids) (void)hipHostFree(c->h_ids);
+    for (auto& r : c->prof_recs) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+static int build_slots(aarh_ctx* c) {
+    const auto& g = c->cfg;
+    const int64_t H = g.hidden_dim, F = g.ffn_dim, QD = c->QD, KD = c->KD;
+    auto add = [&](const std::string& n, int64_t r, int64_t cc, int kind, Part p, float** np, BlockW* b) {
+        TensorSlot s;
+        s.name = n;
+        s.rows = r;
+        s.cols = cc;
+        s.kind = kind;
+        s.part = p;
+        s.norm_ptr = np;
+        s.blk = b;
+        c->slots.push_back(s);
+    };
+    add("embedding.weight", g.vocab_size, H, AARH_T_EMBED, P_EMBED, nullptr, nullptr);
+    for (int l = 0; l < g.n_layers; l++) {
+        BlockW* b = &c->layers[l];
+        std::string p = "blocks." + std::to_string(l) + ".";
+        add(p + "norm1.weight", 1, H, AARH_T_NORM, P_NORM, &b->norm1, b);
+        add(p + "attn.wq.weight", QD, H, AARH_T_LINEAR, P_WQ, nullptr, b);
+        add(p + "attn.wk.weight", KD, H, AARH_T_LINEAR, P_WK, nullptr, b);
+        add(p + "attn.wv.weight", KD, H, AARH_T_LINEAR, P_WV, nullptr, b);
+        add(p + "attn.wo.weight", H, QD, AARH_T_LINEAR, P_WO, nullptr, b);
+        add(p + "norm2.weight", 1, H, AARH_T_NORM, P_NORM, &b->norm2, b);
+        add(p + "ffn.w_gate.weight", F, H, AARH_T_LINEAR, P_GATE, nullptr, b);
+        add(p + "ffn.w_up.weight", F, H, AARH_T_LINEAR, P_UP, nullptr, b);
+        add(p + "ffn.w_down.weight", H, F, AARH_T_LINEAR, P_DOWN, nullptr, b);
+    }
+    add("final_norm.weight", 1, H, AARH_T_NORM, P_NORM, &c->final_norm, nullptr);
+    for (int h = 0; h < c->nheads_mtp; h++) {
+        HeadW* hw = &c->heads[h];
+        BlockW* b = &hw->blk;
+        std::string p = "mtp.heads." + std::to_string(h) + ".";
+        add(p + "trunk_norm.weight", 1, H, AARH_T_NORM, P_NORM, &hw->trunk, nullptr);
+        add(p + "token_norm.weight", 1, H, AARH_T_NORM, P_NORM, &hw->token, nullptr);
+        add(p + "refine.norm1.weight", 1, H, AARH_T_NORM, P_NORM, &b->norm1, b);
+        add(p + "refine.attn.wq.weight", QD, H, AARH_T_LINEAR, P_WQ, nullptr, b);
+        add(p + "refine.attn.wk.weight", KD, H, AARH_T_LINEAR, P_WK, nullptr, b);
+        add(p + "refine.attn.wv.weight", KD, H, AARH_T_LINEAR, P_WV, nullptr, b);
+        add(p + "refine.attn.wo.weight", H, QD, AARH_T_LINEAR, P_WO, nullptr, b);
+        add(p + "refine.norm2.weight", 1, H, AARH_T_NORM, P_NORM, &b->norm2, b);
+        add(p + "refine.ffn.w_gate.weight", F, H, AARH_T_LINEAR, P_GATE, nullptr, b);
+        add(p + "refine.ffn.w_up.weight", F, H, AARH_T_LINEAR, P_UP, nullptr, b);
+        add(p + "refine.ffn.w_down.weight", H, F, AARH_T_LINEAR, P_DOWN, nullptr, b);
+        add(p + "output_norm.weight", 1, H, AARH_T_NORM, P_NORM, &hw->out_norm, nullptr);
+    }
+    return 0;
+}
+
+static int alloc_block(aarh_ctx* c, BlockW& b) {
+    const int fmt = c->cfg.weight_format, H = c->H;
+    if (dalloc(c, &b.norm1, H * 4) || dalloc(c, &b.norm2, H * 4)) return AARH_ERR_DEVICE;
+    KCHK(c, launch_fill_f32(b.norm1, H, 1.0f, c->stream));
+    KCHK(c, launch_fill_f32(b.norm2, H, 1.0f, c->stream));
+    int r;
+    if ((r = alloc_tensor(c, b.qkv, fmt, c->QD + 2 * c->KD, H))) return r;
+    if ((r = alloc_tensor(c, b.wo, fmt, H, c->QD))) return r;
+    if ((r = alloc_tensor(c, b.gu, fmt, 2 * c->Fp, H))) return r;
+    if ((r = alloc_tensor(c, b.down, fmt, H, c->Fp))) return r;
+    return 0;
+}
+
+int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
+    if (!cfg || !out) return AARH_ERR_CONFIG;
+    *out = nullptr;
+    aarh_ctx* c = new aarh_ctx();
+    c->cfg = *cfg;
+    c->device = device;
+    const auto& g = *cfg;
+    auto bad = [&](int code, const char* msg) {
+        c->err = msg;
+        *out = c;
+        return code;
+    };
+    if (g.vocab_size <= 0 || g.hidden_dim <= 0 || g.ffn_dim <= 0 || g.n_layers <= 0 || g.n_heads <= 0 ||
+        g.n_kv_heads <= 0 || g.max_seq_len <= 0 || g.max_batch <= 0 || g.max_rows <= 0)
+        return bad(AARH_ERR_CONFIG, "model dimensions must be non-zero");
+    if (g.hidden_dim % g.n_heads || g.n_heads % g.n_kv_heads)
+        return bad(AARH_ERR_CONFIG, "hidden_dim must divide by n_heads and n_heads by n_kv_heads");
+    c->H = g.hidden_dim;
+    c->V = g.vocab_size;
+    c->hd = g.hidden_dim / g.n_heads;
+    c->QD = g.n_heads * c->hd;
+    c->KD = g.n_kv_heads * c->hd;
+    c->F = g.ffn_dim;
+    c->nheads_mtp = g.num_future_tokens > 1 ? g.num_future_tokens - 1 : 0;
+    if (c->hd > 128 || 128 % c->hd || c->hd % 2) return bad(AARH_ERR_UNSUPPORTED, "head_dim must divide 128");
+    if (c->H % 128 || c->V % 128 || (c->QD + 2 * c->KD) % 128)
+        return bad(AARH_ERR_UNSUPPORTED, "hidden, vocab and q+k+v widths must be multiples of 128");
+    if (g.weight_format != AARH_W_F32 && g.ffn_dim % 128)
+        return bad(AARH_ERR_UNSUPPORTED, "quantised ffn_dim must be a multiple of 128");
+    if (g.weight_format < 0 || g.weight_format > 3 || (g.lm_head_format != 0 && g.lm_head_format != 1) ||
+        g.kv_format < 0 || g.kv_format > 2)
+        return bad(AARH_ERR_CONFIG, "unknown weight / lm head / kv format");
+    if (g.max_rows > 128) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 128");
+    c->Fp = (c->F + 127) / 128 * 128;
+    c->Mmax = g.max_rows;
+    c->cap = g.max_seq_len;
+    *out = c;
+    if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+    HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    c->layers.resize(g.n_layers);
+    c->heads.resize(c->nheads_mtp);
+    build_slots(c);
+    int r;
+    // embedding / LM head
+    c->embed_fmt = g.lm_head_format == 1 ? WF_BF16 : WF_F32;
+    if (dalloc(c, (uint8_t**)&c->embed, weight_bytes(c->embed_fmt, c->V, c->H))) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipMemset(c->embed, 0, weight_bytes(c->embed_fmt, c->V, c->H)));
+    if (c->embed_fmt == WF_F32) {
+        c->lm.fmt = WF_F32;
+        c->lm.N = c->V;
+        c->lm.K = c->H;
+        c->lm.w = (uint8_t*)c->embed;  // row-major f32 weights are shared
+    } else if ((r = alloc_tensor(c, c->lm, WF_BF16, c->V, c->H))) {
+        return r;
+    }
+    for (auto& b : c->layers)
+        if ((r = alloc_block(c, b))) return r;
+    if (dalloc(c, &c->final_norm, c->H * 4)) return AARH_ERR_DEVICE;
+    KCHK(c, launch_fill_f32(c->final_norm, c->H, 1.0f, c->stream));
+    for (auto& h : c->heads) {
+        if ((r = alloc_block(c, h.blk))) return r;
+        if (dalloc(c, &h.trunk, c->H * 4) || dalloc(c, &h.token, c->H * 4) || dalloc(c, &h.out_norm, c->H * 4))
+            return AARH_ERR_DEVICE;
+        KCHK(c, launch_fill_f32(h.trunk, c->H, 1.0f, c->stream));
+        KCHK(c, launch_fill_f32(h.token, c->H, 1.0f, c->stream));
+        KCHK(c, launch_fill_f32(h.out_norm, c->H, 1.0f, c->stream));
+    }
+    // RoPE tables (rope_scaling.rs:6-11, rope.rs:43-72), computed on the host in f32 like the reference.
+    {
+        const int half = c->hd / 2;
+        std::vector<float> cs((size_t)g.max_seq_len * half), sn((size_t)g.max_seq_len * half), inv(half);
+        for (int i = 0; i < half; i++)
+            inv[i] = (float)(1.0 / std::pow((double)g.rope_theta, 2.0 * (double)i / (double)c->hd));
+        for (int p = 0; p < g.max_seq_len; p++)
+            for (int i = 0; i < half; i++) {
+                float a = (float)p * inv[i];
+                cs[(size_t)p * half + i] = cosf(a);
+                sn[(size_t)p * half + i] = sinf(a);
+            }
+        if (dalloc(c, &c->rope_cos, cs.size() * 4) || dalloc(c, &c->rope_sin, sn.size() * 4)) return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    }
+    // KV cache
+    {
+        const size_t esz = g.kv_format == AARH_KV_INT8 ? 1 : (g.kv_format == AARH_KV_F16 ? 2 : 4);
+        const size_t per = (size_t)g.max_batch * g.n_kv_heads * c->cap * c->hd * esz;
+        const size_t sper = (size_t)g.max_batch * g.n_kv_heads * c->cap * 2;
+        c->kc.resize(g.n_layers);
+        c->vc.resize(g.n_layers);
+        c->ksc.assign(g.n_layers, nullptr);
+        c->vsc.assign(g.n_layers, nullptr);
+        for (int l = 0; l < g.n_layers; l++) {
+            if (dalloc(c, (uint8_t**)&c->kc[l], per) || dalloc(c, (uint8_t**)&c->vc[l], per)) return AARH_ERR_DEVICE;
+            HIPCHK(c, hipMemset(c->kc[l], 0, per));
+            HIPCHK(c, hipMemset(c->vc[l], 0, per));
+            if (g.kv_format == AARH_KV_INT8) {
+                if (dalloc(c, &c->ksc[l], sper) || dalloc(c, &c->vsc[l], sper)) return AARH_ERR_DEVICE;
+                HIPCHK(c, hipMemset(c->ksc[l], 0, sper));
+                HIPCHK(c, hipMemset(c->vsc[l], 0, sper));
+            }
+        }
+        c->kv_len.assign(g.max_batch, 0);
+        c->mcap = std::max(2, g.num_future_tokens + 1);
+        const size_t mper = (size_t)c->Mmax * g.n_kv_heads * c->mcap * c->hd * 4;
+        if (dalloc(c, (uint8_t**)&c->mkc, mper) || dalloc(c, (uint8_t**)&c->mvc, mper)) return AARH_ERR_DEVICE;
+    }
+    // scratch
+    {
+        const int M = c->Mmax;
+        const size_t H = c->H;
+        if (dalloc(c, &c->x, M * H * 4) || dalloc(c, &c->q, (size_t)M * c->QD * 4) ||
+            dalloc(c, &c->att, (size_t)M * c->QD * 4) || dalloc(c, &c->h, (size_t)M * c->Fp * 4) ||
+            dalloc(c, &c->ssq_a, (H / 128) * M * 4) || dalloc(c, &c->ssq_b, (H / 128) * M * 4) ||
+            dalloc(c, &c->hidden, M * H * 4) || dalloc(c, &c->hn, M * H * 4) ||
+            dalloc(c, &c->logits, (size_t)M * c->V * 4))
+            return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(c->h, 0, (size_t)M * c->Fp * 4));
+        // split-K scratch: the largest S*M*N over the model's matrices and row counts
+        size_t pe = 0;
+        auto consider = [&](const DevTensor& t) {
+            for (int m = 1; m <= M; m++) {
+                int split = t.fmt != WF_F32 ? 1 : 0;
+                pe = std::max(pe, (size_t)choose_S(t, m, split) * m * t.N);
+            }
+        };
+        if (!c->layers.empty()) {
+            const BlockW& b = c->layers[0];
+            consider(b.qkv);
+            consider(b.wo);
+            consider(b.gu);
+            consider(b.down);
+        }
+        consider(c->lm);
+        c->part_elems = pe;
+        if (dalloc(c, &c->part, pe * 4)) return AARH_ERR_DEVICE;
+        const int maxrg = std::max({c->V, 2 * c->Fp, c->QD + 2 * c->KD, c->H}) / 128;
+        if (dalloc(c, &c->gcnt, (size_t)maxrg * 4)) return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(c->gcnt, 0, (size_t)maxrg * 4));
+        // attention scratch: groups = nseq*n_kv*ntiles <= n_kv*(M + M*G/32); the chunk count
+        // is at most ceil(512/groups) so groups*chunks <= groups + 512.
+        const int G = g.n_heads / g.n_kv_heads;
+        const size_t groups = (size_t)g.n_kv_heads * ((size_t)M + ((size_t)M * G + 31) / 32);
+        c->apart_elems = (groups + 512) * 32 * (c->hd + 2);
+        if (dalloc(c, &c->apart, c->apart_elems * 4)) return AARH_ERR_DEVICE;
+        if (dalloc(c, &c->acnt, groups * 4)) return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(c->acnt, 0, groups * 4));
+        if (dalloc(c, &c->d_pos0, M * 4) || dalloc(c, &c->d_slot, M * 4) || dalloc(c, &c->d_zero, M * 4) ||
+            dalloc(c, &c->d_seqidx, M * 4) || dalloc(c, &c->d_ids, M * 4))
+            return AARH_ERR_DEVICE;
+        std::vector<int32_t> zero(M, 0), idx(M);
+        for (int i = 0; i < M; i++) idx[i] = i;
+        HIPCHK(c, hipMemcpy(c->d_zero, zero.data(), M * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy(c->d_seqidx, idx.data(), M * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipHostMalloc((void**)&c->h_pos0, M * 4, 0));
+        HIPCHK(c, hipHostMalloc((void**)&c->h_slot, M * 4, 0));
+        HIPCHK(c, hipHostMalloc((void**)&c->h_ids, (size_t)M * 4, 0));
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return AARH_OK;
+}
+
+int aarh_num_tensors(const aarh_ctx* c) { return (int)c->slots.size(); }
+
+int aarh_tensor_info(const aarh_ctx* c, int id, char* name, int name_cap, int64_t* rows, int64_t* cols,
+                     int32_t* kind) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return AARH_ERR_SHAPE;
+    const TensorSlot& s = c->slots[id];
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", s.name.c_str());
+    if (rows) *rows = s.rows;
+    if (cols) *cols = s.cols;
+    if (kind) *kind = s.kind;
+    return AARH_OK;
+}
+
+static int ensure_staging(aarh_ctx* c, size_t elems) {
+    if (elems <= c->staging_elems) return 0;
+    if (c->staging) {
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        (void)hipFree(c->staging);
+        c->staging = nullptr;
+    }
+    if (dalloc(c, &c->staging, elems * 4)) return AARH_ERR_DEVICE;
+    c->staging_elems = elems;
+    return 0;
+}
+
+// Destination tensor, row offset and interleave mode of a linear part.
+static void part_target(aarh_ctx* c, const TensorSlot& s, DevTensor** t, int* row_off, int* inter) {
+    BlockW* b = s.blk;
+    *row_off = 0;
+    *inter = 0;
+    switch (s.part) {
+        case P_WQ: *t = &b->qkv; break;
+        case P_WK: *t = &b->qkv; *row_off = c->QD; break;
+        case P_WV: *t = &b->qkv; *row_off = c->QD + c->KD; break;
+        case P_WO: *t = &b->wo; break;
+        case P_GATE: *t = &b->gu; *inter = 1; break;
+        case P_UP: *t = &b->gu; *inter = 2; break;
+        default: *t = &b->down; break;
+    }
+}
+
+// Upload one tensor already resident in c->staging (f32, reference shape).
+static int place_f32_staging(aarh_ctx* c, int id) {
+    const TensorSlot& s = c->slots[id];
+    const int64_t n = s.rows * s.cols;
+    if (s.part == P_EMBED) {
+        if (c->embed_fmt == WF_F32) {
+            HIPCHK(c, hipMemcpyAsync(c->embed, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
+        } else {
+            KCHK(c, launch_to_bf16(c->staging, (uint16_t*)c->embed, n, c->stream));
+            KCHK(c, launch_quantise_tiled(c->staging, c->V, c->H, WF_BF16, c->lm.w, nullptr, nullptr, 0, c->V, 0,
+                                          c->stream));
+        }
+        return 0;
+    }
+    if (s.part == P_NORM) {
+        HIPCHK(c, hipMemcpyAsync(*s.norm_ptr, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
+        return 0;
+    }
+    DevTensor* t;
+    int ro, inter;
+    part_target(c, s, &t, &ro, &inter);
+    if (s.part == P_DOWN && c->Fp != c->F) {
+        // pad K (ffn) to a multiple of 128 with zero columns (f32 weights only);
+        // callers reserve n + rows*Fp staging elements
+        if ((size_t)n + (size_t)s.rows * c->Fp > c->staging_elems) return fail(c, AARH_ERR_SHAPE, "staging too small");
+        float* padded = c->staging + n;
+        HIPCHK(c, hipMemsetAsync(padded, 0, (size_t)s.rows * c->Fp * 4, c->stream));
+        HIPCHK(c, hipMemcpy2DAsync(padded, (size_t)c->Fp * 4, c->staging, (size_t)c->F * 4, (size_t)c->F * 4,
+                                   (size_t)s.rows, hipMemcpyDeviceToDevice, c->stream));
+        KCHK(c, launch_quantise_tiled(padded, (int)s.rows, c->Fp, t->fmt, t->w, t->sz, t->rscale, ro, t->N, inter,
+                                      c->stream));
+        return 0;
+    }
+    KCHK(c, launch_quantise_tiled(c->staging, (int)s.rows, (int)s.cols, t->fmt, t->w, t->sz, t->rscale, ro, t->N,
+                                  inter, c->stream));
+    return 0;
+}
+
+int aarh_load_tensor_f32(aarh_ctx* c, int id, const float* host, int64_t numel) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
+    const TensorSlot& s = c->slots[id];
+    if (numel != s.rows * s.cols)
+        return fail(c, AARH_ERR_SHAPE, "tensor %s expects %lld values, got %lld", s.name.c_str(),
+                    (long long)(s.rows * s.cols), (long long)numel);
+    // room for the zero-padded copy of a down projection whose ffn width is not a multiple of 128
+    const size_t extra = s.part == P_DOWN ? (size_t)s.rows * c->Fp : 0;
+    if (ensure_staging(c, (size_t)numel + extra)) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(c->staging, host, numel * 4, hipMemcpyHostToDevice));
+    int r = place_f32_staging(c, id);
+    if (r) return r;
+    return sync_stream(c);
+}
+
+int aarh_load_tensor_int4(aarh_ctx* c, int id, const uint8_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                          int64_t rows, int64_t cols, int32_t group) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
+    const TensorSlot& s = c->slots[id];
+    if (s.kind != AARH_T_LINEAR || c->cfg.weight_format != AARH_W_INT4_G128)
+        return fail(c, AARH_ERR_UNSUPPORTED, "tensor %s is not an INT4 g128 linear in this model", s.name.c_str());
+    if (rows != s.rows || cols != s.cols || group != 128 || cols % 128)
+        return fail(c, AARH_ERR_SHAPE, "INT4 tensor %s shape/group mismatch", s.name.c_str());
+    const size_t ng = (size_t)rows * (cols / 128);
+    for (size_t i = 0; i < ng; i++) {
+        // zero points must keep (q - z) exact in fp16 on the device path
+        uint16_t h = zeros[i];
+        int e = (h >> 10) & 31;
+        if (e >= 25) return fail(c, AARH_ERR_UNSUPPORTED, "INT4 zero point out of range in %s", s.name.c_str());
+    }
+    const size_t nb = (size_t)rows * cols / 2;
+    if (ensure_staging(c, (nb + 2 * ng * 2 + 3) / 4 + 1)) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    uint8_t* st = (uint8_t*)c->staging;
+    HIPCHK(c, hipMemcpy(st, packed, nb, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(st + nb, scales, ng * 2, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(st + nb + ng * 2, zeros, ng * 2, hipMemcpyHostToDevice));
+    DevTensor* t;
+    int ro, inter;
+    part_target(c, s, &t, &ro, &inter);
+    KCHK(c, launch_repack_int4(st, (const uint16_t*)(st + nb), (const uint16_t*)(st + nb + ng * 2), (int)rows, (int)cols,
+                               t->w, t->sz, ro, t->N, inter, c->stream));
+    return sync_stream(c);
+}
+
+int aarh_load_tensor_int8(aarh_ctx* c, int id, const int8_t* codes, const float* scales, int64_t rows, int64_t cols) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
+    const TensorSlot& s = c->slots[id];
+    if (s.kind != AARH_T_LINEAR || c->cfg.weight_format != AARH_W_INT8_ROW)
+        return fail(c, AARH_ERR_UNSUPPORTED, "tensor %s is not an INT8 linear in this model", s.name.c_str());
+    if (rows != s.rows || cols != s.cols || cols % 128)
+        return fail(c, AARH_ERR_SHAPE, "INT8 tensor %s shape mismatch", s.name.c_str());
+    const size_t nb = (size_t)rows * cols;
+    if (ensure_staging(c, (nb + rows * 4 + 3) / 4 + 1)) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    uint8_t* st = (uint8_t*)c->staging;
+    HIPCHK(c, hipMemcpy(st, codes, nb, hipMemcpyHostToDevice));
+    size_t so = (nb + 3) / 4 * 4;
+    HIPCHK(c, hipMemcpy(st + so, scales, rows * 4, hipMemcpyHostToDevice));
+    DevTensor* t;
+    int ro, inter;
+    part_target(c, s, &t, &ro, &inter);
+    KCHK(c, launch_repack_int8((const int8_t*)st, (const float*)(st + so), (int)rows, (int)cols, t->w, t->rscale, ro,
+                               t->N, inter, c->stream));
+    return sync_stream(c);
+}
+
+int aarh_init_synthetic(aarh_ctx* c, uint64_t seed, float std) {
+    if (!c) return AARH_ERR_CONFIG;
+    size_t maxn = 0;
+    for (auto& s : c->slots) maxn = std::max(maxn, (size_t)(s.rows * s.cols));
+    if (ensure_staging(c, maxn + (size_t)c->H * c->Fp + 16)) return AARH_ERR_DEVICE;
+    for (int id = 0; id < (int)c->slots.size(); id++) {
+        const TensorSlot& s = c->slots[id];
+        const int64_t n = s.rows * s.cols;
+        if (s.kind == AARH_T_NORM) {
+            KCHK(c, launch_fill_f32(c->staging, n, 1.0f, c->stream));
+        } else {
+            KCHK(c, launch_synth_fill(c->staging, n, seed, (unsigned)id, std, c->stream));
+        }
+        int r = place_f32_staging(c, id);
+        if (r) return r;
+    }
+    return sync_stream(c);
+}
+
+int aarh_kv_reset(aarh_ctx* c, int slot) {
+    if (!c || slot < 0 || slot >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", slot);
+    c->kv_len[slot] = 0;
+    return 0;
+}
+
+int aarh_kv_len(const aarh_ctx* c, int slot, int32_t* out) {
+    if (!c || slot < 0 || slot >= c->cfg.max_batch) return AARH_ERR_SHAPE;
+    *out = c->kv_len[slot];
+    return 0;
+}
+
+int aarh_kv_rollback(aarh_ctx* c, int slot, int32_t new_len) {
+    if (!c || slot < 0 || slot >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", slot);
+    if (new_len < 0 || new_len > c->kv_len[slot])
+        return fail(c, AARH_ERR_SHAPE, "cannot grow KV cache from %d to %d with rollback", c->kv_len[slot], new_len);
+    c->kv_len[slot] = new_len;
+    return 0;
+}
+
+int aarh_kv_fill_synthetic(aarh_ctx* c, int slot, int32_t len, uint64_t seed) {
+    if (!c || slot < 0 || slot >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", slot);
+    if (len < 0 || len > c->cap) return fail(c, AARH_ERR_SHAPE, "length %d exceeds capacity %d", len, c->cap);
+    for (int l = 0; l < c->cfg.n_layers; l++)
+        KCHK(c, launch_kv_fill_synthetic(c->kc[l], c->vc[l], c->ksc[l], c->vsc[l], c->cfg.kv_format, slot,
+                                         c->cfg.n_kv_heads, c->hd, c->cap, len, seed, l, c->stream));
+    c->kv_len[slot] = len;
+    return sync_stream(c);
+}
+
+// Validate and stage (slots, offsets, ids) from host arrays; returns max kv length.
+static int stage_rows(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, const int32_t* offsets, int nseq, int S,
+                      int* max_kv) {
+    if (nseq <= 0 || S <= 0) return fail(c, AARH_ERR_SHAPE, "batch and sequence length must be non-zero");
+    if (nseq * S > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq*S=%d exceeds max_rows %d", nseq * S, c->Mmax);
+    int mk = 0;
+    for (int b = 0; b < nseq; b++) {
+        int sl = slots[b], off = offsets[b];
+        if (sl < 0 || sl >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", sl);
+        for (int b2 = 0; b2 < b; b2++)
+            if (slots[b2] == sl) return fail(c, AARH_ERR_SHAPE, "slot %d used twice", sl);
+        if (off < 0 || off > c->kv_len[sl])
+            return fail(c, AARH_ERR_SHAPE, "offset %d beyond cached length %d of slot %d", off, c->kv_len[sl], sl);
+        if (off + S > c->cfg.max_seq_len)
+            return fail(c, AARH_ERR_SHAPE, "sequence length %d with offset %d exceeds max_seq_len %d", S, off,
+                        c->cfg.max_seq_len);
+        mk = std::max(mk, off + S);
+    }
+    for (int i = 0; i < nseq * S; i++)
+        if ((int64_t)ids[i] >= c->V) return fail(c, AARH_ERR_SHAPE, "token id %u exceeds vocabulary", ids[i]);
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    memcpy(c->h_pos0, offsets, nseq * 4);
+    memcpy(c->h_slot, slots, nseq * 4);
+    memcpy(c->h_ids, ids, (size_t)nseq * S * 4);
+    HIPCHK(c, hipMemcpyAsync(c->d_pos0, c->h_pos0, nseq * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_slot, c->h_slot, nseq * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_ids, c->h_ids, (size_t)nseq * S * 4, hipMemcpyHostToDevice, c->stream));
+    *max_kv = mk;
+    return 0;
+}
+
+int aarh_forward(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, const int32_t* offsets, int nseq, int S,
+                 float* logits_out, float* hidden_out) {
+    if (!c) return AARH_ERR_CONFIG;
+    int mk = 0;
+    int r = stage_rows(c, ids, slots, offsets, nseq, S, &mk);
+    if (r) return r;
+    const int M = nseq * S;
+    r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, S, mk, c->logits, rm(M, 0, c->V), c->hidden);
+    if (r) return r;
+    for (int b = 0; b < nseq; b++) c->kv_len[slots[b]] = offsets[b] + S;
+    if (logits_out) HIPCHK(c, hipMemcpyAsync(logits_out, c->logits, (size_t)M * c->V * 4, hipMemcpyDeviceToHost, c->stream));
+    if (hidden_out) HIPCHK(c, hipMemcpyAsync(hidden_out, c->hidden, (size_t)M * c->H * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync_stream(c);
+}
+
+const float* aarh_last_logits_device(const aarh_ctx* c) { return c ? c->logits : nullptr; }
+const float* aarh_last_hidden_device(const aarh_ctx* c) { return c ? c->hidden : nullptr; }
+
+int aarh_mtp_head(aarh_ctx* c, int head, const float* anchor, const uint32_t* ids, int nseq, float* logits_out) {
+    if (!c) return AARH_ERR_CONFIG;
+    if (head < 0 || head >= c->nheads_mtp) return fail(c, AARH_ERR_CONFIG, "MTP head index %d is not configured", head);
+    if (nseq <= 0 || nseq * (head + 2) > c->Mmax) return fail(c, AARH_ERR_SHAPE, "bad MTP batch %d", nseq);
+    for (int i = 0; i < nseq * (head + 1); i++)
+        if ((int64_t)ids[i] >= c->V) return fail(c, AARH_ERR_SHAPE, "token id %u exceeds vocabulary", ids[i]);
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(c->hidden, anchor, (size_t)nseq * c->H * 4, hipMemcpyHostToDevice));
+    memcpy(c->h_ids, ids, (size_t)nseq * (head + 1) * 4);
+    HIPCHK(c, hipMemcpy(c->d_ids, c->h_ids, (size_t)nseq * (head + 1) * 4, hipMemcpyHostToDevice));
+    int r = mtp_head_dev(c, head, c->hidden, c->H, c->d_ids, head + 1, nseq, c->logits, c->V);
+    if (r) return r;
+    if (logits_out) HIPCHK(c, hipMemcpyAsync(logits_out, c->logits, (size_t)nseq * c->V * 4, hipMemcpyDeviceToHost, c->stream));
+    return sync_stream(c);
+}
+
+static int ensure_accept_scratch(aarh_ctx* c, int B, int rows_per_seq) {
+    const int rows = B * rows_per_seq;
+    if (rows > c->acc_rows_cap) {
+        if (c->acc_max) {
+            HIPCHK(c, hipStreamSynchronize(c->stream));
+            (void)hipFree(c->acc_max);
+            (void)hipFree(c->acc_sum);
+            (void)hipFree(c->acc_argmax);
+        }
+        if (dalloc(c, &c->acc_max, rows * 4) || dalloc(c, &c->acc_sum, rows * 4) || dalloc(c, &c->acc_argmax, rows * 4))
+            return AARH_ERR_DEVICE;
+        c->acc_rows_cap = rows;
+    }
+    if (B > c->acc_seq_cap) {
+        if (c->acc_cnt) {
+            HIPCHK(c, hipStreamSynchronize(c->stream));
+            (void)hipFree(c->acc_cnt);
+        }
+        if (dalloc(c, &c->acc_cnt, B * 4)) return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(c->acc_cnt, 0, B * 4));
+        c->acc_seq_cap = B;
+    }
+    return 0;
+}
+
+int aarh_accept_sample(aarh_ctx* c, const float* target, int target_rows, const float* draft,
+                       const uint32_t* draft_tokens, const int32_t* n_proposals, int B, int K, int V, int bonus,
+                       const aarh_sampler* s, const uint64_t* seeds, const uint64_t* word_offsets,
+                       const float* uniforms, int32_t* accept_len, int32_t* token, uint32_t* flags, int32_t* draws,
+                       int32_t* status, void* stream) {
+    if (!c || !s) return AARH_ERR_CONFIG;
+    if (B <= 0 || K < 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0))
+        return fail(c, AARH_ERR_SHAPE, "bad acceptance shape B=%d K=%d V=%d rows=%d", B, K, V, target_rows);
+    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
+    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
+        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
+    if (!greedy && (size_t)V * 4 > 160 * 1024)
+        return fail(c, AARH_ERR_UNSUPPORTED, "vocabulary %d exceeds the LDS-resident sampling limit", V);
+    if (ensure_accept_scratch(c, B, target_rows + K)) return AARH_ERR_DEVICE;
+    AcceptArgs a{};
+    a.target = target;
+    a.target_rows = target_rows;
+    a.draft = draft;
+    a.draft_tokens = draft_tokens;
+    a.n_proposals = n_proposals;
+    a.B = B;
+    a.K = K;
+    a.V = V;
+    a.bonus = bonus ? 1 : 0;
+    a.greedy = greedy ? 1 : 0;
+    a.temperature = s->temperature;
+    a.seeds = seeds;
+    a.word_offsets = word_offsets;
+    a.uniforms = uniforms;
+    a.row_max = c->acc_max;
+    a.row_sum = c->acc_sum;
+    a.row_argmax = c->acc_argmax;
+    a.counters = c->acc_cnt;
+    a.out_accept_len = accept_len;
+    a.out_token = token;
+    a.out_flags = flags;
+    a.out_draws = draws;
+    a.out_status = status;
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    hipStream_t saved = c->stream;
+    c->stream = st;
+    int r;
+    {
+        ProfScope ps(c, AARH_PROF_ACCEPT, (double)B * (target_rows + K) * V * 4.0);
+        r = launch_accept(a, st);
+    }
+    c->stream = saved;
+    if (r) return fail(c, r, "acceptance launch failed: %d %s", r, last_launch_error());
+    return 0;
+}
+
+int aarh_prof_enable(aarh_ctx* c, int enable) {
+    if (!c) return AARH_ERR_CONFIG;
+    c->prof = enable != 0;
+    for (int i = 0; i < AARH_PROF_COUNT; i++) {
+        c->prof_ms[i] = 0;
+        c->prof_bytes[i] = 0;
+        c->prof_n[i] = 0;
+    }
+    return 0;
+}
+
+static int prof_collect(aarh_ctx* c) {
+    if (c->prof_recs.empty()) return 0;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    for (auto& r : c->prof_recs) {
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, r.a, r.b);
+        c->prof_ms[r.cls] += ms;
+        c->prof_bytes[r.cls] += r.bytes;
+        c->prof_n[r.cls] += 1;
+        c->ev_pool.push_back(r.a);
+        c->ev_pool.push_back(r.b);
+    }
+    c->prof_recs.clear();
+    return 0;
+}
+
+int aarh_prof_get(aarh_ctx* c, int cls, double* total_ms, double* alg_bytes, int64_t* launches) {
+    if (!c || cls < 0 || cls >= AARH_PROF_COUNT) return AARH_ERR_CONFIG;
+    int r = prof_collect(c);
+    if (r) return r;
+    if (total_ms) *total_ms = c->prof_ms[cls];
+    if (alg_bytes) *alg_bytes = c->prof_bytes[cls];
+    if (launches) *launches = c->prof_n[cls];
+    return 0;
+}
+
+}  // extern "C"
+
+// ===========================================================================
+// Engine: MtpSpeculativeEngine::generate_with_callback (mtp_speculative.rs:86-336)
+// for nseq independent requests in lock-step rounds.
+// ===========================================================================
+namespace {
+
+struct EngineBufs {
+    float *tgt = nullptr, *drf = nullptr, *anchor = nullptr, *vhid = nullptr;
+    uint32_t* props = nullptr;
+    int32_t *acc_len = nullptr, *acc_tok = nullptr, *acc_draws = nullptr, *acc_status = nullptr, *nprop = nullptr;
+    uint32_t* acc_flags = nullptr;
+    uint64_t *seeds = nullptr, *offs = nullptr;
+    const float** src = nullptr;
+    float** dst = nullptr;
+    void release() {
+        for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)props, (void*)acc_len, (void*)acc_tok,
+                        (void*)acc_draws, (void*)acc_status, (void*)nprop, (void*)acc_flags, (void*)seeds, (void*)offs,
+                        (void*)src, (void*)dst})
+            if (p) (void)hipFree(p);
+    }
+};
+
+constexpr uint32_t EOS_ID = 0;  // tokenizer/src/special.rs:33
+
+}  // namespace
+
+extern "C" int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
+                                 int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds,
+                                 uint32_t* out_tokens, int32_t* out_len, int32_t* finish_reason,
+                                 aarh_spec_stats* stats) {
+    if (!c || !s) return AARH_ERR_CONFIG;
+    const auto& g = c->cfg;
+    if (c->nheads_mtp == 0) return fail(c, AARH_ERR_CONFIG, "internal speculative decoding requires model.mtp configuration");
+    if (num_draft_tokens < 2) return fail(c, AARH_ERR_CONFIG, "MTP speculative decoding requires at least two proposal tokens");
+    if (num_draft_tokens > g.num_future_tokens)
+        return fail(c, AARH_ERR_CONFIG, "requested %d MTP proposal tokens but checkpoint horizon is %d", num_draft_tokens,
+                    g.num_future_tokens);
+    if (nseq <= 0 || nseq > g.max_batch) return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
+    if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
+    if (prompt_len >= g.max_seq_len)
+        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", prompt_len, g.max_seq_len);
+    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
+    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
+        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
+    const int K = num_draft_tokens, V = c->V, H = c->H;
+    if (nseq * K > c->Mmax || nseq * (K + 1) > c->Mmax)
+        return fail(c, AARH_ERR_SHAPE, "nseq x (draft tokens + 1) exceeds max_rows");
+    const int available = g.max_seq_len - prompt_len;
+    const int max_new = std::min(max_new_tokens, available);
+    for (int b = 0; b < nseq; b++) {
+        out_len[b] = 0;
+        finish_reason[b] = AARH_FINISH_MAX_TOKENS;
+        memset(&stats[b], 0, sizeof(aarh_spec_stats));
+    }
+    if (max_new <= 0) {
+        for (int b = 0; b < nseq; b++) finish_reason[b] = AARH_FINISH_CONTEXT_LIMIT;
+        return 0;
+    }
+    EngineBufs eb;
+    int r = 0;
+#define EB_ALLOC(p, bytes) \
+    if ((r = dalloc(c, &eb.p, (bytes)))) { eb.release(); return r; }
+    EB_ALLOC(tgt, (size_t)nseq * (K + 1) * V * 4);
+    EB_ALLOC(drf, (size_t)nseq * K * V * 4);
+    EB_ALLOC(anchor, (size_t)nseq * H * 4);
+    EB_ALLOC(vhid, (size_t)nseq * K * H * 4);
+    EB_ALLOC(props, (size_t)nseq * K * 4);
+    EB_ALLOC(acc_len, nseq * 4);
+    EB_ALLOC(acc_tok, nseq * 4);
+    EB_ALLOC(acc_draws, nseq * 4);
+    EB_ALLOC(acc_status, nseq * 4);
+    EB_ALLOC(nprop, nseq * 4);
+    EB_ALLOC(acc_flags, nseq * 4);
+    EB_ALLOC(seeds, nseq * 8);
+    EB_ALLOC(offs, nseq * 8);
+    EB_ALLOC(src, (size_t)4 * nseq * sizeof(void*));
+    EB_ALLOC(dst, (size_t)4 * nseq * sizeof(void*));
+#undef EB_ALLOC
+    auto done_err = [&](int code) {
+        eb.release();
+        return code;
+    };
+    std::vector<uint64_t> hseeds(nseq), hoffs(nseq, 0);
+    for (int b = 0; b < nseq; b++) hseeds[b] = seeds ? seeds[b] : 0;
+    if (hipMemcpy(eb.seeds, hseeds.data(), nseq * 8, hipMemcpyHostToDevice) != hipSuccess)
+        return done_err(fail(c, AARH_ERR_DEVICE, "seed upload failed"));
+
+    // ---- prefill (chunked so that rows stay within max_rows) ----
+    std::vector<int32_t> slots(nseq), offs(nseq), base(nseq);
+    for (int b = 0; b < nseq; b++) {
+        slots[b] = b;
+        c->kv_len[b] = 0;
+    }
+    {
+        const int chunk = std::max(1, c->Mmax / nseq);
+        std::vector<uint32_t> ids;
+        for (int p0 = 0; p0 < prompt_len; p0 += chunk) {
+            const int S = std::min(chunk, prompt_len - p0);
+            ids.resize((size_t)nseq * S);
+            for (int b = 0; b < nseq; b++) {
+                offs[b] = p0;
+                for (int s2 = 0; s2 < S; s2++) ids[(size_t)b * S + s2] = prompts[(size_t)b * prompt_len + p0 + s2];
+            }
+            int mk = 0;
+            if ((r = stage_rows(c, ids.data(), slots.data(), offs.data(), nseq, S, &mk))) return done_err(r);
+            const bool last = p0 + S == prompt_len;
+            // logits/hidden of the last prompt row -> target_next (tgt row 0) and anchor
+            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, S, mk, c->logits, rm(nseq * S, 0, V),
+                                 c->hidden)))
+                return done_err(r);
+            for (int b = 0; b < nseq; b++) c->kv_len[b] = p0 + S;
+            if (last) {
+                std::vector<const float*> hs(2 * nseq);
+                std::vector<float*> hd(2 * nseq);
+                for (int b = 0; b < nseq; b++) {
+                    hs[b] = c->logits + ((size_t)b * S + S - 1) * V;
+                    hd[b] = eb.tgt + (size_t)b * (K + 1) * V;
+                    hs[nseq + b] = c->hidden + ((size_t)b * S + S - 1) * H;
+                    hd[nseq + b] = eb.anchor + (size_t)b * H;
+                }
+                if (hipMemcpyAsync(eb.src, hs.data(), 2 * nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
+                    hipMemcpyAsync(eb.dst, hd.data(), 2 * nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream))
+                    return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
+                if ((r = launch_copy_rows(eb.src, eb.dst, nseq, V, c->stream)) ||
+                    (r = launch_copy_rows(eb.src + nseq, eb.dst + nseq, nseq, H, c->stream)))
+                    return done_err(fail(c, r, "row copy failed"));
+                if ((r = sync_stream(c))) return done_err(r);
+            }
+        }
+    }
+
+    std::vector<char> finished(nseq, 0);
+    std::vector<uint32_t> hprops((size_t)nseq * K);
+    std::vector<int32_t> hlen(nseq), htok(nseq), hdraws(nseq), hstatus(nseq), hnp(nseq), count(nseq);
+    std::vector<int32_t> zero_pos(nseq, 0);
+    aarh_sampler samp = *s;
+
+    while (true) {
+        bool any = false;
+        for (int b = 0; b < nseq; b++)
+            if (!finished[b] && out_len[b] < max_new) any = true;
+            else finished[b] = 1;
+        if (!any) break;
+        int Kr = 1;
+        for (int b = 0; b < nseq; b++) {
+            base[b] = c->kv_len[b];
+            count[b] = finished[b] ? 1 : std::min(K, max_new - out_len[b]);
+            Kr = std::max(Kr, count[b]);
+        }
+        // ---- proposals: index 0 from target_next, index p from MTP head p-1 ----
+        // draft row 0 = target_next
+        {
+            std::vector<const float*> hs(nseq);
+            std::vector<float*> hd(nseq);
+            for (int b = 0; b < nseq; b++) {
+                hs[b] = eb.tgt + (size_t)b * (K + 1) * V;
+                hd[b] = eb.drf + (size_t)b * K * V;
+            }
+            if (hipMemcpyAsync(eb.src, hs.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
+                hipMemcpyAsync(eb.dst, hd.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream))
+                return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
+            if ((r = launch_copy_rows(eb.src, eb.dst, nseq, V, c->stream))) return done_err(fail(c, r, "row copy failed"));
+        }
+        for (int p = 0; p < Kr; p++) {
+            if (p > 0) {
+                if ((r = mtp_head_dev(c, p - 1, eb.anchor, H, eb.props, K, nseq, eb.drf + (size_t)p * V, (long long)K * V)))
+                    return done_err(r);
+                for (int b = 0; b < nseq; b++)
+                    if (!finished[b] && count[b] > p) stats[b].mtp_head_forwards++;
+            }
+            // sample proposal p from draft row p
+            if (greedy) {
+                if ((r = launch_argmax_rows(eb.drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)eb.props + p, K,
+                                            nullptr, c->stream)))
+                    return done_err(fail(c, r, "argmax failed"));
+            } else {
+                std::vector<uint64_t> o(nseq);
+                for (int b = 0; b < nseq; b++) o[b] = hoffs[b] + p;
+                if (hipMemcpyAsync(eb.offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+                    return done_err(fail(c, AARH_ERR_DEVICE, "offset upload failed"));
+                if ((r = aarh_accept_sample(c, eb.drf + (size_t)p * V, K, nullptr, nullptr, nullptr, nseq, 0, V, 1, &samp,
+                                            eb.seeds, eb.offs, nullptr, eb.acc_len, eb.acc_tok, eb.acc_flags,
+                                            eb.acc_draws, eb.acc_status, nullptr)))
+                    return done_err(r);
+                // sampled tokens come back per sequence; scatter them into the [nseq][K] proposal table
+                if ((r = sync_stream(c))) return done_err(r);
+                std::vector<int32_t> t(nseq);
+                if (hipMemcpy(t.data(), eb.acc_tok, nseq * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                    return done_err(fail(c, AARH_ERR_DEVICE, "proposal download failed"));
+                for (int b = 0; b < nseq; b++) hprops[(size_t)b * K + p] = (uint32_t)t[b];
+                if (hipMemcpy(eb.props, hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice) != hipSuccess)
+                    return done_err(fail(c, AARH_ERR_DEVICE, "proposal upload failed"));
+            }
+        }
+        if ((r = sync_stream(c))) return done_err(r);
+        if (hipMemcpy(hprops.data(), eb.props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return done_err(fail(c, AARH_ERR_DEVICE, "proposal download failed"));
+        for (int b = 0; b < nseq; b++) {
+            int np = 0;
+            if (!finished[b]) {
+                for (int p = 0; p < count[b]; p++) {
+                    np++;
+                    stats[b].draft_tokens_proposed++;
+                    if (hprops[(size_t)b * K + p] == EOS_ID) break;
+                }
+            }
+            hnp[b] = np;
+            if (!greedy) hoffs[b] += np;
+        }
+        // ---- verify forward (finished sequences run at a dummy position 0) ----
+        {
+            std::vector<uint32_t> ids((size_t)nseq * Kr);
+            std::vector<int32_t> off(nseq);
+            for (int b = 0; b < nseq; b++) {
+                for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = hprops[(size_t)b * K + std::min(s2, K - 1)];
+                off[b] = finished[b] ? 0 : base[b];
+                if (finished[b]) c->kv_len[b] = 0;
+            }
+            int mk = 0;
+            if ((r = stage_rows(c, ids.data(), slots.data(), off.data(), nseq, Kr, &mk))) return done_err(r);
+            // logits rows -> tgt rows 1..Kr, hidden rows -> vhid
+            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, eb.tgt + V, rm(Kr, (long long)(K + 1) * V, V),
+                                 eb.vhid)))
+                return done_err(r);
+            for (int b = 0; b < nseq; b++) {
+                if (finished[b]) continue;
+                stats[b].rounds++;
+                stats[b].target_decode_forwards++;
+            }
+        }
+        // ---- acceptance (MTP round: no bonus) ----
+        {
+            std::vector<uint64_t> o(nseq);
+            for (int b = 0; b < nseq; b++) o[b] = hoffs[b];
+            if (hipMemcpyAsync(eb.offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                hipMemcpyAsync(eb.nprop, hnp.data(), nseq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+                return done_err(fail(c, AARH_ERR_DEVICE, "upload failed"));
+            if ((r = aarh_accept_sample(c, eb.tgt, K + 1, eb.drf, eb.props, eb.nprop, nseq, K, V, 0, &samp, eb.seeds, eb.offs,
+                                        nullptr, eb.acc_len, eb.acc_tok, eb.acc_flags, eb.acc_draws, eb.acc_status, nullptr)))
+                return done_err(r);
+            if ((r = sync_stream(c))) return done_err(r);
+            if (hipMemcpy(hlen.data(), eb.acc_len, nseq * 4, hipMemcpyDeviceToHost) ||
+                hipMemcpy(htok.data(), eb.acc_tok, nseq * 4, hipMemcpyDeviceToHost) ||
+                hipMemcpy(hdraws.data(), eb.acc_draws, nseq * 4, hipMemcpyDeviceToHost) ||
+                hipMemcpy(hstatus.data(), eb.acc_status, nseq * 4, hipMemcpyDeviceToHost))
+                return done_err(fail(c, AARH_ERR_DEVICE, "acceptance download failed"));
+        }
+        // ---- commit, rollback, replay ----
+        std::vector<int> replay_seq, replay_len;
+        std::vector<const float*> cs;
+        std::vector<float*> cd;
+        std::vector<const float*> hsrc;
+        std::vector<float*> hdst;
+        for (int b = 0; b < nseq; b++) {
+            if (finished[b]) continue;
+            if (hstatus[b] != 0)
+                return done_err(fail(c, AARH_ERR_CONFIG, "speculative residual distribution has zero probability mass"));
+            if (!greedy) hoffs[b] += hdraws[b];
+            const int np = hnp[b], acc = hlen[b];
+            bool done = false;
+            for (int i = 0; i < acc && !done; i++) {
+                stats[b].draft_tokens_accepted++;
+                const uint32_t t = hprops[(size_t)b * K + i];
+                if (t == EOS_ID) {
+                    finish_reason[b] = AARH_FINISH_EOS;
+                    done = true;
+                    break;
+                }
+                out_tokens[(size_t)b * max_new_tokens + out_len[b]++] = t;
+                if (out_len[b] == max_new) done = true;
+            }
+            if (done) {
+                finished[b] = 1;
+                c->kv_len[b] = base[b] + np;
+                continue;
+            }
+            if (acc < np) {
+                const uint32_t repl = (uint32_t)htok[b];
+                c->kv_len[b] = base[b];  // target_cache.restore(snapshot)
+                if (repl == EOS_ID) {
+                    finish_reason[b] = AARH_FINISH_EOS;
+                    finished[b] = 1;
+                    continue;
+                }
+                out_tokens[(size_t)b * max_new_tokens + out_len[b]++] = repl;
+                hprops[(size_t)b * K + acc] = repl;  // replay ids = proposals[..i] + replacement
+                replay_seq.push_back(b);
+                replay_len.push_back(acc + 1);
+            } else {
+                // everything accepted: target_next / anchor from the last verify row
+                c->kv_len[b] = base[b] + np;
+                cs.push_back(eb.tgt + ((size_t)b * (K + 1) + np) * V);
+                cd.push_back(eb.tgt + (size_t)b * (K + 1) * V);
+                hsrc.push_back(eb.vhid + ((size_t)b * Kr + np - 1) * H);
+                hdst.push_back(eb.anchor + (size_t)b * H);
+            }
+        }
+        if (!replay_seq.empty()) {
+            const int nr = (int)replay_seq.size();
+            int Sr = 0;
+            for (int L : replay_len) Sr = std::max(Sr, L);
+            std::vector<uint32_t> ids((size_t)nr * Sr);
+            std::vector<int32_t> sl(nr), off(nr);
+            for (int j = 0; j < nr; j++) {
+                const int b = replay_seq[j];
+                sl[j] = b;
+                off[j] = base[b];
+                for (int s2 = 0; s2 < Sr; s2++)
+                    ids[(size_t)j * Sr + s2] = hprops[(size_t)b * K + std::min(s2, replay_len[j] - 1)];
+            }
+            int mk = 0;
+            if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk))) return done_err(r);
+            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, Sr, mk, c->logits, rm(nr * Sr, 0, V), c->hidden)))
+                return done_err(r);
+            for (int j = 0; j < nr; j++) {
+                const int b = replay_seq[j];
+                stats[b].target_decode_forwards++;
+                c->kv_len[b] = base[b] + replay_len[j];
+                cs.push_back(c->logits + ((size_t)j * Sr + replay_len[j] - 1) * V);
+                cd.push_back(eb.tgt + (size_t)b * (K + 1) * V);
+                hsrc.push_back(c->hidden + ((size_t)j * Sr + replay_len[j] - 1) * H);
+                hdst.push_back(eb.anchor + (size_t)b * H);
+            }
+        }
+        if (!cs.empty()) {
+            const int n = (int)cs.size();
+            std::vector<const float*> allsrc(cs);
+            allsrc.insert(allsrc.end(), hsrc.begin(), hsrc.end());
+            std::vector<float*> alldst(cd);
+            alldst.insert(alldst.end(), hdst.begin(), hdst.end());
+            if (hipMemcpyAsync(eb.src, allsrc.data(), 2 * n * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
+                hipMemcpyAsync(eb.dst, alldst.data(), 2 * n * sizeof(void*), hipMemcpyHostToDevice, c->stream))
+                return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
+            if ((r = launch_copy_rows(eb.src, eb.dst, n, V, c->stream)) ||
+                (r = launch_copy_rows(eb.src + n, eb.dst + n, n, H, c->stream)))
+                return done_err(fail(c, r, "row copy failed"));
+            if ((r = sync_stream(c))) return done_err(r);
+        }
+        for (int b = 0; b < nseq; b++)
+            if (!finished[b] && out_len[b] >= max_new) finished[b] = 1;
+    }
+    for (int b = 0; b < nseq; b++) {
+        if (out_len[b] == available && finish_reason[b] == AARH_FINISH_MAX_TOKENS)
+            finish_reason[b] = AARH_FINISH_CONTEXT_LIMIT;
+        stats[b].draft_tokens_rejected = std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
+    }
+    eb.release();
+    return 0;
+}

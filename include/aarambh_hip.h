@@ -1,0 +1,152 @@
+/*
+ * aarambh_hip.h -- C ABI of libaarambh_hip, the MI355X (gfx950) speculative
+ * verify path for aarambh-studio.
+ *
+ * Plain pointers and sizes only.  One context owns one HIP stream, the device
+ * copy of one target model (quantised weights, optional MTP heads) and a KV
+ * cache with `max_batch` sequence slots.  A context is not thread-safe; calls
+ * on one context run in order on its stream.  Every int-returning function
+ * returns an aarh_status; aarh_last_error() gives the message of the last
+ * failure.
+ *
+ * Drop-in boundary: this sits at the model + KV level of the reference
+ * (model/src/model.rs forward_with_cache_output / forward_mtp_head and
+ * inference/src/kvcache.rs), plus the engine loop and the acceptance math,
+ * because candle 0.10.2 has no HIP device to plug a CustomOp into
+ * (core/src/device.rs:5-12).
+ */
+#ifndef AARAMBH_HIP_H
+#define AARAMBH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Mirrors AarambhError (core/src/error.rs:5-33): Config, Shape, Unsupported, plus Device. */
+typedef enum {
+    AARH_OK = 0,
+    AARH_ERR_CONFIG = 1,
+    AARH_ERR_SHAPE = 2,
+    AARH_ERR_UNSUPPORTED = 3,
+    AARH_ERR_DEVICE = 4
+} aarh_status;
+
+/* Weight storage formats (quant/src/types.rs:68-90 plus the build's layouts). */
+enum {
+    AARH_W_F32 = 0,       /* reference CPU dtype */
+    AARH_W_BF16 = 1,
+    AARH_W_INT8_ROW = 2,  /* symmetric per-output-channel INT8, f32 row scales */
+    AARH_W_INT4_G128 = 3  /* PackedInt4Tensor semantics, group 128, fp16 scale + zero */
+};
+enum { AARH_KV_F32 = 0, AARH_KV_F16 = 1, AARH_KV_INT8 = 2 };
+enum { AARH_T_NORM = 0, AARH_T_LINEAR = 1, AARH_T_EMBED = 2 };
+enum { AARH_FINISH_MAX_TOKENS = 0, AARH_FINISH_EOS = 1, AARH_FINISH_CONTEXT_LIMIT = 2 };
+enum { AARH_FLAG_RATIO_NEAR = 1u, AARH_FLAG_CDF_NEAR = 2u };
+
+typedef struct aarh_ctx aarh_ctx;
+
+/* ModelConfig subset (core/src/config.rs:734-776) + MtpConfig (:275-283) + device sizing. */
+typedef struct {
+    int32_t vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_heads, max_seq_len;
+    float rope_theta, norm_eps;
+    int32_t num_future_tokens; /* MTP horizon; 0 = no MTP heads */
+    int32_t weight_format;     /* AARH_W_* for every projection */
+    int32_t lm_head_format;    /* AARH_W_F32 or AARH_W_BF16: tied embedding / LM head storage */
+    int32_t kv_format;         /* AARH_KV_* */
+    int32_t max_batch;         /* KV-cache sequence slots */
+    int32_t max_rows;          /* max rows (sequences x tokens) per forward call, <= 128 */
+} aarh_model_config;
+
+/* Sampler (inference/src/sampler.rs:14-65). */
+typedef struct {
+    int32_t greedy;    /* 1 = Sampler::Greedy */
+    float temperature; /* TopKTopP temperature (<= f32::EPSILON behaves greedy) */
+    int32_t top_k;     /* must be 0 on the device path (unsupported otherwise) */
+    float top_p;       /* must be outside (0,1) on the device path */
+} aarh_sampler;
+
+/* SpeculativeStats (inference/src/speculative.rs:41-90). */
+typedef struct {
+    int32_t rounds, draft_tokens_proposed, draft_tokens_accepted, draft_tokens_rejected;
+    int32_t target_decode_forwards, draft_decode_forwards, mtp_head_forwards;
+} aarh_spec_stats;
+
+/* --- context (replaces InferenceEngine::from_paths_with_dtype, inference/src/engine.rs:226-244) --- */
+int aarh_create(int device, const aarh_model_config *cfg, aarh_ctx **out);
+void aarh_destroy(aarh_ctx *ctx);
+const char *aarh_last_error(const aarh_ctx *ctx);
+void *aarh_stream(aarh_ctx *ctx); /* the context's hipStream_t */
+int aarh_sync(aarh_ctx *ctx);
+
+/* --- weights: checkpoint tensors by reference name/order (model/src/model.rs:82-279) --- */
+int aarh_num_tensors(const aarh_ctx *ctx);
+int aarh_tensor_info(const aarh_ctx *ctx, int id, char *name, int name_cap, int64_t *rows,
+                     int64_t *cols, int32_t *kind);
+/* f32 host values, quantised on device per the configured format
+   (quantise_affine_i4 int4.rs:7-41 / fake_quant_symmetric qat.rs:155-169). */
+int aarh_load_tensor_f32(aarh_ctx *ctx, int id, const float *host, int64_t numel);
+/* PackedInt4Tensor (types.rs:79-90) with fp16 scale/zero per 128-group, row-major. */
+int aarh_load_tensor_int4(aarh_ctx *ctx, int id, const uint8_t *packed, const uint16_t *scales_f16,
+                          const uint16_t *zeros_f16, int64_t rows, int64_t cols, int32_t group);
+/* Per-row INT8 codes + f32 row scales (I8QuantizedTensor semantics per channel). */
+int aarh_load_tensor_int8(aarh_ctx *ctx, int id, const int8_t *codes, const float *scales,
+                          int64_t rows, int64_t cols);
+/* Random-init model generated on device: N(0, std^2) linears/embedding, norms 1.0. */
+int aarh_init_synthetic(aarh_ctx *ctx, uint64_t seed, float std);
+
+/* --- KV cache (inference/src/kvcache.rs:22-69; rollback by index, nn/src/kvcache.rs:301-304) --- */
+int aarh_kv_reset(aarh_ctx *ctx, int slot);
+int aarh_kv_len(const aarh_ctx *ctx, int slot, int32_t *out_len);
+int aarh_kv_rollback(aarh_ctx *ctx, int slot, int32_t new_len);
+int aarh_kv_fill_synthetic(aarh_ctx *ctx, int slot, int32_t len, uint64_t seed);
+
+/* --- model forward (AarambhModel::forward_with_cache_output, model.rs:529-587) ---
+   ids [nseq][S] for cache slots slots[nseq] at offsets[nseq] (offset <= cached length;
+   a smaller offset rewinds that slot first).  Logits [nseq][S][vocab] and final normed
+   hidden states [nseq][S][hidden] are copied to host when the pointers are non-null. */
+int aarh_forward(aarh_ctx *ctx, const uint32_t *ids, const int32_t *slots, const int32_t *offsets,
+                 int nseq, int S, float *logits_out, float *hidden_out);
+/* Device pointers of the last forward's outputs (valid until the next call). */
+const float *aarh_last_logits_device(const aarh_ctx *ctx);
+const float *aarh_last_hidden_device(const aarh_ctx *ctx);
+
+/* --- MTP head (AarambhModel::forward_mtp_head, model.rs:783-817) ---
+   anchor [nseq][hidden] (final normed hidden of the anchor position), ids [nseq][head+1]. */
+int aarh_mtp_head(aarh_ctx *ctx, int head, const float *anchor, const uint32_t *ids, int nseq,
+                  float *logits_out);
+
+/* --- acceptance (accept_proposal / residual_distribution / sample_probabilities,
+   inference/src/speculative.rs:755-793, sampler.rs:102-347), all DEVICE pointers:
+   target [B][target_rows][V], draft [B][K][V], draft_tokens [B][K], n_proposals [B] or NULL,
+   seeds/word_offsets [B] (StdRng::seed_from_u64 keystream position) or uniforms [B][K+1].
+   bonus = 1 samples from target row n_proposals when every proposal is accepted
+   (external-draft round); bonus = 0 is the MTP round.  Outputs [B]: accepted count,
+   replacement/bonus token (-1 none), near-tie flags, uniforms consumed, status (0 ok,
+   1 zero-mass residual or invalid distribution).  stream: hipStream_t or NULL (context stream). */
+int aarh_accept_sample(aarh_ctx *ctx, const float *target, int target_rows, const float *draft,
+                       const uint32_t *draft_tokens, const int32_t *n_proposals, int B, int K, int V,
+                       int bonus, const aarh_sampler *sampler, const uint64_t *seeds,
+                       const uint64_t *word_offsets, const float *uniforms, int32_t *accept_len,
+                       int32_t *token, uint32_t *flags, int32_t *draws, int32_t *status, void *stream);
+
+/* --- engine (MtpSpeculativeEngine::generate_with_callback, inference/src/mtp_speculative.rs:86-336)
+   for nseq independent requests run in lock-step rounds on slots 0..nseq-1.
+   prompts [nseq][prompt_len]; out_tokens [nseq][max_new_tokens]. */
+int aarh_mtp_generate(aarh_ctx *ctx, const uint32_t *prompts, int nseq, int prompt_len,
+                      int max_new_tokens, int num_draft_tokens, const aarh_sampler *sampler,
+                      const uint64_t *seeds, uint32_t *out_tokens, int32_t *out_len,
+                      int32_t *finish_reason, aarh_spec_stats *stats);
+
+/* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
+enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
+       AARH_PROF_GEMV_DOWN = 3, AARH_PROF_GEMV_LMHEAD = 4, AARH_PROF_ATTENTION = 5,
+       AARH_PROF_ACCEPT = 6, AARH_PROF_OTHER = 7, AARH_PROF_COUNT = 8 };
+int aarh_prof_enable(aarh_ctx *ctx, int enable);
+int aarh_prof_get(aarh_ctx *ctx, int cls, double *total_ms, double *alg_bytes, int64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

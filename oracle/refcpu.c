@@ -355,7 +355,7 @@ int ref_accept_batch(int B, int K, int64_t V, const float *target, int target_ro
                      int bonus, const ref_sampler *s, const uint64_t *seeds,
                      const uint64_t *word_offsets, const float *uniforms,
                      ref_accept_result *out) {
-    if (B <= 0 || K <= 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0)) return REF_ERR_SHAPE;
+    if (B <= 0 || K < 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0)) return REF_ERR_SHAPE;
     float *p = (float *)malloc(sizeof(float) * (size_t)V);
     float *q = (float *)malloc(sizeof(float) * (size_t)V);
     float *r = (float *)malloc(sizeof(float) * (size_t)V);
@@ -727,6 +727,7 @@ struct ref_model {
 
 struct ref_kv {
     const ref_model *m;
+    int n_layers; /* copied so that freeing never touches the model */
     int capacity, len;
     float **k, **v; /* per layer [capacity, n_kv, head_dim], effective values */
 };
@@ -920,6 +921,7 @@ int ref_model_init_synthetic(ref_model *m, uint64_t seed, float std) {
 ref_kv *ref_kv_create(const ref_model *m, int capacity) {
     ref_kv *kv = (ref_kv *)calloc(1, sizeof(ref_kv));
     kv->m = m;
+    kv->n_layers = m->cfg.n_layers;
     kv->capacity = capacity;
     int L = m->cfg.n_layers;
     size_t per = (size_t)capacity * (size_t)m->cfg.n_kv_heads * (size_t)m->head_dim;
@@ -938,7 +940,7 @@ ref_kv *ref_kv_create(const ref_model *m, int capacity) {
 
 void ref_kv_free(ref_kv *kv) {
     if (!kv) return;
-    for (int l = 0; l < kv->m->cfg.n_layers; l++) {
+    for (int l = 0; l < kv->n_layers; l++) {
         if (kv->k) free(kv->k[l]);
         if (kv->v) free(kv->v[l]);
     }

@@ -1,0 +1,166 @@
+"""Parity of the fused acceptance kernel against the oracle (accept_proposal,
+residual_distribution, sample_probabilities: speculative.rs:755-793,
+sampler.rs:102-347).  Bar: accepted lengths and tokens bit-identical except on
+draws either side flags as near-ties (|p/q - u| < 1e-5, |cdf - u| < 1e-6)."""
+import numpy as np
+import pytest
+import torch
+
+import aarambh_hip as A
+import refcpu as R
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    m = A.HipModel(A.ModelConfig(vocab_size=128, hidden_dim=128, ffn_dim=128, n_layers=1, n_heads=1,
+                                 n_kv_heads=1, max_seq_len=16), max_batch=1, max_rows=16)
+    yield m
+    m.close()
+
+
+def c2_inputs(B=32, K=4, V=32000, T=0.8, seed=0):
+    """target ~ N(0, 3^2), draft = target + N(0, 1), draft tokens
+    sampled from the draft distribution with the oracle's sequential CDF."""
+    rng = np.random.default_rng(seed)
+    tgt = rng.normal(0, 3, (B, K + 1, V)).astype(np.float32)
+    drf = (tgt[:, :K] + rng.normal(0, 1, (B, K, V))).astype(np.float32)
+    s = R.sampler(temperature=T)
+    toks = np.zeros((B, K), np.uint32)
+    for b in range(B):
+        r = R.Rng(10_000 + b)
+        for i in range(K):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    return tgt, drf, toks
+
+
+def run_both(ctx, tgt, drf, toks, T, bonus, seeds=None, offsets=None, uniforms=None, nprop=None, greedy=False):
+    s_dev = A.Sampler.greedy_sampler() if greedy else A.Sampler.top_k_top_p(T)
+    s_ref = R.sampler(greedy=True) if greedy else R.sampler(temperature=T)
+    t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a).astype(dt)).to(DEV)
+    out = ctx.accept_sample(t(tgt, np.float32), t(drf, np.float32), t(toks, np.int32), s_dev, bonus,
+                            seeds=t(seeds, np.int64), word_offsets=t(offsets, np.int64),
+                            uniforms=t(uniforms, np.float32), n_proposals=t(nprop, np.int32))
+    out = {k: v.cpu().numpy() for k, v in out.items()}
+    ref = R.accept_batch(tgt, drf, toks, s_ref, bonus, seeds=seeds, word_offsets=offsets, uniforms=uniforms,
+                         n_proposals=nprop)
+    return out, ref
+
+
+def assert_parity(out, ref, max_flag_frac=0.05):
+    B = len(ref["accept_len"])
+    flagged = (ref["flags"] != 0) | (out["flags"] != 0)
+    ok = (out["accept_len"] == ref["accept_len"]) & (out["token"] == ref["token"])
+    bad = np.nonzero(~ok & ~flagged)[0]
+    assert bad.size == 0, f"mismatch on unflagged sequences {bad}: gpu {out['accept_len'][bad]}/{out['token'][bad]} " \
+                          f"oracle {ref['accept_len'][bad]}/{ref['token'][bad]}"
+    assert flagged.mean() <= max_flag_frac
+    assert np.all(out["status"] == 0)
+    return flagged
+
+
+def test_c2_config_bit_exact_against_oracle(ctx):
+    tgt, drf, toks = c2_inputs()
+    B = tgt.shape[0]
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, True, seeds=np.arange(B, dtype=np.uint64) + 7)
+    assert_parity(out, ref)
+    assert np.array_equal(out["draws"], ref["draws"])
+    # acceptance is exercised: some sequences reject, some accept everything
+    assert (ref["accept_len"] < 4).any() and (ref["accept_len"] > 0).any()
+
+
+def test_c2_with_explicit_uniforms_and_stream_offsets(ctx):
+    tgt, drf, toks = c2_inputs(B=16, seed=1)
+    B, K = toks.shape
+    offs = (np.arange(B, dtype=np.uint64) * 13) % 50
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, True, seeds=np.full(B, 3, np.uint64), offsets=offs)
+    assert_parity(out, ref)
+    uni = np.random.default_rng(4).random((B, K + 1)).astype(np.float32)
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, True, uniforms=uni)
+    assert_parity(out, ref)
+
+
+def test_greedy_acceptance_exact(ctx):
+    tgt, drf, toks = c2_inputs(B=16, V=4096, seed=2)
+    # plant argmax agreement on some positions
+    for b in range(0, 16, 3):
+        drf[b, :2] = tgt[b, :2]
+    out, ref = run_both(ctx, tgt, drf, toks, 0.0, True, greedy=True)
+    assert np.array_equal(out["accept_len"], ref["accept_len"])
+    assert np.array_equal(out["token"], ref["token"])
+    assert np.all(out["draws"] == 0)
+
+
+def test_argmax_ties_take_last_index(ctx):
+    V = 256
+    tgt = np.zeros((1, 2, V), np.float32)
+    drf = np.zeros((1, 1, V), np.float32)
+    tgt[0, 0, [3, 200]] = 5.0
+    drf[0, 0, [3, 200]] = 5.0
+    out, ref = run_both(ctx, tgt, drf, np.array([[7]], np.uint32), 0.0, True, greedy=True)
+    assert out["accept_len"][0] == 1 and out["token"][0] == ref["token"][0] == 255  # bonus row all zeros
+
+
+def test_ragged_proposals_and_mtp_round(ctx):
+    tgt, drf, toks = c2_inputs(B=12, K=4, V=2048, seed=3)
+    nprop = np.array([0, 1, 2, 3, 4, 4, 3, 2, 1, 0, 4, 2], np.int32)
+    for bonus in (False, True):
+        out, ref = run_both(ctx, tgt, drf, toks, 0.7, bonus, seeds=np.arange(12, dtype=np.uint64), nprop=nprop)
+        assert_parity(out, ref)
+        assert np.all(out["accept_len"] <= nprop)
+
+
+def test_sampling_only_launch_is_inverse_cdf(ctx):
+    # K = 0 with bonus: plain sample_probabilities(probabilities(logits)) per sequence
+    rng = np.random.default_rng(5)
+    B, V = 64, 32000
+    tgt = rng.normal(0, 3, (B, 1, V)).astype(np.float32)
+    out, ref = run_both(ctx, tgt, np.zeros((B, 0, V), np.float32), np.zeros((B, 0), np.uint32), 0.8, True,
+                        seeds=np.arange(B, dtype=np.uint64))
+    assert_parity(out, ref)
+    assert np.all(out["draws"] == 1)
+
+
+def test_out_of_vocab_draft_token_rejects(ctx):
+    tgt, drf, toks = c2_inputs(B=4, K=2, V=1024, seed=6)
+    toks[:, 0] = 5000  # q = 0 -> rejected without a draw (speculative.rs:764-767)
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, True, seeds=np.arange(4, dtype=np.uint64))
+    assert np.all(out["accept_len"] == 0) and np.array_equal(out["token"], ref["token"])
+    assert np.all(out["draws"] == 1)
+
+
+def test_zero_mass_residual_reports_error(ctx):
+    # A draft token with q[x] = 0 is rejected without a draw; if p == q the residual
+    # max(0, p - q) has no mass: the reference returns Err (speculative.rs:784-788).
+    V = 512
+    l = np.random.default_rng(7).normal(0, 1, V).astype(np.float32)
+    l[5] = -np.inf
+    tgt = np.stack([l, l])[None]
+    drf = l[None, None]
+    toks = np.array([[5]], np.uint32)
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).astype(dt)).to(DEV)
+    out = ctx.accept_sample(t(tgt, np.float32), t(drf, np.float32), t(toks, np.int32), A.Sampler.top_k_top_p(1.0),
+                            True, seeds=t(np.array([1]), np.int64))
+    assert int(out["accept_len"][0]) == 0 and int(out["status"][0]) == 1
+    with pytest.raises(ValueError):
+        R.accept_batch(tgt, drf, toks, R.sampler(temperature=1.0), True, seeds=np.array([1], np.uint64))
+
+
+def test_speculative_sampling_preserves_target_distribution(ctx):
+    # speculative.rs:926-950 on the device: 50k independent sequences, one round each.
+    target = np.array([0.1, 0.2, 0.7], np.float32)
+    draft = np.array([0.6, 0.3, 0.1], np.float32)
+    B = 50000
+    tl = np.broadcast_to(np.log(target), (B, 2, 3)).astype(np.float32)
+    dl = np.broadcast_to(np.log(draft), (B, 1, 3)).astype(np.float32)
+    rng = np.random.default_rng(8)
+    props = rng.choice(3, size=(B, 1), p=draft / draft.sum()).astype(np.int32)
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).astype(dt)).to(DEV)
+    out = ctx.accept_sample(t(tl, np.float32), t(dl, np.float32), t(props, np.int32), A.Sampler.top_k_top_p(1.0),
+                            False, seeds=t(np.arange(B), np.int64))
+    acc = out["accept_len"].cpu().numpy()
+    tok = np.where(acc == 1, props[:, 0], out["token"].cpu().numpy())
+    freq = np.bincount(tok, minlength=3) / B
+    assert np.max(np.abs(freq - target)) < 0.01

@@ -1,0 +1,132 @@
+"""Parity of the device verify forward (model.rs:529-587) and MTP head
+(model.rs:783-817) against the oracle on identical random-init weights.
+Bar: logits within 2e-3 relative (max|d|/max|ref| per row), hidden states likewise."""
+import numpy as np
+import pytest
+
+import aarambh_hip as A
+import refcpu as R
+from gpu_util import make_pair, rel_rows
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def test_f32_model_prefill_and_verify():
+    # C1 shape family (head_dim 32, ffn 704 not a multiple of 128) at reduced depth.
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=704, n_layers=2, n_heads=8, n_kv_heads=2, max_seq_len=96,
+              num_future_tokens=2)
+    ref, hip = make_pair(seed=1, **kw)
+    ids = R.synth_tokens(1, 1, 24, 1024)
+    kv = ref.kv(96)
+    wl, wh = kv.forward(ids[:20], 0)
+    gl, gh = hip.forward_with_cache_output(ids[None, :20], [0])
+    assert rel_rows(gl[0], wl).max() < 1e-4 and rel_rows(gh[0], wh).max() < 1e-4
+    wl2, _ = kv.forward(ids[20:], 20)
+    gl2, _ = hip.forward_with_cache_output(ids[None, 20:], [20])
+    assert rel_rows(gl2[0], wl2).max() < 1e-4
+    assert hip.kv_len(0) == 24
+    hip.close()
+
+
+@pytest.mark.parametrize("wfmt,kvfmt,lmfmt", [(A.W_INT8_ROW, A.KV_F16, 1), (A.W_INT4_G128, A.KV_INT8, 1),
+                                              (A.W_BF16, A.KV_F32, 0)])
+def test_quantised_verify_matches_oracle(wfmt, kvfmt, lmfmt):
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2, max_seq_len=160,
+              num_future_tokens=3, weight_format=wfmt, kv_format=kvfmt, lm_head_format=lmfmt)
+    ref, hip = make_pair(seed=2, max_batch=3, max_rows=128, **kw)
+    B, P, K = 3, 37, 4
+    prompts = R.synth_tokens(2, 7, B * (P + K), 2048).reshape(B, P + K)
+    kvs = [ref.kv(160) for _ in range(B)]
+    # batched prefill of different lengths via per-sequence offsets: run P tokens for all
+    gl, gh = hip.forward_with_cache_output(prompts[:, :P], [0, 0, 0])
+    for b in range(B):
+        wl, wh = kvs[b].forward(prompts[b, :P], 0)
+        assert rel_rows(gl[b], wl).max() < TOL, (b, rel_rows(gl[b], wl).max())
+        assert rel_rows(gh[b], wh).max() < TOL
+    # verify K tokens at offset P (the hot call)
+    gl, gh = hip.forward_with_cache_output(prompts[:, P:], [P, P, P])
+    for b in range(B):
+        wl, wh = kvs[b].forward(prompts[b, P:], P)
+        assert rel_rows(gl[b], wl).max() < TOL
+    # rollback by index and replay a shorter suffix (mtp_speculative.rs:284-313)
+    gl, _ = hip.forward_with_cache_output(prompts[:, P:P + 2], [P, P, P])
+    for b in range(B):
+        kvs[b].truncate(P)
+        wl, _ = kvs[b].forward(prompts[b, P:P + 2], P)
+        assert rel_rows(gl[b], wl).max() < TOL
+    assert hip.kv_len(1) == P + 2
+    hip.close()
+
+
+def test_int4_preloaded_codes_equal_device_quantisation():
+    """aarh_load_tensor_int4 with the oracle's codes (int4.rs layout) and
+    aarh_load_tensor_f32 (device quantiser) must give bit-identical logits."""
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=64,
+              weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    ref, hip = make_pair(seed=3, **kw)
+    hip2 = A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=64)
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        raw = R.synth_fill(3, i, r * c, 0.02) if kind != R.T_NORM else np.ones(r * c, np.float32)
+        if kind == R.T_LINEAR:
+            p, sh, zh = R.quantise_i4_f16(raw, 128)
+            hip2.load_int4(i, p, sh, zh, r, c, 128)
+        else:
+            hip2.load_f32(i, raw)
+    ids = R.synth_tokens(3, 1, 9, 1024)
+    a, _ = hip.forward_with_cache_output(ids[None], [0])
+    b, _ = hip2.forward_with_cache_output(ids[None], [0])
+    assert np.array_equal(a, b)
+    hip.close()
+    hip2.close()
+
+
+def test_int8_preloaded_codes_equal_device_quantisation():
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=64,
+              weight_format=A.W_INT8_ROW, lm_head_format=1, kv_format=A.KV_F16)
+    ref, hip = make_pair(seed=4, **kw)
+    hip2 = A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=64)
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        raw = R.synth_fill(4, i, r * c, 0.02) if kind != R.T_NORM else np.ones(r * c, np.float32)
+        if kind == R.T_LINEAR:
+            q, sc = R.quantise_i8_rows(raw.reshape(r, c))
+            hip2.load_int8(i, q, sc, r, c)
+        else:
+            hip2.load_f32(i, raw)
+    ids = R.synth_tokens(4, 1, 9, 1024)
+    a, _ = hip.forward_with_cache_output(ids[None], [0])
+    b, _ = hip2.forward_with_cache_output(ids[None], [0])
+    assert np.array_equal(a, b)
+    hip.close()
+    hip2.close()
+
+
+def test_mtp_heads_match_oracle():
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=1, n_heads=4, n_kv_heads=2, max_seq_len=64,
+              num_future_tokens=4, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    ref, hip = make_pair(seed=5, max_batch=2, **kw)
+    anchors = np.random.default_rng(5).normal(0, 1, (2, 512)).astype(np.float32)
+    for head in range(3):
+        ids = R.synth_tokens(5, head, 2 * (head + 1), 2048).reshape(2, head + 1)
+        got = hip.forward_mtp_head(head, anchors, ids)
+        for b in range(2):
+            want = ref.mtp_head(head, anchors[b], ids[b])
+            assert rel_rows(got[b][None], want[None]).max() < TOL
+    with pytest.raises(A.ConfigError):
+        hip.forward_mtp_head(3, anchors, np.zeros((2, 4), np.uint32))
+    hip.close()
+
+
+def test_shape_errors_are_reported():
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=32)
+    hip = A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=32)
+    hip.init_synthetic(0)
+    with pytest.raises(A.ShapeError):  # offset beyond the cached length
+        hip.forward_with_cache_output(np.zeros((1, 2), np.uint32), [5])
+    with pytest.raises(A.ShapeError):  # context overflow (check_token_ids, model.rs:886-907)
+        hip.forward_with_cache_output(np.zeros((1, 33), np.uint32), [0])
+    with pytest.raises(A.ShapeError):
+        hip.forward_with_cache_output(np.full((1, 2), 5000, np.uint32), [0])
+    with pytest.raises(A.ShapeError):
+        hip.restore(3)  # cannot grow by rollback
+    hip.close()
