@@ -110,6 +110,11 @@ def lib():
                                          C.POINTER(_Sampler), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
         "aarh_mtp_generate": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
                                         _P, _P, _P, C.POINTER(_Stats)]),
+        "aarh_session_begin": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler),
+                                         _P, C.POINTER(_P)]),
+        "aarh_session_step": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
+        "aarh_session_result": (C.c_int, [_P, _P, C.c_int32, _P, _P, C.POINTER(_Stats)]),
+        "aarh_session_end": (None, [_P]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
@@ -126,7 +131,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_tensor_info", "aarh_load_tensor_f32", "aarh_load_tensor_int4", "aarh_load_tensor_int8",
             "aarh_init_synthetic", "aarh_kv_reset", "aarh_kv_len", "aarh_kv_rollback", "aarh_kv_fill_synthetic",
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
-            "aarh_accept_sample", "aarh_mtp_generate", "aarh_prof_enable", "aarh_prof_get"]
+            "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
+            "aarh_session_result", "aarh_session_end", "aarh_prof_enable", "aarh_prof_get"]
 
 
 def _ptr(a):
@@ -401,3 +407,51 @@ class MtpSpeculativeEngine:
 
     def generate(self, prompt_ids, max_new_tokens, sampler: Sampler):
         return self.generate_batch(np.asarray(prompt_ids)[None, :], max_new_tokens, sampler)[0]
+
+    def session(self, prompts, max_new_tokens, sampler: Sampler, cached_len=0, seeds=None):
+        return Session(self, prompts, max_new_tokens, sampler, cached_len, seeds)
+
+
+class Session:
+    """Round-by-round driver of the MTP engine (aarh_session_*)."""
+
+    def __init__(self, engine, prompts, max_new_tokens, sampler, cached_len=0, seeds=None):
+        self.engine = engine
+        m = engine.model
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.uint32)
+        self.nseq = prompts.shape[0]
+        self.max_new = max_new_tokens
+        sd = np.ascontiguousarray(
+            np.full(self.nseq, sampler.seed, np.uint64) if seeds is None else seeds, np.uint64)
+        h = _P()
+        m._check(lib().aarh_session_begin(m.h, _ptr(prompts), self.nseq, prompts.shape[1], cached_len,
+                                          max_new_tokens, engine.config.num_draft_tokens, C.byref(sampler._c()),
+                                          _ptr(sd), C.byref(h)))
+        self.h = h
+
+    def step(self, rounds=1):
+        done = C.c_int32()
+        self.engine.model._check(lib().aarh_session_step(self.h, rounds, C.byref(done)))
+        return bool(done.value)
+
+    def result(self):
+        n = self.nseq
+        out = np.zeros((n, max(self.max_new, 1)), np.uint32)
+        ln = np.zeros(n, np.int32)
+        fin = np.zeros(n, np.int32)
+        stats = (_Stats * n)()
+        self.engine.model._check(lib().aarh_session_result(self.h, _ptr(out), out.shape[1], _ptr(ln), _ptr(fin),
+                                                           stats))
+        res = []
+        for b in range(n):
+            st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
+            res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st))
+        return res
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aarh_session_end(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

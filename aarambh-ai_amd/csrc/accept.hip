@@ -42,7 +42,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     __shared__ float red_f[ACC_THREADS / WAVE];
     __shared__ int red_k[ACC_THREADS / WAVE];
     __shared__ int red_i[ACC_THREADS / WAVE];
-    __shared__ int is_last;
+    __shared__ unsigned is_last;
     __shared__ float sh_bcast[4];
     __shared__ int sh_ibcast[8];
 
@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
                 int k0 = red_k[0], i0 = red_i[0];
                 for (int w = 1; w < ACC_THREADS / WAVE; w++)
                     if (red_k[w] > k0 || (red_k[w] == k0 && red_i[w] > i0)) { k0 = red_k[w]; i0 = red_i[w]; }
-                a.row_argmax[row_id] = i0;
+                st_coh_i32(&a.row_argmax[row_id], i0);
             }
         } else {
             const float T = a.temperature;
@@ -107,30 +107,21 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
             if (wid == 0) {
                 SeqSum ss = seq_sum_wave(lds, V, -1.0f);
                 if (lane == 0) {
-                    a.row_max[row_id] = mx;
-                    a.row_sum[row_id] = ss.total;
+                    st_coh(&a.row_max[row_id], mx);
+                    st_coh(&a.row_sum[row_id], ss.total);
                 }
             }
         }
     }
 
     // ---------------- last workgroup of the sequence resolves ----------------
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        unsigned prev = atomicAdd(&a.counters[b], 1u);
-        is_last = (prev == (unsigned)rows_per_seq - 1u);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
+    if (!arrive_last(&a.counters[b], (unsigned)rows_per_seq, &is_last)) return;
 
     const size_t seq_row0 = (size_t)b * rows_per_seq;
     const float* trow0 = a.target + (size_t)b * a.target_rows * V;
     const float* drow0 = a.draft + (size_t)b * a.K * V;
 
     if (tid == 0) {
-        a.counters[b] = 0u;
         uint32_t key[8];
         rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
         uint64_t word = a.word_offsets ? a.word_offsets[b] : 0ull;
@@ -138,7 +129,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
         uint32_t flags = 0;
         for (int i = 0; i < np; i++) {
             if (a.greedy) {
-                if (a.row_argmax[seq_row0 + a.target_rows + i] == a.row_argmax[seq_row0 + i]) {
+                if (ld_coh_i32(&a.row_argmax[seq_row0 + a.target_rows + i]) == ld_coh_i32(&a.row_argmax[seq_row0 + i])) {
                     acc++;
                     continue;
                 }
@@ -150,9 +141,10 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
             const float* dl = drow0 + (size_t)i * V;
             float p = 0.0f, q = 0.0f;
             if ((int)x < V) {
-                p = row_prob(tl, (int)x, 0.f, a.temperature, a.row_max[seq_row0 + i], a.row_sum[seq_row0 + i]);
-                q = row_prob(dl, (int)x, 0.f, a.temperature, a.row_max[seq_row0 + a.target_rows + i],
-                             a.row_sum[seq_row0 + a.target_rows + i]);
+                p = row_prob(tl, (int)x, 0.f, a.temperature, ld_coh(&a.row_max[seq_row0 + i]),
+                             ld_coh(&a.row_sum[seq_row0 + i]));
+                q = row_prob(dl, (int)x, 0.f, a.temperature, ld_coh(&a.row_max[seq_row0 + a.target_rows + i]),
+                             ld_coh(&a.row_sum[seq_row0 + a.target_rows + i]));
             }
             if (!(q > 0.0f)) {
                 rej = i;
@@ -183,15 +175,16 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     int token = -1, status = 0;
 
     if (a.greedy) {
-        if (rej >= 0) token = a.row_argmax[seq_row0 + rej];
-        else if (a.bonus) token = a.row_argmax[seq_row0 + np];
+        if (rej >= 0) token = ld_coh_i32(&a.row_argmax[seq_row0 + rej]);
+        else if (a.bonus) token = ld_coh_i32(&a.row_argmax[seq_row0 + np]);
     } else if (rej >= 0 || a.bonus) {
         const float T = a.temperature;
         if (rej >= 0) {
             const float* tl = trow0 + (size_t)rej * V;
             const float* dl = drow0 + (size_t)rej * V;
-            const float pmx = a.row_max[seq_row0 + rej], pS = a.row_sum[seq_row0 + rej];
-            const float qmx = a.row_max[seq_row0 + a.target_rows + rej], qS = a.row_sum[seq_row0 + a.target_rows + rej];
+            const float pmx = ld_coh(&a.row_max[seq_row0 + rej]), pS = ld_coh(&a.row_sum[seq_row0 + rej]);
+            const float qmx = ld_coh(&a.row_max[seq_row0 + a.target_rows + rej]);
+            const float qS = ld_coh(&a.row_sum[seq_row0 + a.target_rows + rej]);
             for (int j = tid; j < V; j += ACC_THREADS) {
                 float d = row_prob(tl, j, 0.f, T, pmx, pS) - row_prob(dl, j, 0.f, T, qmx, qS);
                 lds[j] = d > 0.0f ? d : 0.0f;
@@ -210,7 +203,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
             }
         } else {
             const float* tl = trow0 + (size_t)np * V;
-            const float pmx = a.row_max[seq_row0 + np], pS = a.row_sum[seq_row0 + np];
+            const float pmx = ld_coh(&a.row_max[seq_row0 + np]), pS = ld_coh(&a.row_sum[seq_row0 + np]);
             for (int j = tid; j < V; j += ACC_THREADS) lds[j] = row_prob(tl, j, 0.f, T, pmx, pS);
         }
         __syncthreads();

@@ -81,6 +81,51 @@ __device__ inline float rng_f32(const uint32_t key[8], uint64_t word) {
 }
 
 // ---------------------------------------------------------------------------
+// Cross-workgroup hand-off without L2 flushes.
+//
+// A device-scope fence on gfx950 writes back the whole XCD L2 (buffer_wbl2),
+// which costs microseconds per workgroup.  Data that one workgroup hands to
+// another inside a kernel (split-K partials, row statistics) is instead written
+// and read with agent-scope relaxed atomics, which compile to sc1 (coherent,
+// L2-bypassing) stores/loads; the writer waits for its stores to complete
+// (s_waitcnt vmcnt(0)) before it signals arrival on the counter.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_i32(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_coh_i32(const int32_t* p) {
+    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this thread's memory operations have completed.
+__device__ __forceinline__ void wait_mem() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Called by every thread of the workgroup after its coherent stores; returns
+// true in the workgroup that arrives last (which also re-arms the counter).
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, unsigned* s_flag) {
+    wait_mem();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool last = prev == expected - 1u;
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    bool last = *s_flag != 0u;
+    wait_mem();
+    return last;
+}
+
+// ---------------------------------------------------------------------------
 // Wave-level primitives
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int wave_excl_scan_i32(int v) {

@@ -230,30 +230,33 @@ __device__ void run_epilogue(const GemvArgs& a, float* yt, int rg) {
 // ---------------------------------------------------------------------------
 __device__ void prologue_inv_rms(const GemvArgs& a, float* s_inv) {
     if (!a.norm_w) return;
-    for (int m = threadIdx.x; m < a.M; m += blockDim.x) {
+    // one wave per row: lane p loads partial p (n_ssq <= 64), one round trip
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int m = wid; m < a.M; m += nw) {
         float ss = 0.0f;
-        for (int p = 0; p < a.n_ssq; p++) ss += a.ssq_part[(size_t)p * a.M + m];
-        s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+        for (int p = lane; p < a.n_ssq; p += 64) ss += a.ssq_part[(size_t)p * a.M + m];
+        ss = wave_sum_f32(ss);
+        if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
     }
 }
 
-// Split-K partial write or (S == 1) direct reduction, then the epilogue.
+// Split-K: the last workgroup of a row group sums the S partials in order.
 __device__ bool finish_partials(const GemvArgs& a, int rg, float* yt, unsigned* s_flag) {
     if (a.S == 1) return true;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(&a.counters[rg], 1u);
-        *s_flag = (prev == (unsigned)a.S - 1u) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!*s_flag) return false;
-    __threadfence();
-    if (threadIdx.x == 0) a.counters[rg] = 0u;
+    if (!arrive_last(&a.counters[rg], (unsigned)a.S, s_flag)) return false;
     for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
         int m = idx >> 7, c = idx & 127;
+        const float* p = a.part + (size_t)m * a.N + rg * 128 + c;
+        const size_t stride = (size_t)a.M * a.N;
         float y = 0.0f;
-        for (int s = 0; s < a.S; s++) y += a.part[((size_t)s * a.M + m) * a.N + rg * 128 + c];
+        // batches of 8 independent coherent loads: one memory round trip per batch
+        for (int s0 = 0; s0 < a.S; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = (s0 + j < a.S) ? ld_coh(p + (size_t)(s0 + j) * stride) : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) y += v[j];
+        }
         yt[idx] = y;
     }
     __syncthreads();
@@ -433,7 +436,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_mfma_kernel(GemvArgs a) {
             }
             if (writer && m < a.M) {
                 if (a.S == 1) yt[m * 128 + wid * 16 + lr] = v;
-                else a.part[((size_t)ks * a.M + m) * a.N + ncol] = v;
+                else st_coh(&a.part[((size_t)ks * a.M + m) * a.N + ncol], v);
             }
         }
     }
@@ -493,7 +496,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_f32_kernel(GemvArgs a) {
                 float v = 0.f;
                 for (int r = 0; r < 16; r++)
                     if (r == lane) v = res[r][mm];
-                a.part[((size_t)ks * a.M + mb + mm) * a.N + rg * 128 + wid * 16 + lane] = v;
+                st_coh(&a.part[((size_t)ks * a.M + mb + mm) * a.N + rg * 128 + wid * 16 + lane], v);
             }
         }
         if (a.S == 1) {

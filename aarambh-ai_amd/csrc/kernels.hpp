@@ -118,6 +118,7 @@ struct AcceptArgs {
 int launch_accept(const AcceptArgs& a, hipStream_t stream);
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
+bool attention_uses_mfma(int kv_fmt, int hd);
 
 // misc kernels
 int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x,

@@ -329,12 +329,14 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
     at.scale = (float)(1.0 / std::sqrt((double)c->hd));
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
     const int Rt = S * G;
-    at.rows_per_tile = std::min(32, Rt);
+    const bool mf = attention_uses_mfma(kv_fmt, c->hd);
+    const int gran = mf ? 128 : 64;  // tokens per chunk granule
+    at.rows_per_tile = std::min(mf ? 16 : 32, Rt);
     at.ntiles = (Rt + at.rows_per_tile - 1) / at.rows_per_tile;
     const int base = nseq * c->cfg.n_kv_heads * at.ntiles;
-    const int max_chunks = std::max(1, (max_kv_len + 63) / 64);
+    const int max_chunks = std::max(1, (max_kv_len + gran - 1) / gran);
     int nch = std::max(1, std::min(max_chunks, (512 + base - 1) / base));
-    int chunk = ((max_kv_len + nch - 1) / nch + 63) / 64 * 64;
+    int chunk = ((max_kv_len + nch - 1) / nch + gran - 1) / gran * gran;
     nch = (max_kv_len + chunk - 1) / chunk;
     at.chunk = chunk;
     at.nchunks = nch;
@@ -579,7 +581,7 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     if (g.max_rows > 128) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 128");
     c->Fp = (c->F + 127) / 128 * 128;
     c->Mmax = g.max_rows;
-    c->cap = g.max_seq_len;
+    c->cap = (g.max_seq_len + 31) / 32 * 32;  // V^T rows padded so 32-token blocks stay in bounds
     *out = c;
     if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -683,10 +685,10 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         const int maxrg = std::max({c->V, 2 * c->Fp, c->QD + 2 * c->KD, c->H}) / 128;
         if (dalloc(c, &c->gcnt, (size_t)maxrg * 4)) return AARH_ERR_DEVICE;
         HIPCHK(c, hipMemset(c->gcnt, 0, (size_t)maxrg * 4));
-        // attention scratch: groups = nseq*n_kv*ntiles <= n_kv*(M + M*G/32); the chunk count
+        // attention scratch: groups = nseq*n_kv*ntiles <= n_kv*(M + M*G/16); the chunk count
         // is at most ceil(512/groups) so groups*chunks <= groups + 512.
         const int G = g.n_heads / g.n_kv_heads;
-        const size_t groups = (size_t)g.n_kv_heads * ((size_t)M + ((size_t)M * G + 31) / 32);
+        const size_t groups = (size_t)g.n_kv_heads * ((size_t)M + ((size_t)M * G + 15) / 16);
         c->apart_elems = (groups + 512) * 32 * (c->hd + 2);
         if (dalloc(c, &c->apart, c->apart_elems * 4)) return AARH_ERR_DEVICE;
         if (dalloc(c, &c->acnt, groups * 4)) return AARH_ERR_DEVICE;
@@ -894,7 +896,8 @@ int aarh_kv_rollback(aarh_ctx* c, int slot, int32_t new_len) {
 
 int aarh_kv_fill_synthetic(aarh_ctx* c, int slot, int32_t len, uint64_t seed) {
     if (!c || slot < 0 || slot >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", slot);
-    if (len < 0 || len > c->cap) return fail(c, AARH_ERR_SHAPE, "length %d exceeds capacity %d", len, c->cap);
+    if (len < 0 || len > c->cfg.max_seq_len)
+        return fail(c, AARH_ERR_SHAPE, "length %d exceeds max_seq_len %d", len, c->cfg.max_seq_len);
     for (int l = 0; l < c->cfg.n_layers; l++)
         KCHK(c, launch_kv_fill_synthetic(c->kc[l], c->vc[l], c->ksc[l], c->vsc[l], c->cfg.kv_format, slot,
                                          c->cfg.n_kv_heads, c->hd, c->cap, len, seed, l, c->stream));
@@ -1086,9 +1089,23 @@ int aarh_prof_get(aarh_ctx* c, int cls, double* total_ms, double* alg_bytes, int
 // Engine: MtpSpeculativeEngine::generate_with_callback (mtp_speculative.rs:86-336)
 // for nseq independent requests in lock-step rounds.
 // ===========================================================================
+// ===========================================================================
+// Engine: MtpSpeculativeEngine::generate_with_callback (mtp_speculative.rs:86-336)
+// for nseq independent requests in lock-step rounds, as a session so callers
+// (benchmarks, servers) can run it round by round.
+// ===========================================================================
 namespace {
 
-struct EngineBufs {
+constexpr uint32_t EOS_ID = 0;  // tokenizer/src/special.rs:33
+
+}  // namespace
+
+struct aarh_session {
+    aarh_ctx* c = nullptr;
+    int nseq = 0, K = 0, max_new = 0, max_new_req = 0, available = 0;
+    bool greedy = true;
+    aarh_sampler samp{};
+    // device
     float *tgt = nullptr, *drf = nullptr, *anchor = nullptr, *vhid = nullptr;
     uint32_t* props = nullptr;
     int32_t *acc_len = nullptr, *acc_tok = nullptr, *acc_draws = nullptr, *acc_status = nullptr, *nprop = nullptr;
@@ -1096,23 +1113,227 @@ struct EngineBufs {
     uint64_t *seeds = nullptr, *offs = nullptr;
     const float** src = nullptr;
     float** dst = nullptr;
-    void release() {
-        for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)props, (void*)acc_len, (void*)acc_tok,
-                        (void*)acc_draws, (void*)acc_status, (void*)nprop, (void*)acc_flags, (void*)seeds, (void*)offs,
-                        (void*)src, (void*)dst})
+    // host state
+    std::vector<uint64_t> hoffs;
+    std::vector<char> finished;
+    std::vector<std::vector<uint32_t>> out;
+    std::vector<int32_t> finish;
+    std::vector<aarh_spec_stats> stats;
+    std::vector<uint32_t> hprops;
+    std::vector<int32_t> slots, base, count, hnp, hlen, htok, hdraws, hstatus;
+
+    ~aarh_session() {
+        for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)props, (void*)acc_len,
+                        (void*)acc_tok, (void*)acc_draws, (void*)acc_status, (void*)nprop, (void*)acc_flags,
+                        (void*)seeds, (void*)offs, (void*)src, (void*)dst})
             if (p) (void)hipFree(p);
     }
 };
 
-constexpr uint32_t EOS_ID = 0;  // tokenizer/src/special.rs:33
+namespace {
+
+int copy_rows_host_lists(aarh_session* e, const std::vector<const float*>& s, const std::vector<float*>& d, int n) {
+    aarh_ctx* c = e->c;
+    if (s.empty()) return 0;
+    const int rows = (int)s.size();
+    HIPCHK(c, hipMemcpyAsync(e->src, s.data(), rows * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(e->dst, d.data(), rows * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+    KCHK(c, launch_copy_rows(e->src, e->dst, rows, n, c->stream));
+    // the host vectors must outlive the async copies
+    return sync_stream(c);
+}
+
+// One round of mtp_speculative.rs:161-322 for every unfinished sequence.
+int session_round(aarh_session* e) {
+    aarh_ctx* c = e->c;
+    const int nseq = e->nseq, K = e->K, V = c->V, H = c->H;
+    int r;
+    int Kr = 1;
+    for (int b = 0; b < nseq; b++) {
+        e->base[b] = c->kv_len[b];
+        e->count[b] = e->finished[b] ? 1 : std::min(K, e->max_new - (int)e->out[b].size());
+        Kr = std::max(Kr, e->count[b]);
+    }
+    // ---- proposals: index 0 from target_next, index p from MTP head p-1 ----
+    {
+        std::vector<const float*> s(nseq);
+        std::vector<float*> d(nseq);
+        for (int b = 0; b < nseq; b++) {
+            s[b] = e->tgt + (size_t)b * (K + 1) * V;
+            d[b] = e->drf + (size_t)b * K * V;
+        }
+        HIPCHK(c, hipMemcpyAsync(e->src, s.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(e->dst, d.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+        KCHK(c, launch_copy_rows(e->src, e->dst, nseq, V, c->stream));
+        if ((r = sync_stream(c))) return r;
+    }
+    for (int p = 0; p < Kr; p++) {
+        if (p > 0) {
+            if ((r = mtp_head_dev(c, p - 1, e->anchor, H, e->props, K, nseq, e->drf + (size_t)p * V, (long long)K * V)))
+                return r;
+            for (int b = 0; b < nseq; b++)
+                if (!e->finished[b] && e->count[b] > p) e->stats[b].mtp_head_forwards++;
+        }
+        if (e->greedy) {
+            KCHK(c, launch_argmax_rows(e->drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)e->props + p, K,
+                                       nullptr, c->stream));
+        } else {
+            std::vector<uint64_t> o(nseq);
+            for (int b = 0; b < nseq; b++) o[b] = e->hoffs[b] + p;
+            HIPCHK(c, hipMemcpyAsync(e->offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
+            if ((r = aarh_accept_sample(c, e->drf + (size_t)p * V, K, nullptr, nullptr, nullptr, nseq, 0, V, 1, &e->samp,
+                                        e->seeds, e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
+                                        e->acc_status, nullptr)))
+                return r;
+            if ((r = sync_stream(c))) return r;
+            std::vector<int32_t> t(nseq);
+            HIPCHK(c, hipMemcpy(t.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
+            for (int b = 0; b < nseq; b++) e->hprops[(size_t)b * K + p] = (uint32_t)t[b];
+            HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
+        }
+    }
+    if ((r = sync_stream(c))) return r;
+    HIPCHK(c, hipMemcpy(e->hprops.data(), e->props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost));
+    for (int b = 0; b < nseq; b++) {
+        int np = 0;
+        if (!e->finished[b]) {
+            for (int p = 0; p < e->count[b]; p++) {
+                np++;
+                e->stats[b].draft_tokens_proposed++;
+                if (e->hprops[(size_t)b * K + p] == EOS_ID) break;
+            }
+        }
+        e->hnp[b] = np;
+        if (!e->greedy) e->hoffs[b] += np;
+    }
+    // ---- verify forward (finished sequences run at a dummy position 0) ----
+    {
+        std::vector<uint32_t> ids((size_t)nseq * Kr);
+        std::vector<int32_t> off(nseq);
+        for (int b = 0; b < nseq; b++) {
+            for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = e->hprops[(size_t)b * K + std::min(s2, K - 1)];
+            off[b] = e->finished[b] ? 0 : e->base[b];
+            if (e->finished[b]) c->kv_len[b] = 0;
+        }
+        int mk = 0;
+        if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk))) return r;
+        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, e->tgt + V, rm(Kr, (long long)(K + 1) * V, V),
+                             e->vhid)))
+            return r;
+        for (int b = 0; b < nseq; b++) {
+            if (e->finished[b]) continue;
+            e->stats[b].rounds++;
+            e->stats[b].target_decode_forwards++;
+        }
+    }
+    // ---- acceptance (MTP round: no bonus) ----
+    {
+        HIPCHK(c, hipMemcpyAsync(e->offs, e->hoffs.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(e->nprop, e->hnp.data(), nseq * 4, hipMemcpyHostToDevice, c->stream));
+        if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 0, &e->samp, e->seeds,
+                                    e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
+                                    nullptr)))
+            return r;
+        if ((r = sync_stream(c))) return r;
+        HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->hdraws.data(), e->acc_draws, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->hstatus.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
+    }
+    // ---- commit, rollback, replay ----
+    std::vector<int> replay_seq, replay_len;
+    std::vector<const float*> ls, hs;
+    std::vector<float*> ld, hdv;
+    for (int b = 0; b < nseq; b++) {
+        if (e->finished[b]) continue;
+        if (e->hstatus[b] != 0)
+            return fail(c, AARH_ERR_CONFIG, "speculative residual distribution has zero probability mass");
+        if (!e->greedy) e->hoffs[b] += e->hdraws[b];
+        const int np = e->hnp[b], acc = e->hlen[b];
+        bool done = false;
+        for (int i = 0; i < acc && !done; i++) {
+            e->stats[b].draft_tokens_accepted++;
+            const uint32_t t = e->hprops[(size_t)b * K + i];
+            if (t == EOS_ID) {
+                e->finish[b] = AARH_FINISH_EOS;
+                done = true;
+                break;
+            }
+            e->out[b].push_back(t);
+            if ((int)e->out[b].size() == e->max_new) done = true;
+        }
+        if (done) {
+            e->finished[b] = 1;
+            c->kv_len[b] = e->base[b] + np;
+            continue;
+        }
+        if (acc < np) {
+            const uint32_t repl = (uint32_t)e->htok[b];
+            c->kv_len[b] = e->base[b];  // target_cache.restore(snapshot)
+            if (repl == EOS_ID) {
+                e->finish[b] = AARH_FINISH_EOS;
+                e->finished[b] = 1;
+                continue;
+            }
+            e->out[b].push_back(repl);
+            e->hprops[(size_t)b * K + acc] = repl;  // replay ids = proposals[..i] + replacement
+            replay_seq.push_back(b);
+            replay_len.push_back(acc + 1);
+        } else {
+            // everything accepted: target_next / anchor from the last verify row
+            c->kv_len[b] = e->base[b] + np;
+            ls.push_back(e->tgt + ((size_t)b * (K + 1) + np) * V);
+            ld.push_back(e->tgt + (size_t)b * (K + 1) * V);
+            hs.push_back(e->vhid + ((size_t)b * Kr + np - 1) * H);
+            hdv.push_back(e->anchor + (size_t)b * H);
+        }
+    }
+    // rows that come from the verify buffers must be copied before the replay reuses scratch
+    if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hs, hdv, H))) return r;
+    if (!replay_seq.empty()) {
+        const int nr = (int)replay_seq.size();
+        int Sr = 0;
+        for (int L : replay_len) Sr = std::max(Sr, L);
+        std::vector<uint32_t> ids((size_t)nr * Sr);
+        std::vector<int32_t> sl(nr), off(nr);
+        for (int j = 0; j < nr; j++) {
+            const int b = replay_seq[j];
+            sl[j] = b;
+            off[j] = e->base[b];
+            for (int s2 = 0; s2 < Sr; s2++)
+                ids[(size_t)j * Sr + s2] = e->hprops[(size_t)b * K + std::min(s2, replay_len[j] - 1)];
+        }
+        int mk = 0;
+        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk))) return r;
+        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, Sr, mk, c->logits, rm(nr * Sr, 0, V), c->hidden)))
+            return r;
+        std::vector<const float*> rs, rhs;
+        std::vector<float*> rd, rhd;
+        for (int j = 0; j < nr; j++) {
+            const int b = replay_seq[j];
+            e->stats[b].target_decode_forwards++;
+            c->kv_len[b] = e->base[b] + replay_len[j];
+            rs.push_back(c->logits + ((size_t)j * Sr + replay_len[j] - 1) * V);
+            rd.push_back(e->tgt + (size_t)b * (K + 1) * V);
+            rhs.push_back(c->hidden + ((size_t)j * Sr + replay_len[j] - 1) * H);
+            rhd.push_back(e->anchor + (size_t)b * H);
+        }
+        if ((r = copy_rows_host_lists(e, rs, rd, V)) || (r = copy_rows_host_lists(e, rhs, rhd, H))) return r;
+    }
+    for (int b = 0; b < nseq; b++)
+        if (!e->finished[b] && (int)e->out[b].size() >= e->max_new) e->finished[b] = 1;
+    return 0;
+}
 
 }  // namespace
 
-extern "C" int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
-                                 int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds,
-                                 uint32_t* out_tokens, int32_t* out_len, int32_t* finish_reason,
-                                 aarh_spec_stats* stats) {
-    if (!c || !s) return AARH_ERR_CONFIG;
+extern "C" {
+
+int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int cached_len,
+                       int max_new_tokens, int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds,
+                       aarh_session** out) {
+    if (!c || !s || !out) return AARH_ERR_CONFIG;
+    *out = nullptr;
     const auto& g = c->cfg;
     if (c->nheads_mtp == 0) return fail(c, AARH_ERR_CONFIG, "internal speculative decoding requires model.mtp configuration");
     if (num_draft_tokens < 2) return fail(c, AARH_ERR_CONFIG, "MTP speculative decoding requires at least two proposal tokens");
@@ -1121,313 +1342,159 @@ extern "C" int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq,
                     g.num_future_tokens);
     if (nseq <= 0 || nseq > g.max_batch) return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
     if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
-    if (prompt_len >= g.max_seq_len)
-        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", prompt_len, g.max_seq_len);
+    if (cached_len < 0) return fail(c, AARH_ERR_SHAPE, "negative cached length");
+    for (int b = 0; b < nseq; b++)
+        if (c->kv_len[b] < cached_len)
+            return fail(c, AARH_ERR_SHAPE, "slot %d holds %d cached tokens, fewer than %d", b, c->kv_len[b], cached_len);
+    const int full = cached_len + prompt_len;
+    if (full >= g.max_seq_len)
+        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", full, g.max_seq_len);
     const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
     if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
         return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
     const int K = num_draft_tokens, V = c->V, H = c->H;
-    if (nseq * K > c->Mmax || nseq * (K + 1) > c->Mmax)
-        return fail(c, AARH_ERR_SHAPE, "nseq x (draft tokens + 1) exceeds max_rows");
-    const int available = g.max_seq_len - prompt_len;
-    const int max_new = std::min(max_new_tokens, available);
-    for (int b = 0; b < nseq; b++) {
-        out_len[b] = 0;
-        finish_reason[b] = AARH_FINISH_MAX_TOKENS;
-        memset(&stats[b], 0, sizeof(aarh_spec_stats));
+    if (nseq * K > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq x draft tokens exceeds max_rows");
+    aarh_session* e = new aarh_session();
+    e->c = c;
+    e->nseq = nseq;
+    e->K = K;
+    e->greedy = greedy;
+    e->samp = *s;
+    e->available = g.max_seq_len - full;
+    e->max_new_req = max_new_tokens;
+    e->max_new = std::min(max_new_tokens, e->available);
+    e->hoffs.assign(nseq, 0);
+    e->finished.assign(nseq, 0);
+    e->out.assign(nseq, {});
+    e->finish.assign(nseq, AARH_FINISH_MAX_TOKENS);
+    e->stats.assign(nseq, aarh_spec_stats{});
+    e->hprops.assign((size_t)nseq * K, 0);
+    for (auto* v : {&e->slots, &e->base, &e->count, &e->hnp, &e->hlen, &e->htok, &e->hdraws, &e->hstatus}) v->assign(nseq, 0);
+    for (int b = 0; b < nseq; b++) e->slots[b] = b;
+    int r = 0;
+#define SA(p, bytes) \
+    if ((r = dalloc(c, &e->p, (bytes)))) { delete e; return r; }
+    SA(tgt, (size_t)nseq * (K + 1) * V * 4);
+    SA(drf, (size_t)nseq * K * V * 4);
+    SA(anchor, (size_t)nseq * H * 4);
+    SA(vhid, (size_t)nseq * K * H * 4);
+    SA(props, (size_t)nseq * K * 4);
+    SA(acc_len, nseq * 4);
+    SA(acc_tok, nseq * 4);
+    SA(acc_draws, nseq * 4);
+    SA(acc_status, nseq * 4);
+    SA(nprop, nseq * 4);
+    SA(acc_flags, nseq * 4);
+    SA(seeds, nseq * 8);
+    SA(offs, nseq * 8);
+    SA(src, (size_t)2 * g.max_batch * sizeof(void*));
+    SA(dst, (size_t)2 * g.max_batch * sizeof(void*));
+#undef SA
+    std::vector<uint64_t> hs(nseq);
+    for (int b = 0; b < nseq; b++) hs[b] = seeds ? seeds[b] : 0;
+    if (hipMemcpy(e->seeds, hs.data(), nseq * 8, hipMemcpyHostToDevice) != hipSuccess) {
+        delete e;
+        return fail(c, AARH_ERR_DEVICE, "seed upload failed");
     }
-    if (max_new <= 0) {
-        for (int b = 0; b < nseq; b++) finish_reason[b] = AARH_FINISH_CONTEXT_LIMIT;
+    if (e->max_new <= 0) {
+        for (int b = 0; b < nseq; b++) {
+            e->finish[b] = AARH_FINISH_CONTEXT_LIMIT;
+            e->finished[b] = 1;
+        }
+        *out = e;
         return 0;
     }
-    EngineBufs eb;
-    int r = 0;
-#define EB_ALLOC(p, bytes) \
-    if ((r = dalloc(c, &eb.p, (bytes)))) { eb.release(); return r; }
-    EB_ALLOC(tgt, (size_t)nseq * (K + 1) * V * 4);
-    EB_ALLOC(drf, (size_t)nseq * K * V * 4);
-    EB_ALLOC(anchor, (size_t)nseq * H * 4);
-    EB_ALLOC(vhid, (size_t)nseq * K * H * 4);
-    EB_ALLOC(props, (size_t)nseq * K * 4);
-    EB_ALLOC(acc_len, nseq * 4);
-    EB_ALLOC(acc_tok, nseq * 4);
-    EB_ALLOC(acc_draws, nseq * 4);
-    EB_ALLOC(acc_status, nseq * 4);
-    EB_ALLOC(nprop, nseq * 4);
-    EB_ALLOC(acc_flags, nseq * 4);
-    EB_ALLOC(seeds, nseq * 8);
-    EB_ALLOC(offs, nseq * 8);
-    EB_ALLOC(src, (size_t)4 * nseq * sizeof(void*));
-    EB_ALLOC(dst, (size_t)4 * nseq * sizeof(void*));
-#undef EB_ALLOC
-    auto done_err = [&](int code) {
-        eb.release();
-        return code;
-    };
-    std::vector<uint64_t> hseeds(nseq), hoffs(nseq, 0);
-    for (int b = 0; b < nseq; b++) hseeds[b] = seeds ? seeds[b] : 0;
-    if (hipMemcpy(eb.seeds, hseeds.data(), nseq * 8, hipMemcpyHostToDevice) != hipSuccess)
-        return done_err(fail(c, AARH_ERR_DEVICE, "seed upload failed"));
-
-    // ---- prefill (chunked so that rows stay within max_rows) ----
-    std::vector<int32_t> slots(nseq), offs(nseq), base(nseq);
-    for (int b = 0; b < nseq; b++) {
-        slots[b] = b;
-        c->kv_len[b] = 0;
-    }
-    {
-        const int chunk = std::max(1, c->Mmax / nseq);
-        std::vector<uint32_t> ids;
-        for (int p0 = 0; p0 < prompt_len; p0 += chunk) {
-            const int S = std::min(chunk, prompt_len - p0);
-            ids.resize((size_t)nseq * S);
-            for (int b = 0; b < nseq; b++) {
-                offs[b] = p0;
-                for (int s2 = 0; s2 < S; s2++) ids[(size_t)b * S + s2] = prompts[(size_t)b * prompt_len + p0 + s2];
-            }
-            int mk = 0;
-            if ((r = stage_rows(c, ids.data(), slots.data(), offs.data(), nseq, S, &mk))) return done_err(r);
-            const bool last = p0 + S == prompt_len;
-            // logits/hidden of the last prompt row -> target_next (tgt row 0) and anchor
-            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, S, mk, c->logits, rm(nseq * S, 0, V),
-                                 c->hidden)))
-                return done_err(r);
-            for (int b = 0; b < nseq; b++) c->kv_len[b] = p0 + S;
-            if (last) {
-                std::vector<const float*> hs(2 * nseq);
-                std::vector<float*> hd(2 * nseq);
-                for (int b = 0; b < nseq; b++) {
-                    hs[b] = c->logits + ((size_t)b * S + S - 1) * V;
-                    hd[b] = eb.tgt + (size_t)b * (K + 1) * V;
-                    hs[nseq + b] = c->hidden + ((size_t)b * S + S - 1) * H;
-                    hd[nseq + b] = eb.anchor + (size_t)b * H;
-                }
-                if (hipMemcpyAsync(eb.src, hs.data(), 2 * nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
-                    hipMemcpyAsync(eb.dst, hd.data(), 2 * nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream))
-                    return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
-                if ((r = launch_copy_rows(eb.src, eb.dst, nseq, V, c->stream)) ||
-                    (r = launch_copy_rows(eb.src + nseq, eb.dst + nseq, nseq, H, c->stream)))
-                    return done_err(fail(c, r, "row copy failed"));
-                if ((r = sync_stream(c))) return done_err(r);
-            }
-        }
-    }
-
-    std::vector<char> finished(nseq, 0);
-    std::vector<uint32_t> hprops((size_t)nseq * K);
-    std::vector<int32_t> hlen(nseq), htok(nseq), hdraws(nseq), hstatus(nseq), hnp(nseq), count(nseq);
-    std::vector<int32_t> zero_pos(nseq, 0);
-    aarh_sampler samp = *s;
-
-    while (true) {
-        bool any = false;
-        for (int b = 0; b < nseq; b++)
-            if (!finished[b] && out_len[b] < max_new) any = true;
-            else finished[b] = 1;
-        if (!any) break;
-        int Kr = 1;
+    // ---- prefill of the uncached prompt tail, chunked so rows stay within max_rows ----
+    const int chunk = std::max(1, c->Mmax / nseq);
+    std::vector<uint32_t> ids;
+    std::vector<int32_t> offs(nseq);
+    for (int b = 0; b < nseq; b++) c->kv_len[b] = cached_len;
+    for (int p0 = 0; p0 < prompt_len; p0 += chunk) {
+        const int S = std::min(chunk, prompt_len - p0);
+        ids.resize((size_t)nseq * S);
         for (int b = 0; b < nseq; b++) {
-            base[b] = c->kv_len[b];
-            count[b] = finished[b] ? 1 : std::min(K, max_new - out_len[b]);
-            Kr = std::max(Kr, count[b]);
+            offs[b] = cached_len + p0;
+            for (int s2 = 0; s2 < S; s2++) ids[(size_t)b * S + s2] = prompts[(size_t)b * prompt_len + p0 + s2];
         }
-        // ---- proposals: index 0 from target_next, index p from MTP head p-1 ----
-        // draft row 0 = target_next
-        {
-            std::vector<const float*> hs(nseq);
-            std::vector<float*> hd(nseq);
+        int mk = 0;
+        if ((r = stage_rows(c, ids.data(), e->slots.data(), offs.data(), nseq, S, &mk)) ||
+            (r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, S, mk, c->logits, rm(nseq * S, 0, V), c->hidden))) {
+            delete e;
+            return r;
+        }
+        for (int b = 0; b < nseq; b++) c->kv_len[b] = cached_len + p0 + S;
+        if (p0 + S == prompt_len) {
+            std::vector<const float*> ls(nseq), hsrc(nseq);
+            std::vector<float*> ld(nseq), hd(nseq);
             for (int b = 0; b < nseq; b++) {
-                hs[b] = eb.tgt + (size_t)b * (K + 1) * V;
-                hd[b] = eb.drf + (size_t)b * K * V;
+                ls[b] = c->logits + ((size_t)b * S + S - 1) * V;
+                ld[b] = e->tgt + (size_t)b * (K + 1) * V;
+                hsrc[b] = c->hidden + ((size_t)b * S + S - 1) * H;
+                hd[b] = e->anchor + (size_t)b * H;
             }
-            if (hipMemcpyAsync(eb.src, hs.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
-                hipMemcpyAsync(eb.dst, hd.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream))
-                return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
-            if ((r = launch_copy_rows(eb.src, eb.dst, nseq, V, c->stream))) return done_err(fail(c, r, "row copy failed"));
-        }
-        for (int p = 0; p < Kr; p++) {
-            if (p > 0) {
-                if ((r = mtp_head_dev(c, p - 1, eb.anchor, H, eb.props, K, nseq, eb.drf + (size_t)p * V, (long long)K * V)))
-                    return done_err(r);
-                for (int b = 0; b < nseq; b++)
-                    if (!finished[b] && count[b] > p) stats[b].mtp_head_forwards++;
-            }
-            // sample proposal p from draft row p
-            if (greedy) {
-                if ((r = launch_argmax_rows(eb.drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)eb.props + p, K,
-                                            nullptr, c->stream)))
-                    return done_err(fail(c, r, "argmax failed"));
-            } else {
-                std::vector<uint64_t> o(nseq);
-                for (int b = 0; b < nseq; b++) o[b] = hoffs[b] + p;
-                if (hipMemcpyAsync(eb.offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream) != hipSuccess)
-                    return done_err(fail(c, AARH_ERR_DEVICE, "offset upload failed"));
-                if ((r = aarh_accept_sample(c, eb.drf + (size_t)p * V, K, nullptr, nullptr, nullptr, nseq, 0, V, 1, &samp,
-                                            eb.seeds, eb.offs, nullptr, eb.acc_len, eb.acc_tok, eb.acc_flags,
-                                            eb.acc_draws, eb.acc_status, nullptr)))
-                    return done_err(r);
-                // sampled tokens come back per sequence; scatter them into the [nseq][K] proposal table
-                if ((r = sync_stream(c))) return done_err(r);
-                std::vector<int32_t> t(nseq);
-                if (hipMemcpy(t.data(), eb.acc_tok, nseq * 4, hipMemcpyDeviceToHost) != hipSuccess)
-                    return done_err(fail(c, AARH_ERR_DEVICE, "proposal download failed"));
-                for (int b = 0; b < nseq; b++) hprops[(size_t)b * K + p] = (uint32_t)t[b];
-                if (hipMemcpy(eb.props, hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice) != hipSuccess)
-                    return done_err(fail(c, AARH_ERR_DEVICE, "proposal upload failed"));
+            if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hsrc, hd, H))) {
+                delete e;
+                return r;
             }
         }
-        if ((r = sync_stream(c))) return done_err(r);
-        if (hipMemcpy(hprops.data(), eb.props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost) != hipSuccess)
-            return done_err(fail(c, AARH_ERR_DEVICE, "proposal download failed"));
-        for (int b = 0; b < nseq; b++) {
-            int np = 0;
-            if (!finished[b]) {
-                for (int p = 0; p < count[b]; p++) {
-                    np++;
-                    stats[b].draft_tokens_proposed++;
-                    if (hprops[(size_t)b * K + p] == EOS_ID) break;
-                }
-            }
-            hnp[b] = np;
-            if (!greedy) hoffs[b] += np;
-        }
-        // ---- verify forward (finished sequences run at a dummy position 0) ----
-        {
-            std::vector<uint32_t> ids((size_t)nseq * Kr);
-            std::vector<int32_t> off(nseq);
-            for (int b = 0; b < nseq; b++) {
-                for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = hprops[(size_t)b * K + std::min(s2, K - 1)];
-                off[b] = finished[b] ? 0 : base[b];
-                if (finished[b]) c->kv_len[b] = 0;
-            }
-            int mk = 0;
-            if ((r = stage_rows(c, ids.data(), slots.data(), off.data(), nseq, Kr, &mk))) return done_err(r);
-            // logits rows -> tgt rows 1..Kr, hidden rows -> vhid
-            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, eb.tgt + V, rm(Kr, (long long)(K + 1) * V, V),
-                                 eb.vhid)))
-                return done_err(r);
-            for (int b = 0; b < nseq; b++) {
-                if (finished[b]) continue;
-                stats[b].rounds++;
-                stats[b].target_decode_forwards++;
-            }
-        }
-        // ---- acceptance (MTP round: no bonus) ----
-        {
-            std::vector<uint64_t> o(nseq);
-            for (int b = 0; b < nseq; b++) o[b] = hoffs[b];
-            if (hipMemcpyAsync(eb.offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-                hipMemcpyAsync(eb.nprop, hnp.data(), nseq * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
-                return done_err(fail(c, AARH_ERR_DEVICE, "upload failed"));
-            if ((r = aarh_accept_sample(c, eb.tgt, K + 1, eb.drf, eb.props, eb.nprop, nseq, K, V, 0, &samp, eb.seeds, eb.offs,
-                                        nullptr, eb.acc_len, eb.acc_tok, eb.acc_flags, eb.acc_draws, eb.acc_status, nullptr)))
-                return done_err(r);
-            if ((r = sync_stream(c))) return done_err(r);
-            if (hipMemcpy(hlen.data(), eb.acc_len, nseq * 4, hipMemcpyDeviceToHost) ||
-                hipMemcpy(htok.data(), eb.acc_tok, nseq * 4, hipMemcpyDeviceToHost) ||
-                hipMemcpy(hdraws.data(), eb.acc_draws, nseq * 4, hipMemcpyDeviceToHost) ||
-                hipMemcpy(hstatus.data(), eb.acc_status, nseq * 4, hipMemcpyDeviceToHost))
-                return done_err(fail(c, AARH_ERR_DEVICE, "acceptance download failed"));
-        }
-        // ---- commit, rollback, replay ----
-        std::vector<int> replay_seq, replay_len;
-        std::vector<const float*> cs;
-        std::vector<float*> cd;
-        std::vector<const float*> hsrc;
-        std::vector<float*> hdst;
-        for (int b = 0; b < nseq; b++) {
-            if (finished[b]) continue;
-            if (hstatus[b] != 0)
-                return done_err(fail(c, AARH_ERR_CONFIG, "speculative residual distribution has zero probability mass"));
-            if (!greedy) hoffs[b] += hdraws[b];
-            const int np = hnp[b], acc = hlen[b];
-            bool done = false;
-            for (int i = 0; i < acc && !done; i++) {
-                stats[b].draft_tokens_accepted++;
-                const uint32_t t = hprops[(size_t)b * K + i];
-                if (t == EOS_ID) {
-                    finish_reason[b] = AARH_FINISH_EOS;
-                    done = true;
-                    break;
-                }
-                out_tokens[(size_t)b * max_new_tokens + out_len[b]++] = t;
-                if (out_len[b] == max_new) done = true;
-            }
-            if (done) {
-                finished[b] = 1;
-                c->kv_len[b] = base[b] + np;
-                continue;
-            }
-            if (acc < np) {
-                const uint32_t repl = (uint32_t)htok[b];
-                c->kv_len[b] = base[b];  // target_cache.restore(snapshot)
-                if (repl == EOS_ID) {
-                    finish_reason[b] = AARH_FINISH_EOS;
-                    finished[b] = 1;
-                    continue;
-                }
-                out_tokens[(size_t)b * max_new_tokens + out_len[b]++] = repl;
-                hprops[(size_t)b * K + acc] = repl;  // replay ids = proposals[..i] + replacement
-                replay_seq.push_back(b);
-                replay_len.push_back(acc + 1);
-            } else {
-                // everything accepted: target_next / anchor from the last verify row
-                c->kv_len[b] = base[b] + np;
-                cs.push_back(eb.tgt + ((size_t)b * (K + 1) + np) * V);
-                cd.push_back(eb.tgt + (size_t)b * (K + 1) * V);
-                hsrc.push_back(eb.vhid + ((size_t)b * Kr + np - 1) * H);
-                hdst.push_back(eb.anchor + (size_t)b * H);
-            }
-        }
-        if (!replay_seq.empty()) {
-            const int nr = (int)replay_seq.size();
-            int Sr = 0;
-            for (int L : replay_len) Sr = std::max(Sr, L);
-            std::vector<uint32_t> ids((size_t)nr * Sr);
-            std::vector<int32_t> sl(nr), off(nr);
-            for (int j = 0; j < nr; j++) {
-                const int b = replay_seq[j];
-                sl[j] = b;
-                off[j] = base[b];
-                for (int s2 = 0; s2 < Sr; s2++)
-                    ids[(size_t)j * Sr + s2] = hprops[(size_t)b * K + std::min(s2, replay_len[j] - 1)];
-            }
-            int mk = 0;
-            if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk))) return done_err(r);
-            if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, Sr, mk, c->logits, rm(nr * Sr, 0, V), c->hidden)))
-                return done_err(r);
-            for (int j = 0; j < nr; j++) {
-                const int b = replay_seq[j];
-                stats[b].target_decode_forwards++;
-                c->kv_len[b] = base[b] + replay_len[j];
-                cs.push_back(c->logits + ((size_t)j * Sr + replay_len[j] - 1) * V);
-                cd.push_back(eb.tgt + (size_t)b * (K + 1) * V);
-                hsrc.push_back(c->hidden + ((size_t)j * Sr + replay_len[j] - 1) * H);
-                hdst.push_back(eb.anchor + (size_t)b * H);
-            }
-        }
-        if (!cs.empty()) {
-            const int n = (int)cs.size();
-            std::vector<const float*> allsrc(cs);
-            allsrc.insert(allsrc.end(), hsrc.begin(), hsrc.end());
-            std::vector<float*> alldst(cd);
-            alldst.insert(alldst.end(), hdst.begin(), hdst.end());
-            if (hipMemcpyAsync(eb.src, allsrc.data(), 2 * n * sizeof(void*), hipMemcpyHostToDevice, c->stream) ||
-                hipMemcpyAsync(eb.dst, alldst.data(), 2 * n * sizeof(void*), hipMemcpyHostToDevice, c->stream))
-                return done_err(fail(c, AARH_ERR_DEVICE, "pointer upload failed"));
-            if ((r = launch_copy_rows(eb.src, eb.dst, n, V, c->stream)) ||
-                (r = launch_copy_rows(eb.src + n, eb.dst + n, n, H, c->stream)))
-                return done_err(fail(c, r, "row copy failed"));
-            if ((r = sync_stream(c))) return done_err(r);
-        }
-        for (int b = 0; b < nseq; b++)
-            if (!finished[b] && out_len[b] >= max_new) finished[b] = 1;
     }
-    for (int b = 0; b < nseq; b++) {
-        if (out_len[b] == available && finish_reason[b] == AARH_FINISH_MAX_TOKENS)
-            finish_reason[b] = AARH_FINISH_CONTEXT_LIMIT;
-        stats[b].draft_tokens_rejected = std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
-    }
-    eb.release();
+    *out = e;
     return 0;
 }
+
+int aarh_session_step(aarh_session* e, int max_rounds, int32_t* all_done) {
+    if (!e) return AARH_ERR_CONFIG;
+    for (int i = 0; i < max_rounds; i++) {
+        bool any = false;
+        for (int b = 0; b < e->nseq; b++)
+            if (!e->finished[b]) any = true;
+        if (!any) break;
+        int r = session_round(e);
+        if (r) return r;
+    }
+    if (all_done) {
+        *all_done = 1;
+        for (int b = 0; b < e->nseq; b++)
+            if (!e->finished[b]) *all_done = 0;
+    }
+    return 0;
+}
+
+int aarh_session_result(aarh_session* e, uint32_t* out_tokens, int32_t out_cap, int32_t* out_len, int32_t* finish_reason,
+                        aarh_spec_stats* stats) {
+    if (!e) return AARH_ERR_CONFIG;
+    for (int b = 0; b < e->nseq; b++) {
+        const int n = (int)e->out[b].size();
+        if (out_len) out_len[b] = n;
+        if (out_tokens)
+            for (int i = 0; i < n && i < out_cap; i++) out_tokens[(size_t)b * out_cap + i] = e->out[b][i];
+        int fin = e->finish[b];
+        if (n == e->available && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
+        if (finish_reason) finish_reason[b] = fin;
+        if (stats) {
+            stats[b] = e->stats[b];
+            stats[b].draft_tokens_rejected =
+                std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
+        }
+    }
+    return 0;
+}
+
+void aarh_session_end(aarh_session* e) { delete e; }
+
+int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
+                      int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds, uint32_t* out_tokens,
+                      int32_t* out_len, int32_t* finish_reason, aarh_spec_stats* stats) {
+    if (!c) return AARH_ERR_CONFIG;
+    for (int b = 0; b < nseq && b < c->cfg.max_batch; b++) c->kv_len[b] = 0;
+    aarh_session* e = nullptr;
+    int r = aarh_session_begin(c, prompts, nseq, prompt_len, 0, max_new_tokens, num_draft_tokens, s, seeds, &e);
+    if (r) return r;
+    int32_t done = 0;
+    r = aarh_session_step(e, 1 << 30, &done);
+    if (!r) r = aarh_session_result(e, out_tokens, max_new_tokens, out_len, finish_reason, stats);
+    aarh_session_end(e);
+    return r;
+}
+
+}  // extern "C"

@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X speculative verify path (BASELINE.json metric).
+
+Workload: random-init decoder, 32 layers, d_model 4096,
+32 query / 8 KV heads (head_dim 128), SwiGLU ffn 11008, vocab 32000; INT4 g128
+weights (fp16 scale/zero) drawn N(0, 0.02^2) before quantisation, bf16 tied LM
+head, 3 MTP heads (num_future_tokens 4, k = 3 drafts + 1 -> K = 4 verify rows),
+INT8 KV cache holding a 4096-token synthetic context per sequence.
+
+A "step" is one speculative round of the MTP engine (mtp_speculative.rs:161-322)
+for every sequence of the batch: 3 MTP-head forwards, one K=4-row verify
+forward over the 4096-token cache, fused acceptance, replay on rejection.
+`value` = committed tokens / wall time of the timed rounds at batch 32 (inputs
+and KV resident in HBM); batch 1 is reported beside it.  The verify-step loop
+(K = 4 rows at offset 4096, repeated) is timed separately with per-kernel HIP
+events; its INT4 GEMV kernel gives `roofline`.  `cpu_baseline` times the CPU
+oracle (restated reference CPU path, f32) on a 2-layer slice of the same model
+and extrapolates to a full round.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "aarambh-ai_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "accepted tokens/s at batch 1 & 32 (INT4, k=3); verify-step HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+C4 = dict(vocab_size=32000, hidden_dim=4096, ffn_dim=11008, n_layers=32, n_heads=32, n_kv_heads=8,
+          max_seq_len=4096 + 512, num_future_tokens=4)
+CTX = 4096
+K_ROWS = 4  # k = 3 MTP drafts + the target-sampled proposal
+
+
+def int4_matrix_bytes(n, k):
+    return n * k // 2 + n * (k // 128) * 4  # codes + fp16 scale + fp16 zero per 128-group
+
+
+def verify_alg_bytes(B, ctx=CTX):
+    """Algorithmic HBM bytes of one K-row verify step at batch B."""
+    H, F, V, L = C4["hidden_dim"], C4["ffn_dim"], C4["vocab_size"], C4["n_layers"]
+    hd = H // C4["n_heads"]
+    QD, KD = C4["n_heads"] * hd, C4["n_kv_heads"] * hd
+    per_layer = int4_matrix_bytes(QD + 2 * KD, H) + int4_matrix_bytes(H, QD) + int4_matrix_bytes(2 * F, H) + \
+        int4_matrix_bytes(H, F)
+    weights = L * per_layer + V * H * 2
+    kv = B * L * 2 * C4["n_kv_heads"] * ctx * (hd + 2)  # INT8 codes + fp16 per-token scale
+    return weights, kv
+
+
+def gemm_flops(M):
+    H, F, V, L = C4["hidden_dim"], C4["ffn_dim"], C4["vocab_size"], C4["n_layers"]
+    hd = H // C4["n_heads"]
+    QD, KD = C4["n_heads"] * hd, C4["n_kv_heads"] * hd
+    per_layer = (QD + 2 * KD) * H + H * QD + 2 * F * H + H * F
+    return 2.0 * M * (L * per_layer)
+
+
+def run_gpu(args):
+    import aarambh_hip as A
+
+    cfg = A.ModelConfig(**C4, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    bmax = max(args.batches)
+    t0 = time.time()
+    m = A.HipModel(cfg, max_batch=bmax, max_rows=128)
+    m.init_synthetic(seed=0, std=0.02)
+    print(f"# model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    eng = A.MtpSpeculativeEngine(m, A.SpeculativeConfig(K_ROWS))
+    rng = np.random.default_rng(0)
+    res = {}
+    for B in args.batches:
+        for b in range(B):
+            m.kv_fill_synthetic(b, CTX, seed=1 + b)
+        # ---- verify step: K rows at offset CTX (rewinds each time), per-kernel events ----
+        ids = rng.integers(1, C4["vocab_size"], (B, K_ROWS)).astype(np.uint32)
+        for _ in range(3):
+            m.forward_with_cache_output(ids, [CTX] * B, want_logits=False, want_hidden=False)
+        m.prof_enable(True)
+        n_verify = args.verify_iters
+        tv = time.perf_counter()
+        for _ in range(n_verify):
+            m.forward_with_cache_output(ids, [CTX] * B, want_logits=False, want_hidden=False)
+        m.sync()
+        tv = (time.perf_counter() - tv) / n_verify
+        prof = m.prof_get()
+        m.prof_enable(False)
+        wbytes, kvbytes = verify_alg_bytes(B)
+        gpu_ms = sum(v["ms"] for v in prof.values()) / n_verify
+        # ---- engine rounds ----
+        prompts = rng.integers(1, C4["vocab_size"], (B, 1)).astype(np.uint32)
+        max_new = K_ROWS * (args.warmup + args.steps + 2) + 8
+        sess = eng.session(prompts, max_new, A.Sampler.greedy_sampler(), cached_len=CTX)
+        sess.step(args.warmup)
+        before = sess.result()
+        tok0 = sum(len(r.token_ids) for r in before)
+        m.sync()
+        ts = time.perf_counter()
+        sess.step(args.steps)
+        m.sync()
+        ts = time.perf_counter() - ts
+        after = sess.result()
+        tok1 = sum(len(r.token_ids) for r in after)
+        st = after[0].speculative_stats
+        stats_all = [r.speculative_stats for r in after]
+        sess.close()
+        rounds = sum(s.rounds for s in stats_all)
+        res[B] = {
+            "tokens_per_s": (tok1 - tok0) / ts,
+            "ms_per_step": ts * 1000.0 / args.steps,
+            "tokens_timed": tok1 - tok0,
+            "acceptance_rate": float(np.mean([s.acceptance_rate() for s in stats_all])),
+            "tokens_per_round": tok1 / max(1, rounds / B),
+            "target_forwards_per_round": sum(s.target_decode_forwards for s in stats_all) / max(1, rounds),
+            "mtp_forwards_per_round": sum(s.mtp_head_forwards for s in stats_all) / max(1, rounds),
+            "verify": {
+                "ms_wall": tv * 1000.0,
+                "ms_kernels": gpu_ms,
+                "alg_bytes": wbytes + kvbytes,
+                "hbm_gbs": (wbytes + kvbytes) / tv / 1e9,
+                "hbm_frac": (wbytes + kvbytes) / tv / 1e9 / HBM_PEAK_GBS,
+                "gemm_tflops": gemm_flops(B * K_ROWS) / tv / 1e12,
+                "kernels": {k: {"ms_per_step": v["ms"] / n_verify, "launches_per_step": v["launches"] / n_verify,
+                                "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] > 0 else 0.0}
+                            for k, v in prof.items() if v["launches"]},
+            },
+            "stats_seq0": st.__dict__,
+        }
+        int4 = [prof[k] for k in ("gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down")]
+        ms = sum(v["ms"] for v in int4)
+        by = sum(v["bytes"] for v in int4)
+        n = sum(v["launches"] for v in int4)
+        res[B]["int4_gemv"] = {"ms_total": ms, "alg_bytes": by, "launches": n,
+                               "avg_us": ms * 1000.0 / max(n, 1), "avg_bytes": by / max(n, 1),
+                               "gbs": by / (ms * 1e-3) / 1e9 if ms else 0.0,
+                               "tflops": gemm_flops(B * K_ROWS) * (1 - 0) / 1e12 / (ms * 1e-3 / n_verify)
+                               if ms else 0.0}
+        print(f"# B={B}: {res[B]['tokens_per_s']:.1f} tok/s, round {res[B]['ms_per_step']:.3f} ms, verify "
+              f"{tv * 1000:.3f} ms ({res[B]['verify']['hbm_gbs']:.0f} GB/s), int4 gemv {res[B]['int4_gemv']['gbs']:.0f}"
+              f" GB/s", file=sys.stderr, flush=True)
+    m.close()
+    return res
+
+
+def cpu_baseline(res_b1, threads):
+    """Oracle (restated reference CPU path, f32 compute) on a 2-layer slice of C4."""
+    import refcpu as R
+
+    cfg = R.make_config(vocab_size=C4["vocab_size"], hidden_dim=C4["hidden_dim"], ffn_dim=C4["ffn_dim"],
+                        n_layers=2, n_heads=C4["n_heads"], n_kv_heads=C4["n_kv_heads"],
+                        max_seq_len=CTX + 16, num_future_tokens=2, weight_format=R.W_INT4_G128,
+                        lm_head_format=1, kv_format=R.KV_INT8)
+    t0 = time.time()
+    model = R.Model(cfg, seed=0, std=0.02)
+    kv = model.kv(CTX + 16)
+    kv.fill_synthetic(1, CTX)
+    setup = time.time() - t0
+    ids = np.arange(1, K_ROWS + 1, dtype=np.uint32)
+
+    def timed(fn, reps):
+        fn()
+        t = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t) / reps
+
+    t1 = timed(lambda: kv.forward_layers(ids, CTX, 1, True, threads), 2)
+    t2 = timed(lambda: kv.forward_layers(ids, CTX, 2, True, threads), 2)
+    per_layer = max(t2 - t1, 1e-9)
+    head = max(t1 - per_layer, 0.0)
+    anchor = np.random.default_rng(0).normal(0, 1, C4["hidden_dim"]).astype(np.float32)
+    t_mtp = timed(lambda: model.mtp_head(0, anchor, np.array([5], np.uint32), threads), 2)
+    t_verify = C4["n_layers"] * per_layer + head
+    tf = res_b1["target_forwards_per_round"]
+    mf = res_b1["mtp_forwards_per_round"]
+    t_round = tf * t_verify + mf * t_mtp
+    tok_round = res_b1["tokens_per_round"]
+    return {
+        "value": tok_round / t_round,
+        "unit": "accepted tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle (C restatement of the reference f32 CPU path: sequential online-softmax "
+                   f"attention, f32 GEMV) on a 2-layer slice of config 4 (INT4-dequantised f32 weights), "
+                   f"K=4 verify rows over a {CTX}-token cache: per-layer {per_layer * 1e3:.1f} ms, head "
+                   f"{head * 1e3:.1f} ms, MTP head {t_mtp * 1e3:.1f} ms; extrapolated to 32 layers and the GPU "
+                   f"run's {tf:.2f} target + {mf:.2f} MTP forwards and {tok_round:.2f} tokens per round at "
+                   f"batch 1; setup {setup:.0f}s untimed"),
+        "verify_ms": t_verify * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=12)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batches", type=str, default="1,32")
+    ap.add_argument("--verify-iters", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one MI355X; the verify path shards by independent "
+              "sequences (see DESIGN.md) and no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+    args.batches = [int(x) for x in args.batches.split(",")]
+    res = run_gpu(args)
+    bmain = max(args.batches)
+    main_r = res[bmain]
+    b1 = res.get(1, main_r)
+    g1 = b1["int4_gemv"]
+    roof = {
+        "kernel": "gemv_mfma_kernel<INT4,1> (all INT4 projections of the batch-1 verify step)",
+        "bound": "hbm",
+        "achieved": round(g1["gbs"], 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(g1["gbs"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "avg_launch_us": round(g1["avg_us"], 3),
+        "avg_alg_bytes_per_launch": round(g1["avg_bytes"]),
+    }
+    cpu = None
+    if not args.no_cpu and 1 in res:
+        threads = min(16, os.cpu_count() or 1)
+        try:
+            cpu = cpu_baseline(res[1], threads)
+        except Exception as exc:  # the CPU leg must not hide the GPU result
+            cpu = {"error": str(exc)}
+    line = {
+        "metric": METRIC,
+        "value": round(main_r["tokens_per_s"], 2),
+        "unit": "accepted tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4-weight x fp16(hi+lo)-activation, f32 accumulate",
+        "data": "synthetic (random-init weights N(0,0.02^2), synthetic 4096-token INT8 KV, greedy MTP)",
+        "config": {"workload": f"C4 INT4 g128 MTP k=3 verify rounds, batch {bmain} (batch 1 beside), "
+                               f"4096-token INT8 KV",
+                   "batch": bmain, "verify_rows_per_seq": K_ROWS, "context": CTX},
+        "batch1": {k: b1[k] for k in ("tokens_per_s", "ms_per_step", "acceptance_rate", "tokens_per_round")}
+        if 1 in res else None,
+        "verify_step": {str(b): {k: r["verify"][k] for k in ("ms_wall", "ms_kernels", "alg_bytes", "hbm_gbs",
+                                                               "hbm_frac", "gemm_tflops")} for b, r in res.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "detail": {str(b): r for b, r in res.items()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

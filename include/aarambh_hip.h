@@ -139,6 +139,20 @@ int aarh_mtp_generate(aarh_ctx *ctx, const uint32_t *prompts, int nseq, int prom
                       const uint64_t *seeds, uint32_t *out_tokens, int32_t *out_len,
                       int32_t *finish_reason, aarh_spec_stats *stats);
 
+/* The same engine as a session, one call per batch of rounds (serving / benchmarking).
+   begin: prefills prompts [nseq][prompt_len] on top of `cached_len` tokens already held by
+   each slot's KV cache (0 = fresh request; the context limit counts cached + prompt tokens).
+   step: runs up to max_rounds speculative rounds (mtp_speculative.rs:161-322).
+   result: committed tokens [nseq][out_cap], lengths, finish reasons, SpeculativeStats. */
+typedef struct aarh_session aarh_session;
+int aarh_session_begin(aarh_ctx *ctx, const uint32_t *prompts, int nseq, int prompt_len, int cached_len,
+                       int max_new_tokens, int num_draft_tokens, const aarh_sampler *sampler,
+                       const uint64_t *seeds, aarh_session **out);
+int aarh_session_step(aarh_session *session, int max_rounds, int32_t *all_done);
+int aarh_session_result(aarh_session *session, uint32_t *out_tokens, int32_t out_cap, int32_t *out_len,
+                        int32_t *finish_reason, aarh_spec_stats *stats);
+void aarh_session_end(aarh_session *session);
+
 /* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
        AARH_PROF_GEMV_DOWN = 3, AARH_PROF_GEMV_LMHEAD = 4, AARH_PROF_ATTENTION = 5,

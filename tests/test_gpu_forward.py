@@ -130,3 +130,26 @@ def test_shape_errors_are_reported():
     with pytest.raises(A.ShapeError):
         hip.restore(3)  # cannot grow by rollback
     hip.close()
+
+
+@pytest.mark.parametrize("kvfmt", [A.KV_INT8, A.KV_F16])
+def test_long_context_verify_over_synthetic_cache(kvfmt):
+    """Verify K=4 rows over 700- and 300-token caches (many attention chunks,
+    ragged offsets); the cache contents come from the shared synthetic formula."""
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=2, n_heads=8, n_kv_heads=2, max_seq_len=800,
+              weight_format=A.W_INT4_G128, kv_format=kvfmt, lm_head_format=1)
+    ref, hip = make_pair(seed=8, max_batch=2, max_rows=64, **kw)
+    lens = [700, 300]
+    kvs = []
+    for b, L in enumerate(lens):
+        hip.kv_fill_synthetic(b, L, seed=11 + b)
+        kv = ref.kv(800)
+        kv.fill_synthetic(11 + b, L)
+        kvs.append(kv)
+    ids = R.synth_tokens(8, 2, 8, 2048).reshape(2, 4)
+    gl, gh = hip.forward_with_cache_output(ids, lens)
+    for b in range(2):
+        wl, wh = kvs[b].forward(ids[b], lens[b])
+        assert rel_rows(gl[b], wl).max() < TOL, (b, rel_rows(gl[b], wl).max())
+        assert rel_rows(gh[b], wh).max() < TOL
+    hip.close()
