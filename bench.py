@@ -148,6 +148,21 @@ def run_gpu(args):
     return res
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_int4_verify_c4_b1_pmc.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the INT4 GEMV from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE runs of this script, scaled by a plain-copy calibration)."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(res_b1, threads):
     """Oracle (restated reference CPU path, f32 compute) on a 2-layer slice of C4."""
     import refcpu as R
@@ -204,7 +219,19 @@ def main():
     ap.add_argument("--batches", type=str, default="1,32")
     ap.add_argument("--verify-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device copy (counter calibration for rocprof --pmc)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
+                          "launches": 5}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X; the verify path shards by independent "
               "sequences (see DESIGN.md) and no multi-GPU figure is produced.", file=sys.stderr)
@@ -222,7 +249,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(g1["gbs"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(),
         "avg_launch_us": round(g1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(g1["avg_bytes"]),
     }
