@@ -219,21 +219,118 @@ __device__ __forceinline__ void lds_wave_sync() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-static constexpr int AM_RT = 2;     // row tiles of 8 real query rows
-static constexpr int AM_ROWS = 16;  // real query rows per workgroup
+static constexpr int AM_ROWS = 16;          // query rows per workgroup (one MFMA column tile)
 static constexpr int AM_HD = 128;
+static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
+static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
+static constexpr int AM_MAXCH = 64;         // chunks one merge combines
+static constexpr float AM_LOG2E = 1.4426950408889634f;
+
+// Raw K/V operands of one 32-token block for one lane (lane = (lr, lg)).
+// K: token rows 8*(lr/4) + 4*ts + lr%4 of the block, dims 32*lg..+32.
+// V^T: dim rows 16*dt + lr, tokens 8*lg..+8.  Scales: tokens 8*lg..+8.
+template <int KVF>
+struct KvRaw;
+template <>
+struct KvRaw<KV_INT8> {
+    uint4 k[2][2];
+    uint2 v[8];
+    uint4 ksc, vsc;
+};
+template <>
+struct KvRaw<KV_F16> {
+    uint4 k[2][4];
+    uint4 v[8];
+};
 
 template <int KVF>
-__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
-    __shared__ __align__(16) uint16_t qs[AM_RT][16][AM_HD + 8];
-    __shared__ __align__(16) uint16_t pt[4][AM_RT][16][32 + 8];
-    __shared__ float mg_m[4][AM_ROWS], mg_l[4][AM_ROWS];
-    __shared__ float mg_o[4][AM_ROWS][AM_HD + 4];
+__device__ __forceinline__ void load_kv_block(const AttnArgs& a, size_t hb, int tb, int lr, int lg, KvRaw<KVF>& r) {
+#pragma unroll
+    for (int ts = 0; ts < 2; ts++) {
+        const int tok = tb + 8 * (lr >> 2) + 4 * ts + (lr & 3);
+        if constexpr (KVF == KV_INT8) {
+            const uint4* kr = (const uint4*)((const uint8_t*)a.kc + (hb * a.cap + tok) * AM_HD + 32 * lg);
+            r.k[ts][0] = kr[0];
+            r.k[ts][1] = kr[1];
+        } else {
+            const uint4* kr = (const uint4*)((const _Float16*)a.kc + (hb * a.cap + tok) * AM_HD + 32 * lg);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) r.k[ts][kk] = kr[kk];
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+        if constexpr (KVF == KV_INT8)
+            r.v[dt] = *(const uint2*)((const uint8_t*)a.vc + (hb * AM_HD + 16 * dt + lr) * a.cap + tb + 8 * lg);
+        else
+            r.v[dt] = *(const uint4*)((const _Float16*)a.vc + (hb * AM_HD + 16 * dt + lr) * a.cap + tb + 8 * lg);
+    }
+    if constexpr (KVF == KV_INT8) {
+        r.ksc = *(const uint4*)(a.ks + hb * a.cap + tb + 8 * lg);
+        r.vsc = *(const uint4*)(a.vs + hb * a.cap + tb + 8 * lg);
+    }
+}
+
+template <int KVF>
+__device__ __forceinline__ half8_t k_operand(const KvRaw<KVF>& r, int ts, int kk) {
+    if constexpr (KVF == KV_INT8) {
+        const uint4 w = r.k[ts][kk >> 1];
+        return (kk & 1) ? i8x8_to_half8_perm(w.z, w.w) : i8x8_to_half8_perm(w.x, w.y);
+    } else {
+        return __builtin_bit_cast(half8_t, r.k[ts][kk]);
+    }
+}
+template <int KVF>
+__device__ __forceinline__ half8_t v_operand(const KvRaw<KVF>& r, int dt) {
+    if constexpr (KVF == KV_INT8) return i8x8_to_half8_perm(r.v[dt].x, r.v[dt].y);
+    else return __builtin_bit_cast(half8_t, r.v[dt]);
+}
+// fp16 scale of token 8*lg + idx (idx = 4*ts + i)
+__device__ __forceinline__ float scale_at(uint4 s, int idx) {
+    const uint32_t w = idx < 2 ? s.x : idx < 4 ? s.y : idx < 6 ? s.z : s.w;
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (w >> 16) : (w & 0xFFFFu)));
+}
+
+// k-slot j of an 8-block holds element perm(j): the order i8x8_to_half8_perm emits
+template <int KVF>
+__device__ __forceinline__ constexpr int slot_elem(int j) {
+    if constexpr (KVF == KV_INT8) return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+    else return j;
+}
+
+// reductions over the four 16-lane rows of a wave (lanes lr, lr+16, lr+32, lr+48)
+__device__ __forceinline__ float rows_max(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Flash-decode attention on MFMA for head_dim 128 and fp16 / INT8 caches.
+// Workgroup = (sequence, kv head, tile of <= 16 query rows, token chunk), 8 waves;
+// wave w takes the chunk's 32-token blocks w, w+8, ... with the next block's
+// loads in flight while the current one computes.  Scores are computed
+// transposed, S^T = K Q^T (A = K rows, B = Q^T as fp16 hi and lo halves), so the
+// MFMA result layout (lane = query row, 8 tokens per lane) is directly the B
+// operand of O^T = V^T P^T: no LDS round trip, and the row statistics live in
+// the lane of their row.  Softmax runs in base 2 (v_exp_f32).  With one chunk
+// the workgroup writes the output; otherwise chunk partials go out with
+// coherent 16-byte stores and the last workgroup of the group merges them.
+template <int KVF>
+__global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
+    __shared__ __align__(16) float mg_o[AM_WAVES][AM_ROWS][AM_REC];
+    __shared__ float mg_m[AM_WAVES][AM_ROWS], mg_l[AM_WAVES][AM_ROWS];
     __shared__ unsigned s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int lr = lane & 15, lg = lane >> 4, rb = (lg & 1) * 4;
-    const int hd = AM_HD, G = a.n_heads / a.n_kv;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int G = a.n_heads / a.n_kv;
     const int R_total = a.S * G;
     int bid = blockIdx.x;
     const int chunk = bid % a.nchunks;
@@ -247,227 +344,188 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
     const int pos0 = a.pos0[seq];
     const int kv_len = pos0 + a.S;
     const int sl = a.slot[seq];
-    const int QD = a.n_heads * hd;
+    const int QD = a.n_heads * AM_HD;
     const size_t hb = (size_t)sl * a.n_kv + kvh;
-
-    // ---- stage Q (hi / lo fp16, format-permuted) ----
-    for (int idx = tid; idx < AM_ROWS * hd; idx += 256) {
-        const int rr = idx / hd, d = idx % hd;
-        float v = 0.f;
-        if (rr < R) {
-            const int real = r0 + rr, s = real / G, g = real % G;
-            v = a.q[(size_t)(seq * a.S + s) * QD + (kvh + g * a.n_kv) * hd + d];
-        }
-        const _Float16 hi = (_Float16)v;
-        const _Float16 lo = (_Float16)(v - (float)hi);
-        const int rt = rr >> 3, r8 = rr & 7, sl2 = kv_slot<KVF>(d);
-        qs[rt][r8][sl2] = __builtin_bit_cast(uint16_t, hi);
-        qs[rt][8 + r8][sl2] = __builtin_bit_cast(uint16_t, lo);
-    }
-    __syncthreads();
-    half8_t qa[AM_RT][4];
-#pragma unroll
-    for (int rt = 0; rt < AM_RT; rt++)
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) qa[rt][kk] = *(const half8_t*)&qs[rt][lr][32 * kk + 8 * lg];
-
-    // causal limit of the real rows this lane tracks (rows rb+i of each row tile)
-    int lim[AM_RT][4];
-#pragma unroll
-    for (int rt = 0; rt < AM_RT; rt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int rr = rt * 8 + rb + i;
-            lim[rt][i] = rr < R ? pos0 + (r0 + rr) / G : -1;
-        }
-    float mrow[AM_RT][4], lrow[AM_RT][4];
-    float4_t o[AM_RT][8];
-#pragma unroll
-    for (int rt = 0; rt < AM_RT; rt++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            mrow[rt][i] = -INFINITY;
-            lrow[rt][i] = 0.f;
-        }
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[rt][dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    }
-
     const int t_begin = chunk * a.chunk;
     const int t_end = min(kv_len, t_begin + a.chunk);
-    const float qk_scale = a.scale;
-    for (int tb = t_begin + 32 * wid; tb < t_end; tb += 128) {
-        // ---- S = Q K^T for two 16-token sub-tiles ----
-        float4_t sc[AM_RT][2];
-        float ksc[2], vsc[2];
-        int tokv[2];
+
+    // ---- this lane's query row (lr): Q^T B operand, hi/lo, dims 32*lg + 8*kk + slot ----
+    const bool row_ok = lr < R;
+    int lim = -1;
+    const float* qp = a.q;
+    if (row_ok) {
+        const int real = r0 + lr, s = real / G, g = real % G;
+        lim = pos0 + s;
+        qp = a.q + (size_t)(seq * a.S + s) * QD + (kvh + g * a.n_kv) * AM_HD + 32 * lg;
+    }
+    float4_t qv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) qv[u] = row_ok ? *(const float4_t*)(qp + 4 * u) : (float4_t){0.f, 0.f, 0.f, 0.f};
+
+    int tb = t_begin + 32 * wid;
+    KvRaw<KVF> cur;
+    if (tb < t_end) load_kv_block<KVF>(a, hb, tb, lr, lg, cur);
+
+    half8_t qh[4], ql[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int e = 8 * kk + slot_elem<KVF>(j);
+            const float v = qv[e >> 2][e & 3];
+            const _Float16 hi = (_Float16)v;
+            qh[kk][j] = hi;
+            ql[kk][j] = (_Float16)(v - (float)hi);
+        }
+
+    float m = -INFINITY, l = 0.f;
+    float4_t o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    const float sc2 = a.scale * AM_LOG2E;
+
+    for (; tb < t_end; tb += 32 * AM_WAVES) {
+        KvRaw<KVF> nxt;
+        if (tb + 32 * AM_WAVES < t_end) load_kv_block<KVF>(a, hb, tb + 32 * AM_WAVES, lr, lg, nxt);
+        // ---- S^T = K Q^T: lane holds tokens 8*lg + 4*ts + i of row lr ----
+        float4_t st[2];
 #pragma unroll
         for (int ts = 0; ts < 2; ts++) {
-            const int tok = tb + 16 * ts + lr;
-            tokv[ts] = tok;
-            const int tk = tok < t_end ? tok : t_end - 1;
-            half8_t kb[4];
-            if (KVF == KV_INT8) {
-                const uint8_t* kr = (const uint8_t*)a.kc + (hb * a.cap + tk) * hd + 8 * lg;
+            float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    const uint2 w = *(const uint2*)(kr + 32 * kk);
-                    kb[kk] = i8x8_to_half8_perm(w.x, w.y);
-                }
-                ksc[ts] = (float)__builtin_bit_cast(_Float16, a.ks[hb * a.cap + tk]);
-                vsc[ts] = (float)__builtin_bit_cast(_Float16, a.vs[hb * a.cap + tk]);
-            } else {
-                const _Float16* kr = (const _Float16*)a.kc + (hb * a.cap + tk) * hd + 8 * lg;
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++) kb[kk] = *(const half8_t*)(kr + 32 * kk);
-                ksc[ts] = 1.0f;
-                vsc[ts] = 1.0f;
+            for (int kk = 0; kk < 4; kk++) {
+                const half8_t ka = k_operand<KVF>(cur, ts, kk);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[kk], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[kk], acc, 0, 0, 0);
             }
-#pragma unroll
-            for (int rt = 0; rt < AM_RT; rt++) {
-                float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][kk], kb[kk], acc, 0, 0, 0);
-                sc[rt][ts] = acc;
-            }
+            st[ts] = acc;
         }
-        // ---- online softmax (rows rb+i; hi+lo summed across the lane halves) ----
-        float pv[AM_RT][2][4];
+        float s[8];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int rt = 0; rt < AM_RT; rt++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float s0 = sc[rt][0][i] + __shfl_xor(sc[rt][0][i], 32, 64);
-                float s1 = sc[rt][1][i] + __shfl_xor(sc[rt][1][i], 32, 64);
-                s0 = (tokv[0] < t_end && tokv[0] <= lim[rt][i]) ? s0 * ksc[0] * qk_scale : -INFINITY;
-                s1 = (tokv[1] < t_end && tokv[1] <= lim[rt][i]) ? s1 * ksc[1] * qk_scale : -INFINITY;
-                float mx = fmaxf(s0, s1);
-#pragma unroll
-                for (int d = 1; d < 16; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-                const float mnew = fmaxf(mrow[rt][i], mx);
-                const float alpha = (mrow[rt][i] == -INFINITY) ? (mnew == -INFINITY ? 1.f : 0.f)
-                                                                : expf(mrow[rt][i] - mnew);
-                const float p0 = s0 == -INFINITY ? 0.f : expf(s0 - mnew);
-                const float p1 = s1 == -INFINITY ? 0.f : expf(s1 - mnew);
-                float ps = p0 + p1;
-#pragma unroll
-                for (int d = 1; d < 16; d <<= 1) ps += __shfl_xor(ps, d, 64);
-                lrow[rt][i] = lrow[rt][i] * alpha + ps;
-                mrow[rt][i] = mnew;
-                pv[rt][0][i] = p0 * vsc[0];
-                pv[rt][1][i] = p1 * vsc[1];
-#pragma unroll
-                for (int dt = 0; dt < 8; dt++) o[rt][dt][i] *= alpha;
-            }
+        for (int idx = 0; idx < 8; idx++) {
+            const int tok = tb + 8 * lg + idx;
+            float ksc = sc2;
+            if constexpr (KVF == KV_INT8) ksc *= scale_at(cur.ksc, idx);
+            const float v = st[idx >> 2][idx & 3] * ksc;
+            s[idx] = (tok < t_end && tok <= lim) ? v : -INFINITY;
+            mx = fmaxf(mx, s[idx]);
         }
-        // ---- P -> LDS (hi rows 0-7, lo rows 8-15, token order permuted like V) ----
-        if (lg < 2) {
+        mx = rows_max(mx);
+        const float mnew = fmaxf(m, mx);
+        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+        float p[8], ps = 0.f;
 #pragma unroll
-            for (int rt = 0; rt < AM_RT; rt++)
-#pragma unroll
-                for (int ts = 0; ts < 2; ts++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float p = pv[rt][ts][i];
-                        const _Float16 hi = (_Float16)p;
-                        const _Float16 lo = (_Float16)(p - (float)hi);
-                        const int col = kv_slot<KVF>(16 * ts + lr);
-                        pt[wid][rt][rb + i][col] = __builtin_bit_cast(uint16_t, hi);
-                        pt[wid][rt][8 + rb + i][col] = __builtin_bit_cast(uint16_t, lo);
-                    }
+        for (int idx = 0; idx < 8; idx++) {
+            p[idx] = s[idx] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[idx] - mnew);
+            ps += p[idx];
         }
-        lds_wave_sync();
-        half8_t pa[AM_RT];
+        ps = rows_sum(ps);
+        l = l * alpha + ps;
+        m = mnew;
 #pragma unroll
-        for (int rt = 0; rt < AM_RT; rt++) pa[rt] = *(const half8_t*)&pt[wid][rt][lr][8 * lg];
-        lds_wave_sync();
-        // ---- O += P V ----
-        const int tv = min(tb + 8 * lg, a.cap - 8);
+        for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+        // ---- P^T B operand (hi / lo), slot j <-> token 8*lg + slot_elem(j) ----
+        half8_t ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int idx = slot_elem<KVF>(j);
+            float pv = p[idx];
+            if constexpr (KVF == KV_INT8) pv *= scale_at(cur.vsc, idx);
+            const _Float16 hi = (_Float16)pv;
+            ph[j] = hi;
+            pl[j] = (_Float16)(pv - (float)hi);
+        }
+        // ---- O^T += V^T P^T ----
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            half8_t vb;
-            if (KVF == KV_INT8) {
-                const uint2 w = *(const uint2*)((const uint8_t*)a.vc + (hb * hd + 16 * dt + lr) * a.cap + tv);
-                vb = i8x8_to_half8_perm(w.x, w.y);
-            } else {
-                vb = *(const half8_t*)((const _Float16*)a.vc + (hb * hd + 16 * dt + lr) * a.cap + tv);
-            }
-#pragma unroll
-            for (int rt = 0; rt < AM_RT; rt++) o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, o[rt][dt], 0, 0, 0);
+            const half8_t va = v_operand<KVF>(cur, dt);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
         }
+        cur = nxt;
     }
-    // ---- merge the 4 waves in LDS ----
+    // ---- merge the waves in LDS: lane holds O^T[16*dt + 4*lg + i][lr] ----
 #pragma unroll
-    for (int rt = 0; rt < AM_RT; rt++) {
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float v = o[rt][dt][i] + __shfl_xor(o[rt][dt][i], 32, 64);
-                if (lg < 2) mg_o[wid][rt * 8 + rb + i][16 * dt + lr] = v;
-            }
-        if (lg < 2 && lr == 0)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                mg_m[wid][rt * 8 + rb + i] = mrow[rt][i];
-                mg_l[wid][rt * 8 + rb + i] = lrow[rt][i];
-            }
+    for (int dt = 0; dt < 8; dt++) *(float4_t*)&mg_o[wid][lr][4 + 16 * dt + 4 * lg] = o[dt];
+    if (lg == 0) {
+        mg_m[wid][lr] = m;
+        mg_l[wid][lr] = l;
     }
     __syncthreads();
+    // thread -> (row r, 4 dims at 4*q); 16 rows x 32 quads = 512 threads
+    const int r = tid >> 5, q = tid & 31;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < AM_WAVES; w++) M = fmaxf(M, mg_m[w][r]);
+    float L = 0.f;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < AM_WAVES; w++) {
+        const float mw = mg_m[w][r];
+        const float sc = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        L += mg_l[w][r] * sc;
+        acc += *(const float4_t*)&mg_o[w][r][4 + 4 * q] * sc;
+    }
+    const int rr = r0 + r;
+    float* out = a.out;
+    if (r < R) out += (size_t)(seq * a.S + rr / G) * QD + (kvh + (rr % G) * a.n_kv) * AM_HD + 4 * q;
+    if (a.nchunks == 1) {
+        if (r < R) *(float4_t*)out = acc * (L > 0.f ? 1.0f / L : 0.f);
+        return;
+    }
     const size_t grp = ((size_t)seq * a.n_kv + kvh) * a.ntiles + tile;
-    const size_t rec = (size_t)hd + 2;
-    float* part = a.part + (grp * a.nchunks + chunk) * (size_t)32 * rec;
-    for (int r = wid; r < R; r += 4) {
-        float M = -INFINITY;
-        for (int w = 0; w < 4; w++) M = fmaxf(M, mg_m[w][r]);
-        float L = 0.f, acc0 = 0.f, acc1 = 0.f;
-        for (int w = 0; w < 4; w++) {
-            const float mw = mg_m[w][r];
-            const float sc = mw == -INFINITY ? 0.f : expf(mw - M);
-            L += mg_l[w][r] * sc;
-            acc0 += mg_o[w][r][lane] * sc;
-            acc1 += mg_o[w][r][64 + lane] * sc;
-        }
-        float* pr = part + (size_t)r * rec;
-        st_coh(&pr[2 + lane], acc0);
-        st_coh(&pr[2 + 64 + lane], acc1);
-        if (lane == 0) {
-            st_coh(&pr[0], M);
-            st_coh(&pr[1], L);
-        }
+    const __amdgpu_buffer_rsrc_t prs = coh_rsrc(a.part + grp * a.nchunks * (size_t)AM_ROWS * AM_REC);
+    if (r < R) {
+        const unsigned rec_off = (unsigned)((chunk * AM_ROWS + r) * AM_REC) * 4u;
+        st4_coh(prs, rec_off + 16u + 16u * q, acc);
+        if (q == 0) st4_coh(prs, rec_off, (float4_t){M, L, 0.f, 0.f});
     }
     if (!arrive_last(&a.counters[grp], (unsigned)a.nchunks, &s_last)) return;
-    const float* gp = a.part + grp * a.nchunks * (size_t)32 * rec;
-    for (int r = wid; r < R; r += 4) {
-        float M = -INFINITY;
-        for (int c = 0; c < a.nchunks; c++) M = fmaxf(M, ld_coh(&gp[((size_t)c * 32 + r) * rec]));
-        float L = 0.f, acc0 = 0.f, acc1 = 0.f;
-        for (int c = 0; c < a.nchunks; c++) {
-            const float* pr = gp + ((size_t)c * 32 + r) * rec;
-            const float mc = ld_coh(&pr[0]);
-            const float w = (mc == -INFINITY) ? 0.f : expf(mc - M);
-            L += ld_coh(&pr[1]) * w;
-            acc0 += ld_coh(&pr[2 + lane]) * w;
-            acc1 += ld_coh(&pr[2 + 64 + lane]) * w;
+
+    // ---- last workgroup: merge the chunks in chunk order ----
+    const int C = a.nchunks;
+    float* sm = &mg_o[0][0][0];  // [C][16] chunk maxima, then [C][16] sums
+    float* sls = sm + AM_MAXCH * AM_ROWS;
+    for (int i = tid; i < C * AM_ROWS; i += 512) {
+        if ((i & 15) < R) {
+            const float4_t v = ld4_coh(prs, (unsigned)(i * AM_REC) * 4u);
+            sm[i] = v[0];
+            sls[i] = v[1];
         }
-        const float inv = L > 0.f ? 1.0f / L : 0.f;
-        const int rr = r0 + r;
-        const int s = rr / G, g = rr % G;
-        float* out = a.out + (size_t)(seq * a.S + s) * QD + (kvh + g * a.n_kv) * hd;
-        out[lane] = acc0 * inv;
-        out[64 + lane] = acc1 * inv;
     }
+    __syncthreads();
+    if (r >= R) return;
+    float4_t ov[AM_MAXCH / 4];
+    float4_t tot = {0.f, 0.f, 0.f, 0.f};
+    float Mc = -INFINITY;
+    for (int c = 0; c < C; c++) Mc = fmaxf(Mc, sm[c * AM_ROWS + r]);
+    float Lc = 0.f;
+    for (int c0 = 0; c0 < C; c0 += AM_MAXCH / 4) {
+#pragma unroll
+        for (int u = 0; u < AM_MAXCH / 4; u++)
+            if (c0 + u < C) ov[u] = ld4_coh(prs, (unsigned)(((c0 + u) * AM_ROWS + r) * AM_REC + 4 + 4 * q) * 4u);
+#pragma unroll
+        for (int u = 0; u < AM_MAXCH / 4; u++)
+            if (c0 + u < C) {
+                const float mc = sm[(c0 + u) * AM_ROWS + r];
+                const float w = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - Mc);
+                Lc += sls[(c0 + u) * AM_ROWS + r] * w;
+                tot += ov[u] * w;
+            }
+    }
+    *(float4_t*)out = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
 }
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
     const int grid = a.nseq * a.n_kv * a.ntiles * a.nchunks;
     (void)hipGetLastError();
     if ((a.kv_fmt == KV_INT8 || a.kv_fmt == KV_F16) && a.hd == AM_HD) {
-        if (a.rows_per_tile > AM_ROWS || a.chunk % 128) return 3;
+        if (a.rows_per_tile > AM_ROWS || a.chunk % (32 * AM_WAVES) || a.nchunks > AM_MAXCH || a.cap % 32) return 3;
         if (a.kv_fmt == KV_INT8)
-            hipLaunchKernelGGL(attn_mfma_kernel<KV_INT8>, dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL(attn_mfma_kernel<KV_INT8>, dim3(grid), dim3(512), 0, stream, a);
         else
-            hipLaunchKernelGGL(attn_mfma_kernel<KV_F16>, dim3(grid), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL(attn_mfma_kernel<KV_F16>, dim3(grid), dim3(512), 0, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
     if (a.hd > AT_MAXHD || a.rows_per_tile > AT_MAXR || a.rows_per_tile <= 0) return 3;

@@ -103,6 +103,19 @@ __device__ __forceinline__ int32_t ld_coh_i32(const int32_t* p) {
     return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // All of this thread's memory operations have completed.
+// 16-byte agent-coherent global access through a raw buffer resource (cache policy
+// sc1: the access is performed at device scope, past the per-XCD L2 state), for
+// partial results handed between workgroups of one launch.  Offsets in bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4_t ld4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
+}
+__device__ __forceinline__ void st4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4_t v) {
+    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)byte_off, 0, 16);
+}
 __device__ __forceinline__ void wait_mem() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

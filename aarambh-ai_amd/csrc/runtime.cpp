@@ -330,17 +330,20 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
     const int G = c->cfg.n_heads / c->cfg.n_kv_heads;
     const int Rt = S * G;
     const bool mf = attention_uses_mfma(kv_fmt, c->hd);
-    const int gran = mf ? 128 : 64;  // tokens per chunk granule
+    // tokens per chunk granule (MFMA: 8 waves x 32-token blocks) and target workgroup count
+    // (MFMA: one 8-wave workgroup per CU)
+    const int gran = mf ? 256 : 64;
+    const int target = mf ? 256 : 512;
     at.rows_per_tile = std::min(mf ? 16 : 32, Rt);
     at.ntiles = (Rt + at.rows_per_tile - 1) / at.rows_per_tile;
     const int base = nseq * c->cfg.n_kv_heads * at.ntiles;
     const int max_chunks = std::max(1, (max_kv_len + gran - 1) / gran);
-    int nch = std::max(1, std::min(max_chunks, (512 + base - 1) / base));
+    int nch = std::max(1, std::min(std::min(max_chunks, 64), (target + base - 1) / base));
     int chunk = ((max_kv_len + nch - 1) / nch + gran - 1) / gran * gran;
     nch = (max_kv_len + chunk - 1) / chunk;
     at.chunk = chunk;
     at.nchunks = nch;
-    size_t need = (size_t)base * nch * 32 * (c->hd + 2);
+    size_t need = (size_t)base * nch * 32 * (c->hd + 4);
     if (need > c->apart_elems) return fail(c, AARH_ERR_SHAPE, "attention scratch too small");
     at.part = c->apart;
     at.counters = c->acnt;
@@ -689,7 +692,7 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         // is at most ceil(512/groups) so groups*chunks <= groups + 512.
         const int G = g.n_heads / g.n_kv_heads;
         const size_t groups = (size_t)g.n_kv_heads * ((size_t)M + ((size_t)M * G + 15) / 16);
-        c->apart_elems = (groups + 512) * 32 * (c->hd + 2);
+        c->apart_elems = (groups + 512) * 32 * (c->hd + 4);
         if (dalloc(c, &c->apart, c->apart_elems * 4)) return AARH_ERR_DEVICE;
         if (dalloc(c, &c->acnt, groups * 4)) return AARH_ERR_DEVICE;
         HIPCHK(c, hipMemset(c->acnt, 0, groups * 4));
