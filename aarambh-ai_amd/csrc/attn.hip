@@ -16,6 +16,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "frag.hpp"
 
 namespace aarh {
 
@@ -23,6 +24,63 @@ static constexpr int AT_THREADS = 256;  // 4 waves
 static constexpr int AT_TOK = 64;       // tokens per LDS sub-block
 static constexpr int AT_MAXR = 32;      // query rows per workgroup
 static constexpr int AT_MAXHD = 128;
+
+// Append this launch's new K / V rows (positions pos0 .. kv_len-1, post-RoPE
+// f32 rows written by the QKV projection) that fall in [t_begin, t_end) to the
+// cache of (slot, kv head).  Every workgroup whose chunk covers a new position
+// writes it (identical bytes) before it reads the chunk, so no other launch
+// is needed.  INT8: per token, per kv head absmax scale (1.0 when <= eps) kept
+// as fp16, codes rounded from the f32 scale.  Returns with the writes visible
+// to the workgroup.
+__device__ void append_new_kv(const AttnArgs& a, int seq, int kvh, size_t hb, int pos0, int t_begin, int t_end) {
+    const int lo = max(t_begin, pos0);
+    if (lo >= t_end) return;  // uniform over the workgroup
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int hd = a.hd, KD = a.n_kv * hd;
+    for (int t = lo + wid; t < t_end; t += nw) {
+        const size_t row = (size_t)seq * a.S + (t - pos0);
+#pragma unroll
+        for (int which = 0; which < 2; which++) {
+            const float* src = a.knew + row * 2 * KD + (size_t)which * KD + (size_t)kvh * hd;
+            const float v0 = lane < hd ? src[lane] : 0.f;
+            const float v1 = lane + 64 < hd ? src[lane + 64] : 0.f;
+            const size_t kbase = (hb * a.cap + t) * hd;          // K [..][cap][hd]
+            const size_t vbase = hb * hd * a.cap + t;            // V^T [..][hd][cap]
+            if (a.kv_fmt == KV_INT8) {
+                const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+                const float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
+                const int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.0f), 127.0f);
+                const int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
+                const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
+                if (which == 0) {
+                    int8_t* kc = (int8_t*)a.kc + kbase;
+                    if (lane < hd) kc[lane] = q0;
+                    if (lane + 64 < hd) kc[lane + 64] = q1;
+                    if (lane == 0) ((uint16_t*)a.ks)[hb * a.cap + t] = sh;
+                } else {
+                    int8_t* vc = (int8_t*)a.vc + vbase;
+                    if (lane < hd) vc[(size_t)lane * a.cap] = q0;
+                    if (lane + 64 < hd) vc[(size_t)(lane + 64) * a.cap] = q1;
+                    if (lane == 0) ((uint16_t*)a.vs)[hb * a.cap + t] = sh;
+                }
+            } else if (a.kv_fmt == KV_F16) {
+                _Float16* dst = (_Float16*)(which == 0 ? a.kc : a.vc);
+                const size_t st = which == 0 ? 1 : (size_t)a.cap;
+                const size_t base = which == 0 ? kbase : vbase;
+                if (lane < hd) dst[base + lane * st] = (_Float16)v0;
+                if (lane + 64 < hd) dst[base + (lane + 64) * st] = (_Float16)v1;
+            } else {
+                float* dst = (float*)(which == 0 ? a.kc : a.vc);
+                const size_t st = which == 0 ? 1 : (size_t)a.cap;
+                const size_t base = which == 0 ? kbase : vbase;
+                if (lane < hd) dst[base + lane * st] = v0;
+                if (lane + 64 < hd) dst[base + (lane + 64) * st] = v1;
+            }
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+}
 
 __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
     __shared__ float qs[AT_MAXR][AT_MAXHD];
@@ -59,6 +117,7 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
 
     const int t_begin = chunk * a.chunk;
     const int t_end = min(kv_len, t_begin + a.chunk);
+    append_new_kv(a, seq, kvh, (size_t)sl * a.n_kv + kvh, pos0, t_begin, t_end);
     // per-wave rows: r = wid + 4*j
     float mrow[AT_MAXR / 4], lrow[AT_MAXR / 4];
     float o0[AT_MAXR / 4], o1[AT_MAXR / 4];
@@ -169,9 +228,14 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
         const int rr = r0 + r;
         const int s = rr / G, g = rr % G;
         const int h = kvh + g * a.n_kv;
-        float* out = a.out + (size_t)(seq * a.S + s) * QD + h * hd;
+        const int orow = seq * a.S + s;
+        float* out = a.out + (size_t)orow * QD + h * hd;
         if (lane < hd) out[lane] = acc0 * inv;
         if (lane + 64 < hd) out[lane + 64] = acc1 * inv;
+        if (a.fo.buf) {
+            if (lane < hd) frag_put(a.fo, orow, h * hd + lane, acc0 * inv);
+            if (lane + 64 < hd) frag_put(a.fo, orow, h * hd + lane + 64, acc1 * inv);
+        }
     }
 }
 
@@ -348,6 +412,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const size_t hb = (size_t)sl * a.n_kv + kvh;
     const int t_begin = chunk * a.chunk;
     const int t_end = min(kv_len, t_begin + a.chunk);
+    append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
 
     // ---- this lane's query row (lr): Q^T B operand, hi/lo, dims 32*lg + 8*kk + slot ----
     const bool row_ok = lr < R;
@@ -468,10 +533,17 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         acc += *(const float4_t*)&mg_o[w][r][4 + 4 * q] * sc;
     }
     const int rr = r0 + r;
+    const int orow = seq * a.S + rr / G, ocol = (kvh + (rr % G) * a.n_kv) * AM_HD + 4 * q;
     float* out = a.out;
-    if (r < R) out += (size_t)(seq * a.S + rr / G) * QD + (kvh + (rr % G) * a.n_kv) * AM_HD + 4 * q;
+    if (r < R) out += (size_t)orow * QD + ocol;
     if (a.nchunks == 1) {
-        if (r < R) *(float4_t*)out = acc * (L > 0.f ? 1.0f / L : 0.f);
+        if (r < R) {
+            const float4_t o4 = acc * (L > 0.f ? 1.0f / L : 0.f);
+            *(float4_t*)out = o4;
+            if (a.fo.buf)
+#pragma unroll
+                for (int i = 0; i < 4; i++) frag_put(a.fo, orow, ocol + i, o4[i]);
+        }
         return;
     }
     const size_t grp = ((size_t)seq * a.n_kv + kvh) * a.ntiles + tile;
@@ -514,7 +586,11 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
                 tot += ov[u] * w;
             }
     }
-    *(float4_t*)out = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
+    const float4_t o4 = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
+    *(float4_t*)out = o4;
+    if (a.fo.buf)
+#pragma unroll
+        for (int i = 0; i < 4; i++) frag_put(a.fo, orow, ocol + i, o4[i]);
 }
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {

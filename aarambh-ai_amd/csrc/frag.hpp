@@ -1,0 +1,32 @@
+// Device-side writer of XFrag activation fragments (see kernels.hpp).
+#pragma once
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aarh {
+
+// Store element (m, c) of an activation matrix (value x before the consumer's
+// norm weight) into its fragment entries.  Rows past f.mp of a chunk with
+// mp <= 8 are never consumed and are not written.
+__device__ __forceinline__ void frag_put(const XFrag& f, int m, int c, float x) {
+    const float v = f.norm_w ? x * f.norm_w[c] : x;
+    uint16_t hi, lo;
+    if (f.fmt == WF_BF16) {
+        hi = f32_to_bf16_rne(v);
+        lo = f32_to_bf16_rne(v - bf16_to_f32(hi));
+    } else {
+        const _Float16 h = (_Float16)v;
+        hi = __builtin_bit_cast(uint16_t, h);
+        lo = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
+    }
+    const int mt = m >> 4, r = m & 15;
+    if (f.mp <= 8 && r >= f.mp) return;
+    const int g = c >> 7, lg = (c >> 5) & 3, t = (c >> 3) & 3, j = frag_slot(f.fmt, c & 7);
+    const int epb = frag_epb(f.mp);
+    const size_t base = ((((size_t)mt * f.G + g) * 4 + t) * 4 + lg) * epb;
+    const int ehi = f.mp <= 8 ? r : 2 * r, elo = f.mp <= 8 ? f.mp + r : 2 * r + 1;
+    f.buf[(base + ehi) * 8 + j] = hi;
+    f.buf[(base + elo) * 8 + j] = lo;
+}
+
+}  // namespace aarh

@@ -7,31 +7,41 @@
 // Layout: W [N, K] is stored as 16-row x 128-column tiles, tile (nt, g) is a
 // contiguous block (1 KiB INT4, 2 KiB INT8, 4 KiB BF16) in which lane l of a
 // wave owns row l%16, columns 32*(l/16)..+32 of the group: one 16/32/64-byte
-// load per lane, 1-4 KiB per wave instruction, fully coalesced.  INT4 scale
-// and zero (fp16) sit beside the tiles, one u32 per (tile, group, row).
+// load per lane, fully coalesced.  INT4 scale and zero (fp16) sit beside the
+// tiles, one u32 per (tile, group, row).
 //
-// Compute: weights are dequantised in registers to EXACT fp16 integers
-// (q - z for INT4, code for INT8: magic-number 0x6400 conversion) or used as
-// bf16; activations are staged in LDS as fp16 (bf16) hi + lo rows, so one
-// v_mfma_f32_16x16x32 tile holds 8 activation rows at ~22-bit precision
-// (rows 8-15 of the A tile would otherwise be padding when M <= 8).  The
-// INT4 group scale multiplies the fp32 group accumulator.  K is split over
-// S workgroups per 128-row group; partials are summed in a fixed order by the
-// last workgroup to arrive (atomic counter), which also runs the fused
-// epilogue: plain store, residual add (+ sum of squares for the next
-// RMSNorm), SwiGLU, or RoPE + KV-cache append for the QKV projection.
+// Work split: one workgroup (4 waves) per 16-row tile and the whole K; wave w
+// takes groups w, w+4, ...  Nothing is exchanged between workgroups: the four
+// wave partials are added in LDS in a fixed order and the workgroup runs the
+// fused epilogue on its 16 output columns (store, residual add, SwiGLU of the
+// 8 gate + 8 up rows of the tile, or RoPE of the 8 (d, d + hd/2) pairs of the
+// tile + query / new K,V rows out).
+//
+// Compute: weights are dequantised in registers to EXACT fp16 integers (q - z
+// for INT4, the code for INT8, magic-number 0x6400 conversion) or used as
+// bf16.  Activations are read as f32 straight from L2 and split into fp16
+// (bf16) hi + lo halves; both halves multiply the same weight fragment
+// (two MFMAs), so products keep ~22 bits.  The INT4 group scale multiplies the
+// fp32 group accumulator.  RMSNorm is fused: the workgroup multiplies x by the
+// norm weight before the MFMA, accumulates sum(x^2) over the rows it reads
+// (the full K) and scales the result rows by 1/rms at the end.
 #include <float.h>
+
+#include <algorithm>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "frag.hpp"
 
 namespace aarh {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-static constexpr int GV_THREADS = 512;  // 8 waves x one 16-row tile = 128 rows per workgroup
-static constexpr int LDS_PAD = 8;       // halves of padding per LDS row
+static constexpr int GT_NW = 8;         // waves per workgroup of the fragment GEMV
+static constexpr int GT_PF = 4;         // its prefetch ring depth (items per wave)
+static constexpr int GT_THREADS = 256;  // f32 GEMV workgroup
+static constexpr int GT_MROWS = 16;     // activation rows per launch (one MFMA row tile)
 
 template <int FMT>
 struct FmtTraits;
@@ -48,14 +58,13 @@ struct FmtTraits<WF_BF16> {
     static constexpr int TILE_BYTES = 4096, LANE_WORDS = 16, PF = 2;
 };
 
-// LDS slot of activation column k so that the A operand matches the order in
-// which the weight dequantisation emits B elements.
+// Element of an 8-column block that k-slot j of an operand holds: the order in
+// which the weight dequantisation below emits B elements.
 template <int FMT>
-__device__ __forceinline__ int a_slot(int k) {
-    const int w = k & 7, blk = k & ~7;
-    if (FMT == WF_INT4) return blk + (((w & 3) << 1) | (w >> 2));
-    if (FMT == WF_INT8) return blk + ((w & 4) | ((w & 1) << 1) | ((w >> 1) & 1));
-    return k;
+__device__ __forceinline__ constexpr int slot_elem(int j) {
+    if (FMT == WF_INT4) return (j >> 1) | ((j & 1) << 2);
+    if (FMT == WF_INT8) return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+    return j;
 }
 
 __device__ __forceinline__ half8_t int4_b_operand(uint32_t v, half2_t zz) {
@@ -88,492 +97,405 @@ __device__ __forceinline__ half8_t int8_b_operand(uint32_t d0, uint32_t d1) {
 }
 
 // ---------------------------------------------------------------------------
-// Epilogues (run by the last workgroup of a 128-row group on the reduced
-// tile yt[M][128] in LDS).
+// Epilogues on the reduced tile yt[m][n] (m < Mc activation rows of this
+// chunk, n < 16 output columns nt*16 + n).
 // ---------------------------------------------------------------------------
-__device__ void epi_store(const GemvArgs& a, float* yt, int rg) {
-    for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
-        int m = idx >> 7, c = idx & 127;
-        a.out[row_off(a.omap, m) + rg * 128 + c] = yt[idx];
-    }
-}
-
-__device__ void epi_resid(const GemvArgs& a, float* yt, int rg) {
-    for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
-        int m = idx >> 7, c = idx & 127;
-        float* p = a.resid + (size_t)m * a.ldr + rg * 128 + c;
-        float xn = *p + yt[idx];
-        *p = xn;
-        yt[idx] = xn;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int m = wid; m < a.M; m += nw) {
-        float v0 = yt[m * 128 + lane], v1 = yt[m * 128 + 64 + lane];
-        float s = wave_sum_f32(v0 * v0 + v1 * v1);
-        if (lane == 0) a.ssq_out[(size_t)rg * a.M + m] = s;
-    }
-}
-
-__device__ void epi_swiglu(const GemvArgs& a, float* yt, int rg) {
-    // 128 rows = 8 tiles of (8 gate rows, 8 up rows) for 64 consecutive ffn columns.
-    for (int idx = threadIdx.x; idx < a.M * 64; idx += blockDim.x) {
-        int m = idx >> 6, j = idx & 63;
-        int tt = j >> 3, w = j & 7;
-        float g = yt[m * 128 + tt * 16 + w];
-        float u = yt[m * 128 + tt * 16 + 8 + w];
-        float silu = g / (1.0f + expf(-g));
-        a.out[row_off(a.omap, m) + rg * 64 + j] = silu * u;
-    }
-}
-
-__device__ void epi_qkv(const GemvArgs& a, float* yt, int rg) {
-    const QkvEpi& e = a.qkv;
-    const int hd = e.hd, half = hd >> 1;
-    const int QD = e.n_heads * hd, KD = e.n_kv * hd;
-    const int S = a.omap.S;
-    // RoPE (rope.rs:107-126) on q and k columns, in place.
-    for (int idx = threadIdx.x; idx < a.M * 64; idx += blockDim.x) {
-        int m = idx >> 6, pp = idx & 63;
-        int hs = pp / half, d = pp % half;
-        int c1 = hs * hd + d, c2 = c1 + half;
-        int n1 = rg * 128 + c1;
-        if (n1 < QD + KD) {
-            int bs = m / S, s = m % S;
-            int pos = e.pos0[bs] + s;
-            float cs = e.rope_cos[(size_t)pos * half + d], sn = e.rope_sin[(size_t)pos * half + d];
-            float x1 = yt[m * 128 + c1], x2 = yt[m * 128 + c2];
-            {
-#pragma clang fp contract(off)
-                float r1 = x1 * cs - x2 * sn;
-                float r2 = x1 * sn + x2 * cs;
-                yt[m * 128 + c1] = r1;
-                yt[m * 128 + c2] = r2;
-            }
+// Threads t0, t0 + stride, ... of the caller share the work; wave_only: the
+// caller is a single wave (no workgroup barrier may be used).
+template <int EPI>
+__device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc, int t0, int stride, bool wave_only) {
+    const int tid = t0;
+    if (EPI == EPI_STORE) {
+        for (int idx = tid; idx < Mc * 16; idx += stride) {
+            const int m = idx >> 4, n = idx & 15;
+            a.out[row_off(a.omap, a.m_base + m) + nt * 16 + n] = yt[m][n];
         }
-    }
-    __syncthreads();
-    if (e.kv_fmt != KV_INT8) {
-        for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
-            int m = idx >> 7, c = idx & 127;
-            int n = rg * 128 + c;
-            float v = yt[idx];
-            if (n < QD) {
-                e.q_out[(size_t)m * QD + n] = v;
-                continue;
-            }
-            int bs = m / S, s = m % S;
-            int pos = e.pos0[bs] + s, sl = e.slot[bs];
-            bool isk = n < QD + KD;
-            int nn = isk ? n - QD : n - QD - KD;
-            int kvh = nn / hd, d = nn % hd;
-            size_t kidx = (((size_t)sl * e.n_kv + kvh) * e.cap + pos) * hd + d;
-            size_t vidx = (((size_t)sl * e.n_kv + kvh) * hd + d) * e.cap + pos;
-            if (e.kv_fmt == KV_F32) {
-                if (isk) ((float*)e.kc)[kidx] = v;
-                else ((float*)e.vc)[vidx] = v;
+    } else if (EPI == EPI_RESID) {
+        // x += y, and the new x as fragments + 16-column sums of squares for the next RMSNorm
+        for (int idx = tid; idx < Mc * 16; idx += stride) {
+            const int m = idx >> 4, n = idx & 15;
+            float* p = a.resid + (size_t)(a.m_base + m) * a.ldr + nt * 16 + n;
+            const float xn = *p + yt[m][n];
+            *p = xn;
+            yt[m][n] = xn;
+            if (a.fo.buf) frag_put(a.fo, a.m_base + m, nt * 16 + n, xn);
+        }
+        if (a.fo.ssq) {
+            if (wave_only) {
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
             } else {
-                if (isk) ((_Float16*)e.kc)[kidx] = (_Float16)v;
-                else ((_Float16*)e.vc)[vidx] = (_Float16)v;
+                __syncthreads();
+            }
+            if (tid < Mc) {
+                float ss = 0.f;
+#pragma unroll
+                for (int n = 0; n < 16; n++) ss += yt[tid][n] * yt[tid][n];
+                a.fo.ssq[(size_t)nt * a.fo.ssq_rows + a.m_base + tid] = ss;
             }
         }
-        return;
-    }
-    // INT8 cache: per token, per kv-head absmax scale (stored fp16), codes from the f32 scale.
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int hpg = 128 / hd;
-    for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
-        int m = idx >> 7, c = idx & 127;
-        int n = rg * 128 + c;
-        if (n < QD) e.q_out[(size_t)m * QD + n] = yt[idx];
-    }
-    for (int task = wid; task < a.M * hpg; task += nw) {
-        int m = task / hpg, hs = task % hpg;
-        int n0 = rg * 128 + hs * hd;
-        if (n0 < QD) continue;
-        int bs = m / S, s = m % S;
-        int pos = e.pos0[bs] + s, sl = e.slot[bs];
-        bool isk = n0 < QD + KD;
-        int kvh = (isk ? n0 - QD : n0 - QD - KD) / hd;
-        float v0 = lane < hd ? yt[m * 128 + hs * hd + lane] : 0.0f;
-        float v1 = (lane + 64) < hd ? yt[m * 128 + hs * hd + lane + 64] : 0.0f;
-        float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
-        float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
-        int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.0f), 127.0f);
-        int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
-        _Float16 sch = (_Float16)sc;
-        if (isk) {
-            int8_t* kc = (int8_t*)e.kc + (((size_t)sl * e.n_kv + kvh) * e.cap + pos) * hd;
-            if (lane < hd) kc[lane] = q0;
-            if (lane + 64 < hd) kc[lane + 64] = q1;
-            if (lane == 0) e.ks[((size_t)sl * e.n_kv + kvh) * e.cap + pos] = __builtin_bit_cast(uint16_t, sch);
-        } else {
-            int8_t* vc = (int8_t*)e.vc + ((size_t)sl * e.n_kv + kvh) * hd * e.cap + pos;
-            if (lane < hd) vc[(size_t)lane * e.cap] = q0;
-            if (lane + 64 < hd) vc[(size_t)(lane + 64) * e.cap] = q1;
-            if (lane == 0) e.vs[((size_t)sl * e.n_kv + kvh) * e.cap + pos] = __builtin_bit_cast(uint16_t, sch);
+    } else if (EPI == EPI_SWIGLU) {
+        // rows 0-7 of the tile are gate rows, 8-15 the matching up rows (ffn columns nt*8 + r)
+        for (int idx = tid; idx < Mc * 8; idx += stride) {
+            const int m = idx >> 3, r = idx & 7;
+            const float g = yt[m][r], u = yt[m][8 + r];
+            const float silu = g / (1.0f + expf(-g));
+            const float h = silu * u;
+            a.out[row_off(a.omap, a.m_base + m) + nt * 8 + r] = h;
+            if (a.fo.buf) frag_put(a.fo, a.m_base + m, nt * 8 + r, h);
+        }
+    } else {
+        // QKV: the tile holds dims d = 8j + r (rows r < 8) and d + hd/2 (rows 8 + r) of one head.
+        const QkvEpi& e = a.qkv;
+        const int hd = e.hd, half = hd >> 1;
+        const int QD = e.n_heads * hd, KD = e.n_kv * hd;
+        const int row0 = nt * 16;
+        const int head = row0 / hd, j = (row0 % hd) >> 4;
+        const bool is_q = row0 < QD, is_k = !is_q && row0 < QD + KD;
+        for (int idx = tid; idx < Mc * 8; idx += stride) {
+            const int m = idx >> 3, r = idx & 7;
+            const int mg = a.m_base + m;
+            const int d1 = 8 * j + r, d2 = d1 + half;
+            float y1 = yt[m][r], y2 = yt[m][8 + r];
+            if (is_q || is_k) {
+                // RoPE (rope.rs:107-126): half-split rotation at the row's position
+                const int bs = mg / e.S, s = mg % e.S;
+                const int pos = e.pos0[bs] + s;
+                const float cs = e.rope_cos[(size_t)pos * half + d1], sn = e.rope_sin[(size_t)pos * half + d1];
+                {
+#pragma clang fp contract(off)
+                    const float r1 = y1 * cs - y2 * sn;
+                    const float r2 = y1 * sn + y2 * cs;
+                    y1 = r1;
+                    y2 = r2;
+                }
+            }
+            float* dst;
+            if (is_q) dst = e.q_out + (size_t)mg * QD + head * hd;
+            else if (is_k) dst = e.kv_out + (size_t)mg * 2 * KD + (head - e.n_heads) * hd;
+            else dst = e.kv_out + (size_t)mg * 2 * KD + KD + (head - e.n_heads - e.n_kv) * hd;
+            dst[d1] = y1;
+            dst[d2] = y2;
         }
     }
 }
 
-__device__ void run_epilogue(const GemvArgs& a, float* yt, int rg) {
-    switch (a.epi) {
-        case EPI_STORE: epi_store(a, yt, rg); break;
-        case EPI_RESID: epi_resid(a, yt, rg); break;
-        case EPI_SWIGLU: epi_swiglu(a, yt, rg); break;
-        default: epi_qkv(a, yt, rg); break;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Shared prologue: per-row inverse RMS from split partial sums of squares.
-// ---------------------------------------------------------------------------
-__device__ void prologue_inv_rms(const GemvArgs& a, float* s_inv) {
-    if (!a.norm_w) return;
-    // one wave per row: lane p loads partial p (n_ssq <= 64), one round trip
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int m = wid; m < a.M; m += nw) {
-        float ss = 0.0f;
-        for (int p = lane; p < a.n_ssq; p += 64) ss += a.ssq_part[(size_t)p * a.M + m];
-        ss = wave_sum_f32(ss);
-        if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-    }
-}
-
-// Split-K: the last workgroup of a row group sums the S partials in order.
-__device__ bool finish_partials(const GemvArgs& a, int rg, float* yt, unsigned* s_flag) {
-    if (a.S == 1) return true;
-    if (!arrive_last(&a.counters[rg], (unsigned)a.S, s_flag)) return false;
-    for (int idx = threadIdx.x; idx < a.M * 128; idx += blockDim.x) {
-        int m = idx >> 7, c = idx & 127;
-        const float* p = a.part + (size_t)m * a.N + rg * 128 + c;
-        const size_t stride = (size_t)a.M * a.N;
-        float y = 0.0f;
-        // batches of 8 independent coherent loads: one memory round trip per batch
-        for (int s0 = 0; s0 < a.S; s0 += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = (s0 + j < a.S) ? ld_coh(p + (size_t)(s0 + j) * stride) : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) y += v[j];
-        }
-        yt[idx] = y;
-    }
-    __syncthreads();
-    return true;
-}
-
-__device__ __forceinline__ void map_block(const GemvArgs& a, int& rg, int& ks) {
-    const int nrg = a.N >> 7;
-    const int total = nrg * a.S;
-    int bid = blockIdx.x, logical = bid;
-    // Keep the S workgroups of one row group on one XCD (workgroups are dealt
-    // round-robin over the 8 XCDs), so the split-K reduction stays in one L2.
-    if ((total & 7) == 0) {
-        int per = total >> 3;
-        logical = (bid & 7) * per + (bid >> 3);
-    }
-    rg = logical / a.S;
-    ks = logical % a.S;
-}
-
-template <int FMT, int MTMAX>
-__global__ void __launch_bounds__(GV_THREADS) gemv_mfma_kernel(GemvArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ unsigned s_flag;
+// Quantised GEMV over fragment inputs, persistent over 16-row weight tiles:
+// workgroup b takes tiles b, b + grid, ...; wave w of the NW waves takes the
+// groups w, w + NW, ... of each tile (ngp items per tile, padded to the ring
+// depth PF; padding items are skipped).  A ring of PF slots holds, per item,
+// the weight tile words and the lane's activation fragment entries, so weights
+// (HBM) and fragments (L2) of the next PF items are in flight while one is
+// computed, across tile boundaries.  Loads are buffer loads with wave-uniform
+// offsets, issued unconditionally (indices clamped into range); only the
+// arithmetic depends on whether a group is real: conditional loads would be
+// merged with register copies that wait for ALL outstanding loads.
+//
+// No workgroup barrier inside the stream: at the end of a tile each wave
+// leaves its partial in an LDS slot (two slots, by tile parity) and the last
+// wave to arrive (LDS counter) adds the NW partials in wave order and runs
+// the epilogue alone while the others go on.  A wave waits before reusing a
+// slot until the epilogue two tiles back has released it.
+template <int FMT, int MP, int EPI>
+__global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
+    constexpr int NW = GT_NW;
+    constexpr bool RS = MP <= 8;        // hi / lo in MFMA rows
+    constexpr int EA = RS ? 1 : 2;      // fragment entries per k-step per lane
+    constexpr int EPB = RS ? 2 * MP : 32;
     typedef FmtTraits<FMT> T;
+    constexpr int PF = GT_PF;
+    __shared__ float4_t part_s[2][NW][64];
+    __shared__ float yt_s[2][16][17];
+    __shared__ float s_inv[16];
+    __shared__ unsigned cnt_s[2], gen_s[2];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int G = a.K >> 7;
-    int rg, ks;
-    map_block(a, rg, ks);
-    const int g0 = (ks * G) / a.S, g1 = ((ks + 1) * G) / a.S;
-    const int ng = g1 - g0, KR = ng * 128, k0 = g0 * 128;
-    const int MT = a.split ? (a.M + 7) >> 3 : (a.M + 15) >> 4;
-    const int ldsrow = KR + LDS_PAD;
-    uint16_t* At = (uint16_t*)smem;
-    float* s_inv = (float*)(smem + (size_t)MT * 16 * ldsrow * 2);
-    const int nt = rg * 8 + wid;
+    const int Mc = a.M;
+    const int ntiles = a.N >> 4;
+    const int ngp = ((G + NW - 1) / NW + PF - 1) / PF * PF;  // items per tile per wave
+    const int nmine = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int mt = a.m_base >> 4;
+    const int elane = RS ? min(lr, 2 * MP - 1) : 2 * lr;  // fragment entry of this lane
+    const int glast = G - 1 - ((G - 1 - wid) % NW + NW) % NW;  // last real group of this wave (may be < 0)
 
-    float4_t acc[MTMAX];
+    // ---- 1/rms of each row from the producer's 16-column partial sums ----
+    if (tid < 2) {
+        cnt_s[tid] = 0u;
+        gen_s[tid] = 0u;
+    }
+    if (a.norm_w) {
+        for (int m = wid; m < Mc; m += NW) {
+            float ss = 0.f;
+            for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)q * a.ssq_rows + a.m_base + m];
 #pragma unroll
-    for (int mt = 0; mt < MTMAX; mt++) acc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+            for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+            if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+        }
+    }
+    __syncthreads();
+    if (nmine <= 0) return;
 
-    for (int gi = 0; gi < ng; gi += T::PF) {
-        uint32_t wv[T::PF][T::LANE_WORDS];
-        uint32_t szv[T::PF];
+    const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
+    const unsigned w_voff = (unsigned)lane * T::LANE_WORDS * 4u;
+    const unsigned f_voff = (unsigned)(lg * EPB + elane) * 16u;
+    const unsigned z_voff = (unsigned)lr * 4u;
+    uint32_t wv[PF][T::LANE_WORDS];
+    uint32_t szv[PF];
+    uint4 av[PF][4][EA];
+    // item (tile tl, slot gi) of this wave -> ring slot p
+    auto load_item = [&](int p, int tl, int gi) {
+        const int g = max(min(wid + NW * gi, glast), 0);
+        const unsigned tile = (unsigned)((int)blockIdx.x + tl * (int)gridDim.x) * G + g;
+        const int w_soff = (int)(tile * T::TILE_BYTES);
 #pragma unroll
-        for (int p = 0; p < T::PF; p++) {
-            if (gi + p < ng) {
-                const size_t tile = (size_t)nt * G + g0 + gi + p;
-                const u32x4_t* src = (const u32x4_t*)(a.w + tile * T::TILE_BYTES + (size_t)lane * T::LANE_WORDS * 4);
+        for (int q = 0; q < T::LANE_WORDS / 4; q++) {
+            const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(w_voff + 16u * q), w_soff, 2));
+            wv[p][4 * q + 0] = v[0];
+            wv[p][4 * q + 1] = v[1];
+            wv[p][4 * q + 2] = v[2];
+            wv[p][4 * q + 3] = v[3];
+        }
+        if (FMT == WF_INT4) szv[p] = __builtin_amdgcn_raw_buffer_load_b32(zr, (int)z_voff, (int)(tile * 64u), 0);
+        const int f_soff = (int)(((unsigned)mt * G + g) * 16u * EPB * 16u);
 #pragma unroll
-                for (int q = 0; q < T::LANE_WORDS / 4; q++) {
-                    u32x4_t v = __builtin_nontemporal_load(src + q);
-                    wv[p][4 * q + 0] = v[0];
-                    wv[p][4 * q + 1] = v[1];
-                    wv[p][4 * q + 2] = v[2];
-                    wv[p][4 * q + 3] = v[3];
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < EA; e++)
+                av[p][t][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             fr, (int)(f_voff + 16u * e), f_soff + t * 4 * EPB * 16, 0));
+    };
+#pragma unroll
+    for (int p = 0; p < PF; p++) load_item(p, 0, p);
+
+    for (int tl = 0; tl < nmine; tl++) {
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int gi0 = 0; gi0 < ngp; gi0 += PF) {
+            // items PF ahead: same tile, or the first slots of the next one (last tile: clamped)
+            const bool wrap = gi0 + PF >= ngp;
+            const int rtl = wrap ? min(tl + 1, nmine - 1) : tl;
+            const int rgi0 = wrap ? 0 : gi0 + PF;
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int gi = gi0 + p;
+                if (wid + NW * gi < G) {
+                    if (FMT == WF_INT4) {
+                        const uint32_t szw = szv[p];
+                        const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(szw >> 16));
+                        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
+                        const _Float16 zz = (_Float16)1024.0f + zh;
+                        const half2_t zz2 = {zz, zz};
+                        float4_t g4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const half8_t b = int4_b_operand(wv[p][t], zz2);
+#pragma unroll
+                            for (int e = 0; e < EA; e++)
+                                g4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av[p][t][e]), b, g4, 0, 0, 0);
+                        }
+                        acc += sc * g4;
+                    } else if (FMT == WF_INT8) {
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const half8_t b = int8_b_operand(wv[p][2 * t], wv[p][2 * t + 1]);
+#pragma unroll
+                            for (int e = 0; e < EA; e++)
+                                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av[p][t][e]), b, acc, 0, 0, 0);
+                        }
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const u32x4_t w4 = {wv[p][4 * t], wv[p][4 * t + 1], wv[p][4 * t + 2], wv[p][4 * t + 3]};
+                            const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
+#pragma unroll
+                            for (int e = 0; e < EA; e++)
+                                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[p][t][e]), b, acc, 0, 0, 0);
+                        }
+                    }
                 }
-                if (FMT == WF_INT4) szv[p] = a.sz[tile * 16 + lr];
+                load_item(p, rtl, rgi0 + p);
             }
         }
-        if (gi == 0) {
-            // Activation prologue overlaps the first weight loads.
-            prologue_inv_rms(a, s_inv);
-            if (a.norm_w) __syncthreads();
-            const int rows = a.split ? MT * 8 : MT * 16;
-            for (int idx = tid; idx < rows * KR; idx += GV_THREADS) {
-                int m = idx / KR, k = idx - m * KR;
-                float v = 0.0f;
-                if (m < a.M) {
-                    v = a.x[row_off(a.xmap, m) + k0 + k];
-                    if (a.norm_w) v = v * s_inv[m] * a.norm_w[k0 + k];
-                    if (a.hidden_out && rg == 0) a.hidden_out[(size_t)m * a.K + k0 + k] = v;
-                }
-                uint16_t hi, lo;
-                if (FMT == WF_BF16) {
-                    hi = f32_to_bf16_rne(v);
-                    lo = f32_to_bf16_rne(v - bf16_to_f32(hi));
-                } else {
-                    _Float16 h = (_Float16)v;
-                    hi = __builtin_bit_cast(uint16_t, h);
-                    lo = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
-                }
-                const int sl = a_slot<FMT>(k);
-                if (a.split) {
-                    const int mt = m >> 3, r = m & 7;
-                    At[(size_t)(mt * 16 + r) * ldsrow + sl] = hi;
-                    At[(size_t)(mt * 16 + 8 + r) * ldsrow + sl] = lo;
-                } else {
-                    At[(size_t)m * ldsrow + sl] = hi;
+        // ---- end of tile tl: partial -> slot, the last wave reduces + epilogue ----
+        const int ps = tl & 1;
+        while (__hip_atomic_load(&gen_s[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (unsigned)(tl >> 1))
+            __builtin_amdgcn_s_sleep(1);
+        part_s[ps][wid][lane] = acc;
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&cnt_s[ps], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __shfl(old, 0, 64);
+        if (old == NW - 1) {
+            const int nt = (int)blockIdx.x + tl * (int)gridDim.x;
+            float4_t sum = part_s[ps][0][lane];
+#pragma unroll
+            for (int w = 1; w < NW; w++) sum += part_s[ps][w][lane];
+            float (*yt)[17] = yt_s[ps];
+#pragma unroll
+            for (int i = 0; i < 4; i++) yt[4 * lg + i][lr] = sum[i];
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            float y[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int idx = lane + 64 * q, m = idx >> 4, n = idx & 15;
+                y[q] = 0.f;
+                if (m < Mc) {
+                    float v = RS ? yt[m][n] + yt[MP + m][n] : yt[m][n];
+                    if (a.norm_w) v *= s_inv[m];
+                    if (FMT == WF_INT8) v *= a.rscale[nt * 16 + n];
+                    y[q] = v;
                 }
             }
-            __syncthreads();
-        }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
-        for (int p = 0; p < T::PF; p++) {
-            if (gi + p >= ng) break;
-            const int gl = gi + p;
-            if (FMT == WF_INT4) {
-                const uint32_t szw = szv[p];
-                const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(szw >> 16));
-                const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
-                const _Float16 zz = (_Float16)1024.0f + zh;
-                const half2_t zz2 = {zz, zz};
-                half8_t bop[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++) bop[t] = int4_b_operand(wv[p][t], zz2);
-#pragma unroll
-                for (int mt = 0; mt < MTMAX; mt++) {
-                    if (mt < MT) {
-                    float4_t g4 = {0.f, 0.f, 0.f, 0.f};
-                    const uint16_t* arow = At + (size_t)(mt * 16 + lr) * ldsrow + gl * 128 + 32 * lg;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        half8_t av = *(const half8_t*)(arow + 8 * t);
-                        g4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop[t], g4, 0, 0, 0);
-                    }
-                    acc[mt] += sc * g4;
-                    }
+            for (int q = 0; q < 4; q++) {
+                const int idx = lane + 64 * q, m = idx >> 4, n = idx & 15;
+                if (m < Mc) yt[m][n] = y[q];
+            }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (EPI == EPI_STORE && a.hidden_out && nt == 0) {
+                // final normed hidden state (model.rs:579-585), written once by tile 0
+                for (int idx = lane; idx < Mc * a.K; idx += 64) {
+                    const int m = idx / a.K, k = idx - m * a.K;
+                    const float v = a.x[row_off(a.xmap, a.m_base + m) + k];
+                    a.hidden_out[(size_t)(a.m_base + m) * a.K + k] = v * s_inv[m] * a.norm_w[k];
                 }
-            } else if (FMT == WF_INT8) {
-                half8_t bop[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++) bop[t] = int8_b_operand(wv[p][2 * t], wv[p][2 * t + 1]);
-#pragma unroll
-                for (int mt = 0; mt < MTMAX; mt++) {
-                    if (mt < MT) {
-                    const uint16_t* arow = At + (size_t)(mt * 16 + lr) * ldsrow + gl * 128 + 32 * lg;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        half8_t av = *(const half8_t*)(arow + 8 * t);
-                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop[t], acc[mt], 0, 0, 0);
-                    }
-                    }
-                }
-            } else {
-                bf16x8_t bop[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    u32x4_t w4 = {wv[p][4 * t], wv[p][4 * t + 1], wv[p][4 * t + 2], wv[p][4 * t + 3]};
-                    bop[t] = __builtin_bit_cast(bf16x8_t, w4);
-                }
-#pragma unroll
-                for (int mt = 0; mt < MTMAX; mt++) {
-                    if (mt < MT) {
-                    const uint16_t* arow = At + (size_t)(mt * 16 + lr) * ldsrow + gl * 128 + 32 * lg;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        bf16x8_t av = *(const bf16x8_t*)(arow + 8 * t);
-                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], acc[mt], 0, 0, 0);
-                    }
-                    }
-                }
+            }
+            run_epilogue<EPI>(a, yt, nt, Mc, lane, 64, true);
+            if (lane == 0) {
+                __hip_atomic_store(&cnt_s[ps], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_add(&gen_s[ps], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
     }
-    // ---- partial results ----
-    const int ncol = nt * 16 + lr;
-    const float rs = (FMT == WF_INT8) ? a.rscale[ncol] : 1.0f;
-    __syncthreads();  // all waves finished reading At before it is reused as yt
-    float* yt = (float*)smem;
-#pragma unroll
-    for (int mt = 0; mt < MTMAX; mt++) {
-        if (mt >= MT) continue;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v = acc[mt][i] * rs;
-            int m;
-            bool writer;
-            if (a.split) {
-                v += __shfl_xor(v, 32, 64);
-                m = mt * 8 + 4 * lg + i;
-                writer = lg < 2;
-            } else {
-                m = mt * 16 + 4 * lg + i;
-                writer = true;
-            }
-            if (writer && m < a.M) {
-                if (a.S == 1) yt[m * 128 + wid * 16 + lr] = v;
-                else st_coh(&a.part[((size_t)ks * a.M + m) * a.N + ncol], v);
-            }
-        }
-    }
-    if (a.S == 1) __syncthreads();
-    if (!finish_partials(a, rg, yt, &s_flag)) return;
-    run_epilogue(a, yt, rg);
 }
 
-// Plain fp32 weights (the reference's CPU dtype): exact fp32 FMA dot products
-// on the vector ALUs, same split-K / epilogue scheme.  Used by fp32 models.
-__global__ void __launch_bounds__(GV_THREADS) gemv_f32_kernel(GemvArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ unsigned s_flag;
+// Plain fp32 weights (the reference's CPU dtype, row-major, rows in the same
+// order as the tiled formats): fp32 FMA dot products on the vector ALUs, one
+// workgroup per 16-row tile; thread (r, c) owns weight row r and activation
+// rows c, c+16, ...; x is staged in LDS 128 columns at a time.
+__global__ void __launch_bounds__(GT_THREADS) gemv_f32_kernel(GemvArgs a) {
+    __shared__ float xs[GT_MROWS][128 + 1];
+    __shared__ float red[4][GT_MROWS][17];
+    __shared__ float s_ssq[4][GT_MROWS];
+    __shared__ float yt[GT_MROWS][17];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int G = a.K >> 7;
-    int rg, ks;
-    map_block(a, rg, ks);
-    const int g0 = (ks * G) / a.S, g1 = ((ks + 1) * G) / a.S;
-    const int KR = (g1 - g0) * 128, k0 = g0 * 128;
-    float* xs = (float*)smem;                 // [M][KR]
-    float* s_inv = xs + (size_t)a.M * KR;     // [M]
-    prologue_inv_rms(a, s_inv);
-    __syncthreads();
-    for (int idx = tid; idx < a.M * KR; idx += GV_THREADS) {
-        int m = idx / KR, k = idx - m * KR;
-        float v = a.x[row_off(a.xmap, m) + k0 + k];
-        if (a.norm_w) v = v * s_inv[m] * a.norm_w[k0 + k];
-        if (a.hidden_out && rg == 0) a.hidden_out[(size_t)m * a.K + k0 + k] = v;
-        xs[idx] = v;
-    }
-    __syncthreads();
-    const float* W = (const float*)a.w;
-    // each wave: 16 rows; lane covers k = lane, lane+64, ...
-    float res[16][4];
-    for (int r = 0; r < 16; r++)
-        for (int m = 0; m < 4; m++) res[r][m] = 0.f;
-    // rows processed in M-chunks of 4
-    float* yt = (float*)(smem);  // reused after the loop
-    for (int mb = 0; mb < a.M; mb += 4) {
-        for (int r = 0; r < 16; r++) {
-            const float* wr = W + (size_t)(rg * 128 + wid * 16 + r) * a.K + k0;
-            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-            for (int k = lane; k < KR; k += 64) {
-                float w = wr[k];
-                s0 = fmaf(xs[(mb + 0) * KR + k], w, s0);
-                if (mb + 1 < a.M) s1 = fmaf(xs[(mb + 1) * KR + k], w, s1);
-                if (mb + 2 < a.M) s2 = fmaf(xs[(mb + 2) * KR + k], w, s2);
-                if (mb + 3 < a.M) s3 = fmaf(xs[(mb + 3) * KR + k], w, s3);
-            }
-            res[r][0] = wave_sum_f32(s0);
-            res[r][1] = wave_sum_f32(s1);
-            res[r][2] = wave_sum_f32(s2);
-            res[r][3] = wave_sum_f32(s3);
+    const int nt = blockIdx.x;
+    const int Mc = a.M;
+    const int r = tid >> 4, c = tid & 15;
+    const float* W = (const float*)a.w + (size_t)(nt * 16 + r) * a.K;
+    float acc[2] = {0.f, 0.f};
+    float ssq_part = 0.f;
+    for (int k0 = 0; k0 < a.K; k0 += 128) {
+        __syncthreads();
+        for (int idx = tid; idx < Mc * 128; idx += GT_THREADS) {
+            const int m = idx >> 7, k = idx & 127;
+            const float v = a.x[row_off(a.xmap, a.m_base + m) + k0 + k];
+            xs[m][k] = a.norm_w ? v * a.norm_w[k0 + k] : v;
         }
-        if (a.S > 1 && lane < 16) {
-            for (int mm = 0; mm < 4 && mb + mm < a.M; mm++) {
-                float v = 0.f;
-                for (int r = 0; r < 16; r++)
-                    if (r == lane) v = res[r][mm];
-                st_coh(&a.part[((size_t)ks * a.M + mb + mm) * a.N + rg * 128 + wid * 16 + lane], v);
+        // sum of squares of the raw rows: wave w covers rows w, w+4, ...
+        if (a.norm_w) {
+            for (int m = wid; m < Mc; m += 4) {
+                const float* xr = a.x + row_off(a.xmap, a.m_base + m) + k0;
+                const float v0 = xr[lane], v1 = xr[64 + lane];
+                const float s = wave_sum_f32(v0 * v0 + v1 * v1);
+                if (lane == 0) s_ssq[0][m] = (k0 == 0 ? 0.f : s_ssq[0][m]) + s;
             }
         }
-        if (a.S == 1) {
-            __syncthreads();
-            if (lane < 16)
-                for (int mm = 0; mm < 4 && mb + mm < a.M; mm++) {
-                    float v = 0.f;
-                    for (int r = 0; r < 16; r++)
-                        if (r == lane) v = res[r][mm];
-                    // stash into the tail of LDS beyond xs (yt region is written after loop)
-                    s_inv[a.M + (mb + mm) * 128 + wid * 16 + lane] = v;
-                }
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < GT_MROWS / 16; mi++) {
+            const int m = c + 16 * mi;
+            if (m < Mc) {
+                float s = acc[mi];
+                for (int k = 0; k < 128; k++) s = fmaf(W[k0 + k], xs[m][k], s);
+                acc[mi] = s;
+            }
         }
     }
-    if (a.S == 1) {
-        __syncthreads();
-        for (int idx = tid; idx < a.M * 128; idx += GV_THREADS) yt[idx] = s_inv[a.M + idx];
-        __syncthreads();
+    (void)ssq_part;
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < 1; mi++) {
+        const int m = c + 16 * mi;
+        if (m < Mc) {
+            float y = acc[mi];
+            if (a.norm_w) y *= 1.0f / sqrtf(s_ssq[0][m] / (float)a.K + a.eps);
+            yt[m][r] = y;
+        }
     }
-    if (!finish_partials(a, rg, yt, &s_flag)) return;
-    run_epilogue(a, yt, rg);
+    if (a.hidden_out && nt == 0) {
+        for (int idx = tid; idx < Mc * a.K; idx += GT_THREADS) {
+            const int m = idx / a.K, k = idx - m * a.K;
+            const float inv = 1.0f / sqrtf(s_ssq[0][m] / (float)a.K + a.eps);
+            const float v = a.x[row_off(a.xmap, a.m_base + m) + k];
+            a.hidden_out[(size_t)(a.m_base + m) * a.K + k] = v * inv * a.norm_w[k];
+        }
+    }
+    (void)red;
+    __syncthreads();
+    switch (a.epi) {
+        case EPI_STORE: run_epilogue<EPI_STORE>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
+        case EPI_RESID: run_epilogue<EPI_RESID>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
+        case EPI_SWIGLU: run_epilogue<EPI_SWIGLU>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
+        default: run_epilogue<EPI_QKV>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
+    }
 }
 
-template <int FMT, int MTMAX>
-static int launch_fmt(const GemvArgs& a, hipStream_t stream, size_t lds) {
-    static bool attr = false;
-    if (!attr) {
-        if (note_error(hipFuncSetAttribute((const void*)gemv_mfma_kernel<FMT, MTMAX>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, MAX_DYN_LDS)))
-            return 4;
-        attr = true;
+template <int FMT, int MP, int EPI>
+static int launch_tile(const GemvArgs& a, hipStream_t stream) {
+    static int grid_cap = 0;
+    if (!grid_cap) {
+        int dev = 0, cus = 0, per_cu = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemv_tile_kernel<FMT, MP, EPI>,
+                                                           GT_NW * 64, 0);
+        grid_cap = std::max(1, cus) * std::max(1, per_cu);
     }
+    const int grid = std::min(a.N / 16, grid_cap);
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemv_mfma_kernel<FMT, MTMAX>), dim3((a.N / 128) * a.S), dim3(GV_THREADS), lds,
-                       stream, a);
+    hipLaunchKernelGGL((gemv_tile_kernel<FMT, MP, EPI>), dim3(grid), dim3(GT_NW * 64), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
+template <int FMT, int MP>
+static int launch_epi(const GemvArgs& a, hipStream_t stream) {
+    switch (a.epi) {
+        case EPI_STORE: return launch_tile<FMT, MP, EPI_STORE>(a, stream);
+        case EPI_RESID: return launch_tile<FMT, MP, EPI_RESID>(a, stream);
+        case EPI_SWIGLU: return launch_tile<FMT, MP, EPI_SWIGLU>(a, stream);
+        default: return launch_tile<FMT, MP, EPI_QKV>(a, stream);
+    }
+}
+
 template <int FMT>
-static int launch_mt(const GemvArgs& a, hipStream_t stream, size_t lds) {
-    const int MT = a.split ? (a.M + 7) / 8 : (a.M + 15) / 16;
-    if (MT <= 1) return launch_fmt<FMT, 1>(a, stream, lds);
-    if (MT <= 4) return launch_fmt<FMT, 4>(a, stream, lds);
-    if (MT <= 16) return launch_fmt<FMT, 16>(a, stream, lds);
-    return 2;
+static int launch_fmt(const GemvArgs& a, hipStream_t stream) {
+    if (a.mp == 4) return launch_epi<FMT, 4>(a, stream);
+    if (a.mp == 8) return launch_epi<FMT, 8>(a, stream);
+    return launch_epi<FMT, 16>(a, stream);
 }
 
 int launch_gemv(const GemvArgs& a, hipStream_t stream) {
-    if (a.N % 128 || a.K % 128 || a.M <= 0 || a.S <= 0 || a.S > a.K / 128) return 2;
-    const int G = a.K / 128;
-    const int maxng = (G + a.S - 1) / a.S;
-    const int KR = maxng * 128;
-    size_t yt = (size_t)a.M * 128 * 4;
-    size_t lds;
+    if (a.N % 16 || a.K % 128 || a.M <= 0 || a.M > GT_MROWS) return 2;
+    if (a.fmt != WF_F32 && (!a.xf || (a.mp != 4 && a.mp != 8 && a.mp != 16) || a.M > a.mp || (a.m_base & 15) ||
+                            (a.norm_w && !a.ssq_in)))
+        return 2;
     if (a.fmt == WF_F32) {
-        lds = (size_t)a.M * KR * 4 + (size_t)a.M * 4 + (size_t)a.M * 128 * 4;
-        if (lds < yt) lds = yt;
-        if (lds > MAX_DYN_LDS) return 3;
-        static bool attr = false;
-        if (!attr) {
-            if (note_error(hipFuncSetAttribute((const void*)gemv_f32_kernel,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, MAX_DYN_LDS)))
-                return 4;
-            attr = true;
-        }
         (void)hipGetLastError();
-        hipLaunchKernelGGL(gemv_f32_kernel, dim3((a.N / 128) * a.S), dim3(GV_THREADS), lds, stream, a);
+        hipLaunchKernelGGL(gemv_f32_kernel, dim3(a.N / 16), dim3(GT_THREADS), 0, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
-    const int MT = a.split ? (a.M + 7) / 8 : (a.M + 15) / 16;
-    lds = (size_t)MT * 16 * (KR + LDS_PAD) * 2 + (size_t)a.M * 4;
-    if (lds < yt) lds = yt;
-    if (lds > MAX_DYN_LDS) return 3;
     switch (a.fmt) {
-        case WF_INT4: return launch_mt<WF_INT4>(a, stream, lds);
-        case WF_INT8: return launch_mt<WF_INT8>(a, stream, lds);
-        case WF_BF16: return launch_mt<WF_BF16>(a, stream, lds);
+        case WF_INT4: return launch_fmt<WF_INT4>(a, stream);
+        case WF_INT8: return launch_fmt<WF_INT8>(a, stream);
+        case WF_BF16: return launch_fmt<WF_BF16>(a, stream);
     }
     return 3;
 }

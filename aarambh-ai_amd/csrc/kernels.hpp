@@ -30,20 +30,51 @@ __host__ __device__ inline long long row_off(const RowMap& r, int m) {
     return (long long)(m / r.S) * r.seq_stride + (long long)(m % r.S) * r.row_stride;
 }
 
-// Cache-append part of the fused QKV epilogue (RoPE + KV write).
+// An activation matrix written once, by its producer, in the operand format of
+// the quantised GEMV that consumes it: fp16 (bf16 for BF16 weights) hi and lo
+// halves of x * norm_w, in MFMA k-slot order.  Layout in 16-byte entries:
+//   index = ((((mt * G + g) * 4 + t) * 4 + lg) * EPB + e)
+// for row chunk mt (16 rows), 128-column group g, k-step t (8 columns), lane
+// group lg (32 columns); EPB = 2*mp entries for mp <= 8 (hi of row r at e = r,
+// lo at e = mp + r: the two halves occupy MFMA rows) and 32 for mp = 16 (hi at
+// e = 2r, lo at 2r + 1: the halves are two MFMAs).  The slot of column c inside
+// an entry is frag_slot(fmt, c % 8).  Sums of squares of the raw values over
+// 16-column tiles go to ssq[(c / 16) * ssq_rows + m] for the consumer's RMSNorm.
+struct XFrag {
+    uint16_t* buf;        // null: the consumer reads f32 rows (no fragments)
+    int fmt;              // consumer weight format (WF_INT4 / WF_INT8 / WF_BF16)
+    int mp;               // 4, 8 or 16 activation rows per MFMA row tile
+    int G;                // consumer K / 128
+    const float* norm_w;  // consumer RMSNorm weight (null: none)
+    float* ssq;           // 16-column partial sums of squares (null: none)
+    int ssq_rows;         // row stride of ssq
+};
+
+__host__ __device__ inline int frag_epb(int mp) { return mp <= 8 ? 2 * mp : 32; }
+
+// k-slot j of an 8-column block holds column frag_elem(fmt, j): the order in
+// which the weight dequantisation of each format emits B elements.
+__host__ __device__ inline int frag_elem(int fmt, int j) {
+    if (fmt == WF_INT4) return (j >> 1) | ((j & 1) << 2);
+    if (fmt == WF_INT8) return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+    return j;
+}
+__host__ __device__ inline int frag_slot(int fmt, int e) {
+    if (fmt == WF_INT4) return ((e & 3) << 1) | (e >> 2);
+    if (fmt == WF_INT8) return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1);
+    return e;
+}
+
+// RoPE part of the fused QKV epilogue: rotated queries and the new K / V rows
+// (appended to the cache by the attention kernel).
 struct QkvEpi {
     int n_heads, n_kv, hd;
-    const int* pos0;    // [nseq] position of row s == 0
-    const int* slot;    // [nseq] cache slot of each sequence
+    int S;                 // rows per sequence
+    const int* pos0;       // [nseq] position of row s == 0
     const float* rope_cos;
     const float* rope_sin; // [max_seq][hd/2]
     float* q_out;          // [M][n_heads*hd] rotated queries
-    int kv_fmt;
-    int cap;               // tokens per slot
-    void* kc;              // K [slot][n_kv][cap][hd]
-    void* vc;              // V [slot][n_kv][hd][cap]  (transposed)
-    uint16_t* ks;          // INT8 K scales [slot][n_kv][cap] (fp16)
-    uint16_t* vs;          // INT8 V scales
+    float* kv_out;         // [M][2][n_kv*hd] rotated keys, then values
 };
 
 struct GemvArgs {
@@ -51,24 +82,24 @@ struct GemvArgs {
     const uint8_t* w;     // tiled weights (BF16/INT8/INT4) or row-major f32
     const uint32_t* sz;   // INT4: fp16 scale | fp16 zero << 16, per (tile, group, row)
     const float* rscale;  // INT8: per-row scales
-    int N, K, M;
-    int S;                // k-splits (workgroups per 128-row group)
-    int split;            // 1: activations as fp16/bf16 hi+lo rows
-    const float* x;       // input activations
+    int N, K;
+    int M;                // activation rows of this launch (<= 16)
+    int m_base;           // index of its first row in the row maps
+    const float* x;       // input activations (f32 rows: F32 weights, hidden_out)
     RowMap xmap;
-    const float* norm_w;  // RMSNorm weight fused as prologue (null: none)
-    const float* ssq_part;
-    int n_ssq;
+    const uint16_t* xf;   // input fragments (quantised formats, XFrag layout)
+    int mp;               // their row-tile size
+    const float* norm_w;  // RMSNorm weight fused into the input (null: none)
+    const float* ssq_in;  // 16-column partial sums of squares of the raw input
+    int ssq_rows;
     float eps;
-    float* hidden_out;    // optional normalised input copy [M][K]
-    float* part;          // [S][M][N] split-K partial sums
-    unsigned* counters;   // [N/128], zero between launches
+    float* hidden_out;    // optional normalised input copy [rows][K]
     int epi;
     float* out;           // STORE / SWIGLU output
     RowMap omap;
-    float* resid;         // RESID target [M][N] (row stride ldr)
+    float* resid;         // RESID target [rows][N] (row stride ldr)
     int ldr;
-    float* ssq_out;       // RESID: [N/128][M]
+    XFrag fo;             // RESID / SWIGLU: fragments of the result for its consumer
     QkvEpi qkv;
 };
 
@@ -82,11 +113,13 @@ struct AttnArgs {
     const void* vc;
     const uint16_t* ks;
     const uint16_t* vs;
+    const float* knew;    // [M][2][n_kv*hd] this launch's K and V rows, appended by the kernel
     float scale;
     int chunk;            // tokens per workgroup
     int nchunks;
     int rows_per_tile;    // query rows (token x group-head) per workgroup
     int ntiles;
+    XFrag fo;             // fragments of the output for the wo projection
     float* part;          // scratch partials
     unsigned* counters;   // [nseq*n_kv*ntiles]
     float* out;           // [M][n_heads*hd]
@@ -122,12 +155,12 @@ bool attention_uses_mfma(int kv_fmt, int hd);
 
 // misc kernels
 int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x,
-                 float* ssq_part, hipStream_t stream);
+                 const XFrag& fo, hipStream_t stream);
 int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* table, int table_fmt,
                     const uint32_t* ids, int ids_stride, int nseq, int L, int H, const float* trunk_w,
-                    const float* token_w, float eps, float* x, float* ssq_part, hipStream_t stream);
+                    const float* token_w, float eps, float* x, const XFrag& fo, hipStream_t stream);
 int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, float eps, float* out,
-                     hipStream_t stream);
+                     const XFrag& fo, hipStream_t stream);
 int launch_quantise_tiled(const float* w, int N, int K, int fmt, uint8_t* tiled, uint32_t* sz,
                           float* rscale, int row_offset, int N_total, int interleave_gu,
                           hipStream_t stream);

@@ -6,6 +6,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "frag.hpp"
 
 namespace aarh {
 
@@ -39,25 +40,32 @@ __device__ inline float block_sum(float v, float* red) {
 
 // TokenEmbedding::forward (model/src/embedding.rs:26-28) + split sums of
 // squares over 128-column groups for the first RMSNorm.
-__global__ void embed_kernel(const void* table, int fmt, int H, const uint32_t* ids, float* x,
-                             float* ssq_part, int M) {
+// Fragments + 16-column sums of squares of row m of an activation matrix whose
+// f32 values are already in `row` (one workgroup per row).
+__device__ void emit_row_fragments(const XFrag& fo, const float* row, int m, int H) {
+    if (!fo.buf) return;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) frag_put(fo, m, k, row[k]);
+    if (fo.ssq)
+        for (int q = threadIdx.x; q < (H >> 4); q += blockDim.x) {
+            float ss = 0.f;
+#pragma unroll
+            for (int n = 0; n < 16; n++) ss += row[q * 16 + n] * row[q * 16 + n];
+            fo.ssq[(size_t)q * fo.ssq_rows + m] = ss;
+        }
+}
+
+__global__ void embed_kernel(const void* table, int fmt, int H, const uint32_t* ids, float* x, XFrag fo) {
     const int m = blockIdx.x;
     const size_t base = (size_t)ids[m] * H;
     for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)m * H + k] = load_table(table, fmt, base + k);
     __syncthreads();
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int cg = wid; cg < H / 128; cg += nw) {
-        float a = x[(size_t)m * H + cg * 128 + lane], b = x[(size_t)m * H + cg * 128 + 64 + lane];
-        float s = wave_sum_f32(a * a + b * b);
-        if (lane == 0) ssq_part[(size_t)cg * M + m] = s;
-    }
+    emit_row_fragments(fo, x + (size_t)m * H, m, H);
 }
 
-int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x,
-                 float* ssq_part, hipStream_t stream) {
+int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x, const XFrag& fo,
+                 hipStream_t stream) {
     (void)hipGetLastError();
-    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), 0, stream, table, table_fmt, H, ids, x,
-                       ssq_part, M);
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), 0, stream, table, table_fmt, H, ids, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -65,7 +73,7 @@ int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, i
 // rows 1.. = token_norm(embedding(ids)); one workgroup per output row.
 __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, const void* table, int fmt,
                                 const uint32_t* ids, int ids_stride, int L, int H, const float* trunk_w,
-                                const float* token_w, float eps, float* x, float* ssq_part, int M) {
+                                const float* token_w, float eps, float* x, XFrag fo) {
     __shared__ float red[MT_THREADS / 64];
     const int row = blockIdx.x;
     const int seq = row / L, l = row % L;
@@ -82,25 +90,20 @@ __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, co
     __syncthreads();
     for (int k = threadIdx.x; k < H; k += blockDim.x) out[k] = out[k] * inv * w[k];
     __syncthreads();
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int cg = wid; cg < H / 128; cg += nw) {
-        float a = out[cg * 128 + lane], b = out[cg * 128 + 64 + lane];
-        float s = wave_sum_f32(a * a + b * b);
-        if (lane == 0) ssq_part[(size_t)cg * M + row] = s;
-    }
+    emit_row_fragments(fo, out, row, H);
 }
 
 int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* table, int table_fmt,
                     const uint32_t* ids, int ids_stride, int nseq, int L, int H, const float* trunk_w,
-                    const float* token_w, float eps, float* x, float* ssq_part, hipStream_t stream) {
+                    const float* token_w, float eps, float* x, const XFrag& fo, hipStream_t stream) {
     (void)hipGetLastError();
     hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(MT_THREADS), 0, stream, anchor, anchor_stride,
-                       table, table_fmt, ids, ids_stride, L, H, trunk_w, token_w, eps, x, ssq_part, nseq * L);
+                       table, table_fmt, ids, ids_stride, L, H, trunk_w, token_w, eps, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
-// RMSNorm of selected rows (nn/src/norm.rs:17-19).
-__global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float* w, float eps, float* out) {
+// RMSNorm of selected rows (nn/src/norm.rs:17-19), plus fragments of the result.
+__global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float* w, float eps, float* out, XFrag fo) {
     __shared__ float red[MT_THREADS / 64];
     const int m = blockIdx.x;
     const float* r = x + row_off(xmap, m);
@@ -109,20 +112,30 @@ __global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
     for (int k = threadIdx.x; k < H; k += blockDim.x) out[(size_t)m * H + k] = r[k] * inv * w[k];
+    __syncthreads();
+    emit_row_fragments(fo, out + (size_t)m * H, m, H);
 }
 
 int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, float eps, float* out,
-                     hipStream_t stream) {
+                     const XFrag& fo, hipStream_t stream) {
     (void)hipGetLastError();
-    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), 0, stream, x, xmap, H, w, eps, out);
+    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), 0, stream, x, xmap, H, w, eps, out, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
 // Destination row of source row n inside a fused matrix.  interleave 1/2 puts
 // gate/up row f at row (f/8)*16 + f%8 (+8 for up) so a 16-row tile holds 8
-// matching gate and up rows.
+// matching gate and up rows.  interleave = hd (>= 16) pairs RoPE dims within a
+// head of hd rows: tile j of the head holds dims 8j..8j+7 (rows 0-7) and
+// hd/2 + 8j.. (rows 8-15), so the rotation of a pair stays inside one tile.
 __device__ __forceinline__ int dest_row(int n, int row_offset, int interleave) {
     if (interleave == 0) return row_offset + n;
+    if (interleave >= 16) {
+        const int hd = interleave, half = hd >> 1;
+        const int head = n / hd, d = n % hd;
+        const int p = ((d % half) >> 3) * 16 + (d & 7) + (d >= half ? 8 : 0);
+        return row_offset + head * hd + p;
+    }
     return (n >> 3) * 16 + (n & 7) + (interleave == 2 ? 8 : 0);
 }
 

@@ -90,10 +90,11 @@ struct aarh_ctx {
 
     // scratch
     int Mmax = 0;
-    float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *ssq_a = nullptr, *ssq_b = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *ssq_a = nullptr, *kvnew = nullptr;
+    uint16_t *frag_a = nullptr, *frag_b = nullptr;  // activation fragments (x-like / att-h-like inputs)
     float *hidden = nullptr, *logits = nullptr, *part = nullptr, *apart = nullptr, *hn = nullptr;
-    size_t part_elems = 0, apart_elems = 0;
-    unsigned *gcnt = nullptr, *acnt = nullptr;
+    size_t apart_elems = 0;
+    unsigned* acnt = nullptr;
     int32_t *d_pos0 = nullptr, *d_slot = nullptr, *d_zero = nullptr, *d_seqidx = nullptr;
     uint32_t* d_ids = nullptr;
     int32_t *h_pos0 = nullptr, *h_slot = nullptr;
@@ -190,25 +191,6 @@ void free_tensor(DevTensor& t) {
     t = DevTensor{};
 }
 
-// k-splits per 128-row group: enough workgroups to cover 256 CUs twice, each
-// with >= 2 K-groups when possible, activation tile within a 64 KiB LDS budget.
-int choose_S(const DevTensor& t, int M, int split) {
-    const int G = t.K / 128, nrg = t.N / 128;
-    int gmax;
-    if (t.fmt == WF_F32) {
-        long long kr = (160LL * 1024 - (long long)M * 516) / (4LL * M);
-        gmax = (int)std::max(1LL, kr / 128);
-    } else {
-        const int MT = split ? (M + 7) / 8 : (M + 15) / 16;
-        long long kr = 65536LL / (MT * 32) - 8;
-        gmax = (int)std::max(1LL, kr / 128);
-    }
-    int s_min = (G + gmax - 1) / gmax;
-    int s_par = (512 + nrg - 1) / nrg;
-    int S = std::max(s_min, std::min(s_par, std::max(1, G / 2)));
-    return std::min(std::max(S, 1), G);
-}
-
 hipEvent_t take_event(aarh_ctx* c) {
     if (!c->ev_pool.empty()) {
         hipEvent_t e = c->ev_pool.back();
@@ -240,9 +222,31 @@ struct ProfScope {
     }
 };
 
-int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, const float* norm_w,
-         const float* ssq, float* hidden_out, int epi, float* out, RowMap omap, float* resid, int ldr,
-         float* ssq_out, const QkvEpi* qkv, int cls) {
+int frag_mp(int M) { return M <= 4 ? 4 : (M <= 8 ? 8 : 16); }
+
+// Fragments of an activation matrix for a consumer of format `fmt` with K = k
+// (null buffer: the consumer reads f32 rows).
+XFrag xfrag(aarh_ctx* c, uint16_t* buf, int fmt, int k, int mp, const float* norm_w, bool ssq) {
+    XFrag f{};
+    if (fmt == WF_F32) return f;
+    f.buf = buf;
+    f.fmt = fmt;
+    f.mp = mp;
+    f.G = k / 128;
+    f.norm_w = norm_w;
+    f.ssq = ssq ? c->ssq_a : nullptr;
+    f.ssq_rows = c->Mmax;
+    return f;
+}
+
+// y = x . W^T over M activation rows with a fused RMSNorm input (norm_w) and
+// epilogue; launched in chunks of at most 16 rows.  Quantised weights read the
+// input as fragments `xf` (row tile mp) with the RMSNorm statistic from the
+// producer's partial sums; f32 weights read the rows x.  `fo` receives the
+// RESID / SWIGLU result as fragments for the next consumer.
+int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, const uint16_t* xf, int mp,
+         const float* norm_w, float* hidden_out, int epi, float* out, RowMap omap, float* resid, int ldr,
+         const XFrag& fo, const QkvEpi* qkv, int cls) {
     GemvArgs a{};
     a.fmt = t.fmt;
     a.w = t.w;
@@ -250,31 +254,31 @@ int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, co
     a.rscale = t.rscale;
     a.N = t.N;
     a.K = t.K;
-    a.M = M;
-    a.split = t.fmt != WF_F32 ? 1 : 0;  // hi+lo activation rows keep ~22-bit products at any M
-    a.S = choose_S(t, M, a.split);
     a.x = x;
     a.xmap = xmap;
+    a.xf = xf;
+    a.mp = mp;
     a.norm_w = norm_w;
-    a.ssq_part = ssq;
-    a.n_ssq = c->H / 128;
+    a.ssq_in = c->ssq_a;
+    a.ssq_rows = c->Mmax;
     a.eps = c->cfg.norm_eps;
     a.hidden_out = hidden_out;
-    a.part = c->part;
-    a.counters = c->gcnt;
     a.epi = epi;
     a.out = out;
     a.omap = omap;
     a.resid = resid;
     a.ldr = ldr;
-    a.ssq_out = ssq_out;
+    a.fo = fo;
     if (qkv) a.qkv = *qkv;
-    if ((size_t)a.S * M * t.N > c->part_elems)
-        return fail(c, AARH_ERR_SHAPE, "split-K scratch too small (S=%d M=%d N=%d)", a.S, M, t.N);
-    ProfScope ps(c, cls, alg_weight_bytes(t));
-    int r = launch_gemv(a, c->stream);
-    if (r) return fail(c, r, "gemv launch failed (fmt %d N %d K %d M %d S %d): code %d %s", t.fmt, t.N, t.K, M, a.S, r,
-                       last_launch_error());
+    ProfScope ps(c, cls, alg_weight_bytes(t) * ((M + 15) / 16));
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        a.m_base = m0;
+        a.M = std::min(16, M - m0);
+        int r = launch_gemv(a, c->stream);
+        if (r)
+            return fail(c, r, "gemv launch failed (fmt %d N %d K %d M %d): code %d %s", t.fmt, t.N, t.K, a.M, r,
+                        last_launch_error());
+    }
     return 0;
 }
 
@@ -288,27 +292,26 @@ RowMap rm(int S, long long seq_stride, long long row_stride) {
 
 // One transformer block (block.rs:331-350) over M = nseq * S rows whose
 // residual stream is c->x and whose ssq partials for norm1 are in c->ssq_a.
+// The input x arrives with fragments in frag_a for w.qkv (norm1); `after`
+// describes the consumer of the block's output x (next block or LM head).
 int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_pos0, const int32_t* d_slot,
-              int kv_fmt, int cap, void* kc, void* vc, uint16_t* ks, uint16_t* vs, int max_kv_len) {
+              int kv_fmt, int cap, void* kc, void* vc, uint16_t* ks, uint16_t* vs, int max_kv_len,
+              const XFrag& after) {
     const int M = nseq * S, H = c->H;
+    const int mp = frag_mp(M);
     QkvEpi e{};
     e.n_heads = c->cfg.n_heads;
     e.n_kv = c->cfg.n_kv_heads;
     e.hd = c->hd;
+    e.S = S;
     e.pos0 = d_pos0;
-    e.slot = d_slot;
     e.rope_cos = c->rope_cos;
     e.rope_sin = c->rope_sin;
     e.q_out = c->q;
-    e.kv_fmt = kv_fmt;
-    e.cap = cap;
-    e.kc = kc;
-    e.vc = vc;
-    e.ks = ks;
-    e.vs = vs;
+    e.kv_out = c->kvnew;
     int r;
-    if ((r = gemv(c, w.qkv, M, c->x, rm(M, 0, H), w.norm1, c->ssq_a, nullptr, EPI_QKV, nullptr, rm(S, 0, 0),
-                  nullptr, 0, nullptr, &e, AARH_PROF_GEMV_QKV)))
+    if ((r = gemv(c, w.qkv, M, c->x, rm(M, 0, H), c->frag_a, mp, w.norm1, nullptr, EPI_QKV, nullptr, rm(S, 0, 0),
+                  nullptr, 0, XFrag{}, &e, AARH_PROF_GEMV_QKV)))
         return r;
     // attention
     AttnArgs at{};
@@ -320,6 +323,7 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
     at.pos0 = d_pos0;
     at.slot = d_slot;
     at.q = c->q;
+    at.knew = c->kvnew;
     at.kv_fmt = kv_fmt;
     at.cap = cap;
     at.kc = kc;
@@ -348,6 +352,7 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
     at.part = c->apart;
     at.counters = c->acnt;
     at.out = c->att;
+    at.fo = xfrag(c, c->frag_b, w.wo.fmt, c->QD, mp, nullptr, false);
     {
         double kvb = 0;
         if (kv_fmt == KV_INT8) kvb = (double)max_kv_len * nseq * c->cfg.n_kv_heads * (2.0 * c->hd + 4.0);
@@ -355,14 +360,16 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
         ProfScope ps(c, AARH_PROF_ATTENTION, kvb);
         KCHK(c, launch_attention(at, c->stream));
     }
-    if ((r = gemv(c, w.wo, M, c->att, rm(M, 0, c->QD), nullptr, nullptr, nullptr, EPI_RESID, nullptr, rm(1, 0, 0),
-                  c->x, H, c->ssq_b, nullptr, AARH_PROF_GEMV_WO)))
+    if ((r = gemv(c, w.wo, M, c->att, rm(M, 0, c->QD), c->frag_b, mp, nullptr, nullptr, EPI_RESID, nullptr,
+                  rm(1, 0, 0), c->x, H, xfrag(c, c->frag_a, w.gu.fmt, H, mp, w.norm2, true), nullptr,
+                  AARH_PROF_GEMV_WO)))
         return r;
-    if ((r = gemv(c, w.gu, M, c->x, rm(M, 0, H), w.norm2, c->ssq_b, nullptr, EPI_SWIGLU, c->h, rm(M, 0, c->Fp),
-                  nullptr, 0, nullptr, nullptr, AARH_PROF_GEMV_GATEUP)))
+    if ((r = gemv(c, w.gu, M, c->x, rm(M, 0, H), c->frag_a, mp, w.norm2, nullptr, EPI_SWIGLU, c->h, rm(M, 0, c->Fp),
+                  nullptr, 0, xfrag(c, c->frag_b, w.down.fmt, c->Fp, mp, nullptr, false), nullptr,
+                  AARH_PROF_GEMV_GATEUP)))
         return r;
-    if ((r = gemv(c, w.down, M, c->h, rm(M, 0, c->Fp), nullptr, nullptr, nullptr, EPI_RESID, nullptr, rm(1, 0, 0),
-                  c->x, H, c->ssq_a, nullptr, AARH_PROF_GEMV_DOWN)))
+    if ((r = gemv(c, w.down, M, c->h, rm(M, 0, c->Fp), c->frag_b, mp, nullptr, nullptr, EPI_RESID, nullptr,
+                  rm(1, 0, 0), c->x, H, after, nullptr, AARH_PROF_GEMV_DOWN)))
         return r;
     return 0;
 }
@@ -374,17 +381,23 @@ int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const
                 int max_kv_len, float* lout, RowMap lmap, float* hout) {
     const int M = nseq * S, H = c->H;
     if (M > c->Mmax) return fail(c, AARH_ERR_SHAPE, "rows %d exceed max_rows %d", M, c->Mmax);
+    const int mp = frag_mp(M);
     {
         ProfScope ps(c, AARH_PROF_OTHER, 0);
-        KCHK(c, launch_embed(c->embed, c->embed_fmt, H, d_ids, M, c->x, c->ssq_a, c->stream));
+        const BlockW& b0 = c->layers[0];
+        KCHK(c, launch_embed(c->embed, c->embed_fmt, H, d_ids, M, c->x,
+                             xfrag(c, c->frag_a, b0.qkv.fmt, H, mp, b0.norm1, true), c->stream));
     }
     for (int l = 0; l < c->cfg.n_layers; l++) {
+        const XFrag after = l + 1 < c->cfg.n_layers
+                                ? xfrag(c, c->frag_a, c->layers[l + 1].qkv.fmt, H, mp, c->layers[l + 1].norm1, true)
+                                : xfrag(c, c->frag_a, c->lm.fmt, H, mp, c->final_norm, true);
         int r = run_block(c, c->layers[l], nseq, S, d_pos0, d_slot, c->cfg.kv_format, c->cap, c->kc[l], c->vc[l],
-                          c->ksc[l], c->vsc[l], max_kv_len);
+                          c->ksc[l], c->vsc[l], max_kv_len, after);
         if (r) return r;
     }
-    return gemv(c, c->lm, M, c->x, rm(M, 0, H), c->final_norm, c->ssq_a, hout, EPI_STORE, lout, lmap, nullptr, 0,
-                nullptr, nullptr, AARH_PROF_GEMV_LMHEAD);
+    return gemv(c, c->lm, M, c->x, rm(M, 0, H), c->frag_a, mp, c->final_norm, hout, EPI_STORE, lout, lmap, nullptr,
+                0, XFrag{}, nullptr, AARH_PROF_GEMV_LMHEAD);
 }
 
 // forward_mtp_head on device for nseq sequences: anchor rows (stride), ids
@@ -398,20 +411,25 @@ int mtp_head_dev(aarh_ctx* c, int head, const float* d_anchor, long long anchor_
     {
         ProfScope ps(c, AARH_PROF_OTHER, 0);
         KCHK(c, launch_mtp_prep(d_anchor, anchor_stride, c->embed, c->embed_fmt, d_ids, ids_stride, nseq, L, H, hw.trunk,
-                                hw.token, c->cfg.norm_eps, c->x, c->ssq_a, c->stream));
+                                hw.token, c->cfg.norm_eps, c->x,
+                                xfrag(c, c->frag_a, hw.blk.qkv.fmt, H, frag_mp(nseq * L), hw.blk.norm1, true),
+                                c->stream));
     }
     // local cache slots 0..nseq-1 at positions 0..L-1 (no KV cache: mtp.rs:104-114)
-    int r = run_block(c, hw.blk, nseq, L, c->d_zero, c->d_seqidx, KV_F32, c->mcap, c->mkc, c->mvc, nullptr, nullptr, L);
+    int r = run_block(c, hw.blk, nseq, L, c->d_zero, c->d_seqidx, KV_F32, c->mcap, c->mkc, c->mvc, nullptr, nullptr, L,
+                      XFrag{});
     if (r) return r;
+    const int mp = frag_mp(nseq);
     {
         ProfScope ps(c, AARH_PROF_OTHER, 0);
         KCHK(c, launch_norm_rows(c->x + (size_t)(L - 1) * H, rm(1, (long long)L * H, 0), nseq, H, hw.out_norm,
-                                 c->cfg.norm_eps, c->hn, c->stream));
+                                 c->cfg.norm_eps, c->hn, xfrag(c, c->frag_a, c->lm.fmt, H, mp, nullptr, false),
+                                 c->stream));
     }
     // LM head without a norm prologue on the normalised last rows
     DevTensor lm = c->lm;
-    return gemv(c, lm, nseq, c->hn, rm(nseq, 0, H), nullptr, nullptr, nullptr, EPI_STORE, lout, rm(1, lstride, 0),
-                nullptr, 0, nullptr, nullptr, AARH_PROF_GEMV_LMHEAD);
+    return gemv(c, lm, nseq, c->hn, rm(nseq, 0, H), c->frag_a, mp, nullptr, nullptr, EPI_STORE, lout,
+                rm(1, lstride, 0), nullptr, 0, XFrag{}, nullptr, AARH_PROF_GEMV_LMHEAD);
 }
 
 int sync_stream(aarh_ctx* c) {
@@ -470,8 +488,9 @@ void aarh_destroy(aarh_ctx* c) {
     }
     F(c->mkc);
     F(c->mvc);
-    for (void* p : {(void*)c->x, (void*)c->q, (void*)c->att, (void*)c->h, (void*)c->ssq_a, (void*)c->ssq_b,
-                    (void*)c->hidden, (void*)c->logits, (void*)c->part, (void*)c->apart, (void*)c->hn, (void*)c->gcnt,
+    for (void* p : {(void*)c->x, (void*)c->q, (void*)c->att, (void*)c->h, (void*)c->ssq_a, (void*)c->kvnew,
+                    (void*)c->frag_a, (void*)c->frag_b,
+                    (void*)c->hidden, (void*)c->logits, (void*)c->apart, (void*)c->hn,
                     (void*)c->acnt, (void*)c->d_pos0, (void*)c->d_slot, (void*)c->d_zero, (void*)c->d_seqidx,
                     (void*)c->d_ids, (void*)c->acc_max, (void*)c->acc_sum, (void*)c->acc_argmax, (void*)c->acc_cnt})
         F(p);
@@ -573,7 +592,8 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     c->KD = g.n_kv_heads * c->hd;
     c->F = g.ffn_dim;
     c->nheads_mtp = g.num_future_tokens > 1 ? g.num_future_tokens - 1 : 0;
-    if (c->hd > 128 || 128 % c->hd || c->hd % 2) return bad(AARH_ERR_UNSUPPORTED, "head_dim must divide 128");
+    if (c->hd > 128 || 128 % c->hd || c->hd % 16)
+        return bad(AARH_ERR_UNSUPPORTED, "head_dim must be 16, 32, 64 or 128");
     if (c->H % 128 || c->V % 128 || (c->QD + 2 * c->KD) % 128)
         return bad(AARH_ERR_UNSUPPORTED, "hidden, vocab and q+k+v widths must be multiples of 128");
     if (g.weight_format != AARH_W_F32 && g.ffn_dim % 128)
@@ -662,32 +682,21 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         const size_t H = c->H;
         if (dalloc(c, &c->x, M * H * 4) || dalloc(c, &c->q, (size_t)M * c->QD * 4) ||
             dalloc(c, &c->att, (size_t)M * c->QD * 4) || dalloc(c, &c->h, (size_t)M * c->Fp * 4) ||
-            dalloc(c, &c->ssq_a, (H / 128) * M * 4) || dalloc(c, &c->ssq_b, (H / 128) * M * 4) ||
+            dalloc(c, &c->ssq_a, (H / 16) * M * 4) ||
             dalloc(c, &c->hidden, M * H * 4) || dalloc(c, &c->hn, M * H * 4) ||
             dalloc(c, &c->logits, (size_t)M * c->V * 4))
             return AARH_ERR_DEVICE;
         HIPCHK(c, hipMemset(c->h, 0, (size_t)M * c->Fp * 4));
-        // split-K scratch: the largest S*M*N over the model's matrices and row counts
-        size_t pe = 0;
-        auto consider = [&](const DevTensor& t) {
-            for (int m = 1; m <= M; m++) {
-                int split = t.fmt != WF_F32 ? 1 : 0;
-                pe = std::max(pe, (size_t)choose_S(t, m, split) * m * t.N);
-            }
-        };
-        if (!c->layers.empty()) {
-            const BlockW& b = c->layers[0];
-            consider(b.qkv);
-            consider(b.wo);
-            consider(b.gu);
-            consider(b.down);
+        // new K / V rows of a forward, appended to the cache by the attention kernel
+        if (dalloc(c, &c->kvnew, (size_t)M * 2 * c->KD * 4)) return AARH_ERR_DEVICE;
+        // activation fragments: row chunks x groups x 16 (t, lg) x 32 entries x 8 halves
+        {
+            const size_t gmax = (size_t)std::max({c->H, c->QD, c->Fp}) / 128;
+            const size_t halves = (size_t)((M + 15) / 16) * gmax * 16 * 32 * 8;
+            if (dalloc(c, &c->frag_a, halves * 2) || dalloc(c, &c->frag_b, halves * 2)) return AARH_ERR_DEVICE;
+            HIPCHK(c, hipMemset(c->frag_a, 0, halves * 2));
+            HIPCHK(c, hipMemset(c->frag_b, 0, halves * 2));
         }
-        consider(c->lm);
-        c->part_elems = pe;
-        if (dalloc(c, &c->part, pe * 4)) return AARH_ERR_DEVICE;
-        const int maxrg = std::max({c->V, 2 * c->Fp, c->QD + 2 * c->KD, c->H}) / 128;
-        if (dalloc(c, &c->gcnt, (size_t)maxrg * 4)) return AARH_ERR_DEVICE;
-        HIPCHK(c, hipMemset(c->gcnt, 0, (size_t)maxrg * 4));
         // attention scratch: groups = nseq*n_kv*ntiles <= n_kv*(M + M*G/16); the chunk count
         // is at most ceil(512/groups) so groups*chunks <= groups + 512.
         const int G = g.n_heads / g.n_kv_heads;
@@ -742,9 +751,9 @@ static void part_target(aarh_ctx* c, const TensorSlot& s, DevTensor** t, int* ro
     *row_off = 0;
     *inter = 0;
     switch (s.part) {
-        case P_WQ: *t = &b->qkv; break;
-        case P_WK: *t = &b->qkv; *row_off = c->QD; break;
-        case P_WV: *t = &b->qkv; *row_off = c->QD + c->KD; break;
+        case P_WQ: *t = &b->qkv; *inter = c->hd; break;
+        case P_WK: *t = &b->qkv; *row_off = c->QD; *inter = c->hd; break;
+        case P_WV: *t = &b->qkv; *row_off = c->QD + c->KD; *inter = c->hd; break;
         case P_WO: *t = &b->wo; break;
         case P_GATE: *t = &b->gu; *inter = 1; break;
         case P_UP: *t = &b->gu; *inter = 2; break;
