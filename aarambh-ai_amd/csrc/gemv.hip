@@ -32,154 +32,14 @@
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "frag.hpp"
+#include "epilogue.hpp"
 
 namespace aarh {
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 static constexpr int GT_NW = 8;         // waves per workgroup of the fragment GEMV
 static constexpr int GT_PF = 4;         // its prefetch ring depth (items per wave)
 static constexpr int GT_THREADS = 256;  // f32 GEMV workgroup
 static constexpr int GT_MROWS = 16;     // activation rows per launch (one MFMA row tile)
-
-template <int FMT>
-struct FmtTraits;
-template <>
-struct FmtTraits<WF_INT4> {
-    static constexpr int TILE_BYTES = 1024, LANE_WORDS = 4, PF = 8;
-};
-template <>
-struct FmtTraits<WF_INT8> {
-    static constexpr int TILE_BYTES = 2048, LANE_WORDS = 8, PF = 4;
-};
-template <>
-struct FmtTraits<WF_BF16> {
-    static constexpr int TILE_BYTES = 4096, LANE_WORDS = 16, PF = 2;
-};
-
-// Element of an 8-column block that k-slot j of an operand holds: the order in
-// which the weight dequantisation below emits B elements.
-template <int FMT>
-__device__ __forceinline__ constexpr int slot_elem(int j) {
-    if (FMT == WF_INT4) return (j >> 1) | ((j & 1) << 2);
-    if (FMT == WF_INT8) return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
-    return j;
-}
-
-__device__ __forceinline__ half8_t int4_b_operand(uint32_t v, half2_t zz) {
-    uint32_t p0 = (v & 0x000F000Fu) | 0x64006400u;
-    uint32_t p1 = ((v >> 4) & 0x000F000Fu) | 0x64006400u;
-    uint32_t p2 = ((v >> 8) & 0x000F000Fu) | 0x64006400u;
-    uint32_t p3 = ((v >> 12) & 0x000F000Fu) | 0x64006400u;
-    half2_t h0 = __builtin_bit_cast(half2_t, p0) - zz;
-    half2_t h1 = __builtin_bit_cast(half2_t, p1) - zz;
-    half2_t h2 = __builtin_bit_cast(half2_t, p2) - zz;
-    half2_t h3 = __builtin_bit_cast(half2_t, p3) - zz;
-    half8_t r;
-    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-    return r;
-}
-
-__device__ __forceinline__ half8_t int8_b_operand(uint32_t d0, uint32_t d1) {
-    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    d0 ^= 0x80808080u;
-    d1 ^= 0x80808080u;
-    half2_t h0 = __builtin_bit_cast(half2_t, (d0 & 0x00FF00FFu) | 0x64006400u) - off;
-    half2_t h1 = __builtin_bit_cast(half2_t, ((d0 >> 8) & 0x00FF00FFu) | 0x64006400u) - off;
-    half2_t h2 = __builtin_bit_cast(half2_t, (d1 & 0x00FF00FFu) | 0x64006400u) - off;
-    half2_t h3 = __builtin_bit_cast(half2_t, ((d1 >> 8) & 0x00FF00FFu) | 0x64006400u) - off;
-    half8_t r;
-    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-    return r;
-}
-
-// ---------------------------------------------------------------------------
-// Epilogues on the reduced tile yt[m][n] (m < Mc activation rows of this
-// chunk, n < 16 output columns nt*16 + n).
-// ---------------------------------------------------------------------------
-// Threads t0, t0 + stride, ... of the caller share the work; wave_only: the
-// caller is a single wave (no workgroup barrier may be used).
-template <int EPI>
-__device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc, int t0, int stride, bool wave_only) {
-    const int tid = t0;
-    if (EPI == EPI_STORE) {
-        for (int idx = tid; idx < Mc * 16; idx += stride) {
-            const int m = idx >> 4, n = idx & 15;
-            a.out[row_off(a.omap, a.m_base + m) + nt * 16 + n] = yt[m][n];
-        }
-    } else if (EPI == EPI_RESID) {
-        // x += y, and the new x as fragments + 16-column sums of squares for the next RMSNorm
-        for (int idx = tid; idx < Mc * 16; idx += stride) {
-            const int m = idx >> 4, n = idx & 15;
-            float* p = a.resid + (size_t)(a.m_base + m) * a.ldr + nt * 16 + n;
-            const float xn = *p + yt[m][n];
-            *p = xn;
-            yt[m][n] = xn;
-            if (a.fo.buf) frag_put(a.fo, a.m_base + m, nt * 16 + n, xn);
-        }
-        if (a.fo.ssq) {
-            if (wave_only) {
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            } else {
-                __syncthreads();
-            }
-            if (tid < Mc) {
-                float ss = 0.f;
-#pragma unroll
-                for (int n = 0; n < 16; n++) ss += yt[tid][n] * yt[tid][n];
-                a.fo.ssq[(size_t)nt * a.fo.ssq_rows + a.m_base + tid] = ss;
-            }
-        }
-    } else if (EPI == EPI_SWIGLU) {
-        // rows 0-7 of the tile are gate rows, 8-15 the matching up rows (ffn columns nt*8 + r)
-        for (int idx = tid; idx < Mc * 8; idx += stride) {
-            const int m = idx >> 3, r = idx & 7;
-            const float g = yt[m][r], u = yt[m][8 + r];
-            const float silu = g / (1.0f + expf(-g));
-            const float h = silu * u;
-            a.out[row_off(a.omap, a.m_base + m) + nt * 8 + r] = h;
-            if (a.fo.buf) frag_put(a.fo, a.m_base + m, nt * 8 + r, h);
-        }
-    } else {
-        // QKV: the tile holds dims d = 8j + r (rows r < 8) and d + hd/2 (rows 8 + r) of one head.
-        const QkvEpi& e = a.qkv;
-        const int hd = e.hd, half = hd >> 1;
-        const int QD = e.n_heads * hd, KD = e.n_kv * hd;
-        const int row0 = nt * 16;
-        const int head = row0 / hd, j = (row0 % hd) >> 4;
-        const bool is_q = row0 < QD, is_k = !is_q && row0 < QD + KD;
-        for (int idx = tid; idx < Mc * 8; idx += stride) {
-            const int m = idx >> 3, r = idx & 7;
-            const int mg = a.m_base + m;
-            const int d1 = 8 * j + r, d2 = d1 + half;
-            float y1 = yt[m][r], y2 = yt[m][8 + r];
-            if (is_q || is_k) {
-                // RoPE (rope.rs:107-126): half-split rotation at the row's position
-                const int bs = mg / e.S, s = mg % e.S;
-                const int pos = e.pos0[bs] + s;
-                const float cs = e.rope_cos[(size_t)pos * half + d1], sn = e.rope_sin[(size_t)pos * half + d1];
-                {
-#pragma clang fp contract(off)
-                    const float r1 = y1 * cs - y2 * sn;
-                    const float r2 = y1 * sn + y2 * cs;
-                    y1 = r1;
-                    y2 = r2;
-                }
-            }
-            float* dst;
-            if (is_q) dst = e.q_out + (size_t)mg * QD + head * hd;
-            else if (is_k) dst = e.kv_out + (size_t)mg * 2 * KD + (head - e.n_heads) * hd;
-            else dst = e.kv_out + (size_t)mg * 2 * KD + KD + (head - e.n_heads - e.n_kv) * hd;
-            dst[d1] = y1;
-            dst[d2] = y2;
-        }
-    }
-}
 
 // Quantised GEMV over fragment inputs, persistent over 16-row weight tiles:
 // workgroup b takes tiles b, b + grid, ...; wave w of the NW waves takes the
@@ -282,19 +142,19 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
                 if (wid + NW * gi < G) {
                     if (FMT == WF_INT4) {
                         const uint32_t szw = szv[p];
-                        const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(szw >> 16));
                         const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
-                        const _Float16 zz = (_Float16)1024.0f + zh;
-                        const half2_t zz2 = {zz, zz};
-                        float4_t g4 = {0.f, 0.f, 0.f, 0.f};
+                        half2_t zl2, zh2;
+                        int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2, zh2);
+                        float4_t g4[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two independent chains
 #pragma unroll
                         for (int t = 0; t < 4; t++) {
-                            const half8_t b = int4_b_operand(wv[p][t], zz2);
+                            const half8_t b = int4_b_operand(wv[p][t], zl2, zh2);
 #pragma unroll
                             for (int e = 0; e < EA; e++)
-                                g4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av[p][t][e]), b, g4, 0, 0, 0);
+                                g4[(t + e) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    __builtin_bit_cast(half8_t, av[p][t][e]), b, g4[(t + e) & 1], 0, 0, 0);
                         }
-                        acc += sc * g4;
+                        acc += sc * (g4[0] + g4[1]);
                     } else if (FMT == WF_INT8) {
 #pragma unroll
                         for (int t = 0; t < 4; t++) {
@@ -367,7 +227,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
                     a.hidden_out[(size_t)(a.m_base + m) * a.K + k] = v * s_inv[m] * a.norm_w[k];
                 }
             }
-            run_epilogue<EPI>(a, yt, nt, Mc, lane, 64, true);
+            run_epilogue<EPI>(a, yt, nt, Mc, a.m_base, lane, 64, true);
             if (lane == 0) {
                 __hip_atomic_store(&cnt_s[ps], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 __hip_atomic_fetch_add(&gen_s[ps], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -441,10 +301,10 @@ __global__ void __launch_bounds__(GT_THREADS) gemv_f32_kernel(GemvArgs a) {
     (void)red;
     __syncthreads();
     switch (a.epi) {
-        case EPI_STORE: run_epilogue<EPI_STORE>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
-        case EPI_RESID: run_epilogue<EPI_RESID>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
-        case EPI_SWIGLU: run_epilogue<EPI_SWIGLU>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
-        default: run_epilogue<EPI_QKV>(a, yt, nt, Mc, threadIdx.x, GT_THREADS, false); break;
+        case EPI_STORE: run_epilogue<EPI_STORE>(a, yt, nt, Mc, a.m_base, threadIdx.x, GT_THREADS, false); break;
+        case EPI_RESID: run_epilogue<EPI_RESID>(a, yt, nt, Mc, a.m_base, threadIdx.x, GT_THREADS, false); break;
+        case EPI_SWIGLU: run_epilogue<EPI_SWIGLU>(a, yt, nt, Mc, a.m_base, threadIdx.x, GT_THREADS, false); break;
+        default: run_epilogue<EPI_QKV>(a, yt, nt, Mc, a.m_base, threadIdx.x, GT_THREADS, false); break;
     }
 }
 

@@ -150,6 +150,8 @@ struct AcceptArgs {
 
 int launch_accept(const AcceptArgs& a, hipStream_t stream);
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
+// Many-row variant (M > 16, fragments with mp = 16, all rows in one launch).
+int launch_gemm(const GemvArgs& a, hipStream_t stream);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
 bool attention_uses_mfma(int kv_fmt, int hd);
 

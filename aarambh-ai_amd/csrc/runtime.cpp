@@ -270,6 +270,16 @@ int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, co
     a.ldr = ldr;
     a.fo = fo;
     if (qkv) a.qkv = *qkv;
+    if (t.fmt != WF_F32 && M > 16) {
+        ProfScope ps(c, cls, alg_weight_bytes(t));
+        a.m_base = 0;
+        a.M = M;
+        int r = launch_gemm(a, c->stream);
+        if (r)
+            return fail(c, r, "gemm launch failed (fmt %d N %d K %d M %d): code %d %s", t.fmt, t.N, t.K, M, r,
+                        last_launch_error());
+        return 0;
+    }
     ProfScope ps(c, cls, alg_weight_bytes(t) * ((M + 15) / 16));
     for (int m0 = 0; m0 < M; m0 += 16) {
         a.m_base = m0;

@@ -243,7 +243,7 @@ def main():
     b1 = res.get(1, main_r)
     g1 = b1["int4_gemv"]
     roof = {
-        "kernel": "gemv_mfma_kernel<INT4,1> (all INT4 projections of the batch-1 verify step)",
+        "kernel": "gemv_tile_kernel<INT4,*> (all INT4 projections of the batch-1 verify step)",
         "bound": "hbm",
         "achieved": round(g1["gbs"], 1),
         "peak": HBM_PEAK_GBS,
