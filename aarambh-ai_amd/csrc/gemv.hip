@@ -45,24 +45,32 @@ static constexpr int GT_MROWS = 16;     // activation rows per launch (one MFMA 
 // workgroup b takes tiles b, b + grid, ...; wave w of the NW waves takes the
 // groups w, w + NW, ... of each tile (ngp items per tile, padded to the ring
 // depth PF; padding items are skipped).  A ring of PF slots holds, per item,
-// the weight tile words and the lane's activation fragment entries, so weights
-// (HBM) and fragments (L2) of the next PF items are in flight while one is
-// computed, across tile boundaries.  Loads are buffer loads with wave-uniform
-// offsets, issued unconditionally (indices clamped into range); only the
-// arithmetic depends on whether a group is real: conditional loads would be
-// merged with register copies that wait for ALL outstanding loads.
+// the weight tile words (and, on the L2 path, the lane's activation fragment
+// entries), so the next PF items are in flight while one is computed, across
+// tile boundaries.  Loads are buffer loads with wave-uniform offsets, issued
+// unconditionally (indices clamped into range); only the arithmetic depends
+// on whether a group is real: conditional loads would be merged with
+// register copies that wait for ALL outstanding loads.
+//
+// Since a wave meets the same groups in every tile, with NGP > 0 (items per
+// tile per wave known at compile time, MP <= 8) the wave loads the fragment
+// entries of its groups into registers once (16 VGPRs per group) and the
+// stream carries weights and scales only.  NGP == 0 reads the fragments of
+// each item from L2 inside the ring (M > 8, or K beyond the register budget).
 //
 // No workgroup barrier inside the stream: at the end of a tile each wave
 // leaves its partial in an LDS slot (two slots, by tile parity) and the last
 // wave to arrive (LDS counter) adds the NW partials in wave order and runs
 // the epilogue alone while the others go on.  A wave waits before reusing a
 // slot until the epilogue two tiles back has released it.
-template <int FMT, int MP, int EPI>
+template <int FMT, int MP, int EPI, int NGP>
 __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     constexpr int NW = GT_NW;
     constexpr bool RS = MP <= 8;        // hi / lo in MFMA rows
     constexpr int EA = RS ? 1 : 2;      // fragment entries per k-step per lane
     constexpr int EPB = RS ? 2 * MP : 32;
+    constexpr bool REG = NGP > 0;       // fragments held in registers
+    static_assert(!REG || (RS && NGP % GT_PF == 0), "register fragments need MP <= 8 and whole rings");
     typedef FmtTraits<FMT> T;
     constexpr int PF = GT_PF;
     __shared__ float4_t part_s[2][NW][64];
@@ -74,7 +82,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     const int G = a.K >> 7;
     const int Mc = a.M;
     const int ntiles = a.N >> 4;
-    const int ngp = ((G + NW - 1) / NW + PF - 1) / PF * PF;  // items per tile per wave
+    const int ngp = REG ? NGP : ((G + NW - 1) / NW + PF - 1) / PF * PF;  // items per tile per wave
     const int nmine = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int mt = a.m_base >> 4;
     const int elane = RS ? min(lr, 2 * MP - 1) : 2 * lr;  // fragment entry of this lane
@@ -95,6 +103,20 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
         }
     }
     __syncthreads();
+    if (EPI == EPI_STORE && a.hidden_out) {
+        // final normed hidden state (model.rs:579-585): workgroup b writes
+        // columns [b*cw, (b+1)*cw) of every row, 4 at a time
+        const int cw = ((a.K + (int)gridDim.x - 1) / (int)gridDim.x + 3) & ~3;
+        const int k0 = (int)blockIdx.x * cw, kn = min(cw, a.K - k0);
+        for (int idx = tid; idx < Mc * (kn >> 2); idx += NW * 64) {
+            const int m = idx / (kn >> 2), k = k0 + 4 * (idx - m * (kn >> 2));
+            const float4 v = *(const float4*)(a.x + row_off(a.xmap, a.m_base + m) + k);
+            const float4 w = *(const float4*)(a.norm_w + k);
+            const float si = s_inv[m];
+            *(float4*)(a.hidden_out + (size_t)(a.m_base + m) * a.K + k) =
+                make_float4(v.x * si * w.x, v.y * si * w.y, v.z * si * w.z, v.w * si * w.w);
+        }
+    }
     if (nmine <= 0) return;
 
     const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
@@ -103,7 +125,48 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     const unsigned z_voff = (unsigned)lr * 4u;
     uint32_t wv[PF][T::LANE_WORDS];
     uint32_t szv[PF];
-    uint4 av[PF][4][EA];
+    constexpr int NA = REG ? 1 : PF;
+    uint4 av[NA][4][EA];  // L2 path: fragment ring
+    // Register path.  MP == 8: one entry per k-step.  MP == 4 uses MFMA rows
+    // 0..7 only, so k-steps 2j and 2j+1 share a register (lanes 0..7 and 8..15
+    // of each 16-lane row); a row_ror:8 move brings the odd one into rows 0..7
+    // and rows 8..15 of the product are never read.
+    constexpr bool PK = MP == 4;
+    constexpr int NREG = PK ? 2 : 4;
+    uint4 fa[REG ? NGP : 1][NREG];
+    auto load_frag_reg = [&](uint4 (&f)[NREG], int g) {
+        const int f_soff = (int)(((unsigned)mt * G + g) * 16u * EPB * 16u);
+        const unsigned voff = PK ? (unsigned)((lg * EPB + (lr & 7)) * 16 + (lr >> 3) * 4 * EPB * 16) : f_voff;
+#pragma unroll
+        for (int j = 0; j < NREG; j++)
+            f[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 fr, (int)voff, f_soff + (PK ? 2 : 1) * j * 4 * EPB * 16, 0));
+    };
+    auto unpack_frag = [&](const uint4 (&f)[NREG], uint4 (&o)[4][EA]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (!PK) {
+                o[t][0] = f[t];
+            } else if ((t & 1) == 0) {
+                o[t][0] = f[t >> 1];
+            } else {
+                const uint4 v = f[t >> 1];
+                o[t][0] = make_uint4(__builtin_amdgcn_update_dpp(0u, v.x, 0x128, 0xF, 0xF, false),
+                                     __builtin_amdgcn_update_dpp(0u, v.y, 0x128, 0xF, 0xF, false),
+                                     __builtin_amdgcn_update_dpp(0u, v.z, 0x128, 0xF, 0xF, false),
+                                     __builtin_amdgcn_update_dpp(0u, v.w, 0x128, 0xF, 0xF, false));
+            }
+        }
+    };
+    auto load_frag = [&](uint4 (&f)[4][EA], int g) {
+        const int f_soff = (int)(((unsigned)mt * G + g) * 16u * EPB * 16u);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < EA; e++)
+                f[t][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        fr, (int)(f_voff + 16u * e), f_soff + t * 4 * EPB * 16, 0));
+    };
     // item (tile tl, slot gi) of this wave -> ring slot p
     auto load_item = [&](int p, int tl, int gi) {
         const int g = max(min(wid + NW * gi, glast), 0);
@@ -118,63 +181,79 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             wv[p][4 * q + 3] = v[3];
         }
         if (FMT == WF_INT4) szv[p] = __builtin_amdgcn_raw_buffer_load_b32(zr, (int)z_voff, (int)(tile * 64u), 0);
-        const int f_soff = (int)(((unsigned)mt * G + g) * 16u * EPB * 16u);
+        if constexpr (!REG) load_frag(av[p], g);
+    };
+    // one item: weights of ring slot p times fragment entries f, added to acc
+    auto mma_item = [&](float4_t& acc, int p, const uint4 (&f)[4][EA]) {
+        if (FMT == WF_INT4) {
+            const uint32_t szw = szv[p];
+            const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
+            half2_t zl2, zh2;
+            int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2, zh2);
+            float4_t g4[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two independent chains
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++) {
+                const half8_t b = int4_b_operand(wv[p][t], zl2, zh2);
 #pragma unroll
-            for (int e = 0; e < EA; e++)
-                av[p][t][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             fr, (int)(f_voff + 16u * e), f_soff + t * 4 * EPB * 16, 0));
+                for (int e = 0; e < EA; e++)
+                    g4[(t + e) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, f[t][e]), b,
+                                                                             g4[(t + e) & 1], 0, 0, 0);
+            }
+            acc += sc * (g4[0] + g4[1]);
+        } else if (FMT == WF_INT8) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const half8_t b = int8_b_operand(wv[p][2 * t], wv[p][2 * t + 1]);
+#pragma unroll
+                for (int e = 0; e < EA; e++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, f[t][e]), b, acc, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const u32x4_t w4 = {wv[p][4 * t], wv[p][4 * t + 1], wv[p][4 * t + 2], wv[p][4 * t + 3]};
+                const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
+#pragma unroll
+                for (int e = 0; e < EA; e++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f[t][e]), b, acc, 0, 0, 0);
+            }
+        }
     };
 #pragma unroll
     for (int p = 0; p < PF; p++) load_item(p, 0, p);
+    if constexpr (REG) {
+#pragma unroll
+        for (int gi = 0; gi < NGP; gi++) load_frag_reg(fa[gi], max(min(wid + NW * gi, glast), 0));
+    }
 
     for (int tl = 0; tl < nmine; tl++) {
         float4_t acc = {0.f, 0.f, 0.f, 0.f};
-        for (int gi0 = 0; gi0 < ngp; gi0 += PF) {
-            // items PF ahead: same tile, or the first slots of the next one (last tile: clamped)
-            const bool wrap = gi0 + PF >= ngp;
-            const int rtl = wrap ? min(tl + 1, nmine - 1) : tl;
-            const int rgi0 = wrap ? 0 : gi0 + PF;
+        if constexpr (REG) {
+            const int ntl = min(tl + 1, nmine - 1);
 #pragma unroll
-            for (int p = 0; p < PF; p++) {
-                const int gi = gi0 + p;
+            for (int gi = 0; gi < NGP; gi++) {
                 if (wid + NW * gi < G) {
-                    if (FMT == WF_INT4) {
-                        const uint32_t szw = szv[p];
-                        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
-                        half2_t zl2, zh2;
-                        int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2, zh2);
-                        float4_t g4[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two independent chains
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            const half8_t b = int4_b_operand(wv[p][t], zl2, zh2);
-#pragma unroll
-                            for (int e = 0; e < EA; e++)
-                                g4[(t + e) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                    __builtin_bit_cast(half8_t, av[p][t][e]), b, g4[(t + e) & 1], 0, 0, 0);
-                        }
-                        acc += sc * (g4[0] + g4[1]);
-                    } else if (FMT == WF_INT8) {
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            const half8_t b = int8_b_operand(wv[p][2 * t], wv[p][2 * t + 1]);
-#pragma unroll
-                            for (int e = 0; e < EA; e++)
-                                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av[p][t][e]), b, acc, 0, 0, 0);
-                        }
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            const u32x4_t w4 = {wv[p][4 * t], wv[p][4 * t + 1], wv[p][4 * t + 2], wv[p][4 * t + 3]};
-                            const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
-#pragma unroll
-                            for (int e = 0; e < EA; e++)
-                                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[p][t][e]), b, acc, 0, 0, 0);
-                        }
-                    }
+                    uint4 f[4][EA];
+                    unpack_frag(fa[gi], f);
+                    mma_item(acc, gi % PF, f);
                 }
-                load_item(p, rtl, rgi0 + p);
+                // the slot's next item: PF further in this tile, or the head of the next one
+                if (gi + PF < NGP)
+                    load_item(gi % PF, tl, gi + PF);
+                else
+                    load_item(gi % PF, ntl, gi + PF - NGP);
+            }
+        } else {
+            for (int gi0 = 0; gi0 < ngp; gi0 += PF) {
+                // items PF ahead: same tile, or the first slots of the next one (last tile: clamped)
+                const bool wrap = gi0 + PF >= ngp;
+                const int rtl = wrap ? min(tl + 1, nmine - 1) : tl;
+                const int rgi0 = wrap ? 0 : gi0 + PF;
+#pragma unroll
+                for (int p = 0; p < PF; p++) {
+                    if (wid + NW * (gi0 + p) < G) mma_item(acc, p, av[p]);
+                    load_item(p, rtl, rgi0 + p);
+                }
             }
         }
         // ---- end of tile tl: partial -> slot, the last wave reduces + epilogue ----
@@ -219,14 +298,6 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (EPI == EPI_STORE && a.hidden_out && nt == 0) {
-                // final normed hidden state (model.rs:579-585), written once by tile 0
-                for (int idx = lane; idx < Mc * a.K; idx += 64) {
-                    const int m = idx / a.K, k = idx - m * a.K;
-                    const float v = a.x[row_off(a.xmap, a.m_base + m) + k];
-                    a.hidden_out[(size_t)(a.m_base + m) * a.K + k] = v * s_inv[m] * a.norm_w[k];
-                }
-            }
             run_epilogue<EPI>(a, yt, nt, Mc, a.m_base, lane, 64, true);
             if (lane == 0) {
                 __hip_atomic_store(&cnt_s[ps], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -308,30 +379,52 @@ __global__ void __launch_bounds__(GT_THREADS) gemv_f32_kernel(GemvArgs a) {
     }
 }
 
-template <int FMT, int MP, int EPI>
+template <int FMT, int MP, int EPI, int NGP>
 static int launch_tile(const GemvArgs& a, hipStream_t stream) {
     static int grid_cap = 0;
     if (!grid_cap) {
         int dev = 0, cus = 0, per_cu = 0;
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemv_tile_kernel<FMT, MP, EPI>,
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemv_tile_kernel<FMT, MP, EPI, NGP>,
                                                            GT_NW * 64, 0);
         grid_cap = std::max(1, cus) * std::max(1, per_cu);
     }
     const int grid = std::min(a.N / 16, grid_cap);
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemv_tile_kernel<FMT, MP, EPI>), dim3(grid), dim3(GT_NW * 64), 0, stream, a);
+    hipLaunchKernelGGL((gemv_tile_kernel<FMT, MP, EPI, NGP>), dim3(grid), dim3(GT_NW * 64), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Items per tile per wave for the register-fragment path: ceil(G / NW) groups
+// rounded up to whole rings, while the fragments fit without spilling (8 VGPRs
+// per group at MP 4, up to 12 groups; 16 at MP 8, up to 8 groups); 0 otherwise.
+static int reg_items(const GemvArgs& a) {
+    if (a.mp > 8) return 0;
+    const int per_wave = ((a.K >> 7) + GT_NW - 1) / GT_NW;
+    const int ngp = (per_wave + GT_PF - 1) / GT_PF * GT_PF;
+    return ngp <= (a.mp == 4 ? 12 : 8) ? ngp : 0;
+}
+
+template <int FMT, int MP, int EPI>
+static int launch_ngp(const GemvArgs& a, hipStream_t stream) {
+    if constexpr (MP <= 8) {
+        const int n = reg_items(a);
+        if (n == 4) return launch_tile<FMT, MP, EPI, 4>(a, stream);
+        if (n == 8) return launch_tile<FMT, MP, EPI, 8>(a, stream);
+        if constexpr (MP == 4)
+            if (n == 12) return launch_tile<FMT, MP, EPI, 12>(a, stream);
+    }
+    return launch_tile<FMT, MP, EPI, 0>(a, stream);
 }
 
 template <int FMT, int MP>
 static int launch_epi(const GemvArgs& a, hipStream_t stream) {
     switch (a.epi) {
-        case EPI_STORE: return launch_tile<FMT, MP, EPI_STORE>(a, stream);
-        case EPI_RESID: return launch_tile<FMT, MP, EPI_RESID>(a, stream);
-        case EPI_SWIGLU: return launch_tile<FMT, MP, EPI_SWIGLU>(a, stream);
-        default: return launch_tile<FMT, MP, EPI_QKV>(a, stream);
+        case EPI_STORE: return launch_ngp<FMT, MP, EPI_STORE>(a, stream);
+        case EPI_RESID: return launch_ngp<FMT, MP, EPI_RESID>(a, stream);
+        case EPI_SWIGLU: return launch_ngp<FMT, MP, EPI_SWIGLU>(a, stream);
+        default: return launch_ngp<FMT, MP, EPI_QKV>(a, stream);
     }
 }
 
@@ -346,6 +439,9 @@ int launch_gemv(const GemvArgs& a, hipStream_t stream) {
     if (a.N % 16 || a.K % 128 || a.M <= 0 || a.M > GT_MROWS) return 2;
     if (a.fmt != WF_F32 && (!a.xf || (a.mp != 4 && a.mp != 8 && a.mp != 16) || a.M > a.mp || (a.m_base & 15) ||
                             (a.norm_w && !a.ssq_in)))
+        return 2;
+    if (a.hidden_out && (!a.norm_w || (a.xmap.seq_stride & 3) || (a.xmap.row_stride & 3) || ((uintptr_t)a.x & 15) ||
+                         ((uintptr_t)a.hidden_out & 15)))
         return 2;
     if (a.fmt == WF_F32) {
         (void)hipGetLastError();

@@ -153,3 +153,24 @@ def test_long_context_verify_over_synthetic_cache(kvfmt):
         assert rel_rows(gl[b], wl).max() < TOL, (b, rel_rows(gl[b], wl).max())
         assert rel_rows(gh[b], wh).max() < TOL
     hip.close()
+
+
+@pytest.mark.parametrize("ffn", [5632, 11008])
+@pytest.mark.parametrize("wfmt", [A.W_INT4_G128, A.W_INT8_ROW])
+def test_wide_ffn_register_fragment_paths(ffn, wfmt):
+    """Down projections with K = 5632 / 11008 fed 6, 4 and 1 rows: the GEMV
+    variants holding 8 and 12 groups of activation fragments per wave in
+    registers (and the L2-fragment variant at 6 rows with K = 11008)."""
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=ffn, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=64,
+              weight_format=wfmt, kv_format=A.KV_F16, lm_head_format=1)
+    ref, hip = make_pair(seed=9, max_batch=1, max_rows=16, **kw)
+    ids = R.synth_tokens(9, 0, 11, 1024)
+    kv = ref.kv(64)
+    pos = 0
+    for n in (6, 4, 1):
+        wl, wh = kv.forward(ids[pos:pos + n], pos)
+        gl, gh = hip.forward_with_cache_output(ids[None, pos:pos + n], [pos])
+        assert rel_rows(gl[0], wl).max() < TOL, (n, rel_rows(gl[0], wl).max())
+        assert rel_rows(gh[0], wh).max() < TOL, (n, rel_rows(gh[0], wh).max())
+        pos += n
+    hip.close()
