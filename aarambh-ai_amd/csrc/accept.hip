@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wid = tid >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rows_per_seq = a.target_rows + a.K;
     const int b = blockIdx.x / rows_per_seq;
     const int r = blockIdx.x % rows_per_seq;

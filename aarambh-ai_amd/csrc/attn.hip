@@ -35,7 +35,7 @@ static constexpr int AT_MAXHD = 128;
 __device__ void append_new_kv(const AttnArgs& a, int seq, int kvh, size_t hb, int pos0, int t_begin, int t_end) {
     const int lo = max(t_begin, pos0);
     if (lo >= t_end) return;  // uniform over the workgroup
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const int hd = a.hd, KD = a.n_kv * hd;
     for (int t = lo + wid; t < t_end; t += nw) {
         const size_t row = (size_t)seq * a.S + (t - pos0);
@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
     __shared__ float ps[AT_MAXR][AT_TOK];
     __shared__ unsigned s_last;
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hd = a.hd, G = a.n_heads / a.n_kv;
     const int R_total = a.S * G;
     int bid = blockIdx.x;
@@ -392,7 +392,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     __shared__ float mg_m[AM_WAVES][AM_ROWS], mg_l[AM_WAVES][AM_ROWS];
     __shared__ unsigned s_last;
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int G = a.n_heads / a.n_kv;
     const int R_total = a.S * G;

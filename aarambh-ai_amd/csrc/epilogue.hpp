@@ -122,7 +122,7 @@ __device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc,
                 float ss = 0.f;
 #pragma unroll
                 for (int n = 0; n < 16; n++) ss += yt[tid][n] * yt[tid][n];
-                a.fo.ssq[(size_t)nt * a.fo.ssq_rows + mbase + tid] = ss;
+                a.fo.ssq[(size_t)(mbase + tid) * a.fo.ssq_ld + nt] = ss;
             }
         }
     } else if (EPI == EPI_SWIGLU) {

@@ -8,8 +8,8 @@ namespace aarh {
 // Store element (m, c) of an activation matrix (value x before the consumer's
 // norm weight) into its fragment entries.  Rows past f.mp of a chunk with
 // mp <= 8 are never consumed and are not written.
-__device__ __forceinline__ void frag_put(const XFrag& f, int m, int c, float x) {
-    const float v = f.norm_w ? x * f.norm_w[c] : x;
+// v = x * norm_w[c] already applied.
+__device__ __forceinline__ void frag_put_w(const XFrag& f, int m, int c, float v) {
     uint16_t hi, lo;
     if (f.fmt == WF_BF16) {
         hi = f32_to_bf16_rne(v);
@@ -24,9 +24,13 @@ __device__ __forceinline__ void frag_put(const XFrag& f, int m, int c, float x) 
     const int g = c >> 7, lg = (c >> 5) & 3, t = (c >> 3) & 3, j = frag_slot(f.fmt, c & 7);
     const int epb = frag_epb(f.mp);
     const size_t base = ((((size_t)mt * f.G + g) * 4 + t) * 4 + lg) * epb;
-    const int ehi = f.mp <= 8 ? r : 2 * r, elo = f.mp <= 8 ? f.mp + r : 2 * r + 1;
+    const int ehi = r, elo = f.mp <= 8 ? f.mp + r : 16 + r;
     f.buf[(base + ehi) * 8 + j] = hi;
     f.buf[(base + elo) * 8 + j] = lo;
+}
+
+__device__ __forceinline__ void frag_put(const XFrag& f, int m, int c, float x) {
+    frag_put_w(f, m, c, f.norm_w ? x * f.norm_w[c] : x);
 }
 
 }  // namespace aarh

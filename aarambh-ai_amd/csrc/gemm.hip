@@ -2,240 +2,545 @@
 // on gfx950.
 //
 // Replaces QatLinear::forward (quant/src/qat.rs:315-348) when the verify
-// forward carries many sequences: y = x . W^T with the weights read from HBM
-// once per 64 activation rows instead of once per 16.
+// forward carries many sequences: y = x . W^T over M = batch * (k+1) rows,
+// every projection of attention.rs:170-222, ffn.rs:29-37 and head.rs:47-49.
+// At M = 128 (batch 32, k = 3) an INT4 weight byte feeds 256 MACs, above the
+// MI355X ridge, so this kernel is MFMA-bound.  Activations arrive as hi + lo
+// fp16 (bf16 for BF16 weights) fragments written by their producer (mp = 16
+// layout: per (chunk, group, k-step, lane group) 16 hi entries then 16 lo);
+// INT4 / INT8 codes are exact in fp16, so products keep ~22 bits.
 //
-// Block = 64 weight rows (4 tiles of 16) x 64 activation rows (4 row chunks of
-// 16), 4 waves; wave w owns row chunk w against all 4 weight tiles, so one
-// activation fragment read from LDS feeds 4 MFMAs.  The activation fragments
-// (producer-written, hi + lo halves as two MFMAs) of each 128-column group are
-// copied to LDS one group ahead (double buffer); the weight tiles of the next
-// groups stream into a register ring.  Weights are dequantised in registers to
-// exact fp16 integers (INT4 q - z, INT8 code) or used as bf16; the INT4 group
-// scale multiplies the fp32 group accumulator.  Each wave then runs the fused
-// epilogue on its 16 rows of each tile.
+// Block: 8 waves = 2 (M) x 4 (N).  It covers MC = 2 * CPW row chunks (16 rows
+// each) x NT = 4 * TPW weight tiles (16 rows each) over a contiguous range of
+// 128-column groups (split-K).  Wave (wm, wn) owns CPW chunks x TPW tiles:
+// per group 8 * CPW * TPW MFMAs 16x16x32, with each INT4 weight word
+// dequantised once per wave for CPW chunks.
+//
+// Data movement: a ring of NS LDS stages, one 128-column group each, filled by
+// direct HBM/L2 -> LDS loads (buffer_load ... lds, no VGPRs): the activation
+// fragments of the block's chunks (8 KiB per chunk), the weight tiles and the
+// INT4 scale/zero words.  Every wave issues the same number of loads per
+// stage, so `s_waitcnt vmcnt(L * (NS - 1))` + a barrier publishes stage g
+// while stages g+1 .. g+NS-1 are in flight.  Each byte enters the CU once.
+//
+// Split-K partials go to scratch with coherent stores; the block that arrives
+// last at its (M-block, N-block) counter adds the S partials in split order
+// (deterministic) and runs the fused epilogue (store, residual add + next
+// fragments, SwiGLU, RoPE + Q/K/V rows) on each 16 x 16 tile.
 #include "epilogue.hpp"
 
 namespace aarh {
 
-static constexpr int GM_TILES = 4;  // weight tiles per block
-static constexpr int GM_CH = 4;     // 16-row activation chunks per block (one per wave)
+static constexpr int GM_WAVES = 8, GM_WM = 2, GM_WN = 4;
+static constexpr int GM_LDS_BUDGET = 150 * 1024;  // dynamic LDS for the stage ring
 
-template <int FMT, int EPI>
-__global__ void __launch_bounds__(256) gemm_kernel(GemvArgs a) {
+// One 1 KiB wave load straight into LDS: lane l's 16 bytes at rsrc + voff +
+// soff land at LDS address lds_base + 16 l (buffer_load_dwordx4 ... lds, base in
+// M0).  Written as inline asm so the compiler does not see an LDS write it would
+// guard with a conservative vmcnt(0) before every LDS read: the kernel counts
+// these loads itself.  M0 is restored before the statement ends.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const void* lds_dst, int voff, int soff) {
+    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+    int saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(voff), "s"(r), "s"(soff)
+        : "memory");
+}
+
+template <int FMT, int CPW>
+struct GmCfg {
     typedef FmtTraits<FMT> T;
-    constexpr int GM_PW = 16 / T::LANE_WORDS > 0 ? 16 / T::LANE_WORDS : 1;  // weight ring depth (groups)
-    constexpr int U = GM_PW > 2 ? GM_PW : 2;                                  // unroll: ring slots, x stages
-    constexpr int EPB = 32;                       // fragment entries per (g, t, lg) with 16-row tiles
-    constexpr int CHUNK_U4 = 4 * 4 * EPB;         // uint4 per (chunk, group) = 8 KiB
-    __shared__ uint4 xs[2][GM_CH][CHUNK_U4];      // 64 KiB: two groups of activation fragments
-    __shared__ float yt_s[GM_CH][16][17];
-    __shared__ float s_inv[GM_CH * 16];
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    static constexpr int TPW = FMT == WF_BF16 ? 2 : 4;              // weight tiles per wave
+    static constexpr int NT = GM_WN * TPW;                          // weight tiles per block
+    static constexpr int MC = GM_WM * CPW;                          // row chunks per block
+    static constexpr int A_BYTES = MC * 8192;                       // hi + lo fragments of one group
+    static constexpr int W_BYTES = NT * T::TILE_BYTES;
+    static constexpr int Z_BYTES = FMT == WF_INT4 ? NT * 64 : 0;
+    static constexpr int STAGE = A_BYTES + W_BYTES + Z_BYTES;
+    static constexpr int NS_RAW = GM_LDS_BUDGET / STAGE;
+    static constexpr int NS = NS_RAW < 2 ? 2 : (NS_RAW > 4 ? 4 : NS_RAW);
+    static constexpr int A_PW = MC * 8 / GM_WAVES;                  // 1 KiB activation pieces per wave
+    static constexpr int W_PW = W_BYTES / 1024 / GM_WAVES;          // 1 KiB weight pieces per wave
+    static constexpr int L = A_PW + W_PW + (FMT == WF_INT4 ? 1 : 0);  // loads per wave per stage
+    static_assert(MC * 8 % GM_WAVES == 0 && W_BYTES % (1024 * GM_WAVES) == 0, "stage pieces split over waves");
+    static_assert(Z_BYTES <= 1024, "scale/zero words of a stage: one 64-lane load");
+    static_assert(NS * STAGE <= GM_LDS_BUDGET, "stage ring exceeds LDS");
+};
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14), other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int FMT, int EPI, int CPW>
+__global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, int gps) {
+    typedef FmtTraits<FMT> T;
+    typedef GmCfg<FMT, CPW> C;
+    constexpr int TPW = C::TPW, NT = C::NT, MC = C::MC, NS = C::NS, LW = T::LANE_WORDS;
+    extern __shared__ __attribute__((aligned(1024))) char lds[];
+    __shared__ float s_inv[MC * 16];
+    __shared__ unsigned s_flag;
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
+    const int wm = wid / GM_WN, wn = wid % GM_WN;
     const int G = a.K >> 7;
     const int ntiles = a.N >> 4;
-    const int nchunks = (a.ssq_rows + 15) >> 4;   // fragment chunks allocated (rows of the buffers)
-    const int bn = blockIdx.x, bm = blockIdx.y;
-    const int nt0 = bn * GM_TILES;
-    const int mt0 = bm * GM_CH;
-    const int row0 = mt0 * 16;
+    const int NB = (ntiles + NT - 1) / NT;
+    const int nchunks = (a.M + 15) >> 4;
+    int bid = blockIdx.x;
+    const int s = bid % S;
+    bid /= S;
+    const int nb = bid % NB, mb = bid / NB;
+    const int g0 = s * gps, ng = min(G, g0 + gps) - g0;
 
-    // ---- 1/rms of the block's rows from the producer's 16-column partial sums ----
-    if (a.norm_w) {
-        for (int r = wid; r < GM_CH * 16; r += 4) {
-            const int m = row0 + r;
-            float ss = 0.f;
-            if (m < a.M)
-                for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)q * a.ssq_rows + m];
+    // 1/rms of the block's rows from the producer's 16-column partial sums (same
+    // summation order as the GEMV kernel)
+    // wave w takes rows w, w + 8, ...; the partials of all its rows are loaded
+    // before any is summed (4 per row per lane per round trip).
+    auto compute_inv = [&]() {
+        constexpr int RPW = MC * 16 / GM_WAVES;
+        const int nq = a.K >> 4;
+        float ss[RPW];
+        int mrow[RPW];
 #pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
-            if (lane == 0) s_inv[r] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+        for (int k = 0; k < RPW; k++) {
+            ss[k] = 0.f;
+            mrow[k] = min(mb * MC * 16 + wid + GM_WAVES * k, a.M - 1);
+        }
+        for (int q0 = lane; q0 < nq; q0 += 256) {
+            float v[RPW][4];
+#pragma unroll
+            for (int k = 0; k < RPW; k++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[k][u] = a.ssq_in[(size_t)mrow[k] * a.ssq_ld + min(q0 + 64 * u, nq - 1)];
+#pragma unroll
+            for (int k = 0; k < RPW; k++)
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (q0 + 64 * u < nq) ss[k] += v[k][u];
+        }
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            float t = ss[k];
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+            if (lane == 0) s_inv[wid + GM_WAVES * k] = 1.0f / sqrtf(t / (float)a.K + a.eps);
+        }
+        __syncthreads();
+    };
+
+    if (EPI == EPI_STORE && a.hidden_out) {
+        // final normed hidden state (model.rs:579-585): the NB * S blocks of this
+        // M-block each write a slice of columns of its rows
+        compute_inv();
+        const int nq = NB * S, q = nb * S + s;
+        const int cw = ((a.K + nq - 1) / nq + 3) & ~3;
+        const int k0 = q * cw, kn = max(0, min(cw, a.K - k0));
+        const int rows = min(MC * 16, a.M - mb * MC * 16);
+        for (int idx = tid; idx < rows * (kn >> 2); idx += GM_WAVES * 64) {
+            const int r = idx / (kn >> 2), k = k0 + 4 * (idx - r * (kn >> 2));
+            const int m = mb * MC * 16 + r;
+            const float4 v = *(const float4*)(a.x + row_off(a.xmap, m) + k);
+            const float4 w = *(const float4*)(a.norm_w + k);
+            const float si = s_inv[r];
+            *(float4*)(a.hidden_out + (size_t)m * a.K + k) =
+                make_float4(v.x * si * w.x, v.y * si * w.y, v.z * si * w.z, v.w * si * w.w);
         }
     }
 
-    // ---- activation fragments of group g -> register stage (thread t copies 8 uint4) ----
-    const __amdgpu_buffer_rsrc_t fr = coh_rsrc(a.xf), wr = coh_rsrc(a.w), zr = coh_rsrc(a.sz);
-    // uint4 u of thread t: chunk u / 2 (uniform), entry t + 256 * (u % 2) of that chunk
-    static_assert(CHUNK_U4 == 512, "two 256-thread passes per chunk");
-    uint4 xstage[2][8];
-    const unsigned x_voff = (unsigned)tid * 16u;
-    auto load_x = [&](int st, int g) {
-        g = min(g, G - 1);
+    // ---- stage loads: this wave's pieces of group g into ring slot st ----
+    const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
+    constexpr int WP = T::TILE_BYTES / 1024;  // 1 KiB pieces per tile
+    const int z_tile = min(nb * NT + (lane >> 2), ntiles - 1);
+    auto issue_stage = [&](int st, int g) {
+        char* base = lds + st * C::STAGE;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int mt = min(mt0 + (u >> 1), nchunks - 1);
-            const int soff = ((mt * G + g) * CHUNK_U4 + 256 * (u & 1)) * 16;
-            xstage[st][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(fr, (int)x_voff, soff, 0));
+        for (int q = 0; q < C::A_PW; q++) {
+            const int pi = wid * C::A_PW + q, cc = pi >> 3, sub = pi & 7;  // block chunk, 1 KiB piece
+            const int mt = min(mb * MC + cc, nchunks - 1);
+            lds_dma16(fr, base + cc * 8192 + sub * 1024, lane * 16 + sub * 1024, (mt * G + g) * 8192);
         }
-    };
-    auto store_x = [&](int st, int buf) {
+        // tile jj, piece sub: every lane's sub-th 16 bytes (lane l owns TILE_BYTES / 64
+        // bytes of the tile), so the wave reading piece sub from LDS is conflict-free
 #pragma unroll
-        for (int u = 0; u < 8; u++) xs[buf][u >> 1][tid + 256 * (u & 1)] = xstage[st][u];
+        for (int q = 0; q < C::W_PW; q++) {
+            const int pi = wid * C::W_PW + q, jj = pi / WP, sub = pi % WP;
+            const int nt = min(nb * NT + jj, ntiles - 1);
+            lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * (16 * WP) + sub * 16,
+                      (int)(((unsigned)nt * G + g) * T::TILE_BYTES));
+        }
+        if (FMT == WF_INT4)
+            lds_dma16(zr, base + C::A_BYTES + C::W_BYTES, (int)(((unsigned)z_tile * G + g) * 64u + (lane & 3) * 16u), 0);
     };
 
-    // ---- weight ring: GM_PW groups x 4 tiles ----
-    const unsigned w_voff = (unsigned)lane * T::LANE_WORDS * 4u;
-    uint32_t wv[GM_PW][GM_TILES][T::LANE_WORDS];
-    uint32_t szv[GM_PW][GM_TILES];
-    auto load_w = [&](int p, int g) {
-        g = min(g, G - 1);
+    float4_t acc[CPW][TPW];
 #pragma unroll
-        for (int j = 0; j < GM_TILES; j++) {
-            const int nt = min(nt0 + j, ntiles - 1);
-            const unsigned tile = (unsigned)nt * G + g;
+    for (int c = 0; c < CPW; c++)
 #pragma unroll
-            for (int q = 0; q < T::LANE_WORDS / 4; q++) {
-                const u32x4_t v = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(w_voff + 16u * q), (int)(tile * T::TILE_BYTES), 2));
-                wv[p][j][4 * q + 0] = v[0];
-                wv[p][j][4 * q + 1] = v[1];
-                wv[p][j][4 * q + 2] = v[2];
-                wv[p][j][4 * q + 3] = v[3];
+        for (int j = 0; j < TPW; j++) acc[c][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+    // ---- one group from ring slot st ----
+    auto compute_stage = [&](int st) {
+        const char* base = lds + st * C::STAGE;
+        uint4 ah[CPW][4], al[CPW][4];
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint4* e = (const uint4*)(base + ((((wm * CPW + c) * 4 + t) * 4 + lg) * 32) * 16);
+                ah[c][t] = e[lr];
+                al[c][t] = e[16 + lr];
             }
-            if (FMT == WF_INT4) szv[p][j] = __builtin_amdgcn_raw_buffer_load_b32(zr, (int)(lr * 4), (int)(tile * 64u), 0);
+        uint32_t wv[TPW][LW];
+#pragma unroll
+        for (int j = 0; j < TPW; j++) {
+            const char* w = base + C::A_BYTES + (wn * TPW + j) * T::TILE_BYTES;
+#pragma unroll
+            for (int q = 0; q < LW / 4; q++) {
+                const uint4 v = ((const uint4*)(w + q * 1024))[lane];
+                wv[j][4 * q + 0] = v.x;
+                wv[j][4 * q + 1] = v.y;
+                wv[j][4 * q + 2] = v.z;
+                wv[j][4 * q + 3] = v.w;
+            }
         }
-    };
-
+        if (FMT == WF_INT4) {
+            half2_t zl2[TPW], zh2[TPW];
+            float sc[TPW];
 #pragma unroll
-    for (int p = 0; p < GM_PW; p++) load_w(p, p);
-    // group g: loaded into stage g % 2 two groups ahead, copied to LDS buffer g % 2 one group ahead
-    load_x(0, 0);
-    load_x(1, 1);
-    store_x(0, 0);
-    __syncthreads();
-
-    float4_t acc[GM_TILES], accl[GM_TILES];  // accl: lo-half products (INT8 / BF16)
+            for (int j = 0; j < TPW; j++) {
+                const uint32_t szw = ((const uint32_t*)(base + C::A_BYTES + C::W_BYTES))[(wn * TPW + j) * 16 + lr];
+                sc[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
+                int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2[j], zh2[j]);
+            }
+            float4_t ga[CPW][TPW];
 #pragma unroll
-    for (int j = 0; j < GM_TILES; j++) acc[j] = accl[j] = (float4_t){0.f, 0.f, 0.f, 0.f};
-
-    for (int g0 = 0; g0 < G; g0 += U) {
+            for (int c = 0; c < CPW; c++)
 #pragma unroll
-        for (int p = 0; p < U; p++) {
-            const int g = g0 + p;
-            const int buf = p & 1;  // == g & 1 (U even)
-            const int wp = p % GM_PW;
-            if (g < G) {
-                // stage `buf` (group g) is already in LDS: reuse it for group g + 2
-                if (g + 2 < G) load_x(buf, g + 2);
-                // A operands of this wave's chunk: 4 k-steps x (hi, lo)
-                uint4 af[4][2];
+                for (int j = 0; j < TPW; j++) ga[c][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int e = (t * 4 + lg) * EPB + 2 * lr;
-                    af[t][0] = xs[buf][wid][e];
-                    af[t][1] = xs[buf][wid][e + 1];
-                }
-                // k-step outer, tiles inner, hi and lo into separate accumulators: eight
-                // independent MFMA chains keep the matrix pipe busy
-                if (FMT == WF_INT4) {
-                    half2_t zl2[GM_TILES], zh2[GM_TILES];
-                    float sc[GM_TILES];
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-                    for (int j = 0; j < GM_TILES; j++) {
-                        const uint32_t szw = szv[wp][j];
-                        sc[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
-                        int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2[j], zh2[j]);
+                for (int j = 0; j < TPW; j++) {
+                    const half8_t b = int4_b_operand(wv[j][t], zl2[j], zh2[j]);
+#pragma unroll
+                    for (int c = 0; c < CPW; c++) {
+                        ga[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ah[c][t]), b,
+                                                                          ga[c][j], 0, 0, 0);
+                        ga[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, al[c][t]), b,
+                                                                          ga[c][j], 0, 0, 0);
                     }
-                    float4_t gh[GM_TILES], gl[GM_TILES];
-#pragma unroll
-                    for (int j = 0; j < GM_TILES; j++) gh[j] = gl[j] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-#pragma unroll
-                        for (int j = 0; j < GM_TILES; j++) {
-                            const half8_t b = int4_b_operand(wv[wp][j][t], zl2[j], zh2[j]);
-                            gh[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[t][0]), b, gh[j], 0, 0, 0);
-                            gl[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[t][1]), b, gl[j], 0, 0, 0);
-                        }
-#pragma unroll
-                    for (int j = 0; j < GM_TILES; j++) acc[j] += sc[j] * (gh[j] + gl[j]);
-                } else if (FMT == WF_INT8) {
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-#pragma unroll
-                        for (int j = 0; j < GM_TILES; j++) {
-                            const half8_t b = int8_b_operand(wv[wp][j][2 * t], wv[wp][j][2 * t + 1]);
-                            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[t][0]), b, acc[j], 0, 0, 0);
-                            accl[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[t][1]), b, accl[j], 0, 0, 0);
-                        }
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-#pragma unroll
-                        for (int j = 0; j < GM_TILES; j++) {
-                            const u32x4_t w4 = {wv[wp][j][4 * t], wv[wp][j][4 * t + 1], wv[wp][j][4 * t + 2], wv[wp][j][4 * t + 3]};
-                            const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
-                            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[t][0]), b, acc[j], 0, 0, 0);
-                            accl[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[t][1]), b, accl[j], 0, 0, 0);
-                        }
                 }
-                load_w(wp, g + GM_PW);
-                // group g + 1 (loaded one iteration ago) -> the other LDS buffer, read after the barrier
-                if (g + 1 < G) store_x(buf ^ 1, buf ^ 1);
-                __syncthreads();
+#pragma unroll
+            for (int c = 0; c < CPW; c++)
+#pragma unroll
+                for (int j = 0; j < TPW; j++) acc[c][j] += sc[j] * ga[c][j];
+        } else if (FMT == WF_INT8) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int j = 0; j < TPW; j++) {
+                    const half8_t b = int8_b_operand(wv[j][2 * t], wv[j][2 * t + 1]);
+#pragma unroll
+                    for (int c = 0; c < CPW; c++) {
+                        acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ah[c][t]), b,
+                                                                           acc[c][j], 0, 0, 0);
+                        acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, al[c][t]), b,
+                                                                           acc[c][j], 0, 0, 0);
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int j = 0; j < TPW; j++) {
+                    const u32x4_t w4 = {wv[j][4 * t], wv[j][4 * t + 1], wv[j][4 * t + 2], wv[j][4 * t + 3]};
+                    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
+#pragma unroll
+                    for (int c = 0; c < CPW; c++) {
+                        acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ah[c][t]), b,
+                                                                            acc[c][j], 0, 0, 0);
+                        acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, al[c][t]), b,
+                                                                            acc[c][j], 0, 0, 0);
+                    }
+                }
+        }
+    };
+
+    // ---- pipeline: NS - 1 stages in flight ahead of the one computed ----
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) issue_stage(i, g0 + min(i, ng - 1));
+    for (int gi = 0; gi < ng; gi++) {
+        issue_stage((gi + NS - 1) % NS, g0 + min(gi + NS - 1, ng - 1));  // past the end: harmless repeats
+        wait_vmcnt<C::L * (NS - 1)>();
+        __syncthreads();
+        compute_stage(gi % NS);
+        __syncthreads();
+    }
+    wait_vmcnt<0>();
+
+    if (S > 1) {
+        // ---- split-K: partial tiles out, the last block of the (mb, nb) pair adds them in order ----
+        const size_t unit = (size_t)mb * NB + nb;
+        const __amdgpu_buffer_rsrc_t pr = coh_rsrc(a.gpart + unit * S * (MC * NT * 256));
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++) {
+                const unsigned o = ((unsigned)(s * MC * NT + (wm * CPW + c) * NT + wn * TPW + j) * 64u + lane) * 16u;
+                st4_coh(pr, o, acc[c][j]);
             }
+        if (!arrive_last(a.gcnt + unit, (unsigned)S, &s_flag)) return;
+        // the wave's CPW * TPW tiles x 4 splits in flight per round trip, added in split order
+        const unsigned step = (unsigned)(MC * NT) * 1024u;
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++) acc[c][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += 4) {
+            float4_t v[CPW][TPW][4];
+#pragma unroll
+            for (int c = 0; c < CPW; c++)
+#pragma unroll
+                for (int j = 0; j < TPW; j++) {
+                    const unsigned o0 = ((unsigned)((wm * CPW + c) * NT + wn * TPW + j) * 64u + lane) * 16u;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[c][j][i] = ld4_coh(pr, o0 + step * (unsigned)min(s0 + i, S - 1));
+                }
+#pragma unroll
+            for (int c = 0; c < CPW; c++)
+#pragma unroll
+                for (int j = 0; j < TPW; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (s0 + i < S) acc[c][j] += v[c][j][i];
         }
     }
 
-    if (FMT != WF_INT4)
+    // ---- epilogue in the MFMA layout: lane (lr, lg) of tile (c, j) holds rows
+    //      4 lg + i of chunk c for weight row lr of tile j.  Every global input of
+    //      the epilogue is loaded for all of the wave's tiles before one is used.
+    int mrw[CPW][4];  // activation row, clamped into range
+    bool rok[CPW][4];
 #pragma unroll
-        for (int j = 0; j < GM_TILES; j++) acc[j] += accl[j];
-    // ---- epilogue: wave w, row chunk mt0 + w, each of the 4 tiles ----
-    const int mrow = row0 + wid * 16;
-    const int Mc = min(16, a.M - mrow);
-    if (Mc <= 0) return;
-    float (*yt)[17] = yt_s[wid];
-#pragma unroll
-    for (int j = 0; j < GM_TILES; j++) {
-        const int nt = nt0 + j;
-        if (nt >= ntiles) break;
+    for (int c = 0; c < CPW; c++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int r = 4 * lg + i;
-            float v = acc[j][i];
-            if (a.norm_w) v *= s_inv[wid * 16 + r];
-            if (FMT == WF_INT8) v *= a.rscale[nt * 16 + lr];
-            yt[r][lr] = v;
+            const int chunk = mb * MC + wm * CPW + c, m = chunk * 16 + 4 * lg + i;
+            rok[c][i] = chunk < nchunks && m < a.M;
+            mrw[c][i] = min(m, a.M - 1);
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (EPI == EPI_STORE && a.hidden_out && nt == 0) {
-            // final normed hidden state (model.rs:579-585), written by the blocks of tile 0
-            for (int idx = lane; idx < Mc * a.K; idx += 64) {
-                const int m = idx / a.K, k = idx - m * a.K;
-                const float xv = a.x[row_off(a.xmap, mrow + m) + k];
-                a.hidden_out[(size_t)(mrow + m) * a.K + k] = xv * s_inv[wid * 16 + m] * a.norm_w[k];
+    int ntv[TPW];
+    bool tok[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int nt = nb * NT + wn * TPW + j;
+        tok[j] = nt < ntiles;
+        ntv[j] = min(nt, ntiles - 1);
+    }
+    float rs[TPW];
+    if (FMT == WF_INT8)
+#pragma unroll
+        for (int j = 0; j < TPW; j++) rs[j] = a.rscale[ntv[j] * 16 + lr];
+    float xo[CPW][TPW][4], nw[TPW];
+    if (EPI == EPI_RESID) {
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) xo[c][j][i] = a.resid[(size_t)mrw[c][i] * a.ldr + ntv[j] * 16 + lr];
+#pragma unroll
+        for (int j = 0; j < TPW; j++) nw[j] = a.fo.norm_w ? a.fo.norm_w[ntv[j] * 16 + lr] : 1.0f;
+    }
+    int pos[CPW][4];
+    if (EPI == EPI_QKV)
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pos[c][i] = a.qkv.pos0[mrw[c][i] / a.qkv.S] + mrw[c][i] % a.qkv.S;
+    if (a.norm_w && !(EPI == EPI_STORE && a.hidden_out)) compute_inv();
+#pragma unroll
+    for (int c = 0; c < CPW; c++)
+#pragma unroll
+        for (int j = 0; j < TPW; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = acc[c][j][i];
+                if (a.norm_w) v *= s_inv[(wm * CPW + c) * 16 + 4 * lg + i];
+                if (FMT == WF_INT8) v *= rs[j];
+                acc[c][j][i] = v;
+            }
+
+    if (EPI == EPI_STORE) {
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (rok[c][i] && tok[j]) a.out[row_off(a.omap, mrw[c][i]) + ntv[j] * 16 + lr] = acc[c][j][i];
+    } else if (EPI == EPI_RESID) {
+        // x += y; the new x as fragments for the next consumer and its 16-column sums of squares
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float xn = xo[c][j][i] + acc[c][j][i];
+                    const int m = mrw[c][i], col = ntv[j] * 16 + lr;
+                    if (rok[c][i] && tok[j]) {
+                        a.resid[(size_t)m * a.ldr + col] = xn;
+                        if (a.fo.buf) frag_put_w(a.fo, m, col, xn * nw[j]);
+                    }
+                    float sq = xn * xn;
+#pragma unroll
+                    for (int d = 8; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
+                    if (a.fo.ssq && lr == 0 && rok[c][i] && tok[j]) a.fo.ssq[(size_t)m * a.fo.ssq_ld + ntv[j]] = sq;
+                }
+    } else if (EPI == EPI_SWIGLU) {
+        // rows 0-7 of a tile are gate rows, 8-15 the matching up rows (ffn columns nt*8 + r)
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float u = __shfl_xor(acc[c][j][i], 8, 64);
+                    if (lr < 8 && rok[c][i] && tok[j]) {
+                        const float g = acc[c][j][i];
+                        const float silu = g / (1.0f + expf(-g));
+                        const float h = silu * u;
+                        const int m = mrw[c][i], col = ntv[j] * 8 + lr;
+                        a.out[row_off(a.omap, m) + col] = h;
+                        if (a.fo.buf) frag_put(a.fo, m, col, h);
+                    }
+                }
+    } else {
+        // QKV: a tile holds dims d = 8 jh + r (weight rows r < 8) and d + hd/2 (rows 8 + r) of one head
+        const QkvEpi& e = a.qkv;
+        const int hd = e.hd, half = hd >> 1;
+        const int QD = e.n_heads * hd, KD = e.n_kv * hd;
+        const int r = lr & 7;
+#pragma unroll
+        for (int j = 0; j < TPW; j++) {
+            const int row0 = ntv[j] * 16;
+            const int head = row0 / hd, jh = (row0 % hd) >> 4;
+            const bool is_q = row0 < QD, is_k = !is_q && row0 < QD + KD;
+            const int d1 = 8 * jh + r;
+#pragma unroll
+            for (int c = 0; c < CPW; c++) {
+                float cs[4], sn[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    cs[i] = e.rope_cos[(size_t)pos[c][i] * half + d1];
+                    sn[i] = e.rope_sin[(size_t)pos[c][i] * half + d1];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float mine = acc[c][j][i], other = __shfl_xor(mine, 8, 64);
+                    float y1 = lr < 8 ? mine : other, y2 = lr < 8 ? other : mine;
+                    if (is_q || is_k) {
+                        // RoPE (rope.rs:107-126): half-split rotation at the row's position
+#pragma clang fp contract(off)
+                        const float r1 = y1 * cs[i] - y2 * sn[i];
+                        const float r2 = y1 * sn[i] + y2 * cs[i];
+                        y1 = r1;
+                        y2 = r2;
+                    }
+                    const int mg = mrw[c][i];
+                    float* dst;
+                    if (is_q) dst = e.q_out + (size_t)mg * QD + head * hd;
+                    else if (is_k) dst = e.kv_out + (size_t)mg * 2 * KD + (head - e.n_heads) * hd;
+                    else dst = e.kv_out + (size_t)mg * 2 * KD + KD + (head - e.n_heads - e.n_kv) * hd;
+                    if (rok[c][i] && tok[j]) {
+                        if (lr < 8) dst[d1] = y1;
+                        else dst[d1 + half] = y2;
+                    }
+                }
             }
         }
-        run_epilogue<EPI>(a, yt, nt, Mc, mrow, lane, 64, true);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
 }
 
-template <int FMT, int EPI>
-static int launch_e(const GemvArgs& a, hipStream_t stream) {
-    const dim3 grid((a.N / 16 + GM_TILES - 1) / GM_TILES, (a.M + 16 * GM_CH - 1) / (16 * GM_CH));
+static int cu_count() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+template <int FMT, int EPI, int CPW>
+static int launch_w(const GemvArgs& a, hipStream_t stream) {
+    typedef GmCfg<FMT, CPW> C;
+    static bool attr = false;
+    const size_t lds_bytes = (size_t)C::NS * C::STAGE;
+    if (!attr) {
+        if (note_error(hipFuncSetAttribute((const void*)gemm_kernel<FMT, EPI, CPW>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes)))
+            return 4;
+        attr = true;
+    }
+    const int G = a.K >> 7;
+    const int NB = (a.N / 16 + C::NT - 1) / C::NT;
+    const int MB = ((a.M + 15) / 16 + C::MC - 1) / C::MC;
+    // Split-K only for the 32-row blocks of small-N projections, at most 4 ways:
+    // each extra split costs a 32 KiB partial round trip through memory, which
+    // measured slower than idle CUs beyond that.
+    int S = 1;
+    if (CPW == 1) {
+        const int units = NB * MB;
+        S = std::max(1, std::min(std::min(4, G / 2), cu_count() / std::max(units, 1)));
+        while (S > 1 && (long long)units * S * C::MC * C::NT * 256 > (a.gpart ? a.gpart_elems : 0)) S--;
+    }
+    const int gps = (G + S - 1) / S;
+    S = (G + gps - 1) / gps;  // every split non-empty
+    if (S > 1 && (!a.gcnt || NB * MB > 8192)) return 2;  // counters: 8192 per context
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemm_kernel<FMT, EPI>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<FMT, EPI, CPW>), dim3(NB * MB * S), dim3(GM_WAVES * 64), lds_bytes, stream, a, S,
+                       gps);
     return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// 64-row blocks (no split) when they already give half a dispatch round of
+// blocks, else 32-row blocks with split-K.
+template <int FMT, int EPI>
+static int launch_m(const GemvArgs& a, hipStream_t stream) {
+    typedef GmCfg<FMT, 2> C;
+    const int units64 = ((a.N / 16 + C::NT - 1) / C::NT) * (((a.M + 15) / 16 + C::MC - 1) / C::MC);
+    if (a.M > 32 && 2 * units64 >= cu_count()) return launch_w<FMT, EPI, 2>(a, stream);
+    return launch_w<FMT, EPI, 1>(a, stream);
 }
 
 template <int FMT>
 static int launch_f(const GemvArgs& a, hipStream_t stream) {
     switch (a.epi) {
-        case EPI_STORE: return launch_e<FMT, EPI_STORE>(a, stream);
-        case EPI_RESID: return launch_e<FMT, EPI_RESID>(a, stream);
-        case EPI_SWIGLU: return launch_e<FMT, EPI_SWIGLU>(a, stream);
-        default: return launch_e<FMT, EPI_QKV>(a, stream);
+        case EPI_STORE: return launch_m<FMT, EPI_STORE>(a, stream);
+        case EPI_RESID: return launch_m<FMT, EPI_RESID>(a, stream);
+        case EPI_SWIGLU: return launch_m<FMT, EPI_SWIGLU>(a, stream);
+        default: return launch_m<FMT, EPI_QKV>(a, stream);
     }
 }
 
 int launch_gemm(const GemvArgs& a, hipStream_t stream) {
     if (a.N % 16 || a.K % 128 || a.M <= 0 || a.m_base != 0 || !a.xf || a.mp != 16 || (a.norm_w && !a.ssq_in))
+        return 2;
+    if (a.hidden_out && (!a.norm_w || (a.xmap.seq_stride & 3) || (a.xmap.row_stride & 3) || ((uintptr_t)a.x & 15) ||
+                         ((uintptr_t)a.hidden_out & 15) || (a.K & 3)))
         return 2;
     switch (a.fmt) {
         case WF_INT4: return launch_f<WF_INT4>(a, stream);

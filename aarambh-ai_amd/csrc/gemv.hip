@@ -77,7 +77,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     __shared__ float yt_s[2][16][17];
     __shared__ float s_inv[16];
     __shared__ unsigned cnt_s[2], gen_s[2];
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int G = a.K >> 7;
     const int Mc = a.M;
@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     const int ngp = REG ? NGP : ((G + NW - 1) / NW + PF - 1) / PF * PF;  // items per tile per wave
     const int nmine = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const int mt = a.m_base >> 4;
-    const int elane = RS ? min(lr, 2 * MP - 1) : 2 * lr;  // fragment entry of this lane
+    const int elane = RS ? min(lr, 2 * MP - 1) : lr;  // fragment entry of this lane (lo: +16 at MP 16)
     const int glast = G - 1 - ((G - 1 - wid) % NW + NW) % NW;  // last real group of this wave (may be < 0)
 
     // ---- 1/rms of each row from the producer's 16-column partial sums ----
@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     if (a.norm_w) {
         for (int m = wid; m < Mc; m += NW) {
             float ss = 0.f;
-            for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)q * a.ssq_rows + a.m_base + m];
+            for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)(a.m_base + m) * a.ssq_ld + q];
 #pragma unroll
             for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
             if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
 #pragma unroll
             for (int e = 0; e < EA; e++)
                 f[t][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        fr, (int)(f_voff + 16u * e), f_soff + t * 4 * EPB * 16, 0));
+                                                        fr, (int)(f_voff + 256u * e), f_soff + t * 4 * EPB * 16, 0));
     };
     // item (tile tl, slot gi) of this wave -> ring slot p
     auto load_item = [&](int p, int tl, int gi) {
@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(GT_THREADS) gemv_f32_kernel(GemvArgs a) {
     __shared__ float red[4][GT_MROWS][17];
     __shared__ float s_ssq[4][GT_MROWS];
     __shared__ float yt[GT_MROWS][17];
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nt = blockIdx.x;
     const int Mc = a.M;
     const int r = tid >> 4, c = tid & 15;

@@ -36,10 +36,12 @@ __host__ __device__ inline long long row_off(const RowMap& r, int m) {
 //   index = ((((mt * G + g) * 4 + t) * 4 + lg) * EPB + e)
 // for row chunk mt (16 rows), 128-column group g, k-step t (8 columns), lane
 // group lg (32 columns); EPB = 2*mp entries for mp <= 8 (hi of row r at e = r,
-// lo at e = mp + r: the two halves occupy MFMA rows) and 32 for mp = 16 (hi at
-// e = 2r, lo at 2r + 1: the halves are two MFMAs).  The slot of column c inside
-// an entry is frag_slot(fmt, c % 8).  Sums of squares of the raw values over
-// 16-column tiles go to ssq[(c / 16) * ssq_rows + m] for the consumer's RMSNorm.
+// lo at e = mp + r: the two halves occupy MFMA rows), 32 for mp = 16 (hi at
+// e = r, lo at 16 + r: the halves are two MFMAs; 16-row chunks also feed the
+// many-row GEMM).  The slot of column c inside an entry is frag_slot(fmt,
+// c % 8).  Sums of squares of the raw values over 16-column tiles go to
+// ssq[m * ssq_ld + c / 16] for the consumer's RMSNorm (a row's partials are contiguous).
+
 struct XFrag {
     uint16_t* buf;        // null: the consumer reads f32 rows (no fragments)
     int fmt;              // consumer weight format (WF_INT4 / WF_INT8 / WF_BF16)
@@ -47,7 +49,7 @@ struct XFrag {
     int G;                // consumer K / 128
     const float* norm_w;  // consumer RMSNorm weight (null: none)
     float* ssq;           // 16-column partial sums of squares (null: none)
-    int ssq_rows;         // row stride of ssq
+    int ssq_ld;           // row stride of ssq (16-column tiles per row)
 };
 
 __host__ __device__ inline int frag_epb(int mp) { return mp <= 8 ? 2 * mp : 32; }
@@ -85,13 +87,16 @@ struct GemvArgs {
     int N, K;
     int M;                // activation rows of this launch (<= 16)
     int m_base;           // index of its first row in the row maps
+    float* gpart;         // many-row GEMM: split-K partial tiles (scratch)
+    unsigned* gcnt;       // many-row GEMM: arrival counters, zero between launches
+    long long gpart_elems;
     const float* x;       // input activations (f32 rows: F32 weights, hidden_out)
     RowMap xmap;
     const uint16_t* xf;   // input fragments (quantised formats, XFrag layout)
     int mp;               // their row-tile size
     const float* norm_w;  // RMSNorm weight fused into the input (null: none)
     const float* ssq_in;  // 16-column partial sums of squares of the raw input
-    int ssq_rows;
+    int ssq_ld;
     float eps;
     float* hidden_out;    // optional normalised input copy [rows][K]
     int epi;

@@ -28,7 +28,7 @@ __device__ inline float load_table(const void* table, int fmt, size_t idx) {
 }
 
 __device__ inline float block_sum(float v, float* red) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     v = wave_sum_f32(v);
     __syncthreads();
     if (lane == 0) red[wid] = v;
@@ -50,7 +50,7 @@ __device__ void emit_row_fragments(const XFrag& fo, const float* row, int m, int
             float ss = 0.f;
 #pragma unroll
             for (int n = 0; n < 16; n++) ss += row[q * 16 + n] * row[q * 16 + n];
-            fo.ssq[(size_t)q * fo.ssq_rows + m] = ss;
+            fo.ssq[(size_t)m * fo.ssq_ld + q] = ss;
         }
 }
 
@@ -181,7 +181,7 @@ __global__ void quant_int8_kernel(const float* w, int N, int K, uint8_t* tiled, 
     float mx = 0.f;
     for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(src[k]));
     mx = wave_max_f32(mx);
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (lane == 0) red[wid] = mx;
     __syncthreads();
     float m = 0.f;
@@ -416,7 +416,7 @@ __global__ void argmax_rows_kernel(const float* x, long long ld, int V, int32_t*
         float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
         t1 = n1; t2 = n2;
     }
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (lane == 0) { rk[wid] = bk; ri[wid] = bi; r1[wid] = t1; r2[wid] = t2; }
     __syncthreads();
     if (threadIdx.x == 0) {

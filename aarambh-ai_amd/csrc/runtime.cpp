@@ -95,6 +95,9 @@ struct aarh_ctx {
     float *hidden = nullptr, *logits = nullptr, *part = nullptr, *apart = nullptr, *hn = nullptr;
     size_t apart_elems = 0;
     unsigned* acnt = nullptr;
+    float* gpart = nullptr;     // many-row GEMM split-K partials
+    size_t gpart_elems = 0;
+    unsigned* gcnt = nullptr;  // its arrival counters
     int32_t *d_pos0 = nullptr, *d_slot = nullptr, *d_zero = nullptr, *d_seqidx = nullptr;
     uint32_t* d_ids = nullptr;
     int32_t *h_pos0 = nullptr, *h_slot = nullptr;
@@ -222,6 +225,11 @@ struct ProfScope {
     }
 };
 
+// Fragment row tile of an M-row activation (hi + lo halves; 16-row chunks for
+// the many-row GEMM).  Plain fp16 activations would halve the GEMM's MFMA work
+// but measured up to 2.8e-3 relative logit error on random-init models (the
+// INT8 KV cache turns k errors of 2^-12 into flipped codes), above the 2e-3
+// bar, so every projection keeps the lo halves.
 int frag_mp(int M) { return M <= 4 ? 4 : (M <= 8 ? 8 : 16); }
 
 // Fragments of an activation matrix for a consumer of format `fmt` with K = k
@@ -235,7 +243,7 @@ XFrag xfrag(aarh_ctx* c, uint16_t* buf, int fmt, int k, int mp, const float* nor
     f.G = k / 128;
     f.norm_w = norm_w;
     f.ssq = ssq ? c->ssq_a : nullptr;
-    f.ssq_rows = c->Mmax;
+    f.ssq_ld = c->H / 16;
     return f;
 }
 
@@ -260,7 +268,7 @@ int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, co
     a.mp = mp;
     a.norm_w = norm_w;
     a.ssq_in = c->ssq_a;
-    a.ssq_rows = c->Mmax;
+    a.ssq_ld = c->H / 16;
     a.eps = c->cfg.norm_eps;
     a.hidden_out = hidden_out;
     a.epi = epi;
@@ -269,6 +277,9 @@ int gemv(aarh_ctx* c, const DevTensor& t, int M, const float* x, RowMap xmap, co
     a.resid = resid;
     a.ldr = ldr;
     a.fo = fo;
+    a.gpart = c->gpart;
+    a.gcnt = c->gcnt;
+    a.gpart_elems = (long long)c->gpart_elems;
     if (qkv) a.qkv = *qkv;
     if (t.fmt != WF_F32 && M > 16) {
         ProfScope ps(c, cls, alg_weight_bytes(t));
@@ -501,7 +512,7 @@ void aarh_destroy(aarh_ctx* c) {
     for (void* p : {(void*)c->x, (void*)c->q, (void*)c->att, (void*)c->h, (void*)c->ssq_a, (void*)c->kvnew,
                     (void*)c->frag_a, (void*)c->frag_b,
                     (void*)c->hidden, (void*)c->logits, (void*)c->apart, (void*)c->hn,
-                    (void*)c->acnt, (void*)c->d_pos0, (void*)c->d_slot, (void*)c->d_zero, (void*)c->d_seqidx,
+                    (void*)c->acnt, (void*)c->gpart, (void*)c->gcnt, (void*)c->d_pos0, (void*)c->d_slot, (void*)c->d_zero, (void*)c->d_seqidx,
                     (void*)c->d_ids, (void*)c->acc_max, (void*)c->acc_sum, (void*)c->acc_argmax, (void*)c->acc_cnt})
         F(p);
     if (c->h_pos0) (void)hipHostFree(c->h_pos0);
@@ -715,6 +726,12 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         if (dalloc(c, &c->apart, c->apart_elems * 4)) return AARH_ERR_DEVICE;
         if (dalloc(c, &c->acnt, groups * 4)) return AARH_ERR_DEVICE;
         HIPCHK(c, hipMemset(c->acnt, 0, groups * 4));
+        if (M > 16) {
+            // GEMM split-K partial tiles (64 KiB per block): up to 1024 blocks
+            c->gpart_elems = (size_t)16 << 20;
+            if (dalloc(c, &c->gpart, c->gpart_elems * 4) || dalloc(c, &c->gcnt, 8192 * 4)) return AARH_ERR_DEVICE;
+            HIPCHK(c, hipMemset(c->gcnt, 0, 8192 * 4));
+        }
         if (dalloc(c, &c->d_pos0, M * 4) || dalloc(c, &c->d_slot, M * 4) || dalloc(c, &c->d_zero, M * 4) ||
             dalloc(c, &c->d_seqidx, M * 4) || dalloc(c, &c->d_ids, M * 4))
             return AARH_ERR_DEVICE;
