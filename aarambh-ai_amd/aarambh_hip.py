@@ -115,6 +115,8 @@ def lib():
         "aarh_session_step": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
         "aarh_session_result": (C.c_int, [_P, _P, C.c_int32, _P, _P, C.POINTER(_Stats)]),
         "aarh_session_end": (None, [_P]),
+        "aarh_spec_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
+                                         _P, _P, _P, C.POINTER(_Stats)]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
@@ -132,7 +134,7 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_init_synthetic", "aarh_kv_reset", "aarh_kv_len", "aarh_kv_rollback", "aarh_kv_fill_synthetic",
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
-            "aarh_session_result", "aarh_session_end", "aarh_prof_enable", "aarh_prof_get"]
+            "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get"]
 
 
 def _ptr(a):
@@ -410,6 +412,42 @@ class MtpSpeculativeEngine:
 
     def session(self, prompts, max_new_tokens, sampler: Sampler, cached_len=0, seeds=None):
         return Session(self, prompts, max_new_tokens, sampler, cached_len, seeds)
+
+
+class SpeculativeEngine:
+    """inference/src/speculative.rs:93-516: external draft model speculation for a
+    batch of independent requests (target and draft are two HipModels on one device)."""
+
+    def __init__(self, target: HipModel, draft: HipModel, config: SpeculativeConfig):
+        if config.num_draft_tokens == 0:
+            raise ConfigError("num_draft_tokens must be greater than zero")
+        if target.cfg.vocab_size != draft.cfg.vocab_size:
+            raise ConfigError("draft and target tokenizers are incompatible (vocabulary sizes differ)")
+        self.target = target
+        self.draft = draft
+        self.config = config
+
+    def generate_batch(self, prompts, max_new_tokens, sampler: Sampler, seeds=None):
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.uint32)
+        nseq, plen = prompts.shape
+        sd = np.ascontiguousarray(
+            np.full(nseq, sampler.seed, np.uint64) if seeds is None else seeds, np.uint64)
+        out = np.zeros((nseq, max(max_new_tokens, 1)), np.uint32)
+        n = np.zeros(nseq, np.int32)
+        fin = np.zeros(nseq, np.int32)
+        stats = (_Stats * nseq)()
+        t = self.target
+        t._check(lib().aarh_spec_generate(t.h, self.draft.h, _ptr(prompts), nseq, plen, max_new_tokens,
+                                          self.config.num_draft_tokens, C.byref(sampler._c()), _ptr(sd),
+                                          _ptr(out), _ptr(n), _ptr(fin), stats))
+        res = []
+        for b in range(nseq):
+            st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
+            res.append(GenerationOutput(list(out[b, :n[b]]), FINISH[int(fin[b])], st))
+        return res
+
+    def generate(self, prompt_ids, max_new_tokens, sampler: Sampler):
+        return self.generate_batch(np.asarray(prompt_ids)[None, :], max_new_tokens, sampler)[0]
 
 
 class Session:

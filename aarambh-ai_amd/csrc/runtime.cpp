@@ -232,6 +232,9 @@ struct ProfScope {
 // bar, so every projection keeps the lo halves.
 int frag_mp(int M) { return M <= 4 ? 4 : (M <= 8 ? 8 : 16); }
 
+// Cache positions past max_seq_len reserved for padding rows of ragged batches.
+constexpr int PAD_SLACK = 32;
+
 // Fragments of an activation matrix for a consumer of format `fmt` with K = k
 // (null buffer: the consumer reads f32 rows).
 XFrag xfrag(aarh_ctx* c, uint16_t* buf, int fmt, int k, int mp, const float* norm_w, bool ssq) {
@@ -625,7 +628,9 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     if (g.max_rows > 128) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 128");
     c->Fp = (c->F + 127) / 128 * 128;
     c->Mmax = g.max_rows;
-    c->cap = (g.max_seq_len + 31) / 32 * 32;  // V^T rows padded so 32-token blocks stay in bounds
+    // V^T rows padded so 32-token blocks stay in bounds; PAD_SLACK positions past the
+    // context limit take the padding rows of ragged lock-step engine batches
+    c->cap = (g.max_seq_len + PAD_SLACK + 31) / 32 * 32;
     *out = c;
     if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -660,10 +665,11 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     // RoPE tables (rope_scaling.rs:6-11, rope.rs:43-72), computed on the host in f32 like the reference.
     {
         const int half = c->hd / 2;
-        std::vector<float> cs((size_t)g.max_seq_len * half), sn((size_t)g.max_seq_len * half), inv(half);
+        const int npos = g.max_seq_len + PAD_SLACK;
+        std::vector<float> cs((size_t)npos * half), sn((size_t)npos * half), inv(half);
         for (int i = 0; i < half; i++)
             inv[i] = (float)(1.0 / std::pow((double)g.rope_theta, 2.0 * (double)i / (double)c->hd));
-        for (int p = 0; p < g.max_seq_len; p++)
+        for (int p = 0; p < npos; p++)
             for (int i = 0; i < half; i++) {
                 float a = (float)p * inv[i];
                 cs[(size_t)p * half + i] = cosf(a);
@@ -945,8 +951,9 @@ int aarh_kv_fill_synthetic(aarh_ctx* c, int slot, int32_t len, uint64_t seed) {
 }
 
 // Validate and stage (slots, offsets, ids) from host arrays; returns max kv length.
+// pad: positions allowed past max_seq_len (engine padding rows only, <= PAD_SLACK).
 static int stage_rows(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, const int32_t* offsets, int nseq, int S,
-                      int* max_kv) {
+                      int* max_kv, int pad = 0) {
     if (nseq <= 0 || S <= 0) return fail(c, AARH_ERR_SHAPE, "batch and sequence length must be non-zero");
     if (nseq * S > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq*S=%d exceeds max_rows %d", nseq * S, c->Mmax);
     int mk = 0;
@@ -957,7 +964,7 @@ static int stage_rows(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, co
             if (slots[b2] == sl) return fail(c, AARH_ERR_SHAPE, "slot %d used twice", sl);
         if (off < 0 || off > c->kv_len[sl])
             return fail(c, AARH_ERR_SHAPE, "offset %d beyond cached length %d of slot %d", off, c->kv_len[sl], sl);
-        if (off + S > c->cfg.max_seq_len)
+        if (off + S > c->cfg.max_seq_len + pad)
             return fail(c, AARH_ERR_SHAPE, "sequence length %d with offset %d exceeds max_seq_len %d", S, off,
                         c->cfg.max_seq_len);
         mk = std::max(mk, off + S);
@@ -1255,7 +1262,7 @@ int session_round(aarh_session* e) {
             if (e->finished[b]) c->kv_len[b] = 0;
         }
         int mk = 0;
-        if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk))) return r;
+        if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK))) return r;
         if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, e->tgt + V, rm(Kr, (long long)(K + 1) * V, V),
                              e->vhid)))
             return r;
@@ -1343,7 +1350,7 @@ int session_round(aarh_session* e) {
                 ids[(size_t)j * Sr + s2] = e->hprops[(size_t)b * K + std::min(s2, replay_len[j] - 1)];
         }
         int mk = 0;
-        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk))) return r;
+        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk, PAD_SLACK))) return r;
         if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, Sr, mk, c->logits, rm(nr * Sr, 0, V), c->hidden)))
             return r;
         std::vector<const float*> rs, rhs;
@@ -1537,3 +1544,419 @@ int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt
 }
 
 }  // extern "C"
+
+// ===========================================================================
+// Engine: SpeculativeEngine::generate_with_callback (speculative.rs:175-516)
+// with an external draft model (second context), nseq requests in lock-step
+// rounds.  Draft forwards, target verify, replays and the fused acceptance run
+// on the device; the host keeps the per-request bookkeeping (commits, finish
+// reasons, statistics, cache lengths).
+// ===========================================================================
+namespace {
+
+struct XSession {
+    aarh_ctx *c = nullptr, *d = nullptr;  // target, draft
+    int nseq = 0, K = 0, max_new = 0, available = 0;
+    bool greedy = true;
+    aarh_sampler samp{};
+    float *tgt = nullptr;  // [nseq][K+1][V] target rows T[i] for proposal i (T[np] = bonus row)
+    float *drf = nullptr;  // [nseq][K][V] draft logits before proposal p (drf[b][0] = draft_next)
+    uint32_t* props = nullptr;
+    int32_t *acc_len = nullptr, *acc_tok = nullptr, *acc_draws = nullptr, *acc_status = nullptr, *nprop = nullptr;
+    uint32_t* acc_flags = nullptr;
+    uint64_t *seeds = nullptr, *offs = nullptr;
+    const float** src = nullptr;
+    float** dst = nullptr;
+    std::vector<uint64_t> hoffs;
+    std::vector<char> finished;
+    std::vector<std::vector<uint32_t>> out;
+    std::vector<int32_t> finish, pending, np, tbase, dbase, hlen, htok, hdraws, hstatus;
+    std::vector<aarh_spec_stats> stats;
+    std::vector<uint32_t> hprops;
+
+    ~XSession() {
+        for (void* p : {(void*)tgt, (void*)drf, (void*)props, (void*)acc_len, (void*)acc_tok, (void*)acc_draws,
+                        (void*)acc_status, (void*)nprop, (void*)acc_flags, (void*)seeds, (void*)offs, (void*)src,
+                        (void*)dst})
+            if (p) (void)hipFree(p);
+    }
+};
+
+// Copy device rows src[i] -> dst[i] (n floats each) on ctx c's stream; waits.
+int copy_rows_lists(XSession* e, aarh_ctx* c, const std::vector<const float*>& s, const std::vector<float*>& d, int n) {
+    if (s.empty()) return 0;
+    const int rows = (int)s.size();
+    for (int r0 = 0; r0 < rows; r0 += 2 * e->c->cfg.max_batch) {
+        const int nr = std::min(rows - r0, 2 * e->c->cfg.max_batch);
+        HIPCHK(c, hipMemcpyAsync(e->src, s.data() + r0, nr * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(e->dst, d.data() + r0, nr * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+        KCHK(c, launch_copy_rows(e->src, e->dst, nr, n, c->stream));
+        if (int r = sync_stream(c)) return r;
+    }
+    return 0;
+}
+
+// One ragged batch: sequence seqs[j] feeds rows[j] (<= S) ids at offset off[j] on
+// its own slot; rows past rows[j] repeat the last id (padding, truncated by the
+// cache length set afterwards).  Logits of (j, s) land in x->logits row j*S + s.
+int ragged_forward(aarh_ctx* x, const std::vector<int>& seqs, const std::vector<std::vector<uint32_t>>& ids,
+                   const std::vector<int>& off, int* S_out) {
+    const int n = (int)seqs.size();
+    int S = 1;
+    for (const auto& v : ids) S = std::max(S, (int)v.size());
+    std::vector<uint32_t> flat((size_t)n * S);
+    std::vector<int32_t> sl(n), of(n);
+    for (int j = 0; j < n; j++) {
+        sl[j] = seqs[j];
+        of[j] = off[j];
+        for (int s2 = 0; s2 < S; s2++) flat[(size_t)j * S + s2] = ids[j][std::min(s2, (int)ids[j].size() - 1)];
+    }
+    int mk = 0, r;
+    if ((r = stage_rows(x, flat.data(), sl.data(), of.data(), n, S, &mk, PAD_SLACK))) return r;
+    if ((r = forward_dev(x, x->d_ids, x->d_pos0, x->d_slot, n, S, mk, x->logits, rm(n * S, 0, x->V), nullptr))) return r;
+    for (int j = 0; j < n; j++) x->kv_len[seqs[j]] = off[j] + (int)ids[j].size();
+    *S_out = S;
+    return 0;
+}
+
+// Sample one token per sequence from rows drf[b][p] (draft proposal p).
+int sample_draft_rows(XSession* e, int p) {
+    aarh_ctx* c = e->c;
+    const int nseq = e->nseq, K = e->K, V = c->V;
+    int r;
+    if (e->greedy) {
+        KCHK(c, launch_argmax_rows(e->drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)e->props + p, K, nullptr,
+                                   c->stream));
+    } else {
+        std::vector<uint64_t> o(nseq);
+        for (int b = 0; b < nseq; b++) o[b] = e->hoffs[b] + p;
+        HIPCHK(c, hipMemcpyAsync(e->offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
+        if ((r = aarh_accept_sample(c, e->drf + (size_t)p * V, K, nullptr, nullptr, nullptr, nseq, 0, V, 1, &e->samp,
+                                    e->seeds, e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
+                                    e->acc_status, nullptr)))
+            return r;
+        if ((r = sync_stream(c))) return r;
+        std::vector<int32_t> t(nseq);
+        HIPCHK(c, hipMemcpy(t.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
+        for (int b = 0; b < nseq; b++) e->hprops[(size_t)b * K + p] = (uint32_t)t[b];
+        HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
+    }
+    if ((r = sync_stream(c))) return r;
+    std::vector<uint32_t> t((size_t)nseq * K);
+    HIPCHK(c, hipMemcpy(t.data(), e->props, t.size() * 4, hipMemcpyDeviceToHost));
+    for (int b = 0; b < nseq; b++) e->hprops[(size_t)b * K + p] = t[(size_t)b * K + p];
+    return 0;
+}
+
+// One round of speculative.rs:251-509 for every unfinished request.
+int xsession_round(XSession* e) {
+    aarh_ctx *c = e->c, *d = e->d;
+    const int nseq = e->nseq, K = e->K, V = c->V;
+    int r;
+    std::vector<int> count(nseq, 0);
+    std::vector<char> alive(nseq, 0);
+    int Kr = 0;
+    for (int b = 0; b < nseq; b++) {
+        if (e->finished[b]) continue;
+        count[b] = std::min(K, e->max_new - (int)e->out[b].size());
+        alive[b] = 1;
+        e->np[b] = 0;
+        e->tbase[b] = c->kv_len[b];
+        e->dbase[b] = d->kv_len[b];
+        Kr = std::max(Kr, count[b]);
+    }
+    // ---- draft proposals (speculative.rs:267-304) ----
+    for (int p = 0; p < Kr; p++) {
+        if ((r = sample_draft_rows(e, p))) return r;
+        std::vector<int> fs, fo;
+        std::vector<std::vector<uint32_t>> fi;
+        for (int b = 0; b < nseq; b++) {
+            if (!alive[b] || p >= count[b]) continue;
+            const uint32_t tok = e->hprops[(size_t)b * K + p];
+            e->np[b]++;
+            e->stats[b].draft_tokens_proposed++;
+            if (tok == EOS_ID) {
+                alive[b] = 0;
+                continue;
+            }
+            fs.push_back(b);
+            fo.push_back(d->kv_len[b]);
+            fi.push_back({tok});
+            e->stats[b].draft_decode_forwards++;
+        }
+        if (fs.empty()) continue;
+        int S = 0;
+        if ((r = ragged_forward(d, fs, fi, fo, &S))) return r;
+        std::vector<const float*> ls;
+        std::vector<float*> ld;
+        for (size_t j = 0; j < fs.size(); j++)
+            if (p + 1 < count[fs[j]] ) {
+                ls.push_back(d->logits + j * (size_t)S * V);
+                ld.push_back(e->drf + ((size_t)fs[j] * K + p + 1) * V);
+            }
+        if ((r = copy_rows_lists(e, d, ls, ld, V))) return r;
+    }
+    // ---- target verify of [pending?] + proposals (speculative.rs:306-323) ----
+    std::vector<int> vs, vo;
+    std::vector<std::vector<uint32_t>> vi;
+    for (int b = 0; b < nseq; b++) {
+        if (e->finished[b]) continue;
+        std::vector<uint32_t> ids;
+        if (e->pending[b] >= 0) ids.push_back((uint32_t)e->pending[b]);
+        for (int i = 0; i < e->np[b]; i++) ids.push_back(e->hprops[(size_t)b * K + i]);
+        vs.push_back(b);
+        vo.push_back(e->tbase[b]);
+        vi.push_back(ids);
+        e->stats[b].rounds++;
+        e->stats[b].target_decode_forwards++;
+    }
+    if (vs.empty()) return 0;
+    {
+        int S = 0;
+        if ((r = ragged_forward(c, vs, vi, vo, &S))) return r;
+        // rows -> T[i]: with a pending token verify row i is T[i]; without, T[0] is
+        // target_next (already in place) and verify row i is T[i + 1]
+        std::vector<const float*> ls;
+        std::vector<float*> ld;
+        for (size_t j = 0; j < vs.size(); j++) {
+            const int b = vs[j], shift = e->pending[b] >= 0 ? 0 : 1;
+            for (int s2 = 0; s2 < (int)vi[j].size(); s2++) {
+                ls.push_back(c->logits + (j * (size_t)S + s2) * V);
+                ld.push_back(e->tgt + ((size_t)b * (K + 1) + s2 + shift) * V);
+            }
+        }
+        if ((r = copy_rows_lists(e, c, ls, ld, V))) return r;
+    }
+    // ---- acceptance with bonus (speculative.rs:329-501) ----
+    {
+        std::vector<uint64_t> o(nseq);
+        std::vector<int32_t> npv(nseq);
+        for (int b = 0; b < nseq; b++) {
+            o[b] = e->hoffs[b] + e->np[b];
+            npv[b] = e->finished[b] ? 0 : e->np[b];
+        }
+        HIPCHK(c, hipMemcpyAsync(e->offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(e->nprop, npv.data(), nseq * 4, hipMemcpyHostToDevice, c->stream));
+        if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 1, &e->samp, e->seeds,
+                                    e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
+                                    e->acc_status, nullptr)))
+            return r;
+        if ((r = sync_stream(c))) return r;
+        HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->hdraws.data(), e->acc_draws, nseq * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(e->hstatus.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
+    }
+    // ---- commit, rollback, replay ----
+    std::vector<int> ts, to, ds, dof;
+    std::vector<std::vector<uint32_t>> ti, di;
+    for (size_t j = 0; j < vs.size(); j++) {
+        const int b = vs[j];
+        if (e->hstatus[b] != 0)
+            return fail(c, AARH_ERR_CONFIG, "speculative residual distribution has zero probability mass");
+        if (!e->greedy) e->hoffs[b] += e->np[b] + e->hdraws[b];
+        const int npb = e->np[b], acc = e->hlen[b], hp = e->pending[b] >= 0 ? 1 : 0;
+        const std::vector<uint32_t>& tin = vi[j];
+        e->pending[b] = -1;
+        bool done = false;
+        for (int i = 0; i < acc && !done; i++) {
+            e->stats[b].draft_tokens_accepted++;
+            const uint32_t t = e->hprops[(size_t)b * K + i];
+            if (t == EOS_ID) {
+                e->finish[b] = AARH_FINISH_EOS;
+                done = true;
+                break;
+            }
+            e->out[b].push_back(t);
+            if ((int)e->out[b].size() == e->max_new) done = true;
+        }
+        if (done) {
+            e->finished[b] = 1;
+            continue;
+        }
+        if (acc < npb) {
+            // rejection at acc: restore both caches, replay the accepted prefix
+            const uint32_t repl = (uint32_t)e->htok[b];
+            c->kv_len[b] = e->tbase[b];
+            d->kv_len[b] = e->dbase[b];
+            if (hp + acc > 0) {
+                ts.push_back(b);
+                to.push_back(e->tbase[b]);
+                ti.emplace_back(tin.begin(), tin.begin() + hp + acc);
+            }
+            if (acc > 0) e->stats[b].draft_decode_forwards++;
+            if (repl == EOS_ID) {
+                e->finish[b] = AARH_FINISH_EOS;
+                e->finished[b] = 1;
+                continue;
+            }
+            e->out[b].push_back(repl);
+            // draft: accepted prefix replay + the replacement, one launch (two reference forwards)
+            std::vector<uint32_t> dr(e->hprops.begin() + (size_t)b * K, e->hprops.begin() + (size_t)b * K + acc);
+            dr.push_back(repl);
+            ds.push_back(b);
+            dof.push_back(e->dbase[b]);
+            di.push_back(dr);
+            e->stats[b].draft_decode_forwards++;
+            e->pending[b] = (int)repl;
+        } else {
+            // every proposal accepted: target cache keeps them, bonus from T[np]
+            c->kv_len[b] = e->tbase[b] + hp + npb;
+            const uint32_t bonus = (uint32_t)e->htok[b];
+            if (bonus == EOS_ID) {
+                e->finish[b] = AARH_FINISH_EOS;
+                e->finished[b] = 1;
+                continue;
+            }
+            e->out[b].push_back(bonus);
+            ds.push_back(b);
+            dof.push_back(d->kv_len[b]);
+            di.push_back({bonus});
+            e->stats[b].draft_decode_forwards++;
+            e->pending[b] = (int)bonus;
+        }
+        if ((int)e->out[b].size() >= e->max_new) e->finished[b] = 1;
+    }
+    if (!ts.empty()) {
+        int S = 0;
+        if ((r = ragged_forward(c, ts, ti, to, &S))) return r;
+    }
+    if (!ds.empty()) {
+        int S = 0;
+        if ((r = ragged_forward(d, ds, di, dof, &S))) return r;
+        std::vector<const float*> ls;
+        std::vector<float*> ld;
+        for (size_t j = 0; j < ds.size(); j++) {
+            ls.push_back(d->logits + (j * (size_t)S + di[j].size() - 1) * V);
+            ld.push_back(e->drf + (size_t)ds[j] * K * V);  // draft_next = proposal 0's logits
+        }
+        if ((r = copy_rows_lists(e, d, ls, ld, V))) return r;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len,
+                                  int max_new_tokens, int num_draft_tokens, const aarh_sampler* s,
+                                  const uint64_t* seeds, uint32_t* out_tokens, int32_t* out_len,
+                                  int32_t* finish_reason, aarh_spec_stats* stats) {
+    if (!c || !d || !s) return AARH_ERR_CONFIG;
+    if (num_draft_tokens <= 0) return fail(c, AARH_ERR_CONFIG, "num_draft_tokens must be greater than zero");
+    if (num_draft_tokens >= PAD_SLACK)
+        return fail(c, AARH_ERR_UNSUPPORTED, "num_draft_tokens must be below %d on the device path", PAD_SLACK);
+    if (c->device != d->device) return fail(c, AARH_ERR_CONFIG, "draft and target models must use the same device");
+    if (c->V != d->V) return fail(c, AARH_ERR_CONFIG, "draft and target vocabularies differ (%d vs %d)", d->V, c->V);
+    if (nseq <= 0 || nseq > c->cfg.max_batch || nseq > d->cfg.max_batch)
+        return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
+    if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
+    const int max_seq = std::min(c->cfg.max_seq_len, d->cfg.max_seq_len);
+    if (prompt_len >= max_seq)
+        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but speculative context limit is %d (target=%d, draft=%d)",
+                    prompt_len, max_seq, c->cfg.max_seq_len, d->cfg.max_seq_len);
+    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
+    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
+        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
+    const int K = num_draft_tokens, V = c->V;
+    if (nseq * (K + 1) > c->Mmax || nseq * (K + 1) > d->Mmax)
+        return fail(c, AARH_ERR_SHAPE, "nseq x (draft tokens + 1) exceeds max_rows");
+    XSession e;
+    e.c = c;
+    e.d = d;
+    e.nseq = nseq;
+    e.K = K;
+    e.greedy = greedy;
+    e.samp = *s;
+    e.available = max_seq - prompt_len;
+    e.max_new = std::min(max_new_tokens, e.available);
+    e.hoffs.assign(nseq, 0);
+    e.finished.assign(nseq, 0);
+    e.out.assign(nseq, {});
+    e.finish.assign(nseq, AARH_FINISH_MAX_TOKENS);
+    e.stats.assign(nseq, aarh_spec_stats{});
+    e.hprops.assign((size_t)nseq * K, 0);
+    for (auto* v : {&e.np, &e.tbase, &e.dbase, &e.hlen, &e.htok, &e.hdraws, &e.hstatus}) v->assign(nseq, 0);
+    e.pending.assign(nseq, -1);
+    int r = 0;
+#define XA(p, bytes) \
+    if ((r = dalloc(c, &e.p, (bytes)))) return r;
+    XA(tgt, (size_t)nseq * (K + 1) * V * 4);
+    XA(drf, (size_t)nseq * K * V * 4);
+    XA(props, (size_t)nseq * K * 4);
+    XA(acc_len, nseq * 4);
+    XA(acc_tok, nseq * 4);
+    XA(acc_draws, nseq * 4);
+    XA(acc_status, nseq * 4);
+    XA(nprop, nseq * 4);
+    XA(acc_flags, nseq * 4);
+    XA(seeds, nseq * 8);
+    XA(offs, nseq * 8);
+    XA(src, (size_t)2 * c->cfg.max_batch * sizeof(void*));
+    XA(dst, (size_t)2 * c->cfg.max_batch * sizeof(void*));
+#undef XA
+    // rows of requests that sit out a step are sampled too (and ignored): keep them finite
+    HIPCHK(c, hipMemset(e.tgt, 0, (size_t)nseq * (K + 1) * V * 4));
+    HIPCHK(c, hipMemset(e.drf, 0, (size_t)nseq * K * V * 4));
+    {
+        std::vector<uint64_t> hs(nseq);
+        for (int b = 0; b < nseq; b++) hs[b] = seeds ? seeds[b] : 0;
+        HIPCHK(c, hipMemcpy(e.seeds, hs.data(), nseq * 8, hipMemcpyHostToDevice));
+    }
+    if (e.max_new > 0) {
+        // prefill both models (speculative.rs:236-247), chunked to max_rows
+        for (aarh_ctx* x : {c, d}) {
+            const int chunk = std::max(1, x->Mmax / nseq);
+            std::vector<int> seqs(nseq), off(nseq);
+            for (int b = 0; b < nseq; b++) {
+                seqs[b] = b;
+                x->kv_len[b] = 0;
+            }
+            for (int p0 = 0; p0 < prompt_len; p0 += chunk) {
+                const int S = std::min(chunk, prompt_len - p0);
+                std::vector<std::vector<uint32_t>> ids(nseq);
+                for (int b = 0; b < nseq; b++) {
+                    off[b] = p0;
+                    ids[b].assign(prompts + (size_t)b * prompt_len + p0, prompts + (size_t)b * prompt_len + p0 + S);
+                }
+                int Sx = 0;
+                if ((r = ragged_forward(x, seqs, ids, off, &Sx))) return r;
+                if (p0 + S == prompt_len) {
+                    std::vector<const float*> ls(nseq);
+                    std::vector<float*> ld(nseq);
+                    for (int b = 0; b < nseq; b++) {
+                        ls[b] = x->logits + ((size_t)b * Sx + S - 1) * V;
+                        ld[b] = x == c ? e.tgt + (size_t)b * (K + 1) * V : e.drf + (size_t)b * K * V;
+                    }
+                    if ((r = copy_rows_lists(&e, x, ls, ld, V))) return r;
+                }
+            }
+        }
+    } else {
+        for (int b = 0; b < nseq; b++) {
+            e.finish[b] = AARH_FINISH_CONTEXT_LIMIT;
+            e.finished[b] = 1;
+        }
+    }
+    for (;;) {
+        bool any = false;
+        for (int b = 0; b < nseq; b++)
+            if (!e.finished[b]) any = true;
+        if (!any) break;
+        if ((r = xsession_round(&e))) return r;
+    }
+    for (int b = 0; b < nseq; b++) {
+        const int n = (int)e.out[b].size();
+        if (out_len) out_len[b] = n;
+        if (out_tokens)
+            for (int i = 0; i < n && i < max_new_tokens; i++) out_tokens[(size_t)b * max_new_tokens + i] = e.out[b][i];
+        int fin = e.finish[b];
+        if (n == e.available && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
+        if (finish_reason) finish_reason[b] = fin;
+        if (stats) {
+            stats[b] = e.stats[b];
+            stats[b].draft_tokens_rejected =
+                std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
+        }
+    }
+    return 0;
+}

@@ -153,6 +153,21 @@ int aarh_session_result(aarh_session *session, uint32_t *out_tokens, int32_t out
                         int32_t *finish_reason, aarh_spec_stats *stats);
 void aarh_session_end(aarh_session *session);
 
+/* --- external-draft engine (SpeculativeEngine::generate_with_callback,
+   inference/src/speculative.rs:175-516; constructor checks :101-122) ---
+   target and draft are contexts of two models with the same vocabulary on one device;
+   both hold nseq requests on slots 0..nseq-1 (prefilled here from fresh caches).  Each
+   round the draft proposes up to num_draft_tokens (1..31) tokens autoregressively, the
+   target verifies [pending?] + proposals in one forward, the fused acceptance kernel
+   tests them in order and samples the replacement (rejection) or bonus token (all
+   accepted), both caches roll back by index and replay the accepted prefix.  The
+   context limit is the smaller of the two models' max_seq_len.  Outputs as for
+   aarh_mtp_generate. */
+int aarh_spec_generate(aarh_ctx *target, aarh_ctx *draft, const uint32_t *prompts, int nseq,
+                       int prompt_len, int max_new_tokens, int num_draft_tokens,
+                       const aarh_sampler *sampler, const uint64_t *seeds, uint32_t *out_tokens,
+                       int32_t *out_len, int32_t *finish_reason, aarh_spec_stats *stats);
+
 /* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
        AARH_PROF_GEMV_DOWN = 3, AARH_PROF_GEMV_LMHEAD = 4, AARH_PROF_ATTENTION = 5,

@@ -1465,6 +1465,196 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
     return st;
 }
 
+/*
+ * SpeculativeEngine::generate_with_callback (speculative.rs:175-516): external
+ * draft model, controllers inactive (ThinkingMode::None, no tools).  Per round
+ * (speculative.rs:251-509): the draft proposes up to k tokens autoregressively
+ * (one sampling draw each, stopping after an EOS proposal), the target verifies
+ * [pending?] + proposals in one forward, proposals are tested in order; on the
+ * first rejection both caches are restored, the target replays
+ * [pending?] + accepted proposals, the draft replays the accepted proposals and
+ * then the replacement, which becomes the pending target token; when every
+ * proposal is accepted a bonus token is sampled from the row after the last
+ * proposal, fed to the draft and kept pending.  The shared context limit is
+ * min(target, draft) max_seq_len (speculative.rs:203-212).
+ */
+int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *prompt, int prompt_len,
+                      int max_new_tokens, int num_draft_tokens, const ref_sampler *s, uint64_t seed,
+                      int nt, uint32_t *out_tokens, int *out_len, int *finish_reason,
+                      ref_spec_stats *stats, float *out_min_gap) {
+    const ref_config *tc = &tm->cfg, *dc = &dm->cfg;
+    if (num_draft_tokens <= 0) return REF_ERR_CONFIG; /* speculative.rs:104-108 */
+    if (tc->vocab_size != dc->vocab_size) return REF_ERR_CONFIG;
+    if (prompt_len <= 0) return REF_ERR_SHAPE;
+    int max_seq = tc->max_seq_len < dc->max_seq_len ? tc->max_seq_len : dc->max_seq_len;
+    if (prompt_len >= max_seq) return REF_ERR_SHAPE;
+    int available = max_seq - prompt_len;
+    int max_new = max_new_tokens < available ? max_new_tokens : available;
+    memset(stats, 0, sizeof(*stats));
+    *out_len = 0;
+    *finish_reason = REF_FINISH_MAX_TOKENS;
+    float min_gap = INFINITY;
+    if (max_new == 0) {
+        *finish_reason = REF_FINISH_CONTEXT_LIMIT;
+        if (out_min_gap) *out_min_gap = min_gap;
+        return REF_OK;
+    }
+    int64_t V = tc->vocab_size;
+    int K = num_draft_tokens;
+    int det = ref_is_deterministic(s);
+    ref_rng rng;
+    ref_rng_seed_u64(&rng, seed);
+    ref_kv *tkv = ref_kv_create(tm, tc->max_seq_len), *dkv = ref_kv_create(dm, dc->max_seq_len);
+    float *tlog = (float *)malloc(sizeof(float) * (size_t)(prompt_len * V));
+    float *dlog = (float *)malloc(sizeof(float) * (size_t)(prompt_len * V));
+    float *target_next = (float *)malloc(sizeof(float) * (size_t)V);
+    float *draft_next = (float *)malloc(sizeof(float) * (size_t)V);
+    float *dist = (float *)malloc(sizeof(float) * (size_t)(K * V));
+    float *vlog = (float *)malloc(sizeof(float) * (size_t)((K + 1) * V));
+    float *pt = (float *)malloc(sizeof(float) * (size_t)V);
+    float *res = (float *)malloc(sizeof(float) * (size_t)V);
+    float *scratch = (float *)malloc(sizeof(float) * (size_t)((K + 1) * V));
+    uint32_t *props = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)K);
+    uint32_t *tin = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(K + 1));
+    int st = ref_forward(tm, tkv, prompt, prompt_len, 0, tlog, NULL, nt);
+    if (!st) st = ref_forward(dm, dkv, prompt, prompt_len, 0, dlog, NULL, nt);
+    if (!st) {
+        memcpy(target_next, tlog + (int64_t)(prompt_len - 1) * V, sizeof(float) * (size_t)V);
+        memcpy(draft_next, dlog + (int64_t)(prompt_len - 1) * V, sizeof(float) * (size_t)V);
+    }
+    free(tlog);
+    free(dlog);
+    int have_target_next = 1, pending = -1, n_out = 0;
+    while (st == REF_OK && n_out < max_new) {
+        int remaining = max_new - n_out;
+        int count = K < remaining ? K : remaining;
+        int committed = prompt_len + n_out;
+        int tbase = tkv->len, dbase = dkv->len; /* snapshots (restore = index rewind) */
+        (void)committed;
+        int np = 0;
+        for (int pi = 0; pi < count; pi++) {
+            if (det) {
+                float gp = top2_gap(draft_next, V);
+                if (gp < min_gap) min_gap = gp;
+            }
+            if ((st = ref_probabilities(s, draft_next, V, dist + (int64_t)pi * V))) break;
+            uint32_t tok;
+            if ((st = ref_sample_probabilities(s, &rng, dist + (int64_t)pi * V, V, &tok, NULL, NULL))) break;
+            props[np++] = tok;
+            stats->draft_tokens_proposed++;
+            if (tok == EOS_ID) break;
+            if ((st = ref_forward(dm, dkv, &tok, 1, dkv->len, draft_next, NULL, nt))) break;
+            stats->draft_decode_forwards++;
+        }
+        if (st) break;
+        int hp = pending >= 0, nin = 0;
+        if (hp) tin[nin++] = (uint32_t)pending;
+        for (int i = 0; i < np; i++) tin[nin++] = props[i];
+        if ((st = ref_forward(tm, tkv, tin, nin, tbase, vlog, NULL, nt))) break;
+        stats->rounds++;
+        stats->target_decode_forwards++;
+        pending = -1;
+        int rejected = 0, done = 0;
+        for (int i = 0; i < np; i++) {
+            const float *tl = (hp || i > 0) ? vlog + (int64_t)(i - (hp ? 0 : 1)) * V : target_next;
+            if (!hp && i == 0 && !have_target_next) { st = REF_ERR_CONFIG; break; }
+            if (det) {
+                float gp = top2_gap(tl, V);
+                if (gp < min_gap) min_gap = gp;
+            }
+            if ((st = ref_probabilities(s, tl, V, pt))) break;
+            int acc = 0, drew = 0;
+            ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, NULL, NULL, &drew);
+            top_candidates(pt, V, 5);
+            if (acc) {
+                stats->draft_tokens_accepted++;
+                if (props[i] == EOS_ID) {
+                    *finish_reason = REF_FINISH_EOS;
+                    done = 1;
+                    break;
+                }
+                out_tokens[n_out++] = props[i];
+                if (n_out == max_new) {
+                    done = 1;
+                    break;
+                }
+                continue;
+            }
+            rejected = 1;
+            uint32_t repl;
+            if (det) {
+                if ((st = ref_sample_probabilities(s, &rng, pt, V, &repl, NULL, NULL))) break;
+            } else {
+                if ((st = ref_residual(pt, dist + (int64_t)i * V, V, res))) break;
+                if ((st = ref_sample_probabilities(s, &rng, res, V, &repl, NULL, NULL))) break;
+            }
+            tkv->len = tbase; /* target_cache.restore */
+            dkv->len = dbase; /* draft_cache.restore */
+            int treplay = hp + i;
+            if (treplay > 0 && (st = ref_forward(tm, tkv, tin, treplay, tbase, scratch, NULL, nt))) break;
+            if (i > 0) {
+                if ((st = ref_forward(dm, dkv, props, i, dbase, scratch, NULL, nt))) break;
+                stats->draft_decode_forwards++;
+            }
+            if (repl == EOS_ID) {
+                *finish_reason = REF_FINISH_EOS;
+                done = 1;
+                break;
+            }
+            out_tokens[n_out++] = repl;
+            if ((st = ref_forward(dm, dkv, &repl, 1, dkv->len, draft_next, NULL, nt))) break;
+            stats->draft_decode_forwards++;
+            pending = (int)repl;
+            break;
+        }
+        if (st || done) break;
+        if (rejected) {
+            have_target_next = 0;
+            continue;
+        }
+        if (n_out == max_new) break;
+        /* every proposal accepted: bonus from the row after the last proposal */
+        const float *bl = vlog + (int64_t)(np - (hp ? 0 : 1)) * V;
+        if (det) {
+            float gp = top2_gap(bl, V);
+            if (gp < min_gap) min_gap = gp;
+        }
+        if ((st = ref_probabilities(s, bl, V, pt))) break;
+        top_candidates(pt, V, 5);
+        uint32_t bonus;
+        if ((st = ref_sample_probabilities(s, &rng, pt, V, &bonus, NULL, NULL))) break;
+        if (bonus == EOS_ID) {
+            *finish_reason = REF_FINISH_EOS;
+            break;
+        }
+        out_tokens[n_out++] = bonus;
+        if ((st = ref_forward(dm, dkv, &bonus, 1, dkv->len, draft_next, NULL, nt))) break;
+        stats->draft_decode_forwards++;
+        pending = (int)bonus;
+        have_target_next = 0;
+    }
+    if (st == REF_OK) {
+        if (n_out == available && *finish_reason == REF_FINISH_MAX_TOKENS)
+            *finish_reason = REF_FINISH_CONTEXT_LIMIT;
+        stats->draft_tokens_rejected = stats->draft_tokens_proposed - stats->draft_tokens_accepted;
+        if (stats->draft_tokens_rejected < 0) stats->draft_tokens_rejected = 0;
+    }
+    *out_len = n_out;
+    if (out_min_gap) *out_min_gap = min_gap;
+    free(target_next);
+    free(draft_next);
+    free(dist);
+    free(vlog);
+    free(pt);
+    free(res);
+    free(scratch);
+    free(props);
+    free(tin);
+    ref_kv_free(tkv);
+    ref_kv_free(dkv);
+    return st;
+}
+
 /* InferenceEngine plain decode (engine.rs generate path): sample, append, one-token forward. */
 int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
                        int max_new_tokens, const ref_sampler *s, uint64_t seed, int nt,

@@ -147,6 +147,10 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
                      int max_new_tokens, int num_draft_tokens, const ref_sampler *s,
                      uint64_t seed, int nthreads, uint32_t *out_tokens, int *out_len,
                      int *finish_reason, ref_spec_stats *stats, float *out_min_gap);
+int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *prompt, int prompt_len,
+                      int max_new_tokens, int num_draft_tokens, const ref_sampler *s, uint64_t seed,
+                      int nthreads, uint32_t *out_tokens, int *out_len, int *finish_reason,
+                      ref_spec_stats *stats, float *out_min_gap);
 int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
                        int max_new_tokens, const ref_sampler *s, uint64_t seed, int nthreads,
                        uint32_t *out_tokens, int *out_len, int *finish_reason);

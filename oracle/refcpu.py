@@ -124,6 +124,9 @@ def lib():
         "ref_mtp_generate": (C.c_int, [C.c_void_p, U32P, C.c_int, C.c_int, C.c_int, C.POINTER(RefSampler),
                                        C.c_uint64, C.c_int, U32P, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                        C.POINTER(RefSpecStats), C.POINTER(C.c_float)]),
+        "ref_spec_generate": (C.c_int, [C.c_void_p, C.c_void_p, U32P, C.c_int, C.c_int, C.c_int,
+                                        C.POINTER(RefSampler), C.c_uint64, C.c_int, U32P, C.POINTER(C.c_int),
+                                        C.POINTER(C.c_int), C.POINTER(RefSpecStats), C.POINTER(C.c_float)]),
         "ref_plain_generate": (C.c_int, [C.c_void_p, U32P, C.c_int, C.c_int, C.POINTER(RefSampler), C.c_uint64,
                                          C.c_int, U32P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     }
@@ -378,6 +381,19 @@ class Model:
                                     nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
         if st:
             raise ValueError(f"mtp_generate failed: {st}")
+        return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value
+
+    def spec_generate(self, draft, prompt, max_new, num_draft, s, seed=0, nthreads=8):
+        """SpeculativeEngine::generate_with_callback (speculative.rs:175-516) with `draft`
+        (another Model) as the external draft model."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(max_new, 1), np.uint32)
+        n, fin, gap = C.c_int(), C.c_int(), C.c_float()
+        stats = RefSpecStats()
+        st = lib().ref_spec_generate(self.h, draft.h, prompt, len(prompt), max_new, num_draft, C.byref(s), seed,
+                                     nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
+        if st:
+            raise ValueError(f"spec_generate failed: {st}")
         return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value
 
     def plain_generate(self, prompt, max_new, s, seed=0, nthreads=8):

@@ -130,3 +130,64 @@ def test_int8_kv_cache_stays_close_to_f32():
     a, _ = m8.kv(48).forward(ids, 0)
     b, _ = m32.kv(48).forward(ids, 0)
     assert 0 < rel(a, b) < 2e-2
+
+
+def test_external_draft_greedy_equal_models_one_round():  # speculative.rs:962-982
+    cfg = tiny_cfg(vocab_size=64, max_seq_len=64)
+    t = R.Model(cfg, seed=6, std=0.3)
+    d = R.Model(cfg, seed=6, std=0.3)  # draft identical to the target
+    prompt = R.synth_tokens(6, 1, 5, cfg.vocab_size)
+    s = R.sampler(greedy=True)
+    plain, _ = t.plain_generate(prompt, 4, s)
+    spec, fin, stats, _ = t.spec_generate(d, prompt, 4, 4, s)
+    assert list(spec) == list(plain) and fin == R.FINISH_MAX_TOKENS
+    assert stats["target_decode_forwards"] == 1 and stats["draft_tokens_accepted"] == 4
+
+
+@pytest.mark.parametrize("k", [1, 2, 4])
+def test_external_draft_greedy_matches_target_only(k):
+    """Any draft model: greedy speculation commits exactly the target's greedy
+    tokens (speculative.rs:962-982 with a disagreeing draft: rejections, replay,
+    pending tokens and bonus tokens all exercised)."""
+    cfg = tiny_cfg(vocab_size=64, max_seq_len=64)
+    t = R.Model(cfg, seed=7, std=0.3)
+    d = R.Model(cfg)  # the target's weights plus noise: a draft that agrees often, not always
+    rng = np.random.default_rng(7)
+    for i, (name, r, c, kind) in enumerate(t.tensors()):
+        w = t.get(i)
+        d.set(i, w + (rng.normal(0, 0.12, w.shape).astype(np.float32) if kind != R.T_NORM else 0))
+    prompt = R.synth_tokens(7, 2, 9, cfg.vocab_size)
+    s = R.sampler(greedy=True)
+    plain, fin_p = t.plain_generate(prompt, 30, s)
+    spec, fin_s, stats, _ = t.spec_generate(d, prompt, 30, k, s)
+    assert list(spec) == list(plain) and fin_s == fin_p
+    assert stats["rounds"] == stats["target_decode_forwards"]
+    assert stats["draft_tokens_proposed"] == stats["draft_tokens_accepted"] + stats["draft_tokens_rejected"]
+    assert stats["draft_tokens_rejected"] > 0 and stats["draft_tokens_accepted"] > 0
+    # a draft forward per proposal (EOS aside) plus one per rejection or bonus, plus accepted-prefix replays
+    assert stats["draft_decode_forwards"] >= stats["draft_tokens_proposed"]
+
+
+def test_external_draft_shared_context_limit():  # speculative.rs:1030-1043, :203-212
+    t = R.Model(tiny_cfg(max_seq_len=16))
+    d = R.Model(tiny_cfg(max_seq_len=16))
+    toks, fin, _, _ = t.spec_generate(d, np.array([1, 2, 3, 4, 5], np.uint32), 20, 4, R.sampler(greedy=True))
+    assert len(toks) == 11 and fin == R.FINISH_CONTEXT_LIMIT
+    d2 = R.Model(tiny_cfg(max_seq_len=12))  # the shorter of the two limits applies
+    toks, fin, _, _ = t.spec_generate(d2, np.array([1, 2, 3, 4, 5], np.uint32), 20, 4, R.sampler(greedy=True))
+    assert len(toks) == 7 and fin == R.FINISH_CONTEXT_LIMIT
+
+
+def test_external_draft_sampled_stream_is_seeded():
+    """Sampled external speculation: reproducible per seed, and different seeds
+    give different streams (the draws come from the request's StdRng)."""
+    cfg = tiny_cfg(vocab_size=64, max_seq_len=64)
+    t = R.Model(cfg, seed=9, std=0.3)
+    d = R.Model(cfg, seed=10, std=0.3)
+    prompt = R.synth_tokens(9, 2, 6, cfg.vocab_size)
+    s = R.sampler(temperature=0.9)
+    a = t.spec_generate(d, prompt, 24, 3, s, seed=5)
+    b = t.spec_generate(d, prompt, 24, 3, s, seed=5)
+    c = t.spec_generate(d, prompt, 24, 3, s, seed=6)
+    assert list(a[0]) == list(b[0]) and a[2] == b[2]
+    assert list(a[0]) != list(c[0])
