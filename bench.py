@@ -148,7 +148,7 @@ def run_gpu(args):
     return res
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_int4_verify_c4_b1_pmc.txt")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_hbm_traffic.txt")
 
 
 def measured_traffic():
@@ -243,7 +243,8 @@ def main():
     b1 = res.get(1, main_r)
     g1 = b1["int4_gemv"]
     roof = {
-        "kernel": "gemv_tile_kernel<INT4,*> (all INT4 projections of the batch-1 verify step)",
+        "kernel": "gemv_tile_kernel<INT4,4,*> (all INT4 projections of the batch-1 verify step: qkv, wo, gate/up, "
+                  "down; K = 4 rows)",
         "bound": "hbm",
         "achieved": round(g1["gbs"], 1),
         "peak": HBM_PEAK_GBS,
