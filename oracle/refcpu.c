@@ -1695,3 +1695,393 @@ int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_le
     ref_kv_free(kv);
     return st;
 }
+
+/* ======================================================================== */
+/* Latent-attention MoE decoder: every block is          */
+/* x += MLA(norm1(x)) (nn/src/mla.rs:300-314,402-489; builder                */
+/* model/src/model.rs:1094-1156) then x += MoE(norm2(x)) (nn/src/moe.rs:     */
+/* 212-340, top_k_gating :361-406, SharedExpertPath :127-178).  The MLA      */
+/* reconstructs K_nope = up_k(c_kv) and V = up_v(c_kv) over the whole cache, */
+/* as the reference does; the device path absorbs up_k / up_v instead.      */
+/* ======================================================================== */
+
+enum { X_NORM1, X_QP, X_KVA, X_KVN, X_UPK, X_UPV, X_KRP, X_OP, X_NORM2, X_ROUTER, X_FIXED };
+
+struct ref_lat {
+    ref_lat_config cfg;
+    int per_layer, n_tensors;
+    ref_tensor *t;
+    float *rope_cos, *rope_sin; /* [max_seq_len, rope_dim/2] (MLA's own RopeCache) */
+};
+
+struct ref_lat_kv {
+    const ref_lat *m;
+    int n_layers, capacity, len;
+    float **ckv, **kr; /* per layer [capacity, latent], [capacity, rope] (cache-rounded values) */
+};
+
+static int lat_id(const ref_lat *m, int l, int which) { return 1 + l * m->per_layer + which; }
+static int lat_expert_id(const ref_lat *m, int l, int e, int part) {
+    return 1 + l * m->per_layer + X_FIXED + 3 * e + part; /* part: 0 gate, 1 up, 2 down */
+}
+static int lat_final_id(const ref_lat *m) { return 1 + m->cfg.n_layers * m->per_layer; }
+
+ref_lat *ref_lat_create(const ref_lat_config *c) {
+    if (c->vocab_size <= 0 || c->hidden_dim <= 0 || c->n_layers <= 0 || c->n_heads <= 0 ||
+        c->max_seq_len <= 0 || c->latent_dim <= 0 || c->rope_dim <= 0 || (c->rope_dim & 1) ||
+        c->nope_dim <= 0 || c->v_dim <= 0 || c->n_experts < 2 || c->top_k < 1 ||
+        c->top_k > c->n_experts || c->expert_dim <= 0 || c->n_shared < 0)
+        return NULL;
+    ref_lat *m = (ref_lat *)calloc(1, sizeof(ref_lat));
+    m->cfg = *c;
+    m->per_layer = X_FIXED + 3 * (c->n_experts + c->n_shared);
+    m->n_tensors = 2 + c->n_layers * m->per_layer;
+    m->t = (ref_tensor *)calloc((size_t)m->n_tensors, sizeof(ref_tensor));
+    int64_t H = c->hidden_dim, h = c->n_heads, D = c->expert_dim;
+    char nm[96];
+    set_info(&m->t[0], "embedding.weight", c->vocab_size, H, REF_T_EMBED);
+    for (int l = 0; l < c->n_layers; l++) {
+#define XT(which, suffix, r, cc, k)                                                                \
+    snprintf(nm, sizeof(nm), "blocks.%d.%s", l, suffix);                                           \
+    set_info(&m->t[lat_id(m, l, which)], nm, r, cc, k);
+        XT(X_NORM1, "norm1.weight", 1, H, REF_T_NORM)
+        XT(X_QP, "attn.q_proj.weight", h * (c->nope_dim + c->rope_dim), H, REF_T_LINEAR)
+        XT(X_KVA, "attn.kv_a_proj.weight", c->latent_dim, H, REF_T_LINEAR)
+        XT(X_KVN, "attn.kv_a_norm.weight", 1, c->latent_dim, REF_T_NORM)
+        XT(X_UPK, "attn.up_k.weight", h * c->nope_dim, c->latent_dim, REF_T_LINEAR)
+        XT(X_UPV, "attn.up_v.weight", h * c->v_dim, c->latent_dim, REF_T_LINEAR)
+        XT(X_KRP, "attn.k_rope_proj.weight", c->rope_dim, H, REF_T_LINEAR)
+        XT(X_OP, "attn.o_proj.weight", H, h * c->v_dim, REF_T_LINEAR)
+        XT(X_NORM2, "norm2.weight", 1, H, REF_T_NORM)
+        XT(X_ROUTER, "ffn.router.weight", c->n_experts, H, REF_T_LINEAR)
+#undef XT
+        for (int e = 0; e < c->n_experts + c->n_shared; e++) {
+            const char *grp = e < c->n_experts ? "experts" : "shared_experts";
+            int ei = e < c->n_experts ? e : e - c->n_experts;
+            snprintf(nm, sizeof(nm), "blocks.%d.ffn.%s.%d.w_gate.weight", l, grp, ei);
+            set_info(&m->t[lat_expert_id(m, l, e, 0)], nm, D, H, REF_T_LINEAR);
+            snprintf(nm, sizeof(nm), "blocks.%d.ffn.%s.%d.w_up.weight", l, grp, ei);
+            set_info(&m->t[lat_expert_id(m, l, e, 1)], nm, D, H, REF_T_LINEAR);
+            snprintf(nm, sizeof(nm), "blocks.%d.ffn.%s.%d.w_down.weight", l, grp, ei);
+            set_info(&m->t[lat_expert_id(m, l, e, 2)], nm, H, D, REF_T_LINEAR);
+        }
+    }
+    set_info(&m->t[lat_final_id(m)], "final_norm.weight", 1, H, REF_T_NORM);
+    for (int i = 0; i < m->n_tensors; i++) {
+        ref_tensor *t = &m->t[i];
+        t->data = (float *)calloc((size_t)(t->rows * t->cols), sizeof(float));
+        if (!t->data) {
+            ref_lat_free(m);
+            return NULL;
+        }
+        if (t->kind == REF_T_NORM)
+            for (int64_t j = 0; j < t->rows * t->cols; j++) t->data[j] = 1.0f;
+    }
+    /* dedicated rope_dim-wide RoPE table (model.rs:1112-1118, rope_scaling.rs:6-11) */
+    int half = c->rope_dim / 2, S = c->max_seq_len;
+    m->rope_cos = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
+    m->rope_sin = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
+    for (int i = 0; i < half; i++) {
+        float inv = (float)(1.0 / pow((double)c->rope_theta, 2.0 * (double)i / (double)c->rope_dim));
+        for (int p = 0; p < S; p++) {
+            float a = (float)p * inv;
+            m->rope_cos[(size_t)p * half + i] = cosf(a);
+            m->rope_sin[(size_t)p * half + i] = sinf(a);
+        }
+    }
+    return m;
+}
+
+void ref_lat_free(ref_lat *m) {
+    if (!m) return;
+    for (int i = 0; i < m->n_tensors; i++) free(m->t[i].data);
+    free(m->t);
+    free(m->rope_cos);
+    free(m->rope_sin);
+    free(m);
+}
+
+int ref_lat_num_tensors(const ref_lat *m) { return m->n_tensors; }
+
+int ref_lat_tensor_info(const ref_lat *m, int id, char *name, int name_cap, int64_t *rows, int64_t *cols,
+                        int32_t *kind) {
+    if (id < 0 || id >= m->n_tensors) return REF_ERR_SHAPE;
+    snprintf(name, (size_t)name_cap, "%s", m->t[id].name);
+    *rows = m->t[id].rows;
+    *cols = m->t[id].cols;
+    *kind = m->t[id].kind;
+    return REF_OK;
+}
+
+/* Storage format of a tensor: experts in expert_format, MLA projections and the
+   router in attn_format, the tied embedding per lm_head_format. */
+static int lat_format(const ref_lat *m, int id) {
+    const ref_tensor *t = &m->t[id];
+    if (t->kind == REF_T_EMBED) return m->cfg.lm_head_format == 1 ? REF_W_BF16 : REF_W_F32;
+    if (id == 0 || id == lat_final_id(m)) return REF_W_F32;
+    int w = (id - 1) % m->per_layer;
+    return w >= X_FIXED ? m->cfg.expert_format : m->cfg.attn_format;
+}
+
+int ref_lat_set_tensor(ref_lat *m, int id, const float *raw) {
+    if (id < 0 || id >= m->n_tensors) return REF_ERR_SHAPE;
+    ref_tensor *t = &m->t[id];
+    int64_t n = t->rows * t->cols;
+    if (t->kind == REF_T_NORM) {
+        memcpy(t->data, raw, sizeof(float) * (size_t)n);
+        return REF_OK;
+    }
+    int fmt = lat_format(m, id);
+    if (fmt == REF_W_F32) {
+        memcpy(t->data, raw, sizeof(float) * (size_t)n);
+    } else if (fmt == REF_W_BF16) {
+        for (int64_t i = 0; i < n; i++) t->data[i] = ref_bf16_to_f32(ref_f32_to_bf16(raw[i]));
+    } else if (fmt == REF_W_INT8_ROW) {
+        int8_t *codes = (int8_t *)malloc((size_t)n);
+        float *sc = (float *)malloc(sizeof(float) * (size_t)t->rows);
+        ref_quantise_i8_rows(raw, t->rows, t->cols, codes, sc);
+        for (int64_t r = 0; r < t->rows; r++)
+            for (int64_t c = 0; c < t->cols; c++) t->data[r * t->cols + c] = (float)codes[r * t->cols + c] * sc[r];
+        free(codes);
+        free(sc);
+    } else if (fmt == REF_W_INT4_G128) {
+        if (t->cols % 128) return REF_ERR_SHAPE;
+        int64_t ng = n / 128;
+        uint8_t *packed = (uint8_t *)malloc((size_t)(n / 2));
+        uint16_t *sh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)ng);
+        uint16_t *zh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)ng);
+        ref_quantise_i4_f16(raw, n, 128, packed, sh, zh);
+        ref_dequantise_i4_f16(packed, n, 128, sh, zh, t->data);
+        free(packed);
+        free(sh);
+        free(zh);
+    } else {
+        return REF_ERR_UNSUPPORTED;
+    }
+    return REF_OK;
+}
+
+int ref_lat_get_tensor(const ref_lat *m, int id, float *out) {
+    if (id < 0 || id >= m->n_tensors) return REF_ERR_SHAPE;
+    memcpy(out, m->t[id].data, sizeof(float) * (size_t)(m->t[id].rows * m->t[id].cols));
+    return REF_OK;
+}
+
+ref_lat_kv *ref_lat_kv_create(const ref_lat *m, int capacity) {
+    ref_lat_kv *kv = (ref_lat_kv *)calloc(1, sizeof(ref_lat_kv));
+    kv->m = m;
+    kv->n_layers = m->cfg.n_layers;
+    kv->capacity = capacity;
+    kv->ckv = (float **)calloc((size_t)kv->n_layers, sizeof(float *));
+    kv->kr = (float **)calloc((size_t)kv->n_layers, sizeof(float *));
+    for (int l = 0; l < kv->n_layers; l++) {
+        kv->ckv[l] = (float *)calloc((size_t)capacity * (size_t)m->cfg.latent_dim, sizeof(float));
+        kv->kr[l] = (float *)calloc((size_t)capacity * (size_t)m->cfg.rope_dim, sizeof(float));
+        if (!kv->ckv[l] || !kv->kr[l]) {
+            ref_lat_kv_free(kv);
+            return NULL;
+        }
+    }
+    return kv;
+}
+
+void ref_lat_kv_free(ref_lat_kv *kv) {
+    if (!kv) return;
+    for (int l = 0; l < kv->n_layers; l++) {
+        if (kv->ckv) free(kv->ckv[l]);
+        if (kv->kr) free(kv->kr[l]);
+    }
+    free(kv->ckv);
+    free(kv->kr);
+    free(kv);
+}
+
+int ref_lat_kv_truncate(ref_lat_kv *kv, int new_len) {
+    if (new_len < 0 || new_len > kv->len) return REF_ERR_SHAPE;
+    kv->len = new_len;
+    return REF_OK;
+}
+
+static float lat_cache_round(const ref_lat *m, float v) {
+    return m->cfg.kv_format == REF_KV_F16 ? ref_f16_to_f32(ref_f32_to_f16(v)) : v;
+}
+
+/* Synthetic latent cache: c_kv and k_rope ~ N(0, 1), streams per layer. */
+int ref_lat_kv_fill_synthetic(ref_lat_kv *kv, uint64_t seed, int len) {
+    const ref_lat *m = kv->m;
+    if (len > kv->capacity) return REF_ERR_SHAPE;
+    int lat = m->cfg.latent_dim, rd = m->cfg.rope_dim;
+    for (int l = 0; l < m->cfg.n_layers; l++) {
+        for (int64_t i = 0; i < (int64_t)len * lat; i++)
+            kv->ckv[l][i] = lat_cache_round(m, ref_synth_normal(seed, 0x4C410000u + (uint32_t)(2 * l), (uint64_t)i));
+        for (int64_t i = 0; i < (int64_t)len * rd; i++)
+            kv->kr[l][i] = lat_cache_round(m, ref_synth_normal(seed, 0x4C410001u + (uint32_t)(2 * l), (uint64_t)i));
+    }
+    kv->len = len;
+    return REF_OK;
+}
+
+/* RoPE of one rope_dim slice at position pos (rope.rs:107-126 on the MLA table). */
+static void lat_rope(const ref_lat *m, float *v, int pos) {
+    int half = m->cfg.rope_dim / 2;
+    const float *c = m->rope_cos + (size_t)pos * half, *sn = m->rope_sin + (size_t)pos * half;
+    for (int i = 0; i < half; i++) {
+        float x1 = v[i], x2 = v[i + half];
+        v[i] = x1 * c[i] - x2 * sn[i];
+        v[i + half] = x1 * sn[i] + x2 * c[i];
+    }
+}
+
+/*
+ * top_k_gating (moe.rs:361-406): arg_sort_last_dim(descending), the first k
+ * indices, softmax over the selected logits.  Equal logits keep the lower
+ * expert index first (a stable descending sort).  idx/w are [rows][k].
+ */
+void ref_topk_gating(const float *logits, int rows, int E, int k, int32_t *idx, float *w) {
+    for (int r = 0; r < rows; r++) {
+        const float *l = logits + (int64_t)r * E;
+        ranked_t *rk = (ranked_t *)malloc(sizeof(ranked_t) * (size_t)E);
+        for (int e = 0; e < E; e++) rk[e] = (ranked_t){l[e], e};
+        qsort(rk, (size_t)E, sizeof(ranked_t), cmp_ranked_desc);
+        float mx = -INFINITY;
+        for (int j = 0; j < k; j++) mx = fmaxf(mx, rk[j].v);
+        float s = 0.0f;
+        for (int j = 0; j < k; j++) {
+            idx[(int64_t)r * k + j] = (int32_t)rk[j].i;
+            w[(int64_t)r * k + j] = expf(rk[j].v - mx);
+            s += w[(int64_t)r * k + j];
+        }
+        for (int j = 0; j < k; j++) w[(int64_t)r * k + j] /= s;
+        free(rk);
+    }
+}
+
+/* SwiGluFfn::forward (ffn.rs:29-37) of expert e on S rows of h (rows x H) -> y. */
+static void lat_expert(const ref_lat *m, int l, int e, const float *h, int S, float *y, int nt) {
+    int64_t H = m->cfg.hidden_dim, D = m->cfg.expert_dim;
+    float *g = (float *)malloc(sizeof(float) * (size_t)(S * D));
+    float *u = (float *)malloc(sizeof(float) * (size_t)(S * D));
+    linear(h, S, H, m->t[lat_expert_id(m, l, e, 0)].data, D, g, nt);
+    linear(h, S, H, m->t[lat_expert_id(m, l, e, 1)].data, D, u, nt);
+    for (int64_t i = 0; i < (int64_t)S * D; i++) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+    linear(g, S, D, m->t[lat_expert_id(m, l, e, 2)].data, H, y, nt);
+    free(g);
+    free(u);
+}
+
+static void lat_block(const ref_lat *m, int l, float *x, int S, int pos0, ref_lat_kv *kv, int nt) {
+    const ref_lat_config *c = &m->cfg;
+    int64_t H = c->hidden_dim;
+    int nh = c->n_heads, nope = c->nope_dim, rd = c->rope_dim, lat = c->latent_dim, vd = c->v_dim;
+    int qw = nope + rd;
+    float *h = (float *)malloc(sizeof(float) * (size_t)(S * H));
+    rms_norm(x, S, H, m->t[lat_id(m, l, X_NORM1)].data, c->norm_eps, h);
+    /* project (mla.rs:402-449) */
+    float *q = (float *)malloc(sizeof(float) * (size_t)S * nh * qw);
+    float *ck = (float *)malloc(sizeof(float) * (size_t)S * lat);
+    float *ckn = (float *)malloc(sizeof(float) * (size_t)S * lat);
+    float *kr = (float *)malloc(sizeof(float) * (size_t)S * rd);
+    linear(h, S, H, m->t[lat_id(m, l, X_QP)].data, (int64_t)nh * qw, q, nt);
+    linear(h, S, H, m->t[lat_id(m, l, X_KVA)].data, lat, ck, nt);
+    rms_norm(ck, S, lat, m->t[lat_id(m, l, X_KVN)].data, c->norm_eps, ckn);
+    linear(h, S, H, m->t[lat_id(m, l, X_KRP)].data, rd, kr, nt);
+    for (int s = 0; s < S; s++) {
+        for (int hh = 0; hh < nh; hh++) lat_rope(m, q + ((int64_t)s * nh + hh) * qw + nope, pos0 + s);
+        lat_rope(m, kr + (int64_t)s * rd, pos0 + s);
+        for (int i = 0; i < lat; i++) kv->ckv[l][(int64_t)(pos0 + s) * lat + i] = lat_cache_round(m, ckn[(int64_t)s * lat + i]);
+        for (int i = 0; i < rd; i++) kv->kr[l][(int64_t)(pos0 + s) * rd + i] = lat_cache_round(m, kr[(int64_t)s * rd + i]);
+    }
+    /* attend (mla.rs:451-489): reconstruct K_nope and V over the whole cache */
+    int T = pos0 + S;
+    float *kn = (float *)malloc(sizeof(float) * (size_t)T * nh * nope);
+    float *vv = (float *)malloc(sizeof(float) * (size_t)T * nh * vd);
+    linear(kv->ckv[l], T, lat, m->t[lat_id(m, l, X_UPK)].data, (int64_t)nh * nope, kn, nt);
+    linear(kv->ckv[l], T, lat, m->t[lat_id(m, l, X_UPV)].data, (int64_t)nh * vd, vv, nt);
+    float scale = (float)(1.0 / sqrt((double)qw));
+    float *att = (float *)malloc(sizeof(float) * (size_t)S * nh * vd);
+#pragma omp parallel for num_threads(nt) schedule(static) collapse(2)
+    for (int hh = 0; hh < nh; hh++)
+        for (int s = 0; s < S; s++) {
+            const float *qq = q + ((int64_t)s * nh + hh) * qw;
+            int lim = pos0 + s; /* causal: shift kv_len - q_len */
+            float mx = -INFINITY, l_ = 0.0f;
+            float *o = att + ((int64_t)s * nh + hh) * vd;
+            for (int i = 0; i < vd; i++) o[i] = 0.0f;
+            for (int t = 0; t <= lim; t++) {
+                float sc = (dotf(qq, kn + ((int64_t)t * nh + hh) * nope, nope) +
+                            dotf(qq + nope, kv->kr[l] + (int64_t)t * rd, rd)) * scale;
+                float mnew = fmaxf(mx, sc);
+                float a = mx == -INFINITY ? 0.0f : expf(mx - mnew);
+                float p = expf(sc - mnew);
+                l_ = l_ * a + p;
+                const float *vr = vv + ((int64_t)t * nh + hh) * vd;
+                for (int i = 0; i < vd; i++) o[i] = o[i] * a + p * vr[i];
+                mx = mnew;
+            }
+            for (int i = 0; i < vd; i++) o[i] /= l_;
+        }
+    float *y = (float *)malloc(sizeof(float) * (size_t)(S * H));
+    linear(att, S, (int64_t)nh * vd, m->t[lat_id(m, l, X_OP)].data, H, y, nt);
+    for (int64_t i = 0; i < (int64_t)S * H; i++) x[i] += y[i];
+    /* MoE FFN (moe.rs:212-340) */
+    rms_norm(x, S, H, m->t[lat_id(m, l, X_NORM2)].data, c->norm_eps, h);
+    int E = c->n_experts, K = c->top_k;
+    float *rl = (float *)malloc(sizeof(float) * (size_t)S * E);
+    linear(h, S, H, m->t[lat_id(m, l, X_ROUTER)].data, E, rl, nt);
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * K);
+    float *w = (float *)malloc(sizeof(float) * (size_t)S * K);
+    ref_topk_gating(rl, S, E, K, idx, w);
+    float *acc = (float *)calloc((size_t)(S * H), sizeof(float));
+    float *ye = (float *)malloc(sizeof(float) * (size_t)H);
+    for (int s = 0; s < S; s++) {
+        /* routed: dispatch-weighted sum over experts in index order (unselected add 0) */
+        for (int e = 0; e < E; e++) {
+            float we = 0.0f;
+            int sel = 0;
+            for (int j = 0; j < K; j++)
+                if (idx[(int64_t)s * K + j] == e) {
+                    we = w[(int64_t)s * K + j];
+                    sel = 1;
+                }
+            if (!sel) continue;
+            lat_expert(m, l, e, h + (int64_t)s * H, 1, ye, 1);
+            for (int64_t i = 0; i < H; i++) acc[(int64_t)s * H + i] += ye[i] * we;
+        }
+        /* shared experts, summed in order, then added to the routed output */
+        if (c->n_shared > 0) {
+            float *sh = (float *)calloc((size_t)H, sizeof(float));
+            for (int e = 0; e < c->n_shared; e++) {
+                lat_expert(m, l, E + e, h + (int64_t)s * H, 1, ye, 1);
+                for (int64_t i = 0; i < H; i++) sh[i] = e == 0 ? ye[i] : sh[i] + ye[i];
+            }
+            for (int64_t i = 0; i < H; i++) acc[(int64_t)s * H + i] += sh[i];
+            free(sh);
+        }
+    }
+    for (int64_t i = 0; i < (int64_t)S * H; i++) x[i] += acc[i];
+    free(h); free(q); free(ck); free(ckn); free(kr); free(kn); free(vv); free(att); free(y);
+    free(rl); free(idx); free(w); free(acc); free(ye);
+}
+
+int ref_lat_forward(const ref_lat *m, ref_lat_kv *kv, const uint32_t *ids, int S, int offset, float *logits,
+                    float *hidden, int nt) {
+    const ref_lat_config *c = &m->cfg;
+    if (S <= 0 || offset + S > c->max_seq_len) return REF_ERR_SHAPE;
+    if (!kv || offset > kv->len || offset + S > kv->capacity) return REF_ERR_SHAPE;
+    int64_t H = c->hidden_dim, V = c->vocab_size;
+    for (int s = 0; s < S; s++)
+        if ((int64_t)ids[s] >= V) return REF_ERR_SHAPE;
+    kv->len = offset;
+    float *x = (float *)malloc(sizeof(float) * (size_t)(S * H));
+    const float *emb = m->t[0].data;
+    for (int s = 0; s < S; s++) memcpy(x + s * H, emb + (int64_t)ids[s] * H, sizeof(float) * (size_t)H);
+    for (int l = 0; l < c->n_layers; l++) lat_block(m, l, x, S, offset, kv, nt);
+    kv->len = offset + S;
+    float *hn = (float *)malloc(sizeof(float) * (size_t)(S * H));
+    rms_norm(x, S, H, m->t[lat_final_id(m)].data, c->norm_eps, hn);
+    if (hidden) memcpy(hidden, hn, sizeof(float) * (size_t)(S * H));
+    if (logits) linear(hn, S, H, emb, V, logits, nt);
+    free(hn);
+    free(x);
+    return REF_OK;
+}

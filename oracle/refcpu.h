@@ -155,6 +155,35 @@ int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_le
                        int max_new_tokens, const ref_sampler *s, uint64_t seed, int nthreads,
                        uint32_t *out_tokens, int *out_len, int *finish_reason);
 
+/* ---------------- Latent-attention MoE decoder ---------------- */
+typedef struct {
+    int32_t vocab_size, hidden_dim, n_layers, n_heads, max_seq_len;
+    float rope_theta, norm_eps;
+    int32_t latent_dim, rope_dim, nope_dim, v_dim;   /* MLA (nn/src/mla.rs) */
+    int32_t n_experts, top_k, expert_dim, n_shared;  /* routed fine experts, top-k, fine width, shared */
+    int32_t expert_format;                           /* routed + shared expert weights (REF_W_*) */
+    int32_t attn_format;                             /* MLA projections and the router */
+    int32_t lm_head_format;                          /* 0 f32, 1 bf16 */
+    int32_t kv_format;                               /* latent cache: REF_KV_F32 or REF_KV_F16 */
+} ref_lat_config;
+
+typedef struct ref_lat ref_lat;
+typedef struct ref_lat_kv ref_lat_kv;
+ref_lat *ref_lat_create(const ref_lat_config *cfg);
+void ref_lat_free(ref_lat *m);
+int ref_lat_num_tensors(const ref_lat *m);
+int ref_lat_tensor_info(const ref_lat *m, int id, char *name, int name_cap, int64_t *rows, int64_t *cols,
+                        int32_t *kind);
+int ref_lat_set_tensor(ref_lat *m, int id, const float *raw);
+int ref_lat_get_tensor(const ref_lat *m, int id, float *out);
+ref_lat_kv *ref_lat_kv_create(const ref_lat *m, int capacity);
+void ref_lat_kv_free(ref_lat_kv *kv);
+int ref_lat_kv_truncate(ref_lat_kv *kv, int new_len);
+int ref_lat_kv_fill_synthetic(ref_lat_kv *kv, uint64_t seed, int len);
+int ref_lat_forward(const ref_lat *m, ref_lat_kv *kv, const uint32_t *ids, int S, int offset, float *logits,
+                    float *hidden, int nthreads);
+void ref_topk_gating(const float *logits, int rows, int E, int k, int32_t *idx, float *w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,14 @@ class RefConfig(C.Structure):
                                           "lm_head_format", "kv_format")]
 
 
+class RefLatConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab_size", "hidden_dim", "n_layers", "n_heads", "max_seq_len")] + \
+               [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
+               [(n, C.c_int32) for n in ("latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
+                                          "expert_dim", "n_shared", "expert_format", "attn_format",
+                                          "lm_head_format", "kv_format")]
+
+
 class RefSpecStats(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("rounds", "draft_tokens_proposed", "draft_tokens_accepted",
                                           "draft_tokens_rejected", "target_decode_forwards",
@@ -127,6 +135,20 @@ def lib():
         "ref_spec_generate": (C.c_int, [C.c_void_p, C.c_void_p, U32P, C.c_int, C.c_int, C.c_int,
                                         C.POINTER(RefSampler), C.c_uint64, C.c_int, U32P, C.POINTER(C.c_int),
                                         C.POINTER(C.c_int), C.POINTER(RefSpecStats), C.POINTER(C.c_float)]),
+        "ref_lat_create": (C.c_void_p, [C.POINTER(RefLatConfig)]),
+        "ref_lat_free": (None, [C.c_void_p]),
+        "ref_lat_num_tensors": (C.c_int, [C.c_void_p]),
+        "ref_lat_tensor_info": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int64),
+                                          C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+        "ref_lat_set_tensor": (C.c_int, [C.c_void_p, C.c_int, F32P]),
+        "ref_lat_get_tensor": (C.c_int, [C.c_void_p, C.c_int, F32P]),
+        "ref_lat_kv_create": (C.c_void_p, [C.c_void_p, C.c_int]),
+        "ref_lat_kv_free": (None, [C.c_void_p]),
+        "ref_lat_kv_truncate": (C.c_int, [C.c_void_p, C.c_int]),
+        "ref_lat_kv_fill_synthetic": (C.c_int, [C.c_void_p, C.c_uint64, C.c_int]),
+        "ref_lat_forward": (C.c_int, [C.c_void_p, C.c_void_p, U32P, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                      C.c_int]),
+        "ref_topk_gating": (None, [F32P, C.c_int, C.c_int, C.c_int, I32P, F32P]),
         "ref_plain_generate": (C.c_int, [C.c_void_p, U32P, C.c_int, C.c_int, C.POINTER(RefSampler), C.c_uint64,
                                          C.c_int, U32P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     }
@@ -456,3 +478,101 @@ class KvCache:
         if st:
             raise ValueError(f"forward_layers failed: status {st}")
         return logits
+
+
+# ---------------- latent-attention MoE decoder ----------------
+def make_lat_config(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, latent_dim, rope_dim, nope_dim, v_dim,
+                    n_experts, top_k, expert_dim, n_shared, expert_format=W_F32, attn_format=W_F32,
+                    lm_head_format=0, kv_format=KV_F32, rope_theta=10000.0, norm_eps=1e-5):
+    return RefLatConfig(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, rope_theta, norm_eps, latent_dim,
+                        rope_dim, nope_dim, v_dim, n_experts, top_k, expert_dim, n_shared, expert_format,
+                        attn_format, lm_head_format, kv_format)
+
+
+def topk_gating(logits, k):
+    """top_k_gating (moe.rs:361-406): selected expert indices and softmax weights per row."""
+    logits = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
+    rows, E = logits.shape
+    idx = np.zeros((rows, k), np.int32)
+    w = np.zeros((rows, k), np.float32)
+    lib().ref_topk_gating(logits, rows, E, k, idx, w)
+    return idx, w
+
+
+class LatModel:
+    """MLA + MoE decoder oracle (mla.rs:300-489, moe.rs:212-406), f32 compute on the
+    effective (dequantised) weights."""
+
+    def __init__(self, cfg):
+        self.cfg = cfg
+        self.h = lib().ref_lat_create(C.byref(cfg))
+        if not self.h:
+            raise ValueError("invalid latent MoE config")
+
+    def close(self):
+        if self.h:
+            lib().ref_lat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def tensors(self):
+        out = []
+        for i in range(lib().ref_lat_num_tensors(self.h)):
+            name = C.create_string_buffer(128)
+            r, c, k = C.c_int64(), C.c_int64(), C.c_int32()
+            lib().ref_lat_tensor_info(self.h, i, name, 128, C.byref(r), C.byref(c), C.byref(k))
+            out.append((name.value.decode(), r.value, c.value, k.value))
+        return out
+
+    def get(self, i):
+        name, r, c, k = self.tensors()[i]
+        out = np.zeros(r * c, np.float32)
+        lib().ref_lat_get_tensor(self.h, i, out)
+        return out.reshape(r, c)
+
+    def set(self, i, raw):
+        st = lib().ref_lat_set_tensor(self.h, i, np.ascontiguousarray(raw, np.float32).ravel())
+        if st:
+            raise ValueError(f"set_tensor {i} failed: {st}")
+
+    def kv(self, capacity):
+        return LatKv(self, capacity)
+
+
+class LatKv:
+    def __init__(self, model, capacity):
+        self.model = model
+        self.h = lib().ref_lat_kv_create(model.h, capacity)
+        if not self.h:
+            raise MemoryError("oracle latent cache allocation failed")
+
+    def close(self):
+        if self.h:
+            lib().ref_lat_kv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def truncate(self, n):
+        st = lib().ref_lat_kv_truncate(self.h, n)
+        if st:
+            raise ValueError(f"truncate failed: {st}")
+
+    def fill_synthetic(self, seed, length):
+        st = lib().ref_lat_kv_fill_synthetic(self.h, seed, length)
+        if st:
+            raise ValueError(f"fill failed: {st}")
+
+    def forward(self, ids, offset, want_hidden=True, nthreads=8):
+        cfg = self.model.cfg
+        ids = np.ascontiguousarray(ids, np.uint32)
+        S = len(ids)
+        logits = np.zeros((S, cfg.vocab_size), np.float32)
+        hidden = np.zeros((S, cfg.hidden_dim), np.float32) if want_hidden else None
+        st = lib().ref_lat_forward(self.model.h, self.h, ids, S, offset, _ptr(logits), _ptr(hidden), nthreads)
+        if st:
+            raise ValueError(f"forward failed: status {st}")
+        return logits, hidden

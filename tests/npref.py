@@ -70,3 +70,63 @@ def mtp_head(W, cfg, head, anchor, ids):
     x = np.stack(loc)
     x = block(W, pre + "refine.", x, cfg, np.arange(len(loc), dtype=np.float64))
     return rms(x[-1], W[pre + "output_norm.weight"], cfg.norm_eps) @ E.T
+
+
+def lat_block(W, pre, x, cfg, pos, absorbed=False):
+    """MLA (mla.rs:402-489) + MoE (moe.rs:212-406) block in float64.  The MoE runs
+    every expert densely and weights it by the dispatch weight (0 when not
+    selected), as the reference does; absorbed=True evaluates attention in the
+    latent space (q . up_k c = (up_k^T q) . c, o = up_v (P c)) instead of
+    reconstructing K and V."""
+    S, H = x.shape
+    nh, nope, rd, lat, vd = cfg.n_heads, cfg.nope_dim, cfg.rope_dim, cfg.latent_dim, cfg.v_dim
+    xn = rms(x, W[pre + "norm1.weight"], cfg.norm_eps)
+    q = (xn @ W[pre + "attn.q_proj.weight"].T).reshape(S, nh, nope + rd)
+    qn, qr = q[..., :nope], rope(q[..., nope:], pos, cfg.rope_theta)
+    c = rms(xn @ W[pre + "attn.kv_a_proj.weight"].T, W[pre + "attn.kv_a_norm.weight"], cfg.norm_eps)
+    kr = rope((xn @ W[pre + "attn.k_rope_proj.weight"].T)[:, None, :], pos, cfg.rope_theta)[:, 0]
+    upk = W[pre + "attn.up_k.weight"].reshape(nh, nope, lat)
+    upv = W[pre + "attn.up_v.weight"].reshape(nh, vd, lat)
+    mask = np.tril(np.ones((S, S), bool))
+    out = np.zeros((S, nh, vd))
+    for h in range(nh):
+        if absorbed:
+            ql = qn[:, h] @ upk[h]                      # [S, lat]
+            sc = (ql @ c.T + qr[:, h] @ kr.T) / np.sqrt(nope + rd)
+        else:
+            kn = c @ upk[h].T                            # [T, nope]
+            sc = (qn[:, h] @ kn.T + qr[:, h] @ kr.T) / np.sqrt(nope + rd)
+        sc = np.where(mask, sc, -np.inf)
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        out[:, h] = (p @ c) @ upv[h].T if absorbed else p @ (c @ upv[h].T)
+    x = x + out.reshape(S, nh * vd) @ W[pre + "attn.o_proj.weight"].T
+    xn = rms(x, W[pre + "norm2.weight"], cfg.norm_eps)
+    logits = xn @ W[pre + "ffn.router.weight"].T
+    E, K = cfg.n_experts, cfg.top_k
+    disp = np.zeros((S, E))
+    for s in range(S):
+        order = sorted(range(E), key=lambda e: (-logits[s, e], e))[:K]
+        sel = logits[s, order]
+        w = np.exp(sel - sel.max())
+        disp[s, order] = w / w.sum()
+
+    def expert(name):
+        g = xn @ W[name + "w_gate.weight"].T
+        u = xn @ W[name + "w_up.weight"].T
+        return (g / (1 + np.exp(-g)) * u) @ W[name + "w_down.weight"].T
+
+    y = sum(expert(pre + f"ffn.experts.{e}.") * disp[:, e:e + 1] for e in range(E))
+    for e in range(cfg.n_shared):
+        y = y + expert(pre + f"ffn.shared_experts.{e}.")
+    return x + y
+
+
+def lat_forward(W, cfg, ids, absorbed=False):
+    E = W["embedding.weight"]
+    x = E[np.asarray(ids, np.int64)]
+    pos = np.arange(len(ids), dtype=np.float64)
+    for l in range(cfg.n_layers):
+        x = lat_block(W, f"blocks.{l}.", x, cfg, pos, absorbed)
+    hn = rms(x, W["final_norm.weight"], cfg.norm_eps)
+    return hn @ E.T, hn
