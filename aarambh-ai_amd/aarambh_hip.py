@@ -63,6 +63,14 @@ class _Cfg(C.Structure):
                                           "max_batch", "max_rows")]
 
 
+class _LatCfg(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab_size", "hidden_dim", "n_layers", "n_heads", "max_seq_len")] + \
+               [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
+               [(n, C.c_int32) for n in ("latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
+                                          "expert_dim", "n_shared", "expert_format", "attn_format",
+                                          "lm_head_format", "kv_format", "max_batch", "max_rows")]
+
+
 class _Sampler(C.Structure):
     _fields_ = [("greedy", C.c_int32), ("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float)]
 
@@ -120,6 +128,23 @@ def lib():
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
+        "aarh_lat_create": (C.c_int, [C.c_int, C.POINTER(_LatCfg), C.POINTER(_P)]),
+        "aarh_lat_destroy": (None, [_P]),
+        "aarh_lat_last_error": (C.c_char_p, [_P]),
+        "aarh_lat_num_tensors": (C.c_int, [_P]),
+        "aarh_lat_tensor_info": (C.c_int, [_P, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int64),
+                                           C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+        "aarh_lat_load_tensor_f32": (C.c_int, [_P, C.c_int, _P, C.c_int64]),
+        "aarh_lat_init_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float]),
+        "aarh_lat_kv_len": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
+        "aarh_lat_kv_rollback": (C.c_int, [_P, C.c_int, C.c_int32]),
+        "aarh_lat_kv_fill_synthetic": (C.c_int, [_P, C.c_int, C.c_int32, C.c_uint64]),
+        "aarh_lat_forward": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, _P, _P]),
+        "aarh_lat_router_gaps": (C.c_int, [_P, _P]),
+        "aarh_lat_expert_counts": (C.c_int, [_P, _P]),
+        "aarh_lat_prof_enable": (C.c_int, [_P, C.c_int]),
+        "aarh_lat_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                        C.POINTER(C.c_int64)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -134,7 +159,11 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_init_synthetic", "aarh_kv_reset", "aarh_kv_len", "aarh_kv_rollback", "aarh_kv_fill_synthetic",
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
-            "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get"]
+            "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
+            "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
+            "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
+            "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
+            "aarh_lat_expert_counts", "aarh_lat_prof_enable", "aarh_lat_prof_get"]
 
 
 def _ptr(a):
@@ -493,3 +522,128 @@ class Session:
 
     def __del__(self):
         self.close()
+
+
+# ---------------------------------------------------------------------------
+# Latent-attention MoE decoder
+# ---------------------------------------------------------------------------
+@dataclass
+class LatConfig:
+    """MLA (nn/src/mla.rs:300-489) + fine-grained MoE (nn/src/moe.rs:127-406) decoder shape."""
+    vocab_size: int
+    hidden_dim: int
+    n_layers: int
+    n_heads: int
+    max_seq_len: int
+    latent_dim: int = 512
+    rope_dim: int = 64
+    nope_dim: int = 128
+    v_dim: int = 128
+    n_experts: int = 64
+    top_k: int = 6
+    expert_dim: int = 1408
+    n_shared: int = 2
+    expert_format: int = W_INT4_G128
+    attn_format: int = W_INT4_G128
+    lm_head_format: int = W_BF16
+    kv_format: int = KV_F16
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+
+
+class HipLatModel:
+    """Device copy of a latent-attention MoE decoder plus its latent cache slots."""
+
+    def __init__(self, cfg: LatConfig, max_batch=1, max_rows=128, device=0):
+        self.cfg = cfg
+        c = _LatCfg(cfg.vocab_size, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.max_seq_len, cfg.rope_theta,
+                    cfg.norm_eps, cfg.latent_dim, cfg.rope_dim, cfg.nope_dim, cfg.v_dim, cfg.n_experts, cfg.top_k,
+                    cfg.expert_dim, cfg.n_shared, cfg.expert_format, cfg.attn_format, cfg.lm_head_format,
+                    cfg.kv_format, max_batch, max_rows)
+        h = _P()
+        st = lib().aarh_lat_create(device, C.byref(c), C.byref(h))
+        self.h = h
+        if st:
+            msg = lib().aarh_lat_last_error(h).decode() if h else "aarh_lat_create failed"
+            self.close()
+            raise _ERRS.get(st, AarambhError)(msg)
+        self.max_batch = max_batch
+        self.max_rows = max_rows
+        _LIVE.add(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aarh_lat_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _check(self, st):
+        if st:
+            raise _ERRS.get(st, AarambhError)(lib().aarh_lat_last_error(self.h).decode())
+
+    def tensors(self):
+        out = []
+        name = C.create_string_buffer(160)
+        for i in range(lib().aarh_lat_num_tensors(self.h)):
+            r, c, k = C.c_int64(), C.c_int64(), C.c_int32()
+            self._check(lib().aarh_lat_tensor_info(self.h, i, name, 160, C.byref(r), C.byref(c), C.byref(k)))
+            out.append((name.value.decode(), r.value, c.value, k.value))
+        return out
+
+    def load_f32(self, tid, values):
+        v = np.ascontiguousarray(values, np.float32)
+        self._check(lib().aarh_lat_load_tensor_f32(self.h, tid, _ptr(v), v.size))
+
+    def init_synthetic(self, seed=0, std=0.02):
+        self._check(lib().aarh_lat_init_synthetic(self.h, seed, std))
+
+    def kv_len(self, slot=0):
+        v = C.c_int32()
+        self._check(lib().aarh_lat_kv_len(self.h, slot, C.byref(v)))
+        return v.value
+
+    def snapshot(self, slot=0):
+        return self.kv_len(slot)
+
+    def restore(self, snapshot, slot=0):
+        self._check(lib().aarh_lat_kv_rollback(self.h, slot, snapshot))
+
+    def kv_fill_synthetic(self, slot, length, seed=0):
+        self._check(lib().aarh_lat_kv_fill_synthetic(self.h, slot, length, seed))
+
+    def forward_with_cache_output(self, ids, offsets, slots=None, want_logits=True, want_hidden=True):
+        """ids [nseq, S]; returns (logits [nseq, S, V], hidden [nseq, S, H])."""
+        ids = np.ascontiguousarray(np.atleast_2d(ids), np.uint32)
+        nseq, S = ids.shape
+        offs = np.ascontiguousarray(np.broadcast_to(np.asarray(offsets, np.int32), (nseq,)), np.int32)
+        sl = np.ascontiguousarray(np.arange(nseq, dtype=np.int32) if slots is None else slots, np.int32)
+        lg = np.empty((nseq, S, self.cfg.vocab_size), np.float32) if want_logits else None
+        hd = np.empty((nseq, S, self.cfg.hidden_dim), np.float32) if want_hidden else None
+        self._check(lib().aarh_lat_forward(self.h, _ptr(ids), _ptr(sl), _ptr(offs), nseq, S, _ptr(lg), _ptr(hd)))
+        self._last_rows = nseq * S
+        return lg, hd
+
+    def router_gaps(self):
+        """Smallest k-th minus (k+1)-th router logit per row of the last forward, over all layers."""
+        out = np.empty(getattr(self, "_last_rows", 0), np.float32)
+        self._check(lib().aarh_lat_router_gaps(self.h, _ptr(out)))
+        return out
+
+    def expert_counts(self):
+        """Rows routed to each expert per layer in the last forward, [n_layers, n_experts + n_shared]."""
+        out = np.empty((self.cfg.n_layers, self.cfg.n_experts + self.cfg.n_shared), np.int32)
+        self._check(lib().aarh_lat_expert_counts(self.h, _ptr(out)))
+        return out
+
+    def prof_enable(self, on=True):
+        self._check(lib().aarh_lat_prof_enable(self.h, 1 if on else 0))
+
+    def prof_get(self):
+        out = {}
+        for i, n in enumerate(PROF_NAMES):
+            ms, by, cnt = C.c_double(), C.c_double(), C.c_int64()
+            self._check(lib().aarh_lat_prof_get(self.h, i, C.byref(ms), C.byref(by), C.byref(cnt)))
+            out[n] = {"ms": ms.value, "bytes": by.value, "launches": cnt.value}
+        return out

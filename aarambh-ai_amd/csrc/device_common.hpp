@@ -9,6 +9,23 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 #define WAVE 64
 
+// Build-defined synthetic generator (same formula as the test oracle):
+// splitmix64 counter hash -> Box-Muller in f64.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ float synth_normal(uint64_t seed, uint32_t stream, uint64_t index) {
+    uint64_t base = splitmix64(seed ^ ((uint64_t)stream * 0xD1B54A32D192ED03ull));
+    uint64_t h = splitmix64(base + index);
+    double u1 = ((double)(h >> 40) + 1.0) * (1.0 / 16777216.0);
+    double u2 = (double)((h >> 16) & 0xFFFFFFull) * (1.0 / 16777216.0);
+    return (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+}
+
 // f32::total_cmp ordering key: larger key == larger value, NaN above +inf.
 __device__ __forceinline__ int32_t total_key(float f) {
     int32_t i = __float_as_int(f);

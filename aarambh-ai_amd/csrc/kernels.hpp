@@ -188,4 +188,72 @@ int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* o
 int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream);
 int launch_fill_f32(float* p, long long n, float v, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// Latent attention (MLA) + fine-grained MoE decoder kernels (lat.hip)
+// ---------------------------------------------------------------------------
+struct MlaArgs {
+    int nseq, S;                 // sequences x rows per sequence (M = nseq * S)
+    int nh, nope, rd, lat;       // heads, nope / rope / latent widths (v width: vd)
+    int vd;
+    const int* pos0;             // [nseq] position of row 0
+    const int* slot;             // [nseq] cache slot
+    const float* raw;            // [M][raw_ld]: q (nh*(nope+rd)) | kv_a (lat) | k_rope (rd)
+    int raw_ld;
+    const float* rope_cos;
+    const float* rope_sin;       // [positions][rd/2]
+    const float* upk;            // [nh*nope][lat] (stored values of up_k)
+    const float* upvT;           // [nh][lat][vd] (up_v transposed per head)
+    const float* kvn_w;          // [lat] latent RMSNorm weight
+    float eps;
+    float* q;                    // [M][nh][lat+rd]: absorbed q_lat | rotated q_rope
+    _Float16* kc;                // [slots][cap][lat+rd]: c_kv | k_rope
+    _Float16* vt;                // [slots][lat][cap]: c_kv transposed
+    int cap;
+    float scale;                 // 1/sqrt(nope + rd)
+    int chunk, nchunks, ntiles;  // tokens per chunk, chunks, 16-row query tiles per sequence
+    int tiles_per_wg;            // query tiles per attention workgroup (1 or 2)
+    float* part;                 // [nseq][ntiles][nchunks][16][lat+4] chunk partials (m, l, pad, pad, o)
+    XFrag fo;                    // fragments of the attention output for o_proj
+    float* out;                  // [M][nh*vd] f32 attention output rows (null: fragments only)
+};
+int launch_mla_qprep(const MlaArgs& a, hipStream_t stream);
+int launch_mla_kvprep(const MlaArgs& a, hipStream_t stream);
+int launch_mla_attn(const MlaArgs& a, hipStream_t stream);
+int launch_mla_out(const MlaArgs& a, hipStream_t stream);
+bool mla_supported(int lat, int rd, int vd, int nope);
+
+struct MoeArgs {
+    int M, E, K, NS;             // rows, routed experts, top-k, shared experts
+    int H, D;                    // hidden, fine expert width
+    const float* logits;         // [M][lld] router logits (first E columns)
+    int lld;
+    int* cnt;                    // [E+NS] assignments per expert
+    int* off;                    // [E+NS+1] their offsets
+    int* arow;                   // [A] token row of each assignment (A = M*(K+NS))
+    float* aw;                   // [A] its dispatch weight (1 for shared experts)
+    int* rowmap;                 // [M][K+NS] assignments of a row: routed in expert order, then shared
+    int fmt;                     // expert weight format (WF_INT4 / WF_INT8 / WF_BF16)
+    const uint8_t* gu;           // tiled [(E+NS)*2D][H], gate/up rows interleaved 8 + 8 per tile
+    const uint32_t* gu_sz;
+    const float* gu_rs;
+    const uint8_t* dn;           // tiled [(E+NS)*H][D]
+    const uint32_t* dn_sz;
+    const float* dn_rs;
+    const float* xn;             // [M][H] normed FFN input (norm2)
+    float* h;                    // [A][D] SwiGLU activations per assignment
+    float* y;                    // [A][H] expert outputs per assignment (unweighted)
+    float* x;                    // [M][H] residual stream
+    XFrag fo;                    // fragments of the new x for the next consumer
+    float* gap;                  // [M] running min of (k-th - (k+1)-th) router logit (null: none)
+};
+int launch_moe_route(const MoeArgs& a, hipStream_t stream);
+int launch_moe_ffn(const MoeArgs& a, int phase, hipStream_t stream);
+int launch_moe_combine(const MoeArgs& a, hipStream_t stream);
+// Row-major f32 copy of a tiled quantised matrix (the values its GEMV multiplies
+// by); tblk > 0 writes row n = b * tblk + i, column k at ((b * K + k) * tblk + i).
+int launch_dequant_tiled(const uint8_t* tiled, const uint32_t* sz, const float* rscale, int fmt, int N, int K,
+                         float* out, int tblk, hipStream_t stream);
+int launch_lat_kv_fill_synthetic(_Float16* kc, _Float16* vt, int slot, int lat, int rd, int cap, int len,
+                                 unsigned long long seed, int layer, hipStream_t stream);
+
 }  // namespace aarh

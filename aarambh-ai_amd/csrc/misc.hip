@@ -124,8 +124,8 @@ int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, 
 }
 
 // Destination row of source row n inside a fused matrix.  interleave 1/2 puts
-// gate/up row f at row (f/8)*16 + f%8 (+8 for up) so a 16-row tile holds 8
-// matching gate and up rows.  interleave = hd (>= 16) pairs RoPE dims within a
+// gate/up row f at row row_offset + (f/8)*16 + f%8 (+8 for up) so a 16-row tile
+// holds 8 matching gate and up rows.  interleave = hd (>= 16) pairs RoPE dims within a
 // head of hd rows: tile j of the head holds dims 8j..8j+7 (rows 0-7) and
 // hd/2 + 8j.. (rows 8-15), so the rotation of a pair stays inside one tile.
 __device__ __forceinline__ int dest_row(int n, int row_offset, int interleave) {
@@ -136,7 +136,7 @@ __device__ __forceinline__ int dest_row(int n, int row_offset, int interleave) {
         const int p = ((d % half) >> 3) * 16 + (d & 7) + (d >= half ? 8 : 0);
         return row_offset + head * hd + p;
     }
-    return (n >> 3) * 16 + (n & 7) + (interleave == 2 ? 8 : 0);
+    return row_offset + (n >> 3) * 16 + (n & 7) + (interleave == 2 ? 8 : 0);
 }
 
 // INT4 g128 quantisation (quant/src/int4.rs:7-41, codes from the f32 scale,
@@ -285,23 +285,6 @@ int launch_repack_int8(const int8_t* codes, const float* sc, int N, int K, uint8
     hipLaunchKernelGGL(repack_int8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, codes, sc, N, K,
                        tiled, rscale, row_offset, interleave);
     return note_error(hipGetLastError()) ? 4 : 0;
-}
-
-// Build-defined synthetic generator (same formula as the test oracle):
-// splitmix64 counter hash -> Box-Muller in f64.
-__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
-    x += 0x9E3779B97F4A7C15ull;
-    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
-    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
-    return x ^ (x >> 31);
-}
-
-__device__ __forceinline__ float synth_normal(uint64_t seed, uint32_t stream, uint64_t index) {
-    uint64_t base = splitmix64(seed ^ ((uint64_t)stream * 0xD1B54A32D192ED03ull));
-    uint64_t h = splitmix64(base + index);
-    double u1 = ((double)(h >> 40) + 1.0) * (1.0 / 16777216.0);
-    double u2 = (double)((h >> 16) & 0xFFFFFFull) * (1.0 / 16777216.0);
-    return (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
 }
 
 __global__ void synth_fill_kernel(float* out, long long n, unsigned long long seed, unsigned stream, float std) {

@@ -175,6 +175,65 @@ enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
 int aarh_prof_enable(aarh_ctx *ctx, int enable);
 int aarh_prof_get(aarh_ctx *ctx, int cls, double *total_ms, double *alg_bytes, int64_t *launches);
 
+/* ===================================================================================
+ * Latent-attention MoE decoder: blocks of multi-head latent
+ * attention (nn/src/mla.rs:300-489, built by model/src/model.rs:1094-1156) and a
+ * fine-grained MoE FFN with top-k routing and shared experts (nn/src/moe.rs:127-406).
+ * A separate context type with the same conventions as aarh_ctx; its cache holds the
+ * normalised KV latent c_kv and the rotated shared key k_rope per token (fp16).
+ * =================================================================================== */
+typedef struct aarh_lat_ctx aarh_lat_ctx;
+
+/* MlaConfig (core/src/config.rs MLA fields) + MoeConfig (fine experts, shared experts)
+   + formats + device sizing. */
+typedef struct {
+    int32_t vocab_size, hidden_dim, n_layers, n_heads, max_seq_len;
+    float rope_theta, norm_eps;
+    int32_t latent_dim, rope_dim, nope_dim, v_dim; /* (512, 64) or (128, 32) latent/rope widths */
+    int32_t n_experts, top_k, expert_dim, n_shared;
+    int32_t expert_format;  /* AARH_W_BF16 / INT8_ROW / INT4_G128: routed + shared experts */
+    int32_t attn_format;    /* AARH_W_*: MLA projections and the router */
+    int32_t lm_head_format; /* AARH_W_F32 or AARH_W_BF16 (tied embedding) */
+    int32_t kv_format;      /* AARH_KV_F16 (the latent cache is fp16) */
+    int32_t max_batch;      /* cache sequence slots */
+    int32_t max_rows;       /* max rows (sequences x tokens) per forward, <= 256 */
+} aarh_lat_config;
+
+/* Context + weights (checkpoint names and order of the latent decoder: embedding,
+   per layer norm1, attn.{q_proj, kv_a_proj, kv_a_norm, up_k, up_v, k_rope_proj,
+   o_proj}, norm2, ffn.router, ffn.experts.{e}.{w_gate,w_up,w_down},
+   ffn.shared_experts.{s}.{...}, then final_norm). */
+int aarh_lat_create(int device, const aarh_lat_config *cfg, aarh_lat_ctx **out);
+void aarh_lat_destroy(aarh_lat_ctx *ctx);
+const char *aarh_lat_last_error(const aarh_lat_ctx *ctx);
+int aarh_lat_num_tensors(const aarh_lat_ctx *ctx);
+int aarh_lat_tensor_info(const aarh_lat_ctx *ctx, int id, char *name, int name_cap, int64_t *rows,
+                         int64_t *cols, int32_t *kind);
+int aarh_lat_load_tensor_f32(aarh_lat_ctx *ctx, int id, const float *host, int64_t numel);
+/* Random init on device: tensor id i ~ N(0, std^2) (router N(0, 1/hidden_dim)), norms 1. */
+int aarh_lat_init_synthetic(aarh_lat_ctx *ctx, uint64_t seed, float std);
+
+/* Latent cache per slot (MlaKvCache; rollback by index like nn/src/kvcache.rs:301-304). */
+int aarh_lat_kv_len(const aarh_lat_ctx *ctx, int slot, int32_t *out_len);
+int aarh_lat_kv_rollback(aarh_lat_ctx *ctx, int slot, int32_t new_len);
+int aarh_lat_kv_fill_synthetic(aarh_lat_ctx *ctx, int slot, int32_t len, uint64_t seed);
+
+/* Verify forward (as aarh_forward): ids [nseq][S] on slots at offsets; logits
+   [nseq][S][vocab], final normed hidden [nseq][S][hidden] when non-null. */
+int aarh_lat_forward(aarh_lat_ctx *ctx, const uint32_t *ids, const int32_t *slots, const int32_t *offsets,
+                     int nseq, int S, float *logits_out, float *hidden_out);
+/* Of the last forward: per row, the smallest gap between the k-th and (k+1)-th router
+   logit over all layers ([nseq*S]; a near-tie may route differently from an f32 CPU
+   path), and the rows routed to each expert per layer ([n_layers][n_experts + n_shared]). */
+int aarh_lat_router_gaps(aarh_lat_ctx *ctx, float *out);
+int aarh_lat_expert_counts(aarh_lat_ctx *ctx, int32_t *out);
+
+/* Per-class timing as aarh_prof_*: QKV = fused q / kv_a / k_rope projection, WO =
+   o_proj, GATEUP = router + routing + expert gate/up, DOWN = expert down + combine,
+   ATTENTION = q absorption, cache append, latent attention, up_v, LMHEAD. */
+int aarh_lat_prof_enable(aarh_lat_ctx *ctx, int enable);
+int aarh_lat_prof_get(aarh_lat_ctx *ctx, int cls, double *total_ms, double *alg_bytes, int64_t *launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1867,6 +1867,27 @@ int ref_lat_get_tensor(const ref_lat *m, int id, float *out) {
     return REF_OK;
 }
 
+/* Synthetic random-init model: tensor id i ~ N(0, std^2) on stream i, the
+   router ~ N(0, 1/hidden_dim) so its logits on RMS-normalised inputs are about
+   N(0, 1), norms 1.  The device's synthetic init uses the
+   same streams and scales. */
+int ref_lat_init_synthetic(ref_lat *m, uint64_t seed, float std) {
+    const float router_std = 1.0f / sqrtf((float)m->cfg.hidden_dim);
+    for (int i = 0; i < m->n_tensors; i++) {
+        ref_tensor *t = &m->t[i];
+        if (t->kind == REF_T_NORM) continue;
+        int64_t n = t->rows * t->cols;
+        float *raw = (float *)malloc(sizeof(float) * (size_t)n);
+        if (!raw) return REF_ERR_CONFIG;
+        int is_router = i > 0 && i < lat_final_id(m) && (i - 1) % m->per_layer == X_ROUTER;
+        ref_synth_fill(seed, (uint32_t)i, n, is_router ? router_std : std, raw);
+        int st = ref_lat_set_tensor(m, i, raw);
+        free(raw);
+        if (st) return st;
+    }
+    return REF_OK;
+}
+
 ref_lat_kv *ref_lat_kv_create(const ref_lat *m, int capacity) {
     ref_lat_kv *kv = (ref_lat_kv *)calloc(1, sizeof(ref_lat_kv));
     kv->m = m;

@@ -176,6 +176,7 @@ int ref_lat_tensor_info(const ref_lat *m, int id, char *name, int name_cap, int6
                         int32_t *kind);
 int ref_lat_set_tensor(ref_lat *m, int id, const float *raw);
 int ref_lat_get_tensor(const ref_lat *m, int id, float *out);
+int ref_lat_init_synthetic(ref_lat *m, uint64_t seed, float std);
 ref_lat_kv *ref_lat_kv_create(const ref_lat *m, int capacity);
 void ref_lat_kv_free(ref_lat_kv *kv);
 int ref_lat_kv_truncate(ref_lat_kv *kv, int new_len);

@@ -142,6 +142,7 @@ def lib():
                                           C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
         "ref_lat_set_tensor": (C.c_int, [C.c_void_p, C.c_int, F32P]),
         "ref_lat_get_tensor": (C.c_int, [C.c_void_p, C.c_int, F32P]),
+        "ref_lat_init_synthetic": (C.c_int, [C.c_void_p, C.c_uint64, C.c_float]),
         "ref_lat_kv_create": (C.c_void_p, [C.c_void_p, C.c_int]),
         "ref_lat_kv_free": (None, [C.c_void_p]),
         "ref_lat_kv_truncate": (C.c_int, [C.c_void_p, C.c_int]),
@@ -536,6 +537,13 @@ class LatModel:
         st = lib().ref_lat_set_tensor(self.h, i, np.ascontiguousarray(raw, np.float32).ravel())
         if st:
             raise ValueError(f"set_tensor {i} failed: {st}")
+
+    def init_synthetic(self, seed, std):
+        """Random-init weights on the streams the device's synthetic init uses
+        (router ~ N(0, 1/hidden) for unit-variance logits)."""
+        st = lib().ref_lat_init_synthetic(self.h, seed, std)
+        if st:
+            raise ValueError(f"synthetic init failed: {st}")
 
     def kv(self, capacity):
         return LatKv(self, capacity)

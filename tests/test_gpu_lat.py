@@ -1,0 +1,173 @@
+"""Parity of the latent-attention MoE decoder on the device (
+MLA mla.rs:300-489 with the latent cache, fine-grained top-k MoE with shared
+experts moe.rs:127-406) against the oracle on identical random-init weights.
+Bar: logits and final hidden states within 2e-3 relative (max|d|/max|ref| per
+row).  The device evaluates attention in the latent space (absorbed up_k /
+up_v) where the oracle reconstructs K and V, and routes only the selected rows
+through each expert where the reference runs every expert densely; both are
+the same function up to rounding.  A row whose k-th and (k+1)-th router logits
+are within GAP_FLAG of each other in some layer can pick a different expert
+than an f32 CPU path (the analogue of the flagged near-tie draws of the
+acceptance test); sequences holding such a row are reported, not compared."""
+import numpy as np
+import pytest
+
+import aarambh_hip as A
+import refcpu as R
+from gpu_util import rel_rows
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+GAP_FLAG = 1e-4
+
+
+def small_kw(**over):
+    kw = dict(vocab_size=1024, hidden_dim=256, n_layers=2, n_heads=4, max_seq_len=128, latent_dim=128, rope_dim=32,
+              nope_dim=32, v_dim=32, n_experts=8, top_k=2, expert_dim=128, n_shared=1, expert_format=A.W_INT4_G128,
+              attn_format=A.W_INT8_ROW, lm_head_format=1, kv_format=A.KV_F16)
+    kw.update(over)
+    return kw
+
+
+def lat_pair(seed, std, max_batch, max_rows, **kw):
+    rc = R.make_lat_config(**kw)
+    ref = R.LatModel(rc)
+    ref.init_synthetic(seed, std)
+    hip = A.HipLatModel(A.LatConfig(**kw), max_batch=max_batch, max_rows=max_rows)
+    hip.init_synthetic(seed, std)
+    return ref, hip
+
+
+def compare(gl, gh, want, gaps, S):
+    """gl/gh [B, S, *]; want = [(logits, hidden)] per sequence; gaps [B*S].
+    Returns the number of sequences compared."""
+    checked = 0
+    for b, (wl, wh) in enumerate(want):
+        if np.min(gaps[b * S:(b + 1) * S]) < GAP_FLAG:
+            print(f"sequence {b}: router near-tie (gap {np.min(gaps[b * S:(b + 1) * S]):.2e}), not compared")
+            continue
+        el, eh = rel_rows(gl[b], wl).max(), rel_rows(gh[b], wh).max()
+        assert el < TOL and eh < TOL, (b, el, eh)
+        checked += 1
+    return checked
+
+
+FORMATS = [(A.W_INT4_G128, A.W_INT8_ROW, 1), (A.W_INT8_ROW, A.W_BF16, 0), (A.W_BF16, A.W_F32, 1),
+           (A.W_INT4_G128, A.W_INT4_G128, 1)]
+
+
+@pytest.mark.parametrize("efmt,afmt,lmfmt", FORMATS)
+def test_lat_prefill_verify_rollback(efmt, afmt, lmfmt):
+    kw = small_kw(expert_format=efmt, attn_format=afmt, lm_head_format=lmfmt)
+    print("lat small", kw, flush=True)
+    ref, hip = lat_pair(5, 0.05, 3, 128, **kw)
+    B, P, K = 3, 37, 4
+    ids = R.synth_tokens(5, 3, B * (P + K), kw["vocab_size"]).reshape(B, P + K)
+    kvs = [ref.kv(128) for _ in range(B)]
+    # prefill (many-row GEMM path), verify K tokens (GEMV path), rollback + shorter replay
+    steps = [(0, P), (P, P + K), (P, P + 2)]
+    total = 0
+    for lo, hi in steps:
+        gl, gh = hip.forward_with_cache_output(ids[:, lo:hi], [lo] * B)
+        gaps = hip.router_gaps()
+        want = []
+        for b in range(B):
+            kvs[b].truncate(lo)
+            want.append(kvs[b].forward(ids[b, lo:hi], lo))
+        total += compare(gl, gh, want, gaps, hi - lo)
+    assert total >= 2 * len(steps)
+    assert hip.kv_len(2) == P + 2
+    counts = hip.expert_counts()
+    assert (counts[:, :kw["n_experts"]].sum(1) == B * 2 * kw["top_k"]).all()
+    assert (counts[:, kw["n_experts"]:] == B * 2).all()
+    hip.close()
+
+
+def test_lat_ragged_offsets_and_host_loaded_weights():
+    """Per-sequence offsets (different cache lengths in one batch) and weights
+    loaded from host f32 values with non-unit norm weights."""
+    kw = small_kw(n_layers=1, n_experts=6, top_k=3, n_shared=2)
+    rc = R.make_lat_config(**kw)
+    ref = R.LatModel(rc)
+    hip = A.HipLatModel(A.LatConfig(**kw), max_batch=2, max_rows=64)
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        if kind == R.T_NORM:
+            raw = 1.0 + 0.2 * R.synth_fill(7, 500 + i, r * c, 1.0)
+        else:
+            raw = R.synth_fill(7, i, r * c, 1.0 / np.sqrt(c) if name.endswith("router.weight") else 0.05)
+        ref.set(i, raw)
+        hip.load_f32(i, raw)
+    ids = R.synth_tokens(7, 1, 40, kw["vocab_size"])
+    kvs = [ref.kv(128), ref.kv(128)]
+    # sequence 0 holds 20 tokens, sequence 1 holds 9
+    hip.forward_with_cache_output(ids[None, :20], [0], slots=[0])
+    hip.forward_with_cache_output(ids[None, 20:29], [0], slots=[1])
+    kvs[0].forward(ids[:20], 0)
+    kvs[1].forward(ids[20:29], 0)
+    nxt = np.stack([ids[29:32], ids[32:35]])
+    gl, gh = hip.forward_with_cache_output(nxt, [20, 9], slots=[0, 1])
+    gaps = hip.router_gaps()
+    want = [kvs[0].forward(nxt[0], 20), kvs[1].forward(nxt[1], 9)]
+    assert compare(gl, gh, want, gaps, 3) >= 1
+    hip.close()
+
+
+def test_lat_c5_shape_one_layer():
+    """BASELINE config 5 widths (d_model 2048, latent 512 + rope 64, 16 heads,
+    64 experts top-6 of width 1408 + 2 shared, INT4 experts, vocab 32000) at one
+    layer over a 1000-token synthetic latent cache; batch 4 x 5 rows (GEMM path)
+    and batch 1 x 5 rows (GEMV path)."""
+    kw = dict(vocab_size=32000, hidden_dim=2048, n_layers=1, n_heads=16, max_seq_len=1056, latent_dim=512,
+              rope_dim=64, nope_dim=128, v_dim=128, n_experts=64, top_k=6, expert_dim=1408, n_shared=2,
+              expert_format=A.W_INT4_G128, attn_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_F16)
+    print("lat c5 one layer: building models", flush=True)
+    ref, hip = lat_pair(11, 0.02, 5, 64, **kw)
+    T, S, B = 1000, 5, 4
+    kvs = []
+    for b in range(B + 1):
+        hip.kv_fill_synthetic(b, T, seed=100 + b)
+        kv = ref.kv(1056)
+        kv.fill_synthetic(100 + b, T)
+        kvs.append(kv)
+    ids = R.synth_tokens(11, 5, (B + 1) * S, kw["vocab_size"]).reshape(B + 1, S)
+    print("lat c5 one layer: batch 4", flush=True)
+    gl, gh = hip.forward_with_cache_output(ids[:B], [T] * B, slots=list(range(B)))
+    gaps = hip.router_gaps()
+    want = [kvs[b].forward(ids[b], T, nthreads=16) for b in range(B)]
+    n4 = compare(gl, gh, want, gaps, S)
+    print("lat c5 one layer: batch 1", flush=True)
+    gl, gh = hip.forward_with_cache_output(ids[B:], [T], slots=[B])
+    gaps = hip.router_gaps()
+    n1 = compare(gl, gh, [kvs[B].forward(ids[B], T, nthreads=16)], gaps, S)
+    assert n4 + n1 >= 3
+    hip.close()
+
+
+def test_lat_bench_shape_properties():
+    """The bench batch (32 sequences x 5 rows = 160 rows over a 4096-token cache)
+    at reduced depth: routed-count invariants, bit-identical repeat, and rollback
+    + replay giving the same logits (the cache rows past the rollback point are
+    rewritten, not appended)."""
+    kw = dict(vocab_size=32000, hidden_dim=2048, n_layers=2, n_heads=16, max_seq_len=4160, latent_dim=512,
+              rope_dim=64, nope_dim=128, v_dim=128, n_experts=64, top_k=6, expert_dim=1408, n_shared=2,
+              expert_format=A.W_INT4_G128, attn_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_F16)
+    hip = A.HipLatModel(A.LatConfig(**kw), max_batch=32, max_rows=160)
+    hip.init_synthetic(12, 0.02)
+    B, S, T = 32, 5, 4096
+    for b in range(B):
+        hip.kv_fill_synthetic(b, T, seed=200 + b)
+    ids = R.synth_tokens(12, 9, B * S, kw["vocab_size"]).reshape(B, S)
+    a, ah = hip.forward_with_cache_output(ids, [T] * B)
+    assert np.isfinite(a).all() and np.isfinite(ah).all()
+    counts = hip.expert_counts()
+    assert (counts[:, :64].sum(1) == B * S * 6).all() and (counts[:, 64:] == B * S).all()
+    for b in range(B):
+        hip.restore(T, slot=b)
+    b2, _ = hip.forward_with_cache_output(ids, [T] * B)
+    assert np.array_equal(a, b2)
+    # one sequence alone (GEMV path) agrees with its row of the batch within the bar
+    for b in range(B):
+        hip.restore(T, slot=b)
+    c, _ = hip.forward_with_cache_output(ids[3:4], [T], slots=[3])
+    assert rel_rows(c[0], a[3]).max() < TOL
+    hip.close()
