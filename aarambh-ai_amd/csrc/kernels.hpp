@@ -207,12 +207,13 @@ struct MlaArgs {
     float eps;
     float* q;                    // [M][nh][lat+rd]: absorbed q_lat | rotated q_rope
     _Float16* kc;                // [slots][cap][lat+rd]: c_kv | k_rope
-    _Float16* vt;                // [slots][lat][cap]: c_kv transposed
+    _Float16* vt;                // [slots][cap/32][lat][32]: c_kv transposed per 32-token block
     int cap;
     float scale;                 // 1/sqrt(nope + rd)
     int chunk, nchunks, ntiles;  // tokens per chunk, chunks, 16-row query tiles per sequence
-    int tiles_per_wg;            // query tiles per attention workgroup (1 or 2)
+    int tiles_per_wg;            // query tiles per attention workgroup (1..mla_tiles_per_wg_max())
     float* part;                 // [nseq][ntiles][nchunks][16][lat+4] chunk partials (m, l, pad, pad, o)
+    float* olat;                 // [M][nh][lat] merged latent attention output
     XFrag fo;                    // fragments of the attention output for o_proj
     float* out;                  // [M][nh*vd] f32 attention output rows (null: fragments only)
 };
@@ -221,6 +222,7 @@ int launch_mla_kvprep(const MlaArgs& a, hipStream_t stream);
 int launch_mla_attn(const MlaArgs& a, hipStream_t stream);
 int launch_mla_out(const MlaArgs& a, hipStream_t stream);
 bool mla_supported(int lat, int rd, int vd, int nope);
+int mla_tiles_per_wg_max();
 
 struct MoeArgs {
     int M, E, K, NS;             // rows, routed experts, top-k, shared experts
@@ -245,9 +247,15 @@ struct MoeArgs {
     float* x;                    // [M][H] residual stream
     XFrag fo;                    // fragments of the new x for the next consumer
     float* gap;                  // [M] running min of (k-th - (k+1)-th) router logit (null: none)
+    int* chunk_e;                // [cmax] expert of each 16-assignment chunk (written by the routing)
+    int* chunk_r0;               // [cmax] its first assignment within the expert
+    int* nchunk;                 // [1] number of chunks
+    int cmax;                    // chunk capacity: M*K/16 + E + NS*ceil(M/16)
+    int bpe;                     // expert projection: workgroups per chunk (tile-step slices)
 };
 int launch_moe_route(const MoeArgs& a, hipStream_t stream);
 int launch_moe_ffn(const MoeArgs& a, int phase, hipStream_t stream);
+int moe_tiles_per_step(int fmt);  // weight tiles per step of the expert projection
 int launch_moe_combine(const MoeArgs& a, hipStream_t stream);
 // Row-major f32 copy of a tiled quantised matrix (the values its GEMV multiplies
 // by); tblk > 0 writes row n = b * tblk + i, column k at ((b * K + k) * tblk + i).

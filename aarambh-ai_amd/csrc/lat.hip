@@ -24,10 +24,13 @@ static constexpr int MOE_MAX_ROWS = 256;    // rows per routing launch
 static constexpr int MOE_MAX_EXPERTS = 72;  // routed (<= 64) + shared experts
 
 static constexpr int MLA_RB = 32;  // query rows per qprep / out workgroup
+static constexpr int MLA_CT = 64;  // output columns per qprep / out workgroup
 
 // ---------------------------------------------------------------------------
 // q prep: rotate q_rope, absorb q_nope through up_k (q_lat = up_k_h^T q_nope_h).
-// Workgroup = 32 rows x 1 head; q_nope staged in LDS as [nope][32].
+// Workgroup = 32 rows x 1 head x 64 latent columns; q_nope staged in LDS as
+// [nope][32]; thread (column c, row group rg) accumulates 8 rows, the up_k
+// loads issued 8 at a time.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) mla_qprep_kernel(MlaArgs a) {
     extern __shared__ float4 qn4[];  // [nope][8] float4 = [nope][32 rows]
@@ -40,37 +43,46 @@ __global__ void __launch_bounds__(256) mla_qprep_kernel(MlaArgs a) {
         qn[d * MLA_RB + k] = k < nr ? a.raw[(size_t)(m0 + k) * a.raw_ld + h * (nope + rd) + d] : 0.f;
     }
     __syncthreads();
-    for (int j = tid; j < lat; j += 256) {
-        float acc[MLA_RB];
+    const int c = tid & 63, rg = tid >> 6, j = blockIdx.z * MLA_CT + c;
+    if (j < lat) {
+        float acc[8];
 #pragma unroll
-        for (int k = 0; k < MLA_RB; k++) acc[k] = 0.f;
+        for (int k = 0; k < 8; k++) acc[k] = 0.f;
         const float* wp = a.upk + (size_t)h * nope * lat + j;
-        for (int d = 0; d < nope; d++) {
-            const float w = wp[(size_t)d * lat];
+        for (int d0 = 0; d0 < nope; d0 += 16) {
+            float w[16];
 #pragma unroll
-            for (int k4 = 0; k4 < MLA_RB / 4; k4++) {
-                const float4 q = qn4[d * (MLA_RB / 4) + k4];
-                acc[4 * k4] = fmaf(w, q.x, acc[4 * k4]);
-                acc[4 * k4 + 1] = fmaf(w, q.y, acc[4 * k4 + 1]);
-                acc[4 * k4 + 2] = fmaf(w, q.z, acc[4 * k4 + 2]);
-                acc[4 * k4 + 3] = fmaf(w, q.w, acc[4 * k4 + 3]);
+            for (int u = 0; u < 16; u++) w[u] = d0 + u < nope ? wp[(size_t)(d0 + u) * lat] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                if (d0 + u >= nope) break;
+                const float4 x0 = qn4[(d0 + u) * (MLA_RB / 4) + 2 * rg], x1 = qn4[(d0 + u) * (MLA_RB / 4) + 2 * rg + 1];
+                acc[0] = fmaf(w[u], x0.x, acc[0]);
+                acc[1] = fmaf(w[u], x0.y, acc[1]);
+                acc[2] = fmaf(w[u], x0.z, acc[2]);
+                acc[3] = fmaf(w[u], x0.w, acc[3]);
+                acc[4] = fmaf(w[u], x1.x, acc[4]);
+                acc[5] = fmaf(w[u], x1.y, acc[5]);
+                acc[6] = fmaf(w[u], x1.z, acc[6]);
+                acc[7] = fmaf(w[u], x1.w, acc[7]);
             }
         }
 #pragma unroll
-        for (int k = 0; k < MLA_RB; k++)
-            if (k < nr) a.q[((size_t)(m0 + k) * a.nh + h) * KD + j] = acc[k];
+        for (int k = 0; k < 8; k++)
+            if (8 * rg + k < nr) a.q[((size_t)(m0 + 8 * rg + k) * a.nh + h) * KD + j] = acc[k];
     }
+    if (blockIdx.z != 0) return;
     for (int i = tid; i < nr * half; i += 256) {
         const int k = i / half, e = i - k * half, m = m0 + k;
         const int pos = a.pos0[m / a.S] + m % a.S;
         const float* src = a.raw + (size_t)m * a.raw_ld + h * (nope + rd) + nope;
         const float x1 = src[e], x2 = src[e + half];
-        const float c = a.rope_cos[(size_t)pos * half + e], s = a.rope_sin[(size_t)pos * half + e];
+        const float cs = a.rope_cos[(size_t)pos * half + e], sn = a.rope_sin[(size_t)pos * half + e];
         float* dst = a.q + ((size_t)m * a.nh + h) * KD + lat;
         {
 #pragma clang fp contract(off)
-            dst[e] = x1 * c - x2 * s;
-            dst[e + half] = x1 * s + x2 * c;
+            dst[e] = x1 * cs - x2 * sn;
+            dst[e + half] = x1 * sn + x2 * cs;
         }
     }
 }
@@ -95,7 +107,7 @@ __global__ void __launch_bounds__(256) mla_kvprep_kernel(MlaArgs a) {
     for (int j = tid; j < lat; j += 256) {
         const _Float16 c = (_Float16)(src[j] * inv * a.kvn_w[j]);
         krow[j] = c;
-        a.vt[((size_t)sl * lat + j) * a.cap + pos] = c;
+        a.vt[(((size_t)sl * (a.cap >> 5) + (pos >> 5)) * lat + j) * 32 + (pos & 31)] = c;
     }
     if (tid < half) {
         const float x1 = src[lat + tid], x2 = src[lat + tid + half];
@@ -125,27 +137,55 @@ __device__ __forceinline__ float lat_rows_sum(float x) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Workgroup-wide barrier ordering only LDS traffic: global loads in flight stay
+// in flight (a plain __syncthreads() would also wait for them).
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---------------------------------------------------------------------------
-// Latent attention.  Workgroup = (sequence, group of up to two 16-row query
-// tiles, token chunk) with two waves per tile; the tile groups of one
+// Latent attention.  Workgroup = (sequence, group of up to three 16-row query
+// tiles, token chunk) with NP waves per tile; the tile groups of one
 // (sequence, chunk) are dispatched to the same XCD back to back, so a cache
 // block comes from HBM once and from that XCD's L2 for the other groups.
-// Query row r of a sequence is (token s = r / nh, head h = r % nh).  Per
-// 32-token block, wave half p: partial S^T = K Q^T over its k-steps (A = key
-// rows [c_kv | k_rope] from the cache, B = Q^T as fp16 hi + lo held in
-// registers), the two halves exchange partials through LDS and add them
-// (identically in both waves), online softmax in base 2 with the causal limit,
-// then O^T += V^T P^T over the wave's half of the latent dims (A = transposed
-// latent rows, B = P^T hi + lo).  The chunk's (m, l, O) rows go to scratch;
-// mla_out merges the chunks in order.
+// Query row r of a sequence is (token s = r / nh, head h = r % nh).  Each
+// 32-token block of keys [c_kv | k_rope] and transposed latents is staged in
+// LDS once for all waves (the next block's loads in flight in registers while
+// the current one is computed).  Wave p of a tile: partial S^T = K Q^T over
+// its k-steps (A = key rows from LDS, B = Q^T as fp16 hi + lo in registers);
+// the NP partials are exchanged through LDS and added in wave order
+// (identically in every wave); online softmax in base 2 with the causal
+// limit; O^T += V^T P^T over the wave's share of the latent dims (A =
+// transposed latent rows from LDS, B = P^T hi + lo).  The chunk's (m, l, O)
+// rows go to scratch; mla_merge combines the chunks in order.
 // ---------------------------------------------------------------------------
 template <int NKK, int NDT>
-__global__ void __launch_bounds__(256) mla_attn_kernel(MlaArgs a) {
-    constexpr int KD = 32 * NKK, LAT = 16 * NDT, KH = (NKK + 1) / 2, DH = NDT / 2;
-    extern __shared__ float4_t sx[];  // [2 parity][tiles_per_wg][2 halves][2][64 lanes]
-    const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wt = wv >> 1, p = wv & 1, TW = a.tiles_per_wg;
+struct MlaLds {
+    static constexpr int KD = 32 * NKK, LAT = 16 * NDT;
+    static constexpr int KROW = KD + 8;           // halves per staged key row (16-byte pad)
+    static constexpr int VROW = 40;               // halves per staged latent row: 32 tokens + pad
+    static constexpr int K_BYTES = 32 * KROW * 2;
+    static constexpr int V_BYTES = LAT * VROW * 2;
+    static constexpr int KCH = 32 * KD / 8;       // 16-byte chunks of a key block
+    static constexpr int VCH = LAT * 4;           // 16-byte chunks of a latent block
+};
+
+template <int NKK, int NDT, int NP, int TW, int DEPTH>
+__global__ void __launch_bounds__(64 * NP * TW) mla_attn_kernel(MlaArgs a) {
+    typedef MlaLds<NKK, NDT> Lc;
+    constexpr int KD = Lc::KD, LAT = Lc::LAT, KH = (NKK + NP - 1) / NP, DH = NDT / NP;
+    constexpr int NT = 64 * NP * TW, NST = (Lc::KCH + Lc::VCH + NT - 1) / NT;
+    static_assert(NDT % NP == 0, "latent tiles split evenly over the waves of a tile");
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    _Float16* ks = (_Float16*)lds;                                   // [32][KROW]
+    _Float16* vs = (_Float16*)(lds + Lc::K_BYTES);                   // [LAT][VROW]
+    float4_t* sx = (float4_t*)(lds + Lc::K_BYTES + Lc::V_BYTES);     // [2 parity][TW][NP][2][64]
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wt = wv / NP, p = wv % NP;
     const int ntg = (a.ntiles + TW - 1) / TW;
     // block b -> XCD b % 8; the ntg tile groups of work group gidx share an XCD
     const int xcd = blockIdx.x & 7, bi = blockIdx.x >> 3;
@@ -161,7 +201,7 @@ __global__ void __launch_bounds__(256) mla_attn_kernel(MlaArgs a) {
     const bool row_ok = tile_ok && rr < R_total;
     const int s_tok = row_ok ? rr / a.nh : 0, hh = row_ok ? rr % a.nh : 0;
     const int lim = row_ok ? pos0 + s_tok : -1;
-    const int q0 = p * KH, q1 = p == 0 ? KH : NKK;  // this wave's k-steps
+    const int q0 = p * KH, q1 = min(NKK, q0 + KH);  // this wave's k-steps
     half8_t qh[KH], ql[KH];
     {
         const float* qv = a.q + ((size_t)(seq * a.S + s_tok) * a.nh + hh) * KD;
@@ -182,68 +222,139 @@ __global__ void __launch_bounds__(256) mla_attn_kernel(MlaArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DH; dt++) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
     const float sc2 = a.scale * LAT_LOG2E;
-    const _Float16* kbase = a.kc + (size_t)sl * a.cap * KD;
-    const _Float16* vbase = a.vt + ((size_t)sl * LAT + p * DH * 16) * a.cap;
-    int par = 0;
-    for (int tb = t_begin; tb < t_end; tb += 32, par ^= 1) {
-        // ---- partial S^T: A row lr of tile ts is token tb + 8 (lr / 4) + 4 ts + lr % 4, so the
-        //      result lane (lr, lg) holds query row lr, tokens tb + 8 lg + (4 ts + i) ----
-        float4_t st[2];
+    const _Float16* kglob = a.kc + (size_t)sl * a.cap * KD;
+    const _Float16* vglob = a.vt + (size_t)sl * LAT * a.cap;  // + (tb / 32) * LAT * 32: one contiguous block
+    // staging: thread chunk idx < KCH is key row idx / (KD/8), 16-byte piece idx % (KD/8); the
+    // rest are latent row (idx - KCH) / 4, token piece (idx - KCH) % 4
+    u32x4_t sa[NST], sb[DEPTH == 2 ? NST : 1];
+    constexpr int nthr = NT;
+    auto fetch = [&](int tb, u32x4_t* stg) __attribute__((always_inline)) {
+        if (tb >= t_end) return;
 #pragma unroll
-        for (int ts = 0; ts < 2; ts++) {
-            const int tok = tb + 8 * (lr >> 2) + 4 * ts + (lr & 3);
-            const _Float16* kp = kbase + (size_t)tok * KD + 8 * lg;
-            float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < KH; i++) {
-                if (q0 + i < q1) {
-                    const half8_t ka = *(const half8_t*)(kp + 32 * (q0 + i));
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[i], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[i], acc, 0, 0, 0);
-                }
+        for (int u = 0; u < NST; u++) {
+            const int idx = tid + u * nthr;
+            if (idx < Lc::KCH) {
+                const int tok = idx / (KD / 8), pc = idx % (KD / 8);
+                stg[u] = *(const u32x4_t*)(kglob + (size_t)(tb + tok) * KD + 8 * pc);
+            } else if (idx < Lc::KCH + Lc::VCH) {
+                stg[u] = *(const u32x4_t*)(vglob + (size_t)tb * LAT + 8 * (idx - Lc::KCH));
             }
-            st[ts] = acc;
         }
-        float4_t* mine = sx + (((size_t)par * TW + wt) * 2 + p) * 128;
-        float4_t* other = sx + (((size_t)par * TW + wt) * 2 + (p ^ 1)) * 128;
-        mine[lane] = st[0];
-        mine[64 + lane] = st[1];
-        __syncthreads();
-        const float4_t o0 = other[lane], o1 = other[64 + lane];
-        float s[8], mx = -INFINITY;
+    };
+    auto stage = [&](const u32x4_t* stg) __attribute__((always_inline)) {
 #pragma unroll
-        for (int idx = 0; idx < 8; idx++) {
-            const int tok = tb + 8 * lg + idx;
-            const float tot = idx < 4 ? st[0][idx] + o0[idx] : st[1][idx - 4] + o1[idx - 4];
-            s[idx] = (tok < t_end && tok <= lim) ? tot * sc2 : -INFINITY;
-            mx = fmaxf(mx, s[idx]);
+        for (int u = 0; u < NST; u++) {
+            const int idx = tid + u * nthr;
+            if (idx < Lc::KCH) {
+                const int tok = idx / (KD / 8), pc = idx % (KD / 8);
+                *(u32x4_t*)(ks + tok * Lc::KROW + 8 * pc) = stg[u];
+            } else if (idx < Lc::KCH + Lc::VCH) {
+                const int d = (idx - Lc::KCH) >> 2, pc = (idx - Lc::KCH) & 3;
+                *(u32x4_t*)(vs + d * Lc::VROW + 8 * pc) = stg[u];
+            }
         }
-        mx = lat_rows_max(mx);
-        const float mnew = fmaxf(m, mx);
-        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
-        float pr[8], ps = 0.f;
+    };
+    // A row lr of S tile ts is token 8 (lr / 4) + 4 ts + lr % 4 of the block, so the result lane
+    // (lr, lg) holds query row lr, tokens tb + 8 lg + (4 ts + i)
+    const int trow0 = 8 * (lr >> 2) + (lr & 3);
+    int par = 0;
+    // one 32-token block: S, exchange, softmax, O (keys and latents of block tb in LDS)
+    auto block = [&](int tb) __attribute__((always_inline)) {
+            float4_t st[2];
 #pragma unroll
-        for (int idx = 0; idx < 8; idx++) {
-            pr[idx] = s[idx] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[idx] - mnew);
-            ps += pr[idx];
+            for (int ts = 0; ts < 2; ts++) {
+                const _Float16* kp = ks + (trow0 + 4 * ts) * Lc::KROW + 8 * lg;
+                float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < KH; i++) {
+                    if (q0 + i < q1) {
+                        const half8_t ka = *(const half8_t*)(kp + 32 * (q0 + i));
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[i], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[i], acc, 0, 0, 0);
+                    }
+                }
+                st[ts] = acc;
+            }
+            float4_t* grp = sx + (size_t)(par * TW + wt) * NP * 128;
+            grp[p * 128 + lane] = st[0];
+            grp[p * 128 + 64 + lane] = st[1];
+            lds_barrier();
+            float4_t t0 = grp[lane], t1 = grp[64 + lane];
+#pragma unroll
+            for (int pp = 1; pp < NP; pp++) {
+                t0 += grp[pp * 128 + lane];
+                t1 += grp[pp * 128 + 64 + lane];
+            }
+            float s[8], mx = -INFINITY;
+#pragma unroll
+            for (int idx = 0; idx < 8; idx++) {
+                const int tok = tb + 8 * lg + idx;
+                const float tot = idx < 4 ? t0[idx] : t1[idx - 4];
+                s[idx] = (tok < t_end && tok <= lim) ? tot * sc2 : -INFINITY;
+                mx = fmaxf(mx, s[idx]);
+            }
+            mx = lat_rows_max(mx);
+            const float mnew = fmaxf(m, mx);
+            const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
+            float pr[8], ps = 0.f;
+#pragma unroll
+            for (int idx = 0; idx < 8; idx++) {
+                pr[idx] = s[idx] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[idx] - mnew);
+                ps += pr[idx];
+            }
+            ps = lat_rows_sum(ps);
+            l = l * alpha + ps;
+            m = mnew;
+            half8_t ph, pl;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const _Float16 h = (_Float16)pr[j];
+                ph[j] = h;
+                pl[j] = (_Float16)(pr[j] - (float)h);
+            }
+            // ---- O^T += V^T P^T over this wave's latent tiles: A = dims 16 dt + lr, tokens 8 lg .. +8 ----
+            const _Float16* vp = vs + (p * DH * 16 + lr) * Lc::VROW + 8 * lg;
+#pragma unroll
+            for (int dt = 0; dt < DH; dt++) {
+                const half8_t va = *(const half8_t*)(vp + 16 * dt * Lc::VROW);
+                o[dt] *= alpha;
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
+            }
+        par ^= 1;
+    };
+    if (DEPTH == 2) {
+        // two blocks in flight in registers (sa / sb alternate) while one is computed from LDS
+        fetch(t_begin, sa);
+        stage(sa);
+        fetch(t_begin + 32, sb);
+        fetch(t_begin + 64, sa);
+        for (int tb = t_begin; tb < t_end; tb += 64) {
+            lds_barrier();  // block tb staged
+            block(tb);
+            if (tb + 32 >= t_end) break;
+            lds_barrier();  // every wave is done with block tb
+            stage(sb);
+            fetch(tb + 96, sb);
+            lds_barrier();  // block tb + 32 staged
+            block(tb + 32);
+            if (tb + 64 >= t_end) break;
+            lds_barrier();
+            stage(sa);
+            fetch(tb + 128, sa);
         }
-        ps = lat_rows_sum(ps);
-        l = l * alpha + ps;
-        m = mnew;
-        half8_t ph, pl;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const _Float16 h = (_Float16)pr[j];
-            ph[j] = h;
-            pl[j] = (_Float16)(pr[j] - (float)h);
-        }
-        // ---- O^T += V^T P^T over this wave's latent tiles: A = dims 16 dt + lr, tokens tb + 8 lg .. +8 ----
-#pragma unroll
-        for (int dt = 0; dt < DH; dt++) {
-            const half8_t va = *(const half8_t*)(vbase + (size_t)(16 * dt + lr) * a.cap + tb + 8 * lg);
-            o[dt] *= alpha;
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
+    } else {
+        // one block in flight in registers while one is computed from LDS
+        fetch(t_begin, sa);
+        stage(sa);
+        fetch(t_begin + 32, sa);
+        for (int tb = t_begin; tb < t_end; tb += 32) {
+            lds_barrier();  // block tb staged
+            block(tb);
+            if (tb + 32 >= t_end) break;
+            lds_barrier();  // every wave is done with block tb
+            stage(sa);
+            fetch(tb + 64, sa);
         }
     }
     if (!tile_ok) return;
@@ -258,179 +369,250 @@ __global__ void __launch_bounds__(256) mla_attn_kernel(MlaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Output: merge the chunk partials of 32 rows of one head (chunk order), apply
-// up_v, write the fragments of the o_proj input (column h * vd + i).
+// Merge: one workgroup per (row, head) combines the chunk partials in chunk
+// order into the latent output o_lat[m][h][lat]: wave 0 derives the weights
+// exp2(m_c - max) / L (one lane per chunk), then every thread sums its latent
+// dims over the chunks with independent loads.
+// ---------------------------------------------------------------------------
+static constexpr int MLA_MAXCH = 64;  // chunks one merge combines
+
+__global__ void __launch_bounds__(256) mla_merge_kernel(MlaArgs a) {
+    __shared__ float wsc[MLA_MAXCH];
+    const int mrow = blockIdx.x / a.nh, h = blockIdx.x % a.nh, tid = threadIdx.x;
+    const int lat = a.lat, REC = lat + 4, nch = a.nchunks;
+    const int seq = mrow / a.S, s = mrow % a.S, r = s * a.nh + h;
+    const size_t cstride = (size_t)16 * REC;
+    const float* rec0 = a.part + (((size_t)seq * a.ntiles + (r >> 4)) * nch * 16 + (r & 15)) * REC;
+    if (tid < 64) {
+        const float mc = tid < nch ? rec0[tid * cstride] : -INFINITY;
+        const float lc = tid < nch ? rec0[tid * cstride + 1] : 0.f;
+        const float Mx = wave_max_f32(mc);
+        const float w = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - Mx);
+        const float L = wave_sum_f32(w * lc);
+        if (tid < MLA_MAXCH) wsc[tid] = L > 0.f ? w / L : 0.f;
+    }
+    __syncthreads();
+    float* dst = a.olat + ((size_t)mrow * a.nh + h) * lat;
+    for (int j = tid; j < lat; j += 256) {
+        const float* p = rec0 + 4 + j;
+        float acc = 0.f;
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = p[(c + u) * cstride];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = fmaf(v[u], wsc[c + u], acc);
+        }
+        for (; c < nch; c++) acc = fmaf(p[c * cstride], wsc[c], acc);
+        dst[j] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// up_v: o[m][h*vd + i] = sum_j up_v[h][i][j] o_lat[m][h][j] for 32 rows x 64
+// columns of one head; o_lat staged in LDS as [lat][32]; the o_proj input is
+// written as fragments (and f32 rows when o_proj reads f32).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) mla_out_kernel(MlaArgs a) {
     extern __shared__ float4 ol4[];  // [lat][8] float4 = [lat][32 rows]
     float* ol = (float*)ol4;
     const int M = a.nseq * a.S, h = blockIdx.y, m0 = blockIdx.x * MLA_RB, tid = threadIdx.x;
-    const int lat = a.lat, vd = a.vd, REC = lat + 4;
+    const int lat = a.lat, vd = a.vd;
     const int nr = min(MLA_RB, M - m0);
-    for (int k = 0; k < MLA_RB; k++) {
-        if (k >= nr) {
-            for (int j = tid; j < lat; j += 256) ol[j * MLA_RB + k] = 0.f;
-            continue;
-        }
-        const int mrow = m0 + k, seq = mrow / a.S, s = mrow % a.S;
-        const int r = s * a.nh + h, tile = r >> 4, rr = r & 15;
-        const float* rec0 = a.part + (((size_t)seq * a.ntiles + tile) * a.nchunks * 16 + rr) * REC;
-        const size_t cstride = (size_t)16 * REC;
-        float Mx = -INFINITY;
-        for (int c = 0; c < a.nchunks; c++) Mx = fmaxf(Mx, rec0[c * cstride]);
-        float L = 0.f;
-        for (int c = 0; c < a.nchunks; c++) {
-            const float mc = rec0[c * cstride];
-            L += mc == -INFINITY ? 0.f : rec0[c * cstride + 1] * __builtin_amdgcn_exp2f(mc - Mx);
-        }
-        const float invL = L > 0.f ? 1.0f / L : 0.f;
-        for (int j = tid; j < lat; j += 256) {
-            float acc = 0.f;
-            for (int c = 0; c < a.nchunks; c++) {
-                const float mc = rec0[c * cstride];
-                if (mc != -INFINITY) acc += rec0[c * cstride + 4 + j] * __builtin_amdgcn_exp2f(mc - Mx);
-            }
-            ol[j * MLA_RB + k] = acc * invL;
-        }
+    for (int idx = tid; idx < MLA_RB * lat; idx += 256) {
+        const int k = idx / lat, j = idx - k * lat;
+        ol[j * MLA_RB + k] = k < nr ? a.olat[((size_t)(m0 + k) * a.nh + h) * lat + j] : 0.f;
     }
     __syncthreads();
-    const float* wp = a.upvT + (size_t)h * lat * vd;
-    for (int idx = tid; idx < vd * (MLA_RB / 16); idx += 256) {
-        const int i = idx % vd, rg = idx / vd;
-        float acc[16];
+    const int c = tid & 63, rg = tid >> 6, i = blockIdx.z * MLA_CT + c;
+    if (i >= vd) return;
+    const float* wp = a.upvT + (size_t)h * lat * vd + i;
+    float acc[8];
 #pragma unroll
-        for (int k = 0; k < 16; k++) acc[k] = 0.f;
-        for (int j = 0; j < lat; j++) {
-            const float w = wp[(size_t)j * vd + i];
+    for (int k = 0; k < 8; k++) acc[k] = 0.f;
+    for (int j0 = 0; j0 < lat; j0 += 16) {
+        float w[16];
 #pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) {
-                const float4 q = ol4[j * (MLA_RB / 4) + rg * 4 + k4];
-                acc[4 * k4] = fmaf(w, q.x, acc[4 * k4]);
-                acc[4 * k4 + 1] = fmaf(w, q.y, acc[4 * k4 + 1]);
-                acc[4 * k4 + 2] = fmaf(w, q.z, acc[4 * k4 + 2]);
-                acc[4 * k4 + 3] = fmaf(w, q.w, acc[4 * k4 + 3]);
-            }
+        for (int u = 0; u < 16; u++) w[u] = wp[(size_t)(j0 + u) * vd];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const float4 x0 = ol4[(j0 + u) * (MLA_RB / 4) + 2 * rg], x1 = ol4[(j0 + u) * (MLA_RB / 4) + 2 * rg + 1];
+            acc[0] = fmaf(w[u], x0.x, acc[0]);
+            acc[1] = fmaf(w[u], x0.y, acc[1]);
+            acc[2] = fmaf(w[u], x0.z, acc[2]);
+            acc[3] = fmaf(w[u], x0.w, acc[3]);
+            acc[4] = fmaf(w[u], x1.x, acc[4]);
+            acc[5] = fmaf(w[u], x1.y, acc[5]);
+            acc[6] = fmaf(w[u], x1.z, acc[6]);
+            acc[7] = fmaf(w[u], x1.w, acc[7]);
         }
+    }
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            if (rg * 16 + k >= nr) continue;
-            const int m = m0 + rg * 16 + k;
-            if (a.fo.buf) frag_put(a.fo, m, h * vd + i, acc[k]);
-            if (a.out) a.out[(size_t)m * a.nh * vd + h * vd + i] = acc[k];
-        }
+    for (int k = 0; k < 8; k++) {
+        if (8 * rg + k >= nr) continue;
+        const int m = m0 + 8 * rg + k;
+        if (a.fo.buf) frag_put(a.fo, m, h * vd + i, acc[k]);
+        if (a.out) a.out[(size_t)m * a.nh * vd + h * vd + i] = acc[k];
     }
 }
 
 // ---------------------------------------------------------------------------
 // MoE routing (moe.rs:361-406): one wave per row ranks the E <= 64 logits
 // (larger first, equal logits keep the lower index), softmax over the top k in
-// rank order; then per-expert assignment lists (rows ascending) and each row's
-// assignment indices (routed experts in index order, then shared experts).
+// rank order; then per-expert assignment lists (rows ascending), each row's
+// assignment indices (routed experts in index order, then shared experts) and
+// the list of 16-assignment chunks the expert projections run over.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) moe_route_kernel(MoeArgs a) {
+static constexpr int MOE_RT_WAVES = 16;
+
+// (v, i) comes before (w, j) in routing order: larger logit first, then lower index.
+__device__ __forceinline__ bool route_before(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+
+__device__ __forceinline__ unsigned long long wave_or_u64(unsigned long long x) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const unsigned lo = __shfl_xor((unsigned)x, d, 64), hi = __shfl_xor((unsigned)(x >> 32), d, 64);
+        x |= ((unsigned long long)hi << 32) | lo;
+    }
+    return x;
+}
+
+__device__ __forceinline__ int lanes_below(unsigned long long bal) {
+    return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+}
+
+__global__ void __launch_bounds__(1024) moe_route_kernel(MoeArgs a) {
     extern __shared__ float wsel[];  // [M][64] dispatch weight of (row, expert)
     __shared__ unsigned long long selm[MOE_MAX_ROWS];
-    __shared__ float tmp[4][64], rankv[4][64];
     __shared__ int offs[MOE_MAX_EXPERTS + 1];
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int E = a.E, K = a.K, NS = a.NS, M = a.M;
-    for (int m = wid; m < M; m += 4) {
-        const float v = lane < E ? a.logits[(size_t)m * a.lld + lane] : -INFINITY;
-        int rank = 0;
-        for (int e2 = 0; e2 < E; e2++) {
-            const float v2 = __shfl(v, e2, 64);
-            rank += (v2 > v || (v2 == v && e2 < lane)) ? 1 : 0;
+    // ---- per row: bitonic sort of (logit, expert) over the wave's lanes into routing order ----
+    for (int m = wid; m < M; m += MOE_RT_WAVES) {
+        float v = lane < E ? a.logits[(size_t)m * a.lld + lane] : -INFINITY;
+        int i = lane;
+#pragma unroll
+        for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                const float pv = __shfl_xor(v, j, 64);
+                const int pi = __shfl_xor(i, j, 64);
+                const bool keep_first = ((lane & j) == 0) == ((lane & k) == 0);
+                const bool take = keep_first ? route_before(pv, pi, v, i) : route_before(v, i, pv, pi);
+                if (take) {
+                    v = pv;
+                    i = pi;
+                }
+            }
         }
-        const bool sel = lane < E && rank < K;
-        const float mx = wave_max_f32(sel ? v : -INFINITY);
-        const float ev = sel ? expf_rn(v - mx) : 0.f;
-        if (sel) tmp[wid][rank] = ev;
-        if (lane < E) rankv[wid][rank] = v;
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave's LDS writes are done
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        // lane r now holds the r-th expert in routing order; softmax over ranks 0..K-1 in order
+        const float mx = __shfl(v, 0, 64);
+        const float ev = lane < K ? expf_rn(v - mx) : 0.f;
         float ssum = 0.f;
-        for (int r = 0; r < K; r++) ssum += tmp[wid][r];
-        wsel[m * 64 + lane] = sel ? ev / ssum : 0.f;
-        const unsigned long long bm = __ballot(sel);
+        for (int r = 0; r < K; r++) ssum += __shfl(ev, r, 64);
+        if (lane < K) wsel[m * 64 + i] = ev / ssum;
+        const unsigned long long bm = wave_or_u64(lane < K ? (1ull << i) : 0ull);
+        const float vk1 = __shfl(v, K - 1, 64), vk = __shfl(v, K < 64 ? K : 63, 64);
         if (lane == 0) {
             selm[m] = bm;
-            if (a.gap && K < E) a.gap[m] = fminf(a.gap[m], rankv[wid][K - 1] - rankv[wid][K]);
+            if (a.gap && K < E) a.gap[m] = fminf(a.gap[m], vk1 - vk);
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
     __syncthreads();
-    if (tid < E + NS) {
+    // ---- rows per expert (shared experts take every row) ----
+    for (int e = wid; e < E + NS; e += MOE_RT_WAVES) {
         int c = 0;
-        if (tid < E) {
-            for (int m = 0; m < M; m++) c += (int)((selm[m] >> tid) & 1ull);
-        } else {
-            c = M;
+        for (int m0 = 0; m0 < M; m0 += 64) {
+            const int m = m0 + lane;
+            const bool sel = m < M && (e >= E || ((selm[m] >> e) & 1ull));
+            c += __popcll(__ballot(sel));
         }
-        a.cnt[tid] = c;
-        offs[tid + 1] = c;
+        if (lane == 0) {
+            a.cnt[e] = c;
+            offs[e + 1] = c;
+        }
     }
     __syncthreads();
     if (tid == 0) {
         offs[0] = 0;
-        for (int e = 0; e < E + NS; e++) offs[e + 1] += offs[e];
+        int nc = 0;
+        for (int e = 0; e < E + NS; e++) {
+            const int c = offs[e + 1];
+            for (int r0 = 0; r0 < c && nc < a.cmax; r0 += 16, nc++) {
+                a.chunk_e[nc] = e;
+                a.chunk_r0[nc] = r0;
+            }
+            offs[e + 1] += offs[e];
+        }
+        *a.nchunk = nc;
         for (int e = 0; e <= E + NS; e++) a.off[e] = offs[e];
     }
     __syncthreads();
-    if (tid < E) {
-        int k = offs[tid];
-        const unsigned long long below = tid == 0 ? 0ull : (~0ull >> (64 - tid));
-        for (int m = 0; m < M; m++) {
-            if (!((selm[m] >> tid) & 1ull)) continue;
-            a.arow[k] = m;
-            a.aw[k] = wsel[m * 64 + tid];
-            a.rowmap[(size_t)m * (K + NS) + __popcll(selm[m] & below)] = k;
-            k++;
-        }
-    } else if (tid < E + NS) {
-        const int sidx = tid - E;
-        for (int m = 0; m < M; m++) {
-            const int k = offs[tid] + m;
-            a.arow[k] = m;
-            a.aw[k] = 1.0f;
-            a.rowmap[(size_t)m * (K + NS) + K + sidx] = k;
+    // ---- assignments: expert lists in ascending rows; a row's slots are its routed experts
+    //      in index order, then the shared experts ----
+    for (int e = wid; e < E + NS; e += MOE_RT_WAVES) {
+        int k = offs[e];
+        const unsigned long long below = e == 0 ? 0ull : (e >= 64 ? ~0ull : (~0ull >> (64 - e)));
+        for (int m0 = 0; m0 < M; m0 += 64) {
+            const int m = m0 + lane;
+            const unsigned long long sm = m < M ? selm[m] : 0ull;
+            const bool sel = m < M && (e >= E || ((sm >> e) & 1ull));
+            const unsigned long long bal = __ballot(sel);
+            if (sel) {
+                const int pos = k + lanes_below(bal);
+                a.arow[pos] = m;
+                a.aw[pos] = e < E ? wsel[m * 64 + e] : 1.0f;
+                a.rowmap[(size_t)m * (K + NS) + (e < E ? __popcll(sm & below) : K + (e - E))] = pos;
+            }
+            k += __popcll(bal);
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Grouped expert projection: block = (expert, 4 weight tiles), 8 waves split
-// the K groups; the expert's assigned rows are taken 16 at a time, gathered
-// from f32 rows and split into fp16 (bf16) hi + lo MFMA operands in registers.
+// Grouped expert projection over the routing's chunk list.  Workgroup = (chunk
+// of up to 16 assignments of one expert, slice of its weight-tile steps); 8
+// waves split the K groups (group g = wave + 8 gi); the chunk's rows are
+// gathered once, split into fp16 (bf16) hi + lo MFMA operands held in
+// registers, and the slice's tile steps (NTB tiles each) stream through with
+// the next step's weights in flight; per step the 8 wave partials meet in LDS
+// (double-buffered, one barrier) and the first NTB waves finish the tiles.
 // PHASE 1: gate/up tiles (8 + 8 interleaved rows) -> SwiGLU -> h[assignment].
 // PHASE 2: down tiles -> y[assignment] (unweighted).
 // ---------------------------------------------------------------------------
-template <int FMT, int PHASE>
+template <int FMT>
+struct MoeCfg {
+    static constexpr int NTB = FMT == WF_INT4 ? 4 : (FMT == WF_INT8 ? 2 : 1);  // tiles per step
+};
+
+template <int FMT, int PHASE, int NGW>
 __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
     typedef FmtTraits<FMT> T;
-    constexpr int NW = 8, NTB = 4, NGW = 4, LW = T::LANE_WORDS;
-    __shared__ float4_t part[NW][NTB][64];
-    __shared__ float yt[NTB][16][17];
+    constexpr int NW = 8, NTB = MoeCfg<FMT>::NTB, LW = T::LANE_WORDS;
+    __shared__ float4_t part[2][NW][NTB][64];
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
+    const int ci = blockIdx.x / a.bpe, slice = blockIdx.x % a.bpe;
+    if (ci >= *a.nchunk) return;
+    const int e = a.chunk_e[ci], r0 = a.chunk_r0[ci];
+    const int nr = min(16, a.cnt[e] - r0);
+    const int base_a = a.off[e] + r0;
     const int Kin = PHASE == 1 ? a.H : a.D;
     const int Ne = PHASE == 1 ? 2 * a.D : a.H;
-    const int G = Kin >> 7, ntiles = Ne >> 4, TB = (ntiles + NTB - 1) / NTB;
-    const int e = blockIdx.x / TB, tg = blockIdx.x % TB;
-    const int n_e = a.cnt[e];
-    if (n_e == 0) return;
-    const int base_a = a.off[e];
+    const int G = Kin >> 7, ntiles = Ne >> 4, nsteps = (ntiles + NTB - 1) / NTB;
+    if (slice >= nsteps) return;
     const uint8_t* W = PHASE == 1 ? a.gu : a.dn;
     const uint32_t* SZ = PHASE == 1 ? a.gu_sz : a.dn_sz;
     const float* RS = PHASE == 1 ? a.gu_rs : a.dn_rs;
+    const size_t tile0 = (size_t)e * ntiles;
 
-    for (int c0 = 0; c0 < n_e; c0 += 16) {
-        const bool rv = c0 + lr < n_e;
-        const int ai = base_a + min(c0 + lr, n_e - 1);
+    // ---- activations of the chunk: A row lr = assignment base_a + lr ----
+    half8_t ah[NGW][4], al[NGW][4];
+    {
+        const bool rv = lr < nr;
+        const int ai = base_a + (rv ? lr : 0);
         const float* rowp = PHASE == 1 ? a.xn + (size_t)a.arow[ai] * a.H : a.h + (size_t)ai * a.D;
-        half8_t ah[NGW][4], al[NGW][4];
 #pragma unroll
         for (int gi = 0; gi < NGW; gi++) {
             const int g = wid + NW * gi;
@@ -454,37 +636,60 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
                         ah[gi][t][j] = __builtin_bit_cast(_Float16, hb);
                         al[gi][t][j] = __builtin_bit_cast(_Float16, f32_to_bf16_rne(x - bf16_to_f32(hb)));
                     } else {
-                        const _Float16 h = (_Float16)x;
-                        ah[gi][t][j] = h;
-                        al[gi][t][j] = (_Float16)(x - (float)h);
+                        const _Float16 hx = (_Float16)x;
+                        ah[gi][t][j] = hx;
+                        al[gi][t][j] = (_Float16)(x - (float)hx);
                     }
                 }
             }
         }
+    }
+
+    // ---- weight words of one step (NTB tiles x this wave's groups), three steps in flight ----
+    typedef uint32_t WStep[NTB][NGW][LW];
+    typedef uint32_t ZStep[NTB][NGW];
+    WStep w0, w1, w2;
+    ZStep z0, z1, z2;
+    auto load_step = [&](int st, WStep& wv, ZStep& zv) {
+        if (st >= nsteps) return;
 #pragma unroll
         for (int j = 0; j < NTB; j++) {
-            const int nt = min(tg * NTB + j, ntiles - 1);
+            const int nt = min(st * NTB + j, ntiles - 1);
+#pragma unroll
+            for (int gi = 0; gi < NGW; gi++) {
+                const int g = wid + NW * gi;
+                if (g >= G) continue;
+                const size_t tile = (tile0 + nt) * G + g;
+#pragma unroll
+                for (int q = 0; q < LW / 4; q++) {
+                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + (size_t)lane * LW * 4 + 16 * q);
+                    wv[j][gi][4 * q] = w4.x;
+                    wv[j][gi][4 * q + 1] = w4.y;
+                    wv[j][gi][4 * q + 2] = w4.z;
+                    wv[j][gi][4 * q + 3] = w4.w;
+                }
+                if (FMT == WF_INT4) zv[j][gi] = SZ[tile * 16 + lr];
+            }
+        }
+    };
+    int buf = 0;
+    auto compute_step = [&](int st, const WStep& wv, const ZStep& zv) {
+#pragma unroll
+        for (int j = 0; j < NTB; j++) {
             float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int gi = 0; gi < NGW; gi++) {
                 const int g = wid + NW * gi;
                 if (g >= G) continue;
-                const size_t tile = ((size_t)e * ntiles + nt) * G + g;
-                uint32_t wv[LW];
-#pragma unroll
-                for (int q = 0; q < LW / 4; q++) {
-                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + (size_t)lane * LW * 4 + 16 * q);
-                    wv[4 * q] = w4.x; wv[4 * q + 1] = w4.y; wv[4 * q + 2] = w4.z; wv[4 * q + 3] = w4.w;
-                }
                 if (FMT == WF_INT4) {
-                    const uint32_t szw = SZ[tile * 16 + lr];
+                    const uint32_t szw = zv[j][gi];
                     const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
                     half2_t zl2, zh2;
                     int4_zero_operands(__builtin_bit_cast(_Float16, (uint16_t)(szw >> 16)), zl2, zh2);
                     float4_t ga = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int t = 0; t < 4; t++) {
-                        const half8_t b = int4_b_operand(wv[t], zl2, zh2);
+                        const half8_t b = int4_b_operand(wv[j][gi][t], zl2, zh2);
                         ga = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[gi][t], b, ga, 0, 0, 0);
                         ga = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[gi][t], b, ga, 0, 0, 0);
                     }
@@ -492,14 +697,15 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
                 } else if (FMT == WF_INT8) {
 #pragma unroll
                     for (int t = 0; t < 4; t++) {
-                        const half8_t b = int8_b_operand(wv[2 * t], wv[2 * t + 1]);
+                        const half8_t b = int8_b_operand(wv[j][gi][2 * t], wv[j][gi][2 * t + 1]);
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[gi][t], b, acc, 0, 0, 0);
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[gi][t], b, acc, 0, 0, 0);
                     }
                 } else {
 #pragma unroll
                     for (int t = 0; t < 4; t++) {
-                        const u32x4_t w4 = {wv[4 * t], wv[4 * t + 1], wv[4 * t + 2], wv[4 * t + 3]};
+                        const u32x4_t w4 = {wv[j][gi][4 * t], wv[j][gi][4 * t + 1], wv[j][gi][4 * t + 2],
+                                            wv[j][gi][4 * t + 3]};
                         const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ah[gi][t]), b, acc,
                                                                       0, 0, 0);
@@ -508,70 +714,89 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
                     }
                 }
             }
-            part[wid][j][lane] = acc;
+            part[buf][wid][j][lane] = acc;
         }
-        __syncthreads();
-        if (tid < NTB * 64) {
-            const int j = tid >> 6, ln = tid & 63;
-            float4_t sum = part[0][j][ln];
+        lds_barrier();
+        if (wid < NTB) {
+            // wave j finishes tile j of the step: lane holds token rows 4 lg + i, weight row lr
+            const int j = wid, nt = st * NTB + j;
+            float4_t sum = part[buf][0][j][lane];
 #pragma unroll
-            for (int w = 1; w < NW; w++) sum += part[w][j][ln];
-            const int nt = min(tg * NTB + j, ntiles - 1);
-            const float rs = FMT == WF_INT8 ? RS[((size_t)e * ntiles + nt) * 16 + (ln & 15)] : 1.0f;
+            for (int w = 1; w < NW; w++) sum += part[buf][w][j][lane];
+            if (FMT == WF_INT8) sum *= RS[(tile0 + min(nt, ntiles - 1)) * 16 + lr];
+            if (PHASE == 1) {
+                // gate rows 0-7, up rows 8-15 of the tile: column nt * 8 + (lr & 7)
 #pragma unroll
-            for (int i = 0; i < 4; i++) yt[j][4 * (ln >> 4) + i][ln & 15] = sum[i] * rs;
-        }
-        __syncthreads();
-        if (PHASE == 1) {
-            for (int idx = tid; idx < NTB * 16 * 8; idx += NW * 64) {
-                const int j = idx >> 7, r16 = (idx >> 3) & 15, q = idx & 7;
-                const int nt = tg * NTB + j;
-                if (nt < ntiles && c0 + r16 < n_e) {
-                    const float g = yt[j][r16][q], u = yt[j][r16][8 + q];
-                    const float silu = g / (1.0f + expf(-g));
-                    a.h[(size_t)(base_a + c0 + r16) * a.D + nt * 8 + q] = silu * u;
+                for (int i = 0; i < 4; i++) {
+                    const float u = __shfl_xor(sum[i], 8, 64);
+                    const int r = 4 * lg + i;
+                    if (lr < 8 && nt < ntiles && r < nr) {
+                        const float g = sum[i];
+                        a.h[(size_t)(base_a + r) * a.D + nt * 8 + lr] = g / (1.0f + expf(-g)) * u;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * lg + i;
+                    if (nt < ntiles && r < nr) a.y[(size_t)(base_a + r) * a.H + nt * 16 + lr] = sum[i];
                 }
             }
-        } else {
-            for (int idx = tid; idx < NTB * 16 * 16; idx += NW * 64) {
-                const int j = idx >> 8, r16 = (idx >> 4) & 15, n = idx & 15;
-                const int nt = tg * NTB + j;
-                if (nt < ntiles && c0 + r16 < n_e) a.y[(size_t)(base_a + c0 + r16) * a.H + nt * 16 + n] = yt[j][r16][n];
-            }
         }
-        __syncthreads();
+        buf ^= 1;
+    };
+    const int B = a.bpe;
+    load_step(slice, w0, z0);
+    load_step(slice + B, w1, z1);
+    for (int st = slice; st < nsteps; st += 3 * B) {
+        load_step(st + 2 * B, w2, z2);
+        compute_step(st, w0, z0);
+        if (st + B >= nsteps) break;
+        load_step(st + 3 * B, w0, z0);
+        compute_step(st + B, w1, z1);
+        if (st + 2 * B >= nsteps) break;
+        load_step(st + 4 * B, w1, z1);
+        compute_step(st + 2 * B, w2, z2);
     }
 }
 
 // ---------------------------------------------------------------------------
 // Combine (moe.rs:290-331): x += (sum_e w_e y_e over the routed experts in index
 // order) + (sum of the shared experts in order); the new x as fragments and
-// 16-column sums of squares for the next RMSNorm.
+// 16-column sums of squares for the next RMSNorm.  Thread per column (coalesced).
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(128) moe_combine_kernel(MoeArgs a) {
-    const int m = blockIdx.x, H = a.H, KS = a.K + a.NS;
-    const int* rmap = a.rowmap + (size_t)m * KS;
-    for (int t = threadIdx.x; t < H / 16; t += blockDim.x) {
-        float ss = 0.f;
-        for (int n = 0; n < 16; n++) {
-            const int c = t * 16 + n;
-            float r = 0.f;
-            for (int j = 0; j < a.K; j++) {
-                const int ai = rmap[j];
-                r += a.y[(size_t)ai * H + c] * a.aw[ai];
-            }
-            if (a.NS > 0) {
-                float sh = a.y[(size_t)rmap[a.K] * H + c];
-                for (int s = 1; s < a.NS; s++) sh = sh + a.y[(size_t)rmap[a.K + s] * H + c];
-                r += sh;
-            }
-            const float xn = a.x[(size_t)m * H + c] + r;
-            a.x[(size_t)m * H + c] = xn;
-            if (a.fo.buf) frag_put(a.fo, m, c, xn);
-            ss += xn * xn;
-        }
-        if (a.fo.ssq) a.fo.ssq[(size_t)m * a.fo.ssq_ld + t] = ss;
+static constexpr int MOE_COMB_MAXK = 16;  // top-k + shared experts a combine handles
+
+__global__ void __launch_bounds__(256) moe_combine_kernel(MoeArgs a) {
+    const int m = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x, H = a.H, K = a.K, NS = a.NS;
+    const int* rmap = a.rowmap + (size_t)m * (K + NS);
+    int ai[MOE_COMB_MAXK];
+    float wt[MOE_COMB_MAXK];
+#pragma unroll
+    for (int j = 0; j < MOE_COMB_MAXK; j++) {
+        ai[j] = j < K + NS ? rmap[j] : 0;
+        wt[j] = j < K ? a.aw[ai[j]] : 0.f;
     }
+    if (c >= H) return;
+    float yv[MOE_COMB_MAXK];
+#pragma unroll
+    for (int j = 0; j < MOE_COMB_MAXK; j++) yv[j] = j < K + NS ? a.y[(size_t)ai[j] * H + c] : 0.f;
+    // routed experts weighted in index order, then the shared experts summed in order
+    float r = 0.f, sh = 0.f;
+#pragma unroll
+    for (int j = 0; j < MOE_COMB_MAXK; j++) {
+        if (j < K) r += yv[j] * wt[j];
+        else if (j == K) sh = yv[j];
+        else if (j < K + NS) sh = sh + yv[j];
+    }
+    if (NS > 0) r += sh;
+    const float xn = a.x[(size_t)m * H + c] + r;
+    a.x[(size_t)m * H + c] = xn;
+    if (a.fo.buf) frag_put(a.fo, m, c, xn);
+    float ss = xn * xn;
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) ss += __shfl_xor(ss, d, 64);
+    if (a.fo.ssq && (c & 15) == 0) a.fo.ssq[(size_t)m * a.fo.ssq_ld + (c >> 4)] = ss;
 }
 
 __global__ void dequant_tiled_kernel(const uint8_t* tiled, const uint32_t* sz, const float* rscale, int fmt, int N,
@@ -619,7 +844,7 @@ __global__ void lat_kv_fill_kernel(_Float16* kc, _Float16* vt, int slot, int lat
         float v;
         if (i < lat) {
             v = synth_normal(seed, 0x4C410000u + (uint32_t)(2 * layer), (uint64_t)t * lat + i);
-            vt[((size_t)slot * lat + i) * cap + t] = (_Float16)v;
+            vt[(((size_t)slot * (cap >> 5) + (t >> 5)) * lat + i) * 32 + (t & 31)] = (_Float16)v;
         } else {
             v = synth_normal(seed, 0x4C410001u + (uint32_t)(2 * layer), (uint64_t)t * rd + (i - lat));
         }
@@ -652,7 +877,8 @@ int launch_mla_qprep(const MlaArgs& a, hipStream_t stream) {
     if (a.nope > 1024) return 3;
     if (!lds_limit(mla_qprep_kernel, (size_t)MLA_RB * 1024 * 4, attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(mla_qprep_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(mla_qprep_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh, (a.lat + MLA_CT - 1) / MLA_CT), dim3(256),
+                       lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -662,20 +888,38 @@ int launch_mla_kvprep(const MlaArgs& a, hipStream_t stream) {
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
-template <int NKK, int NDT>
-static int launch_attn_t(const MlaArgs& a, hipStream_t stream) {
+static constexpr int MLA_NP = 4;     // waves per 16-row query tile
+static constexpr int MLA_TWMAX = 3;  // query tiles per workgroup
+
+template <int NKK, int NDT, int TW>
+static int launch_attn_tw(const MlaArgs& a, hipStream_t stream) {
+    typedef MlaLds<NKK, NDT> Lc;
     static bool attr = false;
-    if (!lds_limit(mla_attn_kernel<NKK, NDT>, (size_t)2 * 2 * 2 * 128 * 16, attr)) return 4;
-    const int ntg = (a.ntiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+    const size_t lds = (size_t)Lc::K_BYTES + Lc::V_BYTES + (size_t)2 * TW * MLA_NP * 128 * 16;
+    constexpr int DEPTH = TW == 3 ? 1 : 2;  // blocks in flight (3 tiles: register budget of 12 waves)
+    if (!lds_limit(mla_attn_kernel<NKK, NDT, MLA_NP, TW, DEPTH>, lds, attr)) return 4;
+    const int ntg = (a.ntiles + TW - 1) / TW;
     const int groups8 = (a.nseq * a.nchunks + 7) / 8 * 8;
-    const size_t lds = (size_t)2 * a.tiles_per_wg * 2 * 128 * 16;
-    hipLaunchKernelGGL((mla_attn_kernel<NKK, NDT>), dim3(groups8 * ntg), dim3(128 * a.tiles_per_wg), lds, stream, a);
+    hipLaunchKernelGGL((mla_attn_kernel<NKK, NDT, MLA_NP, TW, DEPTH>), dim3(groups8 * ntg), dim3(64 * MLA_NP * TW), lds,
+                       stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
+template <int NKK, int NDT>
+static int launch_attn_t(const MlaArgs& a, hipStream_t stream) {
+    switch (a.tiles_per_wg) {
+        case 1: return launch_attn_tw<NKK, NDT, 1>(a, stream);
+        case 2: return launch_attn_tw<NKK, NDT, 2>(a, stream);
+        case 3: return launch_attn_tw<NKK, NDT, 3>(a, stream);
+    }
+    return 2;
+}
+
+int mla_tiles_per_wg_max() { return MLA_TWMAX; }
+
 int launch_mla_attn(const MlaArgs& a, hipStream_t stream) {
     if (a.chunk % 32 || a.cap % 32 || a.chunk <= 0 || a.nchunks <= 0) return 2;
-    if (a.tiles_per_wg < 1 || a.tiles_per_wg > 2 || a.ntiles < 1) return 2;
+    if (a.tiles_per_wg < 1 || a.tiles_per_wg > MLA_TWMAX || a.ntiles < 1) return 2;
     (void)hipGetLastError();
     if (a.lat == 512 && a.rd == 64) return launch_attn_t<18, 32>(a, stream);
     if (a.lat == 128 && a.rd == 32) return launch_attn_t<5, 8>(a, stream);
@@ -686,10 +930,13 @@ int launch_mla_out(const MlaArgs& a, hipStream_t stream) {
     static bool attr = false;
     const int M = a.nseq * a.S;
     const size_t lds = (size_t)MLA_RB * a.lat * 4;
-    if (a.lat > 512) return 3;
+    if (a.lat > 512 || a.lat % 16 || a.nchunks > MLA_MAXCH || !a.olat) return 3;
     if (!lds_limit(mla_out_kernel, (size_t)MLA_RB * 512 * 4, attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(mla_out_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(M * a.nh), dim3(256), 0, stream, a);
+    if (note_error(hipGetLastError())) return 4;
+    hipLaunchKernelGGL(mla_out_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh, (a.vd + MLA_CT - 1) / MLA_CT), dim3(256),
+                       lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -698,35 +945,41 @@ int launch_moe_route(const MoeArgs& a, hipStream_t stream) {
     static bool attr = false;
     if (!lds_limit(moe_route_kernel, (size_t)MOE_MAX_ROWS * 64 * 4, attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), (size_t)a.M * 64 * 4, stream, a);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(64 * MOE_RT_WAVES), (size_t)a.M * 64 * 4, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
-template <int FMT>
-static int launch_ffn_fmt(const MoeArgs& a, int phase, hipStream_t stream) {
-    const int Ne = phase == 1 ? 2 * a.D : a.H;
-    const int TB = (Ne / 16 + 3) / 4;
-    const dim3 grid((a.E + a.NS) * TB);
-    if (phase == 1) hipLaunchKernelGGL((moe_ffn_kernel<FMT, 1>), grid, dim3(512), 0, stream, a);
-    else hipLaunchKernelGGL((moe_ffn_kernel<FMT, 2>), grid, dim3(512), 0, stream, a);
+template <int FMT, int PHASE>
+static int launch_ffn_phase(const MoeArgs& a, hipStream_t stream) {
+    const int G = (PHASE == 1 ? a.H : a.D) >> 7;
+    const dim3 grid(a.cmax * a.bpe), block(512);
+    switch ((G + 7) / 8) {
+        case 1: hipLaunchKernelGGL((moe_ffn_kernel<FMT, PHASE, 1>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((moe_ffn_kernel<FMT, PHASE, 2>), grid, block, 0, stream, a); break;
+        default: return 3;
+    }
     return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+int moe_tiles_per_step(int fmt) {
+    return fmt == WF_INT4 ? MoeCfg<WF_INT4>::NTB : (fmt == WF_INT8 ? MoeCfg<WF_INT8>::NTB : MoeCfg<WF_BF16>::NTB);
 }
 
 int launch_moe_ffn(const MoeArgs& a, int phase, hipStream_t stream) {
-    if (a.H % 128 || a.D % 128 || a.H / 128 > 32 || a.D / 128 > 32) return 3;
+    if (a.H % 128 || a.D % 128 || a.H / 128 > 16 || a.D / 128 > 16 || a.bpe < 1 || a.cmax < 1) return 3;
     (void)hipGetLastError();
     switch (a.fmt) {
-        case WF_INT4: return launch_ffn_fmt<WF_INT4>(a, phase, stream);
-        case WF_INT8: return launch_ffn_fmt<WF_INT8>(a, phase, stream);
-        case WF_BF16: return launch_ffn_fmt<WF_BF16>(a, phase, stream);
+        case WF_INT4: return phase == 1 ? launch_ffn_phase<WF_INT4, 1>(a, stream) : launch_ffn_phase<WF_INT4, 2>(a, stream);
+        case WF_INT8: return phase == 1 ? launch_ffn_phase<WF_INT8, 1>(a, stream) : launch_ffn_phase<WF_INT8, 2>(a, stream);
+        case WF_BF16: return phase == 1 ? launch_ffn_phase<WF_BF16, 1>(a, stream) : launch_ffn_phase<WF_BF16, 2>(a, stream);
     }
     return 3;
 }
 
 int launch_moe_combine(const MoeArgs& a, hipStream_t stream) {
-    if (a.H % 16) return 3;
+    if (a.H % 16 || a.K + a.NS > MOE_COMB_MAXK) return 3;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(a.M), dim3(128), 0, stream, a);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(a.M, (a.H + 255) / 256), dim3(256), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

@@ -90,7 +90,7 @@ struct aarh_lat_ctx {
 
     int Mmax = 0, A = 0;
     float *x = nullptr, *raw = nullptr, *q = nullptr, *att = nullptr, *xn = nullptr, *rl = nullptr;
-    float *hbuf = nullptr, *ybuf = nullptr, *ssq = nullptr, *hidden = nullptr, *logits = nullptr, *gap = nullptr;
+    float *olat = nullptr, *hbuf = nullptr, *ybuf = nullptr, *ssq = nullptr, *hidden = nullptr, *logits = nullptr, *gap = nullptr;
     uint16_t *frag_a = nullptr, *frag_b = nullptr;
     float* apart = nullptr;
     size_t apart_elems = 0;
@@ -98,6 +98,8 @@ struct aarh_lat_ctx {
     size_t gpart_elems = 0;
     unsigned* gcnt = nullptr;
     int *cnt = nullptr, *off = nullptr, *arow = nullptr, *rowmap = nullptr;  // cnt/off per layer
+    int *chunk_e = nullptr, *chunk_r0 = nullptr, *nchunk = nullptr;
+    int cus = 256;
     float* aw = nullptr;
     int32_t *d_pos0 = nullptr, *d_slot = nullptr;
     uint32_t* d_ids = nullptr;
@@ -347,17 +349,19 @@ int run_block(Ctx* c, int l, int nseq, int S, int max_kv, const XFrag& after) {
     m.scale = (float)(1.0 / std::sqrt((double)(c->nope + c->rd)));
     const int rows = S * c->nh;
     m.ntiles = (rows + 15) / 16;
-    m.tiles_per_wg = m.ntiles >= 2 ? 2 : 1;
+    m.tiles_per_wg = std::min(m.ntiles, mla_tiles_per_wg_max());
     const int ntg = (m.ntiles + m.tiles_per_wg - 1) / m.tiles_per_wg;
     const int base = nseq * ntg;
     const int max_chunks = std::max(1, (max_kv + 31) / 32);
-    int nch = std::max(1, std::min(std::min(max_chunks, 64), (512 + base - 1) / base));
+    // about one workgroup per CU (each holds a CU's LDS), at most 64 chunks for the merge
+    int nch = std::max(1, std::min(std::min(max_chunks, 64), (c->cus + base - 1) / base));
     const int chunk = ((max_kv + nch - 1) / nch + 31) / 32 * 32;
     nch = (max_kv + chunk - 1) / chunk;
     m.chunk = chunk;
     m.nchunks = nch;
     if ((r = ensure_apart(c, (size_t)nseq * m.ntiles * nch * 16 * (c->lat + 4)))) return r;
     m.part = c->apart;
+    m.olat = c->olat;
     m.fo = xfrag(c, c->frag_b, w.op.fmt, c->OD, mp, nullptr, false);
     m.out = w.op.fmt == WF_F32 ? c->att : nullptr;
     {
@@ -403,13 +407,26 @@ int run_block(Ctx* c, int l, int nseq, int S, int max_kv, const XFrag& after) {
     e.x = c->x;
     e.fo = after;
     e.gap = c->gap;
+    e.chunk_e = c->chunk_e;
+    e.chunk_r0 = c->chunk_r0;
+    e.nchunk = c->nchunk;
+    // chunk capacity and an estimate of the chunks present (experts hit + shared + overflow)
+    const int mc = (M + 15) / 16;
+    e.cmax = M * c->K / 16 + c->E + c->NS * mc;
+    const int cexp = std::min(c->E, M * c->K) + c->NS * mc + M * c->K / 16;
+    auto slices = [&](int ntiles) {
+        const int nsteps = (ntiles + moe_tiles_per_step(w.gu.fmt) - 1) / moe_tiles_per_step(w.gu.fmt);
+        return std::max(1, std::min(nsteps, (3 * c->cus + cexp - 1) / cexp));
+    };
     {
         ProfScope ps(c, AARH_PROF_GEMV_GATEUP, 0, l, 1);
         KCHK(c, launch_moe_route(e, c->stream));
+        e.bpe = slices(2 * c->D / 16);
         KCHK(c, launch_moe_ffn(e, 1, c->stream));
     }
     {
         ProfScope ps(c, AARH_PROF_GEMV_DOWN, 0, l, 2);
+        e.bpe = slices(H / 16);
         KCHK(c, launch_moe_ffn(e, 2, c->stream));
         KCHK(c, launch_moe_combine(e, c->stream));
     }
@@ -639,9 +656,10 @@ void aarh_lat_destroy(aarh_lat_ctx* c) {
         F(c->vt[i]);
     }
     for (void* p : {(void*)c->x, (void*)c->raw, (void*)c->q, (void*)c->att, (void*)c->xn, (void*)c->rl,
-                    (void*)c->hbuf, (void*)c->ybuf, (void*)c->ssq, (void*)c->hidden, (void*)c->logits, (void*)c->gap,
+                    (void*)c->olat, (void*)c->hbuf, (void*)c->ybuf, (void*)c->ssq, (void*)c->hidden, (void*)c->logits, (void*)c->gap,
                     (void*)c->frag_a, (void*)c->frag_b, (void*)c->apart, (void*)c->gpart, (void*)c->gcnt,
-                    (void*)c->cnt, (void*)c->off, (void*)c->arow, (void*)c->rowmap, (void*)c->aw, (void*)c->d_pos0,
+                    (void*)c->cnt, (void*)c->off, (void*)c->arow, (void*)c->rowmap, (void*)c->aw, (void*)c->chunk_e,
+                    (void*)c->chunk_r0, (void*)c->nchunk, (void*)c->d_pos0,
                     (void*)c->d_slot, (void*)c->d_ids})
         F(p);
     if (c->h_pos0) (void)hipHostFree(c->h_pos0);
@@ -695,7 +713,7 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
                     "hidden, vocab, expert and n_heads*v_dim widths must be multiples of 128 (q/kv rows of 16)");
     if (c->E > 64 || c->E + c->NS > 72)
         return fail(c, AARH_ERR_UNSUPPORTED, "at most 64 routed and 72 total experts");
-    if (c->H / 128 > 32 || c->D / 128 > 32) return fail(c, AARH_ERR_UNSUPPORTED, "hidden / expert width above 4096");
+    if (c->H / 128 > 16 || c->D / 128 > 16) return fail(c, AARH_ERR_UNSUPPORTED, "hidden / expert width above 2048");
     if (g.expert_format < AARH_W_BF16 || g.expert_format > AARH_W_INT4_G128 || g.attn_format < 0 ||
         g.attn_format > AARH_W_INT4_G128 || (g.lm_head_format != 0 && g.lm_head_format != 1))
         return fail(c, AARH_ERR_CONFIG, "unknown or unsupported weight format (experts: bf16, int8, int4)");
@@ -704,6 +722,8 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
     c->cap = (g.max_seq_len + PAD_SLACK + 31) / 32 * 32;
     if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->cus <= 0)
+        c->cus = 256;
     c->layers.resize(c->L);
     build_slots(c);
     int r;
@@ -770,13 +790,17 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
     {
         const size_t M = c->Mmax, H = c->H, A = c->A, EN = c->E + c->NS;
         if (dalloc(c, &c->x, M * H * 4) || dalloc(c, &c->raw, M * c->RAW * 4) ||
-            dalloc(c, &c->q, M * c->nh * c->KDc * 4) || dalloc(c, &c->att, M * c->OD * 4) ||
+            dalloc(c, &c->q, M * c->nh * c->KDc * 4) || dalloc(c, &c->olat, M * c->nh * c->lat * 4) || dalloc(c, &c->att, M * c->OD * 4) ||
             dalloc(c, &c->xn, M * H * 4) || dalloc(c, &c->rl, M * c->E16 * 4) || dalloc(c, &c->hbuf, A * c->D * 4) ||
             dalloc(c, &c->ybuf, A * H * 4) || dalloc(c, &c->ssq, M * (H / 16) * 4) || dalloc(c, &c->hidden, M * H * 4) ||
             dalloc(c, &c->logits, M * c->V * 4) || dalloc(c, &c->gap, M * 4) ||
             dalloc(c, &c->cnt, c->L * EN * 4) || dalloc(c, &c->off, c->L * (EN + 1) * 4) ||
             dalloc(c, &c->arow, A * 4) || dalloc(c, &c->aw, A * 4) || dalloc(c, &c->rowmap, M * (c->K + c->NS) * 4))
             return AARH_ERR_DEVICE;
+        const size_t cmax = M * c->K / 16 + c->E + c->NS * ((M + 15) / 16);
+        if (dalloc(c, &c->chunk_e, cmax * 4) || dalloc(c, &c->chunk_r0, cmax * 4) || dalloc(c, &c->nchunk, 16))
+            return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(c->nchunk, 0, 16));
         HIPCHK(c, hipMemset(c->cnt, 0, c->L * EN * 4));
         const size_t gmax = (size_t)std::max(c->H, c->OD) / 128;
         const size_t halves = ((M + 15) / 16) * gmax * 16 * 32 * 8;
