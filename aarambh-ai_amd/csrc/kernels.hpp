@@ -201,8 +201,10 @@ struct MlaArgs {
     int raw_ld;
     const float* rope_cos;
     const float* rope_sin;       // [positions][rd/2]
-    const float* upk;            // [nh*nope][lat] (stored values of up_k)
-    const float* upvT;           // [nh][lat][vd] (up_v transposed per head)
+    const _Float16* upk_hi;      // up_k as fp16 hi + lo pairs, per head transposed: [nh][lat][nope]
+    const _Float16* upk_lo;
+    const _Float16* upv_hi;      // up_v as fp16 hi + lo pairs: [nh][vd][lat]
+    const _Float16* upv_lo;
     const float* kvn_w;          // [lat] latent RMSNorm weight
     float eps;
     float* q;                    // [M][nh][lat+rd]: absorbed q_lat | rotated q_rope
@@ -247,6 +249,8 @@ struct MoeArgs {
     float* x;                    // [M][H] residual stream
     XFrag fo;                    // fragments of the new x for the next consumer
     float* gap;                  // [M] running min of (k-th - (k+1)-th) router logit (null: none)
+    unsigned long long* selm;    // [M] experts selected per row (bit e), written by the ranking
+    float* wsel;                 // [M][64] dispatch weight of (row, selected expert)
     int* chunk_e;                // [cmax] expert of each 16-assignment chunk (written by the routing)
     int* chunk_r0;               // [cmax] its first assignment within the expert
     int* nchunk;                 // [1] number of chunks
@@ -257,6 +261,9 @@ int launch_moe_route(const MoeArgs& a, hipStream_t stream);
 int launch_moe_ffn(const MoeArgs& a, int phase, hipStream_t stream);
 int moe_tiles_per_step(int fmt);  // weight tiles per step of the expert projection
 int launch_moe_combine(const MoeArgs& a, hipStream_t stream);
+// fp16 hi + lo split of a row-major f32 matrix [N][K] (tblk > 0: row n = b * tblk + i,
+// column k goes to ((b * K + k) * tblk + i)).
+int launch_split_hilo(const float* src, _Float16* hi, _Float16* lo, int N, int K, int tblk, hipStream_t stream);
 // Row-major f32 copy of a tiled quantised matrix (the values its GEMV multiplies
 // by); tblk > 0 writes row n = b * tblk + i, column k at ((b * K + k) * tblk + i).
 int launch_dequant_tiled(const uint8_t* tiled, const uint32_t* sz, const float* rscale, int fmt, int N, int K,

@@ -23,55 +23,63 @@ static constexpr float LAT_LOG2E = 1.4426950408889634f;
 static constexpr int MOE_MAX_ROWS = 256;    // rows per routing launch
 static constexpr int MOE_MAX_EXPERTS = 72;  // routed (<= 64) + shared experts
 
-static constexpr int MLA_RB = 32;  // query rows per qprep / out workgroup
-static constexpr int MLA_CT = 64;  // output columns per qprep / out workgroup
+// Products of f32 values on MFMA: a = a_hi + a_lo and b = b_hi + b_lo in fp16,
+// a.b ~= a_hi b_hi + a_hi b_lo + a_lo b_hi with f32 accumulation (about 22
+// significant bits, like the f32 FMA chain it replaces).
+__device__ __forceinline__ void split_f16x8(const float* v, half8_t& hi, half8_t& lo) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const _Float16 h = (_Float16)v[j];
+        hi[j] = h;
+        lo[j] = (_Float16)(v[j] - (float)h);
+    }
+}
+
+__device__ __forceinline__ float4_t mfma3(const half8_t& ah, const half8_t& al, const half8_t& bh, const half8_t& bl,
+                                         float4_t acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+    return acc;
+}
 
 // ---------------------------------------------------------------------------
-// q prep: rotate q_rope, absorb q_nope through up_k (q_lat = up_k_h^T q_nope_h).
-// Workgroup = 32 rows x 1 head x 64 latent columns; q_nope staged in LDS as
-// [nope][32]; thread (column c, row group rg) accumulates 8 rows, the up_k
-// loads issued 8 at a time.
+// q prep: rotate q_rope, absorb q_nope through up_k (q_lat = up_k_h^T q_nope_h)
+// on MFMA.  Workgroup = 16 rows x 1 head x 64 latent columns, one 16x16 output
+// tile per wave: A = q_nope rows (f32 split hi + lo), B = up_k^T hi + lo.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) mla_qprep_kernel(MlaArgs a) {
-    extern __shared__ float4 qn4[];  // [nope][8] float4 = [nope][32 rows]
-    float* qn = (float*)qn4;
-    const int M = a.nseq * a.S, h = blockIdx.y, m0 = blockIdx.x * MLA_RB, tid = threadIdx.x;
+    const int M = a.nseq * a.S, h = blockIdx.y, mt = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, lr = lane & 15, lg = lane >> 4, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nope = a.nope, rd = a.rd, lat = a.lat, half = rd >> 1, KD = lat + rd;
-    const int nr = min(MLA_RB, M - m0);
-    for (int i = tid; i < MLA_RB * nope; i += 256) {
-        const int k = i / nope, d = i - k * nope;
-        qn[d * MLA_RB + k] = k < nr ? a.raw[(size_t)(m0 + k) * a.raw_ld + h * (nope + rd) + d] : 0.f;
-    }
-    __syncthreads();
-    const int c = tid & 63, rg = tid >> 6, j = blockIdx.z * MLA_CT + c;
-    if (j < lat) {
-        float acc[8];
+    const int jt = blockIdx.z * 4 + wid;  // 16-column tile of q_lat
+    if (jt * 16 < lat) {
+        const int m = mt * 16 + lr;
+        const float* arow = a.raw + (size_t)min(m, M - 1) * a.raw_ld + h * (nope + rd);
+        const size_t boff = ((size_t)h * lat + jt * 16 + lr) * nope;
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < nope; k0 += 32) {
+            float v[8];
+            const float4 v0 = *(const float4*)(arow + k0 + 8 * lg), v1 = *(const float4*)(arow + k0 + 8 * lg + 4);
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w; v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            if (m >= M)
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc[k] = 0.f;
-        const float* wp = a.upk + (size_t)h * nope * lat + j;
-        for (int d0 = 0; d0 < nope; d0 += 16) {
-            float w[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) w[u] = d0 + u < nope ? wp[(size_t)(d0 + u) * lat] : 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                if (d0 + u >= nope) break;
-                const float4 x0 = qn4[(d0 + u) * (MLA_RB / 4) + 2 * rg], x1 = qn4[(d0 + u) * (MLA_RB / 4) + 2 * rg + 1];
-                acc[0] = fmaf(w[u], x0.x, acc[0]);
-                acc[1] = fmaf(w[u], x0.y, acc[1]);
-                acc[2] = fmaf(w[u], x0.z, acc[2]);
-                acc[3] = fmaf(w[u], x0.w, acc[3]);
-                acc[4] = fmaf(w[u], x1.x, acc[4]);
-                acc[5] = fmaf(w[u], x1.y, acc[5]);
-                acc[6] = fmaf(w[u], x1.z, acc[6]);
-                acc[7] = fmaf(w[u], x1.w, acc[7]);
-            }
+                for (int j = 0; j < 8; j++) v[j] = 0.f;
+            half8_t ah, al;
+            split_f16x8(v, ah, al);
+            const half8_t bh = *(const half8_t*)(a.upk_hi + boff + k0 + 8 * lg);
+            const half8_t bl = *(const half8_t*)(a.upk_lo + boff + k0 + 8 * lg);
+            acc = mfma3(ah, al, bh, bl, acc);
         }
+        // D lane: rows 4 lg + i, column lr
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            if (8 * rg + k < nr) a.q[((size_t)(m0 + 8 * rg + k) * a.nh + h) * KD + j] = acc[k];
+        for (int i = 0; i < 4; i++) {
+            const int mm = mt * 16 + 4 * lg + i;
+            if (mm < M) a.q[((size_t)mm * a.nh + h) * KD + jt * 16 + lr] = acc[i];
+        }
     }
     if (blockIdx.z != 0) return;
+    const int m0 = mt * 16, nr = min(16, M - m0);
     for (int i = tid; i < nr * half; i += 256) {
         const int k = i / half, e = i - k * half, m = m0 + k;
         const int pos = a.pos0[m / a.S] + m % a.S;
@@ -410,50 +418,41 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(MlaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// up_v: o[m][h*vd + i] = sum_j up_v[h][i][j] o_lat[m][h][j] for 32 rows x 64
-// columns of one head; o_lat staged in LDS as [lat][32]; the o_proj input is
-// written as fragments (and f32 rows when o_proj reads f32).
+// up_v: o[m][h*vd + i] = sum_j up_v[h][i][j] o_lat[m][h][j] on MFMA.  Workgroup
+// = 16 rows x 1 head x 64 output columns, one 16x16 tile per wave: A = o_lat
+// rows (f32 split hi + lo), B = up_v hi + lo.  The o_proj input is written as
+// fragments (and f32 rows when o_proj reads f32).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) mla_out_kernel(MlaArgs a) {
-    extern __shared__ float4 ol4[];  // [lat][8] float4 = [lat][32 rows]
-    float* ol = (float*)ol4;
-    const int M = a.nseq * a.S, h = blockIdx.y, m0 = blockIdx.x * MLA_RB, tid = threadIdx.x;
+    const int M = a.nseq * a.S, h = blockIdx.y, mt = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, lr = lane & 15, lg = lane >> 4, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lat = a.lat, vd = a.vd;
-    const int nr = min(MLA_RB, M - m0);
-    for (int idx = tid; idx < MLA_RB * lat; idx += 256) {
-        const int k = idx / lat, j = idx - k * lat;
-        ol[j * MLA_RB + k] = k < nr ? a.olat[((size_t)(m0 + k) * a.nh + h) * lat + j] : 0.f;
-    }
-    __syncthreads();
-    const int c = tid & 63, rg = tid >> 6, i = blockIdx.z * MLA_CT + c;
-    if (i >= vd) return;
-    const float* wp = a.upvT + (size_t)h * lat * vd + i;
-    float acc[8];
+    const int it = blockIdx.z * 4 + wid;
+    if (it * 16 >= vd) return;
+    const int m = mt * 16 + lr;
+    const float* arow = a.olat + ((size_t)min(m, M - 1) * a.nh + h) * lat;
+    const size_t boff = ((size_t)h * vd + it * 16 + lr) * lat;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < lat; k0 += 32) {
+        float v[8];
+        const float4 v0 = *(const float4*)(arow + k0 + 8 * lg), v1 = *(const float4*)(arow + k0 + 8 * lg + 4);
+        v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w; v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        if (m >= M)
 #pragma unroll
-    for (int k = 0; k < 8; k++) acc[k] = 0.f;
-    for (int j0 = 0; j0 < lat; j0 += 16) {
-        float w[16];
-#pragma unroll
-        for (int u = 0; u < 16; u++) w[u] = wp[(size_t)(j0 + u) * vd];
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const float4 x0 = ol4[(j0 + u) * (MLA_RB / 4) + 2 * rg], x1 = ol4[(j0 + u) * (MLA_RB / 4) + 2 * rg + 1];
-            acc[0] = fmaf(w[u], x0.x, acc[0]);
-            acc[1] = fmaf(w[u], x0.y, acc[1]);
-            acc[2] = fmaf(w[u], x0.z, acc[2]);
-            acc[3] = fmaf(w[u], x0.w, acc[3]);
-            acc[4] = fmaf(w[u], x1.x, acc[4]);
-            acc[5] = fmaf(w[u], x1.y, acc[5]);
-            acc[6] = fmaf(w[u], x1.z, acc[6]);
-            acc[7] = fmaf(w[u], x1.w, acc[7]);
-        }
+            for (int j = 0; j < 8; j++) v[j] = 0.f;
+        half8_t ah, al;
+        split_f16x8(v, ah, al);
+        const half8_t bh = *(const half8_t*)(a.upv_hi + boff + k0 + 8 * lg);
+        const half8_t bl = *(const half8_t*)(a.upv_lo + boff + k0 + 8 * lg);
+        acc = mfma3(ah, al, bh, bl, acc);
     }
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        if (8 * rg + k >= nr) continue;
-        const int m = m0 + 8 * rg + k;
-        if (a.fo.buf) frag_put(a.fo, m, h * vd + i, acc[k]);
-        if (a.out) a.out[(size_t)m * a.nh * vd + h * vd + i] = acc[k];
+    for (int i = 0; i < 4; i++) {
+        const int mm = mt * 16 + 4 * lg + i;
+        if (mm >= M) continue;
+        const int col = h * vd + it * 16 + lr;
+        if (a.fo.buf) frag_put(a.fo, mm, col, acc[i]);
+        if (a.out) a.out[(size_t)mm * a.nh * vd + col] = acc[i];
     }
 }
 
@@ -482,73 +481,89 @@ __device__ __forceinline__ int lanes_below(unsigned long long bal) {
     return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
 }
 
+// One wave per row: bitonic sort of (logit, expert) over the lanes into routing
+// order, softmax over ranks 0..k-1 summed in rank order, the selected-expert
+// mask, the dispatch weights and the k-th / (k+1)-th logit gap.
+__global__ void __launch_bounds__(256) moe_rank_kernel(MoeArgs a) {
+    const int lane = threadIdx.x & 63, m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int E = a.E, K = a.K;
+    if (m >= a.M) return;
+    float v = lane < E ? a.logits[(size_t)m * a.lld + lane] : -INFINITY;
+    int i = lane;
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const float pv = __shfl_xor(v, j, 64);
+            const int pi = __shfl_xor(i, j, 64);
+            const bool keep_first = ((lane & j) == 0) == ((lane & k) == 0);
+            const bool take = keep_first ? route_before(pv, pi, v, i) : route_before(v, i, pv, pi);
+            if (take) {
+                v = pv;
+                i = pi;
+            }
+        }
+    }
+    // lane r now holds the r-th expert in routing order
+    const float mx = __shfl(v, 0, 64);
+    const float ev = lane < K ? expf_rn(v - mx) : 0.f;
+    float ssum = 0.f;
+    for (int r = 0; r < K; r++) ssum += __shfl(ev, r, 64);
+    if (lane < K) a.wsel[(size_t)m * 64 + i] = ev / ssum;
+    const unsigned long long bm = wave_or_u64(lane < K ? (1ull << i) : 0ull);
+    const float vk1 = __shfl(v, K - 1, 64), vk = __shfl(v, K < 64 ? K : 63, 64);
+    if (lane == 0) {
+        a.selm[m] = bm;
+        if (a.gap && K < E) a.gap[m] = fminf(a.gap[m], vk1 - vk);
+    }
+}
+
+// Single workgroup: per-expert counts, offsets and 16-assignment chunk list,
+// then the assignment lists from the row masks.
 __global__ void __launch_bounds__(1024) moe_route_kernel(MoeArgs a) {
-    extern __shared__ float wsel[];  // [M][64] dispatch weight of (row, expert)
     __shared__ unsigned long long selm[MOE_MAX_ROWS];
     __shared__ int offs[MOE_MAX_EXPERTS + 1];
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int E = a.E, K = a.K, NS = a.NS, M = a.M;
-    // ---- per row: bitonic sort of (logit, expert) over the wave's lanes into routing order ----
-    for (int m = wid; m < M; m += MOE_RT_WAVES) {
-        float v = lane < E ? a.logits[(size_t)m * a.lld + lane] : -INFINITY;
-        int i = lane;
-#pragma unroll
-        for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                const float pv = __shfl_xor(v, j, 64);
-                const int pi = __shfl_xor(i, j, 64);
-                const bool keep_first = ((lane & j) == 0) == ((lane & k) == 0);
-                const bool take = keep_first ? route_before(pv, pi, v, i) : route_before(v, i, pv, pi);
-                if (take) {
-                    v = pv;
-                    i = pi;
-                }
-            }
-        }
-        // lane r now holds the r-th expert in routing order; softmax over ranks 0..K-1 in order
-        const float mx = __shfl(v, 0, 64);
-        const float ev = lane < K ? expf_rn(v - mx) : 0.f;
-        float ssum = 0.f;
-        for (int r = 0; r < K; r++) ssum += __shfl(ev, r, 64);
-        if (lane < K) wsel[m * 64 + i] = ev / ssum;
-        const unsigned long long bm = wave_or_u64(lane < K ? (1ull << i) : 0ull);
-        const float vk1 = __shfl(v, K - 1, 64), vk = __shfl(v, K < 64 ? K : 63, 64);
-        if (lane == 0) {
-            selm[m] = bm;
-            if (a.gap && K < E) a.gap[m] = fminf(a.gap[m], vk1 - vk);
-        }
-    }
+    for (int m = tid; m < M; m += 64 * MOE_RT_WAVES) selm[m] = a.selm[m];
     __syncthreads();
     // ---- rows per expert (shared experts take every row) ----
-    for (int e = wid; e < E + NS; e += MOE_RT_WAVES) {
+    __shared__ int cnt_s[2 * 64];
+    for (int e = wid; e < 2 * 64; e += MOE_RT_WAVES) {
         int c = 0;
-        for (int m0 = 0; m0 < M; m0 += 64) {
-            const int m = m0 + lane;
-            const bool sel = m < M && (e >= E || ((selm[m] >> e) & 1ull));
-            c += __popcll(__ballot(sel));
-        }
-        if (lane == 0) {
-            a.cnt[e] = c;
-            offs[e + 1] = c;
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        offs[0] = 0;
-        int nc = 0;
-        for (int e = 0; e < E + NS; e++) {
-            const int c = offs[e + 1];
-            for (int r0 = 0; r0 < c && nc < a.cmax; r0 += 16, nc++) {
-                a.chunk_e[nc] = e;
-                a.chunk_r0[nc] = r0;
+        if (e < E + NS)
+            for (int m0 = 0; m0 < M; m0 += 64) {
+                const int m = m0 + lane;
+                const bool sel = m < M && (e >= E || ((selm[m] >> e) & 1ull));
+                c += __popcll(__ballot(sel));
             }
-            offs[e + 1] += offs[e];
-        }
-        *a.nchunk = nc;
-        for (int e = 0; e <= E + NS; e++) a.off[e] = offs[e];
+        if (lane == 0) cnt_s[e] = c;
     }
     __syncthreads();
+    // ---- offsets and the chunk list: wave 0 scans (lane l holds experts 2l, 2l + 1) ----
+    if (wid == 0) {
+        const int c0 = cnt_s[2 * lane], c1 = cnt_s[2 * lane + 1];
+        const int k0 = (c0 + 15) >> 4, k1 = (c1 + 15) >> 4;
+        const int o = wave_excl_scan_i32(c0 + c1), ko = wave_excl_scan_i32(k0 + k1);
+        if (2 * lane <= MOE_MAX_EXPERTS) offs[2 * lane] = o;
+        if (2 * lane + 1 <= MOE_MAX_EXPERTS) offs[2 * lane + 1] = o + c0;
+        const int nc = __shfl(ko + k0 + k1, 63, 64);
+        for (int r = 0; r < k0; r++)
+            if (ko + r < a.cmax) {
+                a.chunk_e[ko + r] = 2 * lane;
+                a.chunk_r0[ko + r] = 16 * r;
+            }
+        for (int r = 0; r < k1; r++)
+            if (ko + k0 + r < a.cmax) {
+                a.chunk_e[ko + k0 + r] = 2 * lane + 1;
+                a.chunk_r0[ko + k0 + r] = 16 * r;
+            }
+        if (lane == 0) *a.nchunk = min(nc, a.cmax);
+        if (2 * lane < E + NS) a.cnt[2 * lane] = c0;
+        if (2 * lane + 1 < E + NS) a.cnt[2 * lane + 1] = c1;
+    }
+    __syncthreads();
+    if (tid <= E + NS) a.off[tid] = offs[tid];
     // ---- assignments: expert lists in ascending rows; a row's slots are its routed experts
     //      in index order, then the shared experts ----
     for (int e = wid; e < E + NS; e += MOE_RT_WAVES) {
@@ -562,7 +577,7 @@ __global__ void __launch_bounds__(1024) moe_route_kernel(MoeArgs a) {
             if (sel) {
                 const int pos = k + lanes_below(bal);
                 a.arow[pos] = m;
-                a.aw[pos] = e < E ? wsel[m * 64 + e] : 1.0f;
+                a.aw[pos] = e < E ? a.wsel[(size_t)m * 64 + e] : 1.0f;
                 a.rowmap[(size_t)m * (K + NS) + (e < E ? __popcll(sm & below) : K + (e - E))] = pos;
             }
             k += __popcll(bal);
@@ -799,6 +814,26 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoeArgs a) {
     if (a.fo.ssq && (c & 15) == 0) a.fo.ssq[(size_t)m * a.fo.ssq_ld + (c >> 4)] = ss;
 }
 
+__global__ void split_hilo_kernel(const float* src, _Float16* hi, _Float16* lo, int N, int K, int tblk) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * K) return;
+    const int n = (int)(i / K), k = (int)(i % K);
+    const size_t o = tblk > 0 ? ((size_t)(n / tblk) * K + k) * tblk + n % tblk : i;
+    const float v = src[i];
+    const _Float16 h = (_Float16)v;
+    hi[o] = h;
+    lo[o] = (_Float16)(v - (float)h);
+}
+
+int launch_split_hilo(const float* src, _Float16* hi, _Float16* lo, int N, int K, int tblk, hipStream_t stream) {
+    if (tblk > 0 && N % tblk) return 2;
+    const size_t n = (size_t)N * K;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(split_hilo_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, src, hi, lo, N, K,
+                       tblk);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
 __global__ void dequant_tiled_kernel(const uint8_t* tiled, const uint32_t* sz, const float* rscale, int fmt, int N,
                                      int K, float* out, int tblk) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -857,7 +892,7 @@ __global__ void lat_kv_fill_kernel(_Float16* kc, _Float16* vt, int slot, int lat
 // ---------------------------------------------------------------------------
 bool mla_supported(int lat, int rd, int vd, int nope) {
     const bool c5 = lat == 512 && rd == 64, small = lat == 128 && rd == 32;
-    return (c5 || small) && vd > 0 && nope > 0 && nope <= 1024;
+    return (c5 || small) && vd > 0 && vd % 16 == 0 && nope > 0 && nope % 32 == 0;
 }
 
 // Raise a kernel's dynamic LDS limit to `bytes` once (first launch).
@@ -871,14 +906,10 @@ static bool lds_limit(K kernel, size_t bytes, bool& done) {
 }
 
 int launch_mla_qprep(const MlaArgs& a, hipStream_t stream) {
-    static bool attr = false;
     const int M = a.nseq * a.S;
-    const size_t lds = (size_t)MLA_RB * a.nope * 4;
-    if (a.nope > 1024) return 3;
-    if (!lds_limit(mla_qprep_kernel, (size_t)MLA_RB * 1024 * 4, attr)) return 4;
+    if (a.nope % 32 || a.lat % 16) return 3;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(mla_qprep_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh, (a.lat + MLA_CT - 1) / MLA_CT), dim3(256),
-                       lds, stream, a);
+    hipLaunchKernelGGL(mla_qprep_kernel, dim3((M + 15) / 16, a.nh, (a.lat / 16 + 3) / 4), dim3(256), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -927,25 +958,21 @@ int launch_mla_attn(const MlaArgs& a, hipStream_t stream) {
 }
 
 int launch_mla_out(const MlaArgs& a, hipStream_t stream) {
-    static bool attr = false;
     const int M = a.nseq * a.S;
-    const size_t lds = (size_t)MLA_RB * a.lat * 4;
-    if (a.lat > 512 || a.lat % 16 || a.nchunks > MLA_MAXCH || !a.olat) return 3;
-    if (!lds_limit(mla_out_kernel, (size_t)MLA_RB * 512 * 4, attr)) return 4;
+    if (a.lat % 32 || a.vd % 16 || a.nchunks > MLA_MAXCH || !a.olat) return 3;
     (void)hipGetLastError();
     hipLaunchKernelGGL(mla_merge_kernel, dim3(M * a.nh), dim3(256), 0, stream, a);
     if (note_error(hipGetLastError())) return 4;
-    hipLaunchKernelGGL(mla_out_kernel, dim3((M + MLA_RB - 1) / MLA_RB, a.nh, (a.vd + MLA_CT - 1) / MLA_CT), dim3(256),
-                       lds, stream, a);
+    hipLaunchKernelGGL(mla_out_kernel, dim3((M + 15) / 16, a.nh, (a.vd / 16 + 3) / 4), dim3(256), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
 int launch_moe_route(const MoeArgs& a, hipStream_t stream) {
     if (a.M > MOE_MAX_ROWS || a.E > 64 || a.E + a.NS > MOE_MAX_EXPERTS || a.K > a.E || a.K < 1) return 3;
-    static bool attr = false;
-    if (!lds_limit(moe_route_kernel, (size_t)MOE_MAX_ROWS * 64 * 4, attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(64 * MOE_RT_WAVES), (size_t)a.M * 64 * 4, stream, a);
+    hipLaunchKernelGGL(moe_rank_kernel, dim3((a.M + 3) / 4), dim3(256), 0, stream, a);
+    if (note_error(hipGetLastError())) return 4;
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(64 * MOE_RT_WAVES), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

@@ -40,7 +40,8 @@ struct LTensor {  // tiled quantised (or row-major f32) weight matrix
 struct LatLayer {
     float *norm1 = nullptr, *norm2 = nullptr, *kvn = nullptr;
     LTensor qkr, op, router, gu, dn;
-    float *upk = nullptr, *upvT = nullptr;  // stored values of up_k [nh*nope][lat], up_v^T [nh][lat][vd]
+    // stored values of up_k / up_v as fp16 hi + lo pairs: up_k^T [nh][lat][nope], up_v [nh][vd][lat]
+    _Float16 *upk_hi = nullptr, *upk_lo = nullptr, *upv_hi = nullptr, *upv_lo = nullptr;
 };
 
 enum LPart { L_EMBED, L_NORM, L_QP, L_KVA, L_KRP, L_UPK, L_UPV, L_OP, L_ROUTER, L_GATE, L_UP, L_DOWN };
@@ -82,7 +83,8 @@ struct aarh_lat_ctx {
     float *rope_cos = nullptr, *rope_sin = nullptr;
     float* staging = nullptr;
     size_t staging_elems = 0;
-    LTensor tmpq;  // quantisation target of up_k / up_v before their f32 copies
+    LTensor tmpq;          // quantisation target of up_k / up_v before their MFMA operand copies
+    float* tmpf = nullptr;  // their stored values as f32 rows
 
     int cap = 0;
     std::vector<_Float16*> kc, vt;
@@ -99,6 +101,8 @@ struct aarh_lat_ctx {
     unsigned* gcnt = nullptr;
     int *cnt = nullptr, *off = nullptr, *arow = nullptr, *rowmap = nullptr;  // cnt/off per layer
     int *chunk_e = nullptr, *chunk_r0 = nullptr, *nchunk = nullptr;
+    unsigned long long* selm = nullptr;
+    float* wsel = nullptr;
     int cus = 256;
     float* aw = nullptr;
     int32_t *d_pos0 = nullptr, *d_slot = nullptr;
@@ -338,8 +342,10 @@ int run_block(Ctx* c, int l, int nseq, int S, int max_kv, const XFrag& after) {
     m.raw_ld = c->RAW;
     m.rope_cos = c->rope_cos;
     m.rope_sin = c->rope_sin;
-    m.upk = w.upk;
-    m.upvT = w.upvT;
+    m.upk_hi = w.upk_hi;
+    m.upk_lo = w.upk_lo;
+    m.upv_hi = w.upv_hi;
+    m.upv_lo = w.upv_lo;
     m.kvn_w = w.kvn;
     m.eps = c->cfg.norm_eps;
     m.q = c->q;
@@ -367,7 +373,7 @@ int run_block(Ctx* c, int l, int nseq, int S, int max_kv, const XFrag& after) {
     {
         // cache bytes read (c_kv + k_rope rows, transposed c_kv) and up_k / up_v reads
         const double kvb = (double)max_kv * nseq * (2.0 * (c->lat + c->rd) + 2.0 * c->lat);
-        const double ub = 4.0 * (double)c->nh * c->lat * (c->nope + c->vd);
+        const double ub = 4.0 * (double)c->nh * c->lat * (c->nope + c->vd);  // fp16 hi + lo pairs
         ProfScope ps(c, AARH_PROF_ATTENTION, kvb + ub);
         KCHK(c, launch_mla_qprep(m, c->stream));
         KCHK(c, launch_mla_kvprep(m, c->stream));
@@ -407,6 +413,8 @@ int run_block(Ctx* c, int l, int nseq, int S, int max_kv, const XFrag& after) {
     e.x = c->x;
     e.fo = after;
     e.gap = c->gap;
+    e.selm = c->selm;
+    e.wsel = c->wsel;
     e.chunk_e = c->chunk_e;
     e.chunk_r0 = c->chunk_r0;
     e.nchunk = c->nchunk;
@@ -530,13 +538,15 @@ int place_staging(Ctx* c, int id) {
     }
     LatLayer& b = c->layers[s.layer];
     if (s.part == L_UPK || s.part == L_UPV) {
-        // the f32 copy holds exactly the values the attention format stores
-        float* dst = s.part == L_UPK ? b.upk : b.upvT;
-        const int tblk = s.part == L_UPV ? c->vd : 0;
+        // exactly the values the attention format stores, split into fp16 hi + lo MFMA operands
         LTensor& t = c->tmpq;
         KCHK(c, launch_quantise_tiled(c->staging, (int)s.rows, (int)s.cols, t.fmt, t.w, t.sz, t.rscale, 0, (int)s.rows,
                                       0, c->stream));
-        KCHK(c, launch_dequant_tiled(t.w, t.sz, t.rscale, t.fmt, (int)s.rows, (int)s.cols, dst, tblk, c->stream));
+        KCHK(c, launch_dequant_tiled(t.w, t.sz, t.rscale, t.fmt, (int)s.rows, (int)s.cols, c->tmpf, 0, c->stream));
+        if (s.part == L_UPK)
+            KCHK(c, launch_split_hilo(c->tmpf, b.upk_hi, b.upk_lo, (int)s.rows, (int)s.cols, c->nope, c->stream));
+        else
+            KCHK(c, launch_split_hilo(c->tmpf, b.upv_hi, b.upv_lo, (int)s.rows, (int)s.cols, 0, c->stream));
         return 0;
     }
     LTensor* t = nullptr;
@@ -638,8 +648,10 @@ void aarh_lat_destroy(aarh_lat_ctx* c) {
         F(b.norm1);
         F(b.norm2);
         F(b.kvn);
-        F(b.upk);
-        F(b.upvT);
+        F(b.upk_hi);
+        F(b.upk_lo);
+        F(b.upv_hi);
+        F(b.upv_lo);
         free_tensor(b.qkr);
         free_tensor(b.op);
         free_tensor(b.router);
@@ -647,6 +659,7 @@ void aarh_lat_destroy(aarh_lat_ctx* c) {
         free_tensor(b.dn);
     }
     free_tensor(c->tmpq);
+    F(c->tmpf);
     F(c->final_norm);
     F(c->rope_cos);
     F(c->rope_sin);
@@ -659,7 +672,7 @@ void aarh_lat_destroy(aarh_lat_ctx* c) {
                     (void*)c->olat, (void*)c->hbuf, (void*)c->ybuf, (void*)c->ssq, (void*)c->hidden, (void*)c->logits, (void*)c->gap,
                     (void*)c->frag_a, (void*)c->frag_b, (void*)c->apart, (void*)c->gpart, (void*)c->gcnt,
                     (void*)c->cnt, (void*)c->off, (void*)c->arow, (void*)c->rowmap, (void*)c->aw, (void*)c->chunk_e,
-                    (void*)c->chunk_r0, (void*)c->nchunk, (void*)c->d_pos0,
+                    (void*)c->chunk_r0, (void*)c->nchunk, (void*)c->selm, (void*)c->wsel, (void*)c->d_pos0,
                     (void*)c->d_slot, (void*)c->d_ids})
         F(p);
     if (c->h_pos0) (void)hipHostFree(c->h_pos0);
@@ -706,8 +719,8 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
     c->Mmax = g.max_rows;
     c->A = c->Mmax * (c->K + c->NS);
     if (!mla_supported(c->lat, c->rd, c->vd, c->nope))
-        return fail(c, AARH_ERR_UNSUPPORTED, "latent/rope widths (%d, %d) unsupported: (512, 64) or (128, 32)", c->lat,
-                    c->rd);
+        return fail(c, AARH_ERR_UNSUPPORTED, "latent/rope widths (%d, %d) unsupported: (512, 64) or (128, 32), nope %% 32 == 0, v_dim %% 16 == 0",
+                    c->lat, c->rd);
     if (c->H % 128 || c->V % 128 || c->D % 128 || c->OD % 128 || c->RAW % 16 || (c->nh * c->nope) % 16 || c->OD % 16)
         return fail(c, AARH_ERR_UNSUPPORTED,
                     "hidden, vocab, expert and n_heads*v_dim widths must be multiples of 128 (q/kv rows of 16)");
@@ -750,12 +763,17 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
             (r = alloc_tensor(c, b.gu, ef, (c->E + c->NS) * 2 * c->D, c->H)) ||
             (r = alloc_tensor(c, b.dn, ef, (c->E + c->NS) * c->H, c->D)))
             return r;
-        const size_t ub = (size_t)c->nh * c->nope * c->lat * 4, vb = (size_t)c->nh * c->vd * c->lat * 4;
-        if (dalloc(c, &b.upk, ub) || dalloc(c, &b.upvT, vb)) return AARH_ERR_DEVICE;
-        HIPCHK(c, hipMemset(b.upk, 0, ub));
-        HIPCHK(c, hipMemset(b.upvT, 0, vb));
+        const size_t ub = (size_t)c->nh * c->nope * c->lat * 2, vb = (size_t)c->nh * c->vd * c->lat * 2;
+        if (dalloc(c, &b.upk_hi, ub) || dalloc(c, &b.upk_lo, ub) || dalloc(c, &b.upv_hi, vb) ||
+            dalloc(c, &b.upv_lo, vb))
+            return AARH_ERR_DEVICE;
+        HIPCHK(c, hipMemset(b.upk_hi, 0, ub));
+        HIPCHK(c, hipMemset(b.upk_lo, 0, ub));
+        HIPCHK(c, hipMemset(b.upv_hi, 0, vb));
+        HIPCHK(c, hipMemset(b.upv_lo, 0, vb));
     }
     if ((r = alloc_tensor(c, c->tmpq, af, c->nh * std::max(c->nope, c->vd), c->lat))) return r;
+    if (dalloc(c, &c->tmpf, (size_t)c->nh * std::max(c->nope, c->vd) * c->lat * 4)) return AARH_ERR_DEVICE;
     if (dalloc(c, &c->final_norm, c->H * 4)) return AARH_ERR_DEVICE;
     KCHK(c, launch_fill_f32(c->final_norm, c->H, 1.0f, c->stream));
     // MLA's own rope_dim-wide RoPE table (model.rs:1112-1118, rope_scaling.rs:6-11), host f32
@@ -798,7 +816,8 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
             dalloc(c, &c->arow, A * 4) || dalloc(c, &c->aw, A * 4) || dalloc(c, &c->rowmap, M * (c->K + c->NS) * 4))
             return AARH_ERR_DEVICE;
         const size_t cmax = M * c->K / 16 + c->E + c->NS * ((M + 15) / 16);
-        if (dalloc(c, &c->chunk_e, cmax * 4) || dalloc(c, &c->chunk_r0, cmax * 4) || dalloc(c, &c->nchunk, 16))
+        if (dalloc(c, &c->chunk_e, cmax * 4) || dalloc(c, &c->chunk_r0, cmax * 4) || dalloc(c, &c->nchunk, 16) ||
+            dalloc(c, &c->selm, M * 8) || dalloc(c, &c->wsel, M * 64 * 4))
             return AARH_ERR_DEVICE;
         HIPCHK(c, hipMemset(c->nchunk, 0, 16));
         HIPCHK(c, hipMemset(c->cnt, 0, c->L * EN * 4));
