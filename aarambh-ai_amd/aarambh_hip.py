@@ -29,6 +29,7 @@ W_F32, W_BF16, W_INT8_ROW, W_INT4_G128 = 0, 1, 2, 3
 KV_F32, KV_F16, KV_INT8 = 0, 1, 2
 T_NORM, T_LINEAR, T_EMBED = 0, 1, 2
 FLAG_RATIO_NEAR, FLAG_CDF_NEAR = 1, 2
+TOP_CANDIDATES = 5  # engine.rs:70
 PROF_NAMES = ["gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down", "gemv_lmhead", "attention", "accept", "other"]
 
 
@@ -124,7 +125,9 @@ def lib():
         "aarh_session_result": (C.c_int, [_P, _P, C.c_int32, _P, _P, C.POINTER(_Stats)]),
         "aarh_session_end": (None, [_P]),
         "aarh_spec_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
-                                         _P, _P, _P, C.POINTER(_Stats)]),
+                                         _P, _P, _P, C.POINTER(_Stats), _P, _P]),
+        "aarh_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
+        "aarh_top_candidates": (C.c_int, [_P, _P, C.c_int, C.c_int, C.POINTER(_Sampler), C.c_int, _P, _P, _P]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
@@ -160,6 +163,7 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
+            "aarh_session_candidates", "aarh_top_candidates",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -251,9 +255,16 @@ class GenerationOutput:
     token_ids: list
     finish_reason: str
     speculative_stats: SpeculativeStats = field(default_factory=SpeculativeStats)
+    # per committed token: [(token_id, probability)] * TOP_CANDIDATES (GenerationStep.candidates,
+    # engine.rs:95-110); filled by Session.result and SpeculativeEngine
+    candidates: list = field(default_factory=list)
 
 
 FINISH = {0: "MaxTokens", 1: "EosToken", 2: "ContextLimit"}
+
+
+def _candidate_lists(ids, probs):
+    return [[(int(i), float(p)) for i, p in zip(ri, rp)] for ri, rp in zip(ids, probs)]
 
 
 _LIVE = weakref.WeakSet()
@@ -379,6 +390,20 @@ class HipModel:
             out[n] = {"ms": ms.value, "bytes": by.value, "launches": cnt.value}
         return out
 
+    def top_candidates(self, logits, sampler, n=TOP_CANDIDATES):
+        """Sampler::top_candidates_from_probabilities of each row of a device logits tensor
+        [rows, V] (torch, f32) under `sampler`; returns (ids [rows, n] int32, probs [rows, n])."""
+        import torch
+        rows, V = logits.shape
+        ids = torch.empty((rows, n), dtype=torch.int32, device=logits.device)
+        probs = torch.empty((rows, n), dtype=torch.float32, device=logits.device)
+        torch.cuda.synchronize()
+        self._check(lib().aarh_top_candidates(self.h, C.c_void_p(logits.data_ptr()), rows, V,
+                                              C.byref(sampler._c()), n, C.c_void_p(ids.data_ptr()),
+                                              C.c_void_p(probs.data_ptr()), None))
+        self.sync()
+        return ids, probs
+
     def accept_sample(self, target, draft, draft_tokens, sampler, bonus, seeds=None, word_offsets=None,
                       uniforms=None, n_proposals=None):
         """Acceptance on device tensors (torch cuda tensors).  target [B, Kt, V] f32,
@@ -465,14 +490,18 @@ class SpeculativeEngine:
         n = np.zeros(nseq, np.int32)
         fin = np.zeros(nseq, np.int32)
         stats = (_Stats * nseq)()
+        cap = max(max_new_tokens, 1)
+        ci = np.zeros((nseq, cap, TOP_CANDIDATES), np.uint32)
+        cp = np.zeros((nseq, cap, TOP_CANDIDATES), np.float32)
         t = self.target
         t._check(lib().aarh_spec_generate(t.h, self.draft.h, _ptr(prompts), nseq, plen, max_new_tokens,
                                           self.config.num_draft_tokens, C.byref(sampler._c()), _ptr(sd),
-                                          _ptr(out), _ptr(n), _ptr(fin), stats))
+                                          _ptr(out), _ptr(n), _ptr(fin), stats, _ptr(ci), _ptr(cp)))
         res = []
         for b in range(nseq):
             st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
-            res.append(GenerationOutput(list(out[b, :n[b]]), FINISH[int(fin[b])], st))
+            res.append(GenerationOutput(list(out[b, :n[b]]), FINISH[int(fin[b])], st,
+                                        _candidate_lists(ci[b, :n[b]], cp[b, :n[b]])))
         return res
 
     def generate(self, prompt_ids, max_new_tokens, sampler: Sampler):
@@ -509,10 +538,14 @@ class Session:
         stats = (_Stats * n)()
         self.engine.model._check(lib().aarh_session_result(self.h, _ptr(out), out.shape[1], _ptr(ln), _ptr(fin),
                                                            stats))
+        ci = np.zeros((n, out.shape[1], TOP_CANDIDATES), np.uint32)
+        cp = np.zeros((n, out.shape[1], TOP_CANDIDATES), np.float32)
+        self.engine.model._check(lib().aarh_session_candidates(self.h, _ptr(ci), _ptr(cp), out.shape[1]))
         res = []
         for b in range(n):
             st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
-            res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st))
+            res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st,
+                                        _candidate_lists(ci[b, :ln[b]], cp[b, :ln[b]])))
         return res
 
     def close(self):

@@ -257,4 +257,139 @@ int launch_accept(const AcceptArgs& a, hipStream_t stream) {
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
+// ---------------------------------------------------------------------------
+// Sampler::top_candidates_from_probabilities (sampler.rs:188-208) of each row's
+// distribution as the engines build it (Sampler::probabilities, sampler.rs:
+// 102-118): a stable descending sort truncated to n, i.e. the n largest
+// probabilities, equal probabilities in ascending token order.  Keys
+// (probability bits << 32 | ~token) order both at once; each thread keeps its
+// n best, wave 0 merges the 512 sorted lists.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
+    extern __shared__ float lds[];
+    __shared__ unsigned long long keys[ACC_THREADS][CAND_MAX];
+    __shared__ float red_f[ACC_THREADS / WAVE];
+    __shared__ int red_k[ACC_THREADS / WAVE], red_i[ACC_THREADS / WAVE];
+    __shared__ float sh[2];
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int V = a.V, n = a.n;
+    const float* row = a.logits + (size_t)blockIdx.x * a.ld;
+    int am = -1;
+    float S = 1.0f;
+    if (a.greedy) {
+        // argmax, last index on ties (sampler.rs:211-215 / argmax)
+        int bk = INT_MIN, bi = 0;
+        for (int j = tid; j < V; j += ACC_THREADS) {
+            const int k = total_key(row[j]);
+            if (k >= bk) { bk = k; bi = j; }
+        }
+        for (int d = 32; d >= 1; d >>= 1) {
+            const int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
+            if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
+        }
+        if (lane == 0) { red_k[wid] = bk; red_i[wid] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            int k0 = red_k[0], i0 = red_i[0];
+            for (int w = 1; w < ACC_THREADS / WAVE; w++)
+                if (red_k[w] > k0 || (red_k[w] == k0 && red_i[w] > i0)) { k0 = red_k[w]; i0 = red_i[w]; }
+            red_i[0] = i0;
+        }
+        __syncthreads();
+        am = red_i[0];
+    } else {
+        const float T = a.temperature;
+        float mx = -INFINITY;
+        for (int j = tid; j < V; j += ACC_THREADS) {
+            const float m = row[j] / T;
+            if (isfinite(m)) mx = fmaxf(mx, m);
+        }
+        mx = wave_max_f32(mx);
+        if (lane == 0) red_f[wid] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            float m0 = red_f[0];
+            for (int w = 1; w < ACC_THREADS / WAVE; w++) m0 = fmaxf(m0, red_f[w]);
+            sh[0] = m0;
+        }
+        __syncthreads();
+        mx = sh[0];
+        for (int j = tid; j < V; j += ACC_THREADS) {
+            const float m = row[j] / T;
+            lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
+        }
+        __syncthreads();
+        if (wid == 0) {
+            const SeqSum ss = seq_sum_wave(lds, V, -1.0f);
+            if (lane == 0) sh[1] = ss.total;
+        }
+        __syncthreads();
+        S = sh[1];
+    }
+    // ---- this thread's n best keys, descending ----
+    unsigned long long best[CAND_MAX];
+#pragma unroll
+    for (int i = 0; i < CAND_MAX; i++) best[i] = 0ull;
+    for (int j = tid; j < V; j += ACC_THREADS) {
+        const float p = a.greedy ? (j == am ? 1.0f : 0.0f) : lds[j] / S;
+        unsigned long long k = ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)(~(unsigned)j);
+#pragma unroll
+        for (int i = 0; i < CAND_MAX; i++) {
+            if (i < n && k > best[i]) {
+                const unsigned long long t = best[i];
+                best[i] = k;
+                k = t;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < CAND_MAX; i++) keys[tid][i] = best[i];
+    __syncthreads();
+    if (wid != 0) return;
+    // ---- wave 0: lane l owns lists l + 64 q; n rounds of a wave-wide max over list heads ----
+    int head[ACC_THREADS / 64];
+#pragma unroll
+    for (int q = 0; q < ACC_THREADS / 64; q++) head[q] = 0;
+    for (int r = 0; r < n; r++) {
+        unsigned long long mk = 0ull;
+        int mq = -1;
+#pragma unroll
+        for (int q = 0; q < ACC_THREADS / 64; q++) {
+            const unsigned long long k = head[q] < n ? keys[lane + 64 * q][head[q]] : 0ull;
+            if (k > mk) { mk = k; mq = q; }
+        }
+        unsigned long long wk = mk;
+        for (int d = 32; d >= 1; d >>= 1) {
+            const unsigned lo = __shfl_xor((unsigned)wk, d, 64), hi = __shfl_xor((unsigned)(wk >> 32), d, 64);
+            const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+            wk = o > wk ? o : wk;
+        }
+        if (mk == wk && mk != 0ull) {
+#pragma unroll
+            for (int q = 0; q < ACC_THREADS / 64; q++)
+                if (q == mq) head[q]++;
+        }
+        if (lane == 0) {
+            a.ids[(size_t)blockIdx.x * n + r] = wk ? ~(unsigned)(wk & 0xFFFFFFFFull) : 0xFFFFFFFFu;
+            a.probs[(size_t)blockIdx.x * n + r] = __uint_as_float((unsigned)(wk >> 32));
+        }
+    }
+}
+
+int launch_candidates(const CandArgs& a, hipStream_t stream) {
+    if (a.n < 1 || a.n > CAND_MAX || a.rows <= 0 || a.V <= 0) return 2;
+    const size_t lds = a.greedy ? 0 : (size_t)a.V * sizeof(float);
+    if (lds > MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX) return 3;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (note_error(hipFuncSetAttribute((const void*)candidates_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)(MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX))))
+            return 4;
+        attr_set = true;
+    }
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(candidates_kernel, dim3(a.rows), dim3(ACC_THREADS), lds, stream, a);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
 }  // namespace aarh

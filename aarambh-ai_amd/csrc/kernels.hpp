@@ -154,6 +154,20 @@ struct AcceptArgs {
 };
 
 int launch_accept(const AcceptArgs& a, hipStream_t stream);
+
+// Top-n candidates of each row's sampling distribution (greedy: one-hot at the
+// argmax; else softmax at T with the exact sequential normaliser).
+static constexpr int CAND_MAX = 5;  // engine.rs:70 top_candidates
+struct CandArgs {
+    const float* logits;  // [rows][ld]
+    long long ld;
+    int rows, V, n;
+    int greedy;
+    float temperature;
+    uint32_t* ids;        // [rows][n]
+    float* probs;         // [rows][n]
+};
+int launch_candidates(const CandArgs& a, hipStream_t stream);
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
 // Many-row variant (M > 16, fragments with mp = 16, all rows in one launch).
 int launch_gemm(const GemvArgs& a, hipStream_t stream);

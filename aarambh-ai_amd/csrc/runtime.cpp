@@ -1092,6 +1092,33 @@ int aarh_accept_sample(aarh_ctx* c, const float* target, int target_rows, const 
     return 0;
 }
 
+int aarh_top_candidates(aarh_ctx* c, const float* logits, int rows, int V, const aarh_sampler* s, int n,
+                        uint32_t* ids, float* probs, void* stream) {
+    if (!c || !s || !logits || !ids || !probs) return AARH_ERR_CONFIG;
+    if (rows <= 0 || V <= 0 || n < 1 || n > CAND_MAX)
+        return fail(c, AARH_ERR_SHAPE, "bad candidate shape rows=%d V=%d n=%d (n <= %d)", rows, V, n, CAND_MAX);
+    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
+    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
+        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
+    CandArgs a{};
+    a.logits = logits;
+    a.ld = V;
+    a.rows = rows;
+    a.V = V;
+    a.n = n;
+    a.greedy = greedy ? 1 : 0;
+    a.temperature = s->temperature;
+    a.ids = ids;
+    a.probs = probs;
+    int r;
+    {
+        ProfScope ps(c, AARH_PROF_ACCEPT, (double)rows * V * 4.0);
+        r = launch_candidates(a, stream ? (hipStream_t)stream : c->stream);
+    }
+    if (r) return fail(c, r, "candidate launch failed: %d %s", r, last_launch_error());
+    return 0;
+}
+
 int aarh_prof_enable(aarh_ctx* c, int enable) {
     if (!c) return AARH_ERR_CONFIG;
     c->prof = enable != 0;
@@ -1146,6 +1173,62 @@ constexpr uint32_t EOS_ID = 0;  // tokenizer/src/special.rs:33
 
 }  // namespace
 
+namespace {
+
+// Top candidates of every committed token: Sampler::top_candidates_from_probabilities
+// (sampler.rs:188-208) over the target distribution of the token's position
+// (mtp_speculative.rs:247-250), engine.rs:70 top_candidates = 5.  Output metadata.
+struct CandBuf {
+    uint32_t* ids = nullptr;  // device [rows][CAND_MAX] of the current round
+    float* probs = nullptr;
+    std::vector<uint32_t> hids;
+    std::vector<float> hprobs;
+    std::vector<std::vector<uint32_t>> out_ids;  // per sequence, CAND_MAX per committed token
+    std::vector<std::vector<float>> out_probs;
+
+    int alloc(aarh_ctx* c, int rows, int nseq) {
+        if (dalloc(c, &ids, (size_t)rows * CAND_MAX * 4) || dalloc(c, &probs, (size_t)rows * CAND_MAX * 4))
+            return AARH_ERR_DEVICE;
+        hids.assign((size_t)rows * CAND_MAX, 0);
+        hprobs.assign((size_t)rows * CAND_MAX, 0.f);
+        out_ids.assign(nseq, {});
+        out_probs.assign(nseq, {});
+        return 0;
+    }
+    void release() {
+        if (ids) (void)hipFree(ids);
+        if (probs) (void)hipFree(probs);
+        ids = nullptr;
+        probs = nullptr;
+    }
+    int launch(aarh_ctx* c, const float* rows_base, int rows, int V, const aarh_sampler& s) {
+        return aarh_top_candidates(c, rows_base, rows, V, &s, CAND_MAX, ids, probs, nullptr);
+    }
+    // after the stream has synchronised
+    int fetch(aarh_ctx* c, int rows) {
+        HIPCHK(c, hipMemcpy(hids.data(), ids, (size_t)rows * CAND_MAX * 4, hipMemcpyDeviceToHost));
+        HIPCHK(c, hipMemcpy(hprobs.data(), probs, (size_t)rows * CAND_MAX * 4, hipMemcpyDeviceToHost));
+        return 0;
+    }
+    void commit(int b, int row) {
+        out_ids[b].insert(out_ids[b].end(), hids.begin() + (size_t)row * CAND_MAX,
+                          hids.begin() + (size_t)(row + 1) * CAND_MAX);
+        out_probs[b].insert(out_probs[b].end(), hprobs.begin() + (size_t)row * CAND_MAX,
+                            hprobs.begin() + (size_t)(row + 1) * CAND_MAX);
+    }
+    void copy_out(int nseq, int cap, uint32_t* oi, float* op) const {
+        for (int b = 0; b < nseq; b++) {
+            const size_t n = std::min(out_ids[b].size(), (size_t)cap * CAND_MAX);
+            for (size_t i = 0; i < n; i++) {
+                if (oi) oi[(size_t)b * cap * CAND_MAX + i] = out_ids[b][i];
+                if (op) op[(size_t)b * cap * CAND_MAX + i] = out_probs[b][i];
+            }
+        }
+    }
+};
+
+}  // namespace
+
 struct aarh_session {
     aarh_ctx* c = nullptr;
     int nseq = 0, K = 0, max_new = 0, max_new_req = 0, available = 0;
@@ -1167,8 +1250,10 @@ struct aarh_session {
     std::vector<aarh_spec_stats> stats;
     std::vector<uint32_t> hprops;
     std::vector<int32_t> slots, base, count, hnp, hlen, htok, hdraws, hstatus;
+    CandBuf cand;
 
     ~aarh_session() {
+        cand.release();
         for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)props, (void*)acc_len,
                         (void*)acc_tok, (void*)acc_draws, (void*)acc_status, (void*)nprop, (void*)acc_flags,
                         (void*)seeds, (void*)offs, (void*)src, (void*)dst})
@@ -1280,7 +1365,9 @@ int session_round(aarh_session* e) {
                                     e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
                                     nullptr)))
             return r;
+        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = sync_stream(c))) return r;
+        if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
         HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->hdraws.data(), e->acc_draws, nseq * 4, hipMemcpyDeviceToHost));
@@ -1306,6 +1393,7 @@ int session_round(aarh_session* e) {
                 break;
             }
             e->out[b].push_back(t);
+            e->cand.commit(b, b * (K + 1) + i);
             if ((int)e->out[b].size() == e->max_new) done = true;
         }
         if (done) {
@@ -1322,6 +1410,7 @@ int session_round(aarh_session* e) {
                 continue;
             }
             e->out[b].push_back(repl);
+            e->cand.commit(b, b * (K + 1) + acc);
             e->hprops[(size_t)b * K + acc] = repl;  // replay ids = proposals[..i] + replacement
             replay_seq.push_back(b);
             replay_len.push_back(acc + 1);
@@ -1436,6 +1525,10 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
     SA(src, (size_t)2 * g.max_batch * sizeof(void*));
     SA(dst, (size_t)2 * g.max_batch * sizeof(void*));
 #undef SA
+    if ((r = e->cand.alloc(c, nseq * (K + 1), nseq))) {
+        delete e;
+        return r;
+    }
     std::vector<uint64_t> hs(nseq);
     for (int b = 0; b < nseq; b++) hs[b] = seeds ? seeds[b] : 0;
     if (hipMemcpy(e->seeds, hs.data(), nseq * 8, hipMemcpyHostToDevice) != hipSuccess) {
@@ -1526,6 +1619,12 @@ int aarh_session_result(aarh_session* e, uint32_t* out_tokens, int32_t out_cap, 
     return 0;
 }
 
+int aarh_session_candidates(aarh_session* e, uint32_t* ids, float* probs, int32_t cap) {
+    if (!e || cap < 0) return AARH_ERR_CONFIG;
+    e->cand.copy_out(e->nseq, cap, ids, probs);
+    return 0;
+}
+
 void aarh_session_end(aarh_session* e) { delete e; }
 
 int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
@@ -1573,8 +1672,10 @@ struct XSession {
     std::vector<int32_t> finish, pending, np, tbase, dbase, hlen, htok, hdraws, hstatus;
     std::vector<aarh_spec_stats> stats;
     std::vector<uint32_t> hprops;
+    CandBuf cand;
 
     ~XSession() {
+        cand.release();
         for (void* p : {(void*)tgt, (void*)drf, (void*)props, (void*)acc_len, (void*)acc_tok, (void*)acc_draws,
                         (void*)acc_status, (void*)nprop, (void*)acc_flags, (void*)seeds, (void*)offs, (void*)src,
                         (void*)dst})
@@ -1741,7 +1842,9 @@ int xsession_round(XSession* e) {
                                     e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
                                     e->acc_status, nullptr)))
             return r;
+        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = sync_stream(c))) return r;
+        if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
         HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->hdraws.data(), e->acc_draws, nseq * 4, hipMemcpyDeviceToHost));
@@ -1768,6 +1871,7 @@ int xsession_round(XSession* e) {
                 break;
             }
             e->out[b].push_back(t);
+            e->cand.commit(b, b * (K + 1) + i);
             if ((int)e->out[b].size() == e->max_new) done = true;
         }
         if (done) {
@@ -1791,6 +1895,7 @@ int xsession_round(XSession* e) {
                 continue;
             }
             e->out[b].push_back(repl);
+            e->cand.commit(b, b * (K + 1) + acc);
             // draft: accepted prefix replay + the replacement, one launch (two reference forwards)
             std::vector<uint32_t> dr(e->hprops.begin() + (size_t)b * K, e->hprops.begin() + (size_t)b * K + acc);
             dr.push_back(repl);
@@ -1809,6 +1914,7 @@ int xsession_round(XSession* e) {
                 continue;
             }
             e->out[b].push_back(bonus);
+            e->cand.commit(b, b * (K + 1) + npb);
             ds.push_back(b);
             dof.push_back(d->kv_len[b]);
             di.push_back({bonus});
@@ -1840,7 +1946,8 @@ int xsession_round(XSession* e) {
 extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len,
                                   int max_new_tokens, int num_draft_tokens, const aarh_sampler* s,
                                   const uint64_t* seeds, uint32_t* out_tokens, int32_t* out_len,
-                                  int32_t* finish_reason, aarh_spec_stats* stats) {
+                                  int32_t* finish_reason, aarh_spec_stats* stats, uint32_t* out_cand_ids,
+                                  float* out_cand_probs) {
     if (!c || !d || !s) return AARH_ERR_CONFIG;
     if (num_draft_tokens <= 0) return fail(c, AARH_ERR_CONFIG, "num_draft_tokens must be greater than zero");
     if (num_draft_tokens >= PAD_SLACK)
@@ -1894,6 +2001,7 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
     XA(src, (size_t)2 * c->cfg.max_batch * sizeof(void*));
     XA(dst, (size_t)2 * c->cfg.max_batch * sizeof(void*));
 #undef XA
+    if ((r = e.cand.alloc(c, nseq * (K + 1), nseq))) return r;
     // rows of requests that sit out a step are sampled too (and ignored): keep them finite
     HIPCHK(c, hipMemset(e.tgt, 0, (size_t)nseq * (K + 1) * V * 4));
     HIPCHK(c, hipMemset(e.drf, 0, (size_t)nseq * K * V * 4));
@@ -1958,5 +2066,6 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
                 std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
         }
     }
+    e.cand.copy_out(nseq, max_new_tokens, out_cand_ids, out_cand_probs);
     return 0;
 }

@@ -44,6 +44,7 @@ enum { AARH_KV_F32 = 0, AARH_KV_F16 = 1, AARH_KV_INT8 = 2 };
 enum { AARH_T_NORM = 0, AARH_T_LINEAR = 1, AARH_T_EMBED = 2 };
 enum { AARH_FINISH_MAX_TOKENS = 0, AARH_FINISH_EOS = 1, AARH_FINISH_CONTEXT_LIMIT = 2 };
 enum { AARH_FLAG_RATIO_NEAR = 1u, AARH_FLAG_CDF_NEAR = 2u };
+enum { AARH_TOP_CANDIDATES = 5 };
 
 typedef struct aarh_ctx aarh_ctx;
 
@@ -151,6 +152,11 @@ int aarh_session_begin(aarh_ctx *ctx, const uint32_t *prompts, int nseq, int pro
 int aarh_session_step(aarh_session *session, int max_rounds, int32_t *all_done);
 int aarh_session_result(aarh_session *session, uint32_t *out_tokens, int32_t out_cap, int32_t *out_len,
                         int32_t *finish_reason, aarh_spec_stats *stats);
+/* Top AARH_TOP_CANDIDATES candidates (token id, probability) of every committed token, from the
+   target distribution of its position: Sampler::top_candidates_from_probabilities
+   (inference/src/sampler.rs:188-208, engine.rs:70 top_candidates = 5; GenerationStep.candidates
+   engine.rs:95-110).  ids/probs [nseq][out_cap][AARH_TOP_CANDIDATES], host memory. */
+int aarh_session_candidates(aarh_session *session, uint32_t *ids, float *probs, int32_t out_cap);
 void aarh_session_end(aarh_session *session);
 
 /* --- external-draft engine (SpeculativeEngine::generate_with_callback,
@@ -162,11 +168,20 @@ void aarh_session_end(aarh_session *session);
    tests them in order and samples the replacement (rejection) or bonus token (all
    accepted), both caches roll back by index and replay the accepted prefix.  The
    context limit is the smaller of the two models' max_seq_len.  Outputs as for
-   aarh_mtp_generate. */
+   aarh_mtp_generate, plus (when non-NULL) the committed tokens' top candidates
+   [nseq][max_new_tokens][AARH_TOP_CANDIDATES] as for aarh_session_candidates. */
 int aarh_spec_generate(aarh_ctx *target, aarh_ctx *draft, const uint32_t *prompts, int nseq,
                        int prompt_len, int max_new_tokens, int num_draft_tokens,
                        const aarh_sampler *sampler, const uint64_t *seeds, uint32_t *out_tokens,
-                       int32_t *out_len, int32_t *finish_reason, aarh_spec_stats *stats);
+                       int32_t *out_len, int32_t *finish_reason, aarh_spec_stats *stats,
+                       uint32_t *out_cand_ids, float *out_cand_probs);
+
+/* --- Sampler::top_candidates_from_probabilities (sampler.rs:188-208) of each row's sampling
+   distribution (Sampler::probabilities: greedy one-hot at the argmax, else softmax at T):
+   the n <= AARH_TOP_CANDIDATES largest probabilities, ties in ascending token order.
+   logits [rows][V], ids/probs [rows][n]: DEVICE pointers; stream as for aarh_accept_sample. */
+int aarh_top_candidates(aarh_ctx *ctx, const float *logits, int rows, int V, const aarh_sampler *sampler,
+                        int n, uint32_t *ids, float *probs, void *stream);
 
 /* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,

@@ -1298,15 +1298,41 @@ static float top2_gap(const float *v, int64_t n) {
     return a - b;
 }
 
-/* Sampler::top_candidates_from_probabilities (sampler.rs:188-208): output metadata only. */
-static void top_candidates(const float *p, int64_t n, int k) {
+/* Sampler::top_candidates_from_probabilities (sampler.rs:188-208): stable descending
+   sort of the distribution truncated to k (engine.rs:70: top_candidates = 5).  The
+   engines below compute it for every committed token (mtp_speculative.rs:247-250,
+   speculative.rs); when a sink is set (test harness, single-threaded) the k
+   candidates of committed token `slot` are stored there. */
+static uint32_t *g_cand_ids;
+static float *g_cand_probs;
+static int g_cand_cap;
+
+void ref_set_candidate_sink(uint32_t *ids, float *probs, int cap) {
+    g_cand_ids = ids;
+    g_cand_probs = probs;
+    g_cand_cap = ids && probs ? cap : 0;
+}
+
+void ref_top_candidates(const float *p, int64_t n, int k, uint32_t *ids, float *probs) {
     ranked_t *r = (ranked_t *)malloc(sizeof(ranked_t) * (size_t)n);
     for (int64_t i = 0; i < n; i++) r[i] = (ranked_t){p[i], i};
     qsort(r, (size_t)n, sizeof(ranked_t), cmp_ranked_desc);
-    volatile float sink = 0.0f;
-    for (int i = 0; i < k && i < n; i++) sink += r[i].v;
-    (void)sink;
+    for (int i = 0; i < k; i++) {
+        ids[i] = i < n ? (uint32_t)r[i].i : UINT32_MAX;
+        probs[i] = i < n ? r[i].v : 0.0f;
+    }
     free(r);
+}
+
+static void top_candidates(const float *p, int64_t n, int k, int slot) {
+    uint32_t ids[16];
+    float probs[16];
+    ref_top_candidates(p, n, k, ids, probs);
+    if (slot >= 0 && slot < g_cand_cap)
+        for (int i = 0; i < k; i++) {
+            g_cand_ids[(int64_t)slot * k + i] = ids[i];
+            g_cand_probs[(int64_t)slot * k + i] = probs[i];
+        }
 }
 
 /*
@@ -1400,7 +1426,7 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
             if ((st = ref_probabilities(s, tl, V, pt))) break;
             int acc = 0, drew = 0;
             ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, NULL, NULL, &drew);
-            top_candidates(pt, V, 5);
+            top_candidates(pt, V, 5, n_out);
             if (acc) {
                 stats->draft_tokens_accepted++;
                 if (props[i] == EOS_ID) {
@@ -1565,7 +1591,7 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
             if ((st = ref_probabilities(s, tl, V, pt))) break;
             int acc = 0, drew = 0;
             ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, NULL, NULL, &drew);
-            top_candidates(pt, V, 5);
+            top_candidates(pt, V, 5, n_out);
             if (acc) {
                 stats->draft_tokens_accepted++;
                 if (props[i] == EOS_ID) {
@@ -1620,7 +1646,7 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
             if (gp < min_gap) min_gap = gp;
         }
         if ((st = ref_probabilities(s, bl, V, pt))) break;
-        top_candidates(pt, V, 5);
+        top_candidates(pt, V, 5, n_out);
         uint32_t bonus;
         if ((st = ref_sample_probabilities(s, &rng, pt, V, &bonus, NULL, NULL))) break;
         if (bonus == EOS_ID) {

@@ -185,6 +185,11 @@ int ref_lat_forward(const ref_lat *m, ref_lat_kv *kv, const uint32_t *ids, int S
                     float *hidden, int nthreads);
 void ref_topk_gating(const float *logits, int rows, int E, int k, int32_t *idx, float *w);
 
+/* Sampler::top_candidates_from_probabilities (sampler.rs:188-208) and a sink that
+   records the 5 candidates of every token the engines commit ([cap][5]; NULL: off). */
+void ref_top_candidates(const float *p, int64_t n, int k, uint32_t *ids, float *probs);
+void ref_set_candidate_sink(uint32_t *ids, float *probs, int cap);
+
 #ifdef __cplusplus
 }
 #endif

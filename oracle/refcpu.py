@@ -135,6 +135,8 @@ def lib():
         "ref_spec_generate": (C.c_int, [C.c_void_p, C.c_void_p, U32P, C.c_int, C.c_int, C.c_int,
                                         C.POINTER(RefSampler), C.c_uint64, C.c_int, U32P, C.POINTER(C.c_int),
                                         C.POINTER(C.c_int), C.POINTER(RefSpecStats), C.POINTER(C.c_float)]),
+        "ref_top_candidates": (None, [F32P, C.c_int64, C.c_int, U32P, F32P]),
+        "ref_set_candidate_sink": (None, [C.c_void_p, C.c_void_p, C.c_int]),
         "ref_lat_create": (C.c_void_p, [C.POINTER(RefLatConfig)]),
         "ref_lat_free": (None, [C.c_void_p]),
         "ref_lat_num_tensors": (C.c_int, [C.c_void_p]),
@@ -326,6 +328,18 @@ def quantise_kv_row(x):
     return codes, int(sh[0])
 
 
+TOP_CANDIDATES = 5  # engine.rs:70
+
+
+def top_candidates(p, k=TOP_CANDIDATES):
+    """Sampler::top_candidates_from_probabilities (sampler.rs:188-208): (ids, probs)."""
+    p = np.ascontiguousarray(p, np.float32)
+    ids = np.zeros(k, np.uint32)
+    probs = np.zeros(k, np.float32)
+    lib().ref_top_candidates(p, p.size, k, ids, probs)
+    return ids, probs
+
+
 def synth_fill(seed, stream, n, std):
     out = np.zeros(n, np.float32)
     lib().ref_synth_fill(seed, stream, n, std, out)
@@ -395,13 +409,27 @@ class Model:
             raise ValueError(f"mtp_head failed: {st}")
         return out
 
+    def _sink(self, max_new):
+        """Record the top-5 candidates of every committed token of the next engine call
+        (Sampler::top_candidates_from_probabilities) in self.last_candidates."""
+        ids = np.zeros((max(max_new, 1), TOP_CANDIDATES), np.uint32)
+        probs = np.zeros((max(max_new, 1), TOP_CANDIDATES), np.float32)
+        lib().ref_set_candidate_sink(_ptr(ids), _ptr(probs), max(max_new, 1))
+        return ids, probs
+
+    def _unsink(self, ids, probs, n):
+        lib().ref_set_candidate_sink(None, None, 0)
+        self.last_candidates = (ids[:n].copy(), probs[:n].copy())
+
     def mtp_generate(self, prompt, max_new, num_draft, s, seed=0, nthreads=8):
         prompt = np.ascontiguousarray(prompt, np.uint32)
         out = np.zeros(max(max_new, 1), np.uint32)
         n, fin, gap = C.c_int(), C.c_int(), C.c_float()
         stats = RefSpecStats()
+        ci, cp = self._sink(max_new)
         st = lib().ref_mtp_generate(self.h, prompt, len(prompt), max_new, num_draft, C.byref(s), seed,
                                     nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
+        self._unsink(ci, cp, n.value)
         if st:
             raise ValueError(f"mtp_generate failed: {st}")
         return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value
@@ -413,8 +441,10 @@ class Model:
         out = np.zeros(max(max_new, 1), np.uint32)
         n, fin, gap = C.c_int(), C.c_int(), C.c_float()
         stats = RefSpecStats()
+        ci, cp = self._sink(max_new)
         st = lib().ref_spec_generate(self.h, draft.h, prompt, len(prompt), max_new, num_draft, C.byref(s), seed,
                                      nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
+        self._unsink(ci, cp, n.value)
         if st:
             raise ValueError(f"spec_generate failed: {st}")
         return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value

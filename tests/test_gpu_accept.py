@@ -164,3 +164,30 @@ def test_speculative_sampling_preserves_target_distribution(ctx):
     tok = np.where(acc == 1, props[:, 0], out["token"].cpu().numpy())
     freq = np.bincount(tok, minlength=3) / B
     assert np.max(np.abs(freq - target)) < 0.01
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_top_candidates_bit_exact(ctx, greedy):
+    """Sampler::top_candidates_from_probabilities (sampler.rs:188-208) of C2 target rows
+    (N(0, 3^2) logits, T = 0.8) and of rows with many exact ties: ids identical to the
+    oracle's and probabilities within 2 ulps (the device's exp is correctly rounded,
+    the host libm expf the oracle calls is within 1 ulp); greedy rows are exact."""
+    tgt, _, _ = c2_inputs(B=8, K=4, V=32000)
+    rows = tgt.reshape(-1, 32000)
+    tied = np.round(np.random.default_rng(5).normal(0, 1, (4, 32000)) * 2).astype(np.float32) / 2
+    rows = np.concatenate([rows, tied])
+    s_ref = R.sampler(greedy=True) if greedy else R.sampler(temperature=0.8)
+    s_dev = A.Sampler.greedy_sampler() if greedy else A.Sampler.top_k_top_p(0.8)
+    ids, probs = ctx.top_candidates(torch.from_numpy(rows).to(DEV), s_dev, 5)
+    ids, probs = ids.cpu().numpy().astype(np.uint32), probs.cpu().numpy()
+    for r in range(rows.shape[0]):
+        wi, wp = R.top_candidates(R.probabilities(s_ref, rows[r]), 5)
+        if greedy:
+            assert ids[r].tolist() == wi.tolist() and np.array_equal(probs[r], wp), r
+            continue
+        ulps = np.abs(probs[r].view(np.int32).astype(np.int64) - wp.view(np.int32).astype(np.int64))
+        assert ulps.max() <= 2, (r, ulps)
+        # an id swap is only possible between candidates the rounding cannot order
+        for k in range(5):
+            if ids[r][k] != wi[k]:
+                assert abs(int(wp[k].view(np.int32)) - int(probs[r][k].view(np.int32))) <= 2, (r, k)

@@ -49,6 +49,30 @@ def test_int4_batched_greedy_mtp_matches_oracle_per_sequence():
     hip.close()
 
 
+def test_mtp_session_top_candidates_match_oracle():
+    """Per committed token, the session records the top-5 candidates of the target
+    distribution at its position (mtp_speculative.rs:247-250): identical to the
+    oracle engine's, accepted, rejected-replacement and bonus-free rounds alike."""
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, max_seq_len=128,
+              num_future_tokens=3)
+    ref, hip = make_pair(seed=8, std=0.3, max_batch=2, max_rows=64, **kw)
+    prompts = R.synth_tokens(8, 2, 2 * 9, 1024).reshape(2, 9)
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(3))
+    sess = eng.session(prompts, 30, A.Sampler.greedy_sampler())
+    while not sess.step(4):
+        pass
+    outs = sess.result()
+    sess.close()
+    for b in range(2):
+        want, fin, stats, gap = ref.mtp_generate(prompts[b], 30, 3, R.sampler(greedy=True))
+        assert gap > 1e-5
+        assert outs[b].token_ids == list(want)
+        ci, cp = ref.last_candidates
+        assert [[i for i, _ in c] for c in outs[b].candidates] == ci.tolist()
+        assert [[p for _, p in c] for c in outs[b].candidates] == cp.tolist()
+    hip.close()
+
+
 def test_context_limit_and_engine_validation():
     kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=16,
               num_future_tokens=3)
@@ -106,6 +130,10 @@ def test_external_draft_greedy_matches_oracle(k):
         for key, v in stats.items():
             assert getattr(got, key) == v, (b, key, getattr(got, key), v)
         n_acc += stats["draft_tokens_accepted"]
+        # top candidates of every committed token (sampler.rs:188-208): one-hot at the token
+        ci, cp = ref_t.last_candidates
+        assert [[i for i, _ in c] for c in outs[b].candidates] == ci.tolist()
+        assert [[p for _, p in c] for c in outs[b].candidates] == cp.tolist()
     assert n_acc > 0  # acceptance, rejection and bonus paths all ran
     for m in (hip_t, hip_d):
         m.close()
