@@ -128,6 +128,7 @@ def lib():
                                          _P, _P, _P, C.POINTER(_Stats), _P, _P]),
         "aarh_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
         "aarh_top_candidates": (C.c_int, [_P, _P, C.c_int, C.c_int, C.POINTER(_Sampler), C.c_int, _P, _P, _P]),
+        "aarh_set_graphs": (C.c_int, [_P, C.c_int]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
@@ -163,7 +164,7 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
-            "aarh_session_candidates", "aarh_top_candidates",
+            "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -378,6 +379,10 @@ class HipModel:
 
     def stream(self):
         return lib().aarh_stream(self.h)
+
+    def set_graphs(self, on=True):
+        """Replay captured HIP graphs for repeated verify-forward shapes (default on)."""
+        self._check(lib().aarh_set_graphs(self.h, 1 if on else 0))
 
     def prof_enable(self, on=True):
         self._check(lib().aarh_prof_enable(self.h, 1 if on else 0))

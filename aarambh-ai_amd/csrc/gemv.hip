@@ -88,37 +88,6 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     const int elane = RS ? min(lr, 2 * MP - 1) : lr;  // fragment entry of this lane (lo: +16 at MP 16)
     const int glast = G - 1 - ((G - 1 - wid) % NW + NW) % NW;  // last real group of this wave (may be < 0)
 
-    // ---- 1/rms of each row from the producer's 16-column partial sums ----
-    if (tid < 2) {
-        cnt_s[tid] = 0u;
-        gen_s[tid] = 0u;
-    }
-    if (a.norm_w) {
-        for (int m = wid; m < Mc; m += NW) {
-            float ss = 0.f;
-            for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)(a.m_base + m) * a.ssq_ld + q];
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
-            if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-        }
-    }
-    __syncthreads();
-    if (EPI == EPI_STORE && a.hidden_out) {
-        // final normed hidden state (model.rs:579-585): workgroup b writes
-        // columns [b*cw, (b+1)*cw) of every row, 4 at a time
-        const int cw = ((a.K + (int)gridDim.x - 1) / (int)gridDim.x + 3) & ~3;
-        const int k0 = (int)blockIdx.x * cw, kn = min(cw, a.K - k0);
-        for (int idx = tid; idx < Mc * (kn >> 2); idx += NW * 64) {
-            const int m = idx / (kn >> 2), k = k0 + 4 * (idx - m * (kn >> 2));
-            const float4 v = *(const float4*)(a.x + row_off(a.xmap, a.m_base + m) + k);
-            const float4 w = *(const float4*)(a.norm_w + k);
-            const float si = s_inv[m];
-            *(float4*)(a.hidden_out + (size_t)(a.m_base + m) * a.K + k) =
-                make_float4(v.x * si * w.x, v.y * si * w.y, v.z * si * w.z, v.w * si * w.w);
-        }
-    }
-    if (nmine <= 0) return;
-
     const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
     const unsigned w_voff = (unsigned)lane * T::LANE_WORDS * 4u;
     const unsigned f_voff = (unsigned)(lg * EPB + elane) * 16u;
@@ -219,12 +188,49 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             }
         }
     };
+    // ---- the weight stream starts first: nothing below depends on it ----
+    if (nmine > 0) {
 #pragma unroll
-    for (int p = 0; p < PF; p++) load_item(p, 0, p);
-    if constexpr (REG) {
+        for (int p = 0; p < PF; p++) load_item(p, 0, p);
+        if constexpr (REG) {
 #pragma unroll
-        for (int gi = 0; gi < NGP; gi++) load_frag_reg(fa[gi], max(min(wid + NW * gi, glast), 0));
+            for (int gi = 0; gi < NGP; gi++) load_frag_reg(fa[gi], max(min(wid + NW * gi, glast), 0));
+        }
     }
+    // ---- 1/rms of each row from the producer's 16-column partial sums ----
+    if (tid < 2) {
+        cnt_s[tid] = 0u;
+        gen_s[tid] = 0u;
+    }
+    if (a.norm_w) {
+        for (int m = wid; m < Mc; m += NW) {
+            float ss = 0.f;
+            for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)(a.m_base + m) * a.ssq_ld + q];
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+            if (lane == 0) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+        }
+    }
+    // LDS-only barrier: the weight loads above stay in flight
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (EPI == EPI_STORE && a.hidden_out) {
+        // final normed hidden state (model.rs:579-585): workgroup b writes
+        // columns [b*cw, (b+1)*cw) of every row, 4 at a time
+        const int cw = ((a.K + (int)gridDim.x - 1) / (int)gridDim.x + 3) & ~3;
+        const int k0 = (int)blockIdx.x * cw, kn = min(cw, a.K - k0);
+        for (int idx = tid; idx < Mc * (kn >> 2); idx += NW * 64) {
+            const int m = idx / (kn >> 2), k = k0 + 4 * (idx - m * (kn >> 2));
+            const float4 v = *(const float4*)(a.x + row_off(a.xmap, a.m_base + m) + k);
+            const float4 w = *(const float4*)(a.norm_w + k);
+            const float si = s_inv[m];
+            *(float4*)(a.hidden_out + (size_t)(a.m_base + m) * a.K + k) =
+                make_float4(v.x * si * w.x, v.y * si * w.y, v.z * si * w.z, v.w * si * w.w);
+        }
+    }
+    if (nmine <= 0) return;
 
     for (int tl = 0; tl < nmine; tl++) {
         float4_t acc = {0.f, 0.f, 0.f, 0.f};

@@ -59,6 +59,18 @@ struct ProfRec {
     double bytes;
 };
 
+// A captured verify forward and the arguments its launches bake in.
+struct FwdGraph {
+    int nseq = 0, S = 0, kv_span = 0;
+    float* lout = nullptr;
+    RowMap lmap{};
+    float* hout = nullptr;
+    const uint32_t* ids = nullptr;
+    const int32_t *pos0 = nullptr, *slot = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t last_use = 0;
+};
+
 }  // namespace
 
 struct aarh_ctx {
@@ -107,6 +119,11 @@ struct aarh_ctx {
     int32_t* acc_argmax = nullptr;
     unsigned* acc_cnt = nullptr;
     int acc_rows_cap = 0, acc_seq_cap = 0;
+
+    // captured verify forwards
+    bool graphs = true;
+    std::vector<FwdGraph> gcache;
+    uint64_t gclock = 0;
 
     // profiling
     bool prof = false;
@@ -400,11 +417,11 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
 
 // forward_with_cache_output on device: ids/pos0/slot are device arrays for
 // nseq sequences x S tokens; logits go to `lout` via `lmap`, normed hidden to
-// `hout` ([M][H]) when non-null.  max_kv_len = max(pos0) + S.
-int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const int32_t* d_slot, int nseq, int S,
-                int max_kv_len, float* lout, RowMap lmap, float* hout) {
+// `hout` ([M][H]) when non-null.  kv_span bounds max(pos0) + S (it sets the
+// attention's chunking; chunks past a sequence's own length are empty).
+int forward_launches(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const int32_t* d_slot, int nseq,
+                     int S, int kv_span, float* lout, RowMap lmap, float* hout) {
     const int M = nseq * S, H = c->H;
-    if (M > c->Mmax) return fail(c, AARH_ERR_SHAPE, "rows %d exceed max_rows %d", M, c->Mmax);
     const int mp = frag_mp(M);
     {
         ProfScope ps(c, AARH_PROF_OTHER, 0);
@@ -417,11 +434,80 @@ int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const
                                 ? xfrag(c, c->frag_a, c->layers[l + 1].qkv.fmt, H, mp, c->layers[l + 1].norm1, true)
                                 : xfrag(c, c->frag_a, c->lm.fmt, H, mp, c->final_norm, true);
         int r = run_block(c, c->layers[l], nseq, S, d_pos0, d_slot, c->cfg.kv_format, c->cap, c->kc[l], c->vc[l],
-                          c->ksc[l], c->vsc[l], max_kv_len, after);
+                          c->ksc[l], c->vsc[l], kv_span, after);
         if (r) return r;
     }
     return gemv(c, c->lm, M, c->x, rm(M, 0, H), c->frag_a, mp, c->final_norm, hout, EPI_STORE, lout, lmap, nullptr,
                 0, XFrag{}, nullptr, AARH_PROF_GEMV_LMHEAD);
+}
+
+// The verify forward is about 5 launches per layer of 5-80 us kernels; host
+// launch cost is of the same order, so repeated shapes replay a captured HIP
+// graph (one host call).  Key: everything the launches bake in.  A shape is
+// captured the second time it is seen (the first run also initialises the
+// launchers' one-time attributes outside any capture).
+constexpr int GRAPH_KV_GRANULE = 256;  // kv_span rounding: one graph serves 256 cache positions
+constexpr size_t GRAPH_CACHE_MAX = 48;
+
+bool same_key(const FwdGraph& g, const FwdGraph& k) {
+    return g.nseq == k.nseq && g.S == k.S && g.kv_span == k.kv_span && g.lout == k.lout && g.hout == k.hout &&
+           g.lmap.S == k.lmap.S && g.lmap.seq_stride == k.lmap.seq_stride && g.lmap.row_stride == k.lmap.row_stride &&
+           g.ids == k.ids && g.pos0 == k.pos0 && g.slot == k.slot;
+}
+
+int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const int32_t* d_slot, int nseq, int S,
+                int max_kv_len, float* lout, RowMap lmap, float* hout) {
+    const int M = nseq * S;
+    if (M > c->Mmax) return fail(c, AARH_ERR_SHAPE, "rows %d exceed max_rows %d", M, c->Mmax);
+    const int kv_span = std::min(c->cap, (max_kv_len + GRAPH_KV_GRANULE - 1) / GRAPH_KV_GRANULE * GRAPH_KV_GRANULE);
+    if (!c->graphs || c->prof)
+        return forward_launches(c, d_ids, d_pos0, d_slot, nseq, S, kv_span, lout, lmap, hout);
+    FwdGraph key{};
+    key.nseq = nseq;
+    key.S = S;
+    key.kv_span = kv_span;
+    key.lout = lout;
+    key.lmap = lmap;
+    key.hout = hout;
+    key.ids = d_ids;
+    key.pos0 = d_pos0;
+    key.slot = d_slot;
+    for (auto& g : c->gcache) {
+        if (!same_key(g, key)) continue;
+        g.last_use = ++c->gclock;
+        if (g.exec) {
+            HIPCHK(c, hipGraphLaunch(g.exec, c->stream));
+            return 0;
+        }
+        // second sighting: capture this shape's launches once, then replay
+        hipGraph_t graph = nullptr;
+        HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        int r = forward_launches(c, d_ids, d_pos0, d_slot, nseq, S, kv_span, lout, lmap, hout);
+        hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        if (r) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return r;
+        }
+        if (e != hipSuccess) return fail(c, AARH_ERR_DEVICE, "graph capture failed: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) {
+            g.exec = nullptr;
+            return fail(c, AARH_ERR_DEVICE, "graph instantiation failed: %s", hipGetErrorString(e));
+        }
+        HIPCHK(c, hipGraphLaunch(g.exec, c->stream));
+        return 0;
+    }
+    // first sighting: run directly and remember the shape (evicting the least recently used)
+    if (c->gcache.size() >= GRAPH_CACHE_MAX) {
+        auto lru = std::min_element(c->gcache.begin(), c->gcache.end(),
+                                    [](const FwdGraph& a, const FwdGraph& b) { return a.last_use < b.last_use; });
+        if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+        c->gcache.erase(lru);
+    }
+    key.last_use = ++c->gclock;
+    c->gcache.push_back(key);
+    return forward_launches(c, d_ids, d_pos0, d_slot, nseq, S, kv_span, lout, lmap, hout);
 }
 
 // forward_mtp_head on device for nseq sequences: anchor rows (stride), ids
@@ -476,6 +562,8 @@ void aarh_destroy(aarh_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto& g : c->gcache)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
     auto F = [](void* p) {
         if (p) (void)hipFree(p);
     };
@@ -1119,6 +1207,16 @@ int aarh_top_candidates(aarh_ctx* c, const float* logits, int rows, int V, const
     return 0;
 }
 
+int aarh_set_graphs(aarh_ctx* c, int enable) {
+    if (!c) return AARH_ERR_CONFIG;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->graphs = enable != 0;
+    for (auto& g : c->gcache)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    c->gcache.clear();
+    return 0;
+}
+
 int aarh_prof_enable(aarh_ctx* c, int enable) {
     if (!c) return AARH_ERR_CONFIG;
     c->prof = enable != 0;
@@ -1402,18 +1500,22 @@ int session_round(aarh_session* e) {
             continue;
         }
         if (acc < np) {
+            // target_cache.restore(snapshot) + forward(proposals[..acc] + replacement): the verify
+            // forward already holds the accepted prefix's K / V (same tokens, same positions, same
+            // prefix), so the cache keeps them and only the replacement is forwarded
             const uint32_t repl = (uint32_t)e->htok[b];
-            c->kv_len[b] = e->base[b];  // target_cache.restore(snapshot)
+            c->kv_len[b] = e->base[b] + acc;
             if (repl == EOS_ID) {
                 e->finish[b] = AARH_FINISH_EOS;
                 e->finished[b] = 1;
+                c->kv_len[b] = e->base[b];
                 continue;
             }
             e->out[b].push_back(repl);
             e->cand.commit(b, b * (K + 1) + acc);
-            e->hprops[(size_t)b * K + acc] = repl;  // replay ids = proposals[..i] + replacement
             replay_seq.push_back(b);
-            replay_len.push_back(acc + 1);
+            replay_len.push_back(acc);  // position of the replacement relative to base
+            e->hprops[(size_t)b * K + acc] = repl;
         } else {
             // everything accepted: target_next / anchor from the last verify row
             c->kv_len[b] = e->base[b] + np;
@@ -1426,31 +1528,29 @@ int session_round(aarh_session* e) {
     // rows that come from the verify buffers must be copied before the replay reuses scratch
     if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hs, hdv, H))) return r;
     if (!replay_seq.empty()) {
+        // one row per rejected sequence: the replacement at base + acc
         const int nr = (int)replay_seq.size();
-        int Sr = 0;
-        for (int L : replay_len) Sr = std::max(Sr, L);
-        std::vector<uint32_t> ids((size_t)nr * Sr);
+        std::vector<uint32_t> ids(nr);
         std::vector<int32_t> sl(nr), off(nr);
         for (int j = 0; j < nr; j++) {
             const int b = replay_seq[j];
             sl[j] = b;
-            off[j] = e->base[b];
-            for (int s2 = 0; s2 < Sr; s2++)
-                ids[(size_t)j * Sr + s2] = e->hprops[(size_t)b * K + std::min(s2, replay_len[j] - 1)];
+            off[j] = e->base[b] + replay_len[j];
+            ids[j] = e->hprops[(size_t)b * K + replay_len[j]];
         }
         int mk = 0;
-        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, Sr, &mk, PAD_SLACK))) return r;
-        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, Sr, mk, c->logits, rm(nr * Sr, 0, V), c->hidden)))
+        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, 1, &mk, PAD_SLACK))) return r;
+        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, 1, mk, c->logits, rm(nr, 0, V), c->hidden)))
             return r;
         std::vector<const float*> rs, rhs;
         std::vector<float*> rd, rhd;
         for (int j = 0; j < nr; j++) {
             const int b = replay_seq[j];
             e->stats[b].target_decode_forwards++;
-            c->kv_len[b] = e->base[b] + replay_len[j];
-            rs.push_back(c->logits + ((size_t)j * Sr + replay_len[j] - 1) * V);
+            c->kv_len[b] = off[j] + 1;
+            rs.push_back(c->logits + (size_t)j * V);
             rd.push_back(e->tgt + (size_t)b * (K + 1) * V);
-            rhs.push_back(c->hidden + ((size_t)j * Sr + replay_len[j] - 1) * H);
+            rhs.push_back(c->hidden + (size_t)j * H);
             rhd.push_back(e->anchor + (size_t)b * H);
         }
         if ((r = copy_rows_host_lists(e, rs, rd, V)) || (r = copy_rows_host_lists(e, rhs, rhd, H))) return r;

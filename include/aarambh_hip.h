@@ -183,6 +183,10 @@ int aarh_spec_generate(aarh_ctx *target, aarh_ctx *draft, const uint32_t *prompt
 int aarh_top_candidates(aarh_ctx *ctx, const float *logits, int rows, int V, const aarh_sampler *sampler,
                         int n, uint32_t *ids, float *probs, void *stream);
 
+/* --- launch mode: repeated verify-forward shapes replay a captured HIP graph (default on;
+   0 launches every kernel from the host each call).  Results are identical either way. --- */
+int aarh_set_graphs(aarh_ctx *ctx, int enable);
+
 /* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
        AARH_PROF_GEMV_DOWN = 3, AARH_PROF_GEMV_LMHEAD = 4, AARH_PROF_ATTENTION = 5,
