@@ -44,8 +44,8 @@ __device__ void append_new_kv(const AttnArgs& a, int seq, int kvh, size_t hb, in
             const float* src = a.knew + row * 2 * KD + (size_t)which * KD + (size_t)kvh * hd;
             const float v0 = lane < hd ? src[lane] : 0.f;
             const float v1 = lane + 64 < hd ? src[lane + 64] : 0.f;
-            const size_t kbase = (hb * a.cap + t) * hd;          // K [..][cap][hd]
-            const size_t vbase = hb * hd * a.cap + t;            // V^T [..][hd][cap]
+            auto kdst = [&](int d) { return k_off(hb, t, d, a.cap, hd, a.kv_fmt); };
+            auto vdst = [&](int d) { return vt_off(hb, d, t, a.cap, hd, a.kv_fmt); };  // V^T
             if (a.kv_fmt == KV_INT8) {
                 const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
                 const float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
@@ -53,28 +53,24 @@ __device__ void append_new_kv(const AttnArgs& a, int seq, int kvh, size_t hb, in
                 const int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
                 const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
                 if (which == 0) {
-                    int8_t* kc = (int8_t*)a.kc + kbase;
-                    if (lane < hd) kc[lane] = q0;
-                    if (lane + 64 < hd) kc[lane + 64] = q1;
+                    int8_t* kc = (int8_t*)a.kc;
+                    if (lane < hd) kc[kdst(lane)] = q0;
+                    if (lane + 64 < hd) kc[kdst(lane + 64)] = q1;
                     if (lane == 0) ((uint16_t*)a.ks)[hb * a.cap + t] = sh;
                 } else {
-                    int8_t* vc = (int8_t*)a.vc + vbase;
-                    if (lane < hd) vc[(size_t)lane * a.cap] = q0;
-                    if (lane + 64 < hd) vc[(size_t)(lane + 64) * a.cap] = q1;
+                    int8_t* vc = (int8_t*)a.vc;
+                    if (lane < hd) vc[vdst(lane)] = q0;
+                    if (lane + 64 < hd) vc[vdst(lane + 64)] = q1;
                     if (lane == 0) ((uint16_t*)a.vs)[hb * a.cap + t] = sh;
                 }
             } else if (a.kv_fmt == KV_F16) {
                 _Float16* dst = (_Float16*)(which == 0 ? a.kc : a.vc);
-                const size_t st = which == 0 ? 1 : (size_t)a.cap;
-                const size_t base = which == 0 ? kbase : vbase;
-                if (lane < hd) dst[base + lane * st] = (_Float16)v0;
-                if (lane + 64 < hd) dst[base + (lane + 64) * st] = (_Float16)v1;
+                if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = (_Float16)v0;
+                if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = (_Float16)v1;
             } else {
                 float* dst = (float*)(which == 0 ? a.kc : a.vc);
-                const size_t st = which == 0 ? 1 : (size_t)a.cap;
-                const size_t base = which == 0 ? kbase : vbase;
-                if (lane < hd) dst[base + lane * st] = v0;
-                if (lane + 64 < hd) dst[base + (lane + 64) * st] = v1;
+                if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = v0;
+                if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = v1;
             }
         }
     }
@@ -140,14 +136,14 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
             if (a.kv_fmt == KV_INT8) {
                 float ksc = (float)__builtin_bit_cast(_Float16, a.ks[head_base * a.cap + tt]);
                 float vsc = (float)__builtin_bit_cast(_Float16, a.vs[head_base * a.cap + tt]);
-                kv_ = (float)((const int8_t*)a.kc)[(head_base * a.cap + tt) * hd + d] * ksc;
-                vv_ = (float)((const int8_t*)a.vc)[(head_base * hd + d) * a.cap + tt] * vsc;
+                kv_ = (float)((const int8_t*)a.kc)[k_off(head_base, tt, d, a.cap, hd, KV_INT8)] * ksc;
+                vv_ = (float)((const int8_t*)a.vc)[vt_off(head_base, d, tt, a.cap, hd, KV_INT8)] * vsc;
             } else if (a.kv_fmt == KV_F16) {
-                kv_ = (float)((const _Float16*)a.kc)[(head_base * a.cap + tt) * hd + d];
-                vv_ = (float)((const _Float16*)a.vc)[(head_base * hd + d) * a.cap + tt];
+                kv_ = (float)((const _Float16*)a.kc)[k_off(head_base, tt, d, a.cap, hd, KV_F16)];
+                vv_ = (float)((const _Float16*)a.vc)[vt_off(head_base, d, tt, a.cap, hd, KV_F16)];
             } else {
-                kv_ = ((const float*)a.kc)[(head_base * a.cap + tt) * hd + d];
-                vv_ = ((const float*)a.vc)[(head_base * hd + d) * a.cap + tt];
+                kv_ = ((const float*)a.kc)[k_off(head_base, tt, d, a.cap, hd, KV_F32)];
+                vv_ = ((const float*)a.vc)[vt_off(head_base, d, tt, a.cap, hd, KV_F32)];
             }
             ks[t][d] = kv_;
             vs[t][d] = vv_;
@@ -293,52 +289,56 @@ static constexpr float AM_LOG2E = 1.4426950408889634f;
 // Raw K/V operands of one 32-token block for one lane (lane = (lr, lg)).
 // K: token rows 8*(lr/4) + 4*ts + lr%4 of the block, dims 32*lg..+32.
 // V^T: dim rows 16*dt + lr, tokens 8*lg..+8.  Scales: tokens 8*lg..+8.
+// Vector-register types (not HIP's struct uint4) so a block stays in VGPRs.
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4v_t __attribute__((ext_vector_type(4)));
 template <int KVF>
 struct KvRaw;
 template <>
 struct KvRaw<KV_INT8> {
-    uint4 k[2][2];
-    uint2 v[8];
-    uint4 ksc, vsc;
+    u32x4v_t k[2][2];
+    u32x4v_t ksc;
+    u32x2_t v[8];
+    u32x4v_t vsc;
 };
 template <>
 struct KvRaw<KV_F16> {
-    uint4 k[2][4];
-    uint4 v[8];
+    u32x4v_t k[2][4];
+    u32x4v_t v[8];
 };
 
+// Loads are issued in the order they are consumed (K, K scales, V, V scales),
+// so the scores of a block wait only for its K half.
 template <int KVF>
 __device__ __forceinline__ void load_kv_block(const AttnArgs& a, size_t hb, int tb, int lr, int lg, KvRaw<KVF>& r) {
+    // K: chunk (ts, c) of every lane is one contiguous 1 KiB run of the block (k_off)
+    const int lane = 16 * lg + lr;
+    const uint8_t* kb = (const uint8_t*)a.kc + (hb * a.cap + tb) * AM_HD * (KVF == KV_INT8 ? 1 : 2);
 #pragma unroll
     for (int ts = 0; ts < 2; ts++) {
-        const int tok = tb + 8 * (lr >> 2) + 4 * ts + (lr & 3);
         if constexpr (KVF == KV_INT8) {
-            const uint4* kr = (const uint4*)((const uint8_t*)a.kc + (hb * a.cap + tok) * AM_HD + 32 * lg);
-            r.k[ts][0] = kr[0];
-            r.k[ts][1] = kr[1];
-        } else {
-            const uint4* kr = (const uint4*)((const _Float16*)a.kc + (hb * a.cap + tok) * AM_HD + 32 * lg);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) r.k[ts][kk] = kr[kk];
+            for (int c = 0; c < 2; c++) r.k[ts][c] = *(const u32x4v_t*)(kb + ((ts * 2 + c) * 64 + lane) * 16);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) r.k[ts][c] = *(const u32x4v_t*)(kb + ((ts * 4 + c) * 64 + lane) * 16);
         }
     }
+    if constexpr (KVF == KV_INT8) r.ksc = *(const u32x4v_t*)(a.ks + hb * a.cap + tb + 8 * lg);
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) {
         if constexpr (KVF == KV_INT8)
-            r.v[dt] = *(const uint2*)((const uint8_t*)a.vc + (hb * AM_HD + 16 * dt + lr) * a.cap + tb + 8 * lg);
+            r.v[dt] = *(const u32x2_t*)((const uint8_t*)a.vc + vt_off(hb, 16 * dt + lr, tb + 8 * lg, a.cap, AM_HD, KV_INT8));
         else
-            r.v[dt] = *(const uint4*)((const _Float16*)a.vc + (hb * AM_HD + 16 * dt + lr) * a.cap + tb + 8 * lg);
+            r.v[dt] = *(const u32x4v_t*)((const _Float16*)a.vc + vt_off(hb, 16 * dt + lr, tb + 8 * lg, a.cap, AM_HD, KV_F16));
     }
-    if constexpr (KVF == KV_INT8) {
-        r.ksc = *(const uint4*)(a.ks + hb * a.cap + tb + 8 * lg);
-        r.vsc = *(const uint4*)(a.vs + hb * a.cap + tb + 8 * lg);
-    }
+    if constexpr (KVF == KV_INT8) r.vsc = *(const u32x4v_t*)(a.vs + hb * a.cap + tb + 8 * lg);
 }
 
 template <int KVF>
 __device__ __forceinline__ half8_t k_operand(const KvRaw<KVF>& r, int ts, int kk) {
     if constexpr (KVF == KV_INT8) {
-        const uint4 w = r.k[ts][kk >> 1];
+        const u32x4v_t w = r.k[ts][kk >> 1];
         return (kk & 1) ? i8x8_to_half8_perm(w.z, w.w) : i8x8_to_half8_perm(w.x, w.y);
     } else {
         return __builtin_bit_cast(half8_t, r.k[ts][kk]);
@@ -350,7 +350,7 @@ __device__ __forceinline__ half8_t v_operand(const KvRaw<KVF>& r, int dt) {
     else return __builtin_bit_cast(half8_t, r.v[dt]);
 }
 // fp16 scale of token 8*lg + idx (idx = 4*ts + i)
-__device__ __forceinline__ float scale_at(uint4 s, int idx) {
+__device__ __forceinline__ float scale_at(u32x4v_t s, int idx) {
     const uint32_t w = idx < 2 ? s.x : idx < 4 ? s.y : idx < 6 ? s.z : s.w;
     return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (w >> 16) : (w & 0xFFFFu)));
 }
@@ -386,7 +386,7 @@ __device__ __forceinline__ float rows_sum(float x) {
 // the lane of their row.  Softmax runs in base 2 (v_exp_f32).  With one chunk
 // the workgroup writes the output; otherwise chunk partials go out with
 // coherent 16-byte stores and the last workgroup of the group merges them.
-template <int KVF>
+template <int KVF, int DEPTH>
 __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     __shared__ __align__(16) float mg_o[AM_WAVES][AM_ROWS][AM_REC];
     __shared__ float mg_m[AM_WAVES][AM_ROWS], mg_l[AM_WAVES][AM_ROWS];
@@ -427,9 +427,21 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; u++) qv[u] = row_ok ? *(const float4_t*)(qp + 4 * u) : (float4_t){0.f, 0.f, 0.f, 0.f};
 
+    // Block ring of DEPTH + 1 register buffers, rotated by unrolling (no copies:
+    // a register copy of a block still in flight would wait for every load).
+    // Loads past the wave's last block re-read the chunk's last block (in
+    // bounds, results unused), so inside a non-empty chunk every load is
+    // unconditional; an empty chunk (past the sequence's length) loads nothing.
+    constexpr int STEP = 32 * AM_WAVES;
     int tb = t_begin + 32 * wid;
-    KvRaw<KVF> cur;
-    if (tb < t_end) load_kv_block<KVF>(a, hb, tb, lr, lg, cur);
+    const int t_chunk_last = (t_end - 1) & ~31;
+    // the wave's own last block (re-reads hit L1), or the chunk's last one for a wave without blocks
+    const int t_last = tb <= t_chunk_last ? tb + (t_chunk_last - tb) / STEP * STEP : t_chunk_last;
+    KvRaw<KVF> ring[DEPTH + 1];
+    if (t_end > t_begin) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) load_kv_block<KVF>(a, hb, min(tb + d * STEP, t_last), lr, lg, ring[d]);
+    }
 
     half8_t qh[4], ql[4];
 #pragma unroll
@@ -449,9 +461,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     for (int dt = 0; dt < 8; dt++) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
     const float sc2 = a.scale * AM_LOG2E;
 
-    for (; tb < t_end; tb += 32 * AM_WAVES) {
-        KvRaw<KVF> nxt;
-        if (tb + 32 * AM_WAVES < t_end) load_kv_block<KVF>(a, hb, tb + 32 * AM_WAVES, lr, lg, nxt);
+    auto block = [&](const KvRaw<KVF>& cur) __attribute__((always_inline)) {
         // ---- S^T = K Q^T: lane holds tokens 8*lg + 4*ts + i of row lr ----
         float4_t st[2];
 #pragma unroll
@@ -508,7 +518,16 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
         }
-        cur = nxt;
+    };
+    for (; tb < t_end;) {
+#pragma unroll
+        for (int d = 0; d <= DEPTH; d++) {
+            if (tb >= t_end) break;
+            load_kv_block<KVF>(a, hb, min(tb + DEPTH * STEP, t_last), lr, lg, ring[(d + DEPTH) % (DEPTH + 1)]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the block's math
+            block(ring[d]);
+            tb += STEP;
+        }
     }
     // ---- merge the waves in LDS: lane holds O^T[16*dt + 4*lg + i][lr] ----
 #pragma unroll
@@ -599,9 +618,9 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
     if ((a.kv_fmt == KV_INT8 || a.kv_fmt == KV_F16) && a.hd == AM_HD) {
         if (a.rows_per_tile > AM_ROWS || a.chunk % (32 * AM_WAVES) || a.nchunks > AM_MAXCH || a.cap % 32) return 3;
         if (a.kv_fmt == KV_INT8)
-            hipLaunchKernelGGL(attn_mfma_kernel<KV_INT8>, dim3(grid), dim3(512), 0, stream, a);
+            hipLaunchKernelGGL((attn_mfma_kernel<KV_INT8, 1>), dim3(grid), dim3(512), 0, stream, a);
         else
-            hipLaunchKernelGGL(attn_mfma_kernel<KV_F16>, dim3(grid), dim3(512), 0, stream, a);
+            hipLaunchKernelGGL((attn_mfma_kernel<KV_F16, 1>), dim3(grid), dim3(512), 0, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
     if (a.hd > AT_MAXHD || a.rows_per_tile > AT_MAXR || a.rows_per_tile <= 0) return 3;

@@ -7,6 +7,28 @@ namespace aarh {
 
 enum WFmt { WF_F32 = 0, WF_BF16 = 1, WF_INT8 = 2, WF_INT4 = 3 };
 enum KvFmt { KV_F32 = 0, KV_F16 = 1, KV_INT8 = 2 };
+
+// Element offset of V (dim d, token t) in the cache of head hb (= slot * n_kv + kv head).
+// INT8 / fp16 caches keep V^T in 32-token blocks, [head][cap/32][hd][32]: the 32 tokens x
+// hd dims a decode wave reads per step are one contiguous run (cap is a multiple of 32).
+// f32 caches (MTP head scratch) keep [head][hd][cap].
+__host__ __device__ inline size_t vt_off(size_t hb, int d, int t, int cap, int hd, int kv_fmt) {
+    if (kv_fmt == KV_F32) return (hb * hd + d) * (size_t)cap + t;
+    return ((hb * (size_t)(cap >> 5) + (t >> 5)) * hd + d) * 32 + (t & 31);
+}
+
+// Element offset of K (token t, dim d) in the cache of head hb.  INT8 / fp16 caches with
+// head_dim 128 store each 32-token block (32 x 128 elements, contiguous) in the order the
+// decode wave loads it: 16-byte chunk (ts, c) of lane (lg, lr) holds token row
+// 8 (lr / 4) + 4 ts + lr % 4, dims 32 lg + c * (16 / esize) ..; one load instruction then
+// reads 1 KiB contiguous.  Other caches are row-major [head][cap][hd].
+__host__ __device__ inline size_t k_off(size_t hb, int t, int d, int cap, int hd, int kv_fmt) {
+    if (kv_fmt == KV_F32 || hd != 128) return (hb * cap + t) * (size_t)hd + d;
+    const int r = t & 31, ts = (r >> 2) & 1, lr = ((r >> 3) << 2) | (r & 3), lane = ((d >> 5) << 4) | lr;
+    const int per = kv_fmt == KV_INT8 ? 16 : 8, nc = 32 / per;  // elements per chunk, chunks per lane row
+    const int c = (d & 31) / per, j = d & (per - 1);
+    return (hb * cap + (t & ~31)) * 128 + ((size_t)(ts * nc + c) * 64 + lane) * per + j;
+}
 enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 enum { ACCEPT_FLAG_RATIO_NEAR = 1u, ACCEPT_FLAG_CDF_NEAR = 2u };

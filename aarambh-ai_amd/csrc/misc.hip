@@ -334,25 +334,25 @@ __global__ void kv_fill_kernel(void* kc, void* vc, uint16_t* ks, uint16_t* vs, i
         int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.f), 127.f);
         uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
         if (which == 0) {
-            int8_t* dst = (int8_t*)kc + (hb * cap + t) * hd;
-            if (lane < hd) dst[lane] = q0;
-            if (lane + 64 < hd) dst[lane + 64] = q1;
+            int8_t* dst = (int8_t*)kc;
+            if (lane < hd) dst[k_off(hb, t, lane, cap, hd, KV_INT8)] = q0;
+            if (lane + 64 < hd) dst[k_off(hb, t, lane + 64, cap, hd, KV_INT8)] = q1;
             if (lane == 0) ks[hb * cap + t] = sh;
         } else {
-            int8_t* dst = (int8_t*)vc + hb * hd * cap + t;
-            if (lane < hd) dst[(size_t)lane * cap] = q0;
-            if (lane + 64 < hd) dst[(size_t)(lane + 64) * cap] = q1;
+            int8_t* dst = (int8_t*)vc;
+            if (lane < hd) dst[vt_off(hb, lane, t, cap, hd, KV_INT8)] = q0;
+            if (lane + 64 < hd) dst[vt_off(hb, lane + 64, t, cap, hd, KV_INT8)] = q1;
             if (lane == 0) vs[hb * cap + t] = sh;
         }
     } else if (kv_fmt == KV_F16) {
         if (which == 0) {
-            _Float16* dst = (_Float16*)kc + (hb * cap + t) * hd;
-            if (lane < hd) dst[lane] = (_Float16)v0;
-            if (lane + 64 < hd) dst[lane + 64] = (_Float16)v1;
+            _Float16* dst = (_Float16*)kc;
+            if (lane < hd) dst[k_off(hb, t, lane, cap, hd, KV_F16)] = (_Float16)v0;
+            if (lane + 64 < hd) dst[k_off(hb, t, lane + 64, cap, hd, KV_F16)] = (_Float16)v1;
         } else {
-            _Float16* dst = (_Float16*)vc + hb * hd * cap + t;
-            if (lane < hd) dst[(size_t)lane * cap] = (_Float16)v0;
-            if (lane + 64 < hd) dst[(size_t)(lane + 64) * cap] = (_Float16)v1;
+            _Float16* dst = (_Float16*)vc;
+            if (lane < hd) dst[vt_off(hb, lane, t, cap, hd, KV_F16)] = (_Float16)v0;
+            if (lane + 64 < hd) dst[vt_off(hb, lane + 64, t, cap, hd, KV_F16)] = (_Float16)v1;
         }
     } else {
         if (which == 0) {
