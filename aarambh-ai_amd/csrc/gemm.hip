@@ -137,7 +137,6 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         }
         __syncthreads();
     };
-
     if (EPI == EPI_STORE && a.hidden_out) {
         // final normed hidden state (model.rs:579-585): the NB * S blocks of this
         // M-block each write a slice of columns of its rows
@@ -287,6 +286,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         __syncthreads();
     }
     wait_vmcnt<0>();
+    __syncthreads();  // every wave's stage loads have landed: the ring is free for the epilogue
 
     if (S > 1) {
         // ---- split-K: partial tiles out, the last block of the (mb, nb) pair adds them in order ----
@@ -351,17 +351,6 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     if (FMT == WF_INT8)
 #pragma unroll
         for (int j = 0; j < TPW; j++) rs[j] = a.rscale[ntv[j] * 16 + lr];
-    float xo[CPW][TPW][4], nw[TPW];
-    if (EPI == EPI_RESID) {
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-#pragma unroll
-            for (int j = 0; j < TPW; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) xo[c][j][i] = a.resid[(size_t)mrw[c][i] * a.ldr + ntv[j] * 16 + lr];
-#pragma unroll
-        for (int j = 0; j < TPW; j++) nw[j] = a.fo.norm_w ? a.fo.norm_w[ntv[j] * 16 + lr] : 1.0f;
-    }
     int pos[CPW][4];
     if (EPI == EPI_QKV)
 #pragma unroll
@@ -381,63 +370,22 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                 acc[c][j][i] = v;
             }
 
-    if (EPI == EPI_STORE) {
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-#pragma unroll
-            for (int j = 0; j < TPW; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (rok[c][i] && tok[j]) a.out[row_off(a.omap, mrw[c][i]) + ntv[j] * 16 + lr] = acc[c][j][i];
-    } else if (EPI == EPI_RESID) {
-        // x += y; the new x as fragments for the next consumer and its 16-column sums of squares
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-#pragma unroll
-            for (int j = 0; j < TPW; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float xn = xo[c][j][i] + acc[c][j][i];
-                    const int m = mrw[c][i], col = ntv[j] * 16 + lr;
-                    if (rok[c][i] && tok[j]) {
-                        a.resid[(size_t)m * a.ldr + col] = xn;
-                        if (a.fo.buf) frag_put_w(a.fo, m, col, xn * nw[j]);
-                    }
-                    float sq = xn * xn;
-#pragma unroll
-                    for (int d = 8; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
-                    if (a.fo.ssq && lr == 0 && rok[c][i] && tok[j]) a.fo.ssq[(size_t)m * a.fo.ssq_ld + ntv[j]] = sq;
-                }
-    } else if (EPI == EPI_SWIGLU) {
-        // rows 0-7 of a tile are gate rows, 8-15 the matching up rows (ffn columns nt*8 + r)
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-#pragma unroll
-            for (int j = 0; j < TPW; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float u = __shfl_xor(acc[c][j][i], 8, 64);
-                    if (lr < 8 && rok[c][i] && tok[j]) {
-                        const float g = acc[c][j][i];
-                        const float silu = g / (1.0f + expf(-g));
-                        const float h = silu * u;
-                        const int m = mrw[c][i], col = ntv[j] * 8 + lr;
-                        a.out[row_off(a.omap, m) + col] = h;
-                        if (a.fo.buf) frag_put(a.fo, m, col, h);
-                    }
-                }
-    } else {
-        // QKV: a tile holds dims d = 8 jh + r (weight rows r < 8) and d + hd/2 (rows 8 + r) of one head
+    // ---- the wave's tile goes through LDS (the stage ring is idle now) so that
+    //      every global access is a 16-byte run of 4 (f32) or 8 (fragment)
+    //      consecutive columns of one row ----
+    constexpr int TR = 16 * CPW, TLD = 16 * TPW + 4;
+    float* wt = (float*)lds + wid * TR * TLD;
+    if (EPI == EPI_QKV) {
+        // a tile holds dims d = 8 jh + r (weight rows r < 8) and d + hd/2 (rows 8 + r) of one
+        // head; RoPE (rope.rs:107-126) pairs lane lr with lane lr ^ 8, each keeps its own output
         const QkvEpi& e = a.qkv;
         const int hd = e.hd, half = hd >> 1;
         const int QD = e.n_heads * hd, KD = e.n_kv * hd;
-        const int r = lr & 7;
 #pragma unroll
         for (int j = 0; j < TPW; j++) {
-            const int row0 = ntv[j] * 16;
-            const int head = row0 / hd, jh = (row0 % hd) >> 4;
-            const bool is_q = row0 < QD, is_k = !is_q && row0 < QD + KD;
-            const int d1 = 8 * jh + r;
+            const int rowq = ntv[j] * 16;
+            const bool rot = rowq < QD + KD;
+            const int d1 = 8 * ((rowq % hd) >> 4) + (lr & 7);
 #pragma unroll
             for (int c = 0; c < CPW; c++) {
                 float cs[4], sn[4];
@@ -450,22 +398,146 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                 for (int i = 0; i < 4; i++) {
                     const float mine = acc[c][j][i], other = __shfl_xor(mine, 8, 64);
                     float y1 = lr < 8 ? mine : other, y2 = lr < 8 ? other : mine;
-                    if (is_q || is_k) {
-                        // RoPE (rope.rs:107-126): half-split rotation at the row's position
+                    if (rot) {
 #pragma clang fp contract(off)
                         const float r1 = y1 * cs[i] - y2 * sn[i];
                         const float r2 = y1 * sn[i] + y2 * cs[i];
                         y1 = r1;
                         y2 = r2;
                     }
-                    const int mg = mrw[c][i];
-                    float* dst;
-                    if (is_q) dst = e.q_out + (size_t)mg * QD + head * hd;
-                    else if (is_k) dst = e.kv_out + (size_t)mg * 2 * KD + (head - e.n_heads) * hd;
-                    else dst = e.kv_out + (size_t)mg * 2 * KD + KD + (head - e.n_heads - e.n_kv) * hd;
-                    if (rok[c][i] && tok[j]) {
-                        if (lr < 8) dst[d1] = y1;
-                        else dst[d1 + half] = y2;
+                    wt[(16 * c + 4 * lg + i) * TLD + 16 * j + lr] = lr < 8 ? y1 : y2;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int j = 0; j < TPW; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) wt[(16 * c + 4 * lg + i) * TLD + 16 * j + lr] = acc[c][j][i];
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    {
+        const int row0 = (mb * MC + wm * CPW) * 16, tile0 = nb * NT + wn * TPW;
+        if (EPI == EPI_SWIGLU) {
+            // unit (row, tile): gate rows 0-7 and up rows 8-15 of the tile give h columns nt*8 .. +7
+            for (int u = lane; u < TR * TPW; u += 64) {
+                const int r = u / TPW, j = u % TPW, m = row0 + r, nt = tile0 + j;
+                if (m >= a.M || nt >= ntiles) continue;
+                const float4_t g0 = *(const float4_t*)(wt + r * TLD + 16 * j), g1 = *(const float4_t*)(wt + r * TLD + 16 * j + 4);
+                const float4_t u0 = *(const float4_t*)(wt + r * TLD + 16 * j + 8), u1 = *(const float4_t*)(wt + r * TLD + 16 * j + 12);
+                float h[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    h[e] = g0[e] / (1.0f + expf(-g0[e])) * u0[e];
+                    h[4 + e] = g1[e] / (1.0f + expf(-g1[e])) * u1[e];
+                }
+                float* dst = a.out + row_off(a.omap, m) + nt * 8;
+                if (((uintptr_t)dst & 15) == 0) {
+                    *(float4_t*)dst = (float4_t){h[0], h[1], h[2], h[3]};
+                    *(float4_t*)(dst + 4) = (float4_t){h[4], h[5], h[6], h[7]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) dst[e] = h[e];
+                }
+                if (a.fo.buf) {
+                    if (a.fo.norm_w)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) h[e] *= a.fo.norm_w[nt * 8 + e];
+                    frag_put8_w(a.fo, m, nt * 8, h);
+                }
+            }
+        } else if (EPI == EPI_STORE || EPI == EPI_RESID) {
+            // unit (row, 8-column half of a tile); lanes 2q and 2q+1 hold the two halves of one tile row
+#pragma unroll
+            for (int it = 0; it < TR * 2 * TPW / 64; it++) {
+                const int u = it * 64 + lane;
+                const int r = u / (2 * TPW), s8 = u % (2 * TPW), m = row0 + r, nt = tile0 + (s8 >> 1);
+                const int col = nt * 16 + (s8 & 1) * 8;
+                const bool ok = m < a.M && nt < ntiles;
+                const float4_t v0 = *(const float4_t*)(wt + r * TLD + 8 * s8), v1 = *(const float4_t*)(wt + r * TLD + 8 * s8 + 4);
+                float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                if (EPI == EPI_STORE) {
+                    if (ok) {
+                        float* dst = a.out + row_off(a.omap, m) + col;
+                        if (((uintptr_t)dst & 15) == 0) {
+                            *(float4_t*)dst = v0;
+                            *(float4_t*)(dst + 4) = v1;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) dst[e] = v[e];
+                        }
+                    }
+                } else {
+                    // x += y; the new x as fragments for the next consumer and its 16-column sums of squares
+                    float sq = 0.f;
+                    if (ok) {
+                        float* xr = a.resid + (size_t)m * a.ldr + col;
+                        const bool al = ((uintptr_t)xr & 15) == 0;
+                        float x[8];
+                        if (al) {
+                            const float4_t x0 = *(const float4_t*)xr, x1 = *(const float4_t*)(xr + 4);
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                x[e] = x0[e];
+                                x[4 + e] = x1[e];
+                            }
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) x[e] = xr[e];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            v[e] += x[e];
+                            sq += v[e] * v[e];
+                        }
+                        if (al) {
+                            *(float4_t*)xr = (float4_t){v[0], v[1], v[2], v[3]};
+                            *(float4_t*)(xr + 4) = (float4_t){v[4], v[5], v[6], v[7]};
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) xr[e] = v[e];
+                        }
+                        if (a.fo.buf) {
+                            if (a.fo.norm_w)
+#pragma unroll
+                                for (int e = 0; e < 8; e++) v[e] *= a.fo.norm_w[col + e];
+                            frag_put8_w(a.fo, m, col, v);
+                        }
+                    }
+                    sq += __shfl_xor(sq, 1, 64);
+                    if (a.fo.ssq && ok && (s8 & 1) == 0) a.fo.ssq[(size_t)m * a.fo.ssq_ld + nt] = sq;
+                }
+            }
+        } else if (EPI == EPI_QKV) {
+            // unit (row, tile): dims 8 jh .. +7 and 8 jh + hd/2 .. +7 of one head
+            const QkvEpi& e = a.qkv;
+            const int hd = e.hd, half = hd >> 1;
+            const int QD = e.n_heads * hd, KD = e.n_kv * hd;
+            for (int u = lane; u < TR * TPW; u += 64) {
+                const int r = u / TPW, j = u % TPW, m = row0 + r, nt = tile0 + j;
+                if (m >= a.M || nt >= ntiles) continue;
+                const int rowq = nt * 16, head = rowq / hd, d0 = 8 * ((rowq % hd) >> 4);
+                float* dst;
+                if (rowq < QD) dst = e.q_out + (size_t)m * QD + head * hd;
+                else if (rowq < QD + KD) dst = e.kv_out + (size_t)m * 2 * KD + (head - e.n_heads) * hd;
+                else dst = e.kv_out + (size_t)m * 2 * KD + KD + (head - e.n_heads - e.n_kv) * hd;
+                const float* src = wt + r * TLD + 16 * j;
+                float* p1 = dst + d0;
+                float* p2 = dst + d0 + half;
+                if ((((uintptr_t)p1 | (uintptr_t)p2) & 15) == 0) {
+                    *(float4_t*)p1 = *(const float4_t*)src;
+                    *(float4_t*)(p1 + 4) = *(const float4_t*)(src + 4);
+                    *(float4_t*)p2 = *(const float4_t*)(src + 8);
+                    *(float4_t*)(p2 + 4) = *(const float4_t*)(src + 12);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        p1[q] = src[q];
+                        p2[q] = src[8 + q];
                     }
                 }
             }
