@@ -284,6 +284,7 @@ static constexpr int AM_HD = 128;
 static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
 static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
 static constexpr int AM_MAXCH = 64;         // chunks one merge combines
+static constexpr int AM_STAGE = 2 * 32 * AM_HD + 512;  // one INT8 block staged in LDS: K, V^T, scales
 static constexpr float AM_LOG2E = 1.4426950408889634f;
 
 // Raw K/V operands of one 32-token block for one lane (lane = (lr, lg)).
@@ -376,6 +377,20 @@ __device__ __forceinline__ float rows_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Output dims ocol .. ocol+3 of row orow held by lane q of a row's 32 lanes (ocol % 8 == 0 for
+// even q): lanes q and q ^ 1 together form one 8-column fragment entry, written by the even lane.
+__device__ __forceinline__ void frag_out_pair(const XFrag& fo, int orow, int ocol, float4_t o4, int q) {
+    float4_t p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = __shfl_xor(o4[i], 1, 64);
+    if (q & 1) return;
+    float v[8] = {o4[0], o4[1], o4[2], o4[3], p[0], p[1], p[2], p[3]};
+    if (fo.norm_w)
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] *= fo.norm_w[ocol + e];
+    frag_put8_w(fo, orow, ocol, v);
+}
+
 // Flash-decode attention on MFMA for head_dim 128 and fp16 / INT8 caches.
 // Workgroup = (sequence, kv head, tile of <= 16 query rows, token chunk), 8 waves;
 // wave w takes the chunk's 32-token blocks w, w+8, ... with the next block's
@@ -386,9 +401,11 @@ __device__ __forceinline__ float rows_sum(float x) {
 // the lane of their row.  Softmax runs in base 2 (v_exp_f32).  With one chunk
 // the workgroup writes the output; otherwise chunk partials go out with
 // coherent 16-byte stores and the last workgroup of the group merges them.
-template <int KVF, int DEPTH>
+template <int KVF, int DEPTH, bool DMA>
 __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
-    __shared__ __align__(16) float mg_o[AM_WAVES][AM_ROWS][AM_REC];
+    // dynamic LDS: the DMA block stages during the token loop, then the wave merge
+    extern __shared__ __attribute__((aligned(1024))) char am_lds[];
+    float (*mg_o)[AM_ROWS][AM_REC] = reinterpret_cast<float (*)[AM_ROWS][AM_REC]>(am_lds);
     __shared__ float mg_m[AM_WAVES][AM_ROWS], mg_l[AM_WAVES][AM_ROWS];
     __shared__ unsigned s_last;
 
@@ -412,7 +429,10 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const size_t hb = (size_t)sl * a.n_kv + kvh;
     const int t_begin = chunk * a.chunk;
     const int t_end = min(kv_len, t_begin + a.chunk);
-    append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
+    // The DMA path issues its first two block rows before appending when they end
+    // before the new positions, so the append's round trips overlap those loads.
+    const bool late_append = DMA && t_end > t_begin && t_begin + 2 * 32 * AM_WAVES <= pos0;
+    if (!late_append) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
 
     // ---- this lane's query row (lr): Q^T B operand, hi/lo, dims 32*lg + 8*kk + slot ----
     const bool row_ok = lr < R;
@@ -438,7 +458,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     // the wave's own last block (re-reads hit L1), or the chunk's last one for a wave without blocks
     const int t_last = tb <= t_chunk_last ? tb + (t_chunk_last - tb) / STEP * STEP : t_chunk_last;
     KvRaw<KVF> ring[DEPTH + 1];
-    if (t_end > t_begin) {
+    if (!DMA && t_end > t_begin) {
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) load_kv_block<KVF>(a, hb, min(tb + d * STEP, t_last), lr, lg, ring[d]);
     }
@@ -519,14 +539,64 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
         }
     };
-    for (; tb < t_end;) {
+    if constexpr (DMA) {
+        // INT8 blocks stream into two LDS stages per wave with direct loads (no
+        // VGPRs held in flight, waits counted here): K 4 KiB, V^T 4 KiB, then
+        // 256 bytes each of K and V scales (tokens 2l, 2l+1 in lane l < 16).
+        static_assert(KVF == KV_INT8, "DMA staging is laid out for INT8 blocks");
+        constexpr int KVB = 32 * AM_HD;  // bytes of K (and of V) per block
+        char* st0 = am_lds + wid * 2 * AM_STAGE;
+        const __amdgpu_buffer_rsrc_t kr = coh_rsrc((const uint8_t*)a.kc + hb * a.cap * AM_HD);
+        const __amdgpu_buffer_rsrc_t vr = coh_rsrc((const uint8_t*)a.vc + hb * a.cap * AM_HD);
+        const __amdgpu_buffer_rsrc_t ksr = coh_rsrc(a.ks + hb * a.cap), vsr = coh_rsrc(a.vs + hb * a.cap);
+        const int sc_voff = (lane & 15) * 4;
+        auto issue = [&](char* st, int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int d = 0; d <= DEPTH; d++) {
-            if (tb >= t_end) break;
-            load_kv_block<KVF>(a, hb, min(tb + DEPTH * STEP, t_last), lr, lg, ring[(d + DEPTH) % (DEPTH + 1)]);
-            __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the block's math
-            block(ring[d]);
-            tb += STEP;
+            for (int p = 0; p < 4; p++) lds_dma16(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+#pragma unroll
+            for (int p = 0; p < 4; p++) lds_dma16(vr, st + KVB + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+            lds_dma4(ksr, st + 2 * KVB, sc_voff, t * 2);
+            lds_dma4(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
+        };
+        // A block is copied to registers as soon as it lands and its stage is refilled
+        // at once, so both stages stay in flight while the block is computed.
+        constexpr int NL = 10;  // DMA loads per block
+        if (tb < t_end) {
+            issue(st0, tb);
+            issue(st0 + AM_STAGE, min(tb + STEP, t_last));
+        }
+        if (late_append) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
+        for (int i = 0; tb < t_end; i++, tb += STEP) {
+            char* cur_st = st0 + (i & 1) * AM_STAGE;
+            wait_vmcnt<NL>();  // block i has landed; block i + 1 may still be in flight
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            KvRaw<KVF> cur;
+#pragma unroll
+            for (int ts = 0; ts < 2; ts++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) cur.k[ts][c] = *(const u32x4v_t*)(cur_st + ((ts * 2 + c) * 64 + lane) * 16);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) cur.v[dt] = *(const u32x2_t*)(cur_st + KVB + (16 * dt + lr) * 32 + 8 * lg);
+            cur.ksc = *(const u32x4v_t*)(cur_st + 2 * KVB + 16 * lg);
+            cur.vsc = *(const u32x4v_t*)(cur_st + 2 * KVB + 256 + 16 * lg);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage has been read
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            issue(cur_st, min(tb + 2 * STEP, t_last));
+            block(cur);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();  // every wave's stages are idle before the merge reuses the LDS
+    } else {
+        for (; tb < t_end;) {
+#pragma unroll
+            for (int d = 0; d <= DEPTH; d++) {
+                if (tb >= t_end) break;
+                load_kv_block<KVF>(a, hb, min(tb + DEPTH * STEP, t_last), lr, lg, ring[(d + DEPTH) % (DEPTH + 1)]);
+                __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the block's math
+                block(ring[d]);
+                tb += STEP;
+            }
         }
     }
     // ---- merge the waves in LDS: lane holds O^T[16*dt + 4*lg + i][lr] ----
@@ -559,9 +629,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         if (r < R) {
             const float4_t o4 = acc * (L > 0.f ? 1.0f / L : 0.f);
             *(float4_t*)out = o4;
-            if (a.fo.buf)
-#pragma unroll
-                for (int i = 0; i < 4; i++) frag_put(a.fo, orow, ocol + i, o4[i]);
+            if (a.fo.buf) frag_out_pair(a.fo, orow, ocol, o4, q);
         }
         return;
     }
@@ -607,9 +675,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     }
     const float4_t o4 = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
     *(float4_t*)out = o4;
-    if (a.fo.buf)
-#pragma unroll
-        for (int i = 0; i < 4; i++) frag_put(a.fo, orow, ocol + i, o4[i]);
+    if (a.fo.buf) frag_out_pair(a.fo, orow, ocol, o4, q);
 }
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
@@ -617,10 +683,22 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
     (void)hipGetLastError();
     if ((a.kv_fmt == KV_INT8 || a.kv_fmt == KV_F16) && a.hd == AM_HD) {
         if (a.rows_per_tile > AM_ROWS || a.chunk % (32 * AM_WAVES) || a.nchunks > AM_MAXCH || a.cap % 32) return 3;
+        static bool attr = false;
+        constexpr size_t merge_bytes = sizeof(float) * AM_WAVES * AM_ROWS * AM_REC;
+        constexpr size_t dma_bytes = (size_t)AM_WAVES * 2 * AM_STAGE;
+        constexpr size_t i8_bytes = dma_bytes > merge_bytes ? dma_bytes : merge_bytes;
+        if (!attr) {
+            if (note_error(hipFuncSetAttribute((const void*)attn_mfma_kernel<KV_INT8, 1, true>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)i8_bytes)) ||
+                note_error(hipFuncSetAttribute((const void*)attn_mfma_kernel<KV_F16, 1, false>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)merge_bytes)))
+                return 4;
+            attr = true;
+        }
         if (a.kv_fmt == KV_INT8)
-            hipLaunchKernelGGL((attn_mfma_kernel<KV_INT8, 1>), dim3(grid), dim3(512), 0, stream, a);
+            hipLaunchKernelGGL((attn_mfma_kernel<KV_INT8, 1, true>), dim3(grid), dim3(512), i8_bytes, stream, a);
         else
-            hipLaunchKernelGGL((attn_mfma_kernel<KV_F16, 1>), dim3(grid), dim3(512), 0, stream, a);
+            hipLaunchKernelGGL((attn_mfma_kernel<KV_F16, 1, false>), dim3(grid), dim3(512), merge_bytes, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
     if (a.hd > AT_MAXHD || a.rows_per_tile > AT_MAXR || a.rows_per_tile <= 0) return 3;

@@ -34,25 +34,6 @@ namespace aarh {
 static constexpr int GM_WAVES = 8, GM_WM = 2, GM_WN = 4;
 static constexpr int GM_LDS_BUDGET = 150 * 1024;  // dynamic LDS for the stage ring
 
-// One 1 KiB wave load straight into LDS: lane l's 16 bytes at rsrc + voff +
-// soff land at LDS address lds_base + 16 l (buffer_load_dwordx4 ... lds, base in
-// M0).  Written as inline asm so the compiler does not see an LDS write it would
-// guard with a conservative vmcnt(0) before every LDS read: the kernel counts
-// these loads itself.  M0 is restored before the statement ends.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const void* lds_dst, int voff, int soff) {
-    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
-    int saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(base), "v"(voff), "s"(r), "s"(soff)
-        : "memory");
-}
-
 template <int FMT, int CPW>
 struct GmCfg {
     typedef FmtTraits<FMT> T;
@@ -72,13 +53,6 @@ struct GmCfg {
     static_assert(Z_BYTES <= 1024, "scale/zero words of a stage: one 64-lane load");
     static_assert(NS * STAGE <= GM_LDS_BUDGET, "stage ring exceeds LDS");
 };
-
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14), other counters unconstrained.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 template <int FMT, int EPI, int CPW>
 __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, int gps) {
