@@ -249,15 +249,20 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         }
     };
 
-    // ---- pipeline: NS - 1 stages in flight ahead of the one computed ----
+    // ---- pipeline.  NS >= 3: LA = NS - 2 stages in flight ahead of the one
+    // computed, and the stage a load rewrites was last read two groups ago, so
+    // the one barrier per group (after the wait) also orders every wave's reads
+    // before the rewrite.  NS == 2: one stage ahead and a second barrier after
+    // the compute.
+    constexpr int LA = NS >= 3 ? NS - 2 : 1;
 #pragma unroll
-    for (int i = 0; i < NS - 1; i++) issue_stage(i, g0 + min(i, ng - 1));
+    for (int i = 0; i < LA; i++) issue_stage(i, g0 + min(i, ng - 1));
     for (int gi = 0; gi < ng; gi++) {
-        issue_stage((gi + NS - 1) % NS, g0 + min(gi + NS - 1, ng - 1));  // past the end: harmless repeats
-        wait_vmcnt<C::L * (NS - 1)>();
+        issue_stage((gi + LA) % NS, g0 + min(gi + LA, ng - 1));  // past the end: harmless repeats
+        wait_vmcnt<C::L * LA>();
         __syncthreads();
         compute_stage(gi % NS);
-        __syncthreads();
+        if constexpr (NS == 2) __syncthreads();
     }
     wait_vmcnt<0>();
     __syncthreads();  // every wave's stage loads have landed: the ring is free for the epilogue
