@@ -34,30 +34,33 @@ namespace aarh {
 static constexpr int GM_WAVES = 8, GM_WM = 2, GM_WN = 4;
 static constexpr int GM_LDS_BUDGET = 150 * 1024;  // dynamic LDS for the stage ring
 
-template <int FMT, int CPW>
+template <int FMT, int CPW, int TPW_>
 struct GmCfg {
     typedef FmtTraits<FMT> T;
-    static constexpr int TPW = FMT == WF_BF16 ? 2 : 4;              // weight tiles per wave
+    static constexpr int TPW = TPW_;                                // weight tiles per wave
     static constexpr int NT = GM_WN * TPW;                          // weight tiles per block
     static constexpr int MC = GM_WM * CPW;                          // row chunks per block
     static constexpr int A_BYTES = MC * 8192;                       // hi + lo fragments of one group
     static constexpr int W_BYTES = NT * T::TILE_BYTES;
-    static constexpr int Z_BYTES = FMT == WF_INT4 ? NT * 64 : 0;
+    static constexpr int Z_BYTES = FMT == WF_INT4 ? 1024 : 0;      // one 64-lane load of scale/zero words
     static constexpr int STAGE = A_BYTES + W_BYTES + Z_BYTES;
-    static constexpr int NS_RAW = GM_LDS_BUDGET / STAGE;
+    // narrow 32-row blocks keep the ring small enough for two blocks per CU
+    static constexpr int BUDGET = (CPW == 1 && TPW <= 2) ? 76 * 1024 : GM_LDS_BUDGET;
+    static constexpr int NS_RAW = BUDGET / STAGE;
     static constexpr int NS = NS_RAW < 2 ? 2 : (NS_RAW > 4 ? 4 : NS_RAW);
     static constexpr int A_PW = MC * 8 / GM_WAVES;                  // 1 KiB activation pieces per wave
-    static constexpr int W_PW = W_BYTES / 1024 / GM_WAVES;          // 1 KiB weight pieces per wave
+    static constexpr int W_PIECES = W_BYTES / 1024;
+    static constexpr int W_PW = W_PIECES < GM_WAVES ? 1 : W_PIECES / GM_WAVES;  // 1 KiB weight pieces per wave
     static constexpr int L = A_PW + W_PW + (FMT == WF_INT4 ? 1 : 0);  // loads per wave per stage
-    static_assert(MC * 8 % GM_WAVES == 0 && W_BYTES % (1024 * GM_WAVES) == 0, "stage pieces split over waves");
-    static_assert(Z_BYTES <= 1024, "scale/zero words of a stage: one 64-lane load");
+    static_assert(MC * 8 % GM_WAVES == 0, "activation pieces split over waves");
+    static_assert(W_PIECES < GM_WAVES || W_PIECES % GM_WAVES == 0, "weight pieces split over waves");
     static_assert(NS * STAGE <= GM_LDS_BUDGET, "stage ring exceeds LDS");
 };
 
-template <int FMT, int EPI, int CPW>
+template <int FMT, int EPI, int CPW, int TPW_>
 __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, int gps) {
     typedef FmtTraits<FMT> T;
-    typedef GmCfg<FMT, CPW> C;
+    typedef GmCfg<FMT, CPW, TPW_> C;
     constexpr int TPW = C::TPW, NT = C::NT, MC = C::MC, NS = C::NS, LW = T::LANE_WORDS;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ float s_inv[MC * 16];
@@ -146,7 +149,8 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         // bytes of the tile), so the wave reading piece sub from LDS is conflict-free
 #pragma unroll
         for (int q = 0; q < C::W_PW; q++) {
-            const int pi = wid * C::W_PW + q, jj = pi / WP, sub = pi % WP;
+            // fewer pieces than waves: the extra waves repeat a piece (same bytes, same place)
+            const int pi = (wid * C::W_PW + q) % C::W_PIECES, jj = pi / WP, sub = pi % WP;
             const int nt = min(nb * NT + jj, ntiles - 1);
             lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * (16 * WP) + sub * 16,
                       (int)(((unsigned)nt * G + g) * T::TILE_BYTES));
@@ -431,9 +435,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
             }
         } else if (EPI == EPI_STORE || EPI == EPI_RESID) {
             // unit (row, 8-column half of a tile); lanes 2q and 2q+1 hold the two halves of one tile row
-#pragma unroll
-            for (int it = 0; it < TR * 2 * TPW / 64; it++) {
-                const int u = it * 64 + lane;
+            for (int u = lane; u < TR * 2 * TPW; u += 64) {  // a multiple of 64 units, or 32
                 const int r = u / (2 * TPW), s8 = u % (2 * TPW), m = row0 + r, nt = tile0 + (s8 >> 1);
                 const int col = nt * 16 + (s8 & 1) * 8;
                 const bool ok = m < a.M && nt < ntiles;
@@ -535,46 +537,133 @@ static int cu_count() {
     return cus;
 }
 
-template <int FMT, int EPI, int CPW>
-static int launch_w(const GemvArgs& a, hipStream_t stream) {
-    typedef GmCfg<FMT, CPW> C;
-    static bool attr = false;
-    const size_t lds_bytes = (size_t)C::NS * C::STAGE;
-    if (!attr) {
-        if (note_error(hipFuncSetAttribute((const void*)gemm_kernel<FMT, EPI, CPW>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes)))
-            return 4;
-        attr = true;
+template <int FMT, int EPI, int CPW, int TPW>
+static size_t ring_bytes() {
+    typedef GmCfg<FMT, CPW, TPW> C;
+    return (size_t)C::NS * C::STAGE;
+}
+
+// Resident blocks per CU of one configuration (dynamic LDS attribute set on first use).
+template <int FMT, int EPI, int CPW, int TPW>
+static int blocks_per_cu() {
+    static int per_cu = 0;
+    if (!per_cu) {
+        const size_t lds = ring_bytes<FMT, EPI, CPW, TPW>();
+        if (note_error(hipFuncSetAttribute((const void*)gemm_kernel<FMT, EPI, CPW, TPW>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)))
+            return 0;
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemm_kernel<FMT, EPI, CPW, TPW>,
+                                                           GM_WAVES * 64, lds);
+        per_cu = std::max(per_cu, 1);
     }
+    return per_cu;
+}
+
+// Launch with CPW row chunks and TPW weight tiles per wave and S k-splits.
+template <int FMT, int EPI, int CPW, int TPW>
+static int launch_cfg(const GemvArgs& a, int S, hipStream_t stream) {
+    typedef GmCfg<FMT, CPW, TPW> C;
+    if (!blocks_per_cu<FMT, EPI, CPW, TPW>()) return 4;
     const int G = a.K >> 7;
     const int NB = (a.N / 16 + C::NT - 1) / C::NT;
     const int MB = ((a.M + 15) / 16 + C::MC - 1) / C::MC;
-    // Split-K only for the 32-row blocks of small-N projections, at most 4 ways:
-    // each extra split costs a 32 KiB partial round trip through memory, which
-    // measured slower than idle CUs beyond that.
-    int S = 1;
-    if (CPW == 1) {
-        const int units = NB * MB;
-        S = std::max(1, std::min(std::min(4, G / 2), cu_count() / std::max(units, 1)));
-        while (S > 1 && (long long)units * S * C::MC * C::NT * 256 > (a.gpart ? a.gpart_elems : 0)) S--;
-    }
+    S = std::max(1, std::min(S, G));
+    while (S > 1 && (long long)NB * MB * S * C::MC * C::NT * 256 > (a.gpart ? a.gpart_elems : 0)) S--;
     const int gps = (G + S - 1) / S;
     S = (G + gps - 1) / gps;  // every split non-empty
     if (S > 1 && (!a.gcnt || NB * MB > 8192)) return 2;  // counters: 8192 per context
+    const size_t lds = ring_bytes<FMT, EPI, CPW, TPW>();
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemm_kernel<FMT, EPI, CPW>), dim3(NB * MB * S), dim3(GM_WAVES * 64), lds_bytes, stream, a, S,
+    hipLaunchKernelGGL((gemm_kernel<FMT, EPI, CPW, TPW>), dim3(NB * MB * S), dim3(GM_WAVES * 64), lds, stream, a, S,
                        gps);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
-// 64-row blocks (no split) when they already give half a dispatch round of
-// blocks, else 32-row blocks with split-K.
+// Launch plan: row chunks per wave (CPW), weight tiles per wave (TPW) and k-splits (S).
+struct GmPlan {
+    int cpw, tpw, S;
+};
+
+// Measured best plans for the INT4 projection shapes of the 7B-class decoder
+// (d_model 4096, 32 x 128 query heads, 8 kv heads, ffn 11008) at 32 / 64 / 128
+// rows (replay and MTP batches; verify batches of 16 and 32 sequences x 4 rows).
+struct GmTuned {
+    int N, K, plan[3][3];
+};
+static constexpr GmTuned GM_TUNED[] = {
+    {6144, 4096, {{1, 2, 4}, {2, 2, 4}, {2, 2, 2}}},
+    {4096, 4096, {{1, 1, 4}, {2, 1, 4}, {2, 1, 2}}},
+    {22016, 4096, {{1, 2, 3}, {2, 2, 1}, {2, 4, 1}}},
+    {4096, 11008, {{1, 2, 8}, {2, 1, 4}, {2, 2, 4}}},
+};
+
+template <int FMT, int EPI>
+static int plan_capacity(int cpw, int tpw) {
+    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
+    int per_cu = 1;
+    if (cpw == 2) per_cu = tpw == T4 ? blocks_per_cu<FMT, EPI, 2, T4>() : tpw == 2 ? blocks_per_cu<FMT, EPI, 2, 2>()
+                                                                               : blocks_per_cu<FMT, EPI, 2, 1>();
+    else per_cu = tpw == T4 ? blocks_per_cu<FMT, EPI, 1, T4>() : tpw == 2 ? blocks_per_cu<FMT, EPI, 1, 2>()
+                                                                        : blocks_per_cu<FMT, EPI, 1, 1>();
+    return cu_count() * std::max(per_cu, 1);
+}
+
+// 64-row blocks above 32 rows, 32-row blocks otherwise.  Among the tile widths
+// and splits whose blocks fit one dispatch round, the plan fills the round best
+// (fill counted up to 2/3 of a one-block-per-CU round, 1/2 of a two-block one:
+// beyond that wider blocks measured faster than more of them), then uses the
+// fewest splits, then the widest tiles.
+template <int FMT, int EPI>
+static GmPlan plan_gemm(const GemvArgs& a) {
+    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
+    const int G = a.K >> 7, ntiles = a.N / 16, chunks = (a.M + 15) / 16;
+    if (FMT == WF_INT4)
+        for (const GmTuned& t : GM_TUNED)
+            if (t.N == a.N && t.K == a.K) {
+                const int* p = t.plan[a.M <= 32 ? 0 : a.M <= 64 ? 1 : 2];
+                return {p[0], p[1], p[2]};
+            }
+    const int cpw = a.M > 32 ? 2 : 1;
+    GmPlan best{cpw, 1, 1};
+    double bkey0 = -1.0;
+    int bkey1 = 0, bkey2 = 0;
+    for (int tpw = T4; tpw >= 1; tpw >>= 1) {
+        const int cap = plan_capacity<FMT, EPI>(cpw, tpw);
+        const int units = ((ntiles + GM_WN * tpw - 1) / (GM_WN * tpw)) * ((chunks + GM_WM * cpw - 1) / (GM_WM * cpw));
+        for (int S = 1; S <= std::min(8, G); S++) {
+            const int gps = (G + S - 1) / S;
+            if ((G + gps - 1) / gps != S) continue;  // another S gives the same splits
+            const long long blocks = (long long)units * S;
+            if (blocks > cap) break;
+            const double fill = std::min((double)blocks / cap, cap > cu_count() ? 0.5 : 0.66);
+            const double key0 = std::floor(fill * 100.0 + 1e-9) / 100.0;
+            if (key0 > bkey0 || (key0 == bkey0 && (-S > bkey1 || (-S == bkey1 && tpw > bkey2)))) {
+                bkey0 = key0;
+                bkey1 = -S;
+                bkey2 = tpw;
+                best = {cpw, tpw, S};
+            }
+        }
+    }
+    return best;
+}
+
+template <int FMT, int EPI>
+static int launch_plan(const GemvArgs& a, const GmPlan& p, hipStream_t stream) {
+    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
+    if (p.cpw == 2) {
+        if (p.tpw == T4) return launch_cfg<FMT, EPI, 2, T4>(a, p.S, stream);
+        if (p.tpw == 2) return launch_cfg<FMT, EPI, 2, 2>(a, p.S, stream);
+        return launch_cfg<FMT, EPI, 2, 1>(a, p.S, stream);
+    }
+    if (p.tpw == T4) return launch_cfg<FMT, EPI, 1, T4>(a, p.S, stream);
+    if (p.tpw == 2) return launch_cfg<FMT, EPI, 1, 2>(a, p.S, stream);
+    return launch_cfg<FMT, EPI, 1, 1>(a, p.S, stream);
+}
+
 template <int FMT, int EPI>
 static int launch_m(const GemvArgs& a, hipStream_t stream) {
-    typedef GmCfg<FMT, 2> C;
-    const int units64 = ((a.N / 16 + C::NT - 1) / C::NT) * (((a.M + 15) / 16 + C::MC - 1) / C::MC);
-    if (a.M > 32 && 2 * units64 >= cu_count()) return launch_w<FMT, EPI, 2>(a, stream);
-    return launch_w<FMT, EPI, 1>(a, stream);
+    return launch_plan<FMT, EPI>(a, plan_gemm<FMT, EPI>(a), stream);
 }
 
 template <int FMT>
