@@ -696,13 +696,13 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
             attr = true;
         }
         if (a.kv_fmt == KV_INT8)
-            hipLaunchKernelGGL((attn_mfma_kernel<KV_INT8, 1, true>), dim3(grid), dim3(512), i8_bytes, stream, a);
+            launch_timed(attn_mfma_kernel<KV_INT8, 1, true>, dim3(grid), dim3(512), (uint32_t)i8_bytes, stream, a);
         else
-            hipLaunchKernelGGL((attn_mfma_kernel<KV_F16, 1, false>), dim3(grid), dim3(512), merge_bytes, stream, a);
+            launch_timed(attn_mfma_kernel<KV_F16, 1, false>, dim3(grid), dim3(512), (uint32_t)merge_bytes, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
     if (a.hd > AT_MAXHD || a.rows_per_tile > AT_MAXR || a.rows_per_tile <= 0) return 3;
-    hipLaunchKernelGGL(attn_kernel, dim3(grid), dim3(AT_THREADS), 0, stream, a);
+    launch_timed(attn_kernel, dim3(grid), dim3(AT_THREADS), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

@@ -574,8 +574,8 @@ static int launch_cfg(const GemvArgs& a, int S, hipStream_t stream) {
     if (S > 1 && (!a.gcnt || NB * MB > 8192)) return 2;  // counters: 8192 per context
     const size_t lds = ring_bytes<FMT, EPI, CPW, TPW>();
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemm_kernel<FMT, EPI, CPW, TPW>), dim3(NB * MB * S), dim3(GM_WAVES * 64), lds, stream, a, S,
-                       gps);
+    launch_timed(gemm_kernel<FMT, EPI, CPW, TPW>, dim3(NB * MB * S), dim3(GM_WAVES * 64), (uint32_t)lds, stream, a, S,
+                 gps);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -584,17 +584,19 @@ struct GmPlan {
     int cpw, tpw, S;
 };
 
-// Measured best plans for the INT4 projection shapes of the 7B-class decoder
-// (d_model 4096, 32 x 128 query heads, 8 kv heads, ffn 11008) at 32 / 64 / 128
-// rows (replay and MTP batches; verify batches of 16 and 32 sequences x 4 rows).
+// Measured best plans for the projection shapes of the 7B-class decoder
+// (d_model 4096, 32 x 128 query heads, 8 kv heads, ffn 11008, INT4 g128; bf16
+// LM head over a 32000 vocabulary) at 32 / 64 / 128 rows (replay and MTP
+// batches; verify batches of 16 and 32 sequences x 4 rows).
 struct GmTuned {
-    int N, K, plan[3][3];
+    int fmt, N, K, plan[3][3];
 };
 static constexpr GmTuned GM_TUNED[] = {
-    {6144, 4096, {{1, 2, 4}, {2, 2, 4}, {2, 2, 2}}},
-    {4096, 4096, {{1, 1, 4}, {2, 1, 4}, {2, 1, 2}}},
-    {22016, 4096, {{1, 2, 3}, {2, 2, 1}, {2, 4, 1}}},
-    {4096, 11008, {{1, 2, 8}, {2, 1, 4}, {2, 2, 4}}},
+    {WF_INT4, 6144, 4096, {{1, 2, 4}, {2, 2, 4}, {2, 2, 2}}},
+    {WF_INT4, 4096, 4096, {{1, 1, 4}, {2, 1, 4}, {2, 1, 2}}},
+    {WF_INT4, 22016, 4096, {{1, 2, 3}, {2, 2, 1}, {2, 4, 1}}},
+    {WF_INT4, 4096, 11008, {{1, 2, 8}, {2, 1, 4}, {2, 2, 4}}},
+    {WF_BF16, 32000, 4096, {{1, 2, 1}, {2, 2, 1}, {2, 2, 1}}},
 };
 
 template <int FMT, int EPI>
@@ -617,12 +619,11 @@ template <int FMT, int EPI>
 static GmPlan plan_gemm(const GemvArgs& a) {
     constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
     const int G = a.K >> 7, ntiles = a.N / 16, chunks = (a.M + 15) / 16;
-    if (FMT == WF_INT4)
-        for (const GmTuned& t : GM_TUNED)
-            if (t.N == a.N && t.K == a.K) {
-                const int* p = t.plan[a.M <= 32 ? 0 : a.M <= 64 ? 1 : 2];
-                return {p[0], p[1], p[2]};
-            }
+    for (const GmTuned& t : GM_TUNED)
+        if (t.fmt == FMT && t.N == a.N && t.K == a.K) {
+            const int* p = t.plan[a.M <= 32 ? 0 : a.M <= 64 ? 1 : 2];
+            return {p[0], p[1], p[2]};
+        }
     const int cpw = a.M > 32 ? 2 : 1;
     GmPlan best{cpw, 1, 1};
     double bkey0 = -1.0;

@@ -398,7 +398,7 @@ static int launch_tile(const GemvArgs& a, hipStream_t stream) {
     }
     const int grid = std::min(a.N / 16, grid_cap);
     (void)hipGetLastError();
-    hipLaunchKernelGGL((gemv_tile_kernel<FMT, MP, EPI, NGP>), dim3(grid), dim3(GT_NW * 64), 0, stream, a);
+    launch_timed(gemv_tile_kernel<FMT, MP, EPI, NGP>, dim3(grid), dim3(GT_NW * 64), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -451,7 +451,7 @@ int launch_gemv(const GemvArgs& a, hipStream_t stream) {
         return 2;
     if (a.fmt == WF_F32) {
         (void)hipGetLastError();
-        hipLaunchKernelGGL(gemv_f32_kernel, dim3(a.N / 16), dim3(GT_THREADS), 0, stream, a);
+        launch_timed(gemv_f32_kernel, dim3(a.N / 16), dim3(GT_THREADS), 0, stream, a);
         return note_error(hipGetLastError()) ? 4 : 0;
     }
     switch (a.fmt) {

@@ -1,6 +1,7 @@
 // Kernel argument blocks and launchers of libaarambh_hip (host + device view).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 namespace aarh {
@@ -36,6 +37,29 @@ enum { ACCEPT_FLAG_RATIO_NEAR = 1u, ACCEPT_FLAG_CDF_NEAR = 2u };
 // Dynamic LDS a kernel may request: 160 KiB per workgroup on gfx950 minus room
 // for the kernels' static LDS.
 static constexpr size_t MAX_DYN_LDS = 160 * 1024 - 4096;
+
+// Kernel timing for the runtime's per-class profile: while `stop` is set, the
+// instrumented launches record `start` at the first dispatch's start and `stop`
+// at each dispatch's end (hipExtLaunchKernelGGL), so the profile holds kernel
+// durations without launch gaps.
+struct LaunchTiming {
+    hipEvent_t start, stop;
+    int launches;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+template <typename... Args, typename F = void (*)(Args...)>
+inline void launch_timed(F kernel, const dim3& grid, const dim3& block, uint32_t shmem, hipStream_t stream,
+                         Args... args) {
+    LaunchTiming& t = g_launch_timing;
+    if (t.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, t.launches == 0 ? t.start : nullptr, t.stop, 0u,
+                              args...);
+        t.launches++;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+    }
+}
 
 // Records the message of a failing HIP call (read by the runtime's error path).
 int note_error(hipError_t e);

@@ -13,6 +13,7 @@ namespace aarh {
 static constexpr int MT_THREADS = 256;
 
 static thread_local char g_last_err[256] = "";
+thread_local LaunchTiming g_launch_timing = {nullptr, nullptr, 0};
 
 int note_error(hipError_t e) {
     if (e == hipSuccess) return 0;

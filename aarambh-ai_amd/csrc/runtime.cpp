@@ -227,16 +227,21 @@ struct ProfScope {
     int cls;
     double bytes;
     hipEvent_t a = nullptr;
+    hipEvent_t b = nullptr;
+    // Instrumented launches inside the scope re-record a / b at their own dispatch
+    // start / end; a scope without one keeps the stream-order records taken here.
     ProfScope(aarh_ctx* c_, int cls_, double bytes_) : c(c_), cls(cls_), bytes(bytes_) {
         if (c->prof) {
             a = take_event(c);
+            b = take_event(c);
             (void)hipEventRecord(a, c->stream);
+            g_launch_timing = {a, b, 0};
         }
     }
     ~ProfScope() {
         if (c->prof) {
-            hipEvent_t b = take_event(c);
-            (void)hipEventRecord(b, c->stream);
+            if (g_launch_timing.launches == 0) (void)hipEventRecord(b, c->stream);
+            g_launch_timing = {nullptr, nullptr, 0};
             c->prof_recs.push_back({cls, a, b, bytes});
         }
     }
