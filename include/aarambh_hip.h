@@ -187,7 +187,8 @@ int aarh_top_candidates(aarh_ctx *ctx, const float *logits, int rows, int V, con
    0 launches every kernel from the host each call).  Results are identical either way. --- */
 int aarh_set_graphs(aarh_ctx *ctx, int enable);
 
-/* --- measurement: per-kernel-class HIP-event timing of the context's launches --- */
+/* --- measurement: per-kernel-class timing of the context's launches (HIP events recorded
+   at each kernel dispatch's own start and end; graph replay is off while enabled) --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
        AARH_PROF_GEMV_DOWN = 3, AARH_PROF_GEMV_LMHEAD = 4, AARH_PROF_ATTENTION = 5,
        AARH_PROF_ACCEPT = 6, AARH_PROF_OTHER = 7, AARH_PROF_COUNT = 8 };
