@@ -396,7 +396,13 @@ static int launch_tile(const GemvArgs& a, hipStream_t stream) {
                                                            GT_NW * 64, 0);
         grid_cap = std::max(1, cus) * std::max(1, per_cu);
     }
-    const int grid = std::min(a.N / 16, grid_cap);
+    // Tiles spread evenly over the workgroups (no partial last round).  BF16 items are
+    // 4 KiB per wave, so half the resident workgroups keep as many bytes in flight as
+    // INT4 at full residency; more measured slower (memory queues fill up).
+    const int ntiles = a.N / 16;
+    const int cap = FMT == WF_BF16 ? std::max(1, grid_cap / 2) : grid_cap;
+    const int per_wg = (ntiles + cap - 1) / cap;
+    const int grid = (ntiles + per_wg - 1) / per_wg;
     (void)hipGetLastError();
     launch_timed(gemv_tile_kernel<FMT, MP, EPI, NGP>, dim3(grid), dim3(GT_NW * 64), 0, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
