@@ -50,10 +50,9 @@ struct GmCfg {
     static constexpr int NS = NS_RAW < 2 ? 2 : (NS_RAW > 4 ? 4 : NS_RAW);
     static constexpr int A_PW = MC * 8 / GM_WAVES;                  // 1 KiB activation pieces per wave
     static constexpr int W_PIECES = W_BYTES / 1024;
-    static constexpr int W_PW = W_PIECES < GM_WAVES ? 1 : W_PIECES / GM_WAVES;  // 1 KiB weight pieces per wave
+    static constexpr int W_PW = (W_PIECES + GM_WAVES - 1) / GM_WAVES;  // 1 KiB weight pieces per wave
     static constexpr int L = A_PW + W_PW + (FMT == WF_INT4 ? 1 : 0);  // loads per wave per stage
     static_assert(MC * 8 % GM_WAVES == 0, "activation pieces split over waves");
-    static_assert(W_PIECES < GM_WAVES || W_PIECES % GM_WAVES == 0, "weight pieces split over waves");
     static_assert(NS * STAGE <= GM_LDS_BUDGET, "stage ring exceeds LDS");
 };
 
@@ -149,7 +148,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         // bytes of the tile), so the wave reading piece sub from LDS is conflict-free
 #pragma unroll
         for (int q = 0; q < C::W_PW; q++) {
-            // fewer pieces than waves: the extra waves repeat a piece (same bytes, same place)
+            // pieces not a multiple of the waves: the extra loads repeat a piece (same bytes, same place)
             const int pi = (wid * C::W_PW + q) % C::W_PIECES, jj = pi / WP, sub = pi % WP;
             const int nt = min(nb * NT + jj, ntiles - 1);
             lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * (16 * WP) + sub * 16,
@@ -594,24 +593,26 @@ struct GmTuned {
 static constexpr GmTuned GM_TUNED[] = {
     {WF_INT4, 6144, 4096, {{1, 2, 4}, {2, 2, 4}, {2, 2, 2}}},
     {WF_INT4, 4096, 4096, {{1, 1, 4}, {2, 1, 4}, {2, 1, 2}}},
-    {WF_INT4, 22016, 4096, {{1, 2, 3}, {2, 2, 1}, {2, 4, 1}}},
+    {WF_INT4, 22016, 4096, {{1, 3, 2}, {2, 3, 2}, {2, 3, 1}}},
     {WF_INT4, 4096, 11008, {{1, 2, 8}, {2, 1, 4}, {2, 2, 4}}},
     {WF_BF16, 32000, 4096, {{1, 2, 1}, {2, 2, 1}, {2, 2, 1}}},
 };
 
+template <int FMT, int EPI, int CPW>
+static int per_cu_of(int tpw) {
+    constexpr int T4 = FMT == WF_BF16 ? 2 : 4, T3 = FMT == WF_BF16 ? 2 : 3;
+    return tpw == T4 ? blocks_per_cu<FMT, EPI, CPW, T4>() : tpw == 3 ? blocks_per_cu<FMT, EPI, CPW, T3>()
+         : tpw == 2 ? blocks_per_cu<FMT, EPI, CPW, 2>() : blocks_per_cu<FMT, EPI, CPW, 1>();
+}
+
 template <int FMT, int EPI>
 static int plan_capacity(int cpw, int tpw) {
-    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
-    int per_cu = 1;
-    if (cpw == 2) per_cu = tpw == T4 ? blocks_per_cu<FMT, EPI, 2, T4>() : tpw == 2 ? blocks_per_cu<FMT, EPI, 2, 2>()
-                                                                               : blocks_per_cu<FMT, EPI, 2, 1>();
-    else per_cu = tpw == T4 ? blocks_per_cu<FMT, EPI, 1, T4>() : tpw == 2 ? blocks_per_cu<FMT, EPI, 1, 2>()
-                                                                        : blocks_per_cu<FMT, EPI, 1, 1>();
+    const int per_cu = cpw == 2 ? per_cu_of<FMT, EPI, 2>(tpw) : per_cu_of<FMT, EPI, 1>(tpw);
     return cu_count() * std::max(per_cu, 1);
 }
 
 // 64-row blocks above 32 rows, 32-row blocks otherwise.  Among the tile widths
-// and splits whose blocks fit one dispatch round, the plan fills the round best
+// (4, 3, 2, 1 weight tiles per wave; 2, 1 for BF16) and splits whose blocks fit one dispatch round, the plan fills the round best
 // (fill counted up to 2/3 of a one-block-per-CU round, 1/2 of a two-block one:
 // beyond that wider blocks measured faster than more of them), then uses the
 // fewest splits, then the widest tiles.
@@ -628,7 +629,7 @@ static GmPlan plan_gemm(const GemvArgs& a) {
     GmPlan best{cpw, 1, 1};
     double bkey0 = -1.0;
     int bkey1 = 0, bkey2 = 0;
-    for (int tpw = T4; tpw >= 1; tpw >>= 1) {
+    for (int tpw = T4; tpw >= 1; tpw--) {
         const int cap = plan_capacity<FMT, EPI>(cpw, tpw);
         const int units = ((ntiles + GM_WN * tpw - 1) / (GM_WN * tpw)) * ((chunks + GM_WM * cpw - 1) / (GM_WM * cpw));
         for (int S = 1; S <= std::min(8, G); S++) {
@@ -652,6 +653,9 @@ static GmPlan plan_gemm(const GemvArgs& a) {
 template <int FMT, int EPI>
 static int launch_plan(const GemvArgs& a, const GmPlan& p, hipStream_t stream) {
     constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
+    if constexpr (FMT != WF_BF16)
+        if (p.tpw == 3) return p.cpw == 2 ? launch_cfg<FMT, EPI, 2, 3>(a, p.S, stream)
+                                          : launch_cfg<FMT, EPI, 1, 3>(a, p.S, stream);
     if (p.cpw == 2) {
         if (p.tpw == T4) return launch_cfg<FMT, EPI, 2, T4>(a, p.S, stream);
         if (p.tpw == 2) return launch_cfg<FMT, EPI, 2, 2>(a, p.S, stream);
