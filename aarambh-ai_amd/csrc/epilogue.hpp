@@ -91,9 +91,12 @@ __device__ __forceinline__ half8_t int8_b_operand(uint32_t d0, uint32_t d1) {
 // ---------------------------------------------------------------------------
 // Threads t0, t0 + stride, ... of the caller share the work; wave_only: the
 // caller is a single wave (no workgroup barrier may be used).
+// pf (optional, LDS): inputs of this tile loaded ahead by the caller, entry idx of
+// the loop below: RESID pf[idx] = old x, pf[64 + idx] = consumer norm weight; QKV
+// pf[idx] = cos, pf[64 + idx] = sin of the row's position (valid for idx < 64).
 template <int EPI>
 __device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc, int mbase, int t0, int stride,
-                             bool wave_only) {
+                             bool wave_only, const float* pf = nullptr) {
     const int tid = t0;
     if (EPI == EPI_STORE) {
         for (int idx = tid; idx < Mc * 16; idx += stride) {
@@ -105,10 +108,14 @@ __device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc,
         for (int idx = tid; idx < Mc * 16; idx += stride) {
             const int m = idx >> 4, n = idx & 15;
             float* p = a.resid + (size_t)(mbase + m) * a.ldr + nt * 16 + n;
-            const float xn = *p + yt[m][n];
+            const bool pre = pf && idx < 64;
+            const float xn = (pre ? pf[idx] : *p) + yt[m][n];
             *p = xn;
             yt[m][n] = xn;
-            if (a.fo.buf) frag_put(a.fo, mbase + m, nt * 16 + n, xn);
+            if (a.fo.buf) {
+                if (pre) frag_put_w(a.fo, mbase + m, nt * 16 + n, xn * pf[64 + idx]);
+                else frag_put(a.fo, mbase + m, nt * 16 + n, xn);
+            }
         }
         if (a.fo.ssq) {
             if (wave_only) {
@@ -150,9 +157,16 @@ __device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc,
             float y1 = yt[m][r], y2 = yt[m][8 + r];
             if (is_q || is_k) {
                 // RoPE (rope.rs:107-126): half-split rotation at the row's position
-                const int bs = mg / e.S, s = mg % e.S;
-                const int pos = e.pos0[bs] + s;
-                const float cs = e.rope_cos[(size_t)pos * half + d1], sn = e.rope_sin[(size_t)pos * half + d1];
+                float cs, sn;
+                if (pf && idx < 64) {
+                    cs = pf[idx];
+                    sn = pf[64 + idx];
+                } else {
+                    const int bs = mg / e.S, s = mg % e.S;
+                    const int pos = e.pos0[bs] + s;
+                    cs = e.rope_cos[(size_t)pos * half + d1];
+                    sn = e.rope_sin[(size_t)pos * half + d1];
+                }
                 {
 #pragma clang fp contract(off)
                     const float r1 = y1 * cs - y2 * sn;

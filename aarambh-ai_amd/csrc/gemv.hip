@@ -77,6 +77,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     __shared__ float yt_s[2][16][17];
     __shared__ float s_inv[16];
     __shared__ unsigned cnt_s[2], gen_s[2];
+    __shared__ float ep_pf[128];  // epilogue inputs of the last tile, loaded ahead by wave NW - 1
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int G = a.K >> 7;
@@ -197,6 +198,30 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             for (int gi = 0; gi < NGP; gi++) load_frag_reg(fa[gi], max(min(wid + NW * gi, glast), 0));
         }
     }
+    // ---- epilogue inputs of this workgroup's last tile, loaded now by the last wave
+    //      (RESID: old x and the consumer's norm weight; QKV: RoPE cos / sin), so the
+    //      final epilogue does not wait for them ----
+    constexpr bool PF_EPI = EPI == EPI_RESID || EPI == EPI_QKV;
+    float pf0 = 0.f, pf1 = 1.f;
+    const int nt_last = (int)blockIdx.x + (nmine - 1) * (int)gridDim.x;
+    if (PF_EPI && nmine > 0 && wid == NW - 1) {
+        if (EPI == EPI_RESID) {
+            if (lane < Mc * 16) {
+                const int m = lane >> 4, n = lane & 15;
+                pf0 = a.resid[(size_t)(a.m_base + m) * a.ldr + nt_last * 16 + n];
+                if (a.fo.norm_w) pf1 = a.fo.norm_w[nt_last * 16 + n];
+            }
+        } else {
+            const QkvEpi& e = a.qkv;
+            const int half = e.hd >> 1, row0 = nt_last * 16;
+            if (lane < Mc * 8 && row0 < e.n_heads * e.hd + e.n_kv * e.hd) {
+                const int m = lane >> 3, r = lane & 7, mg = a.m_base + m;
+                const int pos = e.pos0[mg / e.S] + mg % e.S, d1 = 8 * ((row0 % e.hd) >> 4) + r;
+                pf0 = e.rope_cos[(size_t)pos * half + d1];
+                pf1 = e.rope_sin[(size_t)pos * half + d1];
+            }
+        }
+    }
     // ---- 1/rms of each row from the producer's 16-column partial sums ----
     if (tid < 2) {
         cnt_s[tid] = 0u;
@@ -264,6 +289,11 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
         }
         // ---- end of tile tl: partial -> slot, the last wave reduces + epilogue ----
         const int ps = tl & 1;
+        if (PF_EPI && wid == NW - 1 && tl == nmine - 1) {
+            // written before this wave's arrival below (LDS operations of a wave run in order)
+            ep_pf[lane] = pf0;
+            ep_pf[64 + lane] = pf1;
+        }
         while (__hip_atomic_load(&gen_s[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (unsigned)(tl >> 1))
             __builtin_amdgcn_s_sleep(1);
         part_s[ps][wid][lane] = acc;
@@ -304,7 +334,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            run_epilogue<EPI>(a, yt, nt, Mc, a.m_base, lane, 64, true);
+            run_epilogue<EPI>(a, yt, nt, Mc, a.m_base, lane, 64, true, PF_EPI && tl == nmine - 1 ? ep_pf : nullptr);
             if (lane == 0) {
                 __hip_atomic_store(&cnt_s[ps], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 __hip_atomic_fetch_add(&gen_s[ps], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
