@@ -49,6 +49,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 // rand 0.8 StdRng (ChaCha12, rand_chacha 0.3.1) seeded by seed_from_u64
 // (rand_core 0.6.4): keystream word n of sequence seed, evaluated on device.
 // ---------------------------------------------------------------------------
+// Byte offset, inside one 16-row x 128-column weight tile, of byte b of lane l's
+// share (TILE_BYTES / 64 bytes: row l % 16, columns 32 * (l / 16) .. +32 of the
+// group).  The share is cut into 16-byte chunks and chunk q of every lane sits in
+// the q-th KiB of the tile, lanes in order: a 16-byte load per lane reads one
+// contiguous KiB.  INT4 shares are a single chunk.
+__host__ __device__ __forceinline__ int tile_byte(int lane, int b) { return ((b >> 4) << 10) + lane * 16 + (b & 15); }
+
 __device__ __forceinline__ uint32_t rotl32(uint32_t v, int n) { return (v << n) | (v >> (32 - n)); }
 
 __device__ inline void rng_key_from_seed(uint64_t state, uint32_t key[8]) {

@@ -144,14 +144,14 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
             const int mt = min(mb * MC + cc, nchunks - 1);
             lds_dma16(fr, base + cc * 8192 + sub * 1024, lane * 16 + sub * 1024, (mt * G + g) * 8192);
         }
-        // tile jj, piece sub: every lane's sub-th 16 bytes (lane l owns TILE_BYTES / 64
-        // bytes of the tile), so the wave reading piece sub from LDS is conflict-free
+        // tile jj, piece sub: the sub-th KiB of the tile = every lane's sub-th 16-byte
+        // chunk, read contiguously; the wave reading piece sub from LDS is conflict-free
 #pragma unroll
         for (int q = 0; q < C::W_PW; q++) {
             // pieces not a multiple of the waves: the extra loads repeat a piece (same bytes, same place)
             const int pi = (wid * C::W_PW + q) % C::W_PIECES, jj = pi / WP, sub = pi % WP;
             const int nt = min(nb * NT + jj, ntiles - 1);
-            lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * (16 * WP) + sub * 16,
+            lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * 16 + sub * 1024,
                       (int)(((unsigned)nt * G + g) * T::TILE_BYTES));
         }
         if (FMT == WF_INT4)

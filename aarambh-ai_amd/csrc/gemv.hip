@@ -6,9 +6,10 @@
 //
 // Layout: W [N, K] is stored as 16-row x 128-column tiles, tile (nt, g) is a
 // contiguous block (1 KiB INT4, 2 KiB INT8, 4 KiB BF16) in which lane l of a
-// wave owns row l%16, columns 32*(l/16)..+32 of the group: one 16/32/64-byte
-// load per lane, fully coalesced.  INT4 scale and zero (fp16) sit beside the
-// tiles, one u32 per (tile, group, row).
+// wave owns row l%16, columns 32*(l/16)..+32 of the group (16/32/64 bytes), cut
+// into 16-byte chunks: chunk q of all 64 lanes is the q-th KiB of the tile, so
+// each 16-byte load of the wave reads one contiguous KiB (tile_byte()).  INT4
+// scale and zero (fp16) sit beside the tiles, one u32 per (tile, group, row).
 //
 // Work split: one workgroup (4 waves) per 16-row tile and the whole K; wave w
 // takes groups w, w+4, ...  Nothing is exchanged between workgroups: the four
@@ -90,7 +91,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     const int glast = G - 1 - ((G - 1 - wid) % NW + NW) % NW;  // last real group of this wave (may be < 0)
 
     const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
-    const unsigned w_voff = (unsigned)lane * T::LANE_WORDS * 4u;
+    const unsigned w_voff = (unsigned)lane * 16u;
     const unsigned f_voff = (unsigned)(lg * EPB + elane) * 16u;
     const unsigned z_voff = (unsigned)lr * 4u;
     uint32_t wv[PF][T::LANE_WORDS];
@@ -144,7 +145,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
         const int w_soff = (int)(tile * T::TILE_BYTES);
 #pragma unroll
         for (int q = 0; q < T::LANE_WORDS / 4; q++) {
-            const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(w_voff + 16u * q), w_soff, 2));
+            const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)w_voff, w_soff + 1024 * q, 2));
             wv[p][4 * q + 0] = v[0];
             wv[p][4 * q + 1] = v[1];
             wv[p][4 * q + 2] = v[2];

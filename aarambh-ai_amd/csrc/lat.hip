@@ -677,7 +677,7 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
                 const size_t tile = (tile0 + nt) * G + g;
 #pragma unroll
                 for (int q = 0; q < LW / 4; q++) {
-                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + (size_t)lane * LW * 4 + 16 * q);
+                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + tile_byte(lane, 16 * q));
                     wv[j][gi][4 * q] = w4.x;
                     wv[j][gi][4 * q + 1] = w4.y;
                     wv[j][gi][4 * q + 2] = w4.z;
@@ -849,9 +849,9 @@ __global__ void dequant_tiled_kernel(const uint8_t* tiled, const uint32_t* sz, c
         const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
         v = ((float)((c & 1) ? (b >> 4) : (b & 15)) - z) * s;
     } else if (fmt == WF_INT8) {
-        v = (float)(int8_t)tiled[tile * 2048 + 32 * (j * 16 + r) + c] * rscale[n];
+        v = (float)(int8_t)tiled[tile * 2048 + tile_byte(j * 16 + r, c)] * rscale[n];
     } else if (fmt == WF_BF16) {
-        v = bf16_to_f32(((const uint16_t*)tiled)[tile * 2048 + 32 * (j * 16 + r) + c]);
+        v = bf16_to_f32(*(const uint16_t*)(tiled + tile * 4096 + tile_byte(j * 16 + r, 2 * c)));
     } else {
         v = ((const float*)tiled)[i];
     }

@@ -194,7 +194,7 @@ __global__ void quant_int8_kernel(const float* w, int N, int K, uint8_t* tiled, 
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
         int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
         float q = fminf(fmaxf(roundf(src[k] / sc), -127.0f), 127.0f);
-        tiled[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = (uint8_t)(int8_t)q;
+        tiled[((size_t)nt * G + g) * 2048 + tile_byte(j * 16 + r, c)] = (uint8_t)(int8_t)q;
     }
     if (threadIdx.x == 0) rscale[dn] = sc;
 }
@@ -206,7 +206,7 @@ __global__ void quant_bf16_kernel(const float* w, int N, int K, uint8_t* tiled, 
     const int dn = dest_row(n, row_offset, interleave);
     const int nt = dn >> 4, r = dn & 15, G = K >> 7;
     const int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
-    ((uint16_t*)tiled)[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = f32_to_bf16_rne(w[i]);
+    *(uint16_t*)(tiled + ((size_t)nt * G + g) * 4096 + tile_byte(j * 16 + r, 2 * c)) = f32_to_bf16_rne(w[i]);
 }
 
 __global__ void copy_f32_rows_kernel(const float* w, int N, int K, float* dst, int row_offset, int interleave) {
@@ -274,7 +274,7 @@ __global__ void repack_int8_kernel(const int8_t* codes, const float* sc, int N, 
     const int dn = dest_row(n, row_offset, interleave);
     const int nt = dn >> 4, r = dn & 15, G = K >> 7;
     const int g = k >> 7, kk = k & 127, j = kk >> 5, c = kk & 31;
-    tiled[((size_t)nt * G + g) * 2048 + 32 * (j * 16 + r) + c] = (uint8_t)codes[i];
+    tiled[((size_t)nt * G + g) * 2048 + tile_byte(j * 16 + r, c)] = (uint8_t)codes[i];
     if (k == 0) rscale[dn] = sc[n];
 }
 
