@@ -98,10 +98,14 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     uint32_t szv[PF];
     constexpr int NA = REG ? 1 : PF;
     uint4 av[NA][4][EA];  // L2 path: fragment ring
-    // Register path.  MP == 8: one entry per k-step.  MP == 4 uses MFMA rows
-    // 0..7 only, so k-steps 2j and 2j+1 share a register (lanes 0..7 and 8..15
-    // of each 16-lane row); a row_ror:8 move brings the odd one into rows 0..7
-    // and rows 8..15 of the product are never read.
+    // Register path.  MP == 8: one entry per k-step.  MP == 4 needs MFMA rows
+    // 0..7 only, so k-steps 2j and 2j+1 share a register: rows 0..7 (lanes 0..7
+    // of each 16-lane row) hold k-step 2j, rows 8..15 k-step 2j + 1.  The register
+    // is the A operand of both k-steps; even k-steps accumulate into acc[0], whose
+    // product rows 0..7 are right, odd ones into acc[1], whose rows 8..15 are
+    // (rows of a 16x16 product: lanes 0..31 hold 0..7, lanes 32..63 hold 8..15).
+    // The wave's partial takes acc[0] in lanes 0..31 and acc[1] in lanes 32..63;
+    // the epilogue adds product rows r and 8 + r.
     constexpr bool PK = MP == 4;
     constexpr int NREG = PK ? 2 : 4;
     uint4 fa[REG ? NGP : 1][NREG];
@@ -116,17 +120,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     auto unpack_frag = [&](const uint4 (&f)[NREG], uint4 (&o)[4][EA]) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            if (!PK) {
-                o[t][0] = f[t];
-            } else if ((t & 1) == 0) {
-                o[t][0] = f[t >> 1];
-            } else {
-                const uint4 v = f[t >> 1];
-                o[t][0] = make_uint4(__builtin_amdgcn_update_dpp(0u, v.x, 0x128, 0xF, 0xF, false),
-                                     __builtin_amdgcn_update_dpp(0u, v.y, 0x128, 0xF, 0xF, false),
-                                     __builtin_amdgcn_update_dpp(0u, v.z, 0x128, 0xF, 0xF, false),
-                                     __builtin_amdgcn_update_dpp(0u, v.w, 0x128, 0xF, 0xF, false));
-            }
+            o[t][0] = f[PK ? t >> 1 : t];
         }
     };
     auto load_frag = [&](uint4 (&f)[4][EA], int g) {
@@ -154,8 +148,10 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
         if (FMT == WF_INT4) szv[p] = __builtin_amdgcn_raw_buffer_load_b32(zr, (int)z_voff, (int)(tile * 64u), 0);
         if constexpr (!REG) load_frag(av[p], g);
     };
-    // one item: weights of ring slot p times fragment entries f, added to acc
-    auto mma_item = [&](float4_t& acc, int p, const uint4 (&f)[4][EA]) {
+    // one item: weights of ring slot p times fragment entries f, added to acc[0]
+    // (register-packed MP 4: even k-steps to acc[0], odd ones to acc[1])
+    constexpr bool PKR = REG && PK;
+    auto mma_item = [&](float4_t (&acc)[2], int p, const uint4 (&f)[4][EA]) {
         if (FMT == WF_INT4) {
             const uint32_t szw = szv[p];
             const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(szw & 0xFFFFu));
@@ -170,14 +166,20 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
                     g4[(t + e) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, f[t][e]), b,
                                                                              g4[(t + e) & 1], 0, 0, 0);
             }
-            acc += sc * (g4[0] + g4[1]);
+            if (PKR) {
+                acc[0] += sc * g4[0];
+                acc[1] += sc * g4[1];
+            } else {
+                acc[0] += sc * (g4[0] + g4[1]);
+            }
         } else if (FMT == WF_INT8) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const half8_t b = int8_b_operand(wv[p][2 * t], wv[p][2 * t + 1]);
 #pragma unroll
                 for (int e = 0; e < EA; e++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, f[t][e]), b, acc, 0, 0, 0);
+                    acc[PKR ? t & 1 : 0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8_t, f[t][e]), b, acc[PKR ? t & 1 : 0], 0, 0, 0);
             }
         } else {
 #pragma unroll
@@ -186,7 +188,8 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
                 const bf16x8_t b = __builtin_bit_cast(bf16x8_t, w4);
 #pragma unroll
                 for (int e = 0; e < EA; e++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, f[t][e]), b, acc, 0, 0, 0);
+                    acc[PKR ? t & 1 : 0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, f[t][e]), b, acc[PKR ? t & 1 : 0], 0, 0, 0);
             }
         }
     };
@@ -223,12 +226,32 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             }
         }
     }
-    // ---- 1/rms of each row from the producer's 16-column partial sums ----
+    // ---- RMSNorm: 1/rms of each row from the producer's 16-column partial sums.
+    //      Only the epilogues need it, so wave w loads the partials of row w (and
+    //      w + NW) now and reduces them at the end of its first tile: no wait on the
+    //      weight loads issued above.  Buffer loads past the row's K / 16 partials
+    //      (or with no row) read 0. ----
+    constexpr int SQL = 4;                  // partials per lane held in registers
+    constexpr int SQR = MP > 8 ? 2 : 1;     // rows per wave (Mc <= NW * SQR)
+    const int nq = a.K >> 4;
+    const bool ss_late = a.norm_w && !a.hidden_out && nq <= 64 * SQL;
+    float ssr[SQR][SQL];
+#pragma unroll
+    for (int j = 0; j < SQR; j++) {
+        const int m = wid + NW * j;
+        const bool has = ss_late && m < Mc;
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(has ? a.ssq_in + (size_t)(a.m_base + m) * a.ssq_ld : a.x), (short)0, has ? nq * 4 : 0,
+            0x00020000);
+#pragma unroll
+        for (int i = 0; i < SQL; i++)
+            ssr[j][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, (lane + 64 * i) * 4, 0, 0));
+    }
     if (tid < 2) {
         cnt_s[tid] = 0u;
         gen_s[tid] = 0u;
     }
-    if (a.norm_w) {
+    if (a.norm_w && !ss_late) {
         for (int m = wid; m < Mc; m += NW) {
             float ss = 0.f;
             for (int q = lane; q < (a.K >> 4); q += 64) ss += a.ssq_in[(size_t)(a.m_base + m) * a.ssq_ld + q];
@@ -259,7 +282,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
     if (nmine <= 0) return;
 
     for (int tl = 0; tl < nmine; tl++) {
-        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        float4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         if constexpr (REG) {
             const int ntl = min(tl + 1, nmine - 1);
 #pragma unroll
@@ -289,6 +312,22 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
             }
         }
         // ---- end of tile tl: partial -> slot, the last wave reduces + epilogue ----
+        if (ss_late && tl == 0) {
+            // written before this wave's first arrival (LDS operations of a wave run in order)
+#pragma unroll
+            for (int j = 0; j < SQR; j++) {
+                float ss = 0.f;
+#pragma unroll
+                for (int i = 0; i < SQL; i++) {
+                    asm volatile("" : "+v"(ssr[j][i]));  // keeps the sum here, not before the loop
+                    ss += ssr[j][i];
+                }
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+                const int m = wid + NW * j;
+                if (lane == 0 && m < Mc) s_inv[m] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+            }
+        }
         const int ps = tl & 1;
         if (PF_EPI && wid == NW - 1 && tl == nmine - 1) {
             // written before this wave's arrival below (LDS operations of a wave run in order)
@@ -297,7 +336,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
         }
         while (__hip_atomic_load(&gen_s[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (unsigned)(tl >> 1))
             __builtin_amdgcn_s_sleep(1);
-        part_s[ps][wid][lane] = acc;
+        part_s[ps][wid][lane] = PKR && lane >= 32 ? acc[1] : acc[0];
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(&cnt_s[ps], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
         old = __shfl(old, 0, 64);
@@ -319,6 +358,7 @@ __global__ void __launch_bounds__(GT_NW * 64) gemv_tile_kernel(GemvArgs a) {
                 y[q] = 0.f;
                 if (m < Mc) {
                     float v = RS ? yt[m][n] + yt[MP + m][n] : yt[m][n];
+                    if (PKR) v += yt[8 + m][n] + yt[8 + MP + m][n];
                     if (a.norm_w) v *= s_inv[m];
                     if (FMT == WF_INT8) v *= a.rscale[nt * 16 + n];
                     y[q] = v;
@@ -427,12 +467,9 @@ static int launch_tile(const GemvArgs& a, hipStream_t stream) {
                                                            GT_NW * 64, 0);
         grid_cap = std::max(1, cus) * std::max(1, per_cu);
     }
-    // Tiles spread evenly over the workgroups (no partial last round).  BF16 items are
-    // 4 KiB per wave, so half the resident workgroups keep as many bytes in flight as
-    // INT4 at full residency; more measured slower (memory queues fill up).
+    // Tiles spread evenly over the resident workgroups (no partial last round).
     const int ntiles = a.N / 16;
-    const int cap = FMT == WF_BF16 ? std::max(1, grid_cap / 2) : grid_cap;
-    const int per_wg = (ntiles + cap - 1) / cap;
+    const int per_wg = (ntiles + grid_cap - 1) / grid_cap;
     const int grid = (ntiles + per_wg - 1) / per_wg;
     (void)hipGetLastError();
     launch_timed(gemv_tile_kernel<FMT, MP, EPI, NGP>, dim3(grid), dim3(GT_NW * 64), 0, stream, a);
