@@ -44,7 +44,9 @@ def int4_matrix_bytes(n, k):
 
 
 def verify_alg_bytes(B, ctx=CTX):
-    """Algorithmic HBM bytes of one K-row verify step at batch B."""
+    """Algorithmic HBM bytes of one K-row verify step at batch B: every weight byte
+    once (quantised, with scales), the LM head once, and per sequence the K / V
+    cache bytes of the context at every layer."""
     H, F, V, L = C4["hidden_dim"], C4["ffn_dim"], C4["vocab_size"], C4["n_layers"]
     hd = H // C4["n_heads"]
     QD, KD = C4["n_heads"] * hd, C4["n_kv_heads"] * hd
@@ -317,8 +319,9 @@ def main():
                           "launches": 5}))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one MI355X; the verify path shards by independent "
-              "sequences (see DESIGN.md) and no multi-GPU figure is produced.", file=sys.stderr)
+        print("bench.py: this build measures one MI355X; the verify path would shard by "
+              "independent sequences (one engine per GPU, no collectives on the hot path) and "
+              "no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
     args.batches = [int(x) for x in args.batches.split(",")]
     if args.workload == "c5":
