@@ -75,7 +75,22 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     int bid = blockIdx.x;
     const int s = bid % S;
     bid /= S;
-    const int nb = bid % NB, mb = bid / NB;
+    // (N-block, M-block): the M-blocks of one N-block sit 8 workgroups apart in launch
+    // order (workgroups go round-robin to the 8 XCDs), so they run on one XCD at
+    // about the same time and share its L2 for their common weight tiles.  N-blocks
+    // in whole groups of 8 first, the remainder in order.
+    const int MBK = (int)gridDim.x / (NB * S);
+    const int full = NB / 8 * 8;
+    int nb, mb;
+    if (bid < full * MBK) {
+        const int r = bid % (8 * MBK);
+        mb = r / 8;
+        nb = bid / (8 * MBK) * 8 + r % 8;
+    } else {
+        const int r = bid - full * MBK, w = NB - full;
+        mb = r / w;
+        nb = full + r % w;
+    }
     const int g0 = s * gps, ng = min(G, g0 + gps) - g0;
 
     // 1/rms of the block's rows from the producer's 16-column partial sums (same
