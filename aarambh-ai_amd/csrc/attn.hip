@@ -642,34 +642,43 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     }
     if (!arrive_last(&a.counters[grp], (unsigned)a.nchunks, &s_last)) return;
 
-    // ---- last workgroup: merge the chunks in chunk order ----
-    const int C = a.nchunks;
-    float* sm = &mg_o[0][0][0];  // [C][16] chunk maxima, then [C][16] sums
-    float* sls = sm + AM_MAXCH * AM_ROWS;
-    for (int i = tid; i < C * AM_ROWS; i += 512) {
-        if ((i & 15) < R) {
-            const float4_t v = ld4_coh(prs, (unsigned)(i * AM_REC) * 4u);
-            sm[i] = v[0];
-            sls[i] = v[1];
-        }
-    }
-    __syncthreads();
+    // ---- last workgroup: merge the chunks in chunk order.  Each thread loads its
+    //      row's (max, sum) and its 4 dims of up to MB chunks at once (one round
+    //      trip; loads past the last chunk re-read it and are not used), then
+    //      merges them in registers; more chunks go in further batches with a
+    //      running maximum. ----
     if (r >= R) return;
-    float4_t ov[AM_MAXCH / 4];
+    constexpr int MB = 20;
+    const int C = a.nchunks;
     float4_t tot = {0.f, 0.f, 0.f, 0.f};
-    float Mc = -INFINITY;
-    for (int c = 0; c < C; c++) Mc = fmaxf(Mc, sm[c * AM_ROWS + r]);
-    float Lc = 0.f;
-    for (int c0 = 0; c0 < C; c0 += AM_MAXCH / 4) {
+    float Mc = -INFINITY, Lc = 0.f;
+    for (int c0 = 0; c0 < C; c0 += MB) {
+        float ml[MB][2];
+        float4_t ov[MB];
 #pragma unroll
-        for (int u = 0; u < AM_MAXCH / 4; u++)
-            if (c0 + u < C) ov[u] = ld4_coh(prs, (unsigned)(((c0 + u) * AM_ROWS + r) * AM_REC + 4 + 4 * q) * 4u);
+        for (int u = 0; u < MB; u++) {
+            const unsigned rec = (unsigned)((min(c0 + u, C - 1) * AM_ROWS + r) * AM_REC) * 4u;
+            const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(prs, (int)rec, 0, 16));
+            ml[u][0] = __builtin_bit_cast(float, v[0]);
+            ml[u][1] = __builtin_bit_cast(float, v[1]);
+            ov[u] = ld4_coh(prs, rec + 16u + 16u * q);
+        }
+        float Mb = Mc;
 #pragma unroll
-        for (int u = 0; u < AM_MAXCH / 4; u++)
+        for (int u = 0; u < MB; u++)
+            if (c0 + u < C) Mb = fmaxf(Mb, ml[u][0]);
+        if (c0 > 0 && Mc != Mb) {
+            const float w = Mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mc - Mb);
+            Lc *= w;
+            tot *= w;
+        }
+        Mc = Mb;
+#pragma unroll
+        for (int u = 0; u < MB; u++)
             if (c0 + u < C) {
-                const float mc = sm[(c0 + u) * AM_ROWS + r];
+                const float mc = ml[u][0];
                 const float w = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - Mc);
-                Lc += sls[(c0 + u) * AM_ROWS + r] * w;
+                Lc += ml[u][1] * w;
                 tot += ov[u] * w;
             }
     }
