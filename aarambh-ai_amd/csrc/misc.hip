@@ -43,7 +43,7 @@ __device__ inline float block_sum(float v, float* red) {
 // squares over 128-column groups for the first RMSNorm.
 // Fragments + 16-column sums of squares of row m of an activation matrix whose
 // f32 values are already in `row` (one workgroup per row).
-__device__ void emit_row_fragments(const XFrag& fo, const float* row, int m, int H) {
+__device__ __forceinline__ void emit_row_fragments(const XFrag& fo, const float* row, int m, int H) {
     if (!fo.buf) return;
     for (int k = threadIdx.x; k < H; k += blockDim.x) frag_put(fo, m, k, row[k]);
     if (fo.ssq)
@@ -55,18 +55,51 @@ __device__ void emit_row_fragments(const XFrag& fo, const float* row, int m, int
         }
 }
 
+// The row kernels below keep their row in LDS (dynamic, H floats) for the
+// fragment / sum-of-squares pass, so it is not re-read from global memory after
+// its stores; the barrier before that pass waits for LDS only.
+static constexpr int ROW_LDS_MAX = 16384;  // floats of one row held in LDS (64 KiB)
+static constexpr int ROW_U = 8;            // loads a thread issues before the first store
+
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __global__ void embed_kernel(const void* table, int fmt, int H, const uint32_t* ids, float* x, XFrag fo) {
+    extern __shared__ float rowbuf[];
     const int m = blockIdx.x;
     const size_t base = (size_t)ids[m] * H;
-    for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)m * H + k] = load_table(table, fmt, base + k);
-    __syncthreads();
-    emit_row_fragments(fo, x + (size_t)m * H, m, H);
+    // ROW_U loads in flight per thread before their stores (the stores to x could
+    // alias the table as far as the compiler knows, so it would not reorder them)
+    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
+        float v[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            v[u] = k < H ? load_table(table, fmt, base + k) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < H) {
+                x[(size_t)m * H + k] = v[u];
+                rowbuf[k] = v[u];
+            }
+        }
+    }
+    lds_barrier();
+    emit_row_fragments(fo, rowbuf, m, H);
 }
 
 int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, int M, float* x, const XFrag& fo,
                  hipStream_t stream) {
+    if (H > ROW_LDS_MAX) return 2;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), 0, stream, table, table_fmt, H, ids, x, fo);
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream, table,
+                       table_fmt, H, ids, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -75,52 +108,92 @@ int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, i
 __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, const void* table, int fmt,
                                 const uint32_t* ids, int ids_stride, int L, int H, const float* trunk_w,
                                 const float* token_w, float eps, float* x, XFrag fo) {
+    extern __shared__ float rowbuf[];
     __shared__ float red[MT_THREADS / 64];
     const int row = blockIdx.x;
     const int seq = row / L, l = row % L;
     float* out = x + (size_t)row * H;
     const float* w = l == 0 ? trunk_w : token_w;
-    for (int k = threadIdx.x; k < H; k += blockDim.x)
-        out[k] = l == 0 ? anchor[(size_t)seq * anchor_stride + k]
-                        : load_table(table, fmt, (size_t)ids[(size_t)seq * ids_stride + l - 1] * H + k);
-    __syncthreads();
     float ss = 0.f;
-    for (int k = threadIdx.x; k < H; k += blockDim.x) ss += out[k] * out[k];
+    const size_t tbase = l == 0 ? 0 : (size_t)ids[(size_t)seq * ids_stride + l - 1] * H;
+    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
+        float v[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            v[u] = k >= H ? 0.f : l == 0 ? anchor[(size_t)seq * anchor_stride + k] : load_table(table, fmt, tbase + k);
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < H) {
+                rowbuf[k] = v[u];
+                ss += v[u] * v[u];
+            }
+        }
+    }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    __syncthreads();
-    for (int k = threadIdx.x; k < H; k += blockDim.x) out[k] = out[k] * inv * w[k];
-    __syncthreads();
-    emit_row_fragments(fo, out, row, H);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) {
+        const float o = rowbuf[k] * inv * w[k];
+        out[k] = o;
+        rowbuf[k] = o;
+    }
+    lds_barrier();
+    emit_row_fragments(fo, rowbuf, row, H);
 }
 
 int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* table, int table_fmt,
                     const uint32_t* ids, int ids_stride, int nseq, int L, int H, const float* trunk_w,
                     const float* token_w, float eps, float* x, const XFrag& fo, hipStream_t stream) {
+    if (H > ROW_LDS_MAX) return 2;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(MT_THREADS), 0, stream, anchor, anchor_stride,
+    hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream,
+                       anchor, anchor_stride,
                        table, table_fmt, ids, ids_stride, L, H, trunk_w, token_w, eps, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
 // RMSNorm of selected rows (nn/src/norm.rs:17-19), plus fragments of the result.
 __global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float* w, float eps, float* out, XFrag fo) {
+    extern __shared__ float rowbuf[];
     __shared__ float red[MT_THREADS / 64];
     const int m = blockIdx.x;
     const float* r = x + row_off(xmap, m);
     float ss = 0.f;
-    for (int k = threadIdx.x; k < H; k += blockDim.x) ss += r[k] * r[k];
+    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
+        float v[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            v[u] = k < H ? r[k] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < H) {
+                rowbuf[k] = v[u];
+                ss += v[u] * v[u];
+            }
+        }
+    }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k = threadIdx.x; k < H; k += blockDim.x) out[(size_t)m * H + k] = r[k] * inv * w[k];
-    __syncthreads();
-    emit_row_fragments(fo, out + (size_t)m * H, m, H);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) {
+        const float o = rowbuf[k] * inv * w[k];
+        out[(size_t)m * H + k] = o;
+        rowbuf[k] = o;
+    }
+    lds_barrier();
+    emit_row_fragments(fo, rowbuf, m, H);
 }
 
 int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, float eps, float* out,
                      const XFrag& fo, hipStream_t stream) {
+    if (H > ROW_LDS_MAX) return 2;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), 0, stream, x, xmap, H, w, eps, out, fo);
+    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream, x, xmap,
+                       H, w, eps, out, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -386,11 +459,24 @@ __global__ void argmax_rows_kernel(const float* x, long long ld, int V, int32_t*
     const float* row = x + (size_t)blockIdx.x * ld;
     int bk = INT_MIN, bi = 0;
     float t1 = -INFINITY, t2 = -INFINITY;
-    for (int j = threadIdx.x; j < V; j += blockDim.x) {
-        float v = row[j];
-        int k = total_key(v);
-        if (k >= bk) { bk = k; bi = j; }
-        if (v > t1) { t2 = t1; t1 = v; } else if (v > t2) { t2 = v; }
+    // ROW_U loads in flight per thread, then consumed in index order
+    for (int j0 = threadIdx.x; j0 < V; j0 += ROW_U * blockDim.x) {
+        float vv[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int j = j0 + u * blockDim.x;
+            vv[u] = j < V ? row[j] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int j = j0 + u * blockDim.x;
+            if (j < V) {
+                const float v = vv[u];
+                const int k = total_key(v);
+                if (k >= bk) { bk = k; bi = j; }
+                if (v > t1) { t2 = t1; t1 = v; } else if (v > t2) { t2 = v; }
+            }
+        }
     }
     for (int d = 32; d >= 1; d >>= 1) {
         int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
@@ -428,7 +514,19 @@ int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* o
 __global__ void copy_rows_kernel(const float* const* src, float* const* dst, int n) {
     const float* s = src[blockIdx.x];
     float* d = dst[blockIdx.x];
-    for (int k = threadIdx.x; k < n; k += blockDim.x) d[k] = s[k];
+    for (int k0 = threadIdx.x; k0 < n; k0 += ROW_U * blockDim.x) {
+        float v[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            v[u] = k < n ? s[k] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < n) d[k] = v[u];
+        }
+    }
 }
 
 int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream) {
