@@ -23,6 +23,7 @@
 namespace aarh {
 
 static constexpr int ACC_THREADS = 512;
+static constexpr int ACC_U = 8;  // logit loads a thread issues before consuming them
 
 struct RowView {
     const float* p;
@@ -66,9 +67,22 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     if (needed) {
         if (a.greedy) {
             int bk = INT_MIN, bi = 0;
-            for (int j = tid; j < V; j += ACC_THREADS) {
-                int k = total_key(row[j]);
-                if (k >= bk) { bk = k; bi = j; }
+            // ACC_U loads in flight per thread, consumed in index order
+            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+                float vv[ACC_U];
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    vv[u] = j < V ? row[j] : 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    if (j < V) {
+                        const int k = total_key(vv[u]);
+                        if (k >= bk) { bk = k; bi = j; }
+                    }
+                }
             }
             for (int d = 32; d >= 1; d >>= 1) {
                 int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
@@ -85,9 +99,21 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
         } else {
             const float T = a.temperature;
             float mx = -INFINITY;
-            for (int j = tid; j < V; j += ACC_THREADS) {
-                float m = row[j] / T;
-                if (isfinite(m)) mx = fmaxf(mx, m);
+            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+                float vv[ACC_U];
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    vv[u] = j < V ? row[j] : 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    if (j < V) {
+                        const float m = vv[u] / T;
+                        if (isfinite(m)) mx = fmaxf(mx, m);
+                    }
+                }
             }
             mx = wave_max_f32(mx);
             if (lane == 0) red_f[wid] = mx;
@@ -99,9 +125,21 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
             }
             __syncthreads();
             mx = sh_bcast[0];
-            for (int j = tid; j < V; j += ACC_THREADS) {
-                float m = row[j] / T;
-                lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
+            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+                float vv[ACC_U];
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    vv[u] = j < V ? row[j] : 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < ACC_U; u++) {
+                    const int j = j0 + u * ACC_THREADS;
+                    if (j < V) {
+                        const float m = vv[u] / T;
+                        lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
+                    }
+                }
             }
             __syncthreads();
             if (wid == 0) {
@@ -279,9 +317,21 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     if (a.greedy) {
         // argmax, last index on ties (sampler.rs:211-215 / argmax)
         int bk = INT_MIN, bi = 0;
-        for (int j = tid; j < V; j += ACC_THREADS) {
-            const int k = total_key(row[j]);
-            if (k >= bk) { bk = k; bi = j; }
+        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+            float vv[ACC_U];
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                vv[u] = j < V ? row[j] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                if (j < V) {
+                    const int k = total_key(vv[u]);
+                    if (k >= bk) { bk = k; bi = j; }
+                }
+            }
         }
         for (int d = 32; d >= 1; d >>= 1) {
             const int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
@@ -300,9 +350,21 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     } else {
         const float T = a.temperature;
         float mx = -INFINITY;
-        for (int j = tid; j < V; j += ACC_THREADS) {
-            const float m = row[j] / T;
-            if (isfinite(m)) mx = fmaxf(mx, m);
+        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+            float vv[ACC_U];
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                vv[u] = j < V ? row[j] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                if (j < V) {
+                    const float m = vv[u] / T;
+                    if (isfinite(m)) mx = fmaxf(mx, m);
+                }
+            }
         }
         mx = wave_max_f32(mx);
         if (lane == 0) red_f[wid] = mx;
@@ -314,9 +376,21 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
         }
         __syncthreads();
         mx = sh[0];
-        for (int j = tid; j < V; j += ACC_THREADS) {
-            const float m = row[j] / T;
-            lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
+        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+            float vv[ACC_U];
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                vv[u] = j < V ? row[j] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < ACC_U; u++) {
+                const int j = j0 + u * ACC_THREADS;
+                if (j < V) {
+                    const float m = vv[u] / T;
+                    lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
+                }
+            }
         }
         __syncthreads();
         if (wid == 0) {
