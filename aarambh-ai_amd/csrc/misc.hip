@@ -134,10 +134,22 @@ __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, co
     }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k = threadIdx.x; k < H; k += blockDim.x) {
-        const float o = rowbuf[k] * inv * w[k];
-        out[k] = o;
-        rowbuf[k] = o;
+    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
+        float wv[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            wv[u] = k < H ? w[k] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < H) {
+                const float o = rowbuf[k] * inv * wv[u];
+                out[k] = o;
+                rowbuf[k] = o;
+            }
+        }
     }
     lds_barrier();
     emit_row_fragments(fo, rowbuf, row, H);
@@ -179,10 +191,22 @@ __global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float
     }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k = threadIdx.x; k < H; k += blockDim.x) {
-        const float o = rowbuf[k] * inv * w[k];
-        out[(size_t)m * H + k] = o;
-        rowbuf[k] = o;
+    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
+        float wv[ROW_U];
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            wv[u] = k < H ? w[k] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ROW_U; u++) {
+            const int k = k0 + u * blockDim.x;
+            if (k < H) {
+                const float o = rowbuf[k] * inv * wv[u];
+                out[(size_t)m * H + k] = o;
+                rowbuf[k] = o;
+            }
+        }
     }
     lds_barrier();
     emit_row_fragments(fo, rowbuf, m, H);
