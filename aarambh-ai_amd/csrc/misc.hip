@@ -72,6 +72,41 @@ __global__ void embed_kernel(const void* table, int fmt, int H, const uint32_t* 
     extern __shared__ float rowbuf[];
     const int m = blockIdx.x;
     const size_t base = (size_t)ids[m] * H;
+    if (fmt == WF_BF16 && (H & 7) == 0) {
+        // 16-byte loads of 8 bf16 values (the row starts 16-byte aligned)
+        const int nc = H >> 3;
+        const uint4* src = (const uint4*)((const uint16_t*)table + base);
+        for (int c0 = threadIdx.x; c0 < nc; c0 += ROW_U * blockDim.x) {
+            uint4 v[ROW_U];
+#pragma unroll
+            for (int u = 0; u < ROW_U; u++) {
+                const int c = c0 + u * blockDim.x;
+                v[u] = c < nc ? src[c] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < ROW_U; u++) {
+                const int c = c0 + u * blockDim.x;
+                if (c < nc) {
+                    const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                    float f[8];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        f[2 * j] = __uint_as_float(w[j] << 16);
+                        f[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+                    }
+                    const float4 lo = make_float4(f[0], f[1], f[2], f[3]), hi = make_float4(f[4], f[5], f[6], f[7]);
+                    float4* xo = (float4*)(x + (size_t)m * H + 8 * c);
+                    xo[0] = lo;
+                    xo[1] = hi;
+                    ((float4*)(rowbuf + 8 * c))[0] = lo;
+                    ((float4*)(rowbuf + 8 * c))[1] = hi;
+                }
+            }
+        }
+        lds_barrier();
+        emit_row_fragments(fo, rowbuf, m, H);
+        return;
+    }
     // ROW_U loads in flight per thread before their stores (the stores to x could
     // alias the table as far as the compiler knows, so it would not reorder them)
     for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
