@@ -28,7 +28,7 @@ LIB_PATH = os.path.join(_HERE, "libaarambh_hip.so")
 W_F32, W_BF16, W_INT8_ROW, W_INT4_G128 = 0, 1, 2, 3
 KV_F32, KV_F16, KV_INT8 = 0, 1, 2
 T_NORM, T_LINEAR, T_EMBED = 0, 1, 2
-FLAG_RATIO_NEAR, FLAG_CDF_NEAR = 1, 2
+FLAG_RATIO_NEAR, FLAG_CDF_NEAR, FLAG_TOPP_NEAR = 1, 2, 8
 TOP_CANDIDATES = 5  # engine.rs:70
 PROF_NAMES = ["gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down", "gemv_lmhead", "attention", "accept", "other"]
 
@@ -127,6 +127,8 @@ def lib():
         "aarh_spec_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
                                          _P, _P, _P, C.POINTER(_Stats), _P, _P]),
         "aarh_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
+        "aarh_session_rng_offsets": (C.c_int, [_P, _P]),
+        "aarh_session_set_rng_offsets": (C.c_int, [_P, _P]),
         "aarh_top_candidates": (C.c_int, [_P, _P, C.c_int, C.c_int, C.POINTER(_Sampler), C.c_int, _P, _P, _P]),
         "aarh_set_graphs": (C.c_int, [_P, C.c_int]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
@@ -164,7 +166,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_forward", "aarh_last_logits_device", "aarh_last_hidden_device", "aarh_mtp_head",
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
-            "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs",
+            "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs", "aarh_session_rng_offsets",
+            "aarh_session_set_rng_offsets",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -199,7 +202,8 @@ class ModelConfig:
 
 @dataclass
 class Sampler:
-    """inference/src/sampler.rs:14-65 (device path: no top-k / top-p)."""
+    """inference/src/sampler.rs:14-65: Greedy, or TopKTopP with temperature, optional
+    top_k (0: none) and top_p (outside (0, 1): none) and the StdRng seed."""
     greedy: bool = True
     temperature: float = 1.0
     top_k: int = 0
@@ -552,6 +556,16 @@ class Session:
             res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st,
                                         _candidate_lists(ci[b, :ln[b]], cp[b, :ln[b]])))
         return res
+
+    def rng_offsets(self):
+        """Keystream word position of each request's sampler (the next uniform it draws)."""
+        out = np.zeros(self.nseq, np.uint64)
+        self.engine.model._check(lib().aarh_session_rng_offsets(self.h, _ptr(out)))
+        return out
+
+    def set_rng_offsets(self, offsets):
+        o = np.ascontiguousarray(offsets, np.uint64)
+        self.engine.model._check(lib().aarh_session_set_rng_offsets(self.h, _ptr(o)))
 
     def close(self):
         if getattr(self, "h", None):

@@ -1,21 +1,26 @@
 // Fused acceptance sampling for speculative verification on gfx950.
 //
 // Restates, per sequence, the host-side acceptance round of the reference:
-//   probabilities     inference/src/sampler.rs:102-118, 226-312
+//   probabilities     inference/src/sampler.rs:102-118, 226-312 (temperature,
+//                     top-k, top-p, softmax, renormalise)
 //   accept_proposal   inference/src/speculative.rs:755-768
 //   residual          inference/src/speculative.rs:770-793
 //   sample            inference/src/sampler.rs:142-152, 314-347
 // and the round structure of speculative.rs:343-501 (external draft, bonus
 // sample) and mtp_speculative.rs:228-315 (MTP, no bonus).
 //
-// One workgroup per logits row computes the row's softmax max and the EXACT
-// sequential f32 normaliser (seq_sum_wave), then the last workgroup of each
-// sequence to finish resolves the proposals in order, draws ChaCha12 uniforms
-// at the sequence's keystream offset, and on rejection builds the residual
-// max(0, p - q) in LDS, normalises it with the exact sequential sum and walks
-// the exact sequential CDF.  Logits are read once from HBM per row (the
-// rejected position's two rows are read a second time).
+// Stage 1: one workgroup per logits row turns the row into the parameters of
+// its sampling distribution (the temperature max, the EXACT sequential f32
+// normaliser, the top-k and top-p cut keys and the top-p renormaliser), from
+// which any probability is recomputed bit for bit as the reference computes it.
+// Stage 2: the last workgroup of each sequence to finish resolves the proposals
+// in order, draws ChaCha12 uniforms at the sequence's keystream offset, and on
+// rejection walks the residual max(0, p - q): its exact sequential mass, then
+// its exact sequential CDF.  Rows longer than one LDS chunk are scanned chunk by
+// chunk with the running sum carried over, so the vocabulary size is unbounded.
 #include <float.h>
+
+#include <mutex>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -23,29 +28,458 @@
 namespace aarh {
 
 static constexpr int ACC_THREADS = 512;
-static constexpr int ACC_U = 8;  // logit loads a thread issues before consuming them
+static constexpr int ACC_WAVES = ACC_THREADS / WAVE;
+static constexpr int ACC_U = 8;              // logit loads a thread issues before consuming them
+static constexpr int ACC_CHUNK = 32768;      // floats of a row staged in LDS per scan step (128 KiB)
+static constexpr int CAND_CHUNK = 24576;     // the same for the candidate kernel (its key lists use 20 KiB)
+static constexpr int TOPP_PAGE = 4096;       // top-p candidates sorted per page (64-bit keys)
+static constexpr int TOPP_LDS_FLOATS = TOPP_PAGE * 3;  // page keys (8 B) + their probabilities (4 B)
 
-struct RowView {
-    const float* p;
-    float mx;
-    float S;
-};
-
-// Probability of element j under row r: fl(expf(fl(l/T) - max) / S).
-__device__ __forceinline__ float row_prob(const float* lg, int j, float invT_unused, float T, float mx, float S) {
-    float m = lg[j] / T;
-    if (!isfinite(m)) return 0.0f;
-    return expf_rn(m - mx) / S;
+// ---------------------------------------------------------------------------
+// Sampling-distribution parameters of one row (filtered_probs, sampler.rs:226-278)
+// ---------------------------------------------------------------------------
+// Ranking keys: slice::sort_by(total_cmp) descending is stable, so equal values
+// keep ascending index order; (value key << 32 | ~index) orders both at once and
+// is unique per element.
+__device__ __forceinline__ uint64_t logit_key(float l, int j) {
+    return ((uint64_t)((uint32_t)total_key(l) ^ 0x80000000u) << 32) | (uint32_t)(~(uint32_t)j);
+}
+__device__ __forceinline__ uint64_t prob_key(float p, int j) {
+    return ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(~(uint32_t)j);
 }
 
+struct RowFilt {
+    float T;        // temperature
+    float mx;       // max of the finite l / T among the top-k
+    float S;        // sequential sum of exp(l / T - mx) (softmax normaliser)
+    float R2;       // top-p renormaliser (sum of the kept probabilities)
+    uint64_t kkey;  // top-k: logits with logit_key >= kkey are kept (0: all)
+    uint64_t pkey;  // top-p: probabilities with prob_key >= pkey are kept (0: all)
+    int topp;       // top-p applies
+};
+
+// exp(l / T - mx) of element j (0 when top-k drops it or l / T is not finite):
+// softmax of the masked logits, sampler.rs:280-299 with temperature 1 after the
+// division of :254-265.
+__device__ __forceinline__ float filt_exp(const RowFilt& f, float l, int j) {
+    if (logit_key(l, j) < f.kkey) return 0.0f;
+    const float m = l / f.T;
+    if (!isfinite(m)) return 0.0f;
+    return expf_rn(m - f.mx);
+}
+// The probability filtered_probs returns for element j.
+__device__ __forceinline__ float filt_prob(const RowFilt& f, float l, int j) {
+    const float p0 = filt_exp(f, l, j) / f.S;
+    if (!f.topp) return p0;
+    if (!(p0 > 0.0f) || prob_key(p0, j) < f.pkey) return 0.0f;
+    return p0 / f.R2;
+}
+
+// Row statistics handed from stage 1 to the resolving workgroup (ACC_RS_WORDS words per row).
+enum { RS_MX = 0, RS_S = 1, RS_R2 = 2, RS_ARGMAX = 3, RS_KKEY = 4, RS_PKEY = 6, RS_FLAGS = 8, RS_STATUS = 9,
+       RS_TOPP = 10 };
+
+__device__ __forceinline__ void rs_put(uint32_t* w, int f, uint32_t v) {
+    __hip_atomic_store(w + f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t rs_get(const uint32_t* w, int f) {
+    return __hip_atomic_load(const_cast<uint32_t*>(w) + f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void rs_store(uint32_t* w, const RowFilt& f, uint32_t flags, int status) {
+    rs_put(w, RS_MX, __float_as_uint(f.mx));
+    rs_put(w, RS_S, __float_as_uint(f.S));
+    rs_put(w, RS_R2, __float_as_uint(f.R2));
+    rs_put(w, RS_KKEY, (uint32_t)f.kkey);
+    rs_put(w, RS_KKEY + 1, (uint32_t)(f.kkey >> 32));
+    rs_put(w, RS_PKEY, (uint32_t)f.pkey);
+    rs_put(w, RS_PKEY + 1, (uint32_t)(f.pkey >> 32));
+    rs_put(w, RS_FLAGS, flags);
+    rs_put(w, RS_STATUS, (uint32_t)status);
+    rs_put(w, RS_TOPP, (uint32_t)f.topp);
+}
+__device__ inline RowFilt rs_load(const uint32_t* w, float T) {
+    RowFilt f;
+    f.T = T;
+    f.mx = __uint_as_float(rs_get(w, RS_MX));
+    f.S = __uint_as_float(rs_get(w, RS_S));
+    f.R2 = __uint_as_float(rs_get(w, RS_R2));
+    f.kkey = (uint64_t)rs_get(w, RS_KKEY) | ((uint64_t)rs_get(w, RS_KKEY + 1) << 32);
+    f.pkey = (uint64_t)rs_get(w, RS_PKEY) | ((uint64_t)rs_get(w, RS_PKEY + 1) << 32);
+    f.topp = (int)rs_get(w, RS_TOPP);
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup primitives
+// ---------------------------------------------------------------------------
+struct SelShared {
+    unsigned hist[256];
+    unsigned long long key;
+    int digit, kk;
+    unsigned cnt, total;
+};
+
+struct AccShared {
+    SelShared sel;
+    SeqScan scan;
+    float red_f[ACC_WAVES];
+    int red_k[ACC_WAVES], red_i[ACC_WAVES];
+    unsigned n;
+    unsigned is_last;
+    float fb[4];
+    int ib[8];
+};
+
+// hist[d] += number of lanes holding digit d (d < 0: none).  Lanes with equal
+// digits are grouped with 8 ballots so each digit costs one LDS atomic per wave.
+__device__ __forceinline__ void wave_hist_add(unsigned* hist, int d) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long act = __ballot(d >= 0);
+    if (act == 0ull) return;
+    unsigned long long peers = act;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const bool bit = (d >> b) & 1;
+        const unsigned long long bb = __ballot(bit);
+        peers &= bit ? bb : ~bb;
+    }
+    if (d >= 0 && (__ffsll((long long)peers) - 1) == lane) atomicAdd(&hist[d], (unsigned)__popcll(peers));
+}
+
+// Block max of v (all threads get it).
+__device__ inline float block_max(float v, AccShared* sh) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_max_f32(v);
+    if (lane == 0) sh->red_f[wid] = v;
+    __syncthreads();
+    float m = sh->red_f[0];
+    for (int w = 1; w < ACC_WAVES; w++) m = fmaxf(m, sh->red_f[w]);
+    __syncthreads();
+    return m;
+}
+
+// The k-th largest (k >= 1) of the keys kf(l_j, j, ok) with ok and key < U, over
+// j in [0, V): an 8-bit MSD radix select (keys are unique, so it ends on one
+// key).  Returns 0 when fewer than k keys qualify; *total gets their count.
+template <class KF>
+__device__ uint64_t select_desc(const KF& kf, const float* row, int V, int k, uint64_t U, AccShared* sh,
+                                unsigned* total) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint64_t prefix = 0, mask = 0;
+    int kk = k;
+    for (int pass = 0; pass < 8; pass++) {
+        const int shift = 56 - 8 * pass;
+        for (int i = tid; i < 256; i += ACC_THREADS) sh->sel.hist[i] = 0;
+        __syncthreads();
+        for (int jb = 0; jb < V; jb += ACC_U * ACC_THREADS) {  // uniform trip count: whole waves vote
+            const int j0 = jb + tid;
+            float vv[ACC_U];
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int j = j0 + q * ACC_THREADS;
+                vv[q] = j < V ? row[j] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int j = j0 + q * ACC_THREADS;
+                int d = -1;
+                if (j < V) {
+                    bool ok;
+                    const uint64_t key = kf(vv[q], j, ok);
+                    if (ok && key < U && (key & mask) == prefix) d = (int)((key >> shift) & 255);
+                }
+                wave_hist_add(sh->sel.hist, d);
+            }
+        }
+        __syncthreads();
+        if (wid == 0) {
+            // lane l holds bins 255 - 4l .. 252 - 4l, so lanes run from the largest digit down
+            unsigned c[4], sum = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                c[q] = sh->sel.hist[255 - 4 * lane - q];
+                sum += c[q];
+            }
+            unsigned incl = sum;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const unsigned t = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += t;
+            }
+            const unsigned tot = __shfl(incl, 63, 64);
+            const unsigned excl = incl - sum;
+            if (lane == 0) {
+                if (pass == 0) sh->sel.total = tot;
+                if (tot < (unsigned)kk) sh->sel.digit = -1;
+            }
+            if (tot >= (unsigned)kk && excl < (unsigned)kk && (unsigned)kk <= incl) {
+                unsigned run = excl;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (run < (unsigned)kk && run + c[q] >= (unsigned)kk) {
+                        sh->sel.digit = 255 - 4 * lane - q;
+                        sh->sel.kk = kk - (int)run;
+                        sh->sel.cnt = c[q];
+                    }
+                    run += c[q];
+                }
+            }
+        }
+        __syncthreads();
+        if (pass == 0) *total = sh->sel.total;
+        const int d = sh->sel.digit;
+        kk = sh->sel.kk;
+        const unsigned cnt = sh->sel.cnt;
+        __syncthreads();
+        if (d < 0) return 0;
+        prefix |= (uint64_t)d << shift;
+        mask |= (uint64_t)255 << shift;
+        if (cnt == 1 && pass < 7) {
+            // one key carries this prefix: it is the k-th
+            for (int j = tid; j < V; j += ACC_THREADS) {
+                bool ok;
+                const uint64_t key = kf(row[j], j, ok);
+                if (ok && key < U && (key & mask) == prefix) sh->sel.key = key;
+            }
+            __syncthreads();
+            const uint64_t r = sh->sel.key;
+            __syncthreads();
+            return r;
+        }
+    }
+    return prefix;
+}
+
+// Exact sequential sum of f(a_j, b_j, j) >= 0 over j in [0, n) (a = r0[j], b = r1[j]
+// for NR = 2), with the inverse-CDF crossing for u >= 0: the workgroup writes LDS
+// chunks of `chunk` values and wave 0 scans them, carrying the running sum.
+template <int NR, class F>
+__device__ SeqScan block_seq_scan(const float* r0, const float* r1, int n, float u, const F& f, float* buf,
+                                  int chunk, AccShared* sh) {
+    const int tid = threadIdx.x, wid = tid >> 6;
+    SeqScan st = seq_scan_init();
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+        const int m = min(chunk, n - c0);
+        for (int i0 = tid; i0 < m; i0 += ACC_U * ACC_THREADS) {
+            float a[ACC_U], b[ACC_U];
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int i = i0 + q * ACC_THREADS;
+                a[q] = i < m ? r0[c0 + i] : 0.f;
+                b[q] = (NR == 2 && i < m) ? r1[c0 + i] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int i = i0 + q * ACC_THREADS;
+                if (i < m) buf[i] = f(a[q], b[q], c0 + i);
+            }
+        }
+        __syncthreads();
+        if (wid == 0) seq_scan_wave(buf, m, u, c0, st);
+        __syncthreads();
+    }
+    if (tid == 0) sh->scan = st;
+    __syncthreads();
+    const SeqScan r = sh->scan;
+    __syncthreads();
+    return r;
+}
+
+// Argmax with the last index on ties under total_cmp (sampler.rs:217-224).
+__device__ inline int block_argmax(const float* row, int V, AccShared* sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    int bk = INT_MIN, bi = 0;
+    for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+        float vv[ACC_U];
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS;
+            vv[q] = j < V ? row[j] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS;
+            if (j < V) {
+                const int k = total_key(vv[q]);
+                if (k >= bk) { bk = k; bi = j; }
+            }
+        }
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
+        if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
+    }
+    if (lane == 0) { sh->red_k[wid] = bk; sh->red_i[wid] = bi; }
+    __syncthreads();
+    int k0 = sh->red_k[0], i0 = sh->red_i[0];
+    for (int w = 1; w < ACC_WAVES; w++)
+        if (sh->red_k[w] > k0 || (sh->red_k[w] == k0 && sh->red_i[w] > i0)) { k0 = sh->red_k[w]; i0 = sh->red_i[w]; }
+    __syncthreads();
+    return i0;
+}
+
+// Bitonic sort of keys[0..np2) into descending order (np2 a power of two).
+__device__ inline void block_sort_desc(unsigned long long* keys, int np2) {
+    for (int k = 2; k <= np2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < np2; i += ACC_THREADS) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const unsigned long long a = keys[i], b = keys[ixj];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? a < b : a > b) {
+                        keys[i] = b;
+                        keys[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Distribution parameters of a sampled row (TopKTopP at T > EPSILON):
+// filtered_probs (sampler.rs:226-278).  status 1: no finite logit survives or a
+// normaliser is not positive (the reference returns Err).  flags: the top-p
+// cumulative sum crossed top_p within 1e-6 (its decision may flip with an ulp).
+__device__ void row_filter(const float* row, int V, float T, int top_k, float top_p, float* buf, int chunk,
+                           AccShared* sh, RowFilt& f, uint32_t& flags, int& status) {
+    const int tid = threadIdx.x, wid = tid >> 6;
+    f.T = T;
+    f.kkey = 0;
+    f.pkey = 0;
+    f.R2 = 1.0f;
+    f.S = 1.0f;
+    f.mx = 0.0f;
+    f.topp = (top_p > 0.0f && top_p < 1.0f) ? 1 : 0;
+    flags = 0;
+    status = 0;
+    // ---- top-k: the k-th largest logit key under the stable total_cmp ranking ----
+    if (top_k > 0 && top_k < V) {
+        unsigned tot;
+        f.kkey = select_desc(
+            [](float l, int j, bool& ok) {
+                ok = true;
+                return logit_key(l, j);
+            },
+            row, V, top_k, ~0ull, sh, &tot);
+    }
+    // ---- max of the finite masked logits ----
+    float mx = -INFINITY;
+    for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+        float vv[ACC_U];
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS;
+            vv[q] = j < V ? row[j] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS;
+            if (j < V && logit_key(vv[q], j) >= f.kkey) {
+                const float m = vv[q] / T;
+                if (isfinite(m)) mx = fmaxf(mx, m);
+            }
+        }
+    }
+    mx = block_max(mx, sh);
+    if (!(mx > -INFINITY)) {  // "all logits are non-finite" (sampler.rs:286-288)
+        status = 1;
+        return;
+    }
+    f.mx = mx;
+    // ---- softmax normaliser: exact sequential sum in index order ----
+    const RowFilt fe = f;
+    const SeqScan s1 = block_seq_scan<1>(
+        row, nullptr, V, -1.0f, [&](float a, float, int j) { return filt_exp(fe, a, j); }, buf, chunk, sh);
+    f.S = s1.s;
+    if (!(f.S > 0.0f) || !isfinite(f.S)) {
+        status = 1;
+        return;
+    }
+    if (!f.topp) return;
+    // ---- top-p: walk the probabilities in descending (stable) order, a page of the
+    // TOPP_PAGE next-largest keys at a time, with the exact sequential cumulative ----
+    const RowFilt fp = f;
+    auto pkf = [&](float l, int j, bool& ok) {
+        const float p = filt_exp(fp, l, j) / fp.S;
+        ok = p > 0.0f;
+        return prob_key(p, j);
+    };
+    unsigned long long* keys = (unsigned long long*)buf;
+    float* vals = buf + 2 * TOPP_PAGE;
+    uint64_t U = ~0ull;
+    float carry = 0.0f;
+    uint64_t pkey = 0;
+    for (;;) {
+        unsigned remain = 0;
+        const uint64_t L = select_desc(pkf, row, V, TOPP_PAGE, U, sh, &remain);  // 0: fewer than a page left
+        if (remain == 0) break;  // every positive probability taken without reaching top_p: keep all
+        if (tid == 0) sh->n = 0;
+        __syncthreads();
+        for (int jb = 0; jb < V; jb += ACC_THREADS) {  // uniform trip count: the ballot sees whole waves
+            const int j = jb + tid;
+            bool ok = false;
+            uint64_t key = 0;
+            if (j < V) key = pkf(row[j], j, ok);
+            const bool take = ok && key < U && key >= L;
+            const unsigned long long m = __ballot(take);
+            unsigned base = 0;
+            if ((threadIdx.x & 63) == 0 && m) base = atomicAdd(&sh->n, (unsigned)__popcll(m));
+            base = __shfl(base, 0, 64);
+            const unsigned slot = base + (unsigned)__popcll(m & ((1ull << (threadIdx.x & 63)) - 1ull));
+            if (take && slot < (unsigned)TOPP_PAGE) keys[slot] = key;
+        }
+        __syncthreads();
+        const int n = min((int)sh->n, TOPP_PAGE);
+        int np2 = 1;
+        while (np2 < n) np2 <<= 1;
+        for (int i = n + tid; i < np2; i += ACC_THREADS) keys[i] = 0ull;
+        __syncthreads();
+        block_sort_desc(keys, np2);
+        for (int i = tid; i < n; i += ACC_THREADS) vals[i] = __uint_as_float((uint32_t)(keys[i] >> 32));
+        __syncthreads();
+        if (wid == 0) {
+            SeqScan st = seq_scan_init();
+            st.s = carry;
+            seq_scan_wave(vals, n, top_p, 0, st);
+            if (tid == 0) sh->scan = st;
+        }
+        __syncthreads();
+        const SeqScan st = sh->scan;
+        carry = st.s;
+        if (st.cross >= 0) {
+            pkey = keys[st.cross];
+            if (fminf(st.s_at - top_p, top_p - st.s_before) < 1e-6f) flags |= ACCEPT_FLAG_TOPP_NEAR;
+            __syncthreads();
+            break;
+        }
+        __syncthreads();
+        if (L == 0) break;  // that was the last (partial) page: keep all
+        U = L;
+    }
+    f.pkey = pkey;
+    // ---- renormalise over the kept probabilities (sequential sum in index order) ----
+    const RowFilt fr = f;
+    const SeqScan s2 = block_seq_scan<1>(
+        row, nullptr, V, -1.0f,
+        [&](float a, float, int j) {
+            const float p0 = filt_exp(fr, a, j) / fr.S;
+            return (p0 > 0.0f && prob_key(p0, j) >= fr.pkey) ? p0 : 0.0f;
+        },
+        buf, chunk, sh);
+    f.R2 = s2.s;
+    if (!(f.R2 > 0.0f) || !isfinite(f.R2)) status = 1;
+}
+
+__device__ __forceinline__ int acc_chunk_floats(int V) { return V < ACC_CHUNK ? V : ACC_CHUNK; }
+
+// ---------------------------------------------------------------------------
+// Acceptance kernel: grid = B * (target_rows + K) workgroups.
+// ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     extern __shared__ float lds[];
-    __shared__ float red_f[ACC_THREADS / WAVE];
-    __shared__ int red_k[ACC_THREADS / WAVE];
-    __shared__ int red_i[ACC_THREADS / WAVE];
-    __shared__ unsigned is_last;
-    __shared__ float sh_bcast[4];
-    __shared__ int sh_ibcast[8];
+    __shared__ AccShared sh;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -54,10 +488,11 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     const int b = blockIdx.x / rows_per_seq;
     const int r = blockIdx.x % rows_per_seq;
     const int V = a.V;
+    const int chunk = a.chunk;
     int np = a.n_proposals ? a.n_proposals[b] : a.K;
     np = np < 0 ? 0 : (np > a.K ? a.K : np);
 
-    // ---------------- stage 1: per-row statistics ----------------
+    // ---------------- stage 1: per-row distribution parameters ----------------
     const bool is_target = r < a.target_rows;
     const int ridx = is_target ? r : r - a.target_rows;
     const bool needed = is_target ? (ridx < np || (a.bonus && ridx == np)) : (ridx < np);
@@ -65,132 +500,64 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
     const float* row = is_target ? a.target + ((size_t)b * a.target_rows + ridx) * V
                                  : a.draft + ((size_t)b * a.K + ridx) * V;
     if (needed) {
+        uint32_t* w = a.rstat + row_id * ACC_RS_WORDS;
         if (a.greedy) {
-            int bk = INT_MIN, bi = 0;
-            // ACC_U loads in flight per thread, consumed in index order
-            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-                float vv[ACC_U];
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    vv[u] = j < V ? row[j] : 0.f;
-                }
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    if (j < V) {
-                        const int k = total_key(vv[u]);
-                        if (k >= bk) { bk = k; bi = j; }
-                    }
-                }
-            }
-            for (int d = 32; d >= 1; d >>= 1) {
-                int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
-                if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
-            }
-            if (lane == 0) { red_k[wid] = bk; red_i[wid] = bi; }
-            __syncthreads();
-            if (tid == 0) {
-                int k0 = red_k[0], i0 = red_i[0];
-                for (int w = 1; w < ACC_THREADS / WAVE; w++)
-                    if (red_k[w] > k0 || (red_k[w] == k0 && red_i[w] > i0)) { k0 = red_k[w]; i0 = red_i[w]; }
-                st_coh_i32(&a.row_argmax[row_id], i0);
-            }
+            const int am = block_argmax(row, V, &sh);
+            if (tid == 0) rs_put(w, RS_ARGMAX, (uint32_t)am);
         } else {
-            const float T = a.temperature;
-            float mx = -INFINITY;
-            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-                float vv[ACC_U];
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    vv[u] = j < V ? row[j] : 0.f;
-                }
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    if (j < V) {
-                        const float m = vv[u] / T;
-                        if (isfinite(m)) mx = fmaxf(mx, m);
-                    }
-                }
-            }
-            mx = wave_max_f32(mx);
-            if (lane == 0) red_f[wid] = mx;
-            __syncthreads();
-            if (tid == 0) {
-                float m0 = red_f[0];
-                for (int w = 1; w < ACC_THREADS / WAVE; w++) m0 = fmaxf(m0, red_f[w]);
-                sh_bcast[0] = m0;
-            }
-            __syncthreads();
-            mx = sh_bcast[0];
-            for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-                float vv[ACC_U];
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    vv[u] = j < V ? row[j] : 0.f;
-                }
-#pragma unroll
-                for (int u = 0; u < ACC_U; u++) {
-                    const int j = j0 + u * ACC_THREADS;
-                    if (j < V) {
-                        const float m = vv[u] / T;
-                        lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
-                    }
-                }
-            }
-            __syncthreads();
-            if (wid == 0) {
-                SeqSum ss = seq_sum_wave(lds, V, -1.0f);
-                if (lane == 0) {
-                    st_coh(&a.row_max[row_id], mx);
-                    st_coh(&a.row_sum[row_id], ss.total);
-                }
-            }
+            RowFilt f;
+            uint32_t fl;
+            int stt;
+            row_filter(row, V, a.temperature, a.top_k, a.top_p, lds, chunk, &sh, f, fl, stt);
+            if (tid == 0) rs_store(w, f, fl, stt);
         }
     }
 
     // ---------------- last workgroup of the sequence resolves ----------------
-    if (!arrive_last(&a.counters[b], (unsigned)rows_per_seq, &is_last)) return;
+    if (!arrive_last(&a.counters[b], (unsigned)rows_per_seq, &sh.is_last)) return;
 
-    const size_t seq_row0 = (size_t)b * rows_per_seq;
+    const uint32_t* rs0 = a.rstat + (size_t)b * rows_per_seq * ACC_RS_WORDS;
+    const uint32_t* rsd0 = rs0 + (size_t)a.target_rows * ACC_RS_WORDS;
     const float* trow0 = a.target + (size_t)b * a.target_rows * V;
     const float* drow0 = a.draft + (size_t)b * a.K * V;
+    const float T = a.temperature;
 
     if (tid == 0) {
         uint32_t key[8];
         rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
-        uint64_t word = a.word_offsets ? a.word_offsets[b] : 0ull;
-        int draws = 0, acc = 0, rej = -1;
+        const uint64_t word = a.word_offsets ? a.word_offsets[b] : 0ull;
+        int draws = 0, acc = 0, rej = -1, status = 0;
         uint32_t flags = 0;
         for (int i = 0; i < np; i++) {
             if (a.greedy) {
-                if (ld_coh_i32(&a.row_argmax[seq_row0 + a.target_rows + i]) == ld_coh_i32(&a.row_argmax[seq_row0 + i])) {
+                if (rs_get(rsd0 + i * ACC_RS_WORDS, RS_ARGMAX) == rs_get(rs0 + i * ACC_RS_WORDS, RS_ARGMAX)) {
                     acc++;
                     continue;
                 }
                 rej = i;
                 break;
             }
+            const uint32_t* wt = rs0 + i * ACC_RS_WORDS;
+            const uint32_t* wd = rsd0 + i * ACC_RS_WORDS;
+            flags |= rs_get(wt, RS_FLAGS) | rs_get(wd, RS_FLAGS);
+            if (rs_get(wt, RS_STATUS) | rs_get(wd, RS_STATUS)) {
+                status = 1;
+                rej = i;
+                break;
+            }
             const uint32_t x = a.draft_tokens[(size_t)b * a.K + i];
-            const float* tl = trow0 + (size_t)i * V;
-            const float* dl = drow0 + (size_t)i * V;
             float p = 0.0f, q = 0.0f;
             if ((int)x < V) {
-                p = row_prob(tl, (int)x, 0.f, a.temperature, ld_coh(&a.row_max[seq_row0 + i]),
-                             ld_coh(&a.row_sum[seq_row0 + i]));
-                q = row_prob(dl, (int)x, 0.f, a.temperature, ld_coh(&a.row_max[seq_row0 + a.target_rows + i]),
-                             ld_coh(&a.row_sum[seq_row0 + a.target_rows + i]));
+                p = filt_prob(rs_load(wt, T), trow0[(size_t)i * V + x], (int)x);
+                q = filt_prob(rs_load(wd, T), drow0[(size_t)i * V + x], (int)x);
             }
             if (!(q > 0.0f)) {
                 rej = i;
                 break;
             }
-            float u = a.uniforms ? a.uniforms[(size_t)b * (a.K + 1) + draws] : rng_f32(key, word + draws);
+            const float u = a.uniforms ? a.uniforms[(size_t)b * (a.K + 1) + draws] : rng_f32(key, word + draws);
             draws++;
-            float ratio = p / q;
+            const float ratio = p / q;
             float cl = ratio < 1.0f ? ratio : 1.0f;
             if (isnan(ratio)) cl = 1.0f;
             if (fabsf(cl - u) < 1e-5f) flags |= ACCEPT_FLAG_RATIO_NEAR;
@@ -201,95 +568,110 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
             rej = i;
             break;
         }
-        sh_ibcast[0] = acc;
-        sh_ibcast[1] = rej;
-        sh_ibcast[2] = draws;
-        sh_ibcast[3] = (int)flags;
+        if (!a.greedy && rej < 0 && a.bonus) {
+            const uint32_t* wt = rs0 + np * ACC_RS_WORDS;
+            flags |= rs_get(wt, RS_FLAGS);
+            if (rs_get(wt, RS_STATUS)) status = 1;
+        }
+        sh.ib[0] = acc;
+        sh.ib[1] = rej;
+        sh.ib[2] = draws;
+        sh.ib[3] = (int)flags;
+        sh.ib[4] = status;
     }
     __syncthreads();
-    const int acc = sh_ibcast[0], rej = sh_ibcast[1];
-    int draws = sh_ibcast[2];
-    uint32_t flags = (uint32_t)sh_ibcast[3];
-    int token = -1, status = 0;
+    const int acc = sh.ib[0], rej = sh.ib[1];
+    int draws = sh.ib[2];
+    uint32_t flags = (uint32_t)sh.ib[3];
+    int status = sh.ib[4];
+    int token = -1;
+    __syncthreads();
 
     if (a.greedy) {
-        if (rej >= 0) token = ld_coh_i32(&a.row_argmax[seq_row0 + rej]);
-        else if (a.bonus) token = ld_coh_i32(&a.row_argmax[seq_row0 + np]);
-    } else if (rej >= 0 || a.bonus) {
-        const float T = a.temperature;
-        if (rej >= 0) {
-            const float* tl = trow0 + (size_t)rej * V;
-            const float* dl = drow0 + (size_t)rej * V;
-            const float pmx = ld_coh(&a.row_max[seq_row0 + rej]), pS = ld_coh(&a.row_sum[seq_row0 + rej]);
-            const float qmx = ld_coh(&a.row_max[seq_row0 + a.target_rows + rej]);
-            const float qS = ld_coh(&a.row_sum[seq_row0 + a.target_rows + rej]);
-            for (int j = tid; j < V; j += ACC_THREADS) {
-                float d = row_prob(tl, j, 0.f, T, pmx, pS) - row_prob(dl, j, 0.f, T, qmx, qS);
-                lds[j] = d > 0.0f ? d : 0.0f;
-            }
-            __syncthreads();
-            if (wid == 0) {
-                SeqSum ss = seq_sum_wave(lds, V, -1.0f);
-                if (lane == 0) sh_bcast[1] = ss.total;
-            }
-            __syncthreads();
-            const float R = sh_bcast[1];
-            if (!isfinite(R) || R <= FLT_EPSILON) {
-                status = 1;
-            } else {
-                for (int j = tid; j < V; j += ACC_THREADS) lds[j] = lds[j] / R;
-            }
-        } else {
-            const float* tl = trow0 + (size_t)np * V;
-            const float pmx = ld_coh(&a.row_max[seq_row0 + np]), pS = ld_coh(&a.row_sum[seq_row0 + np]);
-            for (int j = tid; j < V; j += ACC_THREADS) lds[j] = row_prob(tl, j, 0.f, T, pmx, pS);
-        }
-        __syncthreads();
-        if (status == 0 && wid == 0) {
+        if (rej >= 0) token = (int)rs_get(rs0 + rej * ACC_RS_WORDS, RS_ARGMAX);
+        else if (a.bonus) token = (int)rs_get(rs0 + np * ACC_RS_WORDS, RS_ARGMAX);
+    } else if (status == 0 && (rej >= 0 || a.bonus)) {
+        float u;
+        {
             uint32_t key[8];
-            float u;
             if (a.uniforms) {
                 u = a.uniforms[(size_t)b * (a.K + 1) + draws];
             } else {
                 rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
                 u = rng_f32(key, (a.word_offsets ? a.word_offsets[b] : 0ull) + draws);
             }
-            SeqSum ss = seq_sum_wave(lds, V, u);
-            if (lane == 0) {
-                sh_ibcast[4] = ss.cross;
-                sh_bcast[2] = fminf(fabsf(ss.s_at - u), fabsf(u - ss.s_before));
-                sh_ibcast[5] = (!isfinite(ss.total) || fabsf(ss.total - 1.0f) > 1e-4f) ? 1 : 0;
-            }
         }
-        __syncthreads();
+        SeqScan cdf = seq_scan_init();
+        if (rej >= 0) {
+            // residual max(0, p - q): exact mass, then the exact CDF of r / mass
+            const RowFilt ft = rs_load(rs0 + rej * ACC_RS_WORDS, T);
+            const RowFilt fd = rs_load(rsd0 + rej * ACC_RS_WORDS, T);
+            const float* tl = trow0 + (size_t)rej * V;
+            const float* dl = drow0 + (size_t)rej * V;
+            auto resid = [&](float lt, float ld, int j) {
+                const float d = filt_prob(ft, lt, j) - filt_prob(fd, ld, j);
+                return d > 0.0f ? d : 0.0f;
+            };
+            const SeqScan m = block_seq_scan<2>(tl, dl, V, -1.0f, resid, lds, chunk, &sh);
+            const float R = m.s;
+            if (!isfinite(R) || R <= FLT_EPSILON) {
+                status = 1;
+            } else {
+                cdf = block_seq_scan<2>(
+                    tl, dl, V, u, [&](float lt, float ld, int j) { return resid(lt, ld, j) / R; }, lds, chunk, &sh);
+            }
+        } else {
+            const RowFilt ft = rs_load(rs0 + np * ACC_RS_WORDS, T);
+            cdf = block_seq_scan<1>(
+                trow0 + (size_t)np * V, nullptr, V, u, [&](float lt, float, int j) { return filt_prob(ft, lt, j); },
+                lds, chunk, &sh);
+        }
         if (status == 0) {
-            token = sh_ibcast[4];
-            status = sh_ibcast[5];
-            if (sh_bcast[2] < 1e-6f) flags |= ACCEPT_FLAG_CDF_NEAR;
+            if (cdf.cross < 0) {  // no partial sum reaches the draw: the last index (sampler.rs:346)
+                cdf.cross = V - 1;
+                cdf.s_at = cdf.s;
+                cdf.s_before = cdf.s;
+            }
+            token = cdf.cross;
+            // validate_probabilities (sampler.rs:314-335): the sampled distribution sums to 1
+            if (!isfinite(cdf.s) || fabsf(cdf.s - 1.0f) > 1e-4f) status = 1;
+            if (fminf(fabsf(cdf.s_at - u), fabsf(u - cdf.s_before)) < 1e-6f) flags |= ACCEPT_FLAG_CDF_NEAR;
             draws++;
         }
     }
+    (void)lane;
+    (void)wid;
     if (tid == 0) {
         a.out_accept_len[b] = acc;
-        a.out_token[b] = token;
+        a.out_token[b] = status ? -1 : token;
         a.out_flags[b] = flags;
         a.out_draws[b] = draws;
         a.out_status[b] = status;
     }
 }
 
-int launch_accept(const AcceptArgs& a, hipStream_t stream) {
+static size_t accept_lds_bytes(int V, int greedy, int top_p_active) {
+    if (greedy) return 0;
+    size_t f = (size_t)(V < ACC_CHUNK ? V : ACC_CHUNK);
+    if (top_p_active && f < (size_t)TOPP_LDS_FLOATS) f = TOPP_LDS_FLOATS;
+    return f * sizeof(float);
+}
+
+int launch_accept(const AcceptArgs& a_in, hipStream_t stream) {
+    AcceptArgs a = a_in;
     const int rows = a.target_rows + a.K;
-    const size_t lds = a.greedy ? 0 : (size_t)a.V * sizeof(float);
-    if (lds > 160 * 1024) return 3;
+    const bool topp = a.top_p > 0.0f && a.top_p < 1.0f;
+    const size_t lds = accept_lds_bytes(a.V, a.greedy, topp);
     if (lds > MAX_DYN_LDS) return 3;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (note_error(hipFuncSetAttribute((const void*)accept_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           MAX_DYN_LDS)))
-            return 4;
-        attr_set = true;
-    }
+    a.chunk = a.V < ACC_CHUNK ? a.V : ACC_CHUNK;
+    if (a.chunk < 1) a.chunk = 1;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)accept_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)MAX_DYN_LDS);
+    });
+    if (note_error(attr)) return 4;
     (void)hipGetLastError();
     hipLaunchKernelGGL(accept_kernel, dim3(a.B * rows), dim3(ACC_THREADS), lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
@@ -306,113 +688,45 @@ int launch_accept(const AcceptArgs& a, hipStream_t stream) {
 __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     extern __shared__ float lds[];
     __shared__ unsigned long long keys[ACC_THREADS][CAND_MAX];
-    __shared__ float red_f[ACC_THREADS / WAVE];
-    __shared__ int red_k[ACC_THREADS / WAVE], red_i[ACC_THREADS / WAVE];
-    __shared__ float sh[2];
+    __shared__ AccShared sh;
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int V = a.V, n = a.n;
     const float* row = a.logits + (size_t)blockIdx.x * a.ld;
     int am = -1;
-    float S = 1.0f;
+    RowFilt f{};
+    int status = 0;
     if (a.greedy) {
-        // argmax, last index on ties (sampler.rs:211-215 / argmax)
-        int bk = INT_MIN, bi = 0;
-        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-            float vv[ACC_U];
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                vv[u] = j < V ? row[j] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                if (j < V) {
-                    const int k = total_key(vv[u]);
-                    if (k >= bk) { bk = k; bi = j; }
-                }
-            }
-        }
-        for (int d = 32; d >= 1; d >>= 1) {
-            const int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
-            if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
-        }
-        if (lane == 0) { red_k[wid] = bk; red_i[wid] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            int k0 = red_k[0], i0 = red_i[0];
-            for (int w = 1; w < ACC_THREADS / WAVE; w++)
-                if (red_k[w] > k0 || (red_k[w] == k0 && red_i[w] > i0)) { k0 = red_k[w]; i0 = red_i[w]; }
-            red_i[0] = i0;
-        }
-        __syncthreads();
-        am = red_i[0];
+        am = block_argmax(row, V, &sh);  // one-hot at the argmax (sampler.rs:211-215)
     } else {
-        const float T = a.temperature;
-        float mx = -INFINITY;
-        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-            float vv[ACC_U];
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                vv[u] = j < V ? row[j] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                if (j < V) {
-                    const float m = vv[u] / T;
-                    if (isfinite(m)) mx = fmaxf(mx, m);
-                }
-            }
-        }
-        mx = wave_max_f32(mx);
-        if (lane == 0) red_f[wid] = mx;
-        __syncthreads();
-        if (tid == 0) {
-            float m0 = red_f[0];
-            for (int w = 1; w < ACC_THREADS / WAVE; w++) m0 = fmaxf(m0, red_f[w]);
-            sh[0] = m0;
-        }
-        __syncthreads();
-        mx = sh[0];
-        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-            float vv[ACC_U];
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                vv[u] = j < V ? row[j] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < ACC_U; u++) {
-                const int j = j0 + u * ACC_THREADS;
-                if (j < V) {
-                    const float m = vv[u] / T;
-                    lds[j] = isfinite(m) ? expf_rn(m - mx) : 0.0f;
-                }
-            }
-        }
-        __syncthreads();
-        if (wid == 0) {
-            const SeqSum ss = seq_sum_wave(lds, V, -1.0f);
-            if (lane == 0) sh[1] = ss.total;
-        }
-        __syncthreads();
-        S = sh[1];
+        uint32_t fl;
+        row_filter(row, V, a.temperature, a.top_k, a.top_p, lds, a.chunk, &sh, f, fl, status);
     }
     // ---- this thread's n best keys, descending ----
     unsigned long long best[CAND_MAX];
 #pragma unroll
     for (int i = 0; i < CAND_MAX; i++) best[i] = 0ull;
-    for (int j = tid; j < V; j += ACC_THREADS) {
-        const float p = a.greedy ? (j == am ? 1.0f : 0.0f) : lds[j] / S;
-        unsigned long long k = ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)(~(unsigned)j);
+    if (status == 0) {
+        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
+            float vv[ACC_U];
 #pragma unroll
-        for (int i = 0; i < CAND_MAX; i++) {
-            if (i < n && k > best[i]) {
-                const unsigned long long t = best[i];
-                best[i] = k;
-                k = t;
+            for (int q = 0; q < ACC_U; q++) {
+                const int j = j0 + q * ACC_THREADS;
+                vv[q] = (j < V && !a.greedy) ? row[j] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int j = j0 + q * ACC_THREADS;
+                if (j >= V) continue;
+                const float p = a.greedy ? (j == am ? 1.0f : 0.0f) : filt_prob(f, vv[q], j);
+                unsigned long long k = prob_key(p, j);
+#pragma unroll
+                for (int i = 0; i < CAND_MAX; i++) {
+                    if (i < n && k > best[i]) {
+                        const unsigned long long t = best[i];
+                        best[i] = k;
+                        k = t;
+                    }
+                }
             }
         }
     }
@@ -420,15 +734,23 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     for (int i = 0; i < CAND_MAX; i++) keys[tid][i] = best[i];
     __syncthreads();
     if (wid != 0) return;
+    if (status != 0) {
+        // the distribution is invalid (the reference returns Err): no candidates
+        if (lane < n) {
+            a.ids[(size_t)blockIdx.x * n + lane] = 0xFFFFFFFFu;
+            a.probs[(size_t)blockIdx.x * n + lane] = __uint_as_float(0x7FC00000u);
+        }
+        return;
+    }
     // ---- wave 0: lane l owns lists l + 64 q; n rounds of a wave-wide max over list heads ----
-    int head[ACC_THREADS / 64];
+    int head[ACC_WAVES];
 #pragma unroll
-    for (int q = 0; q < ACC_THREADS / 64; q++) head[q] = 0;
+    for (int q = 0; q < ACC_WAVES; q++) head[q] = 0;
     for (int r = 0; r < n; r++) {
         unsigned long long mk = 0ull;
         int mq = -1;
 #pragma unroll
-        for (int q = 0; q < ACC_THREADS / 64; q++) {
+        for (int q = 0; q < ACC_WAVES; q++) {
             const unsigned long long k = head[q] < n ? keys[lane + 64 * q][head[q]] : 0ull;
             if (k > mk) { mk = k; mq = q; }
         }
@@ -440,7 +762,7 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
         }
         if (mk == wk && mk != 0ull) {
 #pragma unroll
-            for (int q = 0; q < ACC_THREADS / 64; q++)
+            for (int q = 0; q < ACC_WAVES; q++)
                 if (q == mq) head[q]++;
         }
         if (lane == 0) {
@@ -450,17 +772,23 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     }
 }
 
-int launch_candidates(const CandArgs& a, hipStream_t stream) {
+int launch_candidates(const CandArgs& a_in, hipStream_t stream) {
+    CandArgs a = a_in;
     if (a.n < 1 || a.n > CAND_MAX || a.rows <= 0 || a.V <= 0) return 2;
-    const size_t lds = a.greedy ? 0 : (size_t)a.V * sizeof(float);
-    if (lds > MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX) return 3;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (note_error(hipFuncSetAttribute((const void*)candidates_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)(MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX))))
-            return 4;
-        attr_set = true;
-    }
+    const bool topp = a.top_p > 0.0f && a.top_p < 1.0f;
+    size_t fl = a.greedy ? 0 : (size_t)(a.V < CAND_CHUNK ? a.V : CAND_CHUNK);
+    if (!a.greedy && topp && fl < (size_t)TOPP_LDS_FLOATS) fl = TOPP_LDS_FLOATS;
+    const size_t lds = fl * sizeof(float);
+    const size_t cap = MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX;
+    if (lds > cap) return 3;
+    a.chunk = a.V < CAND_CHUNK ? a.V : CAND_CHUNK;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [cap] {
+        attr = hipFuncSetAttribute((const void*)candidates_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)cap);
+    });
+    if (note_error(attr)) return 4;
     (void)hipGetLastError();
     hipLaunchKernelGGL(candidates_kernel, dim3(a.rows), dim3(ACC_THREADS), lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;

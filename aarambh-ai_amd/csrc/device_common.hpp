@@ -197,10 +197,11 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // ---------------------------------------------------------------------------
 // Exact sequential f32 summation on one wave.
 //
-// Returns s_{n-1} where s_k = fl(s_{k-1} + v[k]), s_{-1} = 0, for v[k] >= 0,
-// bit-identical to a scalar left-to-right f32 loop (the reference's
-// iter().sum::<f32>() and the running cumulative of sample_from_probs).
-// With u >= 0 it also finds the first k with u <= s_k (inverse CDF).
+// Continues s_k = fl(s_{k-1} + v[k]) over v[0..n) for v[k] >= 0 from the running
+// sum st.s, bit-identical to a scalar left-to-right f32 loop (the reference's
+// iter().sum::<f32>() and the running cumulative of sample_from_probs), so a long
+// vector can be summed in pieces.  With u >= 0 it also records the first k with
+// u <= s_k (inverse CDF, `draw <= cumulative`), as gbase + k.
 //
 // Method: while s stays inside one binade [2^e, 2^(e+1)), every partial sum
 // is an integer multiple of ulp(s), and fl(s + x) = s + ulp * RNE(x / ulp)
@@ -209,19 +210,28 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // stops at the first element that leaves the binade or ties; that element is
 // added with a real f32 add and the scan restarts after it.
 // ---------------------------------------------------------------------------
-struct SeqSum {
-    float total;
-    int cross;      // first k with u <= s_k (n-1 if none); -1 when u < 0
-    float s_at;     // s_cross
-    float s_before; // s_{cross-1} (0 for cross == 0)
+struct SeqScan {
+    float s;         // running sum
+    int cross;       // first global index k with u <= s_k; -1 while none
+    float s_at;      // s_cross
+    float s_before;  // s_{cross-1} (0 before the first element)
 };
 
-__device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
+__device__ __forceinline__ SeqScan seq_scan_init() {
+    SeqScan st;
+    st.s = 0.0f;
+    st.cross = -1;
+    st.s_at = 0.0f;
+    st.s_before = 0.0f;
+    return st;
+}
+
+__device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, SeqScan& st) {
     const int lane = threadIdx.x & 63;
-    float s = 0.0f;
+    float s = st.s;
     int pos = 0;
-    int cross = -1;
-    float s_at = 0.0f, s_before = 0.0f;
+    int cross = st.cross;
+    float s_at = st.s_at, s_before = st.s_before;
     const bool want = u >= 0.0f;
     while (pos < n) {
         const int base = pos + 4 * lane;
@@ -237,7 +247,7 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
                 if (base + k < n && x[k] != 0.0f) fnz = k;
             unsigned long long m = __ballot(fnz < 4);
             if (want && cross < 0 && u <= 0.0f) {
-                cross = pos;
+                cross = gbase + pos;
                 s_at = 0.0f;
                 s_before = 0.0f;
             }
@@ -251,7 +261,7 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
             float xt = v[t];
             s = xt;
             if (want && cross < 0 && u <= s) {
-                cross = t;
+                cross = gbase + t;
                 s_at = s;
                 s_before = 0.0f;
             }
@@ -266,7 +276,7 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
             float sp = s;
             s = s + xt;
             if (want && cross < 0 && u <= s) {
-                cross = pos;
+                cross = gbase + pos;
                 s_at = s;
                 s_before = sp;
             }
@@ -317,7 +327,7 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
         if (want && cross < 0 && cm) {
             int cl = __ffsll((long long)cm) - 1;
             int ck = __shfl(first_cross, cl, 64);
-            cross = pos + 4 * cl + ck;
+            cross = gbase + pos + 4 * cl + ck;
             s_at = __shfl(cs_at, cl, 64);
             s_before = __shfl(cs_before, cl, 64);
             if (ck == 0 && cl == 0) s_before = s;
@@ -334,23 +344,41 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
             float xt = v[t];
             s = sp + xt;
             if (want && cross < 0 && u <= s) {
-                cross = t;
+                cross = gbase + t;
                 s_at = s;
                 s_before = sp;
             }
             pos = t + 1;
         }
     }
-    if (want && cross < 0) {
-        cross = n - 1;
-        s_at = s;
-        s_before = s;
-    }
+    st.s = s;
+    st.cross = cross;
+    st.s_at = s_at;
+    st.s_before = s_before;
+}
+
+// One-shot form over v[0..n): total, and the crossing (n - 1 with s_at = total when
+// no partial sum reaches u, as sample_from_probs falls back to the last index).
+struct SeqSum {
+    float total;
+    int cross;      // first k with u <= s_k (n-1 if none); -1 when u < 0
+    float s_at;     // s_cross
+    float s_before; // s_{cross-1} (0 for cross == 0)
+};
+
+__device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
+    SeqScan st = seq_scan_init();
+    seq_scan_wave(v, n, u, 0, st);
     SeqSum res;
-    res.total = s;
-    res.cross = cross;
-    res.s_at = s_at;
-    res.s_before = s_before;
+    res.total = st.s;
+    res.cross = st.cross;
+    res.s_at = st.s_at;
+    res.s_before = st.s_before;
+    if (u >= 0.0f && st.cross < 0) {
+        res.cross = n - 1;
+        res.s_at = st.s;
+        res.s_before = st.s;
+    }
     return res;
 }
 

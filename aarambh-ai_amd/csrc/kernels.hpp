@@ -32,7 +32,11 @@ __host__ __device__ inline size_t k_off(size_t hb, int t, int d, int cap, int hd
 }
 enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
-enum { ACCEPT_FLAG_RATIO_NEAR = 1u, ACCEPT_FLAG_CDF_NEAR = 2u };
+enum { ACCEPT_FLAG_RATIO_NEAR = 1u, ACCEPT_FLAG_CDF_NEAR = 2u, ACCEPT_FLAG_TOPP_NEAR = 8u };
+
+// Acceptance scratch: ACC_RS_WORDS 32-bit words of distribution parameters per
+// logits row, and one arrival counter per sequence (zero between launches).
+static constexpr int ACC_RS_WORDS = 12;
 
 // Dynamic LDS a kernel may request: 160 KiB per workgroup on gfx950 minus room
 // for the kernels' static LDS.
@@ -185,13 +189,14 @@ struct AcceptArgs {
     int B, K, V;
     int bonus, greedy;
     float temperature;
+    int top_k;            // <= 0: none
+    float top_p;          // outside (0, 1): none
     const uint64_t* seeds;
     const uint64_t* word_offsets;
     const float* uniforms;
-    float* row_max;
-    float* row_sum;
-    int32_t* row_argmax;
-    unsigned* counters;
+    uint32_t* rstat;      // [B * (target_rows + K)][ACC_RS_WORDS] row parameters (scratch)
+    unsigned* counters;   // [B] arrival counters, zero between launches
+    int chunk;            // set by the launcher
     int32_t* out_accept_len;
     int32_t* out_token;
     uint32_t* out_flags;
@@ -202,7 +207,8 @@ struct AcceptArgs {
 int launch_accept(const AcceptArgs& a, hipStream_t stream);
 
 // Top-n candidates of each row's sampling distribution (greedy: one-hot at the
-// argmax; else softmax at T with the exact sequential normaliser).
+// argmax; else filtered_probs: softmax at T after top-k, then top-p, with exact
+// sequential normalisers).
 static constexpr int CAND_MAX = 5;  // engine.rs:70 top_candidates
 struct CandArgs {
     const float* logits;  // [rows][ld]
@@ -210,6 +216,9 @@ struct CandArgs {
     int rows, V, n;
     int greedy;
     float temperature;
+    int top_k;
+    float top_p;
+    int chunk;            // set by the launcher
     uint32_t* ids;        // [rows][n]
     float* probs;         // [rows][n]
 };

@@ -114,9 +114,8 @@ struct aarh_ctx {
     uint32_t* d_ids = nullptr;
     int32_t *h_pos0 = nullptr, *h_slot = nullptr;
     uint32_t* h_ids = nullptr;
-    // acceptance scratch
-    float *acc_max = nullptr, *acc_sum = nullptr;
-    int32_t* acc_argmax = nullptr;
+    // acceptance scratch: row distribution parameters and per-sequence arrival counters
+    uint32_t* acc_rstat = nullptr;
     unsigned* acc_cnt = nullptr;
     int acc_rows_cap = 0, acc_seq_cap = 0;
 
@@ -609,7 +608,7 @@ void aarh_destroy(aarh_ctx* c) {
                     (void*)c->frag_a, (void*)c->frag_b,
                     (void*)c->hidden, (void*)c->logits, (void*)c->apart, (void*)c->hn,
                     (void*)c->acnt, (void*)c->gpart, (void*)c->gcnt, (void*)c->d_pos0, (void*)c->d_slot, (void*)c->d_zero, (void*)c->d_seqidx,
-                    (void*)c->d_ids, (void*)c->acc_max, (void*)c->acc_sum, (void*)c->acc_argmax, (void*)c->acc_cnt})
+                    (void*)c->d_ids, (void*)c->acc_rstat, (void*)c->acc_cnt})
         F(p);
     if (c->h_pos0) (void)hipHostFree(c->h_pos0);
     if (c->h_slot) (void)hipHostFree(c->h_slot);
@@ -1112,14 +1111,11 @@ int aarh_mtp_head(aarh_ctx* c, int head, const float* anchor, const uint32_t* id
 static int ensure_accept_scratch(aarh_ctx* c, int B, int rows_per_seq) {
     const int rows = B * rows_per_seq;
     if (rows > c->acc_rows_cap) {
-        if (c->acc_max) {
+        if (c->acc_rstat) {
             HIPCHK(c, hipStreamSynchronize(c->stream));
-            (void)hipFree(c->acc_max);
-            (void)hipFree(c->acc_sum);
-            (void)hipFree(c->acc_argmax);
+            (void)hipFree(c->acc_rstat);
         }
-        if (dalloc(c, &c->acc_max, rows * 4) || dalloc(c, &c->acc_sum, rows * 4) || dalloc(c, &c->acc_argmax, rows * 4))
-            return AARH_ERR_DEVICE;
+        if (dalloc(c, &c->acc_rstat, (size_t)rows * ACC_RS_WORDS * 4)) return AARH_ERR_DEVICE;
         c->acc_rows_cap = rows;
     }
     if (B > c->acc_seq_cap) {
@@ -1143,10 +1139,8 @@ int aarh_accept_sample(aarh_ctx* c, const float* target, int target_rows, const 
     if (B <= 0 || K < 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0))
         return fail(c, AARH_ERR_SHAPE, "bad acceptance shape B=%d K=%d V=%d rows=%d", B, K, V, target_rows);
     const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
-    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
-        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
-    if (!greedy && (size_t)V * 4 > 160 * 1024)
-        return fail(c, AARH_ERR_UNSUPPORTED, "vocabulary %d exceeds the LDS-resident sampling limit", V);
+    if (!greedy && !(s->top_p >= 0.0f && s->top_p <= 1.0f))
+        return fail(c, AARH_ERR_CONFIG, "top_p must be in [0, 1]");
     if (ensure_accept_scratch(c, B, target_rows + K)) return AARH_ERR_DEVICE;
     AcceptArgs a{};
     a.target = target;
@@ -1160,12 +1154,12 @@ int aarh_accept_sample(aarh_ctx* c, const float* target, int target_rows, const 
     a.bonus = bonus ? 1 : 0;
     a.greedy = greedy ? 1 : 0;
     a.temperature = s->temperature;
+    a.top_k = s->top_k;
+    a.top_p = s->top_p;
     a.seeds = seeds;
     a.word_offsets = word_offsets;
     a.uniforms = uniforms;
-    a.row_max = c->acc_max;
-    a.row_sum = c->acc_sum;
-    a.row_argmax = c->acc_argmax;
+    a.rstat = c->acc_rstat;
     a.counters = c->acc_cnt;
     a.out_accept_len = accept_len;
     a.out_token = token;
@@ -1191,8 +1185,6 @@ int aarh_top_candidates(aarh_ctx* c, const float* logits, int rows, int V, const
     if (rows <= 0 || V <= 0 || n < 1 || n > CAND_MAX)
         return fail(c, AARH_ERR_SHAPE, "bad candidate shape rows=%d V=%d n=%d (n <= %d)", rows, V, n, CAND_MAX);
     const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
-    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
-        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
     CandArgs a{};
     a.logits = logits;
     a.ld = V;
@@ -1201,6 +1193,8 @@ int aarh_top_candidates(aarh_ctx* c, const float* logits, int rows, int V, const
     a.n = n;
     a.greedy = greedy ? 1 : 0;
     a.temperature = s->temperature;
+    a.top_k = s->top_k;
+    a.top_p = s->top_p;
     a.ids = ids;
     a.probs = probs;
     int r;
@@ -1420,9 +1414,15 @@ int session_round(aarh_session* e) {
                                         e->acc_status, nullptr)))
                 return r;
             if ((r = sync_stream(c))) return r;
-            std::vector<int32_t> t(nseq);
+            std::vector<int32_t> t(nseq), st(nseq);
             HIPCHK(c, hipMemcpy(t.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
-            for (int b = 0; b < nseq; b++) e->hprops[(size_t)b * K + p] = (uint32_t)t[b];
+            HIPCHK(c, hipMemcpy(st.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
+            for (int b = 0; b < nseq; b++) {
+                // sample_probabilities validates the proposal distribution (sampler.rs:142-152, 314-335)
+                if (!e->finished[b] && e->count[b] > p && st[b] != 0)
+                    return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
+                e->hprops[(size_t)b * K + p] = (uint32_t)(st[b] ? 0 : t[b]);
+            }
             HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
         }
     }
@@ -1590,8 +1590,6 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
     if (full >= g.max_seq_len)
         return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", full, g.max_seq_len);
     const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
-    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
-        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
     const int K = num_draft_tokens, V = c->V, H = c->H;
     if (nseq * K > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq x draft tokens exceeds max_rows");
     aarh_session* e = new aarh_session();
@@ -1730,6 +1728,18 @@ int aarh_session_candidates(aarh_session* e, uint32_t* ids, float* probs, int32_
     return 0;
 }
 
+int aarh_session_rng_offsets(aarh_session* e, uint64_t* out) {
+    if (!e || !out) return AARH_ERR_CONFIG;
+    for (int b = 0; b < e->nseq; b++) out[b] = e->hoffs[b];
+    return 0;
+}
+
+int aarh_session_set_rng_offsets(aarh_session* e, const uint64_t* offsets) {
+    if (!e || !offsets) return AARH_ERR_CONFIG;
+    for (int b = 0; b < e->nseq; b++) e->hoffs[b] = offsets[b];
+    return 0;
+}
+
 void aarh_session_end(aarh_session* e) { delete e; }
 
 int aarh_mtp_generate(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
@@ -1825,8 +1835,9 @@ int ragged_forward(aarh_ctx* x, const std::vector<int>& seqs, const std::vector<
     return 0;
 }
 
-// Sample one token per sequence from rows drf[b][p] (draft proposal p).
-int sample_draft_rows(XSession* e, int p) {
+// Sample one token per sequence from rows drf[b][p] (draft proposal p); active[b]:
+// the sequence proposes at p (its distribution must be valid).
+int sample_draft_rows(XSession* e, int p, const std::vector<char>& active) {
     aarh_ctx* c = e->c;
     const int nseq = e->nseq, K = e->K, V = c->V;
     int r;
@@ -1842,9 +1853,15 @@ int sample_draft_rows(XSession* e, int p) {
                                     e->acc_status, nullptr)))
             return r;
         if ((r = sync_stream(c))) return r;
-        std::vector<int32_t> t(nseq);
+        std::vector<int32_t> t(nseq), st(nseq);
         HIPCHK(c, hipMemcpy(t.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
-        for (int b = 0; b < nseq; b++) e->hprops[(size_t)b * K + p] = (uint32_t)t[b];
+        HIPCHK(c, hipMemcpy(st.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
+        for (int b = 0; b < nseq; b++) {
+            // rows of requests that sit this step out are sampled too and ignored
+            if (active[b] && st[b] != 0)
+                return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
+            e->hprops[(size_t)b * K + p] = (uint32_t)(st[b] ? 0 : t[b]);
+        }
         HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
     }
     if ((r = sync_stream(c))) return r;
@@ -1873,7 +1890,9 @@ int xsession_round(XSession* e) {
     }
     // ---- draft proposals (speculative.rs:267-304) ----
     for (int p = 0; p < Kr; p++) {
-        if ((r = sample_draft_rows(e, p))) return r;
+        std::vector<char> act(nseq);
+        for (int b = 0; b < nseq; b++) act[b] = alive[b] && p < count[b];
+        if ((r = sample_draft_rows(e, p, act))) return r;
         std::vector<int> fs, fo;
         std::vector<std::vector<uint32_t>> fi;
         for (int b = 0; b < nseq; b++) {
@@ -2067,8 +2086,6 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
         return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but speculative context limit is %d (target=%d, draft=%d)",
                     prompt_len, max_seq, c->cfg.max_seq_len, d->cfg.max_seq_len);
     const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
-    if (!greedy && (s->top_k > 0 || (s->top_p > 0.f && s->top_p < 1.f)))
-        return fail(c, AARH_ERR_UNSUPPORTED, "top-k / top-p filtering is not supported on the device path");
     const int K = num_draft_tokens, V = c->V;
     if (nseq * (K + 1) > c->Mmax || nseq * (K + 1) > d->Mmax)
         return fail(c, AARH_ERR_SHAPE, "nseq x (draft tokens + 1) exceeds max_rows");

@@ -43,7 +43,8 @@ enum {
 enum { AARH_KV_F32 = 0, AARH_KV_F16 = 1, AARH_KV_INT8 = 2 };
 enum { AARH_T_NORM = 0, AARH_T_LINEAR = 1, AARH_T_EMBED = 2 };
 enum { AARH_FINISH_MAX_TOKENS = 0, AARH_FINISH_EOS = 1, AARH_FINISH_CONTEXT_LIMIT = 2 };
-enum { AARH_FLAG_RATIO_NEAR = 1u, AARH_FLAG_CDF_NEAR = 2u };
+/* Near-tie flags: |p/q - u| < 1e-5, |cdf - u| < 1e-6, top-p cumulative within 1e-6 of top_p. */
+enum { AARH_FLAG_RATIO_NEAR = 1u, AARH_FLAG_CDF_NEAR = 2u, AARH_FLAG_TOPP_NEAR = 8u };
 enum { AARH_TOP_CANDIDATES = 5 };
 
 typedef struct aarh_ctx aarh_ctx;
@@ -60,12 +61,12 @@ typedef struct {
     int32_t max_rows;          /* max rows (sequences x tokens) per forward call, <= 128 */
 } aarh_model_config;
 
-/* Sampler (inference/src/sampler.rs:14-65). */
+/* Sampler (inference/src/sampler.rs:14-65); probabilities as filtered_probs (:226-278). */
 typedef struct {
     int32_t greedy;    /* 1 = Sampler::Greedy */
     float temperature; /* TopKTopP temperature (<= f32::EPSILON behaves greedy) */
-    int32_t top_k;     /* must be 0 on the device path (unsupported otherwise) */
-    float top_p;       /* must be outside (0,1) on the device path */
+    int32_t top_k;     /* <= 0: none (Option::None); >= vocab: keeps every token */
+    float top_p;       /* in [0, 1]; 0 or 1: none (top_p.filter(0 < p < 1)) */
 } aarh_sampler;
 
 /* SpeculativeStats (inference/src/speculative.rs:41-90). */
@@ -125,7 +126,8 @@ int aarh_mtp_head(aarh_ctx *ctx, int head, const float *anchor, const uint32_t *
    bonus = 1 samples from target row n_proposals when every proposal is accepted
    (external-draft round); bonus = 0 is the MTP round.  Outputs [B]: accepted count,
    replacement/bonus token (-1 none), near-tie flags, uniforms consumed, status (0 ok,
-   1 zero-mass residual or invalid distribution).  stream: hipStream_t or NULL (context stream). */
+   1 zero-mass residual or invalid distribution).  stream: hipStream_t or NULL (context stream).
+   Any vocabulary size; top-k / top-p apply as in filtered_probs. */
 int aarh_accept_sample(aarh_ctx *ctx, const float *target, int target_rows, const float *draft,
                        const uint32_t *draft_tokens, const int32_t *n_proposals, int B, int K, int V,
                        int bonus, const aarh_sampler *sampler, const uint64_t *seeds,
@@ -157,6 +159,12 @@ int aarh_session_result(aarh_session *session, uint32_t *out_tokens, int32_t out
    (inference/src/sampler.rs:188-208, engine.rs:70 top_candidates = 5; GenerationStep.candidates
    engine.rs:95-110).  ids/probs [nseq][out_cap][AARH_TOP_CANDIDATES], host memory. */
 int aarh_session_candidates(aarh_session *session, uint32_t *ids, float *probs, int32_t out_cap);
+/* Keystream position (StdRng word offset) of each request [nseq]: the next uniform a
+   request draws is word `offset` of StdRng::seed_from_u64(seed).  The reference's
+   Sampler owns its StdRng and keeps it across generate calls (sampler.rs:39-65,
+   157-162); set restores a saved position before the next step (resuming a request). */
+int aarh_session_rng_offsets(aarh_session *session, uint64_t *out);
+int aarh_session_set_rng_offsets(aarh_session *session, const uint64_t *offsets);
 void aarh_session_end(aarh_session *session);
 
 /* --- external-draft engine (SpeculativeEngine::generate_with_callback,

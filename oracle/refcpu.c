@@ -207,9 +207,20 @@ static int cmp_ranked_desc(const void *a, const void *b) {
     return x->i < y->i ? -1 : (x->i > y->i);
 }
 
+/* Decision margins of the last filtered_probs call on this thread (test diagnostics:
+   how far a rounding difference would have to move a value to change the kept set):
+   the top-p cumulative sum's distance to top_p at its crossing, and the logit gap
+   between the k-th and (k+1)-th ranked logits.  INFINITY when the filter is off. */
+static __thread float g_topp_margin = INFINITY;
+static __thread float g_topk_gap = INFINITY;
+float ref_last_topp_margin(void) { return g_topp_margin; }
+float ref_last_topk_gap(void) { return g_topk_gap; }
+
 /* sampler.rs:226-278 */
 static int filtered_probs(const float *logits, int64_t n, float temperature, int top_k,
                           float top_p, float *out) {
+    g_topp_margin = INFINITY;
+    g_topk_gap = INFINITY;
     float *masked = (float *)malloc(sizeof(float) * (size_t)n);
     unsigned char *allowed = (unsigned char *)malloc((size_t)n);
     if (!masked || !allowed) {
@@ -223,6 +234,8 @@ static int filtered_probs(const float *logits, int64_t n, float temperature, int
         for (int64_t i = 0; i < n; i++) r[i] = (ranked_t){logits[i], i};
         qsort(r, (size_t)n, sizeof(ranked_t), cmp_ranked_desc);
         for (int64_t j = top_k; j < n; j++) allowed[r[j].i] = 0;
+        g_topk_gap = fabsf(r[top_k - 1].v - r[top_k].v);
+        if (!(g_topk_gap == g_topk_gap)) g_topk_gap = 0.0f;
         free(r);
     }
     for (int64_t i = 0; i < n; i++) masked[i] = allowed[i] ? logits[i] / temperature : -INFINITY;
@@ -235,8 +248,13 @@ static int filtered_probs(const float *logits, int64_t n, float temperature, int
         float cum = 0.0f;
         for (int64_t j = 0; j < n; j++) {
             keep[r[j].i] = 1;
+            float prev = cum;
             cum += r[j].v;
-            if (cum >= top_p) break;
+            if (cum >= top_p) {
+                float a = cum - top_p, b = top_p - prev;
+                g_topp_margin = a < b ? a : b;
+                break;
+            }
         }
         for (int64_t i = 0; i < n; i++)
             if (!keep[i]) out[i] = 0.0f;
@@ -251,6 +269,8 @@ static int filtered_probs(const float *logits, int64_t n, float temperature, int
 
 /* sampler.rs:102-118 (+ one_hot_argmax :211-215) */
 int ref_probabilities(const ref_sampler *s, const float *logits, int64_t n, float *out) {
+    g_topp_margin = INFINITY;
+    g_topk_gap = INFINITY;
     if (n <= 0) return REF_ERR_SHAPE;
     if (s->greedy || !(s->temperature > FLT_EPSILON)) {
         memset(out, 0, sizeof(float) * (size_t)n);
@@ -377,7 +397,9 @@ int ref_accept_batch(int B, int K, int64_t V, const float *target, int target_ro
             const float *tl = target + ((int64_t)b * target_rows + i) * V;
             const float *dl = draft + ((int64_t)b * K + i) * V;
             if ((status = ref_probabilities(s, tl, V, p))) break;
+            if (g_topp_margin < 1e-6f) res.flags |= REF_FLAG_TOPP_NEAR;
             if ((status = ref_probabilities(s, dl, V, q))) break;
+            if (g_topp_margin < 1e-6f) res.flags |= REF_FLAG_TOPP_NEAR;
             uint32_t tok = draft_tokens[(int64_t)b * K + i];
             int acc = 0, drew = 0;
             float ratio = 0, u = 0;
@@ -439,6 +461,7 @@ int ref_accept_batch(int B, int K, int64_t V, const float *target, int target_ro
         if (!rejected && bonus) {
             const float *tl = target + ((int64_t)b * target_rows + np) * V;
             if ((status = ref_probabilities(s, tl, V, p))) break;
+            if (g_topp_margin < 1e-6f) res.flags |= REF_FLAG_TOPP_NEAR;
             uint32_t tokb = 0;
             float cm = INFINITY;
             if (uniforms && !ref_is_deterministic(s)) {
@@ -1313,6 +1336,46 @@ void ref_set_candidate_sink(uint32_t *ids, float *probs, int cap) {
     g_cand_cap = ids && probs ? cap : 0;
 }
 
+/* Per-round trace of the engines (test harness, single-threaded): the state a round
+   starts from (committed tokens, keystream position) and how close its decisions came
+   to flipping, so a device run can be compared round by round and restarted from the
+   oracle's state after a near-tie. */
+static ref_round *g_round_buf;
+static int g_round_cap;
+static int *g_round_count;
+
+void ref_set_round_sink(ref_round *buf, int cap, int *count) {
+    g_round_buf = buf;
+    g_round_cap = buf && count ? cap : 0;
+    g_round_count = count;
+    if (count) *count = 0;
+}
+
+static void round_margin_prob(ref_round *r, float m) {
+    if (m < r->prob_margin) r->prob_margin = m;
+}
+static void round_margin_logit(ref_round *r, float m) {
+    if (m < r->logit_gap) r->logit_gap = m;
+}
+/* margins of the distribution ref_probabilities just built */
+static void round_margin_filter(ref_round *r) {
+    round_margin_prob(r, g_topp_margin);
+    round_margin_logit(r, g_topk_gap);
+}
+static void round_begin(ref_round *r, int committed, const ref_rng *rng) {
+    memset(r, 0, sizeof(*r));
+    r->rng_pos_before = rng->pos;
+    r->committed_before = committed;
+    r->prob_margin = INFINITY;
+    r->logit_gap = INFINITY;
+}
+static void round_end(ref_round *r, int committed, const ref_rng *rng) {
+    r->committed_after = committed;
+    r->rng_pos_after = rng->pos;
+    if (g_round_count && *g_round_count < g_round_cap) g_round_buf[*g_round_count] = *r;
+    if (g_round_count) (*g_round_count)++;
+}
+
 void ref_top_candidates(const float *p, int64_t n, int k, uint32_t *ids, float *probs) {
     ranked_t *r = (ranked_t *)malloc(sizeof(ranked_t) * (size_t)n);
     for (int64_t i = 0; i < n; i++) r[i] = (ranked_t){p[i], i};
@@ -1391,6 +1454,8 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
         int count = K < remaining ? K : remaining;
         int base = kv->len;
         int np = 0;
+        ref_round rr;
+        round_begin(&rr, n_out, &rng);
         for (int pi = 0; pi < count; pi++) {
             const float *lg;
             if (pi == 0) {
@@ -1403,11 +1468,15 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
             if (ref_is_deterministic(s)) {
                 float gp = top2_gap(lg, V);
                 if (gp < min_gap) min_gap = gp;
+                round_margin_logit(&rr, gp);
             }
             if ((st = ref_probabilities(s, lg, V, dist + (int64_t)pi * V))) break;
+            round_margin_filter(&rr);
             uint32_t tok;
-            if ((st = ref_sample_probabilities(s, &rng, dist + (int64_t)pi * V, V, &tok, NULL, NULL)))
+            float cmp = INFINITY;
+            if ((st = ref_sample_probabilities(s, &rng, dist + (int64_t)pi * V, V, &tok, NULL, &cmp)))
                 break;
+            if (!ref_is_deterministic(s)) round_margin_prob(&rr, cmp);
             props[np++] = tok;
             stats->draft_tokens_proposed++;
             if (tok == EOS_ID) break;
@@ -1417,17 +1486,23 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
         stats->rounds++;
         stats->target_decode_forwards++;
         int rejected = 0, done = 0;
+        rr.proposed = np;
         for (int i = 0; i < np; i++) {
             const float *tl = i == 0 ? target_next : vlog + (int64_t)(i - 1) * V;
             if (ref_is_deterministic(s)) {
                 float gp = top2_gap(tl, V);
                 if (gp < min_gap) min_gap = gp;
+                round_margin_logit(&rr, gp);
             }
             if ((st = ref_probabilities(s, tl, V, pt))) break;
+            round_margin_filter(&rr);
             int acc = 0, drew = 0;
-            ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, NULL, NULL, &drew);
+            float ratio = 0.0f, u = 0.0f;
+            ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, &ratio, &u, &drew);
+            if (drew) round_margin_prob(&rr, fabsf(ratio - u));
             top_candidates(pt, V, 5, n_out);
             if (acc) {
+                rr.accepted++;
                 stats->draft_tokens_accepted++;
                 if (props[i] == EOS_ID) {
                     *finish_reason = REF_FINISH_EOS;
@@ -1446,8 +1521,10 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
             if (ref_is_deterministic(s)) {
                 if ((st = ref_sample_probabilities(s, &rng, pt, V, &repl, NULL, NULL))) break;
             } else {
+                float cmr = INFINITY;
                 if ((st = ref_residual(pt, dist + (int64_t)i * V, V, res))) break;
-                if ((st = ref_sample_probabilities(s, &rng, res, V, &repl, NULL, NULL))) break;
+                if ((st = ref_sample_probabilities(s, &rng, res, V, &repl, NULL, &cmr))) break;
+                round_margin_prob(&rr, cmr);
             }
             kv->len = base; /* target_cache.restore(snapshot) */
             if (repl == EOS_ID) {
@@ -1464,6 +1541,7 @@ int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
             memcpy(anchor, vhid + (int64_t)i * H, sizeof(float) * (size_t)H);
             break;
         }
+        if (!st) round_end(&rr, n_out, &rng);
         if (st || done) break;
         if (rejected) continue;
         memcpy(target_next, vlog + (int64_t)(np - 1) * V, sizeof(float) * (size_t)V);
@@ -1558,14 +1636,20 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
         int tbase = tkv->len, dbase = dkv->len; /* snapshots (restore = index rewind) */
         (void)committed;
         int np = 0;
+        ref_round rr;
+        round_begin(&rr, n_out, &rng);
         for (int pi = 0; pi < count; pi++) {
             if (det) {
                 float gp = top2_gap(draft_next, V);
                 if (gp < min_gap) min_gap = gp;
+                round_margin_logit(&rr, gp);
             }
             if ((st = ref_probabilities(s, draft_next, V, dist + (int64_t)pi * V))) break;
+            round_margin_filter(&rr);
             uint32_t tok;
-            if ((st = ref_sample_probabilities(s, &rng, dist + (int64_t)pi * V, V, &tok, NULL, NULL))) break;
+            float cmp = INFINITY;
+            if ((st = ref_sample_probabilities(s, &rng, dist + (int64_t)pi * V, V, &tok, NULL, &cmp))) break;
+            if (!det) round_margin_prob(&rr, cmp);
             props[np++] = tok;
             stats->draft_tokens_proposed++;
             if (tok == EOS_ID) break;
@@ -1581,18 +1665,24 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
         stats->target_decode_forwards++;
         pending = -1;
         int rejected = 0, done = 0;
+        rr.proposed = np;
         for (int i = 0; i < np; i++) {
             const float *tl = (hp || i > 0) ? vlog + (int64_t)(i - (hp ? 0 : 1)) * V : target_next;
             if (!hp && i == 0 && !have_target_next) { st = REF_ERR_CONFIG; break; }
             if (det) {
                 float gp = top2_gap(tl, V);
                 if (gp < min_gap) min_gap = gp;
+                round_margin_logit(&rr, gp);
             }
             if ((st = ref_probabilities(s, tl, V, pt))) break;
+            round_margin_filter(&rr);
             int acc = 0, drew = 0;
-            ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, NULL, NULL, &drew);
+            float ratio = 0.0f, u = 0.0f;
+            ref_accept_proposal(s, &rng, props[i], dist + (int64_t)i * V, pt, V, &acc, &ratio, &u, &drew);
+            if (drew) round_margin_prob(&rr, fabsf(ratio - u));
             top_candidates(pt, V, 5, n_out);
             if (acc) {
+                rr.accepted++;
                 stats->draft_tokens_accepted++;
                 if (props[i] == EOS_ID) {
                     *finish_reason = REF_FINISH_EOS;
@@ -1611,8 +1701,10 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
             if (det) {
                 if ((st = ref_sample_probabilities(s, &rng, pt, V, &repl, NULL, NULL))) break;
             } else {
+                float cmr = INFINITY;
                 if ((st = ref_residual(pt, dist + (int64_t)i * V, V, res))) break;
-                if ((st = ref_sample_probabilities(s, &rng, res, V, &repl, NULL, NULL))) break;
+                if ((st = ref_sample_probabilities(s, &rng, res, V, &repl, NULL, &cmr))) break;
+                round_margin_prob(&rr, cmr);
             }
             tkv->len = tbase; /* target_cache.restore */
             dkv->len = dbase; /* draft_cache.restore */
@@ -1633,7 +1725,9 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
             pending = (int)repl;
             break;
         }
-        if (st || done) break;
+        if (st) break;
+        if (done || rejected || n_out == max_new) round_end(&rr, n_out, &rng);
+        if (done) break;
         if (rejected) {
             have_target_next = 0;
             continue;
@@ -1644,16 +1738,22 @@ int ref_spec_generate(const ref_model *tm, const ref_model *dm, const uint32_t *
         if (det) {
             float gp = top2_gap(bl, V);
             if (gp < min_gap) min_gap = gp;
+            round_margin_logit(&rr, gp);
         }
         if ((st = ref_probabilities(s, bl, V, pt))) break;
+        round_margin_filter(&rr);
         top_candidates(pt, V, 5, n_out);
         uint32_t bonus;
-        if ((st = ref_sample_probabilities(s, &rng, pt, V, &bonus, NULL, NULL))) break;
+        float cmb = INFINITY;
+        if ((st = ref_sample_probabilities(s, &rng, pt, V, &bonus, NULL, &cmb))) break;
+        if (!det) round_margin_prob(&rr, cmb);
         if (bonus == EOS_ID) {
             *finish_reason = REF_FINISH_EOS;
+            round_end(&rr, n_out, &rng);
             break;
         }
         out_tokens[n_out++] = bonus;
+        round_end(&rr, n_out, &rng);
         if ((st = ref_forward(dm, dkv, &bonus, 1, dkv->len, draft_next, NULL, nt))) break;
         stats->draft_decode_forwards++;
         pending = (int)bonus;

@@ -66,7 +66,12 @@ typedef struct {
     float cdf_margin;     /* |u - cdf| distance at the final sample (inf if none) */
 } ref_accept_result;
 
-enum { REF_FLAG_RATIO_NEAR = 1u, REF_FLAG_CDF_NEAR = 2u, REF_FLAG_ARGMAX_NEAR = 4u };
+enum { REF_FLAG_RATIO_NEAR = 1u, REF_FLAG_CDF_NEAR = 2u, REF_FLAG_ARGMAX_NEAR = 4u, REF_FLAG_TOPP_NEAR = 8u };
+
+/* Margins of the last ref_probabilities call on this thread: top-p cumulative vs top_p
+   at the crossing, and the k-th vs (k+1)-th ranked logit gap (INFINITY when unused). */
+float ref_last_topp_margin(void);
+float ref_last_topk_gap(void);
 
 int ref_accept_batch(int B, int K, int64_t V, const float *target, int target_rows,
                      const float *draft, const uint32_t *draft_tokens, const int32_t *n_proposals,
@@ -142,6 +147,20 @@ typedef struct {
 } ref_spec_stats;
 
 enum { REF_FINISH_MAX_TOKENS = 0, REF_FINISH_EOS = 1, REF_FINISH_CONTEXT_LIMIT = 2 };
+
+/* One engine round (test diagnostics): start state, outcome and decision margins. */
+typedef struct {
+    uint64_t rng_pos_before;   /* keystream word position when the round starts */
+    uint64_t rng_pos_after;
+    int32_t committed_before;  /* tokens committed before the round */
+    int32_t committed_after;
+    int32_t proposed, accepted;
+    float prob_margin;         /* min |p/q - u|, |cdf - u| (proposal, residual, bonus draws), top-p margin */
+    float logit_gap;           /* min top-2 logit gap (greedy) or top-k boundary gap (sampled) */
+} ref_round;
+/* Rounds of subsequent ref_mtp_generate / ref_spec_generate calls go to buf[0..cap);
+   *count receives the number of rounds run.  buf = NULL turns the trace off. */
+void ref_set_round_sink(ref_round *buf, int cap, int *count);
 
 int ref_mtp_generate(const ref_model *m, const uint32_t *prompt, int prompt_len,
                      int max_new_tokens, int num_draft_tokens, const ref_sampler *s,

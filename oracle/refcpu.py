@@ -15,7 +15,7 @@ REF_OK, REF_ERR_CONFIG, REF_ERR_SHAPE, REF_ERR_UNSUPPORTED = 0, 1, 2, 3
 W_F32, W_BF16, W_INT8_ROW, W_INT4_G128 = 0, 1, 2, 3
 KV_F32, KV_F16, KV_INT8 = 0, 1, 2
 T_NORM, T_LINEAR, T_EMBED = 0, 1, 2
-FLAG_RATIO_NEAR, FLAG_CDF_NEAR, FLAG_ARGMAX_NEAR = 1, 2, 4
+FLAG_RATIO_NEAR, FLAG_CDF_NEAR, FLAG_ARGMAX_NEAR, FLAG_TOPP_NEAR = 1, 2, 4, 8
 FINISH_MAX_TOKENS, FINISH_EOS, FINISH_CONTEXT_LIMIT = 0, 1, 2
 
 
@@ -32,6 +32,18 @@ class RefSampler(C.Structure):
 class RefAcceptResult(C.Structure):
     _fields_ = [("accept_len", C.c_int32), ("token", C.c_int32), ("flags", C.c_uint32),
                 ("draws", C.c_int32), ("ratio_margin", C.c_float), ("cdf_margin", C.c_float)]
+
+
+class RefRound(C.Structure):
+    """One engine round: start state (committed tokens, keystream position), outcome and
+    the smallest distance of any of its decisions to the boundary that would flip it."""
+    _fields_ = [("rng_pos_before", C.c_uint64), ("rng_pos_after", C.c_uint64),
+                ("committed_before", C.c_int32), ("committed_after", C.c_int32),
+                ("proposed", C.c_int32), ("accepted", C.c_int32),
+                ("prob_margin", C.c_float), ("logit_gap", C.c_float)]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
 
 
 class RefConfig(C.Structure):
@@ -137,6 +149,9 @@ def lib():
                                         C.POINTER(C.c_int), C.POINTER(RefSpecStats), C.POINTER(C.c_float)]),
         "ref_top_candidates": (None, [F32P, C.c_int64, C.c_int, U32P, F32P]),
         "ref_set_candidate_sink": (None, [C.c_void_p, C.c_void_p, C.c_int]),
+        "ref_set_round_sink": (None, [C.c_void_p, C.c_int, C.c_void_p]),
+        "ref_last_topp_margin": (C.c_float, []),
+        "ref_last_topk_gap": (C.c_float, []),
         "ref_lat_create": (C.c_void_p, [C.POINTER(RefLatConfig)]),
         "ref_lat_free": (None, [C.c_void_p]),
         "ref_lat_num_tensors": (C.c_int, [C.c_void_p]),
@@ -201,12 +216,16 @@ def argmax(v):
     return int(lib().ref_argmax(np.ascontiguousarray(v, np.float32), len(v)))
 
 
-def probabilities(s, logits):
+def probabilities(s, logits, margins=False):
+    """Sampler::probabilities (sampler.rs:102-118); with margins=True also returns the
+    top-p cumulative margin and the top-k boundary logit gap of the filter."""
     logits = np.ascontiguousarray(logits, np.float32)
     out = np.zeros_like(logits)
     st = lib().ref_probabilities(C.byref(s), logits, len(logits), out)
     if st:
         raise ValueError(f"probabilities failed: status {st}")
+    if margins:
+        return out, float(lib().ref_last_topp_margin()), float(lib().ref_last_topk_gap())
     return out
 
 
@@ -421,15 +440,28 @@ class Model:
         lib().ref_set_candidate_sink(None, None, 0)
         self.last_candidates = (ids[:n].copy(), probs[:n].copy())
 
+    def _round_sink(self, max_new):
+        """Record the rounds of the next engine call in self.last_rounds (list of dicts)."""
+        buf = (RefRound * (max(max_new, 1) + 2))()
+        cnt = C.c_int(0)
+        lib().ref_set_round_sink(C.cast(buf, C.c_void_p), len(buf), C.addressof(cnt))
+        return buf, cnt
+
+    def _round_unsink(self, buf, cnt):
+        lib().ref_set_round_sink(None, 0, None)
+        self.last_rounds = [buf[i].as_dict() for i in range(min(cnt.value, len(buf)))]
+
     def mtp_generate(self, prompt, max_new, num_draft, s, seed=0, nthreads=8):
         prompt = np.ascontiguousarray(prompt, np.uint32)
         out = np.zeros(max(max_new, 1), np.uint32)
         n, fin, gap = C.c_int(), C.c_int(), C.c_float()
         stats = RefSpecStats()
         ci, cp = self._sink(max_new)
+        rb, rc = self._round_sink(max_new)
         st = lib().ref_mtp_generate(self.h, prompt, len(prompt), max_new, num_draft, C.byref(s), seed,
                                     nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
         self._unsink(ci, cp, n.value)
+        self._round_unsink(rb, rc)
         if st:
             raise ValueError(f"mtp_generate failed: {st}")
         return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value
@@ -442,9 +474,11 @@ class Model:
         n, fin, gap = C.c_int(), C.c_int(), C.c_float()
         stats = RefSpecStats()
         ci, cp = self._sink(max_new)
+        rb, rc = self._round_sink(max_new)
         st = lib().ref_spec_generate(self.h, draft.h, prompt, len(prompt), max_new, num_draft, C.byref(s), seed,
                                      nthreads, out, C.byref(n), C.byref(fin), C.byref(stats), C.byref(gap))
         self._unsink(ci, cp, n.value)
+        self._round_unsink(rb, rc)
         if st:
             raise ValueError(f"spec_generate failed: {st}")
         return out[:n.value].copy(), fin.value, stats.as_dict(), gap.value

@@ -36,9 +36,10 @@ def c2_inputs(B=32, K=4, V=32000, T=0.8, seed=0):
     return tgt, drf, toks
 
 
-def run_both(ctx, tgt, drf, toks, T, bonus, seeds=None, offsets=None, uniforms=None, nprop=None, greedy=False):
-    s_dev = A.Sampler.greedy_sampler() if greedy else A.Sampler.top_k_top_p(T)
-    s_ref = R.sampler(greedy=True) if greedy else R.sampler(temperature=T)
+def run_both(ctx, tgt, drf, toks, T, bonus, seeds=None, offsets=None, uniforms=None, nprop=None, greedy=False,
+             top_k=0, top_p=0.0):
+    s_dev = A.Sampler.greedy_sampler() if greedy else A.Sampler.top_k_top_p(T, top_k=top_k, top_p=top_p)
+    s_ref = R.sampler(greedy=True) if greedy else R.sampler(temperature=T, top_k=top_k, top_p=top_p)
     t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a).astype(dt)).to(DEV)
     out = ctx.accept_sample(t(tgt, np.float32), t(drf, np.float32), t(toks, np.int32), s_dev, bonus,
                             seeds=t(seeds, np.int64), word_offsets=t(offsets, np.int64),
@@ -191,3 +192,99 @@ def test_top_candidates_bit_exact(ctx, greedy):
         for k in range(5):
             if ids[r][k] != wi[k]:
                 assert abs(int(wp[k].view(np.int32)) - int(probs[r][k].view(np.int32))) <= 2, (r, k)
+
+
+# ---------------------------------------------------------------------------
+# top-k / top-p (filtered_probs, sampler.rs:226-278) and long vocabularies
+# ---------------------------------------------------------------------------
+def test_cli_default_sampler_on_c2_shapes(ctx):
+    """The reference CLI's sampled speculation (infer.rs:72-77: T 0.7, top_k 50,
+    top_p 0.9) on C2 shapes: accepted lengths, tokens and draws bit-identical to the
+    oracle except on flagged draws (including a top-p cumulative within 1e-6 of p)."""
+    tgt, drf, toks = c2_inputs(B=32, K=4, V=32000, T=0.7, seed=11)
+    B = tgt.shape[0]
+    # draft tokens from the filtered draft distribution, as the engine proposes them
+    s = R.sampler(temperature=0.7, top_k=50, top_p=0.9)
+    for b in range(B):
+        r = R.Rng(20_000 + b)
+        for i in range(4):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    out, ref = run_both(ctx, tgt, drf, toks, 0.7, True, seeds=np.arange(B, dtype=np.uint64) + 3, top_k=50,
+                        top_p=0.9)
+    flagged = assert_parity(out, ref)
+    assert np.array_equal(out["draws"][~flagged], ref["draws"][~flagged])
+    assert (ref["accept_len"] < 4).any() and (ref["accept_len"] > 0).any()
+
+
+@pytest.mark.parametrize("top_k,top_p", [(50, 0.0), (0, 0.9), (1, 0.0), (700, 0.95), (31999, 0.5)])
+def test_top_k_top_p_variants_match_oracle(ctx, top_k, top_p):
+    """top-k alone, top-p alone (several top-p pages of 4096 sorted candidates on
+    the flat rows), k = 1, and both, on peaked N(0, 3^2) and flat N(0, 0.3^2) rows."""
+    rng = np.random.default_rng(12 + top_k)
+    B, K, V = 8, 3, 32000
+    sc = np.where(np.arange(B) % 2 == 0, 3.0, 0.3).astype(np.float32)[:, None, None]
+    tgt = (rng.normal(0, 1, (B, K + 1, V)) * sc).astype(np.float32)
+    drf = (tgt[:, :K] + rng.normal(0, 0.5, (B, K, V)) * sc).astype(np.float32)
+    s = R.sampler(temperature=0.9, top_k=top_k, top_p=top_p)
+    toks = np.zeros((B, K), np.uint32)
+    for b in range(B):
+        r = R.Rng(30_000 + b)
+        for i in range(K):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    for bonus in (True, False):
+        out, ref = run_both(ctx, tgt, drf, toks, 0.9, bonus, seeds=np.arange(B, dtype=np.uint64), top_k=top_k,
+                            top_p=top_p)
+        # flat rows keep ~28k tokens whose increments near the top-p cut are ~1e-5, so
+        # a cut within 1e-6 of p (flagged) is common there; flagged or not, the
+        # outcomes must still agree on nearly every sequence
+        assert_parity(out, ref, max_flag_frac=0.6)
+        same = (out["accept_len"] == ref["accept_len"]) & (out["token"] == ref["token"])
+        assert same.mean() >= 0.85
+
+
+def test_top_k_keeps_lower_index_among_ties(ctx):
+    """Stable total_cmp ranking: among equal logits at the top-k boundary the lower
+    token ids are kept (sampler.rs:238-245), so the bonus draw can only land on them."""
+    V = 1024
+    l = np.full(V, -5.0, np.float32)
+    l[[10, 20, 30, 40, 50]] = 2.0  # five-way tie, top_k = 3 keeps 10, 20, 30
+    tgt = np.broadcast_to(l, (256, 1, V)).copy()
+    out, ref = run_both(ctx, tgt, np.zeros((256, 0, V), np.float32), np.zeros((256, 0), np.uint32), 1.0, True,
+                        seeds=np.arange(256, dtype=np.uint64), top_k=3)
+    assert_parity(out, ref)
+    assert set(out["token"].tolist()) == {10, 20, 30}
+
+
+def test_long_vocabulary_rows_are_scanned_in_chunks(ctx):
+    """V = 128 000 (beyond one LDS chunk of 32 768): softmax normaliser, residual
+    mass and CDF carried across chunks, bit-identical to the oracle."""
+    tgt, drf, toks = c2_inputs(B=6, K=3, V=128000, T=0.8, seed=13)
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, True, seeds=np.arange(6, dtype=np.uint64) + 50)
+    assert_parity(out, ref)
+    assert np.array_equal(out["draws"], ref["draws"])
+    out, ref = run_both(ctx, tgt, drf, toks, 0.8, False, seeds=np.arange(6, dtype=np.uint64) + 50, top_k=40,
+                        top_p=0.9)
+    assert_parity(out, ref, max_flag_frac=0.34)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(50, 0.9), (0, 0.8), (3, 0.0)])
+def test_top_candidates_of_filtered_distributions(ctx, top_k, top_p):
+    """Candidates of the filtered distribution (mtp_speculative.rs:247-250 pass the
+    target distribution, i.e. after top-k / top-p): dropped tokens carry probability 0
+    and ids equal the oracle's up to 2-ulp rounding swaps."""
+    rng = np.random.default_rng(14)
+    rows = np.concatenate([rng.normal(0, 3, (6, 32000)), rng.normal(0, 0.3, (2, 32000))]).astype(np.float32)
+    s_ref = R.sampler(temperature=0.7, top_k=top_k, top_p=top_p)
+    s_dev = A.Sampler.top_k_top_p(0.7, top_k=top_k, top_p=top_p)
+    ids, probs = ctx.top_candidates(torch.from_numpy(rows).to(DEV), s_dev, 5)
+    ids, probs = ids.cpu().numpy().astype(np.uint32), probs.cpu().numpy()
+    for r in range(rows.shape[0]):
+        p, tm, _ = R.probabilities(s_ref, rows[r], margins=True)
+        if tm < 1e-6:
+            continue  # top-p cut within rounding of p: the kept sets may differ
+        wi, wp = R.top_candidates(p, 5)
+        ulps = np.abs(probs[r].view(np.int32).astype(np.int64) - wp.view(np.int32).astype(np.int64))
+        assert ulps.max() <= 2, (r, ulps, probs[r], wp)
+        for k in range(5):
+            if ids[r][k] != wi[k]:
+                assert wp[k] == 0.0 or ulps[k] <= 2, (r, k)

@@ -176,3 +176,55 @@ def test_accept_batch_explicit_uniforms_equal_stream():
     uni = np.array([[R.Rng(int(seeds[b]), i).next_f32() for i in range(K + 1)] for b in range(B)], np.float32)
     b_ = R.accept_batch(tgt, dft, toks, s, bonus=True, uniforms=uni)
     assert np.array_equal(a["accept_len"], b_["accept_len"]) and np.array_equal(a["token"], b_["token"])
+
+
+def test_top_k_ties_keep_lower_indices():
+    """Stable sort (slice::sort_by is stable): equal logits at the boundary keep the
+    lower token ids (sampler.rs:238-245)."""
+    s = R.sampler(temperature=1.0, top_k=2)
+    p, _, gap = R.probabilities(s, [1.0, 3.0, 3.0, 3.0, 2.0], margins=True)
+    assert p[1] == p[2] == np.float32(0.5) and p[0] == p[3] == p[4] == 0.0
+    assert gap == 0.0  # the 2nd and 3rd ranked logits tie
+    s = R.sampler(temperature=1.0, top_k=3)
+    p = R.probabilities(s, [float("nan"), 5.0, 4.0, 3.0])
+    # NaN ranks highest under total_cmp and takes a top-k slot, but softmax drops it (non-finite)
+    assert p[0] == 0.0 and p[3] == 0.0 and p[1] > p[2] > 0.0
+
+
+def test_top_p_ties_and_exact_boundary():
+    """Equal probabilities are ranked by ascending index; the cumulative sum stops at
+    the first element with cumulative >= top_p (sampler.rs:268-275)."""
+    s = R.sampler(temperature=1.0, top_p=0.5)
+    p, margin, _ = R.probabilities(s, np.zeros(4, np.float32), margins=True)
+    assert list(p) == [0.5, 0.5, 0.0, 0.0]  # 0.25 + 0.25 == 0.5 exactly
+    assert margin == 0.0
+
+
+def test_top_p_against_stable_sort_brute_force():
+    """filtered_probs top-p against numpy's stable argsort and float32 sequential
+    cumsum (np.cumsum accumulates left to right in the requested dtype)."""
+    rng = np.random.default_rng(3)
+    for trial in range(20):
+        V = int(rng.integers(2, 3000))
+        logits = (rng.normal(0, rng.choice([0.3, 3.0]), V)).astype(np.float32)
+        if trial % 4 == 0:
+            logits = np.round(logits)  # many exact ties
+        top_p = float(rng.choice([0.3, 0.8, 0.9, 0.99]))
+        s = R.sampler(temperature=0.7, top_p=top_p)
+        p0 = R.probabilities(R.sampler(temperature=0.7), logits)
+        order = np.argsort(-p0, kind="stable")
+        cum = np.cumsum(p0[order], dtype=np.float32)
+        hit = np.nonzero(cum >= np.float32(top_p))[0]
+        n_keep = int(hit[0]) + 1 if hit.size else V
+        keep = np.zeros(V, bool)
+        keep[order[:n_keep]] = True
+        kept = np.where(keep, p0, np.float32(0))
+        tot = np.float32(0)
+        for v in kept:
+            tot = np.float32(tot + v)
+        want = (kept / tot).astype(np.float32)
+        got, margin, _ = R.probabilities(s, logits, margins=True)
+        assert np.array_equal(got, want), trial
+        if hit.size:
+            prev = cum[hit[0] - 1] if hit[0] > 0 else np.float32(0)
+            assert margin == min(cum[hit[0]] - np.float32(top_p), np.float32(top_p) - prev)
