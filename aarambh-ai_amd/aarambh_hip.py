@@ -117,6 +117,8 @@ def lib():
         "aarh_mtp_head": (C.c_int, [_P, C.c_int, _P, _P, C.c_int, _P]),
         "aarh_accept_sample": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.POINTER(_Sampler), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+        "aarh_accept_sample_static": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                                C.POINTER(_Sampler), _P, _P, _P, _P, _P, _P, _P, _P, _P]),
         "aarh_mtp_generate": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
                                         _P, _P, _P, C.POINTER(_Stats)]),
         "aarh_session_begin": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler),
@@ -167,7 +169,7 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
             "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs", "aarh_session_rng_offsets",
-            "aarh_session_set_rng_offsets",
+            "aarh_session_set_rng_offsets", "aarh_accept_sample_static",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -414,9 +416,10 @@ class HipModel:
         return ids, probs
 
     def accept_sample(self, target, draft, draft_tokens, sampler, bonus, seeds=None, word_offsets=None,
-                      uniforms=None, n_proposals=None):
+                      uniforms=None, n_proposals=None, no_alloc=False):
         """Acceptance on device tensors (torch cuda tensors).  target [B, Kt, V] f32,
-        draft [B, K, V] f32, draft_tokens [B, K] int32.  Returns a dict of torch tensors."""
+        draft [B, K, V] f32, draft_tokens [B, K] int32.  Returns a dict of torch tensors.
+        no_alloc=True calls aarh_accept_sample_static (statically allocated scratch)."""
         import torch
         B, K, V = draft.shape if draft is not None else (target.shape[0], 0, target.shape[2])
         dev = target.device
@@ -427,11 +430,11 @@ class HipModel:
             return None if t is None else C.c_void_p(t.data_ptr())
 
         torch.cuda.synchronize(dev)
-        st = lib().aarh_accept_sample(self.h, p(target), target.shape[1], p(draft), p(draft_tokens),
-                                      p(n_proposals), B, K, V, 1 if bonus else 0, C.byref(sampler._c()),
-                                      p(seeds), p(word_offsets), p(uniforms), p(outs["accept_len"]),
-                                      p(outs["token"]), p(outs["flags"]), p(outs["draws"]), p(outs["status"]),
-                                      None)
+        fn = lib().aarh_accept_sample_static if no_alloc else lib().aarh_accept_sample
+        st = fn(self.h, p(target), target.shape[1], p(draft), p(draft_tokens), p(n_proposals), B, K, V,
+                1 if bonus else 0, C.byref(sampler._c()), p(seeds), p(word_offsets), p(uniforms),
+                p(outs["accept_len"]), p(outs["token"]), p(outs["flags"]), p(outs["draws"]), p(outs["status"]),
+                None)
         self._check(st)
         self.sync()
         return outs

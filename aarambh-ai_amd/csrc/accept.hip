@@ -678,6 +678,60 @@ int launch_accept(const AcceptArgs& a_in, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
+// Statically allocated scratch for aarh_accept_sample_static: the row statistics
+// and arrival counters of one call, in device memory owned by the library from
+// load to process exit (one copy per GPU).  Host code never uses the symbol's
+// name as an address; accept_static_scratch() returns the device address that
+// hipGetSymbolAddress reported for the current device at set-up.
+// ---------------------------------------------------------------------------
+static constexpr size_t ACC_STATIC_WORDS = (size_t)ACC_STATIC_ROWS * ACC_RS_WORDS + ACC_STATIC_SEQS;
+static __device__ __align__(256) uint32_t scratch[ACC_STATIC_WORDS];
+
+static constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static uint32_t* g_scratch_ptr[MAX_DEVICES];
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+int accept_static_init(int device, hipStream_t stream) {
+    if (device < 0 || device >= MAX_DEVICES) return 3;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (g_scratch_ptr[device]) return 0;
+    void* p = nullptr;
+    if (note_error(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))) return 4;
+    if (!p) return 4;
+    // counters start at zero (the kernel re-arms them after every call)
+    uint32_t* cnt = (uint32_t*)p + (size_t)ACC_STATIC_ROWS * ACC_RS_WORDS;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((ACC_STATIC_SEQS + 255) / 256), dim3(256), 0, stream, cnt,
+                       ACC_STATIC_SEQS);
+    if (note_error(hipGetLastError())) return 4;
+    if (note_error(hipStreamSynchronize(stream))) return 4;
+    g_scratch_ptr[device] = (uint32_t*)p;
+    return 0;
+}
+
+int accept_static_scratch(int device, uint32_t** rstat, unsigned** counters) {
+    if (device < 0 || device >= MAX_DEVICES) return 3;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    uint32_t* p = g_scratch_ptr[device];
+    if (!p) return 4;
+    *rstat = p;
+    *counters = p + (size_t)ACC_STATIC_ROWS * ACC_RS_WORDS;
+    return 0;
+}
+
+int launch_zero_u32(uint32_t* p, int n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, p, n);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// ---------------------------------------------------------------------------
 // Sampler::top_candidates_from_probabilities (sampler.rs:188-208) of each row's
 // distribution as the engines build it (Sampler::probabilities, sampler.rs:
 // 102-118): a stable descending sort truncated to n, i.e. the n largest

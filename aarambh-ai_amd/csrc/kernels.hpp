@@ -37,6 +37,9 @@ enum { ACCEPT_FLAG_RATIO_NEAR = 1u, ACCEPT_FLAG_CDF_NEAR = 2u, ACCEPT_FLAG_TOPP_
 // Acceptance scratch: ACC_RS_WORDS 32-bit words of distribution parameters per
 // logits row, and one arrival counter per sequence (zero between launches).
 static constexpr int ACC_RS_WORDS = 12;
+// Capacity of the statically allocated scratch of aarh_accept_sample_static.
+static constexpr int ACC_STATIC_ROWS = 4096;
+static constexpr int ACC_STATIC_SEQS = 1024;
 
 // Dynamic LDS a kernel may request: 160 KiB per workgroup on gfx950 minus room
 // for the kernels' static LDS.
@@ -223,6 +226,11 @@ struct CandArgs {
     float* probs;         // [rows][n]
 };
 int launch_candidates(const CandArgs& a, hipStream_t stream);
+// Statically allocated acceptance scratch (one copy per GPU): set-up on `device`
+// (current) resolves its address once; accept_static_scratch returns it.
+int accept_static_init(int device, hipStream_t stream);
+int accept_static_scratch(int device, uint32_t** rstat, unsigned** counters);
+int launch_zero_u32(uint32_t* p, int n, hipStream_t stream);
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
 // Many-row variant (M > 16, fragments with mp = 16, all rows in one launch).
 int launch_gemm(const GemvArgs& a, hipStream_t stream);

@@ -726,6 +726,9 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     *out = c;
     if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    // the statically allocated acceptance scratch of this device (once per device)
+    if (accept_static_init(device, c->stream))
+        return fail(c, AARH_ERR_DEVICE, "static acceptance scratch set-up failed: %s", last_launch_error());
     c->layers.resize(g.n_layers);
     c->heads.resize(c->nheads_mtp);
     build_slots(c);
@@ -1130,51 +1133,94 @@ static int ensure_accept_scratch(aarh_ctx* c, int B, int rows_per_seq) {
     return 0;
 }
 
+// Validated argument block of an acceptance launch (scratch pointers left empty).
+static int accept_args(aarh_ctx* c, const float* target, int target_rows, const float* draft,
+                       const uint32_t* draft_tokens, const int32_t* n_proposals, int B, int K, int V, int bonus,
+                       const aarh_sampler* s, const uint64_t* seeds, const uint64_t* word_offsets,
+                       const float* uniforms, int32_t* accept_len, int32_t* token, uint32_t* flags, int32_t* draws,
+                       int32_t* status, AcceptArgs* a) {
+    if (B <= 0 || K < 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0))
+        return fail(c, AARH_ERR_SHAPE, "bad acceptance shape B=%d K=%d V=%d rows=%d", B, K, V, target_rows);
+    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
+    if (!greedy && !(s->top_p >= 0.0f && s->top_p <= 1.0f))
+        return fail(c, AARH_ERR_CONFIG, "top_p must be in [0, 1]");
+    *a = AcceptArgs{};
+    a->target = target;
+    a->target_rows = target_rows;
+    a->draft = draft;
+    a->draft_tokens = draft_tokens;
+    a->n_proposals = n_proposals;
+    a->B = B;
+    a->K = K;
+    a->V = V;
+    a->bonus = bonus ? 1 : 0;
+    a->greedy = greedy ? 1 : 0;
+    a->temperature = s->temperature;
+    a->top_k = s->top_k;
+    a->top_p = s->top_p;
+    a->seeds = seeds;
+    a->word_offsets = word_offsets;
+    a->uniforms = uniforms;
+    a->out_accept_len = accept_len;
+    a->out_token = token;
+    a->out_flags = flags;
+    a->out_draws = draws;
+    a->out_status = status;
+    return 0;
+}
+
 int aarh_accept_sample(aarh_ctx* c, const float* target, int target_rows, const float* draft,
                        const uint32_t* draft_tokens, const int32_t* n_proposals, int B, int K, int V, int bonus,
                        const aarh_sampler* s, const uint64_t* seeds, const uint64_t* word_offsets,
                        const float* uniforms, int32_t* accept_len, int32_t* token, uint32_t* flags, int32_t* draws,
                        int32_t* status, void* stream) {
     if (!c || !s) return AARH_ERR_CONFIG;
-    if (B <= 0 || K < 0 || V <= 0 || target_rows < K + (bonus ? 1 : 0))
-        return fail(c, AARH_ERR_SHAPE, "bad acceptance shape B=%d K=%d V=%d rows=%d", B, K, V, target_rows);
-    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
-    if (!greedy && !(s->top_p >= 0.0f && s->top_p <= 1.0f))
-        return fail(c, AARH_ERR_CONFIG, "top_p must be in [0, 1]");
+    AcceptArgs a;
+    int r = accept_args(c, target, target_rows, draft, draft_tokens, n_proposals, B, K, V, bonus, s, seeds,
+                        word_offsets, uniforms, accept_len, token, flags, draws, status, &a);
+    if (r) return r;
     if (ensure_accept_scratch(c, B, target_rows + K)) return AARH_ERR_DEVICE;
-    AcceptArgs a{};
-    a.target = target;
-    a.target_rows = target_rows;
-    a.draft = draft;
-    a.draft_tokens = draft_tokens;
-    a.n_proposals = n_proposals;
-    a.B = B;
-    a.K = K;
-    a.V = V;
-    a.bonus = bonus ? 1 : 0;
-    a.greedy = greedy ? 1 : 0;
-    a.temperature = s->temperature;
-    a.top_k = s->top_k;
-    a.top_p = s->top_p;
-    a.seeds = seeds;
-    a.word_offsets = word_offsets;
-    a.uniforms = uniforms;
     a.rstat = c->acc_rstat;
     a.counters = c->acc_cnt;
-    a.out_accept_len = accept_len;
-    a.out_token = token;
-    a.out_flags = flags;
-    a.out_draws = draws;
-    a.out_status = status;
     hipStream_t st = stream ? (hipStream_t)stream : c->stream;
     hipStream_t saved = c->stream;
     c->stream = st;
-    int r;
     {
         ProfScope ps(c, AARH_PROF_ACCEPT, (double)B * (target_rows + K) * V * 4.0);
         r = launch_accept(a, st);
     }
     c->stream = saved;
+    if (r) return fail(c, r, "acceptance launch failed: %d %s", r, last_launch_error());
+    return 0;
+}
+
+// The same acceptance without any allocation: row statistics and arrival counters
+// live in the library's statically allocated per-GPU scratch (accept.hip), whose
+// device address aarh_create resolved.  Calls that overlap on one GPU share it and race.
+int aarh_accept_sample_static(aarh_ctx* c, const float* target, int target_rows, const float* draft,
+                              const uint32_t* draft_tokens, const int32_t* n_proposals, int B, int K, int V,
+                              int bonus, const aarh_sampler* s, const uint64_t* seeds, const uint64_t* word_offsets,
+                              const float* uniforms, int32_t* accept_len, int32_t* token, uint32_t* flags,
+                              int32_t* draws, int32_t* status, void* stream) {
+    if (!c || !s) return AARH_ERR_CONFIG;
+    AcceptArgs a;
+    int r = accept_args(c, target, target_rows, draft, draft_tokens, n_proposals, B, K, V, bonus, s, seeds,
+                        word_offsets, uniforms, accept_len, token, flags, draws, status, &a);
+    if (r) return r;
+    if (B > ACC_STATIC_SEQS || (long long)B * (target_rows + K) > ACC_STATIC_ROWS)
+        return fail(c, AARH_ERR_SHAPE,
+                    "acceptance of %d sequences x %d logits rows exceeds the static scratch (%d sequences, %d rows)",
+                    B, target_rows + K, ACC_STATIC_SEQS, ACC_STATIC_ROWS);
+    uint32_t* rstat = nullptr;
+    unsigned* cnt = nullptr;
+    if (accept_static_scratch(c->device, &rstat, &cnt))
+        return fail(c, AARH_ERR_DEVICE, "static acceptance scratch is not set up on device %d", c->device);
+    a.rstat = rstat;
+    a.counters = cnt;
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    // this call's arrival counters start at zero whatever the last call left
+    r = launch_zero_u32(cnt, B, st);
+    if (!r) r = launch_accept(a, st);
     if (r) return fail(c, r, "acceptance launch failed: %d %s", r, last_launch_error());
     return 0;
 }

@@ -134,6 +134,19 @@ int aarh_accept_sample(aarh_ctx *ctx, const float *target, int target_rows, cons
                        const uint64_t *word_offsets, const float *uniforms, int32_t *accept_len,
                        int32_t *token, uint32_t *flags, int32_t *draws, int32_t *status, void *stream);
 
+/* aarh_accept_sample without any allocation.  No counterpart in the reference: it is for
+   callers that cannot allocate device memory (HIP graph capture, serving loops that forbid
+   hipMalloc).  Same arguments and results as aarh_accept_sample; its scratch (row statistics,
+   arrival counters) is a statically allocated per-GPU block of the library holding at most
+   1024 sequences and 4096 logits rows (B * (target_rows + K)); larger calls fail with
+   AARH_ERR_SHAPE.  Every call on one GPU shares that block: calls that overlap on one GPU
+   (other streams, other threads, other contexts) race. */
+int aarh_accept_sample_static(aarh_ctx *ctx, const float *target, int target_rows, const float *draft,
+                              const uint32_t *draft_tokens, const int32_t *n_proposals, int B, int K, int V,
+                              int bonus, const aarh_sampler *sampler, const uint64_t *seeds,
+                              const uint64_t *word_offsets, const float *uniforms, int32_t *accept_len,
+                              int32_t *token, uint32_t *flags, int32_t *draws, int32_t *status, void *stream);
+
 /* --- engine (MtpSpeculativeEngine::generate_with_callback, inference/src/mtp_speculative.rs:86-336)
    for nseq independent requests run in lock-step rounds on slots 0..nseq-1.
    prompts [nseq][prompt_len]; out_tokens [nseq][max_new_tokens]. */
