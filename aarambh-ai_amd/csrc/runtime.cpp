@@ -1445,8 +1445,6 @@ int session_round(aarh_session* e) {
         if (p > 0) {
             if ((r = mtp_head_dev(c, p - 1, e->anchor, H, e->props, K, nseq, e->drf + (size_t)p * V, (long long)K * V)))
                 return r;
-            for (int b = 0; b < nseq; b++)
-                if (!e->finished[b] && e->count[b] > p) e->stats[b].mtp_head_forwards++;
         }
         if (e->greedy) {
             KCHK(c, launch_argmax_rows(e->drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)e->props + p, K,
@@ -1484,6 +1482,9 @@ int session_round(aarh_session* e) {
             }
         }
         e->hnp[b] = np;
+        // heads ran in lock-step for every row; the reference stops proposing after an EOS
+        // proposal (mtp_speculative.rs:196-198), so only heads 0 .. np-2 count
+        if (np > 1) e->stats[b].mtp_head_forwards += np - 1;
         if (!e->greedy) e->hoffs[b] += np;
     }
     // ---- verify forward (finished sequences run at a dummy position 0) ----

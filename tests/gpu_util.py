@@ -24,3 +24,66 @@ def make_pair(seed=0, std=0.02, max_batch=1, max_rows=64, **kw):
         ref.set(i, raw)
         hip.load_f32(i, raw)
     return ref, hip
+
+
+def mtp_rounds_vs_oracle(ref, hip, prompt, max_new, K, s_ref, s_dev, seed, tol_p, tol_l, start=0, want=None,
+                         rounds=None):
+    """MtpSpeculativeEngine (mtp_speculative.rs:161-322) on the device, round by round
+    against the oracle engine's trace, with teacher forcing: the device starts from the
+    oracle's state at round `start` (prompt + committed tokens, sampler keystream
+    position) and runs one round at a time; a round must commit the oracle's tokens with
+    the same proposed / accepted counts and end at the same keystream position.  A round
+    that differs must be one the oracle marks as a near-tie (a sampled decision within
+    tol_p of its boundary, or a greedy / top-k logit gap below tol_l); the device then
+    restarts from the oracle's state after that round.
+    Returns (rounds equal, flagged divergences, oracle rounds from `start`)."""
+    prompt = np.asarray(prompt, np.uint32)
+    if want is None:
+        want, _, _, _ = ref.mtp_generate(prompt, max_new, K, s_ref, seed=seed)
+        rounds = ref.last_rounds
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(K))
+    r, same, flagged = start, 0, 0
+    while r < len(rounds):
+        rd = rounds[r]
+        c0 = rd["committed_before"]
+        p = np.concatenate([prompt, np.asarray(want[:c0], np.uint32)])
+        sess = eng.session(p[None], max_new - c0, s_dev, seeds=np.array([seed], np.uint64))
+        sess.set_rng_offsets([rd["rng_pos_before"]])
+        n_prev, prop_prev, acc_prev = 0, 0, 0
+        try:
+            while r < len(rounds):
+                rd = rounds[r]
+                sess.step(1)
+                out = sess.result()[0]
+                st = out.speculative_stats
+                got = [int(t) for t in out.token_ids[n_prev:]]
+                exp = [int(t) for t in want[rd["committed_before"]:rd["committed_after"]]]
+                ok = (got == exp and st.draft_tokens_proposed - prop_prev == rd["proposed"]
+                      and st.draft_tokens_accepted - acc_prev == rd["accepted"]
+                      and int(sess.rng_offsets()[0]) == rd["rng_pos_after"])
+                r += 1
+                if ok:
+                    same += 1
+                    n_prev, prop_prev, acc_prev = len(out.token_ids), st.draft_tokens_proposed, st.draft_tokens_accepted
+                    continue
+                assert rd["prob_margin"] < tol_p or rd["logit_gap"] < tol_l, \
+                    f"round {r - 1} differs without a near-tie: device {got} oracle {exp} ({rd})"
+                flagged += 1
+                break
+        finally:
+            sess.close()
+    return same, flagged, len(rounds) - start
+
+
+def first_divergent_round(rounds, want, got):
+    """Index of the oracle round holding the first token where `got` departs from
+    `want` (None when they are equal)."""
+    n = min(len(want), len(got))
+    diff = [i for i in range(n) if int(want[i]) != int(got[i])]
+    t = diff[0] if diff else (n if len(want) != len(got) else None)
+    if t is None:
+        return None
+    for i, rd in enumerate(rounds):
+        if rd["committed_before"] <= t < max(rd["committed_after"], rd["committed_before"] + 1):
+            return i
+    return len(rounds) - 1
