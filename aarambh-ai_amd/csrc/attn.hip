@@ -642,45 +642,25 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     }
     if (!arrive_last(&a.counters[grp], (unsigned)a.nchunks, &s_last)) return;
 
-    // ---- last workgroup: merge the chunks in chunk order.  Each thread loads its
-    //      row's (max, sum) and its 4 dims of up to MB chunks at once (one round
-    //      trip; loads past the last chunk re-read it and are not used), then
-    //      merges them in registers; more chunks go in further batches with a
-    //      running maximum. ----
+    // ---- last workgroup: merge the chunks in chunk order.  Each thread takes its
+    //      row's maximum over the chunks, then the weighted sums of its row's (max, sum)
+    //      header and its 4 dims, chunk by chunk (8 chunks' loads in flight). ----
     if (r >= R) return;
-    constexpr int MB = 20;
     const int C = a.nchunks;
+    const unsigned rbase = (unsigned)(r * AM_REC) * 4u;
+    constexpr unsigned CSTRIDE = (unsigned)(AM_ROWS * AM_REC) * 4u;
+    float Mc = -INFINITY;
+#pragma unroll 8
+    for (int c = 0; c < C; c++) Mc = fmaxf(Mc, ld4_coh(prs, rbase + (unsigned)c * CSTRIDE)[0]);
     float4_t tot = {0.f, 0.f, 0.f, 0.f};
-    float Mc = -INFINITY, Lc = 0.f;
-    for (int c0 = 0; c0 < C; c0 += MB) {
-        float ml[MB][2];
-        float4_t ov[MB];
-#pragma unroll
-        for (int u = 0; u < MB; u++) {
-            const unsigned rec = (unsigned)((min(c0 + u, C - 1) * AM_ROWS + r) * AM_REC) * 4u;
-            const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(prs, (int)rec, 0, 16));
-            ml[u][0] = __builtin_bit_cast(float, v[0]);
-            ml[u][1] = __builtin_bit_cast(float, v[1]);
-            ov[u] = ld4_coh(prs, rec + 16u + 16u * q);
-        }
-        float Mb = Mc;
-#pragma unroll
-        for (int u = 0; u < MB; u++)
-            if (c0 + u < C) Mb = fmaxf(Mb, ml[u][0]);
-        if (c0 > 0 && Mc != Mb) {
-            const float w = Mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mc - Mb);
-            Lc *= w;
-            tot *= w;
-        }
-        Mc = Mb;
-#pragma unroll
-        for (int u = 0; u < MB; u++)
-            if (c0 + u < C) {
-                const float mc = ml[u][0];
-                const float w = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - Mc);
-                Lc += ml[u][1] * w;
-                tot += ov[u] * w;
-            }
+    float Lc = 0.f;
+#pragma unroll 8
+    for (int c = 0; c < C; c++) {
+        const float4_t hdr = ld4_coh(prs, rbase + (unsigned)c * CSTRIDE);
+        const float4_t ov = ld4_coh(prs, rbase + (unsigned)c * CSTRIDE + 16u + 16u * q);
+        const float w = hdr[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(hdr[0] - Mc);
+        Lc += hdr[1] * w;
+        tot += ov * w;
     }
     const float4_t o4 = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
     *(float4_t*)out = o4;

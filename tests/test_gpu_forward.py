@@ -247,3 +247,34 @@ def test_graph_replay_is_bit_identical_to_direct_launches():
         for b in range(3):
             hip.restore(300, slot=b)
     hip.close()
+
+
+@pytest.mark.parametrize("kvfmt", [A.KV_INT8, A.KV_F16])
+def test_hd128_long_context_chunk_merge(kvfmt):
+    """head_dim 128 (the MFMA decode attention) over caches of 600, 3000, 5400 and
+    9000 tokens with one KV head: 3, 12, 22 and 36 chunks of 256 tokens, so the chunk
+    merge runs with one pass and with the running-max rescale across passes of 20
+    chunks.  Logits and hidden within 2e-3 of the oracle."""
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=1, n_heads=4, n_kv_heads=1,
+              max_seq_len=9100, weight_format=A.W_INT4_G128, kv_format=kvfmt, lm_head_format=1)
+    ref, hip = make_pair(seed=15, max_batch=4, max_rows=64, **kw)
+    lens = [600, 3000, 5400, 9000]
+    for b, L in enumerate(lens):
+        hip.kv_fill_synthetic(b, L, seed=60 + b)
+    ids = R.synth_tokens(15, 2, 16, 2048).reshape(4, 4)
+    gl, gh = hip.forward_with_cache_output(ids, lens)
+    for b, L in enumerate(lens):
+        kv = ref.kv(9100)
+        kv.fill_synthetic(60 + b, L)
+        wl, wh = kv.forward(ids[b], L, nthreads=16)
+        assert rel_rows(gl[b], wl).max() < TOL, (L, rel_rows(gl[b], wl).max())
+        assert rel_rows(gh[b], wh).max() < TOL, (L, rel_rows(gh[b], wh).max())
+    # each length alone (its own chunking: up to 36 chunks for one sequence)
+    for b, L in enumerate(lens):
+        hip.restore(L, slot=b)
+        gl1, _ = hip.forward_with_cache_output(ids[b:b + 1], [L], slots=[b])
+        kv = ref.kv(9100)
+        kv.fill_synthetic(60 + b, L)
+        wl, _ = kv.forward(ids[b], L, nthreads=16)
+        assert rel_rows(gl1[0], wl).max() < TOL, (L, "single", rel_rows(gl1[0], wl).max())
+    hip.close()

@@ -1,0 +1,88 @@
+"""Parity of the verify forward (model.rs:529-587, attention.rs:170-222) at the
+BASELINE workload widths, 2 layers deep, against the oracle on the same synthetic
+weights (N(0, 0.02^2) before quantisation, both sides' generators) and the same
+synthetic caches.  Bar: logits and final hidden within 2e-3 relative per row.
+
+C4: d 4096, 32 query / 8 KV heads (hd 128), ffn 11008, vocab 32000, INT4 g128
+weights, bf16 LM head, INT8 KV cache of 4096 tokens; K = 4 rows at batch 1 (the
+4-row GEMV), 8 and 32 (the many-row GEMM, M = 32 / 128).
+C3: d 2048, 16 / 4 heads (hd 128), ffn 5632, INT8 per-row weights, fp16 KV cache
+of 2048 tokens; K = 4 rows at batch 1 and 16."""
+import numpy as np
+import pytest
+
+import aarambh_hip as A
+import refcpu as R
+from gpu_util import rel_rows
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _pair(kw, max_batch, ctx):
+    rc = R.make_config(**kw)
+    ref = R.Model(rc, seed=0, std=0.02)
+    hip = A.HipModel(A.ModelConfig(**kw), max_batch=max_batch, max_rows=128)
+    hip.init_synthetic(seed=0, std=0.02)
+    return ref, hip
+
+
+@pytest.fixture(scope="module")
+def c4():
+    kw = dict(vocab_size=32000, hidden_dim=4096, ffn_dim=11008, n_layers=2, n_heads=32, n_kv_heads=8,
+              max_seq_len=4096 + 64, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    print("building C4-width models", flush=True)
+    ref, hip = _pair(kw, 32, 4096)
+    yield ref, hip
+    hip.close()
+    ref.close()
+
+
+@pytest.fixture(scope="module")
+def c3():
+    kw = dict(vocab_size=32000, hidden_dim=2048, ffn_dim=5632, n_layers=2, n_heads=16, n_kv_heads=4,
+              max_seq_len=2048 + 64, weight_format=A.W_INT8_ROW, lm_head_format=1, kv_format=A.KV_F16)
+    print("building C3-width models", flush=True)
+    ref, hip = _pair(kw, 16, 2048)
+    yield ref, hip
+    hip.close()
+    ref.close()
+
+
+def _verify_vs_oracle(ref, hip, B, ctx, seed):
+    print(f"verify B={B} over {ctx} cached tokens", flush=True)
+    for b in range(B):
+        hip.kv_fill_synthetic(b, ctx, seed=seed + b)
+    V = ref.cfg.vocab_size
+    ids = R.synth_tokens(seed, B, B * 4, V).reshape(B, 4)
+    gl, gh = hip.forward_with_cache_output(ids, [ctx] * B)
+    for b in sorted({0, B // 3, (2 * B) // 3, B - 1}):
+        kv = ref.kv(ctx + 64)
+        kv.fill_synthetic(seed + b, ctx)
+        wl, wh = kv.forward(ids[b], ctx, nthreads=16)
+        el, eh = rel_rows(gl[b], wl).max(), rel_rows(gh[b], wh).max()
+        print(f"  seq {b}: logits {el:.2e} hidden {eh:.2e}", flush=True)
+        assert el < TOL and eh < TOL, (b, el, eh)
+        kv.close()
+    # rollback by index, then a 1-row replay at the rolled-back position
+    for b in range(B):
+        hip.restore(ctx + 2, slot=b)
+    gl2, _ = hip.forward_with_cache_output(ids[:, 3:4], [ctx + 2] * B)
+    kv = ref.kv(ctx + 64)
+    kv.fill_synthetic(seed, ctx)
+    kv.forward(ids[0, :2], ctx, nthreads=16)
+    wl2, _ = kv.forward(ids[0, 3:4], ctx + 2, nthreads=16)
+    assert rel_rows(gl2[0], wl2).max() < TOL
+    kv.close()
+
+
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_c4_width_int4_verify_over_4096_token_int8_cache(c4, B):
+    ref, hip = c4
+    _verify_vs_oracle(ref, hip, B, 4096, 100 + B)
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_c3_width_int8_verify_over_2048_token_fp16_cache(c3, B):
+    ref, hip = c3
+    _verify_vs_oracle(ref, hip, B, 2048, 200 + B)
