@@ -146,6 +146,52 @@ __device__ __forceinline__ void wave_hist_add(unsigned* hist, int d) {
     if (d >= 0 && (__ffsll((long long)peers) - 1) == lane) atomicAdd(&hist[d], (unsigned)__popcll(peers));
 }
 
+// Visits every element j of one or two rows [0, n) once: g(j, r0[j], r1[j], valid) is
+// called by every thread the same number of times (valid marks real elements), so g
+// may vote across the wave.  16-byte loads, ACC_U per row in flight per thread, when
+// the rows are 16-byte aligned; 4-byte loads otherwise.
+template <int NR, class G>
+__device__ __forceinline__ void rows_foreach(const float* r0, const float* r1, int n, const G& g) {
+    const int tid = threadIdx.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(r0) | (NR == 2 ? reinterpret_cast<uintptr_t>(r1) : 0)) & 15) == 0;
+    int done = 0;
+    if (vec) {
+        const int n4 = n >> 2;
+        const float4_t* a4 = reinterpret_cast<const float4_t*>(r0);
+        const float4_t* b4 = reinterpret_cast<const float4_t*>(r1);
+        for (int q0 = 0; q0 < n4; q0 += ACC_U * ACC_THREADS) {
+            float4_t va[ACC_U], vb[ACC_U];
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int i4 = q0 + q * ACC_THREADS + tid;
+                va[q] = i4 < n4 ? a4[i4] : (float4_t){0.f, 0.f, 0.f, 0.f};
+                if (NR == 2) vb[q] = i4 < n4 ? b4[i4] : (float4_t){0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int q = 0; q < ACC_U; q++) {
+                const int i4 = q0 + q * ACC_THREADS + tid;
+#pragma unroll
+                for (int e = 0; e < 4; e++) g(4 * i4 + e, va[q][e], NR == 2 ? vb[q][e] : 0.f, i4 < n4);
+            }
+        }
+        done = n4 * 4;
+    }
+    for (int j0 = done; j0 < n; j0 += ACC_U * ACC_THREADS) {
+        float va[ACC_U], vb[ACC_U];
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS + tid;
+            va[q] = j < n ? r0[j] : 0.f;
+            vb[q] = (NR == 2 && j < n) ? r1[j] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < ACC_U; q++) {
+            const int j = j0 + q * ACC_THREADS + tid;
+            g(j, va[q], vb[q], j < n);
+        }
+    }
+}
+
 // Block max of v (all threads get it).
 __device__ inline float block_max(float v, AccShared* sh) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -162,7 +208,7 @@ __device__ inline float block_max(float v, AccShared* sh) {
 // j in [0, V): an 8-bit MSD radix select (keys are unique, so it ends on one
 // key).  Returns 0 when fewer than k keys qualify; *total gets their count.
 template <class KF>
-__device__ uint64_t select_desc(const KF& kf, const float* row, int V, int k, uint64_t U, AccShared* sh,
+__device__ __forceinline__ uint64_t select_desc(const KF& kf, const float* row, int V, int k, uint64_t U, AccShared* sh,
                                 unsigned* total) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     uint64_t prefix = 0, mask = 0;
@@ -171,26 +217,15 @@ __device__ uint64_t select_desc(const KF& kf, const float* row, int V, int k, ui
         const int shift = 56 - 8 * pass;
         for (int i = tid; i < 256; i += ACC_THREADS) sh->sel.hist[i] = 0;
         __syncthreads();
-        for (int jb = 0; jb < V; jb += ACC_U * ACC_THREADS) {  // uniform trip count: whole waves vote
-            const int j0 = jb + tid;
-            float vv[ACC_U];
-#pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int j = j0 + q * ACC_THREADS;
-                vv[q] = j < V ? row[j] : 0.f;
+        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+            int d = -1;
+            if (valid) {
+                bool ok;
+                const uint64_t key = kf(l, j, ok);
+                if (ok && key < U && (key & mask) == prefix) d = (int)((key >> shift) & 255);
             }
-#pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int j = j0 + q * ACC_THREADS;
-                int d = -1;
-                if (j < V) {
-                    bool ok;
-                    const uint64_t key = kf(vv[q], j, ok);
-                    if (ok && key < U && (key & mask) == prefix) d = (int)((key >> shift) & 255);
-                }
-                wave_hist_add(sh->sel.hist, d);
-            }
-        }
+            wave_hist_add(sh->sel.hist, d);
+        });
         __syncthreads();
         if (wid == 0) {
             // lane l holds bins 255 - 4l .. 252 - 4l, so lanes run from the largest digit down
@@ -254,26 +289,15 @@ __device__ uint64_t select_desc(const KF& kf, const float* row, int V, int k, ui
 // for NR = 2), with the inverse-CDF crossing for u >= 0: the workgroup writes LDS
 // chunks of `chunk` values and wave 0 scans them, carrying the running sum.
 template <int NR, class F>
-__device__ SeqScan block_seq_scan(const float* r0, const float* r1, int n, float u, const F& f, float* buf,
+__device__ __forceinline__ SeqScan block_seq_scan(const float* r0, const float* r1, int n, float u, const F& f, float* buf,
                                   int chunk, AccShared* sh) {
     const int tid = threadIdx.x, wid = tid >> 6;
     SeqScan st = seq_scan_init();
     for (int c0 = 0; c0 < n; c0 += chunk) {
         const int m = min(chunk, n - c0);
-        for (int i0 = tid; i0 < m; i0 += ACC_U * ACC_THREADS) {
-            float a[ACC_U], b[ACC_U];
-#pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int i = i0 + q * ACC_THREADS;
-                a[q] = i < m ? r0[c0 + i] : 0.f;
-                b[q] = (NR == 2 && i < m) ? r1[c0 + i] : 0.f;
-            }
-#pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int i = i0 + q * ACC_THREADS;
-                if (i < m) buf[i] = f(a[q], b[q], c0 + i);
-            }
-        }
+        rows_foreach<NR>(r0 + c0, NR == 2 ? r1 + c0 : nullptr, m, [&](int i, float a, float b, bool valid) {
+            if (valid) buf[i] = f(a, b, c0 + i);
+        });
         __syncthreads();
         if (wid == 0) seq_scan_wave(buf, m, u, c0, st);
         __syncthreads();
@@ -289,22 +313,12 @@ __device__ SeqScan block_seq_scan(const float* r0, const float* r1, int n, float
 __device__ inline int block_argmax(const float* row, int V, AccShared* sh) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     int bk = INT_MIN, bi = 0;
-    for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-        float vv[ACC_U];
-#pragma unroll
-        for (int q = 0; q < ACC_U; q++) {
-            const int j = j0 + q * ACC_THREADS;
-            vv[q] = j < V ? row[j] : 0.f;
+    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+        if (valid) {
+            const int k = total_key(l);
+            if (k > bk || (k == bk && j > bi)) { bk = k; bi = j; }
         }
-#pragma unroll
-        for (int q = 0; q < ACC_U; q++) {
-            const int j = j0 + q * ACC_THREADS;
-            if (j < V) {
-                const int k = total_key(vv[q]);
-                if (k >= bk) { bk = k; bi = j; }
-            }
-        }
-    }
+    });
     for (int d = 32; d >= 1; d >>= 1) {
         const int ok = __shfl_xor(bk, d, 64), oi = __shfl_xor(bi, d, 64);
         if (ok > bk || (ok == bk && oi > bi)) { bk = ok; bi = oi; }
@@ -366,22 +380,13 @@ __device__ void row_filter(const float* row, int V, float T, int top_k, float to
     }
     // ---- max of the finite masked logits ----
     float mx = -INFINITY;
-    for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-        float vv[ACC_U];
-#pragma unroll
-        for (int q = 0; q < ACC_U; q++) {
-            const int j = j0 + q * ACC_THREADS;
-            vv[q] = j < V ? row[j] : 0.f;
+    const uint64_t kk = f.kkey;
+    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+        if (valid && logit_key(l, j) >= kk) {
+            const float m = l / T;
+            if (isfinite(m)) mx = fmaxf(mx, m);
         }
-#pragma unroll
-        for (int q = 0; q < ACC_U; q++) {
-            const int j = j0 + q * ACC_THREADS;
-            if (j < V && logit_key(vv[q], j) >= f.kkey) {
-                const float m = vv[q] / T;
-                if (isfinite(m)) mx = fmaxf(mx, m);
-            }
-        }
-    }
+    });
     mx = block_max(mx, sh);
     if (!(mx > -INFINITY)) {  // "all logits are non-finite" (sampler.rs:286-288)
         status = 1;
@@ -417,11 +422,10 @@ __device__ void row_filter(const float* row, int V, float T, int top_k, float to
         if (remain == 0) break;  // every positive probability taken without reaching top_p: keep all
         if (tid == 0) sh->n = 0;
         __syncthreads();
-        for (int jb = 0; jb < V; jb += ACC_THREADS) {  // uniform trip count: the ballot sees whole waves
-            const int j = jb + tid;
+        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
             bool ok = false;
             uint64_t key = 0;
-            if (j < V) key = pkf(row[j], j, ok);
+            if (valid) key = pkf(l, j, ok);
             const bool take = ok && key < U && key >= L;
             const unsigned long long m = __ballot(take);
             unsigned base = 0;
@@ -429,7 +433,7 @@ __device__ void row_filter(const float* row, int V, float T, int top_k, float to
             base = __shfl(base, 0, 64);
             const unsigned slot = base + (unsigned)__popcll(m & ((1ull << (threadIdx.x & 63)) - 1ull));
             if (take && slot < (unsigned)TOPP_PAGE) keys[slot] = key;
-        }
+        });
         __syncthreads();
         const int n = min((int)sh->n, TOPP_PAGE);
         int np2 = 1;
@@ -673,7 +677,7 @@ int launch_accept(const AcceptArgs& a_in, hipStream_t stream) {
     });
     if (note_error(attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(accept_kernel, dim3(a.B * rows), dim3(ACC_THREADS), lds, stream, a);
+    launch_timed(accept_kernel, dim3(a.B * rows), dim3(ACC_THREADS), (uint32_t)lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -759,30 +763,23 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     unsigned long long best[CAND_MAX];
 #pragma unroll
     for (int i = 0; i < CAND_MAX; i++) best[i] = 0ull;
-    if (status == 0) {
-        for (int j0 = tid; j0 < V; j0 += ACC_U * ACC_THREADS) {
-            float vv[ACC_U];
+    auto offer = [&](int j, float p) {
+        unsigned long long k = prob_key(p, j);
 #pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int j = j0 + q * ACC_THREADS;
-                vv[q] = (j < V && !a.greedy) ? row[j] : 0.f;
-            }
-#pragma unroll
-            for (int q = 0; q < ACC_U; q++) {
-                const int j = j0 + q * ACC_THREADS;
-                if (j >= V) continue;
-                const float p = a.greedy ? (j == am ? 1.0f : 0.0f) : filt_prob(f, vv[q], j);
-                unsigned long long k = prob_key(p, j);
-#pragma unroll
-                for (int i = 0; i < CAND_MAX; i++) {
-                    if (i < n && k > best[i]) {
-                        const unsigned long long t = best[i];
-                        best[i] = k;
-                        k = t;
-                    }
-                }
+        for (int i = 0; i < CAND_MAX; i++) {
+            if (i < n && k > best[i]) {
+                const unsigned long long t = best[i];
+                best[i] = k;
+                k = t;
             }
         }
+    };
+    if (status == 0 && a.greedy) {
+        for (int j = tid; j < V; j += ACC_THREADS) offer(j, j == am ? 1.0f : 0.0f);
+    } else if (status == 0) {
+        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+            if (valid) offer(j, filt_prob(f, l, j));
+        });
     }
 #pragma unroll
     for (int i = 0; i < CAND_MAX; i++) keys[tid][i] = best[i];
@@ -844,7 +841,7 @@ int launch_candidates(const CandArgs& a_in, hipStream_t stream) {
     });
     if (note_error(attr)) return 4;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(candidates_kernel, dim3(a.rows), dim3(ACC_THREADS), lds, stream, a);
+    launch_timed(candidates_kernel, dim3(a.rows), dim3(ACC_THREADS), (uint32_t)lds, stream, a);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

@@ -226,7 +226,23 @@ __device__ __forceinline__ SeqScan seq_scan_init() {
     return st;
 }
 
-__device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, SeqScan& st) {
+// Inclusive prefix sum over the 64 lanes with DPP row shifts and row broadcasts
+// (register-to-register, no LDS round trip per step).
+__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+__device__ __forceinline__ float readlane_f32(float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+__device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, int gbase, SeqScan& st) {
+    constexpr int E = 16;  // consecutive elements per lane in the binade fast path (1024 per step)
     const int lane = threadIdx.x & 63;
     float s = st.s;
     int pos = 0;
@@ -234,13 +250,12 @@ __device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, 
     float s_at = st.s_at, s_before = st.s_before;
     const bool want = u >= 0.0f;
     while (pos < n) {
-        const int base = pos + 4 * lane;
-        float x[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) x[k] = (base + k < n) ? v[base + k] : 0.0f;
-
         if (s == 0.0f) {
             // Zeros keep s at 0 (0 + 0 = 0); the first non-zero element x gives s = x.
+            const int base = pos + 4 * lane;
+            float x[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) x[k] = (base + k < n) ? v[base + k] : 0.0f;
             int fnz = 4;
 #pragma unroll
             for (int k = 3; k >= 0; k--)
@@ -255,11 +270,9 @@ __device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, 
                 pos += 256;
                 continue;
             }
-            int bl = __ffsll((long long)m) - 1;
-            int bk = __shfl(fnz, bl, 64);
-            int t = pos + 4 * bl + bk;
-            float xt = v[t];
-            s = xt;
+            const int bl = __ffsll((long long)m) - 1;
+            const int t = pos + 4 * bl + __builtin_amdgcn_readlane(fnz, bl);
+            s = v[t];
             if (want && cross < 0 && u <= s) {
                 cross = gbase + t;
                 s_at = s;
@@ -272,8 +285,8 @@ __device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, 
         const int eb = (int)((bits >> 23) & 0xFF);
         if (eb == 0) {
             // subnormal running sum: one scalar step
-            float xt = v[pos];
-            float sp = s;
+            const float xt = v[pos];
+            const float sp = s;
             s = s + xt;
             if (want && cross < 0 && u <= s) {
                 cross = gbase + pos;
@@ -283,65 +296,83 @@ __device__ inline void seq_scan_wave(const float* v, int n, float u, int gbase, 
             pos++;
             continue;
         }
-        const int sh = 150 - eb;                         // x / ulp(s) == ldexp(x, sh)
-        const int ns = (int)((bits & 0x7FFFFFu) | 0x800000u); // s / ulp(s)
-        int r[4];
-        bool special[4];
+        const int sh = 150 - eb;                               // x / ulp(s) == ldexp(x, sh)
+        const int ns = (int)((bits & 0x7FFFFFu) | 0x800000u);  // s / ulp(s)
+        // window [w0, w0 + 64 E) aligned to 4 elements; elements below pos count as 0
+        const int w0 = pos & ~3;
+        const int base = w0 + E * lane;
+        float x[E];
+        if (base + E <= n && base >= pos) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float c = ldexpf(x[k], sh);
-            float a = floorf(c);
-            float f = c - a;
-            special[k] = !(c < 16777216.0f) || (f == 0.5f) || !(x[k] >= 0.0f);
-            r[k] = special[k] ? 16777216 : ((int)a + (f > 0.5f ? 1 : 0));
-        }
-        int lsum = r[0] + r[1] + r[2] + r[3];
-        if (lsum > 16777217) lsum = 16777217;
-        int excl = wave_excl_scan_i32(lsum);
-        int run = ns + excl;
-        int first_bad = 4, first_cross = 4;
-        float cs_at = 0.0f, cs_before = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (first_bad < 4) break;
-            if (base + k >= n) break;
-            int rk = run + r[k];
-            if (special[k] || rk >= 16777216) {
-                first_bad = k;
-                break;
+            for (int c = 0; c < E / 4; c++) {
+                const float4_t q = *(const float4_t*)(v + base + 4 * c);
+                x[4 * c] = q[0];
+                x[4 * c + 1] = q[1];
+                x[4 * c + 2] = q[2];
+                x[4 * c + 3] = q[3];
             }
-            if (want && first_cross == 4) {
-                float sk = ldexpf((float)rk, -sh);
+        } else {
+#pragma unroll
+            for (int k = 0; k < E; k++) {
+                const int i = base + k;
+                x[k] = (i >= pos && i < n) ? v[i] : 0.0f;
+            }
+        }
+        int r[E];
+        bool special = false;
+        int lsum = 0;
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            const float c = ldexpf(x[k], sh);
+            const float a = floorf(c);
+            const float f = c - a;
+            const bool sp = !(c < 16777216.0f) || (f == 0.5f) || !(x[k] >= 0.0f);
+            r[k] = sp ? 16777216 : ((int)a + (f > 0.5f ? 1 : 0));
+            special |= sp;
+            lsum += r[k];
+        }
+        if (special || lsum > 16777217) lsum = 16777217;  // past the binade anyway; keeps the scan in range
+        const int incl = wave_incl_scan_dpp(lsum);
+        int run = ns + incl - lsum;
+        int first_bad = E, first_cross = E, run_bad = 0;
+        float cs_at = 0.0f, cs_before = 0.0f;
+        // walk the lane's elements with predication only (no early exit), so the loop
+        // unrolls and r[] stays in registers
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            const int rk = run + r[k];
+            const bool live = first_bad == E;
+            if (live && (r[k] >= 16777216 || rk >= 16777216)) {
+                first_bad = k;
+                run_bad = run;
+            }
+            if (want && first_bad == E && first_cross == E && r[k] > 0) {
+                const float sk = ldexpf((float)rk, -sh);
                 if (u <= sk) {
                     first_cross = k;
                     cs_at = sk;
                     cs_before = ldexpf((float)run, -sh);
                 }
             }
-            run = rk;
+            if (first_bad == E) run = rk;
         }
-        unsigned long long badm = __ballot(first_bad < 4);
-        int bad_lane = badm ? (__ffsll((long long)badm) - 1) : 64;
-        unsigned long long lanes_ok = bad_lane >= 64 ? ~0ull : ((1ull << bad_lane) | ((1ull << bad_lane) - 1ull));
-        unsigned long long cm = __ballot(first_cross < 4) & lanes_ok;
+        const unsigned long long badm = __ballot(first_bad < E);
+        const int bad_lane = badm ? (__ffsll((long long)badm) - 1) : 64;
+        const unsigned long long lanes_ok = bad_lane >= 64 ? ~0ull : ((1ull << bad_lane) | ((1ull << bad_lane) - 1ull));
+        const unsigned long long cm = __ballot(first_cross < E) & lanes_ok;
         if (want && cross < 0 && cm) {
-            int cl = __ffsll((long long)cm) - 1;
-            int ck = __shfl(first_cross, cl, 64);
-            cross = gbase + pos + 4 * cl + ck;
-            s_at = __shfl(cs_at, cl, 64);
-            s_before = __shfl(cs_before, cl, 64);
-            if (ck == 0 && cl == 0) s_before = s;
+            const int cl = __ffsll((long long)cm) - 1;
+            cross = gbase + w0 + E * cl + __builtin_amdgcn_readlane(first_cross, cl);
+            s_at = readlane_f32(cs_at, cl);
+            s_before = readlane_f32(cs_before, cl);
         }
         if (bad_lane == 64) {
-            int total = __shfl(excl + lsum, 63, 64);
-            s = ldexpf((float)(ns + total), -sh);
-            pos += 256;
+            s = ldexpf((float)(ns + __builtin_amdgcn_readlane(incl, 63)), -sh);
+            pos = w0 + 64 * E;
         } else {
-            int run_before = __shfl(run, bad_lane, 64);
-            int tk = __shfl(first_bad, bad_lane, 64);
-            int t = pos + 4 * bad_lane + tk;
-            float sp = ldexpf((float)run_before, -sh);
-            float xt = v[t];
+            const int t = w0 + E * bad_lane + __builtin_amdgcn_readlane(first_bad, bad_lane);
+            const float sp = ldexpf((float)__builtin_amdgcn_readlane(run_bad, bad_lane), -sh);
+            const float xt = v[t];
             s = sp + xt;
             if (want && cross < 0 && u <= s) {
                 cross = gbase + t;

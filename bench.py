@@ -11,11 +11,15 @@ A "step" is one speculative round of the MTP engine (mtp_speculative.rs:161-322)
 for every sequence of the batch: 3 MTP-head forwards, one K=4-row verify
 forward over the 4096-token cache, fused acceptance, replay on rejection.
 `value` = committed tokens / wall time of the timed rounds at batch 32 (inputs
-and KV resident in HBM); batch 1 is reported beside it.  The verify-step loop
-(K = 4 rows at offset 4096, repeated) is timed separately with per-kernel HIP
-events; its INT4 GEMV kernel gives `roofline`.  `cpu_baseline` times the CPU
-oracle (restated reference CPU path, f32) on a 2-layer slice of the same model
-and extrapolates to a full round.
+and KV resident in HBM); batches 1 and 8 are reported beside it.  The verify
+step (K = 4 rows at offset 4096, repeated) is timed separately with per-kernel
+HIP events at dispatch level: the INT4 GEMV gives `roofline` (batch 1, HBM), the
+decode attention `roofline_attention` (batch 1, HBM) and the many-row GEMM
+`roofline_gemm` (batch 32, MFMA).  Also measured: the standalone sampled
+acceptance kernel of config 2 (32 x 4 x 32000, T = 0.8, HBM) and the config-3
+INT8 verify step at batch 1 and 16 (HBM).  `cpu_baseline` times the CPU oracle
+(restated reference CPU path, f32) on all host cores on a 2-layer slice of the
+same model and extrapolates to a full round.
 """
 import argparse
 import json
@@ -38,34 +42,79 @@ C4 = dict(vocab_size=32000, hidden_dim=4096, ffn_dim=11008, n_layers=32, n_heads
 CTX = 4096
 K_ROWS = 4  # k = 3 MTP drafts + the target-sampled proposal
 
+C3 = dict(vocab_size=32000, hidden_dim=2048, ffn_dim=5632, n_layers=16, n_heads=16, n_kv_heads=4,
+          max_seq_len=2048 + 64)
+C3_CTX = 2048
+
 
 def int4_matrix_bytes(n, k):
     return n * k // 2 + n * (k // 128) * 4  # codes + fp16 scale + fp16 zero per 128-group
 
 
+def int8_matrix_bytes(n, k):
+    return n * k + n * 4  # codes + f32 row scale
+
+
+def layer_shapes(cfg):
+    H, F = cfg["hidden_dim"], cfg["ffn_dim"]
+    hd = H // cfg["n_heads"]
+    QD, KD = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    return [(QD + 2 * KD, H), (H, QD), (2 * F, H), (H, F)], hd
+
+
 def verify_alg_bytes(B, ctx=CTX):
-    """Algorithmic HBM bytes of one K-row verify step at batch B: every weight byte
-    once (quantised, with scales), the LM head once, and per sequence the K / V
+    """Algorithmic HBM bytes of one K-row verify step at batch B (config 4): every weight
+    byte once (quantised, with scales), the LM head once, and per sequence the K / V
     cache bytes of the context at every layer."""
-    H, F, V, L = C4["hidden_dim"], C4["ffn_dim"], C4["vocab_size"], C4["n_layers"]
-    hd = H // C4["n_heads"]
-    QD, KD = C4["n_heads"] * hd, C4["n_kv_heads"] * hd
-    per_layer = int4_matrix_bytes(QD + 2 * KD, H) + int4_matrix_bytes(H, QD) + int4_matrix_bytes(2 * F, H) + \
-        int4_matrix_bytes(H, F)
-    weights = L * per_layer + V * H * 2
-    kv = B * L * 2 * C4["n_kv_heads"] * ctx * (hd + 2)  # INT8 codes + fp16 per-token scale
+    shapes, hd = layer_shapes(C4)
+    per_layer = sum(int4_matrix_bytes(n, k) for n, k in shapes)
+    weights = C4["n_layers"] * per_layer + C4["vocab_size"] * C4["hidden_dim"] * 2
+    kv = B * C4["n_layers"] * 2 * C4["n_kv_heads"] * ctx * (hd + 2)  # INT8 codes + fp16 per-token scale
     return weights, kv
 
 
-def gemm_flops(M):
-    H, F, V, L = C4["hidden_dim"], C4["ffn_dim"], C4["vocab_size"], C4["n_layers"]
-    hd = H // C4["n_heads"]
-    QD, KD = C4["n_heads"] * hd, C4["n_kv_heads"] * hd
-    per_layer = (QD + 2 * KD) * H + H * QD + 2 * F * H + H * F
-    return 2.0 * M * (L * per_layer)
+def c3_alg_bytes(B):
+    shapes, hd = layer_shapes(C3)
+    weights = C3["n_layers"] * sum(int8_matrix_bytes(n, k) for n, k in shapes) + C3["vocab_size"] * C3["hidden_dim"] * 2
+    kv = B * C3["n_layers"] * 2 * C3["n_kv_heads"] * C3_CTX * hd * 2  # fp16 K and V
+    return weights, kv
 
 
-def run_gpu(args):
+def gemm_flops(M, cfg=C4):
+    shapes, _ = layer_shapes(cfg)
+    return 2.0 * M * cfg["n_layers"] * sum(n * k for n, k in shapes)
+
+
+def verify_timing(m, ids, offs, n_iter):
+    """Wall time of the verify step as served (captured-graph replay), then per-kernel
+    classes from HIP events at each dispatch's start / end (direct launches)."""
+    for _ in range(3):
+        m.forward_with_cache_output(ids, offs, want_logits=False, want_hidden=False)
+    m.sync()
+    t = time.perf_counter()
+    for _ in range(n_iter):
+        m.forward_with_cache_output(ids, offs, want_logits=False, want_hidden=False)
+    m.sync()
+    wall = (time.perf_counter() - t) / n_iter
+    m.prof_enable(True)
+    for _ in range(n_iter):
+        m.forward_with_cache_output(ids, offs, want_logits=False, want_hidden=False)
+    m.sync()
+    prof = m.prof_get()
+    m.prof_enable(False)
+    return wall, prof
+
+
+def kernels_summary(prof, n):
+    return {k: {"ms_per_step": v["ms"] / n, "launches_per_step": v["launches"] / n,
+                "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] > 0 else 0.0}
+            for k, v in prof.items() if v["launches"]}
+
+
+INT4_CLASSES = ("gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down")
+
+
+def run_c4(args):
     import aarambh_hip as A
 
     cfg = A.ModelConfig(**C4, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
@@ -77,30 +126,14 @@ def run_gpu(args):
     eng = A.MtpSpeculativeEngine(m, A.SpeculativeConfig(K_ROWS))
     rng = np.random.default_rng(0)
     res = {}
+    _, hd = layer_shapes(C4)
     for B in args.batches:
         for b in range(B):
             m.kv_fill_synthetic(b, CTX, seed=1 + b)
-        # ---- verify step: K rows at offset CTX (rewinds each time), per-kernel events ----
+        # ---- verify step: K rows at offset CTX (rewinds each time) ----
         ids = rng.integers(1, C4["vocab_size"], (B, K_ROWS)).astype(np.uint32)
-        for _ in range(3):
-            m.forward_with_cache_output(ids, [CTX] * B, want_logits=False, want_hidden=False)
-        # wall time of the verify step as served (repeated shape: captured-graph replay) ...
         n_verify = args.verify_iters
-        m.sync()
-        tv = time.perf_counter()
-        for _ in range(n_verify):
-            m.forward_with_cache_output(ids, [CTX] * B, want_logits=False, want_hidden=False)
-        m.sync()
-        tv = (time.perf_counter() - tv) / n_verify
-        # ... and per-kernel-class HIP-event timing (direct launches, events around each)
-        m.prof_enable(True)
-        tvp = time.perf_counter()
-        for _ in range(n_verify):
-            m.forward_with_cache_output(ids, [CTX] * B, want_logits=False, want_hidden=False)
-        m.sync()
-        tvp = (time.perf_counter() - tvp) / n_verify
-        prof = m.prof_get()
-        m.prof_enable(False)
+        tv, prof = verify_timing(m, ids, [CTX] * B, n_verify)
         wbytes, kvbytes = verify_alg_bytes(B)
         gpu_ms = sum(v["ms"] for v in prof.values()) / n_verify
         # ---- engine rounds ----
@@ -108,8 +141,7 @@ def run_gpu(args):
         max_new = K_ROWS * (args.warmup + args.steps + 2) + 8
         sess = eng.session(prompts, max_new, A.Sampler.greedy_sampler(), cached_len=CTX)
         sess.step(args.warmup)
-        before = sess.result()
-        tok0 = sum(len(r.token_ids) for r in before)
+        tok0 = sum(len(r.token_ids) for r in sess.result())
         m.sync()
         ts = time.perf_counter()
         sess.step(args.steps)
@@ -117,10 +149,14 @@ def run_gpu(args):
         ts = time.perf_counter() - ts
         after = sess.result()
         tok1 = sum(len(r.token_ids) for r in after)
-        st = after[0].speculative_stats
         stats_all = [r.speculative_stats for r in after]
         sess.close()
         rounds = sum(s.rounds for s in stats_all)
+        int4 = [prof[k] for k in INT4_CLASSES]
+        ms4 = sum(v["ms"] for v in int4)
+        by4 = sum(v["bytes"] for v in int4)
+        n4 = sum(v["launches"] for v in int4)
+        att = prof["attention"]
         res[B] = {
             "tokens_per_s": (tok1 - tok0) / ts,
             "ms_per_step": ts * 1000.0 / args.steps,
@@ -131,30 +167,85 @@ def run_gpu(args):
             "mtp_forwards_per_round": sum(s.mtp_head_forwards for s in stats_all) / max(1, rounds),
             "verify": {
                 "ms_wall": tv * 1000.0,
-                "ms_wall_direct_launches": tvp * 1000.0,
                 "ms_kernels": gpu_ms,
                 "alg_bytes": wbytes + kvbytes,
                 "hbm_gbs": (wbytes + kvbytes) / tv / 1e9,
                 "hbm_frac": (wbytes + kvbytes) / tv / 1e9 / HBM_PEAK_GBS,
-                "gemm_tflops": gemm_flops(B * K_ROWS) / tv / 1e12,
-                "kernels": {k: {"ms_per_step": v["ms"] / n_verify, "launches_per_step": v["launches"] / n_verify,
-                                "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] > 0 else 0.0}
-                            for k, v in prof.items() if v["launches"]},
+                "kernels": kernels_summary(prof, n_verify),
             },
-            "stats_seq0": st.__dict__,
+            "stats_seq0": stats_all[0].__dict__,
+            "int4_proj": {"ms_per_step": ms4 / n_verify, "alg_bytes": by4, "launches": n4,
+                          "avg_us": ms4 * 1000.0 / max(n4, 1), "avg_bytes": by4 / max(n4, 1),
+                          "gbs": by4 / (ms4 * 1e-3) / 1e9 if ms4 else 0.0,
+                          "useful_tflops": gemm_flops(B * K_ROWS) / (ms4 * 1e-3 / n_verify) / 1e12 if ms4 else 0.0},
+            "attention": {"ms_per_step": att["ms"] / n_verify, "launches": att["launches"],
+                          "avg_us": att["ms"] * 1000.0 / max(att["launches"], 1),
+                          "alg_bytes_per_step": kvbytes,
+                          "gbs": kvbytes / (att["ms"] * 1e-3 / n_verify) / 1e9 if att["ms"] else 0.0},
         }
-        int4 = [prof[k] for k in ("gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down")]
-        ms = sum(v["ms"] for v in int4)
-        by = sum(v["bytes"] for v in int4)
-        n = sum(v["launches"] for v in int4)
-        res[B]["int4_gemv"] = {"ms_total": ms, "alg_bytes": by, "launches": n,
-                               "avg_us": ms * 1000.0 / max(n, 1), "avg_bytes": by / max(n, 1),
-                               "gbs": by / (ms * 1e-3) / 1e9 if ms else 0.0,
-                               "tflops": gemm_flops(B * K_ROWS) * (1 - 0) / 1e12 / (ms * 1e-3 / n_verify)
-                               if ms else 0.0}
         print(f"# B={B}: {res[B]['tokens_per_s']:.1f} tok/s, round {res[B]['ms_per_step']:.3f} ms, verify "
-              f"{tv * 1000:.3f} ms ({res[B]['verify']['hbm_gbs']:.0f} GB/s), int4 gemv {res[B]['int4_gemv']['gbs']:.0f}"
-              f" GB/s", file=sys.stderr, flush=True)
+              f"{tv * 1000:.3f} ms ({res[B]['verify']['hbm_gbs']:.0f} GB/s), int4 proj "
+              f"{res[B]['int4_proj']['gbs']:.0f} GB/s / {res[B]['int4_proj']['useful_tflops']:.0f} TF, attention "
+              f"{res[B]['attention']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    m.close()
+    return res
+
+
+def run_c2(args):
+    """the standalone fused acceptance kernel, 32 sequences x k = 4
+    draft positions x vocab 32000, target logits N(0, 3^2), draft = target + N(0, 1),
+    T = 0.8, draft tokens drawn from the draft distribution, seeded uniforms (external-
+    draft round with bonus row).  One call reads 36 864 000 bytes of logits."""
+    import torch
+    import aarambh_hip as A
+
+    B, K, V = 32, 4, 32000
+    m = A.HipModel(A.ModelConfig(vocab_size=128, hidden_dim=128, ffn_dim=128, n_layers=1, n_heads=1,
+                                 n_kv_heads=1, max_seq_len=16), max_batch=1, max_rows=16)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    tgt = torch.randn((B, K + 1, V), device="cuda", generator=g) * 3.0
+    drf = tgt[:, :K] + torch.randn((B, K, V), device="cuda", generator=g)
+    toks = torch.multinomial(torch.softmax(drf.reshape(-1, V) / 0.8, -1), 1, generator=g).reshape(B, K).int()
+    seeds = torch.arange(B, device="cuda", dtype=torch.int64)
+    s = A.Sampler.top_k_top_p(0.8, seed=0)
+    out = None
+    for _ in range(3):
+        out = m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
+    m.prof_enable(True)
+    n = args.verify_iters * 5
+    for _ in range(n):
+        m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
+    prof = m.prof_get()["accept"]
+    m.prof_enable(False)
+    alg = B * (2 * K + 1) * V * 4
+    us = prof["ms"] * 1000.0 / max(prof["launches"], 1)
+    acc = out["accept_len"].cpu().numpy()
+    m.close()
+    r = {"us_per_call": us, "alg_bytes": alg, "gbs": alg / (us * 1e-6) / 1e9, "hbm_frac": alg / (us * 1e-6) / 1e9 /
+         HBM_PEAK_GBS, "launches": prof["launches"], "mean_accept_len": float(acc.mean())}
+    print(f"# C2 sampled acceptance: {us:.2f} us per call, {r['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    return r
+
+
+def run_c3(args):
+    """INT8 per-row verify, 16 layers, d 2048, 16 / 4 heads, ffn 5632,
+    fp16 KV cache of 2048 tokens, K = 4 rows at batch 1 and 16."""
+    import aarambh_hip as A
+
+    cfg = A.ModelConfig(**C3, weight_format=A.W_INT8_ROW, lm_head_format=1, kv_format=A.KV_F16)
+    m = A.HipModel(cfg, max_batch=16, max_rows=128)
+    m.init_synthetic(seed=0, std=0.02)
+    rng = np.random.default_rng(3)
+    res = {}
+    for B in (1, 16):
+        for b in range(B):
+            m.kv_fill_synthetic(b, C3_CTX, seed=1 + b)
+        ids = rng.integers(1, C3["vocab_size"], (B, K_ROWS)).astype(np.uint32)
+        tv, prof = verify_timing(m, ids, [C3_CTX] * B, args.verify_iters)
+        w, kv = c3_alg_bytes(B)
+        res[B] = {"ms_wall": tv * 1e3, "alg_bytes": w + kv, "hbm_gbs": (w + kv) / tv / 1e9,
+                  "hbm_frac": (w + kv) / tv / 1e9 / HBM_PEAK_GBS, "kernels": kernels_summary(prof, args.verify_iters)}
+        print(f"# C3 B={B}: verify {tv * 1e3:.3f} ms ({res[B]['hbm_gbs']:.0f} GB/s)", file=sys.stderr, flush=True)
     m.close()
     return res
 
@@ -174,10 +265,29 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(res_b1, threads):
-    """Oracle (restated reference CPU path, f32 compute) on a 2-layer slice of C4."""
+def host_cpu():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS") or avail)
+    return model, os.cpu_count() or 1, avail, max(1, min(threads, avail))
+
+
+def cpu_baseline(res_b1):
+    """Oracle (restated reference CPU path, f32 compute) on all host cores, on a 2-layer
+    slice of C4 at batch 1, extrapolated to the full model and the GPU run's round mix."""
     import refcpu as R
 
+    model_name, nproc, avail, threads = host_cpu()
     cfg = R.make_config(vocab_size=C4["vocab_size"], hidden_dim=C4["hidden_dim"], ffn_dim=C4["ffn_dim"],
                         n_layers=2, n_heads=C4["n_heads"], n_kv_heads=C4["n_kv_heads"],
                         max_seq_len=CTX + 16, num_future_tokens=2, weight_format=R.W_INT4_G128,
@@ -196,12 +306,12 @@ def cpu_baseline(res_b1, threads):
             fn()
         return (time.perf_counter() - t) / reps
 
-    t1 = timed(lambda: kv.forward_layers(ids, CTX, 1, True, threads), 2)
-    t2 = timed(lambda: kv.forward_layers(ids, CTX, 2, True, threads), 2)
+    t1 = timed(lambda: kv.forward_layers(ids, CTX, 1, True, threads), 3)
+    t2 = timed(lambda: kv.forward_layers(ids, CTX, 2, True, threads), 3)
     per_layer = max(t2 - t1, 1e-9)
     head = max(t1 - per_layer, 0.0)
     anchor = np.random.default_rng(0).normal(0, 1, C4["hidden_dim"]).astype(np.float32)
-    t_mtp = timed(lambda: model.mtp_head(0, anchor, np.array([5], np.uint32), threads), 2)
+    t_mtp = timed(lambda: model.mtp_head(0, anchor, np.array([5], np.uint32), threads), 3)
     t_verify = C4["n_layers"] * per_layer + head
     tf = res_b1["target_forwards_per_round"]
     mf = res_b1["mtp_forwards_per_round"]
@@ -212,12 +322,15 @@ def cpu_baseline(res_b1, threads):
         "unit": "accepted tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle (C restatement of the reference f32 CPU path: sequential online-softmax "
-                   f"attention, f32 GEMV) on a 2-layer slice of config 4 (INT4-dequantised f32 weights), "
-                   f"K=4 verify rows over a {CTX}-token cache: per-layer {per_layer * 1e3:.1f} ms, head "
-                   f"{head * 1e3:.1f} ms, MTP head {t_mtp * 1e3:.1f} ms; extrapolated to 32 layers and the GPU "
-                   f"run's {tf:.2f} target + {mf:.2f} MTP forwards and {tok_round:.2f} tokens per round at "
-                   f"batch 1; setup {setup:.0f}s untimed"),
+        "batch": 1,
+        "host": {"cpu_model": model_name, "nproc": nproc, "cpus_available": avail},
+        "sample": (f"CPU oracle (C restatement of the reference f32 CPU path: row-parallel online-softmax "
+                   f"attention, f32 GEMV; {threads} OpenMP threads on {avail} available CPUs of '{model_name}') "
+                   f"on a 2-layer slice of config 4 (INT4-dequantised f32 weights), K=4 verify rows over a "
+                   f"{CTX}-token cache at batch 1: per-layer {per_layer * 1e3:.1f} ms, head {head * 1e3:.1f} ms, "
+                   f"MTP head {t_mtp * 1e3:.1f} ms; extrapolated to 32 layers and the GPU run's {tf:.2f} target + "
+                   f"{mf:.2f} MTP forwards and {tok_round:.2f} tokens per round.  The reference engines serve one "
+                   f"request at a time, so this is also its rate at batch 32; setup {setup:.0f}s untimed"),
         "verify_ms": t_verify * 1e3,
     }
 
@@ -300,11 +413,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=12)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batches", type=str, default="1,32")
+    ap.add_argument("--batches", type=str, default="1,8,32")
     ap.add_argument("--verify-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["c4", "c5"], default="c4",
-                    help="c4: the BASELINE metric (default); c5: the MLA + MoE verify step")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config-2 and config-3 measurements")
+    ap.add_argument("--workload", choices=["c4", "c5", "c2", "c3"], default="c4",
+                    help="c4: the BASELINE metric (default, with c2 / c3 beside it); c5: the MLA + MoE verify "
+                         "step; c2 / c3: only that measurement (profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (counter calibration for rocprof --pmc)")
     args = ap.parse_args()
@@ -324,14 +439,27 @@ def main():
               "no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
     args.batches = [int(x) for x in args.batches.split(",")]
+    if args.workload in ("c4", "c2") and not (args.workload == "c4" and args.no_extra):
+        import torch  # torch's device runtime starts before the library's (the c2 inputs are torch tensors)
+        torch.zeros(1, device="cuda")
     if args.workload == "c5":
         run_c5(args)
         return
-    res = run_gpu(args)
+    if args.workload == "c2":
+        print(json.dumps({"c2_acceptance": run_c2(args)}))
+        return
+    if args.workload == "c3":
+        print(json.dumps({"c3_verify": {str(b): v for b, v in run_c3(args).items()}}))
+        return
+    res = run_c4(args)
+    c2 = c3 = None
+    if not args.no_extra:
+        c2 = run_c2(args)
+        c3 = run_c3(args)
     bmain = max(args.batches)
     main_r = res[bmain]
     b1 = res.get(1, main_r)
-    g1 = b1["int4_gemv"]
+    g1 = b1["int4_proj"]
     roof = {
         "kernel": "gemv_tile_kernel<INT4,4,*> (all INT4 projections of the batch-1 verify step: qkv, wo, gate/up, "
                   "down; K = 4 rows)",
@@ -344,11 +472,27 @@ def main():
         "avg_launch_us": round(g1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(g1["avg_bytes"]),
     }
+    a1 = b1["attention"]
+    roof_att = {
+        "kernel": "attn_mfma_kernel<INT8> (decode attention of the batch-1 verify step, 4096-token INT8 cache)",
+        "bound": "hbm", "achieved": round(a1["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(a1["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(a1["avg_us"], 3),
+        "avg_alg_bytes_per_launch": round(a1["alg_bytes_per_step"] / C4["n_layers"]),
+    }
+    roof_gemm = None
+    if 32 in res:
+        gm = res[32]["int4_proj"]
+        roof_gemm = {
+            "kernel": "gemm_kernel<INT4,*> (INT4 projections of the batch-32 verify step, M = 128 rows; useful "
+                      "FLOPs 2*M*N*K, the fp16 hi + lo activation split issues twice as many)",
+            "bound": "mfma", "achieved": round(gm["useful_tflops"], 1), "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(gm["useful_tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+            "avg_launch_us": round(gm["avg_us"], 3),
+        }
     cpu = None
     if not args.no_cpu and 1 in res:
-        threads = min(16, os.cpu_count() or 1)
         try:
-            cpu = cpu_baseline(res[1], threads)
+            cpu = cpu_baseline(res[1])
         except Exception as exc:  # the CPU leg must not hide the GPU result
             cpu = {"error": str(exc)}
     line = {
@@ -364,16 +508,22 @@ def main():
         "vs_baseline": None,
         "dtype": "int4-weight x fp16(hi+lo)-activation, f32 accumulate",
         "data": "synthetic (random-init weights N(0,0.02^2), synthetic 4096-token INT8 KV, greedy MTP)",
-        "config": {"workload": f"C4 INT4 g128 MTP k=3 verify rounds, batch {bmain} (batch 1 beside), "
-                               f"4096-token INT8 KV",
+        "config": {"workload": f"C4 INT4 g128 MTP k=3 verify rounds, batch {bmain} (batches "
+                               f"{','.join(str(b) for b in args.batches)} beside), 4096-token INT8 KV",
                    "batch": bmain, "verify_rows_per_seq": K_ROWS, "context": CTX},
-        "batch1": {k: b1[k] for k in ("tokens_per_s", "ms_per_step", "acceptance_rate", "tokens_per_round")}
-        if 1 in res else None,
+        "per_batch": {str(b): {k: r[k] for k in ("tokens_per_s", "ms_per_step", "acceptance_rate",
+                                                 "tokens_per_round")} for b, r in res.items()},
         "verify_step": {str(b): {k: r["verify"][k] for k in ("ms_wall", "ms_kernels", "alg_bytes", "hbm_gbs",
-                                                               "hbm_frac", "gemm_tflops")} for b, r in res.items()},
+                                                               "hbm_frac")} for b, r in res.items()},
         "roofline": roof,
+        "roofline_attention": roof_att,
+        "roofline_gemm": roof_gemm,
+        "c2_acceptance": c2,
+        "c3_verify": {str(b): {k: v[k] for k in ("ms_wall", "alg_bytes", "hbm_gbs", "hbm_frac")}
+                      for b, v in c3.items()} if c3 else None,
         "cpu_baseline": cpu,
-        "detail": {str(b): r for b, r in res.items()},
+        "detail": {"c4": {str(b): r for b, r in res.items()},
+                   "c3": {str(b): v for b, v in c3.items()} if c3 else None},
     }
     print(json.dumps(line))
 
