@@ -53,7 +53,15 @@ class DeviceError(AarambhError):
     pass
 
 
-_ERRS = {1: ConfigError, 2: ShapeError, 3: UnsupportedError, 4: DeviceError}
+class CheckpointError(AarambhError):
+    pass
+
+
+class IoError(AarambhError):
+    pass
+
+
+_ERRS = {1: ConfigError, 2: ShapeError, 3: UnsupportedError, 4: DeviceError, 5: CheckpointError, 6: IoError}
 
 
 class _Cfg(C.Structure):
@@ -107,6 +115,15 @@ def lib():
         "aarh_load_tensor_int4": (C.c_int, [_P, C.c_int, _P, _P, _P, C.c_int64, C.c_int64, C.c_int32]),
         "aarh_load_tensor_int8": (C.c_int, [_P, C.c_int, _P, _P, C.c_int64, C.c_int64]),
         "aarh_init_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float]),
+        "aarh_get_config": (C.c_int, [_P, C.POINTER(_Cfg)]),
+        "aarh_load_gguf": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
+        "aarh_load_safetensors": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
+        "aarh_gguf_config": (C.c_int, [C.c_char_p, C.POINTER(_Cfg)]),
+        "aarh_gguf_read_tensor": (C.c_int, [C.c_char_p, C.c_char_p, _P, C.c_int64, C.POINTER(C.c_int64),
+                                            C.POINTER(C.c_int32), C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+        "aarh_safetensors_read_tensor": (C.c_int, [C.c_char_p, C.c_char_p, _P, C.c_int64, C.POINTER(C.c_int64),
+                                                   C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
+        "aarh_host_last_error": (C.c_char_p, []),
         "aarh_kv_reset": (C.c_int, [_P, C.c_int]),
         "aarh_kv_len": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
         "aarh_kv_rollback": (C.c_int, [_P, C.c_int, C.c_int32]),
@@ -169,7 +186,9 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
             "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs", "aarh_session_rng_offsets",
-            "aarh_session_set_rng_offsets", "aarh_accept_sample_static",
+            "aarh_session_set_rng_offsets", "aarh_accept_sample_static", "aarh_get_config", "aarh_load_gguf",
+            "aarh_load_safetensors", "aarh_gguf_config", "aarh_gguf_read_tensor", "aarh_host_last_error",
+            "aarh_safetensors_read_tensor",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -178,6 +197,34 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
 
 def _ptr(a):
     return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _host_check(st):
+    if st:
+        raise _ERRS.get(st, AarambhError)(lib().aarh_host_last_error().decode())
+
+
+def gguf_read_tensor(path, name):
+    """One tensor of a GGUF v1 file decoded to f32 by the library's host reader
+    (decode_tensor, weights/src/gguf.rs:143-241).  Returns (values, encoding)."""
+    n, nd, enc = C.c_int64(), C.c_int32(), C.c_int32()
+    shape = (C.c_int64 * 8)()
+    p, nm = os.fsencode(path), name.encode()
+    _host_check(lib().aarh_gguf_read_tensor(p, nm, None, 0, C.byref(n), C.byref(nd), shape, C.byref(enc)))
+    out = np.empty(n.value, np.float32)
+    _host_check(lib().aarh_gguf_read_tensor(p, nm, _ptr(out), out.size, None, None, None, None))
+    return out.reshape([shape[i] for i in range(nd.value)]), enc.value
+
+
+def safetensors_read_tensor(path, name):
+    """One tensor of a safetensors file as f32 by the library's host reader."""
+    n, nd = C.c_int64(), C.c_int32()
+    shape = (C.c_int64 * 8)()
+    p, nm = os.fsencode(path), name.encode()
+    _host_check(lib().aarh_safetensors_read_tensor(p, nm, None, 0, C.byref(n), C.byref(nd), shape))
+    out = np.empty(n.value, np.float32)
+    _host_check(lib().aarh_safetensors_read_tensor(p, nm, _ptr(out), out.size, None, None, None))
+    return out.reshape([shape[i] for i in range(nd.value)])
 
 
 @dataclass
@@ -196,6 +243,18 @@ class ModelConfig:
     weight_format: int = W_F32
     lm_head_format: int = 0
     kv_format: int = KV_F32
+
+    @classmethod
+    def from_gguf(cls, path, **overrides):
+        """Model shape from a GGUF v1 file's config (load_gguf_tensors, gguf.rs:91-125);
+        storage formats come from `overrides` (defaults as the dataclass)."""
+        c = _Cfg()
+        _host_check(lib().aarh_gguf_config(os.fsencode(path), C.byref(c)))
+        kw = dict(vocab_size=c.vocab_size, hidden_dim=c.hidden_dim, ffn_dim=c.ffn_dim, n_layers=c.n_layers,
+                  n_heads=c.n_heads, n_kv_heads=c.n_kv_heads, max_seq_len=c.max_seq_len, rope_theta=c.rope_theta,
+                  norm_eps=c.norm_eps, num_future_tokens=c.num_future_tokens)
+        kw.update(overrides)
+        return cls(**kw)
 
     @property
     def head_dim(self):  # core/src/config.rs:866-868
@@ -338,6 +397,18 @@ class HipModel:
         q = np.ascontiguousarray(codes, np.int8)
         s = np.ascontiguousarray(scales, np.float32)
         self._check(lib().aarh_load_tensor_int8(self.h, tid, _ptr(q), _ptr(s), rows, cols))
+
+    def load_gguf(self, path):
+        """Loads every tensor of a GGUF v1 checkpoint (load_gguf, gguf.rs:82-89); returns the count."""
+        n = C.c_int32()
+        self._check(lib().aarh_load_gguf(self.h, os.fsencode(path), C.byref(n)))
+        return n.value
+
+    def load_safetensors(self, path):
+        """Loads a safetensors checkpoint (load_model_with_dtype, weights/src/lib.rs:68-79)."""
+        n = C.c_int32()
+        self._check(lib().aarh_load_safetensors(self.h, os.fsencode(path), C.byref(n)))
+        return n.value
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(lib().aarh_init_synthetic(self.h, seed, std))

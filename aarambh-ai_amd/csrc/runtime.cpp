@@ -553,6 +553,11 @@ int sync_stream(aarh_ctx* c) {
 
 }  // namespace
 
+namespace aarh {
+// Records a failure on a context for the library's other translation units (weights.cpp).
+int ctx_fail(aarh_ctx* c, int code, const char* msg) { return fail(c, code, "%s", msg); }
+}  // namespace aarh
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -849,6 +854,12 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
 }
 
 int aarh_num_tensors(const aarh_ctx* c) { return (int)c->slots.size(); }
+
+int aarh_get_config(const aarh_ctx* c, aarh_model_config* out) {
+    if (!c || !out) return AARH_ERR_CONFIG;
+    *out = c->cfg;
+    return AARH_OK;
+}
 
 int aarh_tensor_info(const aarh_ctx* c, int id, char* name, int name_cap, int64_t* rows, int64_t* cols,
                      int32_t* kind) {

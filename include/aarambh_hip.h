@@ -24,13 +24,16 @@
 extern "C" {
 #endif
 
-/* Mirrors AarambhError (core/src/error.rs:5-33): Config, Shape, Unsupported, plus Device. */
+/* Mirrors AarambhError (core/src/error.rs:5-33): Config, Shape, Unsupported, Checkpoint,
+   Io, plus Device. */
 typedef enum {
     AARH_OK = 0,
     AARH_ERR_CONFIG = 1,
     AARH_ERR_SHAPE = 2,
     AARH_ERR_UNSUPPORTED = 3,
-    AARH_ERR_DEVICE = 4
+    AARH_ERR_DEVICE = 4,
+    AARH_ERR_CHECKPOINT = 5,
+    AARH_ERR_IO = 6
 } aarh_status;
 
 /* Weight storage formats (quant/src/types.rs:68-90 plus the build's layouts). */
@@ -95,6 +98,35 @@ int aarh_load_tensor_int4(aarh_ctx *ctx, int id, const uint8_t *packed, const ui
 /* Per-row INT8 codes + f32 row scales (I8QuantizedTensor semantics per channel). */
 int aarh_load_tensor_int8(aarh_ctx *ctx, int id, const int8_t *codes, const float *scales,
                           int64_t rows, int64_t cols);
+/* The configuration the context was created with. */
+int aarh_get_config(const aarh_ctx *ctx, aarh_model_config *out);
+
+/* --- checkpoints (host readers; tensors decoded to f32 as the reference decodes them, then
+   quantised on device into the context's formats like aarh_load_tensor_f32) ---
+   GGUF v1 (load_gguf_tensors, weights/src/gguf.rs:91-241): F32, Q8_0 (per-tensor absmax,
+   dequant.rs:7-16) and Q4_K_M (gguf_quant.rs:37-49, custom f16 at :51-112).  The file's
+   config (config.rs:734-776) must match the context's shape, rope_theta and norm_eps, with
+   tied embeddings and no rope_scaling / moe / attention_schedule / dsa_config.
+   safetensors (load_model_with_dtype, weights/src/lib.rs:68-79): F32, F16 and BF16 values.
+   Every context tensor must be present with its checkpoint shape (norms 1-D); other tensors
+   are ignored, as VarBuilder reads by name.  *out_loaded (optional) = tensors loaded. */
+int aarh_load_gguf(aarh_ctx *ctx, const char *path, int32_t *out_loaded);
+int aarh_load_safetensors(aarh_ctx *ctx, const char *path, int32_t *out_loaded);
+/* Fills the model-shape fields of *out (vocab_size .. max_seq_len, rope_theta, norm_eps,
+   num_future_tokens from mtp) from a GGUF file's config; formats and sizing are left to
+   the caller (the file is what from_paths reads its config from, engine.rs:226-244). */
+int aarh_gguf_config(const char *path, aarh_model_config *out);
+/* Decodes one GGUF tensor to f32 on the host (no context, no GPU).  out may be NULL to query
+   numel/ndims/shape (shape holds up to 8 dims)/encoding (0 F32, 1 Q8_0, 2 Q4_K_M). */
+int aarh_gguf_read_tensor(const char *path, const char *name, float *out, int64_t cap,
+                          int64_t *out_numel, int32_t *out_ndims, int64_t *out_shape,
+                          int32_t *out_encoding);
+/* Decodes one safetensors tensor (F32 / F16 / BF16) to f32 on the host (no context, no GPU). */
+int aarh_safetensors_read_tensor(const char *path, const char *name, float *out, int64_t cap,
+                                 int64_t *out_numel, int32_t *out_ndims, int64_t *out_shape);
+/* Message of the last failure of a context-free call on this thread. */
+const char *aarh_host_last_error(void);
+
 /* Random-init model generated on device: N(0, std^2) linears/embedding, norms 1.0. */
 int aarh_init_synthetic(aarh_ctx *ctx, uint64_t seed, float std);
 
