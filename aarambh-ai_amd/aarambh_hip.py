@@ -30,6 +30,7 @@ KV_F32, KV_F16, KV_INT8 = 0, 1, 2
 T_NORM, T_LINEAR, T_EMBED = 0, 1, 2
 FLAG_RATIO_NEAR, FLAG_CDF_NEAR, FLAG_TOPP_NEAR = 1, 2, 8
 TOP_CANDIDATES = 5  # engine.rs:70
+REPLAY_REPLACEMENT, REPLAY_REFERENCE = 0, 1
 PROF_NAMES = ["gemv_qkv", "gemv_wo", "gemv_gateup", "gemv_down", "gemv_lmhead", "attention", "accept", "other"]
 
 
@@ -116,6 +117,7 @@ def lib():
         "aarh_load_tensor_int8": (C.c_int, [_P, C.c_int, _P, _P, C.c_int64, C.c_int64]),
         "aarh_init_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float]),
         "aarh_get_config": (C.c_int, [_P, C.POINTER(_Cfg)]),
+        "aarh_set_replay_schedule": (C.c_int, [_P, C.c_int]),
         "aarh_load_gguf": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
         "aarh_load_safetensors": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
         "aarh_gguf_config": (C.c_int, [C.c_char_p, C.POINTER(_Cfg)]),
@@ -186,7 +188,7 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_accept_sample", "aarh_mtp_generate", "aarh_session_begin", "aarh_session_step",
             "aarh_session_result", "aarh_session_end", "aarh_spec_generate", "aarh_prof_enable", "aarh_prof_get",
             "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs", "aarh_session_rng_offsets",
-            "aarh_session_set_rng_offsets", "aarh_accept_sample_static", "aarh_get_config", "aarh_load_gguf",
+            "aarh_session_set_rng_offsets", "aarh_accept_sample_static", "aarh_get_config", "aarh_set_replay_schedule", "aarh_load_gguf",
             "aarh_load_safetensors", "aarh_gguf_config", "aarh_gguf_read_tensor", "aarh_host_last_error",
             "aarh_safetensors_read_tensor",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
@@ -457,6 +459,10 @@ class HipModel:
     def stream(self):
         return lib().aarh_stream(self.h)
 
+    def set_replay_schedule(self, schedule):
+        """REPLAY_REPLACEMENT (default) or REPLAY_REFERENCE (mtp_speculative.rs:302-313)."""
+        self._check(lib().aarh_set_replay_schedule(self.h, int(schedule)))
+
     def set_graphs(self, on=True):
         """Replay captured HIP graphs for repeated verify-forward shapes (default on)."""
         self._check(lib().aarh_set_graphs(self.h, 1 if on else 0))
@@ -651,7 +657,7 @@ class Session:
 
 
 # ---------------------------------------------------------------------------
-# Latent-attention MoE decoder
+# Latent-attention MoE decoder (benchmark config 5)
 # ---------------------------------------------------------------------------
 @dataclass
 class LatConfig:

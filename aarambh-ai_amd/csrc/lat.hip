@@ -1,5 +1,5 @@
 // Latent-attention (MLA) + fine-grained MoE decoder kernels for gfx950
-//
+// (benchmark config 5).
 //
 // MLA (nn/src/mla.rs:300-489): the cache holds c_kv = RMSNorm(kv_a_proj(x))
 // and the shared rotary key k_rope per token.  Instead of reconstructing

@@ -1,4 +1,4 @@
-// Host runtime of the latent-attention MoE decoder: context,
+// Host runtime of the latent-attention MoE decoder (benchmark config 5): context,
 // device weights, the fp16 latent cache, the verify forward over the gfx950
 // kernels of lat.hip and the aarh_lat_* C ABI of include/aarambh_hip.h.
 //
@@ -175,6 +175,10 @@ int alloc_tensor(Ctx* c, LTensor& t, int fmt, int N, int K) {
     t.fmt = fmt;
     t.N = N;
     t.K = K;
+    // projection kernels address weights through one buffer resource with 32-bit byte offsets
+    if (weight_bytes(fmt, N, K) >= ((size_t)1 << 31))
+        return fail(c, AARH_ERR_UNSUPPORTED, "a %d x %d weight matrix of %zu bytes exceeds the 2 GiB per-tensor limit", N,
+                    K, weight_bytes(fmt, N, K));
     if (dalloc(c, &t.w, weight_bytes(fmt, N, K))) return AARH_ERR_DEVICE;
     HIPCHK(c, hipMemset(t.w, 0, weight_bytes(fmt, N, K)));
     if (fmt == WF_INT4) {

@@ -125,6 +125,7 @@ struct aarh_ctx {
     uint64_t gclock = 0;
 
     // profiling
+    int replay_schedule = AARH_REPLAY_REPLACEMENT;
     bool prof = false;
     std::vector<ProfRec> prof_recs;
     std::vector<hipEvent_t> ev_pool;
@@ -186,6 +187,10 @@ int alloc_tensor(aarh_ctx* c, DevTensor& t, int fmt, int N, int K) {
     t.fmt = fmt;
     t.N = N;
     t.K = K;
+    // GEMV / GEMM address weights through one buffer resource with 32-bit byte offsets
+    if (weight_bytes(fmt, N, K) >= ((size_t)1 << 31))
+        return fail(c, AARH_ERR_UNSUPPORTED, "a %d x %d weight matrix of %zu bytes exceeds the 2 GiB per-tensor limit", N,
+                    K, weight_bytes(fmt, N, K));
     if (dalloc(c, &t.w, weight_bytes(fmt, N, K))) return AARH_ERR_DEVICE;
     HIPCHK(c, hipMemset(t.w, 0, weight_bytes(fmt, N, K)));
     if (fmt == WF_INT4) {
@@ -722,7 +727,7 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     if (g.weight_format < 0 || g.weight_format > 3 || (g.lm_head_format != 0 && g.lm_head_format != 1) ||
         g.kv_format < 0 || g.kv_format > 2)
         return bad(AARH_ERR_CONFIG, "unknown weight / lm head / kv format");
-    if (g.max_rows > 128) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 128");
+    if (g.max_rows > 512) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 512");
     c->Fp = (c->F + 127) / 128 * 128;
     c->Mmax = g.max_rows;
     // V^T rows padded so 32-token blocks stay in bounds; PAD_SLACK positions past the
@@ -1263,6 +1268,14 @@ int aarh_top_candidates(aarh_ctx* c, const float* logits, int rows, int V, const
     return 0;
 }
 
+int aarh_set_replay_schedule(aarh_ctx* c, int schedule) {
+    if (!c) return AARH_ERR_CONFIG;
+    if (schedule != AARH_REPLAY_REPLACEMENT && schedule != AARH_REPLAY_REFERENCE)
+        return fail(c, AARH_ERR_CONFIG, "unknown replay schedule %d", schedule);
+    c->replay_schedule = schedule;
+    return 0;
+}
+
 int aarh_set_graphs(aarh_ctx* c, int enable) {
     if (!c) return AARH_ERR_CONFIG;
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1498,14 +1511,16 @@ int session_round(aarh_session* e) {
         if (np > 1) e->stats[b].mtp_head_forwards += np - 1;
         if (!e->greedy) e->hoffs[b] += np;
     }
-    // ---- verify forward (finished sequences run at a dummy position 0) ----
+    // ---- verify forward ----
+    // Finished sequences ride along with padding rows written just past their committed
+    // length (inside the PAD_SLACK positions every slot has beyond max_seq_len); their
+    // kv_len stays, so the slot's cache remains valid for a cached_len follow-up.
     {
         std::vector<uint32_t> ids((size_t)nseq * Kr);
         std::vector<int32_t> off(nseq);
         for (int b = 0; b < nseq; b++) {
             for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = e->hprops[(size_t)b * K + std::min(s2, K - 1)];
-            off[b] = e->finished[b] ? 0 : e->base[b];
-            if (e->finished[b]) c->kv_len[b] = 0;
+            off[b] = e->base[b];
         }
         int mk = 0;
         if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK))) return r;
@@ -1591,29 +1606,43 @@ int session_round(aarh_session* e) {
     // rows that come from the verify buffers must be copied before the replay reuses scratch
     if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hs, hdv, H))) return r;
     if (!replay_seq.empty()) {
-        // one row per rejected sequence: the replacement at base + acc
+        // replacement schedule: one row per rejected sequence, the replacement at base + acc;
+        // reference schedule: proposals[..acc] + replacement from base (rows padded to the
+        // longest by repeating the replacement past it; kv_len excludes the padding)
         const int nr = (int)replay_seq.size();
-        std::vector<uint32_t> ids(nr);
-        std::vector<int32_t> sl(nr), off(nr);
+        const bool full = c->replay_schedule == AARH_REPLAY_REFERENCE;
+        int S = 1;
+        if (full)
+            for (int j = 0; j < nr; j++) S = std::max(S, replay_len[j] + 1);
+        std::vector<uint32_t> ids((size_t)nr * S);
+        std::vector<int32_t> sl(nr), off(nr), last(nr);
         for (int j = 0; j < nr; j++) {
-            const int b = replay_seq[j];
+            const int b = replay_seq[j], acc = replay_len[j];
             sl[j] = b;
-            off[j] = e->base[b] + replay_len[j];
-            ids[j] = e->hprops[(size_t)b * K + replay_len[j]];
+            if (full) {
+                off[j] = e->base[b];
+                last[j] = j * S + acc;
+                for (int s2 = 0; s2 < S; s2++) ids[(size_t)j * S + s2] = e->hprops[(size_t)b * K + std::min(s2, acc)];
+            } else {
+                off[j] = e->base[b] + acc;
+                last[j] = j;
+                ids[j] = e->hprops[(size_t)b * K + acc];
+            }
         }
         int mk = 0;
-        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, 1, &mk, PAD_SLACK))) return r;
-        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, 1, mk, c->logits, rm(nr, 0, V), c->hidden)))
+        if ((r = stage_rows(c, ids.data(), sl.data(), off.data(), nr, S, &mk, PAD_SLACK))) return r;
+        if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nr, S, mk, c->logits, rm(S, (long long)S * V, V),
+                             c->hidden)))
             return r;
         std::vector<const float*> rs, rhs;
         std::vector<float*> rd, rhd;
         for (int j = 0; j < nr; j++) {
             const int b = replay_seq[j];
             e->stats[b].target_decode_forwards++;
-            c->kv_len[b] = off[j] + 1;
-            rs.push_back(c->logits + (size_t)j * V);
+            c->kv_len[b] = e->base[b] + replay_len[j] + 1;
+            rs.push_back(c->logits + (size_t)last[j] * V);
             rd.push_back(e->tgt + (size_t)b * (K + 1) * V);
-            rhs.push_back(c->hidden + (size_t)j * H);
+            rhs.push_back(c->hidden + (size_t)last[j] * H);
             rhd.push_back(e->anchor + (size_t)b * H);
         }
         if ((r = copy_rows_host_lists(e, rs, rd, V)) || (r = copy_rows_host_lists(e, rhs, rhd, H))) return r;
@@ -1638,6 +1667,8 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
     if (num_draft_tokens > g.num_future_tokens)
         return fail(c, AARH_ERR_CONFIG, "requested %d MTP proposal tokens but checkpoint horizon is %d", num_draft_tokens,
                     g.num_future_tokens);
+    if (num_draft_tokens >= PAD_SLACK)
+        return fail(c, AARH_ERR_UNSUPPORTED, "num_draft_tokens must be below %d on the device path", PAD_SLACK);
     if (nseq <= 0 || nseq > g.max_batch) return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
     if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
     if (cached_len < 0) return fail(c, AARH_ERR_SHAPE, "negative cached length");

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X speculative verify path (BASELINE.json metric).
+"""Benchmark of the MI355X speculative verify path (headline metric).
 
-Workload: random-init decoder, 32 layers, d_model 4096,
+Workload (benchmark config 4): random-init decoder, 32 layers, d_model 4096,
 32 query / 8 KV heads (head_dim 128), SwiGLU ffn 11008, vocab 32000; INT4 g128
 weights (fp16 scale/zero) drawn N(0, 0.02^2) before quantisation, bf16 tied LM
 head, 3 MTP heads (num_future_tokens 4, k = 3 drafts + 1 -> K = 4 verify rows),
@@ -192,7 +192,7 @@ def run_c4(args):
 
 
 def run_c2(args):
-    """the standalone fused acceptance kernel, 32 sequences x k = 4
+    """benchmark config 2: the standalone fused acceptance kernel, 32 sequences x k = 4
     draft positions x vocab 32000, target logits N(0, 3^2), draft = target + N(0, 1),
     T = 0.8, draft tokens drawn from the draft distribution, seeded uniforms (external-
     draft round with bonus row).  One call reads 36 864 000 bytes of logits."""
@@ -228,7 +228,7 @@ def run_c2(args):
 
 
 def run_c3(args):
-    """INT8 per-row verify, 16 layers, d 2048, 16 / 4 heads, ffn 5632,
+    """benchmark config 3: INT8 per-row verify, 16 layers, d 2048, 16 / 4 heads, ffn 5632,
     fp16 KV cache of 2048 tokens, K = 4 rows at batch 1 and 16."""
     import aarambh_hip as A
 
@@ -341,7 +341,7 @@ C5_ROWS = 5  # k = 4 drafts + 1
 
 
 def run_c5(args):
-    """BASELINE config 5 verify step: 24-layer MLA + fine-grained MoE decoder, k = 4
+    """benchmark config 5 verify step: 24-layer MLA + fine-grained MoE decoder, k = 4
     (5 rows per sequence) over a 4096-token latent cache, INT4 g128 experts (MLA
     projections and router INT4 too), bf16 tied LM head."""
     import aarambh_hip as A
@@ -418,7 +418,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config-2 and config-3 measurements")
     ap.add_argument("--workload", choices=["c4", "c5", "c2", "c3"], default="c4",
-                    help="c4: the BASELINE metric (default, with c2 / c3 beside it); c5: the MLA + MoE verify "
+                    help="c4: the headline metric (default, with c2 / c3 beside it); c5: the MLA + MoE verify "
                          "step; c2 / c3: only that measurement (profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (counter calibration for rocprof --pmc)")

@@ -61,7 +61,7 @@ typedef struct {
     int32_t lm_head_format;    /* AARH_W_F32 or AARH_W_BF16: tied embedding / LM head storage */
     int32_t kv_format;         /* AARH_KV_* */
     int32_t max_batch;         /* KV-cache sequence slots */
-    int32_t max_rows;          /* max rows (sequences x tokens) per forward call, <= 128 */
+    int32_t max_rows;          /* max rows (sequences x tokens) per forward call, <= 512 */
 } aarh_model_config;
 
 /* Sampler (inference/src/sampler.rs:14-65); probabilities as filtered_probs (:226-278). */
@@ -240,6 +240,14 @@ int aarh_top_candidates(aarh_ctx *ctx, const float *logits, int rows, int V, con
    0 launches every kernel from the host each call).  Results are identical either way. --- */
 int aarh_set_graphs(aarh_ctx *ctx, int enable);
 
+/* --- MTP rejection replay schedule.  AARH_REPLAY_REPLACEMENT (default): the verify forward
+   already wrote the accepted proposals' K / V at their positions, so only the replacement
+   token is forwarded.  AARH_REPLAY_REFERENCE: restore to the round's base and forward
+   proposals[..i] + replacement as mtp_speculative.rs:284-313 does.  Both give the same
+   function; they differ only in rounding (which rows are computed together). --- */
+enum { AARH_REPLAY_REPLACEMENT = 0, AARH_REPLAY_REFERENCE = 1 };
+int aarh_set_replay_schedule(aarh_ctx *ctx, int schedule);
+
 /* --- measurement: per-kernel-class timing of the context's launches (HIP events recorded
    at each kernel dispatch's own start and end; graph replay is off while enabled) --- */
 enum { AARH_PROF_GEMV_QKV = 0, AARH_PROF_GEMV_WO = 1, AARH_PROF_GEMV_GATEUP = 2,
@@ -249,7 +257,7 @@ int aarh_prof_enable(aarh_ctx *ctx, int enable);
 int aarh_prof_get(aarh_ctx *ctx, int cls, double *total_ms, double *alg_bytes, int64_t *launches);
 
 /* ===================================================================================
- * Latent-attention MoE decoder: blocks of multi-head latent
+ * Latent-attention MoE decoder (benchmark config 5): blocks of multi-head latent
  * attention (nn/src/mla.rs:300-489, built by model/src/model.rs:1094-1156) and a
  * fine-grained MoE FFN with top-k routing and shared experts (nn/src/moe.rs:127-406).
  * A separate context type with the same conventions as aarh_ctx; its cache holds the

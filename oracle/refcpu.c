@@ -795,7 +795,7 @@ ref_model *ref_model_create(const ref_config *cfg) {
         c->n_heads <= 0 || c->n_kv_heads <= 0 || c->max_seq_len <= 0)
         return NULL;
     if (c->hidden_dim % c->n_heads || c->n_heads % c->n_kv_heads) return NULL;
-    /* model.rs:309-313 requires head_dim == 64; the BASELINE shapes use 32 and 128,
+    /* model.rs:309-313 requires head_dim == 64; the benchmark shapes use 32 and 128,
        so that check is dropped here (documented divergence). */
     ref_model *m = (ref_model *)calloc(1, sizeof(ref_model));
     m->cfg = *c;
@@ -1823,7 +1823,7 @@ int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_le
 }
 
 /* ======================================================================== */
-/* Latent-attention MoE decoder: every block is          */
+/* Latent-attention MoE decoder (benchmark config 5): every block is          */
 /* x += MLA(norm1(x)) (nn/src/mla.rs:300-314,402-489; builder                */
 /* model/src/model.rs:1094-1156) then x += MoE(norm2(x)) (nn/src/moe.rs:     */
 /* 212-340, top_k_gating :361-406, SharedExpertPath :127-178).  The MLA      */
@@ -1995,7 +1995,7 @@ int ref_lat_get_tensor(const ref_lat *m, int id, float *out) {
 
 /* Synthetic random-init model: tensor id i ~ N(0, std^2) on stream i, the
    router ~ N(0, 1/hidden_dim) so its logits on RMS-normalised inputs are about
-   N(0, 1), norms 1.  The device's synthetic init uses the
+   N(0, 1) (benchmark config 5), norms 1.  The device's synthetic init uses the
    same streams and scales. */
 int ref_lat_init_synthetic(ref_lat *m, uint64_t seed, float std) {
     const float router_std = 1.0f / sqrtf((float)m->cfg.hidden_dim);

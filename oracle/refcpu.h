@@ -174,7 +174,7 @@ int ref_plain_generate(const ref_model *m, const uint32_t *prompt, int prompt_le
                        int max_new_tokens, const ref_sampler *s, uint64_t seed, int nthreads,
                        uint32_t *out_tokens, int *out_len, int *finish_reason);
 
-/* ---------------- Latent-attention MoE decoder ---------------- */
+/* ---------------- Latent-attention MoE decoder (benchmark config 5) ---------------- */
 typedef struct {
     int32_t vocab_size, hidden_dim, n_layers, n_heads, max_seq_len;
     float rope_theta, norm_eps;

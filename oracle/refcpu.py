@@ -545,7 +545,7 @@ class KvCache:
         return logits
 
 
-# ---------------- latent-attention MoE decoder ----------------
+# ---------------- latent-attention MoE decoder (benchmark config 5) ----------------
 def make_lat_config(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, latent_dim, rope_dim, nope_dim, v_dim,
                     n_experts, top_k, expert_dim, n_shared, expert_format=W_F32, attn_format=W_F32,
                     lm_head_format=0, kv_format=KV_F32, rope_theta=10000.0, norm_eps=1e-5):

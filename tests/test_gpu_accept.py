@@ -22,7 +22,7 @@ def ctx():
 
 
 def c2_inputs(B=32, K=4, V=32000, T=0.8, seed=0):
-    """target ~ N(0, 3^2), draft = target + N(0, 1), draft tokens
+    """benchmark config 2: target ~ N(0, 3^2), draft = target + N(0, 1), draft tokens
     sampled from the draft distribution with the oracle's sequential CDF."""
     rng = np.random.default_rng(seed)
     tgt = rng.normal(0, 3, (B, K + 1, V)).astype(np.float32)

@@ -10,17 +10,19 @@ import pytest
 
 import aarambh_hip as A
 import refcpu as R
-from gpu_util import first_divergent_round, make_pair, mtp_rounds_vs_oracle
+from gpu_util import first_divergent_round, make_pair, mtp_rounds_vs_oracle, rel_rows
 
 pytestmark = pytest.mark.gpu
 
 
-def test_c1_config_greedy_mtp_bit_exact():
-    # 4 layers, d 256, 8q/2kv (hd 32), ffn 704, vocab 4096, 1 MTP head,
+@pytest.mark.parametrize("replay", ["replacement", "reference"])
+def test_c1_config_greedy_mtp_bit_exact(replay):
+    # Config 1: 4 layers, d 256, 8q/2kv (hd 32), ffn 704, vocab 4096, 1 MTP head,
     # greedy k=1 (SpeculativeConfig(2)), prompt 64 ids, 128 new tokens.
     kw = dict(vocab_size=4096, hidden_dim=256, ffn_dim=704, n_layers=4, n_heads=8, n_kv_heads=2, max_seq_len=256,
               num_future_tokens=2)
     ref, hip = make_pair(seed=0, max_batch=1, max_rows=64, **kw)
+    hip.set_replay_schedule(A.REPLAY_REFERENCE if replay == "reference" else A.REPLAY_REPLACEMENT)
     prompt = R.synth_tokens(0, 0xC1, 64, 4096)
     want, fin, stats, gap = ref.mtp_generate(prompt, 128, 2, R.sampler(greedy=True))
     eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(2))
@@ -67,13 +69,16 @@ def test_int4_batched_greedy_mtp_matches_oracle_per_round():
     hip.close()
 
 
-@pytest.mark.parametrize("cfg", ["c1_t08", "k3_cli_default"])
-def test_sampled_mtp_engine_round_by_round(cfg):
-    """Sampled MTP speculation (SURVEY A.9 draw order: K proposal draws, one acceptance
-    draw per tested proposal with q > 0, one residual draw on rejection) on the device,
-    every round compared with the oracle's: committed tokens, proposed / accepted counts
-    and the keystream position after the round.  C1 model at T 0.8 (k = 1), and a
-    3-head model with the reference CLI's default sampler (T 0.7, top-k 50, top-p 0.9)."""
+@pytest.mark.parametrize("cfg,replay", [("c1_t08", "replacement"), ("k3_cli_default", "replacement"),
+                                        ("k3_cli_default", "reference")])
+def test_sampled_mtp_engine_round_by_round(cfg, replay):
+    """Sampled MTP speculation (draw order: K proposal draws, one acceptance draw per
+    tested proposal with q > 0, one residual draw on rejection) on the device, every
+    round compared with the oracle's: committed tokens, proposed / accepted counts and
+    the keystream position after the round.  C1 model at T 0.8 (k = 1), and a 3-head
+    model with the reference CLI's default sampler (T 0.7, top-k 50, top-p 0.9), under
+    both rejection replay schedules (the oracle always runs the reference's,
+    mtp_speculative.rs:302-313)."""
     if cfg == "c1_t08":
         kw = dict(vocab_size=4096, hidden_dim=256, ffn_dim=704, n_layers=4, n_heads=8, n_kv_heads=2,
                   max_seq_len=256, num_future_tokens=2)
@@ -89,6 +94,7 @@ def test_sampled_mtp_engine_round_by_round(cfg):
         s_ref = R.sampler(temperature=0.7, top_k=50, top_p=0.9)
         s_dev = A.Sampler.top_k_top_p(0.7, top_k=50, top_p=0.9, seed=seed)
         tol_p = 2e-4  # f32 path, |l| up to ~10: probabilities agree to ~1e-5
+    hip.set_replay_schedule(A.REPLAY_REFERENCE if replay == "reference" else A.REPLAY_REPLACEMENT)
     want, fin, stats, _ = ref.mtp_generate(prompt, n_new, K, s_ref, seed=seed)
     rounds = ref.last_rounds
     assert stats["draft_tokens_accepted"] > 0 and stats["draft_tokens_rejected"] > 0
@@ -143,6 +149,46 @@ def test_context_limit_and_engine_validation():
     want, fin, _, _ = ref.mtp_generate(np.arange(1, 6, dtype=np.uint32), 20, 3, R.sampler(greedy=True))
     assert len(out.token_ids) == 11 and out.finish_reason == "ContextLimit"
     assert out.token_ids == list(want)
+    hip.close()
+
+
+def test_ragged_finish_keeps_every_slot_cache():
+    """A sequence that finishes rounds before the others (EOS) keeps its cache: its slot
+    holds the reference's cache state (prompt + committed tokens, restored to the round's
+    base when the replacement is EOS, mtp_speculative.rs:284-288) and a follow-up forward
+    from the cached length matches the oracle's forward of the same tokens."""
+    kw = dict(vocab_size=512, hidden_dim=128, ffn_dim=256, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=96,
+              num_future_tokens=3)
+    ref, hip = make_pair(seed=21, max_batch=2, **kw)
+    emb = ref.get(0).copy()
+    emb[0] *= 6.0  # make EOS (id 0) a frequent greedy choice
+    ref.set(0, emb)
+    hip.load_f32(0, emb)
+    g = R.sampler(greedy=True)
+    runs = []
+    for ps in range(60):
+        prompt = R.synth_tokens(21, ps, 12, 512)
+        want, fin, stats, gap = ref.mtp_generate(prompt, 24, 3, g)
+        if gap > 1e-4:
+            runs.append((stats["rounds"], fin, prompt, list(want)))
+    early = [r for r in runs if r[1] == R.FINISH_EOS and len(r[3]) > 0]
+    late = [r for r in runs if r[1] == R.FINISH_MAX_TOKENS]
+    assert early and late, "no ragged pair among the candidate prompts"
+    pair = [min(early, key=lambda r: r[0]), late[0]]
+    assert pair[0][0] < pair[1][0]
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(3))
+    outs = eng.generate_batch(np.stack([pair[0][2], pair[1][2]]), 24, A.Sampler.greedy_sampler())
+    for b, (rounds, fin, prompt, want) in enumerate(pair):
+        assert outs[b].token_ids == want
+        seq = np.concatenate([prompt, np.asarray(want, np.uint32)])
+        n = hip.kv_len(b)
+        # an accepted EOS proposal leaves the whole verify in the cache (no restore)
+        assert len(prompt) <= n <= len(seq) + 3, (b, n, len(seq))
+        # forward the last cached committed token again at its own position: reads positions < m
+        m = min(n, len(seq)) - 1
+        got, _ = hip.forward_with_cache_output(seq[None, m:m + 1], [m], slots=[b])
+        wl, _ = ref.kv(96).forward(seq[:m + 1], 0)
+        assert rel_rows(got[0], wl[-1:]).max() < 1e-4
     hip.close()
 
 

@@ -133,6 +133,50 @@ def test_shape_errors_are_reported():
 
 
 @pytest.mark.parametrize("kvfmt", [A.KV_INT8, A.KV_F16])
+def test_forwards_above_128_rows(kvfmt):
+    """max_rows up to 512: a 32-sequence x 5-row verify (k = 4, 160 rows) at ragged
+    offsets, and a 384-token single-sequence prefill, at hd 128 against the oracle."""
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2, max_seq_len=512,
+              weight_format=A.W_INT4_G128, kv_format=kvfmt, lm_head_format=1)
+    ref, hip = make_pair(seed=12, max_batch=32, max_rows=512, **kw)
+    B, P, K = 32, 20, 5
+    rng = np.random.default_rng(12)
+    toks = R.synth_tokens(12, 1, B * (P + K), 2048).reshape(B, P + K)
+    plen = rng.integers(6, P + 1, B)
+    # prefill every sequence to its own length (ragged), 32 x 20 = 640 rows in two calls
+    for half in (slice(0, 16), slice(16, 32)):
+        hip.forward_with_cache_output(toks[half, :P], [0] * 16, slots=np.arange(32)[half], want_logits=False,
+                                      want_hidden=False)
+    ids = np.stack([toks[b, plen[b]:plen[b] + K] for b in range(B)])
+    gl, gh = hip.forward_with_cache_output(ids, plen)  # rewinds each slot to its offset
+    worst = 0.0
+    for b in range(B):
+        kv = ref.kv(512)  # same call structure: prefill P, rewind to plen, verify K rows
+        kv.forward(toks[b, :P], 0)
+        kv.truncate(int(plen[b]))
+        wl, wh = kv.forward(ids[b], int(plen[b]))
+        worst = max(worst, rel_rows(gl[b], wl).max(), rel_rows(gh[b], wh).max())
+    assert worst < TOL, worst
+    long = R.synth_tokens(12, 2, 384, 2048)
+    gl, _ = hip.forward_with_cache_output(long[None], [0])
+    wl, _ = ref.kv(512).forward(long, 0, nthreads=16)
+    assert rel_rows(gl[0], wl).max() < TOL
+    hip.close()
+
+
+def test_weight_tensors_of_2gib_are_rejected():
+    # a bf16 LM head of 131072 x 8192 is 2 GiB: beyond the 32-bit offsets of the
+    # projection kernels' buffer resources, so creation fails instead of wrapping
+    kw = dict(vocab_size=131072, hidden_dim=8192, ffn_dim=128, n_layers=1, n_heads=64, n_kv_heads=8, max_seq_len=32,
+              weight_format=A.W_INT4_G128, lm_head_format=1)
+    with pytest.raises(A.UnsupportedError, match="2 GiB"):
+        A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=8)
+    # 128 rows less fits
+    hip = A.HipModel(A.ModelConfig(**dict(kw, vocab_size=130944)), max_batch=1, max_rows=8)
+    hip.close()
+
+
+@pytest.mark.parametrize("kvfmt", [A.KV_INT8, A.KV_F16])
 def test_long_context_verify_over_synthetic_cache(kvfmt):
     """Verify K=4 rows over 700- and 300-token caches (many attention chunks,
     ragged offsets); the cache contents come from the shared synthetic formula."""

@@ -1,4 +1,4 @@
-"""Parity of the latent-attention MoE decoder on the device (
+"""Parity of the latent-attention MoE decoder on the device (benchmark config 5:
 MLA mla.rs:300-489 with the latent cache, fine-grained top-k MoE with shared
 experts moe.rs:127-406) against the oracle on identical random-init weights.
 Bar: logits and final hidden states within 2e-3 relative (max|d|/max|ref| per
@@ -113,7 +113,7 @@ def test_lat_ragged_offsets_and_host_loaded_weights():
 
 
 def test_lat_c5_shape_one_layer():
-    """BASELINE config 5 widths (d_model 2048, latent 512 + rope 64, 16 heads,
+    """benchmark config 5 widths (d_model 2048, latent 512 + rope 64, 16 heads,
     64 experts top-6 of width 1408 + 2 shared, INT4 experts, vocab 32000) at one
     layer over a 1000-token synthetic latent cache; batch 4 x 5 rows (GEMM path)
     and batch 1 x 5 rows (GEMV path)."""

@@ -1,5 +1,5 @@
 """Parity of the verify forward (model.rs:529-587, attention.rs:170-222) at the
-BASELINE workload widths, 2 layers deep, against the oracle on the same synthetic
+benchmark workload widths, 2 layers deep, against the oracle on the same synthetic
 weights (N(0, 0.02^2) before quantisation, both sides' generators) and the same
 synthetic caches.  Bar: logits and final hidden within 2e-3 relative per row.
 

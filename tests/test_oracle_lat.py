@@ -1,4 +1,4 @@
-"""Pins the latent-attention MoE oracle: MLA (mla.rs:300-489)
+"""Pins the latent-attention MoE oracle (benchmark config 5): MLA (mla.rs:300-489)
 and fine-grained MoE with shared experts (moe.rs:127-406)."""
 import numpy as np
 import pytest
