@@ -278,6 +278,9 @@ bool decode_payload(int enc, const std::vector<uint8_t>& pl, int64_t n, float* o
     return false;
 }
 
+int64_t numel(const std::vector<int64_t>& shape);
+bool payload_fits(int enc, uint64_t len, int64_t n);
+
 // ---------------------------------------------------------------------------
 // GGUF v1 reader (load_gguf_tensors, gguf.rs:91-125)
 // ---------------------------------------------------------------------------
@@ -313,6 +316,9 @@ int gguf_open(const char* path, Gguf& g, std::string& err) {
         return AARH_ERR_IO;
     }
     FILE* f = g.file.f;
+    fseek(f, 0, SEEK_END);
+    const uint64_t fsize = (uint64_t)ftell(f);
+    fseek(f, 0, SEEK_SET);
     char magic[4];
     uint32_t version = 0;
     if (!rd(f, magic, 4) || memcmp(magic, "GGUF", 4) != 0) {
@@ -324,7 +330,7 @@ int gguf_open(const char* path, Gguf& g, std::string& err) {
         return AARH_ERR_CHECKPOINT;
     }
     uint64_t mlen = 0;
-    if (!rd_u64(f, &mlen) || mlen > (1u << 26)) {
+    if (!rd_u64(f, &mlen) || mlen > (1u << 26) || mlen > fsize) {
         err = "invalid GGUF metadata length";
         return AARH_ERR_CHECKPOINT;
     }
@@ -356,16 +362,35 @@ int gguf_open(const char* path, Gguf& g, std::string& err) {
         t.enc = enc;
         if (!rd_u64(f, &t.payload_len)) { err = "truncated GGUF tensor " + t.name; return AARH_ERR_IO; }
         t.payload_off = ftell(f);
+        if (t.payload_len > fsize - (uint64_t)t.payload_off) { err = "truncated GGUF payload of " + t.name; return AARH_ERR_IO; }
+        if (numel(t.shape) < 0) { err = "invalid GGUF shape in " + t.name; return AARH_ERR_CHECKPOINT; }
+        if (!payload_fits(t.enc, t.payload_len, numel(t.shape))) {
+            err = std::string(t.enc == ENC_F32 ? "invalid F32 GGUF payload length" : t.enc == ENC_Q8_0 ? "invalid Q8_0 payload"
+                                                                                   : "invalid Q4_K_M GGUF payload length") +
+                  " (" + t.name + ")";
+            return AARH_ERR_CHECKPOINT;
+        }
         if (fseek(f, (long)t.payload_len, SEEK_CUR) != 0) { err = "truncated GGUF payload of " + t.name; return AARH_ERR_IO; }
         g.tensors.push_back(std::move(t));
     }
     return 0;
 }
 
+// Element count of a shape; -1 when it overflows or exceeds 2^40 values (a corrupt header).
 int64_t numel(const std::vector<int64_t>& shape) {
     int64_t n = 1;
-    for (int64_t d : shape) n *= d;
+    for (int64_t d : shape)
+        if (d < 0 || __builtin_mul_overflow(n, d, &n) || n > ((int64_t)1 << 40)) return -1;
     return n;
+}
+
+// Payload length consistent with the tensor's value count for its encoding
+// (decode_f32_tensor / decode_q8_tensor / decode_q4_k_m_tensor, gguf.rs:155-241).
+bool payload_fits(int enc, uint64_t len, int64_t n) {
+    if (n < 0) return false;
+    if (enc == ENC_F32) return len % 4 == 0 && len / 4 == (uint64_t)n;
+    if (enc == ENC_Q8_0) return len >= 4 && len - 4 == (uint64_t)n;
+    return len % Q4KM_BYTES == 0 && len / Q4KM_BYTES * Q4KM_BLOCK >= (uint64_t)n;
 }
 
 int gguf_decode(Gguf& g, const GgufTensor& t, std::vector<float>& out, std::string& err) {
@@ -397,8 +422,11 @@ int st_open(const char* path, File& file, std::vector<StTensor>& out, uint64_t* 
         err = std::string("cannot open ") + path + ": " + strerror(errno);
         return AARH_ERR_IO;
     }
+    fseek(file.f, 0, SEEK_END);
+    const uint64_t fsize0 = (uint64_t)ftell(file.f);
+    fseek(file.f, 0, SEEK_SET);
     uint64_t hlen = 0;
-    if (!rd_u64(file.f, &hlen) || hlen > (1u << 28)) {
+    if (!rd_u64(file.f, &hlen) || hlen > (1u << 28) || hlen > fsize0) {
         err = "invalid safetensors header length";
         return AARH_ERR_CHECKPOINT;
     }
@@ -438,6 +466,12 @@ int st_open(const char* path, File& file, std::vector<StTensor>& out, uint64_t* 
         t.end = (uint64_t)e;
         if (*data_off + t.end > fsize) {
             err = "safetensors data of " + t.name + " past the end of the file";
+            return AARH_ERR_CHECKPOINT;
+        }
+        const int64_t n = numel(t.shape);
+        const int esz = t.dtype == "F32" ? 4 : (t.dtype == "F16" || t.dtype == "BF16") ? 2 : 0;
+        if (n < 0 || (esz && (uint64_t)(t.end - t.begin) != (uint64_t)n * esz)) {
+            err = "safetensors byte range of " + t.name + " does not match its shape";
             return AARH_ERR_CHECKPOINT;
         }
         out.push_back(std::move(t));

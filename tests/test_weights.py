@@ -213,6 +213,20 @@ def test_malformed_gguf_errors(tmp_path, blob, err):
         A.gguf_read_tensor(str(p), "w")
 
 
+def test_corrupt_sizes_fail_before_allocating(tmp_path):
+    # a shape of 2^20 x 2^20 values over an 8-byte payload, and a payload length past the
+    # end of the file, are refused from the header alone
+    p = tmp_path / "big.gguf"
+    p.write_bytes(_gguf_bytes(shape=(1 << 20, 1 << 20)))
+    with pytest.raises(A.CheckpointError):
+        A.gguf_read_tensor(str(p), "w")
+    b = bytearray(_gguf_bytes())
+    struct.pack_into("<Q", b, len(b) - 16, 1 << 60)  # the payload length field
+    p.write_bytes(bytes(b))
+    with pytest.raises(A.IoError):
+        A.gguf_read_tensor(str(p), "w")
+
+
 def test_missing_file_and_tensor(tmp_path):
     with pytest.raises(A.IoError):
         A.gguf_read_tensor(str(tmp_path / "none.gguf"), "w")
