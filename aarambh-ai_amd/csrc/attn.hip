@@ -250,13 +250,15 @@ typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half8_t i8x8_to_half8_perm(uint32_t d0, uint32_t d1) {
     // exact int8 -> fp16 via 0x6400 magic; emits element order [0,2,1,3,4,6,5,7]
+    // v_perm_b32 places bytes (0, 2) or (1, 3) under 0x64 high bytes: fp16 1024 + (b ^ 0x80)
     const half2v_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    constexpr uint32_t HI = 0x64646464u, SEL_EVEN = 0x04020400u, SEL_ODD = 0x04030401u;
     d0 ^= 0x80808080u;
     d1 ^= 0x80808080u;
-    half2v_t h0 = __builtin_bit_cast(half2v_t, (d0 & 0x00FF00FFu) | 0x64006400u) - off;
-    half2v_t h1 = __builtin_bit_cast(half2v_t, ((d0 >> 8) & 0x00FF00FFu) | 0x64006400u) - off;
-    half2v_t h2 = __builtin_bit_cast(half2v_t, (d1 & 0x00FF00FFu) | 0x64006400u) - off;
-    half2v_t h3 = __builtin_bit_cast(half2v_t, ((d1 >> 8) & 0x00FF00FFu) | 0x64006400u) - off;
+    half2v_t h0 = __builtin_bit_cast(half2v_t, __builtin_amdgcn_perm(HI, d0, SEL_EVEN)) - off;
+    half2v_t h1 = __builtin_bit_cast(half2v_t, __builtin_amdgcn_perm(HI, d0, SEL_ODD)) - off;
+    half2v_t h2 = __builtin_bit_cast(half2v_t, __builtin_amdgcn_perm(HI, d1, SEL_EVEN)) - off;
+    half2v_t h3 = __builtin_bit_cast(half2v_t, __builtin_amdgcn_perm(HI, d1, SEL_ODD)) - off;
     half8_t r;
     r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
     r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
@@ -283,7 +285,7 @@ static constexpr int AM_ROWS = 16;          // query rows per workgroup (one MFM
 static constexpr int AM_HD = 128;
 static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
 static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
-static constexpr int AM_MAXCH = 64;         // chunks one merge combines
+static constexpr int AM_MAXCH = 32;         // chunks one merge combines
 static constexpr int AM_STAGE = 2 * 32 * AM_HD + 512;  // one INT8 block staged in LDS: K, V^T, scales
 static constexpr float AM_LOG2E = 1.4426950408889634f;
 
@@ -429,10 +431,41 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const size_t hb = (size_t)sl * a.n_kv + kvh;
     const int t_begin = chunk * a.chunk;
     const int t_end = min(kv_len, t_begin + a.chunk);
-    // The DMA path issues its first two block rows before appending when they end
-    // before the new positions, so the append's round trips overlap those loads.
-    const bool late_append = DMA && t_end > t_begin && t_begin + 2 * 32 * AM_WAVES <= pos0;
-    if (!late_append) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
+    constexpr int STEP = 32 * AM_WAVES;
+    int tb = t_begin + 32 * wid;
+    const int t_chunk_last = (t_end - 1) & ~31;
+    // the wave's own last block (re-reads hit L1), or the chunk's last one for a wave without blocks
+    const int t_last = tb <= t_chunk_last ? tb + (t_chunk_last - tb) / STEP * STEP : t_chunk_last;
+
+    // INT8 blocks stream into two LDS stages per wave with direct loads (no VGPRs held
+    // in flight, waits counted in the token loop): K 4 KiB, V^T 4 KiB, then 256 bytes
+    // each of K and V scales (tokens 2l, 2l+1 in lane l < 16).
+    constexpr int KVB = 32 * AM_HD;  // bytes of K (and of V) per block
+    char* st0 = am_lds + wid * 2 * AM_STAGE;
+    const __amdgpu_buffer_rsrc_t kr = coh_rsrc((const uint8_t*)a.kc + hb * a.cap * AM_HD);
+    const __amdgpu_buffer_rsrc_t vr = coh_rsrc((const uint8_t*)a.vc + hb * a.cap * AM_HD);
+    const __amdgpu_buffer_rsrc_t ksr = coh_rsrc(a.ks + hb * a.cap), vsr = coh_rsrc(a.vs + hb * a.cap);
+    const int sc_voff = (lane & 15) * 4;
+    auto issue = [&](char* st, int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) lds_dma16(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+#pragma unroll
+        for (int p = 0; p < 4; p++) lds_dma16(vr, st + KVB + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+        lds_dma4(ksr, st + 2 * KVB, sc_voff, t * 2);
+        lds_dma4(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
+    };
+    // A wave whose two staged blocks hold no new position issues them first of all, so
+    // their round trip overlaps the query loads and the append; the others issue after
+    // the append (which writes the new positions they read).
+    bool staged = false;
+    if constexpr (DMA) {
+        if (tb < t_end && max(tb, min(tb + STEP, t_last)) + 32 <= pos0) {
+            issue(st0, tb);
+            issue(st0 + AM_STAGE, min(tb + STEP, t_last));
+            staged = true;
+        }
+    }
+    if (t_end > pos0) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
 
     // ---- this lane's query row (lr): Q^T B operand, hi/lo, dims 32*lg + 8*kk + slot ----
     const bool row_ok = lr < R;
@@ -452,11 +485,6 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     // Loads past the wave's last block re-read the chunk's last block (in
     // bounds, results unused), so inside a non-empty chunk every load is
     // unconditional; an empty chunk (past the sequence's length) loads nothing.
-    constexpr int STEP = 32 * AM_WAVES;
-    int tb = t_begin + 32 * wid;
-    const int t_chunk_last = (t_end - 1) & ~31;
-    // the wave's own last block (re-reads hit L1), or the chunk's last one for a wave without blocks
-    const int t_last = tb <= t_chunk_last ? tb + (t_chunk_last - tb) / STEP * STEP : t_chunk_last;
     KvRaw<KVF> ring[DEPTH + 1];
     if (!DMA && t_end > t_begin) {
 #pragma unroll
@@ -497,14 +525,26 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         }
         float s[8];
         float mx = -INFINITY;
+        // a block wholly inside the chunk and before every row's own position needs no mask
+        // (wave-uniform: tb is the wave's block)
+        if (tb + 32 <= t_end && tb + 31 <= pos0) {
 #pragma unroll
-        for (int idx = 0; idx < 8; idx++) {
-            const int tok = tb + 8 * lg + idx;
-            float ksc = sc2;
-            if constexpr (KVF == KV_INT8) ksc *= scale_at(cur.ksc, idx);
-            const float v = st[idx >> 2][idx & 3] * ksc;
-            s[idx] = (tok < t_end && tok <= lim) ? v : -INFINITY;
-            mx = fmaxf(mx, s[idx]);
+            for (int idx = 0; idx < 8; idx++) {
+                float ksc = sc2;
+                if constexpr (KVF == KV_INT8) ksc *= scale_at(cur.ksc, idx);
+                s[idx] = st[idx >> 2][idx & 3] * ksc;
+                mx = fmaxf(mx, s[idx]);
+            }
+        } else {
+#pragma unroll
+            for (int idx = 0; idx < 8; idx++) {
+                const int tok = tb + 8 * lg + idx;
+                float ksc = sc2;
+                if constexpr (KVF == KV_INT8) ksc *= scale_at(cur.ksc, idx);
+                const float v = st[idx >> 2][idx & 3] * ksc;
+                s[idx] = (tok < t_end && tok <= lim) ? v : -INFINITY;
+                mx = fmaxf(mx, s[idx]);
+            }
         }
         mx = rows_max(mx);
         const float mnew = fmaxf(m, mx);
@@ -518,8 +558,11 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         ps = rows_sum(ps);
         l = l * alpha + ps;
         m = mnew;
+        // rescale only when some row's maximum moved (a factor of exactly 1 changes nothing)
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+            for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+        }
         // ---- P^T B operand (hi / lo), slot j <-> token 8*lg + slot_elem(j) ----
         half8_t ph, pl;
 #pragma unroll
@@ -540,32 +583,14 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         }
     };
     if constexpr (DMA) {
-        // INT8 blocks stream into two LDS stages per wave with direct loads (no
-        // VGPRs held in flight, waits counted here): K 4 KiB, V^T 4 KiB, then
-        // 256 bytes each of K and V scales (tokens 2l, 2l+1 in lane l < 16).
         static_assert(KVF == KV_INT8, "DMA staging is laid out for INT8 blocks");
-        constexpr int KVB = 32 * AM_HD;  // bytes of K (and of V) per block
-        char* st0 = am_lds + wid * 2 * AM_STAGE;
-        const __amdgpu_buffer_rsrc_t kr = coh_rsrc((const uint8_t*)a.kc + hb * a.cap * AM_HD);
-        const __amdgpu_buffer_rsrc_t vr = coh_rsrc((const uint8_t*)a.vc + hb * a.cap * AM_HD);
-        const __amdgpu_buffer_rsrc_t ksr = coh_rsrc(a.ks + hb * a.cap), vsr = coh_rsrc(a.vs + hb * a.cap);
-        const int sc_voff = (lane & 15) * 4;
-        auto issue = [&](char* st, int t) __attribute__((always_inline)) {
-#pragma unroll
-            for (int p = 0; p < 4; p++) lds_dma16(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
-#pragma unroll
-            for (int p = 0; p < 4; p++) lds_dma16(vr, st + KVB + p * 1024, lane * 16 + p * 1024, t * AM_HD);
-            lds_dma4(ksr, st + 2 * KVB, sc_voff, t * 2);
-            lds_dma4(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
-        };
         // A block is copied to registers as soon as it lands and its stage is refilled
         // at once, so both stages stay in flight while the block is computed.
         constexpr int NL = 10;  // DMA loads per block
-        if (tb < t_end) {
+        if (tb < t_end && !staged) {
             issue(st0, tb);
             issue(st0 + AM_STAGE, min(tb + STEP, t_last));
         }
-        if (late_append) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
         for (int i = 0; tb < t_end; i++, tb += STEP) {
             char* cur_st = st0 + (i & 1) * AM_STAGE;
             wait_vmcnt<NL>();  // block i has landed; block i + 1 may still be in flight
@@ -642,26 +667,35 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     }
     if (!arrive_last(&a.counters[grp], (unsigned)a.nchunks, &s_last)) return;
 
-    // ---- last workgroup: merge the chunks in chunk order.  Each thread takes its
-    //      row's maximum over the chunks, then the weighted sums of its row's (max, sum)
-    //      header and its 4 dims, chunk by chunk (8 chunks' loads in flight). ----
+    // ---- last workgroup: merge the chunks in chunk order.  Every chunk's (max, sum)
+    //      header of the thread's row and every chunk's 4 dims of the thread are loaded
+    //      at once (one round trip for up to AM_MAXCH chunks); then the row maximum over
+    //      the chunks and the weighted sums, chunk by chunk. ----
     if (r >= R) return;
     const int C = a.nchunks;
     const unsigned rbase = (unsigned)(r * AM_REC) * 4u;
     constexpr unsigned CSTRIDE = (unsigned)(AM_ROWS * AM_REC) * 4u;
+    float2_t hl[AM_MAXCH];
+    float4_t ov[AM_MAXCH];
+#pragma unroll
+    for (int c = 0; c < AM_MAXCH; c++)
+        if (c < C) {
+            hl[c] = ld2_coh(prs, rbase + (unsigned)c * CSTRIDE);
+            ov[c] = ld4_coh(prs, rbase + (unsigned)c * CSTRIDE + 16u + 16u * q);
+        }
     float Mc = -INFINITY;
-#pragma unroll 8
-    for (int c = 0; c < C; c++) Mc = fmaxf(Mc, ld4_coh(prs, rbase + (unsigned)c * CSTRIDE)[0]);
+#pragma unroll
+    for (int c = 0; c < AM_MAXCH; c++)
+        if (c < C) Mc = fmaxf(Mc, hl[c][0]);
     float4_t tot = {0.f, 0.f, 0.f, 0.f};
     float Lc = 0.f;
-#pragma unroll 8
-    for (int c = 0; c < C; c++) {
-        const float4_t hdr = ld4_coh(prs, rbase + (unsigned)c * CSTRIDE);
-        const float4_t ov = ld4_coh(prs, rbase + (unsigned)c * CSTRIDE + 16u + 16u * q);
-        const float w = hdr[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(hdr[0] - Mc);
-        Lc += hdr[1] * w;
-        tot += ov * w;
-    }
+#pragma unroll
+    for (int c = 0; c < AM_MAXCH; c++)
+        if (c < C) {
+            const float w = hl[c][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(hl[c][0] - Mc);
+            Lc += hl[c][1] * w;
+            tot += ov[c] * w;
+        }
     const float4_t o4 = tot * (Lc > 0.f ? 1.0f / Lc : 0.f);
     *(float4_t*)out = o4;
     if (a.fo.buf) frag_out_pair(a.fo, orow, ocol, o4, q);

@@ -6,6 +6,7 @@
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 #define WAVE 64
 
@@ -135,6 +136,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
 }
 __device__ __forceinline__ float4_t ld4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
     return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
+}
+__device__ __forceinline__ float2_t ld2_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+    return __builtin_bit_cast(float2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, 16));
 }
 __device__ __forceinline__ void st4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4_t v) {
     typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));

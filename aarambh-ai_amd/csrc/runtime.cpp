@@ -392,7 +392,7 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
     at.ntiles = (Rt + at.rows_per_tile - 1) / at.rows_per_tile;
     const int base = nseq * c->cfg.n_kv_heads * at.ntiles;
     const int max_chunks = std::max(1, (max_kv_len + gran - 1) / gran);
-    int nch = std::max(1, std::min(std::min(max_chunks, 64), (target + base - 1) / base));
+    int nch = std::max(1, std::min(std::min(max_chunks, mf ? 32 : 64), (target + base - 1) / base));
     int chunk = ((max_kv_len + nch - 1) / nch + gran - 1) / gran * gran;
     nch = (max_kv_len + chunk - 1) / chunk;
     at.chunk = chunk;
