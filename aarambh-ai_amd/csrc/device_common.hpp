@@ -337,6 +337,19 @@ __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, in
         }
         if (special || lsum > 16777217) lsum = 16777217;  // past the binade anyway; keeps the scan in range
         const int incl = wave_incl_scan_dpp(lsum);
+        // Fast path: no element is special and the window ends inside the binade, and no
+        // partial sum of the window reaches u (sums only grow, so each lane's end value
+        // decides): the window advances without walking its elements.
+        {
+            const int lane_end = ns + incl;
+            const bool lane_bad = special || lane_end >= 16777216;
+            const bool lane_cross = want && cross < 0 && u <= ldexpf((float)lane_end, -sh);
+            if (__ballot(lane_bad || lane_cross) == 0ull) {
+                s = ldexpf((float)(ns + __builtin_amdgcn_readlane(incl, 63)), -sh);
+                pos = w0 + 64 * E;
+                continue;
+            }
+        }
         int run = ns + incl - lsum;
         int first_bad = E, first_cross = E, run_bad = 0;
         float cs_at = 0.0f, cs_before = 0.0f;
