@@ -11,6 +11,9 @@
 namespace aarh {
 
 static constexpr int MT_THREADS = 256;
+static constexpr int RW_THREADS = 512;    // row kernels over a hidden-width row (one pass of ROW_U loads at 4096)
+static constexpr int WIDE_THREADS = 1024; // row kernels over a vocabulary-width row
+static constexpr int WIDE_U = 32;         // their loads in flight per thread (32768 floats per pass)
 
 static thread_local char g_last_err[256] = "";
 thread_local LaunchTiming g_launch_timing = {nullptr, nullptr, 0};
@@ -133,7 +136,7 @@ int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, i
                  hipStream_t stream) {
     if (H > ROW_LDS_MAX) return 2;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream, table,
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(RW_THREADS), (unsigned)(H * sizeof(float)), stream, table,
                        table_fmt, H, ids, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
@@ -143,48 +146,40 @@ int launch_embed(const void* table, int table_fmt, int H, const uint32_t* ids, i
 __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, const void* table, int fmt,
                                 const uint32_t* ids, int ids_stride, int L, int H, const float* trunk_w,
                                 const float* token_w, float eps, float* x, XFrag fo) {
-    extern __shared__ float rowbuf[];
-    __shared__ float red[MT_THREADS / 64];
+    extern __shared__ float rowbuf[];  // [H] row, then [H] norm weight
+    __shared__ float red[16];
     const int row = blockIdx.x;
     const int seq = row / L, l = row % L;
     float* out = x + (size_t)row * H;
     const float* w = l == 0 ? trunk_w : token_w;
     float ss = 0.f;
     const size_t tbase = l == 0 ? 0 : (size_t)ids[(size_t)seq * ids_stride + l - 1] * H;
+    float* wbuf = rowbuf + H;
+    // the row and the norm weight in one round trip
     for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
-        float v[ROW_U];
+        float v[ROW_U], wv[ROW_U];
 #pragma unroll
         for (int u = 0; u < ROW_U; u++) {
             const int k = k0 + u * blockDim.x;
             v[u] = k >= H ? 0.f : l == 0 ? anchor[(size_t)seq * anchor_stride + k] : load_table(table, fmt, tbase + k);
-        }
-#pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
-            const int k = k0 + u * blockDim.x;
-            if (k < H) {
-                rowbuf[k] = v[u];
-                ss += v[u] * v[u];
-            }
-        }
-    }
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
-        float wv[ROW_U];
-#pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
-            const int k = k0 + u * blockDim.x;
             wv[u] = k < H ? w[k] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < ROW_U; u++) {
             const int k = k0 + u * blockDim.x;
             if (k < H) {
-                const float o = rowbuf[k] * inv * wv[u];
-                out[k] = o;
-                rowbuf[k] = o;
+                rowbuf[k] = v[u];
+                wbuf[k] = wv[u];
+                ss += v[u] * v[u];
             }
         }
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) {
+        const float o = rowbuf[k] * inv * wbuf[k];
+        out[k] = o;
+        rowbuf[k] = o;
     }
     lds_barrier();
     emit_row_fragments(fo, rowbuf, row, H);
@@ -193,9 +188,9 @@ __global__ void mtp_prep_kernel(const float* anchor, long long anchor_stride, co
 int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* table, int table_fmt,
                     const uint32_t* ids, int ids_stride, int nseq, int L, int H, const float* trunk_w,
                     const float* token_w, float eps, float* x, const XFrag& fo, hipStream_t stream) {
-    if (H > ROW_LDS_MAX) return 2;
+    if (2 * H > ROW_LDS_MAX) return 2;  // row + norm weight in LDS
     (void)hipGetLastError();
-    hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream,
+    hipLaunchKernelGGL(mtp_prep_kernel, dim3(nseq * L), dim3(RW_THREADS), (unsigned)(2 * H * sizeof(float)), stream,
                        anchor, anchor_stride,
                        table, table_fmt, ids, ids_stride, L, H, trunk_w, token_w, eps, x, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
@@ -203,45 +198,37 @@ int launch_mtp_prep(const float* anchor, long long anchor_stride, const void* ta
 
 // RMSNorm of selected rows (nn/src/norm.rs:17-19), plus fragments of the result.
 __global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float* w, float eps, float* out, XFrag fo) {
-    extern __shared__ float rowbuf[];
-    __shared__ float red[MT_THREADS / 64];
+    extern __shared__ float rowbuf[];  // [H] row, then [H] norm weight
+    __shared__ float red[16];
     const int m = blockIdx.x;
     const float* r = x + row_off(xmap, m);
+    float* wbuf = rowbuf + H;
     float ss = 0.f;
+    // the row and the norm weight in one round trip
     for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
-        float v[ROW_U];
+        float v[ROW_U], wv[ROW_U];
 #pragma unroll
         for (int u = 0; u < ROW_U; u++) {
             const int k = k0 + u * blockDim.x;
             v[u] = k < H ? r[k] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
-            const int k = k0 + u * blockDim.x;
-            if (k < H) {
-                rowbuf[k] = v[u];
-                ss += v[u] * v[u];
-            }
-        }
-    }
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k0 = threadIdx.x; k0 < H; k0 += ROW_U * blockDim.x) {
-        float wv[ROW_U];
-#pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
-            const int k = k0 + u * blockDim.x;
             wv[u] = k < H ? w[k] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < ROW_U; u++) {
             const int k = k0 + u * blockDim.x;
             if (k < H) {
-                const float o = rowbuf[k] * inv * wv[u];
-                out[(size_t)m * H + k] = o;
-                rowbuf[k] = o;
+                rowbuf[k] = v[u];
+                wbuf[k] = wv[u];
+                ss += v[u] * v[u];
             }
         }
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) {
+        const float o = rowbuf[k] * inv * wbuf[k];
+        out[(size_t)m * H + k] = o;
+        rowbuf[k] = o;
     }
     lds_barrier();
     emit_row_fragments(fo, rowbuf, m, H);
@@ -249,9 +236,9 @@ __global__ void norm_rows_kernel(const float* x, RowMap xmap, int H, const float
 
 int launch_norm_rows(const float* x, RowMap xmap, int M, int H, const float* w, float eps, float* out,
                      const XFrag& fo, hipStream_t stream) {
-    if (H > ROW_LDS_MAX) return 2;
+    if (2 * H > ROW_LDS_MAX) return 2;  // row + norm weight in LDS
     (void)hipGetLastError();
-    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(MT_THREADS), (unsigned)(H * sizeof(float)), stream, x, xmap,
+    hipLaunchKernelGGL(norm_rows_kernel, dim3(M), dim3(RW_THREADS), (unsigned)(2 * H * sizeof(float)), stream, x, xmap,
                        H, w, eps, out, fo);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
@@ -513,21 +500,21 @@ int launch_kv_fill_synthetic(void* kc, void* vc, uint16_t* ks, uint16_t* vs, int
 // argmax under f32::total_cmp keeping the last maximal index (sampler.rs:217-224),
 // plus the top-2 value gap (greedy near-tie measure).
 __global__ void argmax_rows_kernel(const float* x, long long ld, int V, int32_t* out, int out_stride, float* gap) {
-    __shared__ int rk[MT_THREADS / 64], ri[MT_THREADS / 64];
-    __shared__ float r1[MT_THREADS / 64], r2[MT_THREADS / 64];
+    __shared__ int rk[16], ri[16];
+    __shared__ float r1[16], r2[16];
     const float* row = x + (size_t)blockIdx.x * ld;
     int bk = INT_MIN, bi = 0;
     float t1 = -INFINITY, t2 = -INFINITY;
-    // ROW_U loads in flight per thread, then consumed in index order
-    for (int j0 = threadIdx.x; j0 < V; j0 += ROW_U * blockDim.x) {
-        float vv[ROW_U];
+    // WIDE_U loads in flight per thread, then consumed in index order
+    for (int j0 = threadIdx.x; j0 < V; j0 += WIDE_U * blockDim.x) {
+        float vv[WIDE_U];
 #pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
+        for (int u = 0; u < WIDE_U; u++) {
             const int j = j0 + u * blockDim.x;
             vv[u] = j < V ? row[j] : 0.f;
         }
 #pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
+        for (int u = 0; u < WIDE_U; u++) {
             const int j = j0 + u * blockDim.x;
             if (j < V) {
                 const float v = vv[u];
@@ -565,7 +552,7 @@ __global__ void argmax_rows_kernel(const float* x, long long ld, int V, int32_t*
 int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* out, int out_stride, float* gap,
                        hipStream_t stream) {
     (void)hipGetLastError();
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(MT_THREADS), 0, stream, x, ld, V, out, out_stride, gap);
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(WIDE_THREADS), 0, stream, x, ld, V, out, out_stride, gap);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
@@ -573,15 +560,15 @@ int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* o
 __global__ void copy_rows_kernel(const float* const* src, float* const* dst, int n) {
     const float* s = src[blockIdx.x];
     float* d = dst[blockIdx.x];
-    for (int k0 = threadIdx.x; k0 < n; k0 += ROW_U * blockDim.x) {
-        float v[ROW_U];
+    for (int k0 = threadIdx.x; k0 < n; k0 += WIDE_U * blockDim.x) {
+        float v[WIDE_U];
 #pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
+        for (int u = 0; u < WIDE_U; u++) {
             const int k = k0 + u * blockDim.x;
             v[u] = k < n ? s[k] : 0.f;
         }
 #pragma unroll
-        for (int u = 0; u < ROW_U; u++) {
+        for (int u = 0; u < WIDE_U; u++) {
             const int k = k0 + u * blockDim.x;
             if (k < n) d[k] = v[u];
         }
@@ -591,7 +578,7 @@ __global__ void copy_rows_kernel(const float* const* src, float* const* dst, int
 int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream) {
     if (rows <= 0) return 0;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(copy_rows_kernel, dim3(rows), dim3(MT_THREADS), 0, stream, src, dst, n);
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(rows), dim3(WIDE_THREADS), 0, stream, src, dst, n);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
