@@ -755,6 +755,14 @@ __global__ void __launch_bounds__(ACC_THREADS) candidates_kernel(CandArgs a) {
     int status = 0;
     if (a.greedy) {
         am = block_argmax(row, V, &sh);  // one-hot at the argmax (sampler.rs:211-215)
+        // The stable descending order of a one-hot vector is the argmax (1.0), then the
+        // zeros in ascending index order: the n - 1 smallest indices other than am.
+        if (tid < n) {
+            const int id = tid == 0 ? am : (tid - 1 < am ? tid - 1 : tid);
+            a.ids[(size_t)blockIdx.x * n + tid] = id < V ? (uint32_t)id : 0xFFFFFFFFu;
+            a.probs[(size_t)blockIdx.x * n + tid] = tid == 0 ? 1.0f : 0.0f;
+        }
+        return;
     } else {
         uint32_t fl;
         row_filter(row, V, a.temperature, a.top_k, a.top_p, lds, a.chunk, &sh, f, fl, status);
