@@ -139,7 +139,7 @@ __device__ void run_epilogue(const GemvArgs& a, float (*yt)[17], int nt, int Mc,
             const float g = yt[m][r], u = yt[m][8 + r];
             const float silu = g / (1.0f + expf(-g));
             const float h = silu * u;
-            a.out[row_off(a.omap, mbase + m) + nt * 8 + r] = h;
+            if (a.out) a.out[row_off(a.omap, mbase + m) + nt * 8 + r] = h;
             if (a.fo.buf) frag_put(a.fo, mbase + m, nt * 8 + r, h);
         }
     } else {

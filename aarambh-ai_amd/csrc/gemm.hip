@@ -275,6 +275,28 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     constexpr int LA = NS >= 3 ? NS - 2 : 1;
 #pragma unroll
     for (int i = 0; i < LA; i++) issue_stage(i, g0 + min(i, ng - 1));
+    // the epilogue's 1/rms while the first stages are in flight (loads complete in
+    // order, so its wait also covers those stages: the loop's first wait is then free)
+    const bool norm_rows = a.norm_w && !(EPI == EPI_STORE && a.hidden_out);
+    if (norm_rows) compute_inv();
+    // rows and tiles of this wave's epilogue; QKV positions loaded up front
+    const int row0 = (mb * MC + wm * CPW) * 16, tile0 = nb * NT + wn * TPW;
+    int mrw[CPW][4];  // activation row, clamped into range
+    bool rok[CPW][4];
+#pragma unroll
+    for (int c = 0; c < CPW; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int chunk = mb * MC + wm * CPW + c, m = chunk * 16 + 4 * lg + i;
+            rok[c][i] = chunk < nchunks && m < a.M;
+            mrw[c][i] = min(m, a.M - 1);
+        }
+    int pos[CPW][4];
+    if (EPI == EPI_QKV)
+#pragma unroll
+        for (int c = 0; c < CPW; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pos[c][i] = a.qkv.pos0[mrw[c][i] / a.qkv.S] + mrw[c][i] % a.qkv.S;
     for (int gi = 0; gi < ng; gi++) {
         issue_stage((gi + LA) % NS, g0 + min(gi + LA, ng - 1));  // past the end: harmless repeats
         wait_vmcnt<C::L * LA>();
@@ -284,6 +306,71 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     }
     wait_vmcnt<0>();
     __syncthreads();  // every wave's stage loads have landed: the ring is free for the epilogue
+
+    // ---- epilogue inputs that do not depend on this kernel's products: loaded in the
+    //      same round trip as the split-K partials (after the arrival, which waits for
+    //      every outstanding access), or right away without a split ----
+    int ntv[TPW];
+    bool tok[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int nt = tile0 + j;
+        tok[j] = nt < ntiles;
+        ntv[j] = min(nt, ntiles - 1);
+    }
+    // RESID: unit u = (row r, 8-column half s8 of a tile) of the wave's region; the old
+    // residual and the next consumer's norm weights of every unit of the lane
+    constexpr int TR = 16 * CPW, TLD = 16 * TPW + 4;
+    constexpr int RU = TR * 2 * TPW, RI = (RU + 63) / 64;
+    float rs[TPW];
+    float xres[EPI == EPI_RESID ? RI : 1][8], nres[EPI == EPI_RESID ? RI : 1][8];
+    float qcs[EPI == EPI_QKV ? TPW : 1][CPW][4], qsn[EPI == EPI_QKV ? TPW : 1][CPW][4];
+    auto load_epi_inputs = [&]() {
+        if (FMT == WF_INT8)
+#pragma unroll
+            for (int j = 0; j < TPW; j++) rs[j] = a.rscale[ntv[j] * 16 + lr];
+        if (EPI == EPI_RESID) {
+#pragma unroll
+            for (int it = 0; it < RI; it++) {
+                const int u = lane + 64 * it;
+                const int r = u / (2 * TPW), s8 = u % (2 * TPW), m = row0 + r, nt = tile0 + (s8 >> 1);
+                const int col = nt * 16 + (s8 & 1) * 8;
+                const bool ok = u < RU && m < a.M && nt < ntiles;
+                const float* xr = a.resid + (size_t)min(m, a.M - 1) * a.ldr + min(col, a.N - 8);
+                if (ok && ((uintptr_t)xr & 15) == 0) {
+                    const float4_t x0 = *(const float4_t*)xr, x1 = *(const float4_t*)(xr + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        xres[it][e] = x0[e];
+                        xres[it][4 + e] = x1[e];
+                    }
+                } else if (ok) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) xres[it][e] = xr[e];
+                }
+                if (ok && a.fo.buf && a.fo.norm_w)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) nres[it][e] = a.fo.norm_w[col + e];
+            }
+        }
+        // QKV: RoPE cos / sin of every (tile, row) of the lane
+        if (EPI == EPI_QKV) {
+            const int half = a.qkv.hd >> 1;
+#pragma unroll
+            for (int j = 0; j < TPW; j++) {
+                const int rowq = ntv[j] * 16;
+                const int d1 = 8 * ((rowq % a.qkv.hd) >> 4) + (lr & 7);
+#pragma unroll
+                for (int c = 0; c < CPW; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        qcs[j][c][i] = a.qkv.rope_cos[(size_t)pos[c][i] * half + d1];
+                        qsn[j][c][i] = a.qkv.rope_sin[(size_t)pos[c][i] * half + d1];
+                    }
+            }
+        }
+    };
+    if (S == 1) load_epi_inputs();
 
     if (S > 1) {
         // ---- split-K: partial tiles out, the last block of the (mb, nb) pair adds them in order ----
@@ -297,6 +384,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                 st4_coh(pr, o, acc[c][j]);
             }
         if (!arrive_last(a.gcnt + unit, (unsigned)S, &s_flag)) return;
+        load_epi_inputs();
         // the wave's CPW * TPW tiles x 4 splits in flight per round trip, added in split order
         const unsigned step = (unsigned)(MC * NT) * 1024u;
 #pragma unroll
@@ -324,37 +412,8 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     }
 
     // ---- epilogue in the MFMA layout: lane (lr, lg) of tile (c, j) holds rows
-    //      4 lg + i of chunk c for weight row lr of tile j.  Every global input of
-    //      the epilogue is loaded for all of the wave's tiles before one is used.
-    int mrw[CPW][4];  // activation row, clamped into range
-    bool rok[CPW][4];
-#pragma unroll
-    for (int c = 0; c < CPW; c++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int chunk = mb * MC + wm * CPW + c, m = chunk * 16 + 4 * lg + i;
-            rok[c][i] = chunk < nchunks && m < a.M;
-            mrw[c][i] = min(m, a.M - 1);
-        }
-    int ntv[TPW];
-    bool tok[TPW];
-#pragma unroll
-    for (int j = 0; j < TPW; j++) {
-        const int nt = nb * NT + wn * TPW + j;
-        tok[j] = nt < ntiles;
-        ntv[j] = min(nt, ntiles - 1);
-    }
-    float rs[TPW];
-    if (FMT == WF_INT8)
-#pragma unroll
-        for (int j = 0; j < TPW; j++) rs[j] = a.rscale[ntv[j] * 16 + lr];
-    int pos[CPW][4];
-    if (EPI == EPI_QKV)
-#pragma unroll
-        for (int c = 0; c < CPW; c++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) pos[c][i] = a.qkv.pos0[mrw[c][i] / a.qkv.S] + mrw[c][i] % a.qkv.S;
-    if (a.norm_w && !(EPI == EPI_STORE && a.hidden_out)) compute_inv();
+    //      4 lg + i of chunk c for weight row lr of tile j.  Its global inputs were
+    //      loaded for all of the wave's tiles before the split-K exchange.
 #pragma unroll
     for (int c = 0; c < CPW; c++)
 #pragma unroll
@@ -370,35 +429,25 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     // ---- the wave's tile goes through LDS (the stage ring is idle now) so that
     //      every global access is a 16-byte run of 4 (f32) or 8 (fragment)
     //      consecutive columns of one row ----
-    constexpr int TR = 16 * CPW, TLD = 16 * TPW + 4;
     float* wt = (float*)lds + wid * TR * TLD;
     if (EPI == EPI_QKV) {
         // a tile holds dims d = 8 jh + r (weight rows r < 8) and d + hd/2 (rows 8 + r) of one
         // head; RoPE (rope.rs:107-126) pairs lane lr with lane lr ^ 8, each keeps its own output
         const QkvEpi& e = a.qkv;
-        const int hd = e.hd, half = hd >> 1;
-        const int QD = e.n_heads * hd, KD = e.n_kv * hd;
+        const int QD = e.n_heads * e.hd, KD = e.n_kv * e.hd;
 #pragma unroll
         for (int j = 0; j < TPW; j++) {
-            const int rowq = ntv[j] * 16;
-            const bool rot = rowq < QD + KD;
-            const int d1 = 8 * ((rowq % hd) >> 4) + (lr & 7);
+            const bool rot = ntv[j] * 16 < QD + KD;
 #pragma unroll
             for (int c = 0; c < CPW; c++) {
-                float cs[4], sn[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    cs[i] = e.rope_cos[(size_t)pos[c][i] * half + d1];
-                    sn[i] = e.rope_sin[(size_t)pos[c][i] * half + d1];
-                }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float mine = acc[c][j][i], other = __shfl_xor(mine, 8, 64);
                     float y1 = lr < 8 ? mine : other, y2 = lr < 8 ? other : mine;
                     if (rot) {
 #pragma clang fp contract(off)
-                        const float r1 = y1 * cs[i] - y2 * sn[i];
-                        const float r2 = y1 * sn[i] + y2 * cs[i];
+                        const float r1 = y1 * qcs[j][c][i] - y2 * qsn[j][c][i];
+                        const float r2 = y1 * qsn[j][c][i] + y2 * qcs[j][c][i];
                         y1 = r1;
                         y2 = r2;
                     }
@@ -418,7 +467,6 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     {
-        const int row0 = (mb * MC + wm * CPW) * 16, tile0 = nb * NT + wn * TPW;
         if (EPI == EPI_SWIGLU) {
             // unit (row, tile): gate rows 0-7 and up rows 8-15 of the tile give h columns nt*8 .. +7
             for (int u = lane; u < TR * TPW; u += 64) {
@@ -432,13 +480,15 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                     h[e] = g0[e] / (1.0f + expf(-g0[e])) * u0[e];
                     h[4 + e] = g1[e] / (1.0f + expf(-g1[e])) * u1[e];
                 }
-                float* dst = a.out + row_off(a.omap, m) + nt * 8;
-                if (((uintptr_t)dst & 15) == 0) {
-                    *(float4_t*)dst = (float4_t){h[0], h[1], h[2], h[3]};
-                    *(float4_t*)(dst + 4) = (float4_t){h[4], h[5], h[6], h[7]};
-                } else {
+                if (a.out) {  // f32 rows only for a consumer that reads them (f32 weights)
+                    float* dst = a.out + row_off(a.omap, m) + nt * 8;
+                    if (((uintptr_t)dst & 15) == 0) {
+                        *(float4_t*)dst = (float4_t){h[0], h[1], h[2], h[3]};
+                        *(float4_t*)(dst + 4) = (float4_t){h[4], h[5], h[6], h[7]};
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 8; e++) dst[e] = h[e];
+                        for (int e = 0; e < 8; e++) dst[e] = h[e];
+                    }
                 }
                 if (a.fo.buf) {
                     if (a.fo.norm_w)
@@ -449,7 +499,10 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
             }
         } else if (EPI == EPI_STORE || EPI == EPI_RESID) {
             // unit (row, 8-column half of a tile); lanes 2q and 2q+1 hold the two halves of one tile row
-            for (int u = lane; u < TR * 2 * TPW; u += 64) {  // a multiple of 64 units, or 32
+#pragma unroll
+            for (int it = 0; it < RI; it++) {  // RU is a multiple of 64 units, or 32
+                const int u = lane + 64 * it;
+                if (u >= RU) break;
                 const int r = u / (2 * TPW), s8 = u % (2 * TPW), m = row0 + r, nt = tile0 + (s8 >> 1);
                 const int col = nt * 16 + (s8 & 1) * 8;
                 const bool ok = m < a.M && nt < ntiles;
@@ -467,29 +520,17 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                         }
                     }
                 } else {
-                    // x += y; the new x as fragments for the next consumer and its 16-column sums of squares
+                    // x += y (old x loaded before the split-K exchange); the new x as fragments
+                    // for the next consumer and its 16-column sums of squares
                     float sq = 0.f;
                     if (ok) {
                         float* xr = a.resid + (size_t)m * a.ldr + col;
-                        const bool al = ((uintptr_t)xr & 15) == 0;
-                        float x[8];
-                        if (al) {
-                            const float4_t x0 = *(const float4_t*)xr, x1 = *(const float4_t*)(xr + 4);
-#pragma unroll
-                            for (int e = 0; e < 4; e++) {
-                                x[e] = x0[e];
-                                x[4 + e] = x1[e];
-                            }
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 8; e++) x[e] = xr[e];
-                        }
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
-                            v[e] += x[e];
+                            v[e] += xres[it][e];
                             sq += v[e] * v[e];
                         }
-                        if (al) {
+                        if (((uintptr_t)xr & 15) == 0) {
                             *(float4_t*)xr = (float4_t){v[0], v[1], v[2], v[3]};
                             *(float4_t*)(xr + 4) = (float4_t){v[4], v[5], v[6], v[7]};
                         } else {
@@ -499,7 +540,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
                         if (a.fo.buf) {
                             if (a.fo.norm_w)
 #pragma unroll
-                                for (int e = 0; e < 8; e++) v[e] *= a.fo.norm_w[col + e];
+                                for (int e = 0; e < 8; e++) v[e] *= nres[it][e];
                             frag_put8_w(a.fo, m, col, v);
                         }
                     }

@@ -414,7 +414,10 @@ int run_block(aarh_ctx* c, const BlockW& w, int nseq, int S, const int32_t* d_po
                   rm(1, 0, 0), c->x, H, xfrag(c, c->frag_a, w.gu.fmt, H, mp, w.norm2, true), nullptr,
                   AARH_PROF_GEMV_WO)))
         return r;
-    if ((r = gemv(c, w.gu, M, c->x, rm(M, 0, H), c->frag_a, mp, w.norm2, nullptr, EPI_SWIGLU, c->h, rm(M, 0, c->Fp),
+    // h as f32 rows only when the down projection reads rows (f32 weights); quantised
+    // weights read the fragments written beside it
+    if ((r = gemv(c, w.gu, M, c->x, rm(M, 0, H), c->frag_a, mp, w.norm2, nullptr, EPI_SWIGLU,
+                  w.down.fmt == WF_F32 ? c->h : nullptr, rm(M, 0, c->Fp),
                   nullptr, 0, xfrag(c, c->frag_b, w.down.fmt, c->Fp, mp, nullptr, false), nullptr,
                   AARH_PROF_GEMV_GATEUP)))
         return r;
