@@ -263,6 +263,8 @@ int launch_kv_fill_synthetic(void* kc, void* vc, uint16_t* ks, uint16_t* vs, int
 int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* out, int out_stride, float* gap,
                        hipStream_t stream);
 int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream);
+int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit, uint32_t eos,
+                           uint32_t* ids, int32_t* nprop, hipStream_t stream);
 int launch_fill_f32(float* p, long long n, float v, hipStream_t stream);
 
 // ---------------------------------------------------------------------------

@@ -582,6 +582,37 @@ int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
+// Verify rows of a greedy MTP round (mtp_speculative.rs:211-221): row r of sequence b
+// carries proposal min(r, K - 1) (rows past the proposals repeat the last one), and
+// nprop[b] counts the proposals up to and including the first end-of-sequence id, at
+// most limit[b] (0 for a finished sequence) -- the proposal loop of
+// mtp_speculative.rs:169-209 that stops after an EOS proposal (:201-203).
+__global__ void mtp_verify_rows_kernel(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit,
+                                       uint32_t eos, uint32_t* ids, int32_t* nprop) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nseq * Kr) return;
+    const int b = i / Kr, r = i - b * Kr;
+    ids[i] = props[(size_t)b * K + min(r, K - 1)];
+    if (r == 0) {
+        const int lim = min(limit[b], K);
+        int np = 0;
+        for (int p = 0; p < lim; p++) {
+            np++;
+            if (props[(size_t)b * K + p] == eos) break;
+        }
+        nprop[b] = np;
+    }
+}
+
+int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit, uint32_t eos,
+                           uint32_t* ids, int32_t* nprop, hipStream_t stream) {
+    if (nseq <= 0 || Kr <= 0 || K <= 0) return 2;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(mtp_verify_rows_kernel, dim3((nseq * Kr + 255) / 256), dim3(256), 0, stream, props, K, Kr,
+                       nseq, limit, eos, ids, nprop);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
 __global__ void fill_f32_kernel(float* p, long long n, float v) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;

@@ -114,6 +114,15 @@ struct aarh_ctx {
     uint32_t* d_ids = nullptr;
     int32_t *h_pos0 = nullptr, *h_slot = nullptr;
     uint32_t* h_ids = nullptr;
+    // pinned staging slots for the small per-call host -> device arrays (row ids,
+    // positions, pointer lists): a slot is written again once the event recorded
+    // after its copies has completed, so staging needs no stream synchronisation
+    static constexpr int STAGE_SLOTS = 8;
+    static constexpr size_t STAGE_BYTES = (size_t)64 << 10;
+    char* h_stage = nullptr;
+    hipEvent_t stage_ev[STAGE_SLOTS] = {};
+    bool stage_busy[STAGE_SLOTS] = {};
+    int stage_next = 0;
     // acceptance scratch: row distribution parameters and per-sequence arrival counters
     uint32_t* acc_rstat = nullptr;
     unsigned* acc_cnt = nullptr;
@@ -559,6 +568,27 @@ int sync_stream(aarh_ctx* c) {
     return 0;
 }
 
+// The next pinned staging slot (STAGE_BYTES), once the copies that last read it
+// have run; nullptr when the context has no staging slots or the wait fails.
+char* stage_acquire(aarh_ctx* c, int* slot) {
+    if (!c->h_stage) return nullptr;
+    const int i = c->stage_next;
+    c->stage_next = (i + 1) % aarh_ctx::STAGE_SLOTS;
+    if (c->stage_busy[i]) {
+        if (hipEventSynchronize(c->stage_ev[i]) != hipSuccess) return nullptr;
+        c->stage_busy[i] = false;
+    }
+    *slot = i;
+    return c->h_stage + (size_t)i * aarh_ctx::STAGE_BYTES;
+}
+
+// Marks a slot in use until the copies enqueued from it so far have run.
+int stage_release(aarh_ctx* c, int slot) {
+    HIPCHK(c, hipEventRecord(c->stage_ev[slot], c->stream));
+    c->stage_busy[slot] = true;
+    return 0;
+}
+
 }  // namespace
 
 namespace aarh {
@@ -626,6 +656,9 @@ void aarh_destroy(aarh_ctx* c) {
     if (c->h_pos0) (void)hipHostFree(c->h_pos0);
     if (c->h_slot) (void)hipHostFree(c->h_slot);
     if (c->h_ids) (void)hipHostFree(c->h_ids);
+    if (c->h_stage) (void)hipHostFree(c->h_stage);
+    for (auto ev : c->stage_ev)
+        if (ev) (void)hipEventDestroy(ev);
     for (auto& r : c->prof_recs) {
         (void)hipEventDestroy(r.a);
         (void)hipEventDestroy(r.b);
@@ -856,6 +889,8 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         HIPCHK(c, hipHostMalloc((void**)&c->h_pos0, M * 4, 0));
         HIPCHK(c, hipHostMalloc((void**)&c->h_slot, M * 4, 0));
         HIPCHK(c, hipHostMalloc((void**)&c->h_ids, (size_t)M * 4, 0));
+        HIPCHK(c, hipHostMalloc((void**)&c->h_stage, aarh_ctx::STAGE_SLOTS * aarh_ctx::STAGE_BYTES, 0));
+        for (auto& ev : c->stage_ev) HIPCHK(c, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     }
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return AARH_OK;
@@ -1085,6 +1120,22 @@ static int stage_rows(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, co
     }
     for (int i = 0; i < nseq * S; i++)
         if ((int64_t)ids[i] >= c->V) return fail(c, AARH_ERR_SHAPE, "token id %u exceeds vocabulary", ids[i]);
+    *max_kv = mk;
+    if (((size_t)nseq * S + 2 * (size_t)nseq) * 4 <= aarh_ctx::STAGE_BYTES) {
+        int sl = 0;
+        char* p = stage_acquire(c, &sl);
+        if (!p) return fail(c, AARH_ERR_DEVICE, "staging slot wait failed");
+        int32_t* hp = (int32_t*)p;
+        int32_t* hs = hp + nseq;
+        uint32_t* hi = (uint32_t*)(hs + nseq);
+        memcpy(hp, offsets, nseq * 4);
+        memcpy(hs, slots, nseq * 4);
+        memcpy(hi, ids, (size_t)nseq * S * 4);
+        HIPCHK(c, hipMemcpyAsync(c->d_pos0, hp, nseq * 4, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(c->d_slot, hs, nseq * 4, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(c->d_ids, hi, (size_t)nseq * S * 4, hipMemcpyHostToDevice, c->stream));
+        return stage_release(c, sl);
+    }
     HIPCHK(c, hipStreamSynchronize(c->stream));
     memcpy(c->h_pos0, offsets, nseq * 4);
     memcpy(c->h_slot, slots, nseq * 4);
@@ -1094,6 +1145,53 @@ static int stage_rows(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, co
     HIPCHK(c, hipMemcpyAsync(c->d_ids, c->h_ids, (size_t)nseq * S * 4, hipMemcpyHostToDevice, c->stream));
     *max_kv = mk;
     return 0;
+}
+
+// stage_rows for rows whose ids a device kernel writes into d_ids: validates the slots
+// and offsets and stages positions, slots and nseq extra words (`meta`, to `d_meta`).
+static int stage_rows_meta(aarh_ctx* c, const int32_t* slots, const int32_t* offsets, int nseq, int S, int* max_kv,
+                           int pad, const int32_t* meta, int32_t* d_meta) {
+    if (nseq <= 0 || S <= 0) return fail(c, AARH_ERR_SHAPE, "batch and sequence length must be non-zero");
+    if (nseq * S > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq*S=%d exceeds max_rows %d", nseq * S, c->Mmax);
+    int mk = 0;
+    for (int b = 0; b < nseq; b++) {
+        int sl = slots[b], off = offsets[b];
+        if (sl < 0 || sl >= c->cfg.max_batch) return fail(c, AARH_ERR_SHAPE, "bad slot %d", sl);
+        for (int b2 = 0; b2 < b; b2++)
+            if (slots[b2] == sl) return fail(c, AARH_ERR_SHAPE, "slot %d used twice", sl);
+        if (off < 0 || off > c->kv_len[sl])
+            return fail(c, AARH_ERR_SHAPE, "offset %d beyond cached length %d of slot %d", off, c->kv_len[sl], sl);
+        if (off + S > c->cfg.max_seq_len + pad)
+            return fail(c, AARH_ERR_SHAPE, "sequence length %d with offset %d exceeds max_seq_len %d", S, off,
+                        c->cfg.max_seq_len);
+        mk = std::max(mk, off + S);
+    }
+    *max_kv = mk;
+    if ((size_t)3 * nseq * 4 > aarh_ctx::STAGE_BYTES) return fail(c, AARH_ERR_SHAPE, "batch %d too large to stage", nseq);
+    int sl = 0;
+    char* p = stage_acquire(c, &sl);
+    if (!p) return fail(c, AARH_ERR_DEVICE, "staging slot wait failed");
+    int32_t* hp = (int32_t*)p;
+    memcpy(hp, offsets, nseq * 4);
+    memcpy(hp + nseq, slots, nseq * 4);
+    memcpy(hp + 2 * nseq, meta, nseq * 4);
+    HIPCHK(c, hipMemcpyAsync(c->d_pos0, hp, nseq * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_slot, hp + nseq, nseq * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_meta, hp + 2 * nseq, nseq * 4, hipMemcpyHostToDevice, c->stream));
+    return stage_release(c, sl);
+}
+
+// Host array -> device through a staging slot (no wait for the device).
+static int stage_copy(aarh_ctx* c, void* dst, const void* src, size_t bytes) {
+    int sl = 0;
+    char* p = bytes <= aarh_ctx::STAGE_BYTES ? stage_acquire(c, &sl) : nullptr;
+    if (!p) {  // too large for a slot: an ordered copy the host waits for
+        HIPCHK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+        return sync_stream(c);
+    }
+    memcpy(p, src, bytes);
+    HIPCHK(c, hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, c->stream));
+    return stage_release(c, sl);
 }
 
 int aarh_forward(aarh_ctx* c, const uint32_t* ids, const int32_t* slots, const int32_t* offsets, int nseq, int S,
@@ -1406,8 +1504,13 @@ struct aarh_session {
     aarh_sampler samp{};
     // device
     float *tgt = nullptr, *drf = nullptr, *anchor = nullptr, *vhid = nullptr;
+    // acceptance results, proposals and the proposal limits share one allocation (`pack`,
+    // int32 words: len, tok, draws, status [nseq each], props [nseq * K], limit [nseq])
+    // so that one read-back returns everything a round's host step needs
+    int32_t* pack = nullptr;
     uint32_t* props = nullptr;
     int32_t *acc_len = nullptr, *acc_tok = nullptr, *acc_draws = nullptr, *acc_status = nullptr, *nprop = nullptr;
+    int32_t* limit = nullptr;
     uint32_t* acc_flags = nullptr;
     uint64_t *seeds = nullptr, *offs = nullptr;
     const float** src = nullptr;
@@ -1424,24 +1527,42 @@ struct aarh_session {
 
     ~aarh_session() {
         cand.release();
-        for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)props, (void*)acc_len,
-                        (void*)acc_tok, (void*)acc_draws, (void*)acc_status, (void*)nprop, (void*)acc_flags,
-                        (void*)seeds, (void*)offs, (void*)src, (void*)dst})
+        for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)pack, (void*)nprop,
+                        (void*)acc_flags, (void*)seeds, (void*)offs, (void*)src, (void*)dst})
             if (p) (void)hipFree(p);
     }
 };
 
 namespace {
 
-int copy_rows_host_lists(aarh_session* e, const std::vector<const float*>& s, const std::vector<float*>& d, int n) {
-    aarh_ctx* c = e->c;
+// Copies row s[i] (n floats) to d[i] on the stream; the pointer lists travel through a
+// pinned staging slot, so nothing waits for the device.
+int copy_rows_staged(aarh_ctx* c, const float** dsrc, float** ddst, const std::vector<const float*>& s,
+                     const std::vector<float*>& d, int n) {
     if (s.empty()) return 0;
     const int rows = (int)s.size();
-    HIPCHK(c, hipMemcpyAsync(e->src, s.data(), rows * sizeof(void*), hipMemcpyHostToDevice, c->stream));
-    HIPCHK(c, hipMemcpyAsync(e->dst, d.data(), rows * sizeof(void*), hipMemcpyHostToDevice, c->stream));
-    KCHK(c, launch_copy_rows(e->src, e->dst, rows, n, c->stream));
-    // the host vectors must outlive the async copies
-    return sync_stream(c);
+    const size_t bytes = (size_t)rows * sizeof(void*);
+    int sl = 0;
+    char* p = 2 * bytes <= aarh_ctx::STAGE_BYTES ? stage_acquire(c, &sl) : nullptr;
+    if (!p) {
+        HIPCHK(c, hipMemcpyAsync(dsrc, s.data(), bytes, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(ddst, d.data(), bytes, hipMemcpyHostToDevice, c->stream));
+        KCHK(c, launch_copy_rows(dsrc, ddst, rows, n, c->stream));
+        // the host vectors must outlive the async copies
+        return sync_stream(c);
+    }
+    memcpy(p, s.data(), bytes);
+    memcpy(p + bytes, d.data(), bytes);
+    HIPCHK(c, hipMemcpyAsync(dsrc, p, bytes, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(ddst, p + bytes, bytes, hipMemcpyHostToDevice, c->stream));
+    int r = stage_release(c, sl);
+    if (r) return r;
+    KCHK(c, launch_copy_rows(dsrc, ddst, rows, n, c->stream));
+    return 0;
+}
+
+int copy_rows_host_lists(aarh_session* e, const std::vector<const float*>& s, const std::vector<float*>& d, int n) {
+    return copy_rows_staged(e->c, e->src, e->dst, s, d, n);
 }
 
 // One round of mtp_speculative.rs:161-322 for every unfinished sequence.
@@ -1463,10 +1584,7 @@ int session_round(aarh_session* e) {
             s[b] = e->tgt + (size_t)b * (K + 1) * V;
             d[b] = e->drf + (size_t)b * K * V;
         }
-        HIPCHK(c, hipMemcpyAsync(e->src, s.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream));
-        HIPCHK(c, hipMemcpyAsync(e->dst, d.data(), nseq * sizeof(void*), hipMemcpyHostToDevice, c->stream));
-        KCHK(c, launch_copy_rows(e->src, e->dst, nseq, V, c->stream));
-        if ((r = sync_stream(c))) return r;
+        if ((r = copy_rows_host_lists(e, s, d, V))) return r;
     }
     for (int p = 0; p < Kr; p++) {
         if (p > 0) {
@@ -1497,36 +1615,53 @@ int session_round(aarh_session* e) {
             HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
         }
     }
-    if ((r = sync_stream(c))) return r;
-    HIPCHK(c, hipMemcpy(e->hprops.data(), e->props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost));
-    for (int b = 0; b < nseq; b++) {
-        int np = 0;
-        if (!e->finished[b]) {
-            for (int p = 0; p < e->count[b]; p++) {
-                np++;
-                e->stats[b].draft_tokens_proposed++;
-                if (e->hprops[(size_t)b * K + p] == EOS_ID) break;
+    // Proposal counts (the EOS cut) and their statistics, from the host copy of the proposals.
+    auto count_proposals = [&]() {
+        for (int b = 0; b < nseq; b++) {
+            int np = 0;
+            if (!e->finished[b]) {
+                for (int p = 0; p < e->count[b]; p++) {
+                    np++;
+                    e->stats[b].draft_tokens_proposed++;
+                    if (e->hprops[(size_t)b * K + p] == EOS_ID) break;
+                }
             }
+            e->hnp[b] = np;
+            // heads ran in lock-step for every row; the reference stops proposing after an EOS
+            // proposal (mtp_speculative.rs:196-198), so only heads 0 .. np-2 count
+            if (np > 1) e->stats[b].mtp_head_forwards += np - 1;
+            if (!e->greedy) e->hoffs[b] += np;
         }
-        e->hnp[b] = np;
-        // heads ran in lock-step for every row; the reference stops proposing after an EOS
-        // proposal (mtp_speculative.rs:196-198), so only heads 0 .. np-2 count
-        if (np > 1) e->stats[b].mtp_head_forwards += np - 1;
-        if (!e->greedy) e->hoffs[b] += np;
+    };
+    // Greedy proposals stay on the device: a kernel writes the verify rows and the counts,
+    // and the host reads the proposals back with the acceptance results (one wait per
+    // round).  Sampled proposals were read back while they were drawn.
+    const bool dev_rows = e->greedy;
+    if (!dev_rows) {
+        if ((r = sync_stream(c))) return r;
+        HIPCHK(c, hipMemcpy(e->hprops.data(), e->props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost));
+        count_proposals();
     }
     // ---- verify forward ----
     // Finished sequences ride along with padding rows written just past their committed
     // length (inside the PAD_SLACK positions every slot has beyond max_seq_len); their
     // kv_len stays, so the slot's cache remains valid for a cached_len follow-up.
     {
-        std::vector<uint32_t> ids((size_t)nseq * Kr);
         std::vector<int32_t> off(nseq);
-        for (int b = 0; b < nseq; b++) {
-            for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = e->hprops[(size_t)b * K + std::min(s2, K - 1)];
-            off[b] = e->base[b];
-        }
+        for (int b = 0; b < nseq; b++) off[b] = e->base[b];
         int mk = 0;
-        if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK))) return r;
+        if (dev_rows) {
+            std::vector<int32_t> lim(nseq);
+            for (int b = 0; b < nseq; b++) lim[b] = e->finished[b] ? 0 : e->count[b];
+            if ((r = stage_rows_meta(c, e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK, lim.data(), e->limit)))
+                return r;
+            KCHK(c, launch_mtp_verify_rows(e->props, K, Kr, nseq, e->limit, EOS_ID, c->d_ids, e->nprop, c->stream));
+        } else {
+            std::vector<uint32_t> ids((size_t)nseq * Kr);
+            for (int b = 0; b < nseq; b++)
+                for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = e->hprops[(size_t)b * K + std::min(s2, K - 1)];
+            if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK))) return r;
+        }
         if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, e->tgt + V, rm(Kr, (long long)(K + 1) * V, V),
                              e->vhid)))
             return r;
@@ -1538,8 +1673,8 @@ int session_round(aarh_session* e) {
     }
     // ---- acceptance (MTP round: no bonus) ----
     {
-        HIPCHK(c, hipMemcpyAsync(e->offs, e->hoffs.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
-        HIPCHK(c, hipMemcpyAsync(e->nprop, e->hnp.data(), nseq * 4, hipMemcpyHostToDevice, c->stream));
+        if ((r = stage_copy(c, e->offs, e->hoffs.data(), nseq * 8))) return r;
+        if (!dev_rows && (r = stage_copy(c, e->nprop, e->hnp.data(), nseq * 4))) return r;
         if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 0, &e->samp, e->seeds,
                                     e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
                                     nullptr)))
@@ -1547,10 +1682,19 @@ int session_round(aarh_session* e) {
         if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
-        HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
-        HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
-        HIPCHK(c, hipMemcpy(e->hdraws.data(), e->acc_draws, nseq * 4, hipMemcpyDeviceToHost));
-        HIPCHK(c, hipMemcpy(e->hstatus.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
+        // one read-back: lengths, tokens, draws, status, then the proposals
+        std::vector<int32_t> hp((size_t)nseq * (4 + K));
+        HIPCHK(c, hipMemcpy(hp.data(), e->pack, hp.size() * 4, hipMemcpyDeviceToHost));
+        for (int b = 0; b < nseq; b++) {
+            e->hlen[b] = hp[b];
+            e->htok[b] = hp[nseq + b];
+            e->hdraws[b] = hp[2 * nseq + b];
+            e->hstatus[b] = hp[3 * nseq + b];
+        }
+        if (dev_rows) {
+            memcpy(e->hprops.data(), hp.data() + 4 * nseq, (size_t)nseq * K * 4);
+            count_proposals();
+        }
     }
     // ---- commit, rollback, replay ----
     std::vector<int> replay_seq, replay_len;
@@ -1708,11 +1852,13 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
     SA(drf, (size_t)nseq * K * V * 4);
     SA(anchor, (size_t)nseq * H * 4);
     SA(vhid, (size_t)nseq * K * H * 4);
-    SA(props, (size_t)nseq * K * 4);
-    SA(acc_len, nseq * 4);
-    SA(acc_tok, nseq * 4);
-    SA(acc_draws, nseq * 4);
-    SA(acc_status, nseq * 4);
+    SA(pack, ((size_t)nseq * (5 + K)) * 4);
+    e->acc_len = e->pack;
+    e->acc_tok = e->pack + nseq;
+    e->acc_draws = e->pack + 2 * nseq;
+    e->acc_status = e->pack + 3 * nseq;
+    e->props = (uint32_t*)(e->pack + 4 * nseq);
+    e->limit = e->pack + (size_t)nseq * (4 + K);
     SA(nprop, nseq * 4);
     SA(acc_flags, nseq * 4);
     SA(seeds, nseq * 8);
