@@ -408,6 +408,51 @@ def run_c5(args):
     print(json.dumps(line))
 
 
+def probe_memory():
+    """Two device reference figures beside the roofline peaks: the HBM rate of a plain
+    device copy (read + write bytes of 256 MiB copies between four rotating buffer pairs, so
+    that no launch finds its input in the 256 MB last-level cache), and the time per kernel
+    of a replayed graph of 100 one-element kernels (the floor every dependent launch pays)."""
+    import torch
+    n = 64 << 20
+    src = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(4)]
+    dst = [torch.empty_like(a) for a in src]
+    for a, b in zip(src, dst):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    rates = []
+    for i in range(16):
+        ev[0].record()
+        dst[i % 4].copy_(src[i % 4])
+        ev[1].record()
+        torch.cuda.synchronize()
+        rates.append(2 * n * 4 / (ev[0].elapsed_time(ev[1]) * 1e-3) / 1e9)
+    rates = rates[4:]
+    x = torch.zeros(1, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            x.add_(1.0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(100):
+                x.add_(1.0)
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(5):
+        ev[0].record()
+        g.replay()
+        ev[1].record()
+        torch.cuda.synchronize()
+        per.append(ev[0].elapsed_time(ev[1]) * 1e3 / 100)
+    return {"probe": "memory", "copy_bytes_read_plus_written": 2 * n * 4,
+            "copy_gbs_mean": round(sum(rates) / len(rates), 1), "copy_gbs_max": round(max(rates), 1),
+            "hbm_peak_gbs": HBM_PEAK_GBS, "graph_kernel_floor_us": round(min(per), 2),
+            "graph_kernel_floor_us_mean": round(sum(per) / len(per), 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,7 +467,13 @@ def main():
                          "step; c2 / c3: only that measurement (profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (counter calibration for rocprof --pmc)")
+    ap.add_argument("--probe-memory", action="store_true",
+                    help="run only two reference measurements of the device: the HBM rate a plain device "
+                         "copy reaches, and the per-kernel floor of a replayed graph")
     args = ap.parse_args()
+    if args.probe_memory:
+        print(json.dumps(probe_memory()))
+        return
     if args.calibrate_copy:
         import torch
         a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
