@@ -158,7 +158,10 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
             float sc = -INFINITY;
             const int t = tb + lane;
             if (lane < nt && t <= limit) {
+                // one accumulation chain in dimension order; unrolled so the LDS reads of
+                // later dimensions are in flight while earlier products accumulate
                 float dot = 0.f;
+#pragma unroll 16
                 for (int d = 0; d < hd; d++) dot = fmaf(qs[r][d], ks[lane][d], dot);
                 sc = dot * a.scale;
             }
@@ -179,6 +182,7 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
             const int r = wid + 4 * j;
             if (r >= R) break;
             float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
             for (int t = 0; t < nt; t++) {
                 float p = ps[r][t];
                 a0 = fmaf(p, vs[t][lane], a0);
@@ -189,6 +193,26 @@ __global__ void __launch_bounds__(AT_THREADS) attn_kernel(AttnArgs a) {
         }
     }
 
+    if (a.nchunks == 1) {
+        // one chunk: its (m, l, O) is the result (the merge below would weight it by exp(0) = 1)
+#pragma unroll
+        for (int j = 0; j < AT_MAXR / 4; j++) {
+            const int r = wid + 4 * j;
+            if (r >= R) break;
+            const float inv = lrow[j] > 0.f ? 1.0f / lrow[j] : 0.f;
+            const int rr = r0 + r;
+            const int h = kvh + (rr % G) * a.n_kv;
+            const int orow = seq * a.S + rr / G;
+            float* out = a.out + (size_t)orow * QD + h * hd;
+            if (lane < hd) out[lane] = o0[j] * inv;
+            if (lane + 64 < hd) out[lane + 64] = o1[j] * inv;
+            if (a.fo.buf) {
+                if (lane < hd) frag_put(a.fo, orow, h * hd + lane, o0[j] * inv);
+                if (lane + 64 < hd) frag_put(a.fo, orow, h * hd + lane + 64, o1[j] * inv);
+            }
+        }
+        return;
+    }
     // ---- write partial (m, l, O) for this chunk ----
     const size_t grp = ((size_t)seq * a.n_kv + kvh) * a.ntiles + tile;
     const size_t rec = (size_t)hd + 2;
