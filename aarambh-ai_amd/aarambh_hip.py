@@ -15,6 +15,7 @@ Errors raise AarambhError subclasses (core/src/error.rs:5-33).  There is no
 CPU fallback: a missing or unloadable library raises immediately.
 """
 import atexit
+import collections
 import ctypes as C
 import os
 import weakref
@@ -145,6 +146,10 @@ def lib():
         "aarh_session_step": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
         "aarh_session_result": (C.c_int, [_P, _P, C.c_int32, _P, _P, C.POINTER(_Stats)]),
         "aarh_session_end": (None, [_P]),
+        "aarh_session_open": (C.c_int, [_P, C.c_int, C.c_int, C.POINTER(_Sampler), C.POINTER(_P)]),
+        "aarh_session_admit": (C.c_int, [_P, C.c_int, _P, C.c_int, C.c_int, C.c_uint64, C.c_int]),
+        "aarh_session_retire": (C.c_int, [_P, C.c_int]),
+        "aarh_session_rows": (C.c_int, [_P, _P]),
         "aarh_spec_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
                                          _P, _P, _P, C.POINTER(_Stats), _P, _P]),
         "aarh_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
@@ -190,7 +195,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_session_candidates", "aarh_top_candidates", "aarh_set_graphs", "aarh_session_rng_offsets",
             "aarh_session_set_rng_offsets", "aarh_accept_sample_static", "aarh_get_config", "aarh_set_replay_schedule", "aarh_load_gguf",
             "aarh_load_safetensors", "aarh_gguf_config", "aarh_gguf_read_tensor", "aarh_host_last_error",
-            "aarh_safetensors_read_tensor",
+            "aarh_safetensors_read_tensor", "aarh_session_open", "aarh_session_admit", "aarh_session_retire",
+            "aarh_session_rows",
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
@@ -597,6 +603,26 @@ class SpeculativeEngine:
         return self.generate_batch(np.asarray(prompt_ids)[None, :], max_new_tokens, sampler)[0]
 
 
+def _session_outputs(model, h, n, cap, candidates=True):
+    """GenerationOutput of every row of a session (committed tokens up to `cap` per row)."""
+    cap = max(cap, 1)
+    out = np.zeros((n, cap), np.uint32)
+    ln = np.zeros(n, np.int32)
+    fin = np.zeros(n, np.int32)
+    stats = (_Stats * n)()
+    model._check(lib().aarh_session_result(h, _ptr(out), cap, _ptr(ln), _ptr(fin), stats))
+    if candidates:
+        ci = np.zeros((n, cap, TOP_CANDIDATES), np.uint32)
+        cp = np.zeros((n, cap, TOP_CANDIDATES), np.float32)
+        model._check(lib().aarh_session_candidates(h, _ptr(ci), _ptr(cp), cap))
+    res = []
+    for b in range(n):
+        st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
+        cands = _candidate_lists(ci[b, :ln[b]], cp[b, :ln[b]]) if candidates else []
+        res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st, cands))
+    return res
+
+
 class Session:
     """Round-by-round driver of the MTP engine (aarh_session_*)."""
 
@@ -620,22 +646,7 @@ class Session:
         return bool(done.value)
 
     def result(self):
-        n = self.nseq
-        out = np.zeros((n, max(self.max_new, 1)), np.uint32)
-        ln = np.zeros(n, np.int32)
-        fin = np.zeros(n, np.int32)
-        stats = (_Stats * n)()
-        self.engine.model._check(lib().aarh_session_result(self.h, _ptr(out), out.shape[1], _ptr(ln), _ptr(fin),
-                                                           stats))
-        ci = np.zeros((n, out.shape[1], TOP_CANDIDATES), np.uint32)
-        cp = np.zeros((n, out.shape[1], TOP_CANDIDATES), np.float32)
-        self.engine.model._check(lib().aarh_session_candidates(self.h, _ptr(ci), _ptr(cp), out.shape[1]))
-        res = []
-        for b in range(n):
-            st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
-            res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st,
-                                        _candidate_lists(ci[b, :ln[b]], cp[b, :ln[b]])))
-        return res
+        return _session_outputs(self.engine.model, self.h, self.nseq, self.max_new)
 
     def rng_offsets(self):
         """Keystream word position of each request's sampler (the next uniform it draws)."""
@@ -654,6 +665,168 @@ class Session:
 
     def __del__(self):
         self.close()
+
+
+class ContinuousSession:
+    """Row-level driver of the MTP engine for continuous batching (aarh_session_open /
+    _admit / _retire / _rows): a request joins a free row between rounds with its own
+    prompt, token budget and seed (prepare_session_with_chunk_size, engine.rs:271-317)
+    and leaves when it completes or is cancelled; the rounds run every generating row."""
+
+    FREE, GENERATING, FINISHED = 0, 1, 2
+
+    def __init__(self, engine, capacity, sampler: Sampler):
+        self.engine = engine
+        self.capacity = capacity
+        self.budget = [0] * capacity
+        h = _P()
+        engine.model._check(lib().aarh_session_open(engine.model.h, capacity, engine.config.num_draft_tokens,
+                                                    C.byref(sampler._c()), C.byref(h)))
+        self.h = h
+
+    def admit(self, row, prompt_ids, max_new_tokens, seed=0, prefill_chunk=128):
+        p = np.ascontiguousarray(np.asarray(prompt_ids).reshape(-1), np.uint32)
+        self.engine.model._check(lib().aarh_session_admit(self.h, row, _ptr(p), p.size, max_new_tokens, seed,
+                                                          prefill_chunk))
+        self.budget[row] = max_new_tokens
+
+    def retire(self, row):
+        self.engine.model._check(lib().aarh_session_retire(self.h, row))
+        self.budget[row] = 0
+
+    def rows(self):
+        st = np.zeros(self.capacity, np.int32)
+        self.engine.model._check(lib().aarh_session_rows(self.h, _ptr(st)))
+        return st
+
+    def step(self, rounds=1):
+        done = C.c_int32()
+        self.engine.model._check(lib().aarh_session_step(self.h, rounds, C.byref(done)))
+        return bool(done.value)
+
+    def results(self, candidates=True):
+        return _session_outputs(self.engine.model, self.h, self.capacity, max(self.budget), candidates)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aarh_session_end(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+@dataclass
+class BatcherConfig:
+    """serve/src/batching.rs:18-40 (batch_wait has no counterpart: step() is driven by the
+    caller)."""
+    max_batch_size: int = 8
+    queue_capacity: int = 128
+    prefill_chunk_size: int = 128
+
+
+@dataclass
+class GenerationRequest:
+    """One request (batching.rs:42-51) as token ids (the tokenizer is not on this path):
+    its token budget and its sampler seed (the sampler settings are the batcher's)."""
+    prompt_ids: object
+    max_new_tokens: int
+    seed: int = 0
+
+
+class QueueFull(AarambhError):
+    """SubmitError::QueueFull (batching.rs:66-73)."""
+
+
+class SpeculativeBatcher:
+    """Continuous batching with speculative rounds: one step() is one iteration of the
+    serving worker (run_worker, serve/src/batching.rs:324-445) with its single-token
+    batched decode (decode_sessions, inference/src/engine.rs:323-355) replaced by MTP
+    speculative rounds over the active requests:
+      1. admit queued requests in submission order while fewer than max_batch_size are
+         active (admit_job, :463-483): a request whose prefill fails is answered with a
+         failure and takes no row;
+      2. drop requests whose caller cancelled them (:363-367);
+      3. run `rounds` speculative rounds over every active request;
+      4. report each active request's newly committed tokens, and complete and free the
+         requests that finished (:405-432).
+    step() returns the events of the iteration in that order: ("delta", id, token_ids),
+    ("completed", id, GenerationOutput), ("failed", id, message)."""
+
+    def __init__(self, engine: MtpSpeculativeEngine, config: BatcherConfig, sampler: Sampler):
+        if config.max_batch_size == 0 or config.queue_capacity == 0 or config.prefill_chunk_size == 0:
+            raise ConfigError("batch size and queue capacity must be greater than zero")
+        self.config = config
+        self.session = ContinuousSession(engine, config.max_batch_size, sampler)
+        self.queue = collections.deque()
+        self.active = {}  # row -> [request id, tokens reported]
+        self.cancelled = set()
+        self.next_id = 0
+
+    def submit(self, request: GenerationRequest):
+        if len(self.queue) >= self.config.queue_capacity:
+            raise QueueFull("request queue is full")
+        rid = self.next_id
+        self.next_id += 1
+        self.queue.append((rid, request))
+        return rid
+
+    def cancel(self, rid):
+        self.cancelled.add(rid)
+
+    def pending(self):
+        return len(self.queue) + len(self.active)
+
+    def step(self, rounds=1):
+        events = []
+        free = [b for b in range(self.config.max_batch_size) if b not in self.active]
+        while self.queue and free:
+            rid, req = self.queue.popleft()
+            if rid in self.cancelled:
+                self.cancelled.discard(rid)
+                continue
+            row = free[0]
+            try:
+                self.session.admit(row, req.prompt_ids, req.max_new_tokens, req.seed,
+                                   self.config.prefill_chunk_size)
+            except AarambhError as exc:
+                events.append(("failed", rid, str(exc)))
+                continue
+            free.pop(0)
+            self.active[row] = [rid, 0]
+        for row, (rid, _) in list(self.active.items()):
+            if rid in self.cancelled:
+                self.cancelled.discard(rid)
+                self.session.retire(row)
+                del self.active[row]
+        if not self.active:
+            return events
+        self.session.step(rounds)
+        state = self.session.rows()
+        done = [row for row in self.active if state[row] == ContinuousSession.FINISHED]
+        outs = self.session.results(candidates=bool(done))
+        for row in sorted(self.active):
+            rid, seen = self.active[row]
+            toks = outs[row].token_ids
+            if len(toks) > seen:
+                events.append(("delta", rid, [int(t) for t in toks[seen:]]))
+                self.active[row][1] = len(toks)
+        for row in done:
+            events.append(("completed", self.active[row][0], outs[row]))
+            self.session.retire(row)
+            del self.active[row]
+        return events
+
+    def run(self, rounds=1):
+        """Steps until every submitted request has completed, failed or been cancelled;
+        returns the events in order."""
+        events = []
+        while self.queue or self.active:
+            events += self.step(rounds)
+        return events
+
+    def close(self):
+        self.session.close()
 
 
 # ---------------------------------------------------------------------------

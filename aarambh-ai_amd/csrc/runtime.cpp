@@ -466,9 +466,13 @@ int forward_launches(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, 
 // launch cost is of the same order, so repeated shapes replay a captured HIP
 // graph (one host call).  Key: everything the launches bake in.  A shape is
 // captured the second time it is seen (the first run also initialises the
-// launchers' one-time attributes outside any capture).
+// launchers' one-time attributes outside any capture).  Prompt prefill chunks
+// (more rows per sequence than any round forward has) run without a graph: their
+// kernels are long enough to hide the launches, and their shapes (the last chunk of
+// each prompt length) rarely repeat, so capturing them would only churn the cache.
 constexpr int GRAPH_KV_GRANULE = 256;  // kv_span rounding: one graph serves 256 cache positions
-constexpr size_t GRAPH_CACHE_MAX = 48;
+constexpr size_t GRAPH_CACHE_MAX = 160;
+constexpr int GRAPH_MAX_S = PAD_SLACK;  // verify and replay forwards have at most num_draft_tokens + 1 rows
 
 bool same_key(const FwdGraph& g, const FwdGraph& k) {
     return g.nseq == k.nseq && g.S == k.S && g.kv_span == k.kv_span && g.lout == k.lout && g.hout == k.hout &&
@@ -481,7 +485,7 @@ int forward_dev(aarh_ctx* c, const uint32_t* d_ids, const int32_t* d_pos0, const
     const int M = nseq * S;
     if (M > c->Mmax) return fail(c, AARH_ERR_SHAPE, "rows %d exceed max_rows %d", M, c->Mmax);
     const int kv_span = std::min(c->cap, (max_kv_len + GRAPH_KV_GRANULE - 1) / GRAPH_KV_GRANULE * GRAPH_KV_GRANULE);
-    if (!c->graphs || c->prof)
+    if (!c->graphs || c->prof || S > GRAPH_MAX_S)
         return forward_launches(c, d_ids, d_pos0, d_slot, nseq, S, kv_span, lout, lmap, hout);
     FwdGraph key{};
     key.nseq = nseq;
@@ -1499,7 +1503,7 @@ struct CandBuf {
 
 struct aarh_session {
     aarh_ctx* c = nullptr;
-    int nseq = 0, K = 0, max_new = 0, max_new_req = 0, available = 0;
+    int nseq = 0, K = 0;  // nseq: rows (request capacity)
     bool greedy = true;
     aarh_sampler samp{};
     // device
@@ -1515,9 +1519,11 @@ struct aarh_session {
     uint64_t *seeds = nullptr, *offs = nullptr;
     const float** src = nullptr;
     float** dst = nullptr;
-    // host state
+    // host state, per row: `live` = the row holds a request (admitted and not retired);
+    // `finished` = it takes no further rounds (done, or a free row)
     std::vector<uint64_t> hoffs;
-    std::vector<char> finished;
+    std::vector<char> live, finished;
+    std::vector<int> max_new, available;
     std::vector<std::vector<uint32_t>> out;
     std::vector<int32_t> finish;
     std::vector<aarh_spec_stats> stats;
@@ -1565,15 +1571,25 @@ int copy_rows_host_lists(aarh_session* e, const std::vector<const float*>& s, co
     return copy_rows_staged(e->c, e->src, e->dst, s, d, n);
 }
 
+// Rows a round runs over: 0 .. the last unfinished row.  Finished and free rows below
+// it ride along as padding; rows above it take no work.
+int session_rows(const aarh_session* e) {
+    int n = 0;
+    for (int b = 0; b < e->nseq; b++)
+        if (!e->finished[b]) n = b + 1;
+    return n;
+}
+
 // One round of mtp_speculative.rs:161-322 for every unfinished sequence.
 int session_round(aarh_session* e) {
     aarh_ctx* c = e->c;
-    const int nseq = e->nseq, K = e->K, V = c->V, H = c->H;
+    const int nseq = session_rows(e), K = e->K, V = c->V, H = c->H;
+    const int cap = e->nseq;  // row stride of the packed acceptance results
     int r;
     int Kr = 1;
     for (int b = 0; b < nseq; b++) {
         e->base[b] = c->kv_len[b];
-        e->count[b] = e->finished[b] ? 1 : std::min(K, e->max_new - (int)e->out[b].size());
+        e->count[b] = e->finished[b] ? 1 : std::min(K, e->max_new[b] - (int)e->out[b].size());
         Kr = std::max(Kr, e->count[b]);
     }
     // ---- proposals: index 0 from target_next, index p from MTP head p-1 ----
@@ -1647,8 +1663,9 @@ int session_round(aarh_session* e) {
     // length (inside the PAD_SLACK positions every slot has beyond max_seq_len); their
     // kv_len stays, so the slot's cache remains valid for a cached_len follow-up.
     {
+        // (a free row's padding goes to position 0 of its slot, so its attention is short)
         std::vector<int32_t> off(nseq);
-        for (int b = 0; b < nseq; b++) off[b] = e->base[b];
+        for (int b = 0; b < nseq; b++) off[b] = e->live[b] ? e->base[b] : 0;
         int mk = 0;
         if (dev_rows) {
             std::vector<int32_t> lim(nseq);
@@ -1682,17 +1699,18 @@ int session_round(aarh_session* e) {
         if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
-        // one read-back: lengths, tokens, draws, status, then the proposals
-        std::vector<int32_t> hp((size_t)nseq * (4 + K));
+        // one read-back: lengths, tokens, draws, status, then the proposals (rows of the
+        // round; the sections are `cap` rows apart)
+        std::vector<int32_t> hp((size_t)cap * 4 + (size_t)nseq * K);
         HIPCHK(c, hipMemcpy(hp.data(), e->pack, hp.size() * 4, hipMemcpyDeviceToHost));
         for (int b = 0; b < nseq; b++) {
             e->hlen[b] = hp[b];
-            e->htok[b] = hp[nseq + b];
-            e->hdraws[b] = hp[2 * nseq + b];
-            e->hstatus[b] = hp[3 * nseq + b];
+            e->htok[b] = hp[cap + b];
+            e->hdraws[b] = hp[2 * cap + b];
+            e->hstatus[b] = hp[3 * cap + b];
         }
         if (dev_rows) {
-            memcpy(e->hprops.data(), hp.data() + 4 * nseq, (size_t)nseq * K * 4);
+            memcpy(e->hprops.data(), hp.data() + 4 * cap, (size_t)nseq * K * 4);
             count_proposals();
         }
     }
@@ -1717,7 +1735,7 @@ int session_round(aarh_session* e) {
             }
             e->out[b].push_back(t);
             e->cand.commit(b, b * (K + 1) + i);
-            if ((int)e->out[b].size() == e->max_new) done = true;
+            if ((int)e->out[b].size() == e->max_new[b]) done = true;
         }
         if (done) {
             e->finished[b] = 1;
@@ -1795,19 +1813,13 @@ int session_round(aarh_session* e) {
         if ((r = copy_rows_host_lists(e, rs, rd, V)) || (r = copy_rows_host_lists(e, rhs, rhd, H))) return r;
     }
     for (int b = 0; b < nseq; b++)
-        if (!e->finished[b] && (int)e->out[b].size() >= e->max_new) e->finished[b] = 1;
+        if (!e->finished[b] && (int)e->out[b].size() >= e->max_new[b]) e->finished[b] = 1;
     return 0;
 }
 
-}  // namespace
-
-extern "C" {
-
-int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int cached_len,
-                       int max_new_tokens, int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds,
-                       aarh_session** out) {
-    if (!c || !s || !out) return AARH_ERR_CONFIG;
-    *out = nullptr;
+// A session of nseq rows, every row free (finished, holding no request): the checks of
+// MtpSpeculativeEngine::new (mtp_speculative.rs:40-71) and the device buffers.
+int session_create(aarh_ctx* c, int nseq, int num_draft_tokens, const aarh_sampler* s, aarh_session** out) {
     const auto& g = c->cfg;
     if (c->nheads_mtp == 0) return fail(c, AARH_ERR_CONFIG, "internal speculative decoding requires model.mtp configuration");
     if (num_draft_tokens < 2) return fail(c, AARH_ERR_CONFIG, "MTP speculative decoding requires at least two proposal tokens");
@@ -1817,28 +1829,19 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
     if (num_draft_tokens >= PAD_SLACK)
         return fail(c, AARH_ERR_UNSUPPORTED, "num_draft_tokens must be below %d on the device path", PAD_SLACK);
     if (nseq <= 0 || nseq > g.max_batch) return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
-    if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
-    if (cached_len < 0) return fail(c, AARH_ERR_SHAPE, "negative cached length");
-    for (int b = 0; b < nseq; b++)
-        if (c->kv_len[b] < cached_len)
-            return fail(c, AARH_ERR_SHAPE, "slot %d holds %d cached tokens, fewer than %d", b, c->kv_len[b], cached_len);
-    const int full = cached_len + prompt_len;
-    if (full >= g.max_seq_len)
-        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", full, g.max_seq_len);
-    const bool greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
     const int K = num_draft_tokens, V = c->V, H = c->H;
     if (nseq * K > c->Mmax) return fail(c, AARH_ERR_SHAPE, "nseq x draft tokens exceeds max_rows");
     aarh_session* e = new aarh_session();
     e->c = c;
     e->nseq = nseq;
     e->K = K;
-    e->greedy = greedy;
+    e->greedy = s->greedy || !(s->temperature > 1.1920929e-07f);
     e->samp = *s;
-    e->available = g.max_seq_len - full;
-    e->max_new_req = max_new_tokens;
-    e->max_new = std::min(max_new_tokens, e->available);
     e->hoffs.assign(nseq, 0);
-    e->finished.assign(nseq, 0);
+    e->live.assign(nseq, 0);
+    e->finished.assign(nseq, 1);
+    e->max_new.assign(nseq, 0);
+    e->available.assign(nseq, 0);
     e->out.assign(nseq, {});
     e->finish.assign(nseq, AARH_FINISH_MAX_TOKENS);
     e->stats.assign(nseq, aarh_spec_stats{});
@@ -1870,55 +1873,162 @@ int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int promp
         delete e;
         return r;
     }
+    *out = e;
+    return 0;
+}
+
+// Row b takes a new request of `full` context tokens (cached + prompt): fresh output,
+// statistics, candidates and keystream, and the token budget min(max_new_tokens,
+// available) of prepare_session (engine.rs:288-297); a zero budget finishes at once
+// with ContextLimit (GenerationSession::new, engine.rs:771).  Returns the budget.
+int session_row_reset(aarh_session* e, int b, int full, int max_new_tokens) {
+    e->live[b] = 1;
+    e->available[b] = e->c->cfg.max_seq_len - full;
+    e->max_new[b] = std::min(max_new_tokens, e->available[b]);
+    e->finished[b] = e->max_new[b] <= 0;
+    e->finish[b] = e->max_new[b] <= 0 ? AARH_FINISH_CONTEXT_LIMIT : AARH_FINISH_MAX_TOKENS;
+    e->out[b].clear();
+    e->stats[b] = aarh_spec_stats{};
+    e->hoffs[b] = 0;
+    e->cand.out_ids[b].clear();
+    e->cand.out_probs[b].clear();
+    return e->max_new[b];
+}
+
+// Prefill of rows[i]'s prompt tail (S0 tokens each, [n][S0]) from position `from`, in
+// forwards of at most `chunk` tokens per row (prepare_session_with_chunk_size,
+// engine.rs:300-307); the last row's logits and hidden state seed the first round.
+int session_prefill(aarh_session* e, const int32_t* rows, int n, const uint32_t* prompts, int S0, int from, int chunk) {
+    aarh_ctx* c = e->c;
+    const int K = e->K, V = c->V, H = c->H;
+    chunk = std::max(1, std::min(chunk, c->Mmax / n));
+    std::vector<uint32_t> ids;
+    std::vector<int32_t> offs(n);
+    int r;
+    for (int i = 0; i < n; i++) c->kv_len[rows[i]] = from;
+    for (int p0 = 0; p0 < S0; p0 += chunk) {
+        const int S = std::min(chunk, S0 - p0);
+        ids.resize((size_t)n * S);
+        for (int i = 0; i < n; i++) {
+            offs[i] = from + p0;
+            for (int s2 = 0; s2 < S; s2++) ids[(size_t)i * S + s2] = prompts[(size_t)i * S0 + p0 + s2];
+        }
+        int mk = 0;
+        if ((r = stage_rows(c, ids.data(), rows, offs.data(), n, S, &mk)) ||
+            (r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, n, S, mk, c->logits, rm(n * S, 0, V), c->hidden)))
+            return r;
+        for (int i = 0; i < n; i++) c->kv_len[rows[i]] = from + p0 + S;
+        if (p0 + S == S0) {
+            std::vector<const float*> ls(n), hsrc(n);
+            std::vector<float*> ld(n), hd(n);
+            for (int i = 0; i < n; i++) {
+                ls[i] = c->logits + ((size_t)i * S + S - 1) * V;
+                ld[i] = e->tgt + (size_t)rows[i] * (K + 1) * V;
+                hsrc[i] = c->hidden + ((size_t)i * S + S - 1) * H;
+                hd[i] = e->anchor + (size_t)rows[i] * H;
+            }
+            if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hsrc, hd, H))) return r;
+        }
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aarh_session_begin(aarh_ctx* c, const uint32_t* prompts, int nseq, int prompt_len, int cached_len,
+                       int max_new_tokens, int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds,
+                       aarh_session** out) {
+    if (!c || !s || !out) return AARH_ERR_CONFIG;
+    *out = nullptr;
+    const auto& g = c->cfg;
+    if (nseq <= 0 || nseq > g.max_batch) return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
+    if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
+    if (cached_len < 0) return fail(c, AARH_ERR_SHAPE, "negative cached length");
+    for (int b = 0; b < nseq; b++)
+        if (c->kv_len[b] < cached_len)
+            return fail(c, AARH_ERR_SHAPE, "slot %d holds %d cached tokens, fewer than %d", b, c->kv_len[b], cached_len);
+    const int full = cached_len + prompt_len;
+    if (full >= g.max_seq_len)
+        return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model context limit is %d", full, g.max_seq_len);
+    aarh_session* e = nullptr;
+    int r = session_create(c, nseq, num_draft_tokens, s, &e);
+    if (r) return r;
     std::vector<uint64_t> hs(nseq);
     for (int b = 0; b < nseq; b++) hs[b] = seeds ? seeds[b] : 0;
     if (hipMemcpy(e->seeds, hs.data(), nseq * 8, hipMemcpyHostToDevice) != hipSuccess) {
         delete e;
         return fail(c, AARH_ERR_DEVICE, "seed upload failed");
     }
-    if (e->max_new <= 0) {
-        for (int b = 0; b < nseq; b++) {
-            e->finish[b] = AARH_FINISH_CONTEXT_LIMIT;
-            e->finished[b] = 1;
-        }
-        *out = e;
-        return 0;
-    }
-    // ---- prefill of the uncached prompt tail, chunked so rows stay within max_rows ----
-    const int chunk = std::max(1, c->Mmax / nseq);
-    std::vector<uint32_t> ids;
-    std::vector<int32_t> offs(nseq);
-    for (int b = 0; b < nseq; b++) c->kv_len[b] = cached_len;
-    for (int p0 = 0; p0 < prompt_len; p0 += chunk) {
-        const int S = std::min(chunk, prompt_len - p0);
-        ids.resize((size_t)nseq * S);
-        for (int b = 0; b < nseq; b++) {
-            offs[b] = cached_len + p0;
-            for (int s2 = 0; s2 < S; s2++) ids[(size_t)b * S + s2] = prompts[(size_t)b * prompt_len + p0 + s2];
-        }
-        int mk = 0;
-        if ((r = stage_rows(c, ids.data(), e->slots.data(), offs.data(), nseq, S, &mk)) ||
-            (r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, S, mk, c->logits, rm(nseq * S, 0, V), c->hidden))) {
+    int budget = 0;
+    for (int b = 0; b < nseq; b++) budget = session_row_reset(e, b, full, max_new_tokens);
+    if (budget > 0) {
+        // ---- prefill of the uncached prompt tail, chunked so rows stay within max_rows ----
+        if ((r = session_prefill(e, e->slots.data(), nseq, prompts, prompt_len, cached_len, c->Mmax))) {
             delete e;
             return r;
         }
-        for (int b = 0; b < nseq; b++) c->kv_len[b] = cached_len + p0 + S;
-        if (p0 + S == prompt_len) {
-            std::vector<const float*> ls(nseq), hsrc(nseq);
-            std::vector<float*> ld(nseq), hd(nseq);
-            for (int b = 0; b < nseq; b++) {
-                ls[b] = c->logits + ((size_t)b * S + S - 1) * V;
-                ld[b] = e->tgt + (size_t)b * (K + 1) * V;
-                hsrc[b] = c->hidden + ((size_t)b * S + S - 1) * H;
-                hd[b] = e->anchor + (size_t)b * H;
-            }
-            if ((r = copy_rows_host_lists(e, ls, ld, V)) || (r = copy_rows_host_lists(e, hsrc, hd, H))) {
-                delete e;
-                return r;
-            }
-        }
     }
     *out = e;
+    return 0;
+}
+
+int aarh_session_open(aarh_ctx* c, int capacity, int num_draft_tokens, const aarh_sampler* s, aarh_session** out) {
+    if (!c || !s || !out) return AARH_ERR_CONFIG;
+    *out = nullptr;
+    return session_create(c, capacity, num_draft_tokens, s, out);
+}
+
+int aarh_session_admit(aarh_session* e, int row, const uint32_t* prompt, int prompt_len, int max_new_tokens,
+                       uint64_t seed, int prefill_chunk) {
+    if (!e) return AARH_ERR_CONFIG;
+    aarh_ctx* c = e->c;
+    if (prefill_chunk <= 0) return fail(c, AARH_ERR_CONFIG, "prefill chunk size must be greater than zero");
+    if (row < 0 || row >= e->nseq) return fail(c, AARH_ERR_SHAPE, "row %d outside the session's %d rows", row, e->nseq);
+    if (e->live[row]) return fail(c, AARH_ERR_CONFIG, "row %d holds a request that has not been retired", row);
+    if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
+    if (!prompt) return fail(c, AARH_ERR_CONFIG, "null prompt");
+    if (max_new_tokens < 0) return fail(c, AARH_ERR_SHAPE, "negative max_new_tokens");
+    const int msl = c->cfg.max_seq_len;
+    if (prompt_len >= msl) return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but model max_seq_len is %d", prompt_len, msl);
+    int r = stage_copy(c, e->seeds + row, &seed, 8);
+    if (r) return r;
+    if (session_row_reset(e, row, prompt_len, max_new_tokens) <= 0) {
+        c->kv_len[row] = 0;
+        return 0;
+    }
+    const int32_t rows[1] = {row};
+    if ((r = session_prefill(e, rows, 1, prompt, prompt_len, 0, prefill_chunk))) {
+        // the row stays free: the request failed before it joined (admit_job, batching.rs:471-482)
+        e->live[row] = 0;
+        e->finished[row] = 1;
+        c->kv_len[row] = 0;
+        return r;
+    }
+    return 0;
+}
+
+int aarh_session_retire(aarh_session* e, int row) {
+    if (!e) return AARH_ERR_CONFIG;
+    if (row < 0 || row >= e->nseq) return fail(e->c, AARH_ERR_SHAPE, "row %d outside the session's %d rows", row, e->nseq);
+    // the request leaves (completed or cancelled, batching.rs:363-367, 405-432): its row and
+    // KV slot are free; a free row rides along in later rounds as padding at position 0
+    e->live[row] = 0;
+    e->finished[row] = 1;
+    e->finish[row] = AARH_FINISH_MAX_TOKENS;
+    e->max_new[row] = e->available[row] = 0;
+    e->out[row].clear();
+    e->stats[row] = aarh_spec_stats{};
+    e->cand.out_ids[row].clear();
+    e->cand.out_probs[row].clear();
+    e->c->kv_len[row] = 0;
+    return 0;
+}
+
+int aarh_session_rows(aarh_session* e, int32_t* state) {
+    if (!e || !state) return AARH_ERR_CONFIG;
+    for (int b = 0; b < e->nseq; b++) state[b] = !e->live[b] ? 0 : !e->finished[b] ? 1 : 2;
     return 0;
 }
 
@@ -1949,7 +2059,7 @@ int aarh_session_result(aarh_session* e, uint32_t* out_tokens, int32_t out_cap, 
         if (out_tokens)
             for (int i = 0; i < n && i < out_cap; i++) out_tokens[(size_t)b * out_cap + i] = e->out[b][i];
         int fin = e->finish[b];
-        if (n == e->available && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
+        if (e->live[b] && n == e->available[b] && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
         if (finish_reason) finish_reason[b] = fin;
         if (stats) {
             stats[b] = e->stats[b];

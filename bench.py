@@ -191,6 +191,69 @@ def run_c4(args):
     return res
 
 
+def run_serve(args):
+    """Continuous batching with speculative rounds (the serving worker's loop,
+    serve/src/batching.rs:324-445, with decode_sessions replaced by MTP rounds) on the C4
+    model: 8 rows, a stream of 24 greedy requests with ragged prompts (64-512 tokens) and
+    token budgets (64-192), all queued at the start (a loaded server).  Requests join
+    free rows between rounds (prefill in 128-token chunks, the reference's
+    prefill_chunk_size) and leave when done.  Committed tokens / wall time of the whole
+    stream, admission prefills included; the stream runs once untimed first so that the
+    forward graphs of its shapes are captured (a warm server)."""
+    import aarambh_hip as A
+
+    cfg = A.ModelConfig(**C4, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    cap, nreq = 8, 24
+    m = A.HipModel(cfg, max_batch=cap, max_rows=128)
+    m.init_synthetic(seed=0, std=0.02)
+    if args.no_graphs:
+        m.set_graphs(False)
+    eng = A.MtpSpeculativeEngine(m, A.SpeculativeConfig(K_ROWS))
+    rng = np.random.default_rng(5)
+    reqs = [A.GenerationRequest(rng.integers(1, C4["vocab_size"], int(rng.integers(64, 513))).astype(np.uint32),
+                                int(rng.integers(64, 193)), seed=i) for i in range(nreq)]
+
+    def stream():
+        bat = A.SpeculativeBatcher(eng, A.BatcherConfig(max_batch_size=cap, queue_capacity=nreq),
+                                   A.Sampler.greedy_sampler())
+        for r in reqs:
+            bat.submit(r)
+        steps = 0
+        events = []
+        m.sync()
+        t = time.perf_counter()
+        while bat.pending():
+            events += bat.step()
+            steps += 1
+        m.sync()
+        t = time.perf_counter() - t
+        bat.close()
+        done = [e[2] for e in events if e[0] == "completed"]
+        assert len(done) == nreq, [e for e in events if e[0] == "failed"]
+        return t, steps, done
+
+    stream()
+    t, steps, done = stream()
+    toks = sum(len(o.token_ids) for o in done)
+    st = [o.speculative_stats for o in done]
+    rounds = sum(s.rounds for s in st)
+    m.close()
+    res = {
+        "tokens_per_s": toks / t,
+        "requests_per_s": nreq / t,
+        "wall_s": t,
+        "tokens": toks,
+        "prompt_tokens": int(sum(len(r.prompt_ids) for r in reqs)),
+        "batcher_steps": steps,
+        "mean_rows_per_round": rounds / max(steps, 1),
+        "acceptance_rate": float(np.mean([s.acceptance_rate() for s in st])),
+        "tokens_per_request_round": toks / max(rounds, 1),
+    }
+    print(f"# serve: {res['tokens_per_s']:.1f} tok/s over {nreq} requests in {t:.2f}s, "
+          f"{res['mean_rows_per_round']:.2f} rows per round", file=sys.stderr, flush=True)
+    return res
+
+
 def run_c2(args):
     """benchmark config 2: the standalone fused acceptance kernel, 32 sequences x k = 4
     draft positions x vocab 32000, target logits N(0, 3^2), draft = target + N(0, 1),
@@ -462,9 +525,11 @@ def main():
     ap.add_argument("--verify-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the config-2 and config-3 measurements")
-    ap.add_argument("--workload", choices=["c4", "c5", "c2", "c3"], default="c4",
-                    help="c4: the headline metric (default, with c2 / c3 beside it); c5: the MLA + MoE verify "
-                         "step; c2 / c3: only that measurement (profiling)")
+    ap.add_argument("--workload", choices=["c4", "c5", "c2", "c3", "serve"], default="c4",
+                    help="c4: the headline metric (default, with c2 / c3 / serve beside it); c5: the MLA + MoE "
+                         "verify step; c2 / c3 / serve: only that measurement (profiling)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="serve workload: launch every forward directly instead of replaying captured graphs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (counter calibration for rocprof --pmc)")
     ap.add_argument("--probe-memory", action="store_true",
@@ -502,11 +567,15 @@ def main():
     if args.workload == "c3":
         print(json.dumps({"c3_verify": {str(b): v for b, v in run_c3(args).items()}}))
         return
+    if args.workload == "serve":
+        print(json.dumps({"serve_continuous": run_serve(args)}))
+        return
     res = run_c4(args)
-    c2 = c3 = None
+    c2 = c3 = serve = None
     if not args.no_extra:
         c2 = run_c2(args)
         c3 = run_c3(args)
+        serve = run_serve(args)
     bmain = max(args.batches)
     main_r = res[bmain]
     b1 = res.get(1, main_r)
@@ -572,6 +641,7 @@ def main():
         "c2_acceptance": c2,
         "c3_verify": {str(b): {k: v[k] for k in ("ms_wall", "alg_bytes", "hbm_gbs", "hbm_frac")}
                       for b, v in c3.items()} if c3 else None,
+        "serve_continuous": serve,
         "cpu_baseline": cpu,
         "detail": {"c4": {str(b): r for b, r in res.items()},
                    "c3": {str(b): v for b, v in c3.items()} if c3 else None},

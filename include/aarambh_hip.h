@@ -212,6 +212,27 @@ int aarh_session_rng_offsets(aarh_session *session, uint64_t *out);
 int aarh_session_set_rng_offsets(aarh_session *session, const uint64_t *offsets);
 void aarh_session_end(aarh_session *session);
 
+/* Continuous batching of speculative requests: the serving worker's loop
+   (serve/src/batching.rs:324-445: admit while active < max_batch_size, advance, drop
+   finished or cancelled requests, then one batched decode) with its batched decode
+   (InferenceEngine::decode_sessions, inference/src/engine.rs:323-355) replaced by MTP
+   speculative rounds.  open: a session of `capacity` rows (<= max_batch), all free.
+   admit: a free row takes a request (prompt of its own length, its own token budget
+   and sampler seed): prepare_session_with_chunk_size (engine.rs:271-317) prefills the
+   prompt from position 0 of the row's KV slot in forwards of at most prefill_chunk
+   tokens; errors as there (SHAPE: prompt_len >= max_seq_len; CONFIG: chunk 0).
+   aarh_session_step then runs rounds over every generating row; aarh_session_result /
+   _candidates report every row (free rows: length 0).  retire: the row's request
+   leaves (completed or cancelled) and the row and its slot are free again.
+   rows: per row 0 = free, 1 = generating, 2 = finished (result ready, not retired).
+   Requests share the session's sampler settings (temperature, top-k, top-p). */
+int aarh_session_open(aarh_ctx *ctx, int capacity, int num_draft_tokens, const aarh_sampler *sampler,
+                      aarh_session **out);
+int aarh_session_admit(aarh_session *session, int row, const uint32_t *prompt, int prompt_len,
+                       int max_new_tokens, uint64_t seed, int prefill_chunk);
+int aarh_session_retire(aarh_session *session, int row);
+int aarh_session_rows(aarh_session *session, int32_t *state);
+
 /* --- external-draft engine (SpeculativeEngine::generate_with_callback,
    inference/src/speculative.rs:175-516; constructor checks :101-122) ---
    target and draft are contexts of two models with the same vocabulary on one device;
