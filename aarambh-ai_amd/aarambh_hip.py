@@ -753,11 +753,13 @@ class SpeculativeBatcher:
     step() returns the events of the iteration in that order: ("delta", id, token_ids),
     ("completed", id, GenerationOutput), ("failed", id, message)."""
 
-    def __init__(self, engine: MtpSpeculativeEngine, config: BatcherConfig, sampler: Sampler):
+    def __init__(self, engine: MtpSpeculativeEngine, config: BatcherConfig, sampler: Sampler, session=None):
         if config.max_batch_size == 0 or config.queue_capacity == 0 or config.prefill_chunk_size == 0:
             raise ConfigError("batch size and queue capacity must be greater than zero")
         self.config = config
-        self.session = ContinuousSession(engine, config.max_batch_size, sampler)
+        # `session`: an object with ContinuousSession's methods (admit, retire, rows, step,
+        # results, close) to drive instead of a new device session
+        self.session = session if session is not None else ContinuousSession(engine, config.max_batch_size, sampler)
         self.queue = collections.deque()
         self.active = {}  # row -> [request id, tokens reported]
         self.cancelled = set()
