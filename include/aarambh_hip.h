@@ -225,7 +225,9 @@ void aarh_session_end(aarh_session *session);
    _candidates report every row (free rows: length 0).  retire: the row's request
    leaves (completed or cancelled) and the row and its slot are free again.
    rows: per row 0 = free, 1 = generating, 2 = finished (result ready, not retired).
-   Requests share the session's sampler settings (temperature, top-k, top-p). */
+   Requests share the session's sampler settings (temperature, top-k, top-p).  Row b
+   uses KV slot b: the session owns slots 0..capacity-1, and a free row's slot keeps
+   no cache (rounds write padding rows at its position 0). */
 int aarh_session_open(aarh_ctx *ctx, int capacity, int num_draft_tokens, const aarh_sampler *sampler,
                       aarh_session **out);
 int aarh_session_admit(aarh_session *session, int row, const uint32_t *prompt, int prompt_len,
