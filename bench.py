@@ -314,14 +314,17 @@ def run_c3(args):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_hbm_traffic.txt")
+TRAFFIC_PROFILE_B32 = os.path.join(ROOT, "profiles", "verify_c4_b32_hbm_traffic.txt")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the INT4 GEMV from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE runs of this script, scaled by a plain-copy calibration)."""
+def measured_traffic(key="traffic_bytes_per_launch", path=None):
+    """HBM bytes per launch of a kernel class from a committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE runs of this script, scaled by a plain-copy calibration):
+    the INT4 GEMV and the decode attention of the batch-1 verify, the many-row INT4 GEMM
+    of the batch-32 verify."""
     try:
-        for line in open(TRAFFIC_PROFILE):
-            if line.startswith("traffic_bytes_per_launch"):
+        for line in open(path or TRAFFIC_PROFILE):
+            if line.startswith(key + " "):
                 return float(line.split("=")[1])
     except OSError:
         pass
@@ -596,7 +599,8 @@ def main():
     roof_att = {
         "kernel": "attn_mfma_kernel<INT8> (decode attention of the batch-1 verify step, 4096-token INT8 cache)",
         "bound": "hbm", "achieved": round(a1["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(a1["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(a1["avg_us"], 3),
+        "frac": round(a1["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("attention_traffic_bytes_per_launch"),
+        "avg_launch_us": round(a1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(a1["alg_bytes_per_step"] / C4["n_layers"]),
     }
     roof_gemm = None
@@ -606,7 +610,8 @@ def main():
             "kernel": "gemm_kernel<INT4,*> (INT4 projections of the batch-32 verify step, M = 128 rows; useful "
                       "FLOPs 2*M*N*K, the fp16 hi + lo activation split issues twice as many)",
             "bound": "mfma", "achieved": round(gm["useful_tflops"], 1), "peak": MFMA_F16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(gm["useful_tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(gm["useful_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "traffic": measured_traffic("gemm_traffic_bytes_per_launch", TRAFFIC_PROFILE_B32),
             "avg_launch_us": round(gm["avg_us"], 3),
         }
     cpu = None
