@@ -30,8 +30,8 @@ namespace aarh {
 static constexpr int ACC_THREADS = 512;
 static constexpr int ACC_WAVES = ACC_THREADS / WAVE;
 static constexpr int ACC_U = 8;              // logit loads a thread issues before consuming them
-static constexpr int ACC_CHUNK = 32768;      // floats of a row staged in LDS per scan step (128 KiB)
-static constexpr int CAND_CHUNK = 24576;     // the same for the candidate kernel (its key lists use 20 KiB)
+static constexpr int ACC_CHUNK = 8192;       // floats of a row per scan step; LDS holds two (64 KiB)
+static constexpr int CAND_CHUNK = 8192;      // the same for the candidate kernel (its key lists use 20 KiB)
 static constexpr int TOPP_PAGE = 4096;       // top-p candidates sorted per page (64-bit keys)
 static constexpr int TOPP_LDS_FLOATS = TOPP_PAGE * 3;  // page keys (8 B) + their probabilities (4 B)
 
@@ -286,20 +286,43 @@ __device__ __forceinline__ uint64_t select_desc(const KF& kf, const float* row, 
 }
 
 // Exact sequential sum of f(a_j, b_j, j) >= 0 over j in [0, n) (a = r0[j], b = r1[j]
-// for NR = 2), with the inverse-CDF crossing for u >= 0: the workgroup writes LDS
-// chunks of `chunk` values and wave 0 scans them, carrying the running sum.
+// for NR = 2), with the inverse-CDF crossing for u >= 0.  The row goes through LDS in
+// chunks of `chunk` values, double buffered (buf holds 2 * chunk floats): every wave
+// writes chunk 0, then wave 0 scans chunk c, carrying the running sum, while the
+// other waves write chunk c + 1 into the other half.
 template <int NR, class F>
 __device__ __forceinline__ SeqScan block_seq_scan(const float* r0, const float* r1, int n, float u, const F& f, float* buf,
                                   int chunk, AccShared* sh) {
     const int tid = threadIdx.x, wid = tid >> 6;
     SeqScan st = seq_scan_init();
+    rows_foreach<NR>(r0, NR == 2 ? r1 : nullptr, min(chunk, n), [&](int i, float a, float b, bool valid) {
+        if (valid) buf[i] = f(a, b, i);
+    });
+    __syncthreads();
     for (int c0 = 0; c0 < n; c0 += chunk) {
         const int m = min(chunk, n - c0);
-        rows_foreach<NR>(r0 + c0, NR == 2 ? r1 + c0 : nullptr, m, [&](int i, float a, float b, bool valid) {
-            if (valid) buf[i] = f(a, b, c0 + i);
-        });
-        __syncthreads();
-        if (wid == 0) seq_scan_wave(buf, m, u, c0, st);
+        float* cur = buf + ((c0 / chunk) & 1) * chunk;
+        if (wid == 0) {
+            seq_scan_wave(cur, m, u, c0, st);
+        } else if (c0 + chunk < n) {
+            const int c1 = c0 + chunk, m1 = min(chunk, n - c1);
+            float* nxt = buf + (((c0 / chunk) + 1) & 1) * chunk;
+            constexpr int NT = ACC_THREADS - 64, U = 4;
+            for (int i0 = tid - 64; i0 < m1; i0 += U * NT) {
+                float va[U], vb[U];
+#pragma unroll
+                for (int q = 0; q < U; q++) {
+                    const int i = i0 + q * NT;
+                    va[q] = i < m1 ? r0[c1 + i] : 0.f;
+                    vb[q] = (NR == 2 && i < m1) ? r1[c1 + i] : 0.f;
+                }
+#pragma unroll
+                for (int q = 0; q < U; q++) {
+                    const int i = i0 + q * NT;
+                    if (i < m1) nxt[i] = f(va[q], vb[q], c1 + i);
+                }
+            }
+        }
         __syncthreads();
     }
     if (tid == 0) sh->scan = st;
@@ -656,7 +679,7 @@ __global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
 
 static size_t accept_lds_bytes(int V, int greedy, int top_p_active) {
     if (greedy) return 0;
-    size_t f = (size_t)(V < ACC_CHUNK ? V : ACC_CHUNK);
+    size_t f = 2 * (size_t)(V < ACC_CHUNK ? V : ACC_CHUNK);
     if (top_p_active && f < (size_t)TOPP_LDS_FLOATS) f = TOPP_LDS_FLOATS;
     return f * sizeof(float);
 }
@@ -835,7 +858,7 @@ int launch_candidates(const CandArgs& a_in, hipStream_t stream) {
     CandArgs a = a_in;
     if (a.n < 1 || a.n > CAND_MAX || a.rows <= 0 || a.V <= 0) return 2;
     const bool topp = a.top_p > 0.0f && a.top_p < 1.0f;
-    size_t fl = a.greedy ? 0 : (size_t)(a.V < CAND_CHUNK ? a.V : CAND_CHUNK);
+    size_t fl = a.greedy ? 0 : 2 * (size_t)(a.V < CAND_CHUNK ? a.V : CAND_CHUNK);
     if (!a.greedy && topp && fl < (size_t)TOPP_LDS_FLOATS) fl = TOPP_LDS_FLOATS;
     const size_t lds = fl * sizeof(float);
     const size_t cap = MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX;
