@@ -245,6 +245,8 @@ __device__ __forceinline__ float readlane_f32(float x, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
 }
 
+// Elements added one at a time after the sum first becomes non-zero (see below).
+constexpr int SCAN_SCALAR = 64;
 __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, int gbase, SeqScan& st) {
     constexpr int E = 16;  // consecutive elements per lane in the binade fast path (1024 per step)
     const int lane = threadIdx.x & 63;
@@ -253,7 +255,33 @@ __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, in
     int cross = st.cross;
     float s_at = st.s_at, s_before = st.s_before;
     const bool want = u >= 0.0f;
+    int scal = 0;  // elements still to add one at a time
     while (pos < n) {
+        if (scal > 0) {
+            // Plain f32 adds in element order (64 loaded per round trip, four added per
+            // crossing check).  Used for the first SCAN_SCALAR elements after the sum
+            // becomes non-zero, where the sum still doubles every few elements and the
+            // binade windows would restart at almost every element.
+            const int cnt = min(64, min(scal, n - pos));
+            const float xv = lane < cnt ? v[pos + lane] : 0.0f;  // lanes past cnt add 0: no change
+            for (int i = 0; i < cnt; i += 4) {
+                const float x0 = readlane_f32(xv, i), x1 = readlane_f32(xv, i + 1);
+                const float x2 = readlane_f32(xv, i + 2), x3 = readlane_f32(xv, i + 3);
+                const float s0 = s + x0, s1 = s0 + x1, s2 = s1 + x2, s3 = s2 + x3;
+                if (want && cross < 0 && (u <= s0 || u <= s1 || u <= s2 || u <= s3)) {
+                    // the first of the four partial sums to reach u (a padding lane repeats
+                    // the last real sum, so the first one found is a real element)
+                    const int k = u <= s0 ? 0 : u <= s1 ? 1 : u <= s2 ? 2 : 3;
+                    cross = gbase + pos + i + k;
+                    s_at = k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3;
+                    s_before = k == 0 ? s : k == 1 ? s0 : k == 2 ? s1 : s2;
+                }
+                s = s3;
+            }
+            pos += cnt;
+            scal -= cnt;
+            continue;
+        }
         if (s == 0.0f) {
             // Zeros keep s at 0 (0 + 0 = 0); the first non-zero element x gives s = x.
             const int base = pos + 4 * lane;
@@ -283,6 +311,7 @@ __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, in
                 s_before = 0.0f;
             }
             pos = t + 1;
+            scal = SCAN_SCALAR;
             continue;
         }
         const uint32_t bits = __float_as_uint(s);
