@@ -158,3 +158,38 @@ def test_session_rows_admit_retire_validation():
     assert s.results()[1].token_ids == []
     s.close()
     hip.close()
+
+
+def test_continuous_batching_int4_int8kv_matches_oracle_per_round():
+    """The same loop over INT4 g128 weights, a bf16 LM head and an INT8 KV cache: every
+    completed request equals the oracle's stand-alone run up to its first round that
+    the oracle marks as a near-tie (top-2 logit gap below the INT4 logit tolerance),
+    and most rounds compare equal."""
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2, max_seq_len=160,
+              num_future_tokens=4, weight_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_INT8)
+    ref, hip = make_pair(seed=6, std=0.05, max_batch=4, max_rows=64, **kw)
+    g = R.sampler(greedy=True)
+    shapes = [(16, 30), (7, 12), (25, 40), (11, 22), (3, 35), (19, 18)]
+    reqs = [A.GenerationRequest(R.synth_tokens(6, 40 + i, p, 2048), n) for i, (p, n) in enumerate(shapes)]
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(4))
+    bat = A.SpeculativeBatcher(eng, A.BatcherConfig(max_batch_size=4, prefill_chunk_size=16),
+                               A.Sampler.greedy_sampler())
+    ids = [bat.submit(r) for r in reqs]
+    _, done, failed = _collect(bat.run())
+    assert not failed and set(done) == set(ids)
+    tol_l = 4e-3  # |logit error| of the INT4 path
+    same = total = 0
+    for rid, r in zip(ids, reqs):
+        w, fin, stats, _ = ref.mtp_generate(r.prompt_ids, r.max_new_tokens, 4, g)
+        rounds = ref.last_rounds
+        total += len(rounds)
+        d = first_divergent_round(rounds, w, [int(t) for t in done[rid].token_ids])
+        if d is None:
+            same += len(rounds)
+            assert done[rid].finish_reason == A.FINISH[fin]
+            continue
+        assert rounds[d]["logit_gap"] < tol_l, (rid, d, rounds[d])
+        same += d
+    assert total >= 20 and same >= 0.7 * total, (same, total)
+    bat.close()
+    hip.close()
