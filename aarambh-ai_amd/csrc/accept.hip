@@ -379,7 +379,7 @@ __device__ inline void block_sort_desc(unsigned long long* keys, int np2) {
 // filtered_probs (sampler.rs:226-278).  status 1: no finite logit survives or a
 // normaliser is not positive (the reference returns Err).  flags: the top-p
 // cumulative sum crossed top_p within 1e-6 (its decision may flip with an ulp).
-__device__ void row_filter(const float* row, int V, float T, int top_k, float top_p, float* buf, int chunk,
+__device__ __forceinline__ void row_filter(const float* row, int V, float T, int top_k, float top_p, float* buf, int chunk,
                            AccShared* sh, RowFilt& f, uint32_t& flags, int& status) {
     const int tid = threadIdx.x, wid = tid >> 6;
     f.T = T;
@@ -504,7 +504,10 @@ __device__ __forceinline__ int acc_chunk_floats(int V) { return V < ACC_CHUNK ? 
 // ---------------------------------------------------------------------------
 // Acceptance kernel: grid = B * (target_rows + K) workgroups.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(ACC_THREADS) accept_kernel(AcceptArgs a) {
+// Four waves per SIMD (at most 128 VGPRs, the rest spilled): two 8-wave workgroups
+// per CU, so C2's 288 rows run in one dispatch round (measured faster than one
+// workgroup per CU with no spills, also on the top-k / top-p path).
+__global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_eu(4, 4))) accept_kernel(AcceptArgs a) {
     extern __shared__ float lds[];
     __shared__ AccShared sh;
 
