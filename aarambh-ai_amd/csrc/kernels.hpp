@@ -264,7 +264,9 @@ int launch_argmax_rows(const float* x, long long ld, int rows, int V, int32_t* o
                        hipStream_t stream);
 int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n, hipStream_t stream);
 int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit, uint32_t eos,
-                           uint32_t* ids, int32_t* nprop, hipStream_t stream);
+                           uint32_t* ids, int32_t* nprop, const uint64_t* obase, uint64_t* offs, hipStream_t stream);
+int launch_sampled_props(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p, int nseq,
+                         const int32_t* limit, int32_t* pstat, hipStream_t stream);
 int launch_fill_f32(float* p, long long n, float v, hipStream_t stream);
 
 // ---------------------------------------------------------------------------

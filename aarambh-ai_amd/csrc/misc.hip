@@ -588,7 +588,8 @@ int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n
 // most limit[b] (0 for a finished sequence) -- the proposal loop of
 // mtp_speculative.rs:169-209 that stops after an EOS proposal (:201-203).
 __global__ void mtp_verify_rows_kernel(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit,
-                                       uint32_t eos, uint32_t* ids, int32_t* nprop) {
+                                       uint32_t eos, uint32_t* ids, int32_t* nprop, const uint64_t* obase,
+                                       uint64_t* offs) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nseq * Kr) return;
     const int b = i / Kr, r = i - b * Kr;
@@ -601,15 +602,42 @@ __global__ void mtp_verify_rows_kernel(const uint32_t* props, int K, int Kr, int
             if (props[(size_t)b * K + p] == eos) break;
         }
         nprop[b] = np;
+        // sampled rounds: the acceptance draws start after the np proposal draws
+        if (offs) offs[b] = obase[b] + (uint64_t)np;
     }
 }
 
 int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit, uint32_t eos,
-                           uint32_t* ids, int32_t* nprop, hipStream_t stream) {
-    if (nseq <= 0 || Kr <= 0 || K <= 0) return 2;
+                           uint32_t* ids, int32_t* nprop, const uint64_t* obase, uint64_t* offs, hipStream_t stream) {
+    if (nseq <= 0 || Kr <= 0 || K <= 0 || (offs && !obase)) return 2;
     (void)hipGetLastError();
     hipLaunchKernelGGL(mtp_verify_rows_kernel, dim3((nseq * Kr + 255) / 256), dim3(256), 0, stream, props, K, Kr,
-                       nseq, limit, eos, ids, nprop);
+                       nseq, limit, eos, ids, nprop, obase, offs);
+    return note_error(hipGetLastError()) ? 4 : 0;
+}
+
+// Sampled MTP proposal p (mtp_speculative.rs:169-209): the token the sampling kernel
+// drew for each sequence goes to props[b * K + p] (0 when its distribution was
+// invalid); a sequence whose proposal p counts (p < limit[b]) and whose distribution
+// was invalid is flagged in pstat[b] (set at p = 0, accumulated after), which the
+// host checks with the round's one read-back (sample_probabilities returns Err,
+// sampler.rs:142-152).
+__global__ void sampled_props_kernel(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p,
+                                     int nseq, const int32_t* limit, int32_t* pstat) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nseq) return;
+    const bool bad = status[b] != 0;
+    props[(size_t)b * K + p] = bad ? 0u : (uint32_t)tok[b];
+    const int32_t flag = (bad && p < limit[b]) ? 1 : 0;
+    pstat[b] = p == 0 ? flag : (pstat[b] | flag);
+}
+
+int launch_sampled_props(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p, int nseq,
+                         const int32_t* limit, int32_t* pstat, hipStream_t stream) {
+    if (nseq <= 0 || K <= 0 || p < 0 || p >= K) return 2;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(sampled_props_kernel, dim3((nseq + 255) / 256), dim3(256), 0, stream, tok, status, props, K, p,
+                       nseq, limit, pstat);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

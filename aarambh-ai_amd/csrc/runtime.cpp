@@ -77,6 +77,10 @@ struct aarh_ctx {
     aarh_model_config cfg{};
     int device = 0;
     hipStream_t stream = nullptr;
+    // second stream (default priority) for output metadata that no later kernel of the
+    // round reads: the top candidates run there beside the acceptance kernel
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     int hd = 0, QD = 0, KD = 0, F = 0, Fp = 0, H = 0, V = 0, nheads_mtp = 0;
     std::string err;
 
@@ -668,6 +672,12 @@ void aarh_destroy(aarh_ctx* c) {
         (void)hipEventDestroy(r.b);
     }
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    if (c->side) {
+        (void)hipStreamSynchronize(c->side);
+        (void)hipStreamDestroy(c->side);
+    }
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -776,6 +786,9 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     *out = c;
     if (hipSetDevice(device) != hipSuccess) return fail(c, AARH_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     HIPCHK(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    HIPCHK(c, hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));
+    HIPCHK(c, hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
+    HIPCHK(c, hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming));
     // the statically allocated acceptance scratch of this device (once per device)
     if (accept_static_init(device, c->stream))
         return fail(c, AARH_ERR_DEVICE, "static acceptance scratch set-up failed: %s", last_launch_error());
@@ -1473,8 +1486,29 @@ struct CandBuf {
         ids = nullptr;
         probs = nullptr;
     }
+    bool pending = false;  // launched on the side stream, not yet joined
+    // Sampled rows: on the side stream (after everything queued on the main stream so
+    // far), so the kernels the caller queues next on the main stream run beside it;
+    // join() makes the main stream wait for it.  Greedy rows (a one-pass argmax, about
+    // 10 us) and profiling runs stay on the main stream: the cross-stream waits cost
+    // more than the greedy kernel.
     int launch(aarh_ctx* c, const float* rows_base, int rows, int V, const aarh_sampler& s) {
-        return aarh_top_candidates(c, rows_base, rows, V, &s, CAND_MAX, ids, probs, nullptr);
+        const bool greedy = s.greedy || !(s.temperature > 1.1920929e-07f);
+        if (greedy || c->prof || !c->side)
+            return aarh_top_candidates(c, rows_base, rows, V, &s, CAND_MAX, ids, probs, nullptr);
+        HIPCHK(c, hipEventRecord(c->ev_fork, c->stream));
+        HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
+        int r = aarh_top_candidates(c, rows_base, rows, V, &s, CAND_MAX, ids, probs, c->side);
+        if (r) return r;
+        HIPCHK(c, hipEventRecord(c->ev_join, c->side));
+        pending = true;
+        return 0;
+    }
+    int join(aarh_ctx* c) {
+        if (!pending) return 0;
+        pending = false;
+        HIPCHK(c, hipStreamWaitEvent(c->stream, c->ev_join, 0));
+        return 0;
     }
     // after the stream has synchronised
     int fetch(aarh_ctx* c, int rows) {
@@ -1508,15 +1542,18 @@ struct aarh_session {
     aarh_sampler samp{};
     // device
     float *tgt = nullptr, *drf = nullptr, *anchor = nullptr, *vhid = nullptr;
-    // acceptance results, proposals and the proposal limits share one allocation (`pack`,
-    // int32 words: len, tok, draws, status [nseq each], props [nseq * K], limit [nseq])
-    // so that one read-back returns everything a round's host step needs
+    // acceptance results, proposals, the proposal limits and the sampled-proposal flags
+    // share one allocation (`pack`, int32 words: len, tok, draws, status [nseq each],
+    // props [nseq * K], limit [nseq], pstat [nseq]) so that one read-back returns
+    // everything a round's host step needs
     int32_t* pack = nullptr;
     uint32_t* props = nullptr;
     int32_t *acc_len = nullptr, *acc_tok = nullptr, *acc_draws = nullptr, *acc_status = nullptr, *nprop = nullptr;
     int32_t* limit = nullptr;
+    int32_t* pstat = nullptr;  // sampled proposals: invalid-distribution flags (in pack)
     uint32_t* acc_flags = nullptr;
     uint64_t *seeds = nullptr, *offs = nullptr;
+    uint64_t* offs_k = nullptr;  // sampled proposals: keystream word of head p for row b at [p][nseq]
     const float** src = nullptr;
     float** dst = nullptr;
     // host state, per row: `live` = the row holds a request (admitted and not retired);
@@ -1534,7 +1571,7 @@ struct aarh_session {
     ~aarh_session() {
         cand.release();
         for (void* p : {(void*)tgt, (void*)drf, (void*)anchor, (void*)vhid, (void*)pack, (void*)nprop,
-                        (void*)acc_flags, (void*)seeds, (void*)offs, (void*)src, (void*)dst})
+                        (void*)acc_flags, (void*)seeds, (void*)offs, (void*)offs_k, (void*)src, (void*)dst})
             if (p) (void)hipFree(p);
     }
 };
@@ -1602,6 +1639,17 @@ int session_round(aarh_session* e) {
         }
         if ((r = copy_rows_host_lists(e, s, d, V))) return r;
     }
+    // proposals counted this round (0 for finished rows); sampled rounds draw proposal p
+    // of row b at keystream word hoffs[b] + p
+    std::vector<int32_t> lim(nseq);
+    for (int b = 0; b < nseq; b++) lim[b] = e->finished[b] ? 0 : e->count[b];
+    if (!e->greedy) {
+        std::vector<uint64_t> o((size_t)Kr * nseq);
+        for (int p = 0; p < Kr; p++)
+            for (int b = 0; b < nseq; b++) o[(size_t)p * nseq + b] = e->hoffs[b] + p;
+        if ((r = stage_copy(c, e->offs_k, o.data(), o.size() * 8)) || (r = stage_copy(c, e->limit, lim.data(), nseq * 4)))
+            return r;
+    }
     for (int p = 0; p < Kr; p++) {
         if (p > 0) {
             if ((r = mtp_head_dev(c, p - 1, e->anchor, H, e->props, K, nseq, e->drf + (size_t)p * V, (long long)K * V)))
@@ -1611,24 +1659,13 @@ int session_round(aarh_session* e) {
             KCHK(c, launch_argmax_rows(e->drf + (size_t)p * V, (long long)K * V, nseq, V, (int32_t*)e->props + p, K,
                                        nullptr, c->stream));
         } else {
-            std::vector<uint64_t> o(nseq);
-            for (int b = 0; b < nseq; b++) o[b] = e->hoffs[b] + p;
-            HIPCHK(c, hipMemcpyAsync(e->offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
+            // sample_probabilities on the proposal distribution (sampler.rs:142-152), on the
+            // device; its validation (:314-335) is read back with the acceptance results
             if ((r = aarh_accept_sample(c, e->drf + (size_t)p * V, K, nullptr, nullptr, nullptr, nseq, 0, V, 1, &e->samp,
-                                        e->seeds, e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
-                                        e->acc_status, nullptr)))
+                                        e->seeds, e->offs_k + (size_t)p * nseq, nullptr, e->acc_len, e->acc_tok,
+                                        e->acc_flags, e->acc_draws, e->acc_status, nullptr)))
                 return r;
-            if ((r = sync_stream(c))) return r;
-            std::vector<int32_t> t(nseq), st(nseq);
-            HIPCHK(c, hipMemcpy(t.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
-            HIPCHK(c, hipMemcpy(st.data(), e->acc_status, nseq * 4, hipMemcpyDeviceToHost));
-            for (int b = 0; b < nseq; b++) {
-                // sample_probabilities validates the proposal distribution (sampler.rs:142-152, 314-335)
-                if (!e->finished[b] && e->count[b] > p && st[b] != 0)
-                    return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
-                e->hprops[(size_t)b * K + p] = (uint32_t)(st[b] ? 0 : t[b]);
-            }
-            HIPCHK(c, hipMemcpy(e->props, e->hprops.data(), (size_t)nseq * K * 4, hipMemcpyHostToDevice));
+            KCHK(c, launch_sampled_props(e->acc_tok, e->acc_status, e->props, K, p, nseq, e->limit, e->pstat, c->stream));
         }
     }
     // Proposal counts (the EOS cut) and their statistics, from the host copy of the proposals.
@@ -1649,15 +1686,9 @@ int session_round(aarh_session* e) {
             if (!e->greedy) e->hoffs[b] += np;
         }
     };
-    // Greedy proposals stay on the device: a kernel writes the verify rows and the counts,
-    // and the host reads the proposals back with the acceptance results (one wait per
-    // round).  Sampled proposals were read back while they were drawn.
-    const bool dev_rows = e->greedy;
-    if (!dev_rows) {
-        if ((r = sync_stream(c))) return r;
-        HIPCHK(c, hipMemcpy(e->hprops.data(), e->props, (size_t)nseq * K * 4, hipMemcpyDeviceToHost));
-        count_proposals();
-    }
+    // Proposals stay on the device: a kernel writes the verify rows, the counts and (sampled)
+    // the acceptance's keystream offsets, and the host reads the proposals back with the
+    // acceptance results (one wait per round).
     // ---- verify forward ----
     // Finished sequences ride along with padding rows written just past their committed
     // length (inside the PAD_SLACK positions every slot has beyond max_seq_len); their
@@ -1667,18 +1698,10 @@ int session_round(aarh_session* e) {
         std::vector<int32_t> off(nseq);
         for (int b = 0; b < nseq; b++) off[b] = e->live[b] ? e->base[b] : 0;
         int mk = 0;
-        if (dev_rows) {
-            std::vector<int32_t> lim(nseq);
-            for (int b = 0; b < nseq; b++) lim[b] = e->finished[b] ? 0 : e->count[b];
-            if ((r = stage_rows_meta(c, e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK, lim.data(), e->limit)))
-                return r;
-            KCHK(c, launch_mtp_verify_rows(e->props, K, Kr, nseq, e->limit, EOS_ID, c->d_ids, e->nprop, c->stream));
-        } else {
-            std::vector<uint32_t> ids((size_t)nseq * Kr);
-            for (int b = 0; b < nseq; b++)
-                for (int s2 = 0; s2 < Kr; s2++) ids[(size_t)b * Kr + s2] = e->hprops[(size_t)b * K + std::min(s2, K - 1)];
-            if ((r = stage_rows(c, ids.data(), e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK))) return r;
-        }
+        if ((r = stage_rows_meta(c, e->slots.data(), off.data(), nseq, Kr, &mk, PAD_SLACK, lim.data(), e->limit)))
+            return r;
+        KCHK(c, launch_mtp_verify_rows(e->props, K, Kr, nseq, e->limit, EOS_ID, c->d_ids, e->nprop,
+                                       e->greedy ? nullptr : e->offs_k, e->greedy ? nullptr : e->offs, c->stream));
         if ((r = forward_dev(c, c->d_ids, c->d_pos0, c->d_slot, nseq, Kr, mk, e->tgt + V, rm(Kr, (long long)(K + 1) * V, V),
                              e->vhid)))
             return r;
@@ -1690,29 +1713,29 @@ int session_round(aarh_session* e) {
     }
     // ---- acceptance (MTP round: no bonus) ----
     {
-        if ((r = stage_copy(c, e->offs, e->hoffs.data(), nseq * 8))) return r;
-        if (!dev_rows && (r = stage_copy(c, e->nprop, e->hnp.data(), nseq * 4))) return r;
+        // the top candidates (output metadata) run beside the acceptance kernel
+        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 0, &e->samp, e->seeds,
                                     e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
                                     nullptr)))
             return r;
-        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
-        if ((r = sync_stream(c))) return r;
+        if ((r = e->cand.join(c)) || (r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
-        // one read-back: lengths, tokens, draws, status, then the proposals (rows of the
-        // round; the sections are `cap` rows apart)
-        std::vector<int32_t> hp((size_t)cap * 4 + (size_t)nseq * K);
+        // one read-back: lengths, tokens, draws, status, the proposals, the limits and the
+        // sampled-proposal flags (sections `cap` rows apart)
+        std::vector<int32_t> hp((size_t)cap * (6 + K));
         HIPCHK(c, hipMemcpy(hp.data(), e->pack, hp.size() * 4, hipMemcpyDeviceToHost));
         for (int b = 0; b < nseq; b++) {
             e->hlen[b] = hp[b];
             e->htok[b] = hp[cap + b];
             e->hdraws[b] = hp[2 * cap + b];
             e->hstatus[b] = hp[3 * cap + b];
+            // sample_probabilities validates the proposal distribution (sampler.rs:142-152, 314-335)
+            if (!e->greedy && !e->finished[b] && hp[(size_t)(5 + K) * cap + b] != 0)
+                return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
         }
-        if (dev_rows) {
-            memcpy(e->hprops.data(), hp.data() + 4 * cap, (size_t)nseq * K * 4);
-            count_proposals();
-        }
+        memcpy(e->hprops.data(), hp.data() + 4 * cap, (size_t)nseq * K * 4);
+        count_proposals();
     }
     // ---- commit, rollback, replay ----
     std::vector<int> replay_seq, replay_len;
@@ -1855,17 +1878,19 @@ int session_create(aarh_ctx* c, int nseq, int num_draft_tokens, const aarh_sampl
     SA(drf, (size_t)nseq * K * V * 4);
     SA(anchor, (size_t)nseq * H * 4);
     SA(vhid, (size_t)nseq * K * H * 4);
-    SA(pack, ((size_t)nseq * (5 + K)) * 4);
+    SA(pack, ((size_t)nseq * (6 + K)) * 4);
     e->acc_len = e->pack;
     e->acc_tok = e->pack + nseq;
     e->acc_draws = e->pack + 2 * nseq;
     e->acc_status = e->pack + 3 * nseq;
     e->props = (uint32_t*)(e->pack + 4 * nseq);
     e->limit = e->pack + (size_t)nseq * (4 + K);
+    e->pstat = e->pack + (size_t)nseq * (5 + K);
     SA(nprop, nseq * 4);
     SA(acc_flags, nseq * 4);
     SA(seeds, nseq * 8);
     SA(offs, nseq * 8);
+    SA(offs_k, (size_t)K * nseq * 8);
     SA(src, (size_t)2 * g.max_batch * sizeof(void*));
     SA(dst, (size_t)2 * g.max_batch * sizeof(void*));
 #undef SA
@@ -2310,12 +2335,13 @@ int xsession_round(XSession* e) {
         }
         HIPCHK(c, hipMemcpyAsync(e->offs, o.data(), nseq * 8, hipMemcpyHostToDevice, c->stream));
         HIPCHK(c, hipMemcpyAsync(e->nprop, npv.data(), nseq * 4, hipMemcpyHostToDevice, c->stream));
+        // the top candidates (output metadata) run beside the acceptance kernel
+        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
         if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 1, &e->samp, e->seeds,
                                     e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
                                     e->acc_status, nullptr)))
             return r;
-        if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
-        if ((r = sync_stream(c))) return r;
+        if ((r = e->cand.join(c)) || (r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
         HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));
