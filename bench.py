@@ -10,8 +10,10 @@ INT8 KV cache holding a 4096-token synthetic context per sequence.
 A "step" is one speculative round of the MTP engine (mtp_speculative.rs:161-322)
 for every sequence of the batch: 3 MTP-head forwards, one K=4-row verify
 forward over the 4096-token cache, fused acceptance, replay on rejection.
-`value` = committed tokens / wall time of the timed rounds at batch 32 (inputs
-and KV resident in HBM); batches 1 and 8 are reported beside it.  The verify
+`value` = committed tokens / wall time of the timed greedy rounds at batch 32
+(inputs and KV resident in HBM); batches 1 and 8 are reported beside it, and the
+same rounds with the reference CLI's sampler (T 0.7, top-k 50, top-p 0.9) in
+`per_batch_sampled_cli`.  The verify
 step (K = 4 rows at offset 4096, repeated) is timed separately with per-kernel
 HIP events at dispatch level: the INT4 GEMV gives `roofline` (batch 1, HBM), the
 decode attention `roofline_attention` (batch 1, HBM) and the many-row GEMM
@@ -152,6 +154,24 @@ def run_c4(args):
         stats_all = [r.speculative_stats for r in after]
         sess.close()
         rounds = sum(s.rounds for s in stats_all)
+        # the same rounds with the reference CLI's sampler (T 0.7, top-k 50, top-p 0.9,
+        # infer.rs:72-77), one seed per sequence
+        for b in range(B):
+            m.kv_fill_synthetic(b, CTX, seed=1 + b)
+        ssess = eng.session(prompts, max_new, A.Sampler.top_k_top_p(0.7, top_k=50, top_p=0.9), cached_len=CTX,
+                            seeds=np.arange(B, dtype=np.uint64))
+        ssess.step(args.warmup)
+        st0 = sum(len(r.token_ids) for r in ssess.result())
+        m.sync()
+        tss = time.perf_counter()
+        ssess.step(args.steps)
+        m.sync()
+        tss = time.perf_counter() - tss
+        sres = ssess.result()
+        ssess.close()
+        sampled = {"tokens_per_s": (sum(len(r.token_ids) for r in sres) - st0) / tss,
+                   "ms_per_step": tss * 1000.0 / args.steps,
+                   "acceptance_rate": float(np.mean([r.speculative_stats.acceptance_rate() for r in sres]))}
         int4 = [prof[k] for k in INT4_CLASSES]
         ms4 = sum(v["ms"] for v in int4)
         by4 = sum(v["bytes"] for v in int4)
@@ -174,6 +194,7 @@ def run_c4(args):
                 "kernels": kernels_summary(prof, n_verify),
             },
             "stats_seq0": stats_all[0].__dict__,
+            "sampled_cli": sampled,
             "int4_proj": {"ms_per_step": ms4 / n_verify, "alg_bytes": by4, "launches": n4,
                           "avg_us": ms4 * 1000.0 / max(n4, 1), "avg_bytes": by4 / max(n4, 1),
                           "gbs": by4 / (ms4 * 1e-3) / 1e9 if ms4 else 0.0,
@@ -186,7 +207,8 @@ def run_c4(args):
         print(f"# B={B}: {res[B]['tokens_per_s']:.1f} tok/s, round {res[B]['ms_per_step']:.3f} ms, verify "
               f"{tv * 1000:.3f} ms ({res[B]['verify']['hbm_gbs']:.0f} GB/s), int4 proj "
               f"{res[B]['int4_proj']['gbs']:.0f} GB/s / {res[B]['int4_proj']['useful_tflops']:.0f} TF, attention "
-              f"{res[B]['attention']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+              f"{res[B]['attention']['gbs']:.0f} GB/s; sampled (T 0.7, top-k 50, top-p 0.9) "
+              f"{sampled['tokens_per_s']:.1f} tok/s, round {sampled['ms_per_step']:.3f} ms", file=sys.stderr, flush=True)
     m.close()
     return res
 
@@ -638,6 +660,7 @@ def main():
                    "batch": bmain, "verify_rows_per_seq": K_ROWS, "context": CTX},
         "per_batch": {str(b): {k: r[k] for k in ("tokens_per_s", "ms_per_step", "acceptance_rate",
                                                  "tokens_per_round")} for b, r in res.items()},
+        "per_batch_sampled_cli": {str(b): r["sampled_cli"] for b, r in res.items()},
         "verify_step": {str(b): {k: r["verify"][k] for k in ("ms_wall", "ms_kernels", "alg_bytes", "hbm_gbs",
                                                                "hbm_frac")} for b, r in res.items()},
         "roofline": roof,
