@@ -622,27 +622,60 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
     const float* RS = PHASE == 1 ? a.gu_rs : a.dn_rs;
     const size_t tile0 = (size_t)e * ntiles;
 
+    // ---- weight words of one step (NTB tiles x this wave's groups), three steps in flight.
+    //      Every load is unconditional: a step past the end re-reads the last step and a
+    //      group past G re-reads group G - 1 (in bounds, results unused), so the compiler
+    //      counts the loads in flight instead of waiting for all of them before each step.
+    typedef uint32_t WStep[NTB][NGW][LW];
+    typedef uint32_t ZStep[NTB][NGW];
+    WStep w0, w1, w2;
+    ZStep z0, z1, z2;
+    auto load_step = [&](int st, WStep& wv, ZStep& zv) __attribute__((always_inline)) {
+        const int stc = min(st, nsteps - 1);
+#pragma unroll
+        for (int j = 0; j < NTB; j++) {
+            const int nt = min(stc * NTB + j, ntiles - 1);
+#pragma unroll
+            for (int gi = 0; gi < NGW; gi++) {
+                const int g = min(wid + NW * gi, G - 1);
+                const size_t tile = (tile0 + nt) * G + g;
+#pragma unroll
+                for (int q = 0; q < LW / 4; q++) {
+                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + tile_byte(lane, 16 * q));
+                    wv[j][gi][4 * q] = w4.x;
+                    wv[j][gi][4 * q + 1] = w4.y;
+                    wv[j][gi][4 * q + 2] = w4.z;
+                    wv[j][gi][4 * q + 3] = w4.w;
+                }
+                if (FMT == WF_INT4) zv[j][gi] = SZ[tile * 16 + lr];
+            }
+        }
+    };
+    // the chunk row's source index first, then the first two steps, then the activation
+    // gather: the weights' round trip overlaps the gather
+    const bool rv = lr < nr;
+    const int ai = base_a + (rv ? lr : 0);
+    const float* rowp = PHASE == 1 ? a.xn + (size_t)a.arow[ai] * a.H : a.h + (size_t)ai * a.D;
+    const int B = a.bpe;
+    load_step(slice, w0, z0);
+    load_step(slice + B, w1, z1);
+
     // ---- activations of the chunk: A row lr = assignment base_a + lr ----
     half8_t ah[NGW][4], al[NGW][4];
     {
-        const bool rv = lr < nr;
-        const int ai = base_a + (rv ? lr : 0);
-        const float* rowp = PHASE == 1 ? a.xn + (size_t)a.arow[ai] * a.H : a.h + (size_t)ai * a.D;
 #pragma unroll
         for (int gi = 0; gi < NGW; gi++) {
             const int g = wid + NW * gi;
+            const bool use = g < G && rv;
+            const int gc = min(g, G - 1);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                float v[8];
-                if (g < G && rv) {
-                    const float4 v0 = *(const float4*)(rowp + g * 128 + 32 * lg + 8 * t);
-                    const float4 v1 = *(const float4*)(rowp + g * 128 + 32 * lg + 8 * t + 4);
-                    v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
-                    v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
-                } else {
+                // unconditional loads (clamped group, row 0 of the chunk for padding rows)
+                const float4 v0 = *(const float4*)(rowp + gc * 128 + 32 * lg + 8 * t);
+                const float4 v1 = *(const float4*)(rowp + gc * 128 + 32 * lg + 8 * t + 4);
+                float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-                    for (int j = 0; j < 8; j++) v[j] = 0.f;
-                }
+                for (int j = 0; j < 8; j++) v[j] = use ? v[j] : 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float x = v[frag_elem(FMT, j)];
@@ -660,33 +693,6 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
         }
     }
 
-    // ---- weight words of one step (NTB tiles x this wave's groups), three steps in flight ----
-    typedef uint32_t WStep[NTB][NGW][LW];
-    typedef uint32_t ZStep[NTB][NGW];
-    WStep w0, w1, w2;
-    ZStep z0, z1, z2;
-    auto load_step = [&](int st, WStep& wv, ZStep& zv) {
-        if (st >= nsteps) return;
-#pragma unroll
-        for (int j = 0; j < NTB; j++) {
-            const int nt = min(st * NTB + j, ntiles - 1);
-#pragma unroll
-            for (int gi = 0; gi < NGW; gi++) {
-                const int g = wid + NW * gi;
-                if (g >= G) continue;
-                const size_t tile = (tile0 + nt) * G + g;
-#pragma unroll
-                for (int q = 0; q < LW / 4; q++) {
-                    const uint4 w4 = *(const uint4*)(W + tile * T::TILE_BYTES + tile_byte(lane, 16 * q));
-                    wv[j][gi][4 * q] = w4.x;
-                    wv[j][gi][4 * q + 1] = w4.y;
-                    wv[j][gi][4 * q + 2] = w4.z;
-                    wv[j][gi][4 * q + 3] = w4.w;
-                }
-                if (FMT == WF_INT4) zv[j][gi] = SZ[tile * 16 + lr];
-            }
-        }
-    };
     int buf = 0;
     auto compute_step = [&](int st, const WStep& wv, const ZStep& zv) {
 #pragma unroll
@@ -760,9 +766,6 @@ __global__ void __launch_bounds__(512) moe_ffn_kernel(MoeArgs a) {
         }
         buf ^= 1;
     };
-    const int B = a.bpe;
-    load_step(slice, w0, z0);
-    load_step(slice + B, w1, z1);
     for (int st = slice; st < nsteps; st += 3 * B) {
         load_step(st + 2 * B, w2, z2);
         compute_step(st, w0, z0);
