@@ -469,11 +469,13 @@ def run_c5(args):
             "kernels": {k: {"ms_per_step": v["ms"] / args.steps, "launches_per_step": v["launches"] / args.steps,
                             "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] > 0 else 0.0}
                         for k, v in prof.items() if v["launches"]},
+            # expert weight bytes over the MoE block's profiled time (eager launches with events;
+            # includes routing and combine, so it reads below the expert kernels' own rate)
             "moe_ffn_gbs": (prof["gemv_gateup"]["bytes"] + prof["gemv_down"]["bytes"]) / args.steps / (ffn_ms * 1e-3)
             / 1e9 if ffn_ms else 0.0,
         }
         print(f"# c5 B={B}: verify {t * 1e3:.3f} ms, {res[B]['rows_per_s']:.0f} rows/s, experts/layer "
-              f"{used / L:.1f}, moe ffn {res[B]['moe_ffn_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+              f"{used / L:.1f}, moe block (route + experts + combine) {res[B]['moe_ffn_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     m.close()
     bmain = max(args.batches)
     r = res[bmain]
