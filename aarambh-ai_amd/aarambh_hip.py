@@ -803,7 +803,17 @@ class SpeculativeBatcher:
                 del self.active[row]
         if not self.active:
             return events
-        self.session.step(rounds)
+        try:
+            self.session.step(rounds)
+        except AarambhError as exc:
+            # a failed batched decode fails every active request and frees its row; the
+            # batcher keeps serving the queue (run_worker, batching.rs:441-450)
+            msg = str(exc)
+            for row in sorted(self.active):
+                events.append(("failed", self.active[row][0], msg))
+                self.session.retire(row)
+            self.active.clear()
+            return events
         state = self.session.rows()
         done = [row for row in self.active if state[row] == ContinuousSession.FINISHED]
         outs = self.session.results(candidates=bool(done))

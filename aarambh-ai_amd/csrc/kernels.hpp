@@ -266,7 +266,7 @@ int launch_copy_rows(const float* const* src, float* const* dst, int rows, int n
 int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const int32_t* limit, uint32_t eos,
                            uint32_t* ids, int32_t* nprop, const uint64_t* obase, uint64_t* offs, hipStream_t stream);
 int launch_sampled_props(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p, int nseq,
-                         const int32_t* limit, int32_t* pstat, hipStream_t stream);
+                         const int32_t* limit, uint32_t eos, int32_t* pstat, hipStream_t stream);
 int launch_fill_f32(float* p, long long n, float v, hipStream_t stream);
 
 // ---------------------------------------------------------------------------

@@ -493,13 +493,13 @@ void build_slots(Ctx* c) {
         LatLayer* b = &c->layers[l];
         const std::string p = "blocks." + std::to_string(l) + ".";
         add(p + "norm1.weight", 1, H, AARH_T_NORM, L_NORM, l, -1, &b->norm1);
-        add(p + "attn.q_proj.weight", c->QW, H, AARH_T_LINEAR, L_QP, l, -1, nullptr);
-        add(p + "attn.kv_a_proj.weight", c->lat, H, AARH_T_LINEAR, L_KVA, l, -1, nullptr);
-        add(p + "attn.kv_a_norm.weight", 1, c->lat, AARH_T_NORM, L_NORM, l, -1, &b->kvn);
-        add(p + "attn.up_k.weight", (int64_t)c->nh * c->nope, c->lat, AARH_T_LINEAR, L_UPK, l, -1, nullptr);
-        add(p + "attn.up_v.weight", (int64_t)c->nh * c->vd, c->lat, AARH_T_LINEAR, L_UPV, l, -1, nullptr);
-        add(p + "attn.k_rope_proj.weight", c->rd, H, AARH_T_LINEAR, L_KRP, l, -1, nullptr);
-        add(p + "attn.o_proj.weight", H, c->OD, AARH_T_LINEAR, L_OP, l, -1, nullptr);
+        add(p + "mla.q_proj.weight", c->QW, H, AARH_T_LINEAR, L_QP, l, -1, nullptr);
+        add(p + "mla.kv_a_proj.weight", c->lat, H, AARH_T_LINEAR, L_KVA, l, -1, nullptr);
+        add(p + "mla.kv_a_norm.weight", 1, c->lat, AARH_T_NORM, L_NORM, l, -1, &b->kvn);
+        add(p + "mla.up_k.weight", (int64_t)c->nh * c->nope, c->lat, AARH_T_LINEAR, L_UPK, l, -1, nullptr);
+        add(p + "mla.up_v.weight", (int64_t)c->nh * c->vd, c->lat, AARH_T_LINEAR, L_UPV, l, -1, nullptr);
+        add(p + "mla.k_rope_proj.weight", c->rd, H, AARH_T_LINEAR, L_KRP, l, -1, nullptr);
+        add(p + "mla.o_proj.weight", H, c->OD, AARH_T_LINEAR, L_OP, l, -1, nullptr);
         add(p + "norm2.weight", 1, H, AARH_T_NORM, L_NORM, l, -1, &b->norm2);
         add(p + "ffn.router.weight", c->E, H, AARH_T_LINEAR, L_ROUTER, l, -1, nullptr);
         for (int e = 0; e < c->E + c->NS; e++) {

@@ -618,26 +618,29 @@ int launch_mtp_verify_rows(const uint32_t* props, int K, int Kr, int nseq, const
 
 // Sampled MTP proposal p (mtp_speculative.rs:169-209): the token the sampling kernel
 // drew for each sequence goes to props[b * K + p] (0 when its distribution was
-// invalid); a sequence whose proposal p counts (p < limit[b]) and whose distribution
-// was invalid is flagged in pstat[b] (set at p = 0, accumulated after), which the
-// host checks with the round's one read-back (sample_probabilities returns Err,
-// sampler.rs:142-152).
+// invalid).  A sequence whose proposal p counts -- p < limit[b] and no earlier
+// proposal of the round is the end-of-sequence id, after which the reference stops
+// proposing (:196-203) -- and whose distribution was invalid is flagged in pstat[b]
+// (set at p = 0, accumulated after), which the host checks with the round's one
+// read-back (sample_probabilities returns Err, sampler.rs:142-152).
 __global__ void sampled_props_kernel(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p,
-                                     int nseq, const int32_t* limit, int32_t* pstat) {
+                                     int nseq, const int32_t* limit, uint32_t eos, int32_t* pstat) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nseq) return;
     const bool bad = status[b] != 0;
     props[(size_t)b * K + p] = bad ? 0u : (uint32_t)tok[b];
-    const int32_t flag = (bad && p < limit[b]) ? 1 : 0;
+    bool after_eos = false;
+    for (int j = 0; j < p; j++) after_eos |= props[(size_t)b * K + j] == eos;
+    const int32_t flag = (bad && p < limit[b] && !after_eos) ? 1 : 0;
     pstat[b] = p == 0 ? flag : (pstat[b] | flag);
 }
 
 int launch_sampled_props(const int32_t* tok, const int32_t* status, uint32_t* props, int K, int p, int nseq,
-                         const int32_t* limit, int32_t* pstat, hipStream_t stream) {
+                         const int32_t* limit, uint32_t eos, int32_t* pstat, hipStream_t stream) {
     if (nseq <= 0 || K <= 0 || p < 0 || p >= K) return 2;
     (void)hipGetLastError();
     hipLaunchKernelGGL(sampled_props_kernel, dim3((nseq + 255) / 256), dim3(256), 0, stream, tok, status, props, K, p,
-                       nseq, limit, pstat);
+                       nseq, limit, eos, pstat);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 

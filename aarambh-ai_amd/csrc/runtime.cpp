@@ -1665,7 +1665,8 @@ int session_round(aarh_session* e) {
                                         e->seeds, e->offs_k + (size_t)p * nseq, nullptr, e->acc_len, e->acc_tok,
                                         e->acc_flags, e->acc_draws, e->acc_status, nullptr)))
                 return r;
-            KCHK(c, launch_sampled_props(e->acc_tok, e->acc_status, e->props, K, p, nseq, e->limit, e->pstat, c->stream));
+            KCHK(c, launch_sampled_props(e->acc_tok, e->acc_status, e->props, K, p, nseq, e->limit, EOS_ID, e->pstat,
+                                         c->stream));
         }
     }
     // Proposal counts (the EOS cut) and their statistics, from the host copy of the proposals.
@@ -1715,11 +1716,12 @@ int session_round(aarh_session* e) {
     {
         // the top candidates (output metadata) run beside the acceptance kernel
         if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
-        if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 0, &e->samp, e->seeds,
-                                    e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
-                                    nullptr)))
-            return r;
-        if ((r = e->cand.join(c)) || (r = sync_stream(c))) return r;
+        r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 0, &e->samp, e->seeds,
+                               e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
+                               nullptr);
+        // join the side stream on every path: its kernel reads tgt, which later work rewrites
+        const int rj = e->cand.join(c);
+        if (r || (r = rj) || (r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
         // one read-back: lengths, tokens, draws, status, the proposals, the limits and the
         // sampled-proposal flags (sections `cap` rows apart)
@@ -2337,11 +2339,12 @@ int xsession_round(XSession* e) {
         HIPCHK(c, hipMemcpyAsync(e->nprop, npv.data(), nseq * 4, hipMemcpyHostToDevice, c->stream));
         // the top candidates (output metadata) run beside the acceptance kernel
         if ((r = e->cand.launch(c, e->tgt, nseq * (K + 1), V, e->samp))) return r;
-        if ((r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 1, &e->samp, e->seeds,
-                                    e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws,
-                                    e->acc_status, nullptr)))
-            return r;
-        if ((r = e->cand.join(c)) || (r = sync_stream(c))) return r;
+        r = aarh_accept_sample(c, e->tgt, K + 1, e->drf, e->props, e->nprop, nseq, K, V, 1, &e->samp, e->seeds,
+                               e->offs, nullptr, e->acc_len, e->acc_tok, e->acc_flags, e->acc_draws, e->acc_status,
+                               nullptr);
+        // join the side stream on every path: its kernel reads tgt, which later work rewrites
+        const int rj = e->cand.join(c);
+        if (r || (r = rj) || (r = sync_stream(c))) return r;
         if ((r = e->cand.fetch(c, nseq * (K + 1)))) return r;
         HIPCHK(c, hipMemcpy(e->hlen.data(), e->acc_len, nseq * 4, hipMemcpyDeviceToHost));
         HIPCHK(c, hipMemcpy(e->htok.data(), e->acc_tok, nseq * 4, hipMemcpyDeviceToHost));

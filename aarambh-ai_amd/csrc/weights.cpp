@@ -164,7 +164,7 @@ struct JParser {
             v.kind = JVal::NUL;
         } else {
             const char* s = p;
-            while (p < end && (strchr("+-0123456789.eE", *p) != nullptr)) p++;
+            while (p < end && *p != '\0' && strchr("+-0123456789.eE", *p) != nullptr) p++;
             if (p == s) return false;
             v.kind = JVal::NUM;
             v.str.assign(s, p);

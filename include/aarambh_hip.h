@@ -303,10 +303,11 @@ typedef struct {
     int32_t max_rows;       /* max rows (sequences x tokens) per forward, <= 256 */
 } aarh_lat_config;
 
-/* Context + weights (checkpoint names and order of the latent decoder: embedding,
-   per layer norm1, attn.{q_proj, kv_a_proj, kv_a_norm, up_k, up_v, k_rope_proj,
-   o_proj}, norm2, ffn.router, ffn.experts.{e}.{w_gate,w_up,w_down},
-   ffn.shared_experts.{s}.{...}, then final_norm). */
+/* Context + weights (checkpoint names and order of the latent decoder, as
+   AarambhModel::named_tensors writes them, model.rs:1053-1054, mla.rs:383-393,
+   model.rs:944-1000: embedding, per layer blocks.{l}.norm1, blocks.{l}.mla.{q_proj,
+   kv_a_proj, kv_a_norm, up_k, up_v, k_rope_proj, o_proj}, norm2, ffn.router,
+   ffn.experts.{e}.{w_gate,w_up,w_down}, ffn.shared_experts.{s}.{...}, then final_norm). */
 int aarh_lat_create(int device, const aarh_lat_config *cfg, aarh_lat_ctx **out);
 void aarh_lat_destroy(aarh_lat_ctx *ctx);
 const char *aarh_lat_last_error(const aarh_lat_ctx *ctx);

@@ -1871,13 +1871,13 @@ ref_lat *ref_lat_create(const ref_lat_config *c) {
     snprintf(nm, sizeof(nm), "blocks.%d.%s", l, suffix);                                           \
     set_info(&m->t[lat_id(m, l, which)], nm, r, cc, k);
         XT(X_NORM1, "norm1.weight", 1, H, REF_T_NORM)
-        XT(X_QP, "attn.q_proj.weight", h * (c->nope_dim + c->rope_dim), H, REF_T_LINEAR)
-        XT(X_KVA, "attn.kv_a_proj.weight", c->latent_dim, H, REF_T_LINEAR)
-        XT(X_KVN, "attn.kv_a_norm.weight", 1, c->latent_dim, REF_T_NORM)
-        XT(X_UPK, "attn.up_k.weight", h * c->nope_dim, c->latent_dim, REF_T_LINEAR)
-        XT(X_UPV, "attn.up_v.weight", h * c->v_dim, c->latent_dim, REF_T_LINEAR)
-        XT(X_KRP, "attn.k_rope_proj.weight", c->rope_dim, H, REF_T_LINEAR)
-        XT(X_OP, "attn.o_proj.weight", H, h * c->v_dim, REF_T_LINEAR)
+        XT(X_QP, "mla.q_proj.weight", h * (c->nope_dim + c->rope_dim), H, REF_T_LINEAR)
+        XT(X_KVA, "mla.kv_a_proj.weight", c->latent_dim, H, REF_T_LINEAR)
+        XT(X_KVN, "mla.kv_a_norm.weight", 1, c->latent_dim, REF_T_NORM)
+        XT(X_UPK, "mla.up_k.weight", h * c->nope_dim, c->latent_dim, REF_T_LINEAR)
+        XT(X_UPV, "mla.up_v.weight", h * c->v_dim, c->latent_dim, REF_T_LINEAR)
+        XT(X_KRP, "mla.k_rope_proj.weight", c->rope_dim, H, REF_T_LINEAR)
+        XT(X_OP, "mla.o_proj.weight", H, h * c->v_dim, REF_T_LINEAR)
         XT(X_NORM2, "norm2.weight", 1, H, REF_T_NORM)
         XT(X_ROUTER, "ffn.router.weight", c->n_experts, H, REF_T_LINEAR)
 #undef XT

@@ -81,12 +81,12 @@ def lat_block(W, pre, x, cfg, pos, absorbed=False):
     S, H = x.shape
     nh, nope, rd, lat, vd = cfg.n_heads, cfg.nope_dim, cfg.rope_dim, cfg.latent_dim, cfg.v_dim
     xn = rms(x, W[pre + "norm1.weight"], cfg.norm_eps)
-    q = (xn @ W[pre + "attn.q_proj.weight"].T).reshape(S, nh, nope + rd)
+    q = (xn @ W[pre + "mla.q_proj.weight"].T).reshape(S, nh, nope + rd)
     qn, qr = q[..., :nope], rope(q[..., nope:], pos, cfg.rope_theta)
-    c = rms(xn @ W[pre + "attn.kv_a_proj.weight"].T, W[pre + "attn.kv_a_norm.weight"], cfg.norm_eps)
-    kr = rope((xn @ W[pre + "attn.k_rope_proj.weight"].T)[:, None, :], pos, cfg.rope_theta)[:, 0]
-    upk = W[pre + "attn.up_k.weight"].reshape(nh, nope, lat)
-    upv = W[pre + "attn.up_v.weight"].reshape(nh, vd, lat)
+    c = rms(xn @ W[pre + "mla.kv_a_proj.weight"].T, W[pre + "mla.kv_a_norm.weight"], cfg.norm_eps)
+    kr = rope((xn @ W[pre + "mla.k_rope_proj.weight"].T)[:, None, :], pos, cfg.rope_theta)[:, 0]
+    upk = W[pre + "mla.up_k.weight"].reshape(nh, nope, lat)
+    upv = W[pre + "mla.up_v.weight"].reshape(nh, vd, lat)
     mask = np.tril(np.ones((S, S), bool))
     out = np.zeros((S, nh, vd))
     for h in range(nh):
@@ -100,7 +100,7 @@ def lat_block(W, pre, x, cfg, pos, absorbed=False):
         p = np.exp(sc - sc.max(-1, keepdims=True))
         p /= p.sum(-1, keepdims=True)
         out[:, h] = (p @ c) @ upv[h].T if absorbed else p @ (c @ upv[h].T)
-    x = x + out.reshape(S, nh * vd) @ W[pre + "attn.o_proj.weight"].T
+    x = x + out.reshape(S, nh * vd) @ W[pre + "mla.o_proj.weight"].T
     xn = rms(x, W[pre + "norm2.weight"], cfg.norm_eps)
     logits = xn @ W[pre + "ffn.router.weight"].T
     E, K = cfg.n_experts, cfg.top_k

@@ -150,3 +150,41 @@ def test_zero_budget_completes_at_admission():
     z = bat.submit(A.GenerationRequest([1, 2, 3], 0))
     d, done, _ = collect(bat.step())
     assert done[z].token_ids == [] and z not in d
+
+
+class FailingSession(ScriptedSession):
+    """A ScriptedSession whose step() raises on its `fail_at`-th call (a device error
+    or an invalid proposal distribution in the batched rounds)."""
+
+    def __init__(self, capacity, fail_at):
+        super().__init__(capacity)
+        self.calls = 0
+        self.fail_at = fail_at
+
+    def step(self, rounds=1):
+        self.calls += 1
+        if self.calls == self.fail_at:
+            raise A.ConfigError("proposal distribution is invalid (zero mass or does not sum to one)")
+        return super().step(rounds)
+
+
+def test_failed_decode_fails_every_active_request_and_keeps_serving():
+    """decode_sessions failing (batching.rs:441-450): every active request is answered
+    with a failure and leaves its row; queued requests are served afterwards."""
+    sess = FailingSession(2, fail_at=2)
+    bat = A.SpeculativeBatcher(None, A.BatcherConfig(max_batch_size=2, queue_capacity=8),
+                               A.Sampler.greedy_sampler(), session=sess)
+    a = bat.submit(A.GenerationRequest([1], 6, seed=1))
+    b = bat.submit(A.GenerationRequest([1], 6, seed=2))
+    c = bat.submit(A.GenerationRequest([1], 2, seed=3))
+    ev = bat.step()  # both rows commit two tokens each
+    ev2 = bat.step()  # the batched decode fails
+    d, done, failed = collect(ev2)
+    assert set(failed) == {a, b} and "proposal distribution" in failed[a] and not done and not d
+    assert not bat.active and ("retire", 0) in sess.log and ("retire", 1) in sess.log
+    assert sess.rows() == [A.ContinuousSession.FREE] * 2
+    ev3 = bat.run()  # the queued request still runs to completion in a freed row
+    d, done, failed = collect(ev + ev2 + ev3)
+    assert set(done) == {c} and done[c].token_ids == [3000, 3001]
+    assert d[a] == [1000, 1001] and d[b] == [2000, 2001]
+    assert not bat.active and not bat.queue

@@ -328,3 +328,56 @@ def test_external_draft_sampled_whole_run(sampler):
     assert total >= 20 and same >= 0.5 * total, (same, total)
     for m in (hip_t, hip_d):
         m.close()
+
+
+def _eos_then_nan_head_model(max_batch=1):
+    """Three-horizon f32 model whose EOS embedding row is scaled by 10 (EOS is a frequent
+    draw) and whose second MTP head has NaN norm weights (its logits are NaN, an invalid
+    sampling distribution)."""
+    kw = dict(vocab_size=512, hidden_dim=128, ffn_dim=256, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=96,
+              num_future_tokens=3)
+    ref, hip = make_pair(seed=21, max_batch=max_batch, **kw)
+    emb = ref.get(0).copy()
+    emb[0] *= 10.0
+    ref.set(0, emb)
+    hip.load_f32(0, emb)
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        if name.startswith("mtp.heads.1.") and kind == R.T_NORM:
+            ref.set(i, np.full(r * c, np.nan, np.float32))
+            hip.load_f32(i, np.full(r * c, np.nan, np.float32))
+    return ref, hip
+
+
+def test_sampled_mtp_no_error_after_eos_proposal():
+    """After an EOS proposal the reference stops proposing (mtp_speculative.rs:196-203),
+    so a later head's invalid distribution is never sampled and raises nothing.  The
+    device runs every head in lock-step; the runs where the oracle finishes without an
+    error (EOS proposed by target_next, or by the first head, before the NaN head) must
+    finish on the device with the same tokens, finish reason and statistics."""
+    ref, hip = _eos_then_nan_head_model()
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(3))
+    by_props = {1: 0, 2: 0}
+    checked = 0
+    for seed in range(300):
+        prompt = R.synth_tokens(21, seed % 7, 10, 512)
+        try:
+            want, fin, stats, _ = ref.mtp_generate(prompt, 12, 3, R.sampler(temperature=0.8), seed=seed)
+        except ValueError:
+            continue  # the NaN head's proposal counted: the reference errors too
+        rd = ref.last_rounds
+        if any(r["prob_margin"] < 2e-5 for r in rd):
+            continue
+        if by_props.get(stats["draft_tokens_proposed"], 9) >= 4:
+            continue
+        out = eng.generate_batch(prompt[None], 12, A.Sampler.top_k_top_p(0.8, seed=seed),
+                                 seeds=np.array([seed], np.uint64))[0]
+        assert [int(t) for t in out.token_ids] == [int(t) for t in want], seed
+        assert out.finish_reason == A.FINISH[fin] == "EosToken"
+        for k in ("rounds", "draft_tokens_proposed", "draft_tokens_accepted", "mtp_head_forwards"):
+            assert getattr(out.speculative_stats, k) == stats[k], (seed, k)
+        by_props[stats["draft_tokens_proposed"]] += 1
+        checked += 1
+        if min(by_props.values()) >= 4:
+            break
+    assert by_props[1] >= 2 and by_props[2] >= 1 and checked >= 4, by_props
+    hip.close()

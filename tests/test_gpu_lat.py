@@ -171,3 +171,47 @@ def test_lat_bench_shape_properties():
     c, _ = hip.forward_with_cache_output(ids[3:4], [T], slots=[3])
     assert rel_rows(c[0], a[3]).max() < TOL
     hip.close()
+
+
+def test_lat_c5_bench_shape_vs_oracle():
+    """The config-5 bench batch against the oracle: one C5-width layer (INT4 experts
+    and MLA projections, latent 512 + rope 64, 16 heads, 64 experts top-6 + 2 shared),
+    32 sequences x 5 verify rows over synthetic latent caches of about 4096 tokens.
+    At this shape the latent attention streams about 32 blocks per chunk (a few long
+    chunks per sequence) and the projections and experts take the many-row (160-row)
+    GEMM path.  Odd sequences hold ragged cache lengths, so their chunks end inside a
+    32-token block.  A final batch-1 forward covers the GEMV path at the same cache
+    length.  Every sequence without a router near-tie must match the oracle
+    (mla.rs:402-489, moe.rs:212-340) within 2e-3."""
+    kw = dict(vocab_size=32000, hidden_dim=2048, n_layers=1, n_heads=16, max_seq_len=4160, latent_dim=512,
+              rope_dim=64, nope_dim=128, v_dim=128, n_experts=64, top_k=6, expert_dim=1408, n_shared=2,
+              expert_format=A.W_INT4_G128, attn_format=A.W_INT4_G128, lm_head_format=1, kv_format=A.KV_F16)
+    B, S = 32, 5
+    print("lat c5 bench shape: building models", flush=True)
+    ref, hip = lat_pair(13, 0.02, B + 1, B * S, **kw)
+    lens = [4096 if b % 2 == 0 else 4096 - 3 - 13 * b for b in range(B)] + [4096]
+    assert any((t + S) % 32 for t in lens)
+    kvs = []
+    for b, t in enumerate(lens):
+        hip.kv_fill_synthetic(b, t, seed=300 + b)
+        kv = ref.kv(4160)
+        kv.fill_synthetic(300 + b, t)
+        kvs.append(kv)
+    ids = R.synth_tokens(13, 5, (B + 1) * S, kw["vocab_size"]).reshape(B + 1, S)
+    print("lat c5 bench shape: batch 32 x 5 rows", flush=True)
+    gl, gh = hip.forward_with_cache_output(ids[:B], lens[:B], slots=list(range(B)))
+    gaps = hip.router_gaps()
+    counts = hip.expert_counts()
+    assert (counts[:, :64].sum(1) == B * S * 6).all() and (counts[:, 64:] == B * S).all()
+    want = []
+    for b in range(B):
+        want.append(kvs[b].forward(ids[b], lens[b], nthreads=16))
+        if b % 8 == 7:
+            print(f"lat c5 bench shape: oracle {b + 1}/{B}", flush=True)
+    n32 = compare(gl, gh, want, gaps, S)
+    print(f"lat c5 bench shape: {n32} of {B} sequences compared; batch 1", flush=True)
+    gl, gh = hip.forward_with_cache_output(ids[B:], [lens[B]], slots=[B])
+    gaps = hip.router_gaps()
+    n1 = compare(gl, gh, [kvs[B].forward(ids[B], lens[B], nthreads=16)], gaps, S)
+    assert n32 >= B - 4 and n32 + n1 >= B - 3
+    hip.close()

@@ -191,3 +191,33 @@ def test_external_draft_sampled_stream_is_seeded():
     c = t.spec_generate(d, prompt, 24, 3, s, seed=6)
     assert list(a[0]) == list(b[0]) and a[2] == b[2]
     assert list(a[0]) != list(c[0])
+
+
+def test_mtp_invalid_head_after_eos_proposal_is_not_sampled():
+    """mtp_speculative.rs:196-203: proposing stops after an EOS proposal, so a later
+    head with an invalid (NaN) distribution raises nothing; when that head's proposal
+    counts, sample_probabilities fails (sampler.rs:142-152, 286-288) and so does the run."""
+    kw = dict(vocab_size=512, hidden_dim=128, ffn_dim=256, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=96,
+              num_future_tokens=3)
+    ref = R.Model(R.make_config(**kw))
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        ref.set(i, R.synth_fill(21, i, r * c, 0.02) if kind != R.T_NORM else np.ones(r * c, np.float32))
+    emb = ref.get(0).copy()
+    emb[0] *= 10.0
+    ref.set(0, emb)
+    for i, (name, r, c, kind) in enumerate(ref.tensors()):
+        if name.startswith("mtp.heads.1.") and kind == R.T_NORM:
+            ref.set(i, np.full(r * c, np.nan, np.float32))
+    ok = failed = 0
+    for seed in range(60):
+        prompt = R.synth_tokens(21, seed % 7, 10, 512)
+        try:
+            want, fin, stats, _ = ref.mtp_generate(prompt, 12, 3, R.sampler(temperature=0.8), seed=seed)
+        except ValueError:
+            failed += 1
+            continue
+        ok += 1
+        # three proposals a round (target_next, head 0, head 1): a run that never samples the
+        # NaN head ends in its first round on an EOS proposed by target_next or head 0
+        assert fin == R.FINISH_EOS and stats["rounds"] == 1 and stats["draft_tokens_proposed"] in (1, 2)
+    assert ok >= 3 and failed >= 10

@@ -190,8 +190,11 @@ def test_gguf_config_from_file(tmp_path):
     assert c.weight_format == A.W_INT4_G128
 
 
-def _gguf_bytes(version=1, enc=0, payload=b"\0" * 8, shape=(2,), magic=b"GGUF"):
-    meta = json.dumps({"config": G.model_config_json(8, 4, 8, 1, 1, 1, 16), "format": "Q80"}).encode()
+def _gguf_bytes(version=1, enc=0, payload=b"\0" * 8, shape=(2,), magic=b"GGUF", meta_edit=None):
+    meta = json.dumps({"config": G.model_config_json(8, 4, 8, 1, 1, 1, 16), "format": "Q80"})
+    if meta_edit:
+        meta = meta_edit(meta)
+    meta = meta.encode()
     b = magic + struct.pack("<IQ", version, len(meta)) + meta + struct.pack("<Q", 1)
     b += struct.pack("<Q", 1) + b"w" + struct.pack("<Q", len(shape)) + b"".join(struct.pack("<Q", d) for d in shape)
     return b + bytes([enc]) + struct.pack("<Q", len(payload)) + payload
@@ -205,6 +208,8 @@ def _gguf_bytes(version=1, enc=0, payload=b"\0" * 8, shape=(2,), magic=b"GGUF"):
     (_gguf_bytes(enc=1, payload=b"\0" * 3), A.CheckpointError),  # invalid Q8_0 payload
     (_gguf_bytes(enc=2, payload=b"\0" * 131), A.CheckpointError),  # invalid Q4_K_M payload length
     (_gguf_bytes()[:-3], A.IoError),                           # read_exact past the end
+    # a NUL byte after a number is not JSON (serde_json rejects the metadata)
+    (_gguf_bytes(meta_edit=lambda m: m.replace('"vocab_size": 8', '"vocab_size": 8\0')), A.CheckpointError),
 ])
 def test_malformed_gguf_errors(tmp_path, blob, err):
     p = tmp_path / "bad.gguf"
