@@ -116,6 +116,11 @@ def lib():
         "aarh_load_tensor_f32": (C.c_int, [_P, C.c_int, _P, C.c_int64]),
         "aarh_load_tensor_int4": (C.c_int, [_P, C.c_int, _P, _P, _P, C.c_int64, C.c_int64, C.c_int32]),
         "aarh_load_tensor_int8": (C.c_int, [_P, C.c_int, _P, _P, C.c_int64, C.c_int64]),
+        "aarh_load_tensor_packed_i4": (C.c_int, [_P, C.c_int, _P, C.c_int32, C.c_int64, _P, C.c_int64, _P, _P,
+                                                 C.c_int64]),
+        "aarh_lat_load_tensor_packed_i4": (C.c_int, [_P, C.c_int, _P, C.c_int32, C.c_int64, _P, C.c_int64, _P, _P,
+                                                     C.c_int64]),
+        "aarh_packed_i4_params": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int64, _P, _P, C.c_int64, _P, _P]),
         "aarh_init_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float]),
         "aarh_get_config": (C.c_int, [_P, C.POINTER(_Cfg)]),
         "aarh_set_replay_schedule": (C.c_int, [_P, C.c_int]),
@@ -200,7 +205,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_lat_create", "aarh_lat_destroy", "aarh_lat_last_error", "aarh_lat_num_tensors",
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
-            "aarh_lat_expert_counts", "aarh_lat_prof_enable", "aarh_lat_prof_get"]
+            "aarh_lat_expert_counts", "aarh_lat_prof_enable", "aarh_lat_prof_get", "aarh_load_tensor_packed_i4",
+            "aarh_lat_load_tensor_packed_i4", "aarh_packed_i4_params"]
 
 
 def _ptr(a):
@@ -233,6 +239,42 @@ def safetensors_read_tensor(path, name):
     out = np.empty(n.value, np.float32)
     _host_check(lib().aarh_safetensors_read_tensor(p, nm, _ptr(out), out.size, None, None, None))
     return out.reshape([shape[i] for i in range(nd.value)])
+
+
+@dataclass
+class PackedInt4Tensor:
+    """quant/src/types.rs:79-90: packed 4-bit codes over the flattened row-major tensor
+    (low nibble = even index, int4.rs:45-53), f32 scale and zero point per group of
+    `group_size` values; value = (q - zero) * scale (dequantise_packed_i4_to_vec,
+    int4.rs:70-91)."""
+    shape: tuple
+    group_size: int
+    data: np.ndarray
+    scales: np.ndarray
+    zeros: np.ndarray
+
+    def _args(self):
+        shape = np.ascontiguousarray(self.shape, np.int64)
+        data = np.ascontiguousarray(self.data, np.uint8).reshape(-1)
+        sc = np.ascontiguousarray(self.scales, np.float32).reshape(-1)
+        zz = np.ascontiguousarray(self.zeros, np.float32).reshape(-1)
+        if sc.size != zz.size:
+            raise ShapeError(f"got {sc.size} scales and {zz.size} zeros")
+        return shape, data, sc, zz
+
+
+def packed_i4_params(t: PackedInt4Tensor):
+    """The device's per-(row, 128-column group) fp16 scale and zero bits of a
+    PackedInt4Tensor (aarh_packed_i4_params): (scales_f16, zeros_f16) as uint16 [rows, cols/128]."""
+    shape, data, sc, zz = t._args()
+    cols = int(shape[-1]) if shape.size else 0
+    rows = int(np.prod(shape[:-1])) if shape.size > 1 else 1
+    ng = max(rows * (cols // 128), 1)
+    sh = np.zeros(ng, np.uint16)
+    zh = np.zeros(ng, np.uint16)
+    _host_check(lib().aarh_packed_i4_params(_ptr(shape), shape.size, int(t.group_size), data.size, _ptr(sc), _ptr(zz),
+                                            sc.size, _ptr(sh), _ptr(zh)))
+    return sh.reshape(rows, -1), zh.reshape(rows, -1)
 
 
 @dataclass
@@ -400,6 +442,12 @@ class HipModel:
         s = np.ascontiguousarray(scales_f16, np.uint16)
         z = np.ascontiguousarray(zeros_f16, np.uint16)
         self._check(lib().aarh_load_tensor_int4(self.h, tid, _ptr(p), _ptr(s), _ptr(z), rows, cols, group))
+
+    def load_packed_i4(self, tid, t: PackedInt4Tensor):
+        """A PackedInt4Tensor as the quant crate holds it (aarh_load_tensor_packed_i4)."""
+        shape, data, sc, zz = t._args()
+        self._check(lib().aarh_load_tensor_packed_i4(self.h, tid, _ptr(shape), shape.size, int(t.group_size),
+                                                     _ptr(data), data.size, _ptr(sc), _ptr(zz), sc.size))
 
     def load_int8(self, tid, codes, scales, rows, cols):
         q = np.ascontiguousarray(codes, np.int8)
@@ -912,6 +960,12 @@ class HipLatModel:
     def load_f32(self, tid, values):
         v = np.ascontiguousarray(values, np.float32)
         self._check(lib().aarh_lat_load_tensor_f32(self.h, tid, _ptr(v), v.size))
+
+    def load_packed_i4(self, tid, t: PackedInt4Tensor):
+        """A PackedInt4Tensor into an INT4 g128 tensor (aarh_lat_load_tensor_packed_i4)."""
+        shape, data, sc, zz = t._args()
+        self._check(lib().aarh_lat_load_tensor_packed_i4(self.h, tid, _ptr(shape), shape.size, int(t.group_size),
+                                                         _ptr(data), data.size, _ptr(sc), _ptr(zz), sc.size))
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(lib().aarh_lat_init_synthetic(self.h, seed, std))

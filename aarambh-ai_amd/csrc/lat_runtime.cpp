@@ -526,6 +526,35 @@ int ensure_staging(Ctx* c, size_t elems) {
     return 0;
 }
 
+// The tiled matrix (and its row offset and gate/up interleave) holding a linear tensor.
+void linear_target(Ctx* c, const LSlot& s, LTensor** t, int* ro, int* inter) {
+    LatLayer& b = c->layers[s.layer];
+    *ro = 0;
+    *inter = 0;
+    switch (s.part) {
+        case L_QP: *t = &b.qkr; break;
+        case L_KVA: *t = &b.qkr; *ro = c->QW; break;
+        case L_KRP: *t = &b.qkr; *ro = c->QW + c->lat; break;
+        case L_OP: *t = &b.op; break;
+        case L_ROUTER: *t = &b.router; break;
+        case L_GATE: *t = &b.gu; *ro = s.expert * 2 * c->D; *inter = 1; break;
+        case L_UP: *t = &b.gu; *ro = s.expert * 2 * c->D; *inter = 2; break;
+        default: *t = &b.dn; *ro = s.expert * c->H; break;
+    }
+}
+
+// up_k / up_v held in tmpq (the attention format's stored values) -> fp16 hi + lo operands.
+int split_upkv(Ctx* c, const LSlot& s) {
+    LatLayer& b = c->layers[s.layer];
+    LTensor& t = c->tmpq;
+    KCHK(c, launch_dequant_tiled(t.w, t.sz, t.rscale, t.fmt, (int)s.rows, (int)s.cols, c->tmpf, 0, c->stream));
+    if (s.part == L_UPK)
+        KCHK(c, launch_split_hilo(c->tmpf, b.upk_hi, b.upk_lo, (int)s.rows, (int)s.cols, c->nope, c->stream));
+    else
+        KCHK(c, launch_split_hilo(c->tmpf, b.upv_hi, b.upv_lo, (int)s.rows, (int)s.cols, 0, c->stream));
+    return 0;
+}
+
 // Place the tensor held in c->staging (f32, reference shape) into its device form.
 int place_staging(Ctx* c, int id) {
     const LSlot& s = c->slots[id];
@@ -544,31 +573,16 @@ int place_staging(Ctx* c, int id) {
         HIPCHK(c, hipMemcpyAsync(*s.norm_ptr, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
         return 0;
     }
-    LatLayer& b = c->layers[s.layer];
     if (s.part == L_UPK || s.part == L_UPV) {
         // exactly the values the attention format stores, split into fp16 hi + lo MFMA operands
         LTensor& t = c->tmpq;
         KCHK(c, launch_quantise_tiled(c->staging, (int)s.rows, (int)s.cols, t.fmt, t.w, t.sz, t.rscale, 0, (int)s.rows,
                                       0, c->stream));
-        KCHK(c, launch_dequant_tiled(t.w, t.sz, t.rscale, t.fmt, (int)s.rows, (int)s.cols, c->tmpf, 0, c->stream));
-        if (s.part == L_UPK)
-            KCHK(c, launch_split_hilo(c->tmpf, b.upk_hi, b.upk_lo, (int)s.rows, (int)s.cols, c->nope, c->stream));
-        else
-            KCHK(c, launch_split_hilo(c->tmpf, b.upv_hi, b.upv_lo, (int)s.rows, (int)s.cols, 0, c->stream));
-        return 0;
+        return split_upkv(c, s);
     }
     LTensor* t = nullptr;
     int ro = 0, inter = 0;
-    switch (s.part) {
-        case L_QP: t = &b.qkr; break;
-        case L_KVA: t = &b.qkr; ro = c->QW; break;
-        case L_KRP: t = &b.qkr; ro = c->QW + c->lat; break;
-        case L_OP: t = &b.op; break;
-        case L_ROUTER: t = &b.router; break;
-        case L_GATE: t = &b.gu; ro = s.expert * 2 * c->D; inter = 1; break;
-        case L_UP: t = &b.gu; ro = s.expert * 2 * c->D; inter = 2; break;
-        default: t = &b.dn; ro = s.expert * c->H; break;
-    }
+    linear_target(c, s, &t, &ro, &inter);
     KCHK(c, launch_quantise_tiled(c->staging, (int)s.rows, (int)s.cols, t->fmt, t->w, t->sz, t->rscale, ro, t->N,
                                   inter, c->stream));
     return 0;
@@ -873,6 +887,45 @@ int aarh_lat_load_tensor_f32(aarh_lat_ctx* c, int id, const float* host, int64_t
     HIPCHK(c, hipMemcpy(c->staging, host, numel * 4, hipMemcpyHostToDevice));
     int r = place_staging(c, id);
     if (r) return r;
+    return sync_stream(c);
+}
+
+int aarh_lat_load_tensor_packed_i4(aarh_lat_ctx* c, int id, const int64_t* shape, int32_t ndims, int64_t group_size,
+                                   const uint8_t* data, int64_t data_len, const float* scales, const float* zeros,
+                                   int64_t n_groups) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
+    const LSlot& s = c->slots[id];
+    if (s.kind != AARH_T_LINEAR)
+        return fail(c, AARH_ERR_UNSUPPORTED, "tensor %s is not a linear weight", s.name.c_str());
+    const bool expert = s.part == L_GATE || s.part == L_UP || s.part == L_DOWN;
+    const int fmt = expert ? c->cfg.expert_format : c->cfg.attn_format;
+    if (fmt != AARH_W_INT4_G128)
+        return fail(c, AARH_ERR_UNSUPPORTED, "tensor %s is not stored as INT4 g128 in this model", s.name.c_str());
+    if (!shape || !data || ndims != 2 || shape[0] != s.rows || shape[1] != s.cols)
+        return fail(c, AARH_ERR_SHAPE, "PackedInt4Tensor shape does not match %s [%lld, %lld]", s.name.c_str(),
+                    (long long)s.rows, (long long)s.cols);
+    const size_t ng = (size_t)s.rows * (s.cols / 128), nb = (size_t)s.rows * s.cols / 2;
+    std::vector<uint16_t> sh(ng), zh(ng);
+    int r = aarh_packed_i4_params(shape, ndims, group_size, data_len, scales, zeros, n_groups, sh.data(), zh.data());
+    if (r) return fail(c, r, "%s: %s", s.name.c_str(), aarh_host_last_error());
+    if (ensure_staging(c, (nb + 4 * ng + 3) / 4 + 1)) return AARH_ERR_DEVICE;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    uint8_t* st = (uint8_t*)c->staging;
+    HIPCHK(c, hipMemcpy(st, data, nb, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(st + nb, sh.data(), ng * 2, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(st + nb + ng * 2, zh.data(), ng * 2, hipMemcpyHostToDevice));
+    const uint16_t* dsh = (const uint16_t*)(st + nb);
+    const uint16_t* dzh = (const uint16_t*)(st + nb + ng * 2);
+    if (s.part == L_UPK || s.part == L_UPV) {
+        LTensor& t = c->tmpq;
+        KCHK(c, launch_repack_int4(st, dsh, dzh, (int)s.rows, (int)s.cols, t.w, t.sz, 0, (int)s.rows, 0, c->stream));
+        if ((r = split_upkv(c, s))) return r;
+        return sync_stream(c);
+    }
+    LTensor* t = nullptr;
+    int ro = 0, inter = 0;
+    linear_target(c, s, &t, &ro, &inter);
+    KCHK(c, launch_repack_int4(st, dsh, dzh, (int)s.rows, (int)s.cols, t->w, t->sz, ro, t->N, inter, c->stream));
     return sync_stream(c);
 }
 

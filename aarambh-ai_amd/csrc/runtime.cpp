@@ -1044,6 +1044,23 @@ int aarh_load_tensor_int4(aarh_ctx* c, int id, const uint8_t* packed, const uint
     return sync_stream(c);
 }
 
+int aarh_load_tensor_packed_i4(aarh_ctx* c, int id, const int64_t* shape, int32_t ndims, int64_t group_size,
+                               const uint8_t* data, int64_t data_len, const float* scales, const float* zeros,
+                               int64_t n_groups) {
+    if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
+    const TensorSlot& s = c->slots[id];
+    if (s.kind != AARH_T_LINEAR || c->cfg.weight_format != AARH_W_INT4_G128)
+        return fail(c, AARH_ERR_UNSUPPORTED, "tensor %s is not an INT4 g128 linear in this model", s.name.c_str());
+    if (!shape || !data || ndims != 2 || shape[0] != s.rows || shape[1] != s.cols)
+        return fail(c, AARH_ERR_SHAPE, "PackedInt4Tensor shape does not match %s [%lld, %lld]", s.name.c_str(),
+                    (long long)s.rows, (long long)s.cols);
+    const size_t ng = (size_t)s.rows * (s.cols / 128);
+    std::vector<uint16_t> sh(ng), zh(ng);
+    int r = aarh_packed_i4_params(shape, ndims, group_size, data_len, scales, zeros, n_groups, sh.data(), zh.data());
+    if (r) return fail(c, r, "%s: %s", s.name.c_str(), aarh_host_last_error());
+    return aarh_load_tensor_int4(c, id, data, sh.data(), zh.data(), s.rows, s.cols, 128);
+}
+
 int aarh_load_tensor_int8(aarh_ctx* c, int id, const int8_t* codes, const float* scales, int64_t rows, int64_t cols) {
     if (!c || id < 0 || id >= (int)c->slots.size()) return fail(c, AARH_ERR_SHAPE, "bad tensor id %d", id);
     const TensorSlot& s = c->slots[id];

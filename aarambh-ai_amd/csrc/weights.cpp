@@ -595,6 +595,22 @@ int check_gguf_config(aarh_ctx* c, const JVal& meta) {
     return 0;
 }
 
+// IEEE binary16 nearest value, ties to even (the conversion of a float to _Float16).
+uint16_t f32_to_f16_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // 65520 and above round to infinity
+    if (ax < 0x38800000u) {                                    // below 2^-14: a multiple of 2^-24
+        float a;
+        memcpy(&a, &ax, 4);
+        return (uint16_t)(sign | (uint32_t)std::nearbyint(a * 16777216.0f));
+    }
+    const uint32_t m = ax + 0xFFFu + ((ax >> 13) & 1u) - (112u << 23);
+    return (uint16_t)(sign | (m >> 13));
+}
+
 }  // namespace
 
 extern "C" {
@@ -651,6 +667,86 @@ int aarh_load_safetensors(aarh_ctx* c, const char* path, int32_t* out_loaded) {
     for (const auto& kv : slots)
         if (!kv.second.loaded) return fail_ctx(c, AARH_ERR_CHECKPOINT, "checkpoint lacks tensor " + kv.first);
     if (out_loaded) *out_loaded = loaded;
+    return AARH_OK;
+}
+
+// PackedInt4Tensor (quant/src/types.rs:79-90) -> the device's INT4 g128 parameters.
+// Checks follow dequantise_packed_i4_to_vec (int4.rs:70-91): a non-zero group size,
+// ceil(numel / group_size) scales and zeros, and enough packed bytes for the shape.
+// The device layout then needs the last dimension and the group size to be multiples
+// of 128 (a reference group covers whole 128-column device groups), finite fp16 scales
+// and integral zero points below 1024 in magnitude ((q - zero) stays exact in fp16).
+int aarh_packed_i4_params(const int64_t* shape, int32_t ndims, int64_t group_size, int64_t data_len,
+                          const float* scales, const float* zeros, int64_t n_groups, uint16_t* scales_f16,
+                          uint16_t* zeros_f16) {
+    char msg[256];
+    auto bad = [&](int code) {
+        g_host_err = msg;
+        return code;
+    };
+    if (!shape || !scales || !zeros || !scales_f16 || !zeros_f16) {
+        snprintf(msg, sizeof(msg), "null PackedInt4Tensor field");
+        return bad(AARH_ERR_CONFIG);
+    }
+    if (ndims < 1 || ndims > 8) {
+        snprintf(msg, sizeof(msg), "int4 tensor rank %d is not supported (1 to 8 dimensions)", ndims);
+        return bad(AARH_ERR_SHAPE);
+    }
+    int64_t n = 1;
+    for (int i = 0; i < ndims; i++) {
+        if (shape[i] <= 0 || n > ((int64_t)1 << 40) / shape[i]) {
+            snprintf(msg, sizeof(msg), "int4 tensor dimension %d has size %lld", i, (long long)shape[i]);
+            return bad(AARH_ERR_SHAPE);
+        }
+        n *= shape[i];
+    }
+    if (group_size <= 0) {
+        snprintf(msg, sizeof(msg), "group_size must be non-zero");
+        return bad(AARH_ERR_CONFIG);
+    }
+    const int64_t expected = (n + group_size - 1) / group_size;
+    if (n_groups != expected) {
+        snprintf(msg, sizeof(msg), "expected %lld int4 groups, got %lld scales and %lld zeros", (long long)expected,
+                 (long long)n_groups, (long long)n_groups);
+        return bad(AARH_ERR_SHAPE);
+    }
+    if (data_len < 0 || data_len < (n + 1) / 2) {
+        snprintf(msg, sizeof(msg), "int4 tensor holds %lld values but its shape has %lld elements",
+                 (long long)(data_len < 0 ? 0 : 2 * data_len), (long long)n);
+        return bad(AARH_ERR_SHAPE);
+    }
+    const int64_t cols = shape[ndims - 1], rows = n / cols;
+    if (cols % 128) {
+        snprintf(msg, sizeof(msg), "last dimension %lld is not a multiple of 128 (the device's INT4 group width)",
+                 (long long)cols);
+        return bad(AARH_ERR_UNSUPPORTED);
+    }
+    if (group_size % 128) {
+        snprintf(msg, sizeof(msg),
+                 "group_size %lld is not a multiple of 128: the device stores one scale and zero per 128 columns",
+                 (long long)group_size);
+        return bad(AARH_ERR_UNSUPPORTED);
+    }
+    for (int64_t g = 0; g < n_groups; g++) {
+        const float sc = scales[g], z = zeros[g];
+        const uint16_t h = f32_to_f16_rne(sc);
+        if (!std::isfinite(sc) || (h & 0x7C00u) == 0x7C00u) {
+            snprintf(msg, sizeof(msg), "scale %g of int4 group %lld has no finite fp16 value", (double)sc, (long long)g);
+            return bad(AARH_ERR_UNSUPPORTED);
+        }
+        if (!(std::fabs(z) < 1024.0f) || z != std::nearbyint(z)) {
+            snprintf(msg, sizeof(msg), "zero point %g of int4 group %lld is not an integer below 1024 in magnitude",
+                     (double)z, (long long)g);
+            return bad(AARH_ERR_UNSUPPORTED);
+        }
+    }
+    const int64_t G = cols / 128;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t g = 0; g < G; g++) {
+            const int64_t src = (r * cols + 128 * g) / group_size;
+            scales_f16[r * G + g] = f32_to_f16_rne(scales[src]);
+            zeros_f16[r * G + g] = f32_to_f16_rne(zeros[src]);
+        }
     return AARH_OK;
 }
 

@@ -95,6 +95,28 @@ int aarh_load_tensor_f32(aarh_ctx *ctx, int id, const float *host, int64_t numel
 /* PackedInt4Tensor (types.rs:79-90) with fp16 scale/zero per 128-group, row-major. */
 int aarh_load_tensor_int4(aarh_ctx *ctx, int id, const uint8_t *packed, const uint16_t *scales_f16,
                           const uint16_t *zeros_f16, int64_t rows, int64_t cols, int32_t group);
+/* A PackedInt4Tensor as the quant crate defines it (quant/src/types.rs:79-90: shape,
+   group_size, data = packed nibbles over the flattened row-major tensor, low nibble first,
+   int4.rs:45-53; f32 scales and zeros per group, value = (q - zero) * scale,
+   dequantise_packed_i4_to_vec int4.rs:70-91).  shape must be the tensor's [rows, cols].
+   Errors as the reference: CONFIG for group_size 0, SHAPE for a group count other than
+   ceil(numel / group_size) or too few data bytes.  The device keeps one fp16 scale and
+   one fp16 zero per 128 columns of a row, so the load needs group_size and cols to be
+   multiples of 128 (UNSUPPORTED otherwise), each scale is rounded to the nearest fp16
+   value (ties to even; UNSUPPORTED when that is infinite) and each zero must be an
+   integer with |zero| < 1024 (kept exactly).  The device then multiplies by
+   (q - zero) * fp16(scale): equal to the reference's value whenever the scale is an fp16
+   value, within 2^-11 of it relatively for normal-range scales otherwise. */
+int aarh_load_tensor_packed_i4(aarh_ctx *ctx, int id, const int64_t *shape, int32_t ndims,
+                               int64_t group_size, const uint8_t *data, int64_t data_len,
+                               const float *scales, const float *zeros, int64_t n_groups);
+/* The conversion aarh_load_tensor_packed_i4 applies, without a context or a GPU: fills
+   scales_f16 / zeros_f16 [rows][cols / 128] (rows = product of all but the last dim) with
+   the fp16 parameters of each 128-column device group; same checks and errors (message
+   in aarh_host_last_error). */
+int aarh_packed_i4_params(const int64_t *shape, int32_t ndims, int64_t group_size, int64_t data_len,
+                          const float *scales, const float *zeros, int64_t n_groups,
+                          uint16_t *scales_f16, uint16_t *zeros_f16);
 /* Per-row INT8 codes + f32 row scales (I8QuantizedTensor semantics per channel). */
 int aarh_load_tensor_int8(aarh_ctx *ctx, int id, const int8_t *codes, const float *scales,
                           int64_t rows, int64_t cols);
@@ -315,6 +337,12 @@ int aarh_lat_num_tensors(const aarh_lat_ctx *ctx);
 int aarh_lat_tensor_info(const aarh_lat_ctx *ctx, int id, char *name, int name_cap, int64_t *rows,
                          int64_t *cols, int32_t *kind);
 int aarh_lat_load_tensor_f32(aarh_lat_ctx *ctx, int id, const float *host, int64_t numel);
+/* A PackedInt4Tensor (quant/src/types.rs:79-90) into an INT4 g128 tensor of the latent
+   decoder (experts in expert_format, MLA projections and the router in attn_format);
+   same rules, rounding and errors as aarh_load_tensor_packed_i4. */
+int aarh_lat_load_tensor_packed_i4(aarh_lat_ctx *ctx, int id, const int64_t *shape, int32_t ndims,
+                                   int64_t group_size, const uint8_t *data, int64_t data_len,
+                                   const float *scales, const float *zeros, int64_t n_groups);
 /* Random init on device: tensor id i ~ N(0, std^2) (router N(0, 1/hidden_dim)), norms 1. */
 int aarh_lat_init_synthetic(aarh_lat_ctx *ctx, uint64_t seed, float std);
 

@@ -322,3 +322,52 @@ def test_hd128_long_context_chunk_merge(kvfmt):
         wl, _ = kv.forward(ids[b], L, nthreads=16)
         assert rel_rows(gl1[0], wl).max() < TOL, (L, "single", rel_rows(gl1[0], wl).max())
     hip.close()
+
+
+@pytest.mark.parametrize("group", [128, 256, 512])
+def test_packed_int4_tensor_loads(group):
+    """PackedInt4Tensor as the quant crate holds it (f32 scales / zeros, group_size):
+    at group 128 the device holds exactly what the device quantiser makes of the same
+    f32 weights (logits bit-identical); at every group size the logits equal the
+    oracle's forward on dequantise_packed_i4_to_vec's values with fp16 scales (the
+    device's stored function) within 2e-3, and on the f32-scale values within 2e-3."""
+    # fp16 KV and an f32 LM head: this small model's INT8 KV / bf16 head roundings move its
+    # logits by up to 1.6e-3 under a 3e-6 input perturbation, which is not what this tests
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=2, n_heads=2, n_kv_heads=1, max_seq_len=64,
+              weight_format=A.W_INT4_G128, lm_head_format=0, kv_format=A.KV_F16)
+    fkw = dict(kw, weight_format=A.W_F32)
+    ref_dev = R.Model(R.make_config(**fkw))   # values the device stores
+    ref_f32 = R.Model(R.make_config(**fkw))   # values dequantise_packed_i4_to_vec gives
+    hip = A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=64)
+    hq = A.HipModel(A.ModelConfig(**kw), max_batch=1, max_rows=64) if group == 128 else None
+    for i, (name, r, c, kind) in enumerate(hip.tensors()):
+        raw = R.synth_fill(17, i, r * c, 0.02) if kind != R.T_NORM else np.ones(r * c, np.float32)
+        if kind == R.T_LINEAR:
+            data, sc, zz = R.quantise_i4(raw, group)
+            t = A.PackedInt4Tensor((r, c), group, data, sc, zz)
+            hip.load_packed_i4(i, t)
+            sh, zh = A.packed_i4_params(t)
+            codes = np.zeros(r * c, np.float32)
+            codes[0::2], codes[1::2] = data & 15, data >> 4
+            gi = np.repeat(np.arange(c // 128), 128)
+            s, z = sh.view(np.float16).astype(np.float32), zh.view(np.float16).astype(np.float32)
+            ref_dev.set(i, (codes.reshape(r, c) - z[:, gi]) * s[:, gi])
+            ref_f32.set(i, R.dequantise_i4(data, r * c, group, sc, zz))
+            if hq:
+                hq.load_f32(i, raw)
+        else:
+            for m in (hip, hq):
+                if m:
+                    m.load_f32(i, raw)
+            ref_dev.set(i, raw)
+            ref_f32.set(i, raw)
+    ids = R.synth_tokens(17, 1, 9, 1024)
+    got, _ = hip.forward_with_cache_output(ids[None], [0])
+    if hq:
+        same, _ = hq.forward_with_cache_output(ids[None], [0])
+        assert np.array_equal(got, same)
+        hq.close()
+    for ref in (ref_dev, ref_f32):
+        want, _ = ref.kv(64).forward(ids, 0)
+        assert rel_rows(got[0], want).max() < 2e-3
+    hip.close()

@@ -215,3 +215,42 @@ def test_lat_c5_bench_shape_vs_oracle():
     n1 = compare(gl, gh, [kvs[B].forward(ids[B], lens[B], nthreads=16)], gaps, S)
     assert n32 >= B - 4 and n32 + n1 >= B - 3
     hip.close()
+
+
+def test_lat_packed_int4_tensors_equal_device_quantisation():
+    """Every INT4 tensor of the latent decoder (MLA projections incl. up_k / up_v, the
+    router, routed and shared experts) loaded as a PackedInt4Tensor with the quant
+    crate's group-128 codes and f32 scales holds exactly what the device quantiser makes
+    of the same f32 weights: logits and hidden states bit-identical; a group-256 load
+    matches the oracle within the bar."""
+    kw = small_kw(n_layers=1, attn_format=A.W_INT4_G128)
+    a = A.HipLatModel(A.LatConfig(**kw), max_batch=1, max_rows=64)
+    b = A.HipLatModel(A.LatConfig(**kw), max_batch=1, max_rows=64)
+    c = A.HipLatModel(A.LatConfig(**kw), max_batch=1, max_rows=64)
+    ref = R.LatModel(R.make_lat_config(**dict(kw, attn_format=A.W_F32, expert_format=A.W_F32)))
+    n_packed = 0
+    for i, (name, r, cc, kind) in enumerate(a.tensors()):
+        raw = R.synth_fill(19, i, r * cc, 0.05) if kind != R.T_NORM else np.ones(r * cc, np.float32)
+        a.load_f32(i, raw)
+        if kind == R.T_LINEAR:
+            data, sc, zz = R.quantise_i4(raw, 128)
+            b.load_packed_i4(i, A.PackedInt4Tensor((r, cc), 128, data, sc, zz))
+            d2, s2, z2 = R.quantise_i4(raw, 256)
+            c.load_packed_i4(i, A.PackedInt4Tensor((r, cc), 256, d2, s2, z2))
+            # the oracle holds the device's stored function: fp16 scales of the group-256 codes
+            ref.set(i, R.dequantise_i4(d2, r * cc, 256, s2.astype(np.float16).astype(np.float32), z2))
+            n_packed += 1
+        else:
+            b.load_f32(i, raw)
+            c.load_f32(i, raw)
+            ref.set(i, raw)
+    assert n_packed > 10
+    ids = R.synth_tokens(19, 1, 7, kw["vocab_size"])
+    la, ha = a.forward_with_cache_output(ids[None], [0])
+    lb, hb = b.forward_with_cache_output(ids[None], [0])
+    assert np.array_equal(la, lb) and np.array_equal(ha, hb)
+    lc, hc = c.forward_with_cache_output(ids[None], [0])
+    gaps = c.router_gaps()
+    assert compare(lc, hc, [ref.kv(128).forward(ids, 0)], gaps, 7) == 1
+    for m in (a, b, c):
+        m.close()
