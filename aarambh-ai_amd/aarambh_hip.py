@@ -158,6 +158,14 @@ def lib():
         "aarh_spec_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler), _P,
                                          _P, _P, _P, C.POINTER(_Stats), _P, _P]),
         "aarh_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
+        "aarh_spec_session_begin": (C.c_int, [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_Sampler),
+                                              _P, C.POINTER(_P)]),
+        "aarh_spec_session_step": (C.c_int, [_P, C.c_int, C.POINTER(C.c_int32)]),
+        "aarh_spec_session_result": (C.c_int, [_P, _P, C.c_int32, _P, _P, C.POINTER(_Stats)]),
+        "aarh_spec_session_candidates": (C.c_int, [_P, _P, _P, C.c_int32]),
+        "aarh_spec_session_rng_offsets": (C.c_int, [_P, _P]),
+        "aarh_spec_session_set_rng_offsets": (C.c_int, [_P, _P]),
+        "aarh_spec_session_end": (None, [_P]),
         "aarh_session_rng_offsets": (C.c_int, [_P, _P]),
         "aarh_session_set_rng_offsets": (C.c_int, [_P, _P]),
         "aarh_top_candidates": (C.c_int, [_P, _P, C.c_int, C.c_int, C.POINTER(_Sampler), C.c_int, _P, _P, _P]),
@@ -206,7 +214,9 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_lat_tensor_info", "aarh_lat_load_tensor_f32", "aarh_lat_init_synthetic", "aarh_lat_kv_len",
             "aarh_lat_kv_rollback", "aarh_lat_kv_fill_synthetic", "aarh_lat_forward", "aarh_lat_router_gaps",
             "aarh_lat_expert_counts", "aarh_lat_prof_enable", "aarh_lat_prof_get", "aarh_load_tensor_packed_i4",
-            "aarh_lat_load_tensor_packed_i4", "aarh_packed_i4_params"]
+            "aarh_lat_load_tensor_packed_i4", "aarh_packed_i4_params", "aarh_spec_session_begin",
+            "aarh_spec_session_step", "aarh_spec_session_result", "aarh_spec_session_candidates",
+            "aarh_spec_session_rng_offsets", "aarh_spec_session_set_rng_offsets", "aarh_spec_session_end"]
 
 
 def _ptr(a):
@@ -649,6 +659,68 @@ class SpeculativeEngine:
 
     def generate(self, prompt_ids, max_new_tokens, sampler: Sampler):
         return self.generate_batch(np.asarray(prompt_ids)[None, :], max_new_tokens, sampler)[0]
+
+    def session(self, prompts, max_new_tokens, sampler: Sampler, seeds=None):
+        return SpecSession(self, prompts, max_new_tokens, sampler, seeds)
+
+
+class SpecSession:
+    """Round-by-round driver of the external-draft engine (aarh_spec_session_*)."""
+
+    def __init__(self, engine, prompts, max_new_tokens, sampler, seeds=None):
+        self.engine = engine
+        t = engine.target
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.uint32)
+        self.nseq = prompts.shape[0]
+        self.max_new = max_new_tokens
+        sd = np.ascontiguousarray(
+            np.full(self.nseq, sampler.seed, np.uint64) if seeds is None else seeds, np.uint64)
+        h = _P()
+        t._check(lib().aarh_spec_session_begin(t.h, engine.draft.h, _ptr(prompts), self.nseq, prompts.shape[1],
+                                               max_new_tokens, engine.config.num_draft_tokens,
+                                               C.byref(sampler._c()), _ptr(sd), C.byref(h)))
+        self.h = h
+
+    def step(self, rounds=1):
+        done = C.c_int32()
+        self.engine.target._check(lib().aarh_spec_session_step(self.h, rounds, C.byref(done)))
+        return bool(done.value)
+
+    def result(self):
+        cap = max(self.max_new, 1)
+        n = self.nseq
+        out = np.zeros((n, cap), np.uint32)
+        ln = np.zeros(n, np.int32)
+        fin = np.zeros(n, np.int32)
+        stats = (_Stats * n)()
+        t = self.engine.target
+        t._check(lib().aarh_spec_session_result(self.h, _ptr(out), cap, _ptr(ln), _ptr(fin), stats))
+        ci = np.zeros((n, cap, TOP_CANDIDATES), np.uint32)
+        cp = np.zeros((n, cap, TOP_CANDIDATES), np.float32)
+        t._check(lib().aarh_spec_session_candidates(self.h, _ptr(ci), _ptr(cp), cap))
+        res = []
+        for b in range(n):
+            st = SpeculativeStats(**{k: getattr(stats[b], k) for k, _ in _Stats._fields_})
+            res.append(GenerationOutput(list(out[b, :ln[b]]), FINISH[int(fin[b])], st,
+                                        _candidate_lists(ci[b, :ln[b]], cp[b, :ln[b]])))
+        return res
+
+    def rng_offsets(self):
+        out = np.zeros(self.nseq, np.uint64)
+        self.engine.target._check(lib().aarh_spec_session_rng_offsets(self.h, _ptr(out)))
+        return out
+
+    def set_rng_offsets(self, offsets):
+        o = np.ascontiguousarray(offsets, np.uint64)
+        self.engine.target._check(lib().aarh_spec_session_set_rng_offsets(self.h, _ptr(o)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aarh_spec_session_end(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 def _session_outputs(model, h, n, cap, candidates=True):

@@ -2461,11 +2461,16 @@ int xsession_round(XSession* e) {
 
 }  // namespace
 
-extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len,
-                                  int max_new_tokens, int num_draft_tokens, const aarh_sampler* s,
-                                  const uint64_t* seeds, uint32_t* out_tokens, int32_t* out_len,
-                                  int32_t* finish_reason, aarh_spec_stats* stats, uint32_t* out_cand_ids,
-                                  float* out_cand_probs) {
+// The external-draft engine as a session (round-by-round driving, keystream positions).
+struct aarh_spec_session {
+    XSession e;
+    int max_new_tokens = 0;  // the caller's budget: row capacity of the results
+};
+
+namespace {
+
+int spec_begin(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len, int max_new_tokens,
+               int num_draft_tokens, const aarh_sampler* s, const uint64_t* seeds, XSession& e) {
     if (!c || !d || !s) return AARH_ERR_CONFIG;
     if (num_draft_tokens <= 0) return fail(c, AARH_ERR_CONFIG, "num_draft_tokens must be greater than zero");
     if (num_draft_tokens >= PAD_SLACK)
@@ -2475,6 +2480,8 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
     if (nseq <= 0 || nseq > c->cfg.max_batch || nseq > d->cfg.max_batch)
         return fail(c, AARH_ERR_SHAPE, "nseq %d exceeds max_batch", nseq);
     if (prompt_len <= 0) return fail(c, AARH_ERR_SHAPE, "prompt must be non-empty");
+    if (!prompts) return fail(c, AARH_ERR_CONFIG, "null prompts");
+    if (max_new_tokens < 0) return fail(c, AARH_ERR_SHAPE, "negative max_new_tokens");
     const int max_seq = std::min(c->cfg.max_seq_len, d->cfg.max_seq_len);
     if (prompt_len >= max_seq)
         return fail(c, AARH_ERR_SHAPE, "prompt has %d tokens but speculative context limit is %d (target=%d, draft=%d)",
@@ -2483,7 +2490,6 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
     const int K = num_draft_tokens, V = c->V;
     if (nseq * (K + 1) > c->Mmax || nseq * (K + 1) > d->Mmax)
         return fail(c, AARH_ERR_SHAPE, "nseq x (draft tokens + 1) exceeds max_rows");
-    XSession e;
     e.c = c;
     e.d = d;
     e.nseq = nseq;
@@ -2561,20 +2567,56 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
             e.finished[b] = 1;
         }
     }
-    for (;;) {
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int aarh_spec_session_begin(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len,
+                                       int max_new_tokens, int num_draft_tokens, const aarh_sampler* s,
+                                       const uint64_t* seeds, aarh_spec_session** out) {
+    if (!out) return fail(c, AARH_ERR_CONFIG, "null session pointer");
+    *out = nullptr;
+    auto* ss = new aarh_spec_session();
+    ss->max_new_tokens = max_new_tokens;
+    const int r = spec_begin(c, d, prompts, nseq, prompt_len, max_new_tokens, num_draft_tokens, s, seeds, ss->e);
+    if (r) {
+        delete ss;
+        return r;
+    }
+    *out = ss;
+    return 0;
+}
+
+extern "C" int aarh_spec_session_step(aarh_spec_session* ss, int max_rounds, int32_t* all_done) {
+    if (!ss) return AARH_ERR_CONFIG;
+    XSession& e = ss->e;
+    for (int i = 0; i < max_rounds; i++) {
         bool any = false;
-        for (int b = 0; b < nseq; b++)
+        for (int b = 0; b < e.nseq; b++)
             if (!e.finished[b]) any = true;
         if (!any) break;
-        if ((r = xsession_round(&e))) return r;
+        if (int r = xsession_round(&e)) return r;
     }
-    for (int b = 0; b < nseq; b++) {
+    if (all_done) {
+        *all_done = 1;
+        for (int b = 0; b < e.nseq; b++)
+            if (!e.finished[b]) *all_done = 0;
+    }
+    return 0;
+}
+
+extern "C" int aarh_spec_session_result(aarh_spec_session* ss, uint32_t* out_tokens, int32_t out_cap,
+                                        int32_t* out_len, int32_t* finish_reason, aarh_spec_stats* stats) {
+    if (!ss) return AARH_ERR_CONFIG;
+    const XSession& e = ss->e;
+    for (int b = 0; b < e.nseq; b++) {
         const int n = (int)e.out[b].size();
         if (out_len) out_len[b] = n;
         if (out_tokens)
-            for (int i = 0; i < n && i < max_new_tokens; i++) out_tokens[(size_t)b * max_new_tokens + i] = e.out[b][i];
+            for (int i = 0; i < n && i < out_cap; i++) out_tokens[(size_t)b * out_cap + i] = e.out[b][i];
         int fin = e.finish[b];
-        if (n == e.available && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
+        if (e.finished[b] && n == e.available && fin == AARH_FINISH_MAX_TOKENS) fin = AARH_FINISH_CONTEXT_LIMIT;
         if (finish_reason) finish_reason[b] = fin;
         if (stats) {
             stats[b] = e.stats[b];
@@ -2582,6 +2624,47 @@ extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prom
                 std::max(0, stats[b].draft_tokens_proposed - stats[b].draft_tokens_accepted);
         }
     }
-    e.cand.copy_out(nseq, max_new_tokens, out_cand_ids, out_cand_probs);
     return 0;
+}
+
+extern "C" int aarh_spec_session_candidates(aarh_spec_session* ss, uint32_t* ids, float* probs, int32_t out_cap) {
+    if (!ss) return AARH_ERR_CONFIG;
+    ss->e.cand.copy_out(ss->e.nseq, out_cap, ids, probs);
+    return 0;
+}
+
+extern "C" int aarh_spec_session_rng_offsets(aarh_spec_session* ss, uint64_t* out) {
+    if (!ss || !out) return AARH_ERR_CONFIG;
+    for (int b = 0; b < ss->e.nseq; b++) out[b] = ss->e.hoffs[b];
+    return 0;
+}
+
+extern "C" int aarh_spec_session_set_rng_offsets(aarh_spec_session* ss, const uint64_t* offsets) {
+    if (!ss || !offsets) return AARH_ERR_CONFIG;
+    for (int b = 0; b < ss->e.nseq; b++) ss->e.hoffs[b] = offsets[b];
+    return 0;
+}
+
+extern "C" void aarh_spec_session_end(aarh_spec_session* ss) {
+    if (!ss) return;
+    (void)hipStreamSynchronize(ss->e.c->stream);
+    (void)hipStreamSynchronize(ss->e.d->stream);
+    if (ss->e.c->side) (void)hipStreamSynchronize(ss->e.c->side);
+    delete ss;
+}
+
+extern "C" int aarh_spec_generate(aarh_ctx* c, aarh_ctx* d, const uint32_t* prompts, int nseq, int prompt_len,
+                                  int max_new_tokens, int num_draft_tokens, const aarh_sampler* s,
+                                  const uint64_t* seeds, uint32_t* out_tokens, int32_t* out_len,
+                                  int32_t* finish_reason, aarh_spec_stats* stats, uint32_t* out_cand_ids,
+                                  float* out_cand_probs) {
+    aarh_spec_session* ss = nullptr;
+    int r = aarh_spec_session_begin(c, d, prompts, nseq, prompt_len, max_new_tokens, num_draft_tokens, s, seeds, &ss);
+    if (r) return r;
+    int32_t done = 0;
+    while (!done && !r) r = aarh_spec_session_step(ss, 1 << 20, &done);
+    if (!r) r = aarh_spec_session_result(ss, out_tokens, max_new_tokens, out_len, finish_reason, stats);
+    if (!r) r = aarh_spec_session_candidates(ss, out_cand_ids, out_cand_probs, max_new_tokens);
+    aarh_spec_session_end(ss);
+    return r;
 }

@@ -274,6 +274,25 @@ int aarh_spec_generate(aarh_ctx *target, aarh_ctx *draft, const uint32_t *prompt
                        int32_t *out_len, int32_t *finish_reason, aarh_spec_stats *stats,
                        uint32_t *out_cand_ids, float *out_cand_probs);
 
+/* The external-draft engine as a session, one call per batch of rounds
+   (speculative.rs:175-516, as aarh_spec_generate, which is begin + step until done +
+   result + candidates + end).  begin: the constructor checks and both prefills
+   (speculative.rs:236-247); step: up to max_rounds rounds (:251-508); result /
+   candidates: committed tokens, finish reasons, SpeculativeStats and top candidates so
+   far (out_cap tokens per request).  rng_offsets / set_rng_offsets: the keystream
+   position (StdRng word offset) of each request's sampler, as for aarh_session_*. */
+typedef struct aarh_spec_session aarh_spec_session;
+int aarh_spec_session_begin(aarh_ctx *target, aarh_ctx *draft, const uint32_t *prompts, int nseq,
+                            int prompt_len, int max_new_tokens, int num_draft_tokens,
+                            const aarh_sampler *sampler, const uint64_t *seeds, aarh_spec_session **out);
+int aarh_spec_session_step(aarh_spec_session *session, int max_rounds, int32_t *all_done);
+int aarh_spec_session_result(aarh_spec_session *session, uint32_t *out_tokens, int32_t out_cap,
+                             int32_t *out_len, int32_t *finish_reason, aarh_spec_stats *stats);
+int aarh_spec_session_candidates(aarh_spec_session *session, uint32_t *ids, float *probs, int32_t out_cap);
+int aarh_spec_session_rng_offsets(aarh_spec_session *session, uint64_t *out);
+int aarh_spec_session_set_rng_offsets(aarh_spec_session *session, const uint64_t *offsets);
+void aarh_spec_session_end(aarh_spec_session *session);
+
 /* --- Sampler::top_candidates_from_probabilities (sampler.rs:188-208) of each row's sampling
    distribution (Sampler::probabilities: greedy one-hot at the argmax, else softmax at T):
    the n <= AARH_TOP_CANDIDATES largest probabilities, ties in ascending token order.
