@@ -34,6 +34,17 @@ static constexpr int ACC_CHUNK = 8192;       // floats of a row per scan step; L
 static constexpr int CAND_CHUNK = 8192;      // the same for the candidate kernel (its key lists use 20 KiB)
 static constexpr int TOPP_PAGE = 4096;       // top-p candidates sorted per page (64-bit keys)
 static constexpr int TOPP_LDS_FLOATS = TOPP_PAGE * 3;  // page keys (8 B) + their probabilities (4 B)
+// A top-k filter keeping at most TOPK_FAST tokens takes the compact path: every
+// probability outside the k survivors is exactly 0, and adding an exact 0 never
+// changes an f32 running sum, so the sequential sums and CDFs of the reference
+// (index order over the whole row) equal the same sums over the survivors in index
+// order.  LDS: survivor keys (8 B), values (4 B) and top-p keys (8 B) per survivor.
+static constexpr int TOPK_FAST = 1024;
+static constexpr int TOPK_GATHER = 2048;  // candidate keys of the threshold selection (8 B each)
+static constexpr int TOPK_LDS_FLOATS = TOPK_FAST * 5 + TOPK_GATHER * 2;
+__host__ __device__ __forceinline__ bool topk_compact(int top_k, int V) {
+    return top_k > 0 && top_k < V && top_k <= TOPK_FAST;
+}
 
 // ---------------------------------------------------------------------------
 // Sampling-distribution parameters of one row (filtered_probs, sampler.rs:226-278)
@@ -375,6 +386,348 @@ __device__ inline void block_sort_desc(unsigned long long* keys, int np2) {
     }
 }
 
+// Appends make(j, l) for every element j of row[0..V) with take(l, j) to out[0..cap)
+// in arbitrary order and returns the count (taken elements past cap are counted, not
+// written).  Meant for rare takes: a thread tests 16 elements per step into a bit mask
+// and the wave computes slots only in the steps where some lane took one.
+template <class P, class M>
+__device__ inline int gather_rare(const float* row, int V, const P& take, const M& make, unsigned long long* out,
+                                  int cap, AccShared* sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid == 0) sh->n = 0;
+    __syncthreads();
+    const bool vec = ((uintptr_t)row & 15) == 0;
+    for (int j0 = 0; j0 < V; j0 += 16 * ACC_THREADS) {
+        float l[16];
+        int jb[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            jb[q] = j0 + 4 * (q * ACC_THREADS + tid);
+            if (vec && jb[q] + 3 < V) {
+                const float4_t v = *(const float4_t*)(row + jb[q]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) l[4 * q + e] = v[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) l[4 * q + e] = jb[q] + e < V ? row[jb[q] + e] : 0.0f;
+            }
+        }
+        uint32_t mask = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int j = jb[i >> 2] + (i & 3);
+            if (j < V && take(l[i], j)) mask |= 1u << i;
+        }
+        if (__ballot(mask != 0u) == 0ull) continue;  // wave-uniform
+        const int cnt = __popc(mask);
+        int incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int t = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += t;
+        }
+        const int total = __shfl(incl, 63, 64);
+        unsigned base = 0;
+        if (lane == 0) base = atomicAdd(&sh->n, (unsigned)total);
+        base = __builtin_amdgcn_readfirstlane(base);
+        unsigned slot = base + (unsigned)(incl - cnt);
+        while (mask) {
+            const int i = __ffs(mask) - 1;
+            mask &= mask - 1u;
+            if (slot < (unsigned)cap) out[slot] = make(l[i], jb[i >> 2] + (i & 3));
+            slot++;
+        }
+    }
+    __syncthreads();
+    const int n = (int)sh->n;
+    __syncthreads();
+    return n;
+}
+
+// Sequential f32 sum of v[0..n) (index order) on wave 0 from registers, 64 values per
+// load; returned to the whole workgroup.
+__device__ inline float seq_sum_w0(const float* v, int n, AccShared* sh) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float s = 0.0f;
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int cnt = min(64, n - c0);
+            const float x = lane < cnt ? v[c0 + lane] : 0.0f;
+            for (int i = 0; i < cnt; i++) s += readlane_f32(x, i);
+        }
+        if (lane == 0) sh->fb[0] = s;
+    }
+    __syncthreads();
+    const float s = sh->fb[0];
+    __syncthreads();
+    return s;
+}
+
+// Places the n unique keys in[0..n) into out[0..n) in descending order by rank (the
+// number of keys above each), without a sorting network: O(n^2 / threads) LDS
+// broadcast reads and two barriers.
+__device__ inline void rank_sort_desc(const unsigned long long* in, unsigned long long* out, int n) {
+    for (int i = threadIdx.x; i < n; i += ACC_THREADS) {
+        const unsigned long long k = in[i];
+        int r = 0;
+        for (int j = 0; j < n; j++) r += in[j] > k;
+        out[r] = k;
+    }
+    __syncthreads();
+}
+
+// The survivors of a top-k filter (logit keys >= kkey) of `row`, gathered in LDS and
+// sorted by ascending index: keys[i] = (~index << 32 | logit bits).  Returns their
+// count (<= TOPK_FAST; the keys are unique, so it is exactly k).
+__device__ inline int topk_survivors(const float* row, int V, uint64_t kkey, unsigned long long* keys, AccShared* sh) {
+    // the keys >= kkey: logits whose value key is above kkey's, or equal with index <= kkey's
+    const uint32_t kv = (uint32_t)(kkey >> 32);
+    const int kj = (int)~(uint32_t)kkey;
+    const int n = min(gather_rare(
+                          row, V,
+                          [&](float l, int j) {
+                              const uint32_t v = (uint32_t)total_key(l) ^ 0x80000000u;
+                              return v > kv || (v == kv && j <= kj);
+                          },
+                          [](float l, int j) {
+                              return ((unsigned long long)(~(uint32_t)j) << 32) | (unsigned long long)__float_as_uint(l);
+                          },
+                          keys + TOPK_FAST, TOPK_FAST, sh),
+                      TOPK_FAST);
+    // ranked descending by ~index: ascending index
+    rank_sort_desc(keys + TOPK_FAST, keys, n);
+    return n;
+}
+__device__ __forceinline__ int surv_index(unsigned long long k) { return (int)~(uint32_t)(k >> 32); }
+__device__ __forceinline__ float surv_logit(unsigned long long k) { return __uint_as_float((uint32_t)k); }
+
+// Inverse CDF of sample_from_probs (sampler.rs:337-347) over survivors in index order
+// with values v[i] / div (div = 1: the values themselves), on thread 0: the first index
+// with u <= cumulative, as seq_scan_wave reports it (u <= 0 stops at index 0 with the
+// partial sums 0).
+__device__ inline SeqScan block_cdf_small(const unsigned long long* keys, const float* v, int n, float div, float u,
+                                          AccShared* sh) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        SeqScan st = seq_scan_init();
+        if (u <= 0.0f) st.cross = 0;
+        float s = 0.0f;
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int cnt = min(64, n - c0);
+            const float x = lane < cnt ? (div == 1.0f ? v[c0 + lane] : v[c0 + lane] / div) : 0.0f;
+            for (int i = 0; i < cnt; i++) {
+                const float before = s;
+                s += readlane_f32(x, i);
+                if (st.cross < 0 && u <= s) {
+                    st.cross = surv_index(keys[c0 + i]);
+                    st.s_at = s;
+                    st.s_before = before;
+                }
+            }
+        }
+        st.s = s;
+        if (lane == 0) sh->scan = st;
+    }
+    __syncthreads();
+    const SeqScan r = sh->scan;
+    __syncthreads();
+    return r;
+}
+
+// Band of a finite logit l below the row max mx: q = (mx - l) / R (R = mx - mn, taken as
+// (mx - l) * (1 / R)) in quarter octaves, b = 4 * (-exponent of q) - (top two fraction
+// bits of q) - 1, clamped to [0, 63].  b is non-decreasing in l, so {b >= c} is an upper
+// set of logit values; the top quarter of the range is b >= 8.
+__device__ __forceinline__ int topk_band(float l, float mx, float rinv) {
+    const float q = (mx - l) * rinv;
+    if (!(q > 0.0f)) return 63;
+    const uint32_t u = __float_as_uint(q);
+    const int e = (int)((u >> 23) & 255u) - 127;
+    return max(0, min(63, -4 * e - (int)((u >> 21) & 3u) - 1));
+}
+
+// Top-k selection for k <= TOPK_FAST without radix passes: one pass for the finite
+// max / min, one counting the logits of each band in the top quarter of the range, one
+// gathering the narrowest upper set of bands holding at least k logits (at most
+// TOPK_GATHER keys); ranking those keys gives the k-th key, and ranking the k survivors
+// by index puts them in keys[0..k) as topk_survivors leaves them.  Returns false (the
+// caller falls back to the radix select) on non-finite logits, a constant row, or when
+// no band set of at most TOPK_GATHER logits holds k.
+__device__ inline bool topk_fast_select(const float* row, int V, int k, float* buf, AccShared* sh, uint64_t* kkey) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    unsigned long long* keys = (unsigned long long*)buf;
+    unsigned long long* cand = (unsigned long long*)(buf + 5 * TOPK_FAST);
+    unsigned long long* tmp = (unsigned long long*)(buf + 3 * TOPK_FAST);  // k <= TOPK_FAST entries
+    float mx = -INFINITY, mn = INFINITY;
+    int nonfin = 0;
+    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+        if (valid) {
+            if (isfinite(l)) {
+                mx = fmaxf(mx, l);
+                mn = fminf(mn, l);
+            } else {
+                nonfin = 1;
+            }
+        }
+    });
+    mx = wave_max_f32(mx);
+    mn = -wave_max_f32(-mn);
+    nonfin = __any(nonfin) ? 1 : 0;
+    if (lane == 0) {
+        sh->red_f[wid] = mx;
+        sh->red_i[wid] = nonfin;
+        sh->red_k[wid] = __float_as_int(mn);
+    }
+    if (tid < 64) sh->sel.hist[tid] = 0u;
+    __syncthreads();
+    for (int w = 0; w < ACC_WAVES; w++) {
+        mx = fmaxf(mx, sh->red_f[w]);
+        mn = fminf(mn, __int_as_float(sh->red_k[w]));
+        nonfin |= sh->red_i[w];
+    }
+    const float R = mx - mn;
+    if (nonfin || !(R > 0.0f) || !isfinite(R)) {
+        __syncthreads();
+        return false;
+    }
+    const float rinv = 1.0f / R;
+    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+        const int b = valid ? topk_band(l, mx, rinv) : 0;
+        if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
+    });
+    __syncthreads();
+    if (tid == 0) {
+        int pick = -1;
+        unsigned acc = 0, cnt = 0;
+        for (int b = 63; b >= 8; b--) {
+            acc += sh->sel.hist[b];
+            if (acc >= (unsigned)k) {
+                pick = b;
+                cnt = acc;
+                break;
+            }
+        }
+        sh->sel.digit = (pick >= 0 && cnt <= (unsigned)TOPK_GATHER) ? pick : -1;
+        sh->n = 0;
+    }
+    __syncthreads();
+    const int band = sh->sel.digit;
+    if (band < 0) {
+        __syncthreads();
+        return false;
+    }
+    const int c = min(gather_rare(
+                          row, V, [&](float l, int j) { return topk_band(l, mx, rinv) >= band; },
+                          [](float l, int j) { return (unsigned long long)logit_key(l, j); }, cand, TOPK_GATHER, sh),
+                      TOPK_GATHER);
+    // the k largest candidate keys, by rank; the k-th is the top-k cut
+    for (int i = tid; i < c; i += ACC_THREADS) {
+        const unsigned long long key = cand[i];
+        int r = 0;
+        for (int j = 0; j < c; j++) r += cand[j] > key;
+        if (r < k) {
+            const int jj = (int)~(uint32_t)key;
+            tmp[r] = ((unsigned long long)(~(uint32_t)jj) << 32) | (unsigned long long)__float_as_uint(row[jj]);
+            if (r == k - 1) sh->sel.key = key;
+        }
+    }
+    __syncthreads();
+    *kkey = sh->sel.key;
+    // survivors (~index << 32 | logit bits): descending order is ascending index
+    rank_sort_desc(tmp, keys, k);
+    return true;
+}
+
+// filtered_probs (sampler.rs:226-278) for a top-k row on the compact path; f.kkey is set.
+// The k survivors are in buf (keys[0..n), sorted by index, as topk_survivors leaves them).
+__device__ inline void row_filter_topk(float top_p, int n, float* buf, AccShared* sh, RowFilt& f, uint32_t& flags,
+                                       int& status) {
+    const int tid = threadIdx.x;
+    unsigned long long* keys = (unsigned long long*)buf;
+    float* vals = buf + 2 * TOPK_FAST;
+    unsigned long long* pk = (unsigned long long*)(buf + 3 * TOPK_FAST);
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += ACC_THREADS) {
+        const float m = surv_logit(keys[i]) / f.T;
+        if (isfinite(m)) mx = fmaxf(mx, m);
+    }
+    mx = block_max(mx, sh);
+    if (!(mx > -INFINITY)) {  // "all logits are non-finite" (sampler.rs:286-288)
+        status = 1;
+        return;
+    }
+    f.mx = mx;
+    const RowFilt fe = f;
+    for (int i = tid; i < n; i += ACC_THREADS) vals[i] = filt_exp(fe, surv_logit(keys[i]), surv_index(keys[i]));
+    __syncthreads();
+    f.S = seq_sum_w0(vals, n, sh);
+    if (!(f.S > 0.0f) || !isfinite(f.S)) {
+        status = 1;
+        return;
+    }
+    if (!f.topp) return;
+    // top-p: probabilities in descending (stable) order, cumulative until it reaches top_p
+    // probability keys (0 for p = 0), ranked descending: the positive keys are unique and
+    // take ranks 0 .. P-1; every zero key has rank P and writes the 0 that ends the walk
+    unsigned long long* pk_in = (unsigned long long*)(buf + 5 * TOPK_FAST);
+    for (int i = tid; i < n; i += ACC_THREADS) {
+        const float p = vals[i] / f.S;
+        vals[i] = p;
+        pk_in[i] = p > 0.0f ? prob_key(p, surv_index(keys[i])) : 0ull;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += ACC_THREADS) {
+        const unsigned long long k = pk_in[i];
+        int r = 0;
+        for (int j = 0; j < n; j++) r += pk_in[j] > k;
+        pk[r] = k;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // cumulative in descending probability order until it reaches top_p (wave 0, registers)
+        const int lane = tid;
+        float cum = 0.0f;
+        unsigned long long pkey = 0ull;
+        bool done = false;
+        for (int c0 = 0; c0 < n && !done; c0 += 64) {
+            const int cnt = min(64, n - c0);
+            const unsigned long long k = lane < cnt ? pk[c0 + lane] : 0ull;
+            const float p = __uint_as_float((uint32_t)(k >> 32));
+            for (int i = 0; i < cnt; i++) {
+                const float pi = readlane_f32(p, i);
+                if (!(pi > 0.0f)) {  // the zero keys: every positive probability taken
+                    done = true;
+                    break;
+                }
+                const float before = cum;
+                cum += pi;
+                if (top_p <= cum) {
+                    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, i);
+                    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), i);
+                    pkey = ((unsigned long long)hi << 32) | lo;
+                    if (fminf(cum - top_p, top_p - before) < 1e-6f && lane == 0) sh->ib[7] = (int)ACCEPT_FLAG_TOPP_NEAR;
+                    done = true;
+                    break;
+                }
+            }
+        }
+        if (lane == 0) sh->sel.key = pkey;
+    }
+    __syncthreads();
+    f.pkey = sh->sel.key;
+    // renormalise over the kept probabilities, sequential in index order
+    float* kept = (float*)(buf + 5 * TOPK_FAST);  // pk_in is dead after the ranking
+    for (int i = tid; i < n; i += ACC_THREADS) {
+        const float p0 = vals[i];
+        kept[i] = (p0 > 0.0f && prob_key(p0, surv_index(keys[i])) >= f.pkey) ? p0 : 0.0f;
+    }
+    __syncthreads();
+    f.R2 = seq_sum_w0(kept, n, sh);
+    flags |= (uint32_t)sh->ib[7];
+    __syncthreads();
+    if (!(f.R2 > 0.0f) || !isfinite(f.R2)) status = 1;
+}
+
 // Distribution parameters of a sampled row (TopKTopP at T > EPSILON):
 // filtered_probs (sampler.rs:226-278).  status 1: no finite logit survives or a
 // normaliser is not positive (the reference returns Err).  flags: the top-p
@@ -393,13 +746,24 @@ __device__ __forceinline__ void row_filter(const float* row, int V, float T, int
     status = 0;
     // ---- top-k: the k-th largest logit key under the stable total_cmp ranking ----
     if (top_k > 0 && top_k < V) {
+        auto kf = [](float l, int j, bool& ok) {
+            ok = true;
+            return logit_key(l, j);
+        };
+        if (topk_compact(top_k, V)) {
+            if (tid == 0) sh->ib[7] = 0;
+            __syncthreads();
+            int n = top_k;
+            if (!topk_fast_select(row, V, top_k, buf, sh, &f.kkey)) {
+                unsigned tot;
+                f.kkey = select_desc(kf, row, V, top_k, ~0ull, sh, &tot);
+                n = topk_survivors(row, V, f.kkey, (unsigned long long*)buf, sh);
+            }
+            row_filter_topk(top_p, n, buf, sh, f, flags, status);
+            return;
+        }
         unsigned tot;
-        f.kkey = select_desc(
-            [](float l, int j, bool& ok) {
-                ok = true;
-                return logit_key(l, j);
-            },
-            row, V, top_k, ~0ull, sh, &tot);
+        f.kkey = select_desc(kf, row, V, top_k, ~0ull, sh, &tot);
     }
     // ---- max of the finite masked logits ----
     float mx = -INFINITY;
@@ -500,6 +864,51 @@ __device__ __forceinline__ void row_filter(const float* row, int V, float T, int
 }
 
 __device__ __forceinline__ int acc_chunk_floats(int V) { return V < ACC_CHUNK ? V : ACC_CHUNK; }
+
+// Row statistics with every field read once into scalar registers (they are uniform).
+__device__ __forceinline__ RowFilt rs_load_uniform(const uint32_t* w, float T) {
+    RowFilt f = rs_load(w, T);
+    f.mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f.mx)));
+    f.S = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f.S)));
+    f.R2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f.R2)));
+    f.kkey = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)f.kkey) |
+             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(f.kkey >> 32)) << 32);
+    f.pkey = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)f.pkey) |
+             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(f.pkey >> 32)) << 32);
+    f.topp = __builtin_amdgcn_readfirstlane(f.topp);
+    return f;
+}
+
+// The resolver's draw on the compact top-k path.  wd == nullptr: the bonus draw from
+// the target row's distribution.  Otherwise the residual max(0, p - q), which is 0
+// outside the target row's top-k survivors: its exact mass, then its exact CDF.
+__device__ __noinline__ void resolve_compact(const uint32_t* wt, const uint32_t* wd, const float* tl, const float* dl,
+                                             int V, float T, float u, float* lds, AccShared* sh, SeqScan* cdf,
+                                             int* status) {
+    const int tid = threadIdx.x;
+    unsigned long long* ckeys = (unsigned long long*)lds;
+    float* cvals = lds + 2 * TOPK_FAST;
+    const RowFilt ft = rs_load_uniform(wt, T);
+    const int n = topk_survivors(tl, V, ft.kkey, ckeys, sh);
+    if (wd) {
+        const RowFilt fd = rs_load_uniform(wd, T);
+        for (int i = tid; i < n; i += ACC_THREADS) {
+            const int j = surv_index(ckeys[i]);
+            const float d = filt_prob(ft, surv_logit(ckeys[i]), j) - filt_prob(fd, dl[j], j);
+            cvals[i] = d > 0.0f ? d : 0.0f;
+        }
+        __syncthreads();
+        const float R = seq_sum_w0(cvals, n, sh);
+        if (!isfinite(R) || R <= FLT_EPSILON)
+            *status = 1;
+        else
+            *cdf = block_cdf_small(ckeys, cvals, n, R, u, sh);
+    } else {
+        for (int i = tid; i < n; i += ACC_THREADS) cvals[i] = filt_prob(ft, surv_logit(ckeys[i]), surv_index(ckeys[i]));
+        __syncthreads();
+        *cdf = block_cdf_small(ckeys, cvals, n, 1.0f, u, sh);
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Acceptance kernel: grid = B * (target_rows + K) workgroups.
@@ -632,7 +1041,12 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
             }
         }
         SeqScan cdf = seq_scan_init();
-        if (rej >= 0) {
+        if (topk_compact(a.top_k, V)) {
+            const int row = rej >= 0 ? rej : np;
+            resolve_compact(rs0 + row * ACC_RS_WORDS, rej >= 0 ? rsd0 + rej * ACC_RS_WORDS : nullptr,
+                            trow0 + (size_t)row * V, rej >= 0 ? drow0 + (size_t)rej * V : nullptr, V, T, u, lds, &sh,
+                            &cdf, &status);
+        } else if (rej >= 0) {
             // residual max(0, p - q): exact mass, then the exact CDF of r / mass
             const RowFilt ft = rs_load(rs0 + rej * ACC_RS_WORDS, T);
             const RowFilt fd = rs_load(rsd0 + rej * ACC_RS_WORDS, T);
@@ -680,10 +1094,11 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
     }
 }
 
-static size_t accept_lds_bytes(int V, int greedy, int top_p_active) {
+static size_t accept_lds_bytes(int V, int greedy, int top_p_active, int top_k) {
     if (greedy) return 0;
     size_t f = 2 * (size_t)(V < ACC_CHUNK ? V : ACC_CHUNK);
     if (top_p_active && f < (size_t)TOPP_LDS_FLOATS) f = TOPP_LDS_FLOATS;
+    if (topk_compact(top_k, V) && f < (size_t)TOPK_LDS_FLOATS) f = TOPK_LDS_FLOATS;
     return f * sizeof(float);
 }
 
@@ -691,7 +1106,7 @@ int launch_accept(const AcceptArgs& a_in, hipStream_t stream) {
     AcceptArgs a = a_in;
     const int rows = a.target_rows + a.K;
     const bool topp = a.top_p > 0.0f && a.top_p < 1.0f;
-    const size_t lds = accept_lds_bytes(a.V, a.greedy, topp);
+    const size_t lds = accept_lds_bytes(a.V, a.greedy, topp, a.top_k);
     if (lds > MAX_DYN_LDS) return 3;
     a.chunk = a.V < ACC_CHUNK ? a.V : ACC_CHUNK;
     if (a.chunk < 1) a.chunk = 1;
@@ -863,6 +1278,7 @@ int launch_candidates(const CandArgs& a_in, hipStream_t stream) {
     const bool topp = a.top_p > 0.0f && a.top_p < 1.0f;
     size_t fl = a.greedy ? 0 : 2 * (size_t)(a.V < CAND_CHUNK ? a.V : CAND_CHUNK);
     if (!a.greedy && topp && fl < (size_t)TOPP_LDS_FLOATS) fl = TOPP_LDS_FLOATS;
+    if (!a.greedy && topk_compact(a.top_k, a.V) && fl < (size_t)TOPK_LDS_FLOATS) fl = TOPK_LDS_FLOATS;
     const size_t lds = fl * sizeof(float);
     const size_t cap = MAX_DYN_LDS - sizeof(unsigned long long) * ACC_THREADS * CAND_MAX;
     if (lds > cap) return 3;

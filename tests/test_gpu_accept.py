@@ -216,7 +216,8 @@ def test_cli_default_sampler_on_c2_shapes(ctx):
     assert (ref["accept_len"] < 4).any() and (ref["accept_len"] > 0).any()
 
 
-@pytest.mark.parametrize("top_k,top_p", [(50, 0.0), (0, 0.9), (1, 0.0), (700, 0.95), (31999, 0.5)])
+@pytest.mark.parametrize("top_k,top_p", [(50, 0.0), (0, 0.9), (1, 0.0), (700, 0.95), (1024, 0.9), (1025, 0.0),
+                                         (31999, 0.5)])
 def test_top_k_top_p_variants_match_oracle(ctx, top_k, top_p):
     """top-k alone, top-p alone (several top-p pages of 4096 sorted candidates on
     the flat rows), k = 1, and both, on peaked N(0, 3^2) and flat N(0, 0.3^2) rows."""
