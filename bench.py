@@ -337,13 +337,15 @@ def run_c3(args):
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_hbm_traffic.txt")
 TRAFFIC_PROFILE_B32 = os.path.join(ROOT, "profiles", "verify_c4_b32_hbm_traffic.txt")
+STATS_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_kernel_stats.txt")
 
 
 def measured_traffic(key="traffic_bytes_per_launch", path=None):
-    """HBM bytes per launch of a kernel class from a committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE runs of this script, scaled by a plain-copy calibration):
-    the INT4 GEMV and the decode attention of the batch-1 verify, the many-row INT4 GEMM
-    of the batch-32 verify."""
+    """A `key = value` line of a committed rocprofv3 summary under profiles/: HBM bytes per
+    launch of a kernel class from the --pmc summaries (FETCH_SIZE and WRITE_SIZE runs of
+    this script, scaled by a plain-copy calibration: the INT4 GEMV and the decode attention
+    of the batch-1 verify, the many-row INT4 GEMM of the batch-32 verify), or the mean
+    INT4 GEMV duration of the batch-1 kernel-trace summary."""
     try:
         for line in open(path or TRAFFIC_PROFILE):
             if line.startswith(key + " "):
@@ -477,6 +479,10 @@ def run_c5(args):
         print(f"# c5 B={B}: verify {t * 1e3:.3f} ms, {res[B]['rows_per_s']:.0f} rows/s, experts/layer "
               f"{used / L:.1f}, moe block (route + experts + combine) {res[B]['moe_ffn_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     m.close()
+    return res
+
+
+def c5_line(args, res):
     bmain = max(args.batches)
     r = res[bmain]
     line = {
@@ -543,6 +549,48 @@ def probe_memory():
             "graph_kernel_floor_us_mean": round(sum(per) / len(per), 2)}
 
 
+def summarize_trace(path, title, cmd):
+    """Text summary of a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv) for profiles/:
+    per-kernel calls / total / mean / min / max, the verify-path kernels by workgroup
+    count, and the mean duration of the INT4 GEMV launches (gemv_tile_kernel<3, ...>) as
+    `int4_gemv_avg_launch_us`, which bench.py quotes beside its own dispatch-timed figure."""
+    import csv
+    rows = list(csv.DictReader(open(path)))
+    col = {k.lower(): k for k in rows[0].keys()} if rows else {}
+    kn, t0, t1 = col.get("kernel_name"), col.get("start_timestamp"), col.get("end_timestamp")
+    wgx = col.get("grid_size_x") or col.get("grid_x")
+    wsx = col.get("workgroup_size_x") or col.get("workgroup_x")
+    stats, byname_wg = {}, {}
+    for r in rows:
+        name = r[kn].split("(")[0] if r[kn].startswith("void ") else r[kn]
+        d = (int(r[t1]) - int(r[t0])) / 1000.0
+        st = stats.setdefault(name, [0, 0.0, 1e30, 0.0])
+        st[0] += 1
+        st[1] += d
+        st[2] = min(st[2], d)
+        st[3] = max(st[3], d)
+        if wgx and wsx:
+            byname_wg.setdefault(name, set()).add(int(r[wgx]) // max(1, int(r[wsx])))
+    total = sum(v[1] for v in stats.values())
+    out = [f"# {title}", "# command (repository root, after `cd /tmp && export TMPDIR=/tmp`):", f"#   {cmd}",
+           f"# source: {os.path.basename(path)} of that run (times in microseconds); summary by "
+           f"`python3 bench.py --summarize-trace <run_kernel_trace.csv>`", "",
+           f"{'kernel':74s} {'calls':>6s} {'total_ms':>9s} {'avg_us':>8s} {'min_us':>8s} {'max_us':>8s} {'pct':>6s}"]
+    for name, (n, t, lo, hi) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"{name[:74]:74s} {n:6d} {t / 1e3:9.3f} {t / n:8.2f} {lo:8.2f} {hi:8.2f} {100 * t / total:6.2f}")
+    g = [(n, t) for name, (n, t, _, _) in stats.items() if name.startswith("void aarh::gemv_tile_kernel<3,")]
+    if g:
+        n, t = sum(x[0] for x in g), sum(x[1] for x in g)
+        out += ["", f"# all INT4 GEMV launches (gemv_tile_kernel<3, ...>): {n} dispatches, {t / 1e3:.3f} ms, mean "
+                    f"{t / n:.3f} us", f"int4_gemv_avg_launch_us = {t / n:.3f}"]
+    hot = [n for n in byname_wg if any(k in n for k in ("gemv_tile", "gemm_kernel", "attn", "accept", "candidates"))]
+    if hot:
+        out += ["", "# verify-path kernels: workgroups per launch"]
+        for name in sorted(hot):
+            out.append(f"{name[:74]:74s} wg {','.join(str(w) for w in sorted(byname_wg[name]))}")
+    return "\n".join(out) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -562,7 +610,14 @@ def main():
     ap.add_argument("--probe-memory", action="store_true",
                     help="run only two reference measurements of the device: the HBM rate a plain device "
                          "copy reaches, and the per-kernel floor of a replayed graph")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print a profiles/ summary of a rocprofv3 --kernel-trace CSV and exit")
+    ap.add_argument("--summary-title", default="rocprofv3 kernel statistics")
+    ap.add_argument("--summary-cmd", default="")
     args = ap.parse_args()
+    if args.summarize_trace:
+        sys.stdout.write(summarize_trace(args.summarize_trace, args.summary_title, args.summary_cmd))
+        return
     if args.probe_memory:
         print(json.dumps(probe_memory()))
         return
@@ -586,7 +641,7 @@ def main():
         import torch  # torch's device runtime starts before the library's (the c2 inputs are torch tensors)
         torch.zeros(1, device="cuda")
     if args.workload == "c5":
-        run_c5(args)
+        c5_line(args, run_c5(args))
         return
     if args.workload == "c2":
         print(json.dumps({"c2_acceptance": run_c2(args)}))
@@ -598,11 +653,12 @@ def main():
         print(json.dumps({"serve_continuous": run_serve(args)}))
         return
     res = run_c4(args)
-    c2 = c3 = serve = None
+    c2 = c3 = serve = c5 = None
     if not args.no_extra:
         c2 = run_c2(args)
         c3 = run_c3(args)
         serve = run_serve(args)
+        c5 = run_c5(argparse.Namespace(batches=[1, 32], warmup=2, steps=5))
     bmain = max(args.batches)
     main_r = res[bmain]
     b1 = res.get(1, main_r)
@@ -619,6 +675,12 @@ def main():
         "avg_launch_us": round(g1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(g1["avg_bytes"]),
     }
+    # the same kernels' mean duration in the committed rocprofv3 kernel trace of this workload
+    prof_us = measured_traffic("int4_gemv_avg_launch_us", STATS_PROFILE)
+    if prof_us:
+        gbs = g1["avg_bytes"] / (prof_us * 1e-6) / 1e9
+        roof["profile"] = {"file": os.path.relpath(STATS_PROFILE, ROOT), "avg_launch_us": prof_us,
+                           "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     a1 = b1["attention"]
     roof_att = {
         "kernel": "attn_mfma_kernel<INT8> (decode attention of the batch-1 verify step, 4096-token INT8 cache)",
@@ -672,6 +734,8 @@ def main():
         "c3_verify": {str(b): {k: v[k] for k in ("ms_wall", "alg_bytes", "hbm_gbs", "hbm_frac")}
                       for b, v in c3.items()} if c3 else None,
         "serve_continuous": serve,
+        "c5_verify": {str(b): {k: v[k] for k in ("ms_per_step", "rows_per_s", "experts_touched_per_layer", "moe_ffn_gbs")}
+                      for b, v in c5.items()} if c5 else None,
         "cpu_baseline": cpu,
         "detail": {"c4": {str(b): r for b, r in res.items()},
                    "c3": {str(b): v for b, v in c3.items()} if c3 else None},
