@@ -20,6 +20,7 @@ import ctypes as C
 import os
 import weakref
 from dataclasses import dataclass, field
+from typing import Optional
 
 import numpy as np
 
@@ -71,7 +72,12 @@ class _Cfg(C.Structure):
                                           "n_kv_heads", "max_seq_len")] + \
                [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
                [(n, C.c_int32) for n in ("num_future_tokens", "weight_format", "lm_head_format", "kv_format",
-                                          "max_batch", "max_rows")]
+                                          "max_batch", "max_rows", "untied_lm_head")]
+
+
+class _RopeScaling(C.Structure):
+    _fields_ = [("method", C.c_int32), ("original_max_seq_len", C.c_int32), ("factor", C.c_double),
+                ("beta_fast", C.c_double), ("beta_slow", C.c_double), ("attn_factor", C.c_double)]
 
 
 class _LatCfg(C.Structure):
@@ -170,6 +176,8 @@ def lib():
         "aarh_session_set_rng_offsets": (C.c_int, [_P, _P]),
         "aarh_top_candidates": (C.c_int, [_P, _P, C.c_int, C.c_int, C.POINTER(_Sampler), C.c_int, _P, _P, _P]),
         "aarh_set_graphs": (C.c_int, [_P, C.c_int]),
+        "aarh_set_rope_scaling": (C.c_int, [_P, C.POINTER(_RopeScaling)]),
+        "aarh_gguf_rope_scaling": (C.c_int, [C.c_char_p, C.POINTER(_RopeScaling)]),
         "aarh_prof_enable": (C.c_int, [_P, C.c_int]),
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
@@ -216,7 +224,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_lat_expert_counts", "aarh_lat_prof_enable", "aarh_lat_prof_get", "aarh_load_tensor_packed_i4",
             "aarh_lat_load_tensor_packed_i4", "aarh_packed_i4_params", "aarh_spec_session_begin",
             "aarh_spec_session_step", "aarh_spec_session_result", "aarh_spec_session_candidates",
-            "aarh_spec_session_rng_offsets", "aarh_spec_session_set_rng_offsets", "aarh_spec_session_end"]
+            "aarh_spec_session_rng_offsets", "aarh_spec_session_set_rng_offsets", "aarh_spec_session_end",
+            "aarh_set_rope_scaling", "aarh_gguf_rope_scaling"]
 
 
 def _ptr(a):
@@ -287,6 +296,27 @@ def packed_i4_params(t: PackedInt4Tensor):
     return sh.reshape(rows, -1), zh.reshape(rows, -1)
 
 
+ROPE_METHODS = {"yarn": 1, "ntk": 2, "linear": 3}
+
+
+@dataclass
+class RopeScaling:
+    """RopeScalingConfig (core/src/config.rs:19-47; field defaults as its Default impl):
+    method "yarn" | "ntk" | "linear"."""
+    method: str = "yarn"
+    factor: float = 1.0
+    original_max_seq_len: int = 0
+    beta_fast: float = 32.0
+    beta_slow: float = 1.0
+    attn_factor: float = 1.0
+
+    def _c(self):
+        if self.method not in ROPE_METHODS:
+            raise ConfigError(f"unknown rope_scaling method {self.method!r}")
+        return _RopeScaling(ROPE_METHODS[self.method], int(self.original_max_seq_len), float(self.factor),
+                            float(self.beta_fast), float(self.beta_slow), float(self.attn_factor))
+
+
 @dataclass
 class ModelConfig:
     """ModelConfig subset (core/src/config.rs:734-776) plus MtpConfig.num_future_tokens."""
@@ -303,16 +333,27 @@ class ModelConfig:
     weight_format: int = W_F32
     lm_head_format: int = 0
     kv_format: int = KV_F32
+    tie_embeddings: bool = True
+    rope_scaling: Optional[RopeScaling] = None
 
     @classmethod
     def from_gguf(cls, path, **overrides):
-        """Model shape from a GGUF v1 file's config (load_gguf_tensors, gguf.rs:91-125);
-        storage formats come from `overrides` (defaults as the dataclass)."""
+        """Model shape from a GGUF v1 file's config (load_gguf_tensors, gguf.rs:91-125),
+        tie_embeddings and rope_scaling included; storage formats come from `overrides`
+        (defaults as the dataclass)."""
         c = _Cfg()
-        _host_check(lib().aarh_gguf_config(os.fsencode(path), C.byref(c)))
+        p = os.fsencode(path)
+        _host_check(lib().aarh_gguf_config(p, C.byref(c)))
+        rs = _RopeScaling()
+        _host_check(lib().aarh_gguf_rope_scaling(p, C.byref(rs)))
+        scaling = None
+        if rs.method:
+            name = {v: k for k, v in ROPE_METHODS.items()}[rs.method]
+            scaling = RopeScaling(name, rs.factor, rs.original_max_seq_len, rs.beta_fast, rs.beta_slow, rs.attn_factor)
         kw = dict(vocab_size=c.vocab_size, hidden_dim=c.hidden_dim, ffn_dim=c.ffn_dim, n_layers=c.n_layers,
                   n_heads=c.n_heads, n_kv_heads=c.n_kv_heads, max_seq_len=c.max_seq_len, rope_theta=c.rope_theta,
-                  norm_eps=c.norm_eps, num_future_tokens=c.num_future_tokens)
+                  norm_eps=c.norm_eps, num_future_tokens=c.num_future_tokens,
+                  tie_embeddings=not c.untied_lm_head, rope_scaling=scaling)
         kw.update(overrides)
         return cls(**kw)
 
@@ -410,7 +451,7 @@ class HipModel:
         self.cfg = cfg
         c = _Cfg(cfg.vocab_size, cfg.hidden_dim, cfg.ffn_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads,
                  cfg.max_seq_len, cfg.rope_theta, cfg.norm_eps, cfg.num_future_tokens, cfg.weight_format,
-                 cfg.lm_head_format, cfg.kv_format, max_batch, max_rows)
+                 cfg.lm_head_format, cfg.kv_format, max_batch, max_rows, 0 if cfg.tie_embeddings else 1)
         h = _P()
         st = lib().aarh_create(device, C.byref(c), C.byref(h))
         self.h = h
@@ -418,6 +459,12 @@ class HipModel:
             msg = lib().aarh_last_error(h).decode() if h else "aarh_create failed"
             self.close()
             raise _ERRS.get(st, AarambhError)(msg)
+        if cfg.rope_scaling is not None:
+            try:
+                self.set_rope_scaling(cfg.rope_scaling)
+            except AarambhError:
+                self.close()
+                raise
         self.max_batch = max_batch
         self.max_rows = max_rows
         _LIVE.add(self)
@@ -526,6 +573,11 @@ class HipModel:
     def set_replay_schedule(self, schedule):
         """REPLAY_REPLACEMENT (default) or REPLAY_REFERENCE (mtp_speculative.rs:302-313)."""
         self._check(lib().aarh_set_replay_schedule(self.h, int(schedule)))
+
+    def set_rope_scaling(self, scaling: Optional[RopeScaling]):
+        """RopeCache::from_config with rope_scaling (rope_scaling.rs:24-92); None: unscaled."""
+        self._check(lib().aarh_set_rope_scaling(self.h, None if scaling is None else C.byref(scaling._c())))
+        self.rope_scaling = scaling
 
     def set_graphs(self, on=True):
         """Replay captured HIP graphs for repeated verify-forward shapes (default on)."""

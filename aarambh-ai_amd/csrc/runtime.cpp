@@ -43,7 +43,7 @@ struct HeadW {
 // per layer [norm1, wq, wk, wv, wo, norm2, w_gate, w_up, w_down], final_norm,
 // per MTP head [trunk_norm, token_norm, refine.norm1, wq, wk, wv, wo,
 // refine.norm2, w_gate, w_up, w_down, output_norm].
-enum Part { P_EMBED, P_NORM, P_WQ, P_WK, P_WV, P_WO, P_GATE, P_UP, P_DOWN };
+enum Part { P_EMBED, P_NORM, P_WQ, P_WK, P_WV, P_WO, P_GATE, P_UP, P_DOWN, P_LMHEAD };
 struct TensorSlot {
     std::string name;
     int64_t rows = 0, cols = 0;
@@ -728,6 +728,9 @@ static int build_slots(aarh_ctx* c) {
         add(p + "refine.ffn.w_down.weight", H, F, AARH_T_LINEAR, P_DOWN, nullptr, b);
         add(p + "output_norm.weight", 1, H, AARH_T_NORM, P_NORM, &hw->out_norm, nullptr);
     }
+    // LmHead::untied_with_qat (model.rs:239-248): its own [vocab, hidden] weight, which the
+    // MTP heads' output projection shares (model.rs:250-262)
+    if (g.untied_lm_head) add("lm_head.weight", g.vocab_size, H, AARH_T_EMBED, P_LMHEAD, nullptr, nullptr);
     return 0;
 }
 
@@ -743,6 +746,118 @@ static int alloc_block(aarh_ctx* c, BlockW& b) {
     if ((r = alloc_tensor(c, b.down, fmt, H, c->Fp))) return r;
     return 0;
 }
+
+}  // extern "C"
+
+namespace {
+
+// Inverse frequencies and cos / sin factor of the model's RoPE (inverse_frequencies_for_config,
+// rope_scaling.rs:24-33): base frequencies (:6-11), linear (:46-52), NTK-aware theta (:14-22,
+// 53-56) or YaRN (:62-92, correction range :107-136), all in f64 and cast to f32.
+// Returns 0, or AARH_ERR_CONFIG with RopeScalingConfig::validate's message (config.rs:52-98).
+int rope_frequencies(int hd, double theta, int max_seq_len, const aarh_rope_scaling* s, std::vector<float>& inv,
+                     float* attn, std::string& err) {
+    const int half = hd / 2;
+    inv.assign(half, 0.0f);
+    *attn = 1.0f;
+    auto base = [&](double th, std::vector<float>& out) {
+        for (int i = 0; i < half; i++) out[i] = (float)(1.0 / std::pow(th, 2.0 * (double)i / (double)hd));
+    };
+    if (!s || s->method == AARH_ROPE_NONE) {
+        base(theta, inv);
+        return 0;
+    }
+    if (!(s->factor > 1.0) || !std::isfinite(s->factor)) {
+        err = "rope_scaling.factor must be finite and greater than 1.0";
+        return AARH_ERR_CONFIG;
+    }
+    if (s->original_max_seq_len <= 0) {
+        err = "rope_scaling.original_max_seq_len must be non-zero";
+        return AARH_ERR_CONFIG;
+    }
+    if (max_seq_len < s->original_max_seq_len) {
+        err = "max_seq_len " + std::to_string(max_seq_len) + " must be >= rope_scaling.original_max_seq_len " +
+              std::to_string(s->original_max_seq_len);
+        return AARH_ERR_CONFIG;
+    }
+    if (hd <= 2) {
+        err = "head_dim must be greater than 2 for RoPE scaling";
+        return AARH_ERR_CONFIG;
+    }
+    if (!(s->attn_factor > 0.0) || !std::isfinite(s->attn_factor)) {
+        err = "rope_scaling.attn_factor must be finite and positive";
+        return AARH_ERR_CONFIG;
+    }
+    if (s->method == AARH_ROPE_YARN) {
+        if (!(s->beta_fast > 0.0) || !(s->beta_slow > 0.0) || !std::isfinite(s->beta_fast) ||
+            !std::isfinite(s->beta_slow)) {
+            err = "rope_scaling beta values must be finite and positive";
+            return AARH_ERR_CONFIG;
+        }
+        if (s->beta_fast <= s->beta_slow) {
+            err = "rope_scaling.beta_fast must be greater than beta_slow";
+            return AARH_ERR_CONFIG;
+        }
+    }
+    *attn = (float)s->attn_factor;
+    if (s->method == AARH_ROPE_LINEAR) {
+        base(theta, inv);
+        const float f = (float)s->factor;
+        for (int i = 0; i < half; i++) inv[i] = inv[i] / f;
+        return 0;
+    }
+    if (s->method == AARH_ROPE_NTK) {
+        base(theta * std::pow(s->factor, (double)hd / ((double)hd - 2.0)), inv);
+        return 0;
+    }
+    if (s->method != AARH_ROPE_YARN) {
+        err = "unknown rope_scaling method";
+        return AARH_ERR_CONFIG;
+    }
+    // YaRN: blend of the extrapolated and interpolated frequency by a linear ramp over the
+    // correction range [low, high] of dimension indices
+    const double pi = 3.14159265358979323846;
+    auto corr_dim = [&](double rot) {
+        return (double)hd * std::log((double)s->original_max_seq_len / (rot * 2.0 * pi)) / (2.0 * std::log(theta));
+    };
+    const double max_dim = (double)std::max(0, half - 1);
+    double low = std::min(std::max(std::floor(corr_dim(s->beta_fast)), 0.0), max_dim);
+    double high = std::min(std::max(std::ceil(corr_dim(s->beta_slow)), 0.0), max_dim);
+    if (std::fabs(high - low) < 2.220446049250313e-16) high += 0.001;
+    for (int i = 0; i < half; i++) {
+        const double extrapolated = 1.0 / std::pow(theta, 2.0 * (double)i / (double)hd);
+        const double interpolated = extrapolated / s->factor;
+        const double ramp = std::min(std::max(((double)i - low) / (high - low), 0.0), 1.0);
+        inv[i] = (float)(interpolated * ramp + extrapolated * (1.0 - ramp));
+    }
+    return 0;
+}
+
+// cos / sin tables [positions][hd / 2] (rope.rs:43-72: angle pos * freq in f32, times the
+// attention factor) uploaded into the context's table buffers.
+int upload_rope(aarh_ctx* c, const aarh_rope_scaling* s) {
+    const int half = c->hd / 2, npos = c->cfg.max_seq_len + PAD_SLACK;
+    std::vector<float> inv;
+    float attn = 1.0f;
+    std::string err;
+    int r = rope_frequencies(c->hd, (double)c->cfg.rope_theta, c->cfg.max_seq_len, s, inv, &attn, err);
+    if (r) return fail(c, r, "%s", err.c_str());
+    std::vector<float> cs((size_t)npos * half), sn((size_t)npos * half);
+    for (int p = 0; p < npos; p++)
+        for (int i = 0; i < half; i++) {
+            const float a = (float)p * inv[i];
+            cs[(size_t)p * half + i] = cosf(a) * attn;
+            sn[(size_t)p * half + i] = sinf(a) * attn;
+        }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
 
 int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     if (!cfg || !out) return AARH_ERR_CONFIG;
@@ -775,7 +890,7 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     if (g.weight_format != AARH_W_F32 && g.ffn_dim % 128)
         return bad(AARH_ERR_UNSUPPORTED, "quantised ffn_dim must be a multiple of 128");
     if (g.weight_format < 0 || g.weight_format > 3 || (g.lm_head_format != 0 && g.lm_head_format != 1) ||
-        g.kv_format < 0 || g.kv_format > 2)
+        g.kv_format < 0 || g.kv_format > 2 || (g.untied_lm_head != 0 && g.untied_lm_head != 1))
         return bad(AARH_ERR_CONFIG, "unknown weight / lm head / kv format");
     if (g.max_rows > 512) return bad(AARH_ERR_UNSUPPORTED, "max_rows must be <= 512");
     c->Fp = (c->F + 127) / 128 * 128;
@@ -804,7 +919,12 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
         c->lm.fmt = WF_F32;
         c->lm.N = c->V;
         c->lm.K = c->H;
-        c->lm.w = (uint8_t*)c->embed;  // row-major f32 weights are shared
+        if (!g.untied_lm_head) {
+            c->lm.w = (uint8_t*)c->embed;  // row-major f32 weights are shared
+        } else {
+            if (dalloc(c, &c->lm.w, weight_bytes(WF_F32, c->V, c->H))) return AARH_ERR_DEVICE;
+            HIPCHK(c, hipMemset(c->lm.w, 0, weight_bytes(WF_F32, c->V, c->H)));
+        }
     } else if ((r = alloc_tensor(c, c->lm, WF_BF16, c->V, c->H))) {
         return r;
     }
@@ -822,20 +942,9 @@ int aarh_create(int device, const aarh_model_config* cfg, aarh_ctx** out) {
     }
     // RoPE tables (rope_scaling.rs:6-11, rope.rs:43-72), computed on the host in f32 like the reference.
     {
-        const int half = c->hd / 2;
-        const int npos = g.max_seq_len + PAD_SLACK;
-        std::vector<float> cs((size_t)npos * half), sn((size_t)npos * half), inv(half);
-        for (int i = 0; i < half; i++)
-            inv[i] = (float)(1.0 / std::pow((double)g.rope_theta, 2.0 * (double)i / (double)c->hd));
-        for (int p = 0; p < npos; p++)
-            for (int i = 0; i < half; i++) {
-                float a = (float)p * inv[i];
-                cs[(size_t)p * half + i] = cosf(a);
-                sn[(size_t)p * half + i] = sinf(a);
-            }
-        if (dalloc(c, &c->rope_cos, cs.size() * 4) || dalloc(c, &c->rope_sin, sn.size() * 4)) return AARH_ERR_DEVICE;
-        HIPCHK(c, hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-        HIPCHK(c, hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+        const size_t n = (size_t)(g.max_seq_len + PAD_SLACK) * (c->hd / 2);
+        if (dalloc(c, &c->rope_cos, n * 4) || dalloc(c, &c->rope_sin, n * 4)) return AARH_ERR_DEVICE;
+        if ((r = upload_rope(c, nullptr))) return r;
     }
     // KV cache
     {
@@ -965,10 +1074,21 @@ static int place_f32_staging(aarh_ctx* c, int id) {
     const TensorSlot& s = c->slots[id];
     const int64_t n = s.rows * s.cols;
     if (s.part == P_EMBED) {
+        // the tied LM head reads the embedding: row-major f32 in place, or its own bf16 tiles
         if (c->embed_fmt == WF_F32) {
             HIPCHK(c, hipMemcpyAsync(c->embed, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
         } else {
             KCHK(c, launch_to_bf16(c->staging, (uint16_t*)c->embed, n, c->stream));
+            if (!c->cfg.untied_lm_head)
+                KCHK(c, launch_quantise_tiled(c->staging, c->V, c->H, WF_BF16, c->lm.w, nullptr, nullptr, 0, c->V, 0,
+                                              c->stream));
+        }
+        return 0;
+    }
+    if (s.part == P_LMHEAD) {
+        if (c->embed_fmt == WF_F32) {
+            HIPCHK(c, hipMemcpyAsync(c->lm.w, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
+        } else {
             KCHK(c, launch_quantise_tiled(c->staging, c->V, c->H, WF_BF16, c->lm.w, nullptr, nullptr, 0, c->V, 0,
                                           c->stream));
         }
@@ -1419,6 +1539,11 @@ int aarh_set_graphs(aarh_ctx* c, int enable) {
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
     c->gcache.clear();
     return 0;
+}
+
+int aarh_set_rope_scaling(aarh_ctx* c, const aarh_rope_scaling* s) {
+    if (!c) return AARH_ERR_CONFIG;
+    return upload_rope(c, s);
 }
 
 int aarh_prof_enable(aarh_ctx* c, int enable) {

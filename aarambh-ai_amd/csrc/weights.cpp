@@ -552,6 +552,52 @@ int fail_ctx(aarh_ctx* c, int code, const std::string& msg) {
     return code;
 }
 
+// ModelConfig.rope_scaling (config.rs:19-47, serde(default) per field, method in snake_case)
+// into *out; method AARH_ROPE_NONE when the key is absent or null.  Values are checked by
+// the table builder (RopeScalingConfig::validate), not here.
+int parse_rope_scaling(const JVal* cfg, aarh_rope_scaling* out, std::string& err) {
+    *out = aarh_rope_scaling{AARH_ROPE_NONE, 0, 1.0, 32.0, 1.0, 1.0};
+    const JVal* rs = cfg->get("rope_scaling");
+    if (!rs || rs->kind == JVal::NUL) return 0;
+    if (rs->kind != JVal::OBJ) {
+        err = "GGUF config rope_scaling is not an object";
+        return AARH_ERR_CHECKPOINT;
+    }
+    out->method = AARH_ROPE_YARN;
+    if (const JVal* m = rs->get("method")) {
+        if (m->kind != JVal::STR || (m->str != "yarn" && m->str != "ntk" && m->str != "linear")) {
+            err = "GGUF config rope_scaling.method must be \"yarn\", \"ntk\" or \"linear\"";
+            return AARH_ERR_CHECKPOINT;
+        }
+        out->method = m->str == "yarn" ? AARH_ROPE_YARN : m->str == "ntk" ? AARH_ROPE_NTK : AARH_ROPE_LINEAR;
+    }
+    const struct {
+        const char* key;
+        double* dst;
+    } reals[] = {{"factor", &out->factor},
+                 {"beta_fast", &out->beta_fast},
+                 {"beta_slow", &out->beta_slow},
+                 {"attn_factor", &out->attn_factor}};
+    for (const auto& f : reals) {
+        const JVal* v = rs->get(f.key);
+        if (!v) continue;
+        if (v->kind != JVal::NUM) {
+            err = std::string("GGUF config rope_scaling.") + f.key + " is not a number";
+            return AARH_ERR_CHECKPOINT;
+        }
+        *f.dst = v->num;
+    }
+    if (const JVal* v = rs->get("original_max_seq_len")) {
+        int64_t n = 0;
+        if (!json_i64(v, &n) || n < 0 || n > INT32_MAX) {
+            err = "GGUF config rope_scaling.original_max_seq_len is not a valid length";
+            return AARH_ERR_CHECKPOINT;
+        }
+        out->original_max_seq_len = (int32_t)n;
+    }
+    return 0;
+}
+
 // GGUF metadata ModelConfig (core/src/config.rs:732-776) against the context's configuration.
 int check_gguf_config(aarh_ctx* c, const JVal& meta) {
     const JVal* cfg = meta.get("config");
@@ -582,17 +628,25 @@ int check_gguf_config(aarh_ctx* c, const JVal& meta) {
             return fail_ctx(c, AARH_ERR_CONFIG, std::string("checkpoint ") + fld.key + " " + v->str +
                                                     " does not match the context's configuration");
     }
-    // Layer variants the device forward does not implement.
-    for (const char* key : {"rope_scaling", "moe", "attention_schedule", "dsa_config"}) {
+    // Layer variants the dense device forward does not implement (latent contexts load them).
+    for (const char* key : {"moe", "attention_schedule", "dsa_config"}) {
         const JVal* v = cfg->get(key);
         if (v && v->kind != JVal::NUL)
             return fail_ctx(c, AARH_ERR_UNSUPPORTED, std::string("checkpoint config sets ") + key +
-                                                         ", which the device forward does not implement");
+                                                         ", which the dense device forward does not implement");
     }
     const JVal* tie = cfg->get("tie_embeddings");
-    if (tie && tie->kind == JVal::BOOL && !tie->b)
-        return fail_ctx(c, AARH_ERR_UNSUPPORTED, "untied LM head checkpoints are not supported (the device LM head is tied)");
-    return 0;
+    if (!tie || tie->kind != JVal::BOOL) return fail_ctx(c, AARH_ERR_CHECKPOINT, "GGUF config lacks tie_embeddings");
+    if (tie->b == (mc.untied_lm_head != 0))
+        return fail_ctx(c, AARH_ERR_CONFIG, std::string("checkpoint tie_embeddings ") + (tie->b ? "true" : "false") +
+                                                " does not match the context's LM head (" +
+                                                (mc.untied_lm_head ? "untied" : "tied") + ")");
+    // the checkpoint's RoPE (scaled or not) replaces the context's tables
+    aarh_rope_scaling rs;
+    std::string err;
+    int r = parse_rope_scaling(cfg, &rs, err);
+    if (r) return fail_ctx(c, r, err);
+    return aarh_set_rope_scaling(c, &rs);
 }
 
 // IEEE binary16 nearest value, ties to even (the conversion of a float to _Float16).
@@ -779,12 +833,30 @@ int aarh_gguf_config(const char* path, aarh_model_config* out) {
         return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks rope_theta / norm_eps");
     out->rope_theta = (float)th->num;
     out->norm_eps = (float)ep->num;
+    const JVal* tie = cfg->get("tie_embeddings");
+    if (!tie || tie->kind != JVal::BOOL) return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks tie_embeddings");
+    out->untied_lm_head = tie->b ? 0 : 1;
     out->num_future_tokens = 0;
     const JVal* mtp = cfg->get("mtp");
     if (mtp && mtp->kind == JVal::OBJ) {
         int64_t nft = 0;
         if (json_i64(mtp->get("num_future_tokens"), &nft) && nft > 0 && nft <= 64) out->num_future_tokens = (int32_t)nft;
     }
+    return AARH_OK;
+}
+
+int aarh_gguf_rope_scaling(const char* path, aarh_rope_scaling* out) {
+    if (!path || !out) {
+        g_host_err = "null path or output";
+        return AARH_ERR_CONFIG;
+    }
+    Gguf g;
+    std::string err;
+    int r = gguf_open(path, g, err);
+    if (r) return fail_ctx(nullptr, r, err);
+    const JVal* cfg = g.meta.get("config");
+    if (!cfg || cfg->kind != JVal::OBJ) return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF metadata has no model config");
+    if ((r = parse_rope_scaling(cfg, out, err))) return fail_ctx(nullptr, r, err);
     return AARH_OK;
 }
 

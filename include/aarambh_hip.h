@@ -62,6 +62,10 @@ typedef struct {
     int32_t kv_format;         /* AARH_KV_* */
     int32_t max_batch;         /* KV-cache sequence slots */
     int32_t max_rows;          /* max rows (sequences x tokens) per forward call, <= 512 */
+    int32_t untied_lm_head;    /* 0: LM head tied to the embedding (tie_embeddings = true);
+                                  1: its own lm_head.weight [vocab][hidden] in lm_head_format,
+                                  the last tensor id, shared by the MTP heads' output
+                                  projection (model.rs:239-262) */
 } aarh_model_config;
 
 /* Sampler (inference/src/sampler.rs:14-65); probabilities as filtered_probs (:226-278). */
@@ -127,15 +131,18 @@ int aarh_get_config(const aarh_ctx *ctx, aarh_model_config *out);
    quantised on device into the context's formats like aarh_load_tensor_f32) ---
    GGUF v1 (load_gguf_tensors, weights/src/gguf.rs:91-241): F32, Q8_0 (per-tensor absmax,
    dequant.rs:7-16) and Q4_K_M (gguf_quant.rs:37-49, custom f16 at :51-112).  The file's
-   config (config.rs:734-776) must match the context's shape, rope_theta and norm_eps, with
-   tied embeddings and no rope_scaling / moe / attention_schedule / dsa_config.
+   config (config.rs:734-776) must match the context's shape, rope_theta and norm_eps and its
+   tie_embeddings must match untied_lm_head (CONFIG otherwise; a config without it is a
+   CHECKPOINT error, as serde requires the field); moe / attention_schedule / dsa_config are
+   UNSUPPORTED here (aarh_lat_load_gguf takes MLA + MoE files).  The file's rope_scaling (or
+   its absence) is applied as aarh_set_rope_scaling does, before any tensor is read.
    safetensors (load_model_with_dtype, weights/src/lib.rs:68-79): F32, F16 and BF16 values.
    Every context tensor must be present with its checkpoint shape (norms 1-D); other tensors
    are ignored, as VarBuilder reads by name.  *out_loaded (optional) = tensors loaded. */
 int aarh_load_gguf(aarh_ctx *ctx, const char *path, int32_t *out_loaded);
 int aarh_load_safetensors(aarh_ctx *ctx, const char *path, int32_t *out_loaded);
 /* Fills the model-shape fields of *out (vocab_size .. max_seq_len, rope_theta, norm_eps,
-   num_future_tokens from mtp) from a GGUF file's config; formats and sizing are left to
+   num_future_tokens from mtp, untied_lm_head from tie_embeddings) from a GGUF file's config; formats and sizing are left to
    the caller (the file is what from_paths reads its config from, engine.rs:226-244). */
 int aarh_gguf_config(const char *path, aarh_model_config *out);
 /* Decodes one GGUF tensor to f32 on the host (no context, no GPU).  out may be NULL to query
@@ -299,6 +306,32 @@ void aarh_spec_session_end(aarh_spec_session *session);
    logits [rows][V], ids/probs [rows][n]: DEVICE pointers; stream as for aarh_accept_sample. */
 int aarh_top_candidates(aarh_ctx *ctx, const float *logits, int rows, int V, const aarh_sampler *sampler,
                         int n, uint32_t *ids, float *probs, void *stream);
+
+/* --- RoPE scaling (RopeScalingConfig, core/src/config.rs:22-35; applied by
+   inverse_frequencies_for_config, nn/src/rope_scaling.rs:24-92, to the transformer's RoPE
+   cache, nn/src/rope.rs:17-28).  Rebuilds the context's cos / sin tables in place:
+   linear divides the base inverse frequencies by factor, NTK raises theta by
+   factor^(hd / (hd - 2)), YaRN blends the extrapolated and factor-interpolated frequency by a
+   linear ramp over the beta_fast / beta_slow correction range at original_max_seq_len; every
+   method multiplies cos and sin by attn_factor.  NULL or method AARH_ROPE_NONE restores the
+   unscaled tables.  Validation follows RopeScalingConfig::validate (config.rs:52-96):
+   AARH_ERR_CONFIG with its message, tables unchanged.  Call between forwards (it waits for
+   the context's stream); latent contexts are unaffected, since MLA keeps an unscaled RoPE
+   cache of its own (model.rs:1107-1116). --- */
+enum { AARH_ROPE_NONE = 0, AARH_ROPE_YARN = 1, AARH_ROPE_NTK = 2, AARH_ROPE_LINEAR = 3 };
+typedef struct aarh_rope_scaling {
+    int32_t method;               /* AARH_ROPE_* */
+    int32_t original_max_seq_len; /* base model's training context */
+    double factor;                /* context extension factor, > 1 */
+    double beta_fast;             /* YaRN high-frequency correction boundary */
+    double beta_slow;             /* YaRN low-frequency correction boundary */
+    double attn_factor;           /* cos / sin multiplier, > 0 */
+} aarh_rope_scaling;
+int aarh_set_rope_scaling(aarh_ctx *ctx, const aarh_rope_scaling *scaling);
+/* A GGUF file's config rope_scaling (serde defaults per field: method yarn, factor 1,
+   original_max_seq_len 0, beta_fast 32, beta_slow 1, attn_factor 1; method AARH_ROPE_NONE
+   when absent).  Values are not validated here; aarh_set_rope_scaling does that. */
+int aarh_gguf_rope_scaling(const char *path, aarh_rope_scaling *out);
 
 /* --- launch mode: repeated verify-forward shapes replay a captured HIP graph (default on;
    0 launches every kernel from the host each call).  Results are identical either way. --- */

@@ -761,6 +761,11 @@ static int tensor_id_final(const ref_config *c) { return 1 + c->n_layers * L_COU
 static int tensor_id_head(const ref_config *c, int h, int which) {
     return 2 + c->n_layers * L_COUNT + h * H_COUNT + which;
 }
+/* Output projection of the model and of every MTP head (model.rs:239-262): the embedding,
+   or lm_head.weight when the head is untied. */
+static const float *lm_head_w(const ref_model *m) {
+    return m->cfg.untied_lm_head ? m->t[m->n_tensors - 1].data : m->t[0].data;
+}
 static int n_heads_mtp(const ref_config *c) {
     return c->num_future_tokens > 1 ? c->num_future_tokens - 1 : 0;
 }
@@ -772,21 +777,93 @@ static void set_info(ref_tensor *t, const char *name, int64_t rows, int64_t cols
     t->kind = kind;
 }
 
-/* rope_scaling.rs:6-11 then rope.rs:43-72: inv_freq in f64 cast to f32, angle pos*freq in f32. */
-static void build_rope(ref_model *m) {
-    int hd = m->head_dim, half = hd / 2, S = m->cfg.max_seq_len;
-    m->rope_cos = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
-    m->rope_sin = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
-    float *inv = (float *)malloc(sizeof(float) * (size_t)half);
-    for (int i = 0; i < half; i++)
-        inv[i] = (float)(1.0 / pow((double)m->cfg.rope_theta, 2.0 * (double)i / (double)hd));
+/* RoPE inverse frequencies and cos / sin factor (inverse_frequencies_for_config,
+   rope_scaling.rs:24-57): base (:6-11), linear (:46-52), NTK-aware theta (:14-22), YaRN
+   (:60-92 with correction_range :107-130 and linear_ramp :132-139); validation and messages
+   from RopeScalingConfig::validate (config.rs:52-96).  f64 arithmetic, results cast to f32.
+   method: 0 none, 1 yarn, 2 ntk, 3 linear.  Returns 0, or -1 with the message in err. */
+int ref_rope_frequencies(int hd, double theta, int max_seq_len, int method, double factor,
+                         int original_max_seq_len, double beta_fast, double beta_slow,
+                         double attn_factor, float *inv, float *attn, char *err, int err_cap) {
+    int half = hd / 2;
+#define ROPE_FAIL(...) do { if (err && err_cap > 0) snprintf(err, (size_t)err_cap, __VA_ARGS__); return -1; } while (0)
+    if (hd <= 0 || hd % 2) ROPE_FAIL("RoPE head_dim must be non-zero and even");
+    if (!(theta > 0.0) || !isfinite(theta)) ROPE_FAIL("RoPE theta must be finite and positive");
+    *attn = 1.0f;
+    for (int i = 0; i < half; i++) inv[i] = (float)(1.0 / pow(theta, 2.0 * (double)i / (double)hd));
+    if (method == 0) return 0;
+    if (!(factor > 1.0) || !isfinite(factor)) ROPE_FAIL("rope_scaling.factor must be finite and greater than 1.0");
+    if (original_max_seq_len <= 0) ROPE_FAIL("rope_scaling.original_max_seq_len must be non-zero");
+    if (max_seq_len < original_max_seq_len)
+        ROPE_FAIL("max_seq_len %d must be >= rope_scaling.original_max_seq_len %d", max_seq_len, original_max_seq_len);
+    if (hd <= 2) ROPE_FAIL("head_dim must be greater than 2 for RoPE scaling");
+    if (!(attn_factor > 0.0) || !isfinite(attn_factor)) ROPE_FAIL("rope_scaling.attn_factor must be finite and positive");
+    if (method == 1) {
+        if (!(beta_fast > 0.0) || !(beta_slow > 0.0) || !isfinite(beta_fast) || !isfinite(beta_slow))
+            ROPE_FAIL("rope_scaling beta values must be finite and positive");
+        if (beta_fast <= beta_slow) ROPE_FAIL("rope_scaling.beta_fast must be greater than beta_slow");
+    }
+    *attn = (float)attn_factor;
+    if (method == 3) {
+        for (int i = 0; i < half; i++) inv[i] = inv[i] / (float)factor;
+        return 0;
+    }
+    if (method == 2) {
+        double th = theta * pow(factor, (double)hd / ((double)hd - 2.0));
+        for (int i = 0; i < half; i++) inv[i] = (float)(1.0 / pow(th, 2.0 * (double)i / (double)hd));
+        return 0;
+    }
+    if (method != 1) ROPE_FAIL("unknown rope_scaling method %d", method);
+    {
+        const double two_pi = 2.0 * 3.14159265358979323846, max_dim = half > 1 ? (double)(half - 1) : 0.0;
+        double lo = floor((double)hd * log((double)original_max_seq_len / (beta_fast * two_pi)) / (2.0 * log(theta)));
+        double hi = ceil((double)hd * log((double)original_max_seq_len / (beta_slow * two_pi)) / (2.0 * log(theta)));
+        lo = lo < 0.0 ? 0.0 : (lo > max_dim ? max_dim : lo);
+        hi = hi < 0.0 ? 0.0 : (hi > max_dim ? max_dim : hi);
+        if (fabs(hi - lo) < 2.220446049250313e-16) hi += 0.001;
+        for (int i = 0; i < half; i++) {
+            double ex = 1.0 / pow(theta, 2.0 * (double)i / (double)hd), in = ex / factor;
+            double ramp = ((double)i - lo) / (hi - lo);
+            ramp = ramp < 0.0 ? 0.0 : (ramp > 1.0 ? 1.0 : ramp);
+            inv[i] = (float)(in * ramp + ex * (1.0 - ramp));
+        }
+    }
+    return 0;
+#undef ROPE_FAIL
+}
+
+/* rope.rs:43-72: angle pos * freq in f32, cos and sin each times the attention factor. */
+static void fill_rope(ref_model *m, const float *inv, float attn) {
+    int half = m->head_dim / 2, S = m->cfg.max_seq_len;
     for (int p = 0; p < S; p++)
         for (int i = 0; i < half; i++) {
             float a = (float)p * inv[i];
-            m->rope_cos[(size_t)p * half + i] = cosf(a) * 1.0f;
-            m->rope_sin[(size_t)p * half + i] = sinf(a) * 1.0f;
+            m->rope_cos[(size_t)p * half + i] = cosf(a) * attn;
+            m->rope_sin[(size_t)p * half + i] = sinf(a) * attn;
         }
+}
+
+static void build_rope(ref_model *m) {
+    int half = m->head_dim / 2, S = m->cfg.max_seq_len;
+    m->rope_cos = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
+    m->rope_sin = (float *)malloc(sizeof(float) * (size_t)S * (size_t)half);
+    float *inv = (float *)malloc(sizeof(float) * (size_t)half);
+    float attn = 1.0f;
+    ref_rope_frequencies(m->head_dim, (double)m->cfg.rope_theta, S, 0, 0, 0, 0, 0, 0, inv, &attn, NULL, 0);
+    fill_rope(m, inv, attn);
     free(inv);
+}
+
+/* RopeCache::from_config (rope.rs:17-28) with cfg.rope_scaling set: rebuilds the tables. */
+int ref_model_set_rope_scaling(ref_model *m, int method, double factor, int original_max_seq_len,
+                               double beta_fast, double beta_slow, double attn_factor, char *err, int err_cap) {
+    int half = m->head_dim / 2;
+    float *inv = (float *)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1)), attn = 1.0f;
+    int r = ref_rope_frequencies(m->head_dim, (double)m->cfg.rope_theta, m->cfg.max_seq_len, method, factor,
+                                 original_max_seq_len, beta_fast, beta_slow, attn_factor, inv, &attn, err, err_cap);
+    if (!r) fill_rope(m, inv, attn);
+    free(inv);
+    return r;
 }
 
 ref_model *ref_model_create(const ref_config *cfg) {
@@ -795,13 +872,14 @@ ref_model *ref_model_create(const ref_config *cfg) {
         c->n_heads <= 0 || c->n_kv_heads <= 0 || c->max_seq_len <= 0)
         return NULL;
     if (c->hidden_dim % c->n_heads || c->n_heads % c->n_kv_heads) return NULL;
+    if (c->untied_lm_head != 0 && c->untied_lm_head != 1) return NULL;
     /* model.rs:309-313 requires head_dim == 64; the benchmark shapes use 32 and 128,
        so that check is dropped here (documented divergence). */
     ref_model *m = (ref_model *)calloc(1, sizeof(ref_model));
     m->cfg = *c;
     m->head_dim = c->hidden_dim / c->n_heads;
     int nh = n_heads_mtp(c);
-    m->n_tensors = 2 + c->n_layers * L_COUNT + nh * H_COUNT;
+    m->n_tensors = 2 + c->n_layers * L_COUNT + nh * H_COUNT + c->untied_lm_head;
     m->t = (ref_tensor *)calloc((size_t)m->n_tensors, sizeof(ref_tensor));
     int64_t H = c->hidden_dim, F = c->ffn_dim, QD = (int64_t)c->n_heads * m->head_dim,
             KD = (int64_t)c->n_kv_heads * m->head_dim;
@@ -841,6 +919,8 @@ ref_model *ref_model_create(const ref_config *cfg) {
         HT(H_OUT, "output_norm.weight", 1, H, REF_T_NORM)
 #undef HT
     }
+    /* LmHead::untied_with_qat (model.rs:239-248), stored like the embedding */
+    if (c->untied_lm_head) set_info(&m->t[m->n_tensors - 1], "lm_head.weight", c->vocab_size, H, REF_T_EMBED);
     for (int i = 0; i < m->n_tensors; i++) {
         size_t n = (size_t)(m->t[i].rows * m->t[i].cols);
         m->t[i].data = (float *)calloc(n, sizeof(float));
@@ -1232,7 +1312,7 @@ int ref_forward_layers(const ref_model *m, ref_kv *kv, const uint32_t *ids, int 
     if (with_head) {
         float *hn = (float *)malloc(sizeof(float) * (size_t)(S * H));
         rms_norm(x, S, H, m->t[tensor_id_final(c)].data, c->norm_eps, hn);
-        if (logits) linear(hn, S, H, emb, V, logits, nt);
+        if (logits) linear(hn, S, H, lm_head_w(m), V, logits, nt);
         free(hn);
     }
     free(x);
@@ -1260,7 +1340,7 @@ int ref_forward(const ref_model *m, ref_kv *kv, const uint32_t *ids, int S, int 
     float *hn = (float *)malloc(sizeof(float) * (size_t)(S * H));
     rms_norm(x, S, H, m->t[tensor_id_final(c)].data, c->norm_eps, hn);
     if (hidden) memcpy(hidden, hn, sizeof(float) * (size_t)(S * H));
-    if (logits) linear(hn, S, H, emb, V, logits, nt);
+    if (logits) linear(hn, S, H, lm_head_w(m), V, logits, nt);
     free(hn);
     free(x);
     return REF_OK;
@@ -1295,7 +1375,7 @@ int ref_mtp_head(const ref_model *m, int head, const float *anchor, const uint32
     float *hn = (float *)malloc(sizeof(float) * (size_t)H);
     rms_norm(x + (int64_t)(L - 1) * H, 1, H, m->t[tensor_id_head(c, head, H_OUT)].data,
              c->norm_eps, hn);
-    linear(hn, 1, H, emb, V, logits, nt);
+    linear(hn, 1, H, lm_head_w(m), V, logits, nt);
     free(hn);
     free(x);
     return REF_OK;

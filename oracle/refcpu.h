@@ -109,6 +109,7 @@ typedef struct {
     int32_t weight_format;     /* 0 f32, 1 bf16, 2 int8 per-row, 3 int4 g128 */
     int32_t lm_head_format;    /* 0 f32, 1 bf16 (tied embedding storage) */
     int32_t kv_format;         /* 0 f32, 1 f16, 2 int8 per token per kv-head */
+    int32_t untied_lm_head;    /* 1: lm_head.weight (last tensor) instead of the embedding */
 } ref_config;
 
 enum { REF_W_F32 = 0, REF_W_BF16 = 1, REF_W_INT8_ROW = 2, REF_W_INT4_G128 = 3 };
@@ -119,6 +120,12 @@ typedef struct ref_model ref_model;
 typedef struct ref_kv ref_kv;
 
 ref_model *ref_model_create(const ref_config *cfg);
+/* RoPE scaling (rope_scaling.rs:24-92): method 0 none, 1 yarn, 2 ntk, 3 linear. */
+int ref_rope_frequencies(int hd, double theta, int max_seq_len, int method, double factor,
+                         int original_max_seq_len, double beta_fast, double beta_slow,
+                         double attn_factor, float *inv, float *attn, char *err, int err_cap);
+int ref_model_set_rope_scaling(ref_model *m, int method, double factor, int original_max_seq_len,
+                               double beta_fast, double beta_slow, double attn_factor, char *err, int err_cap);
 void ref_model_free(ref_model *m);
 int ref_model_num_tensors(const ref_model *m);
 int ref_model_tensor_info(const ref_model *m, int id, char *name, int name_cap, int64_t *rows,

@@ -51,7 +51,7 @@ class RefConfig(C.Structure):
                                           "n_heads", "n_kv_heads", "max_seq_len")] + \
                [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
                [(n, C.c_int32) for n in ("num_future_tokens", "weight_format",
-                                          "lm_head_format", "kv_format")]
+                                          "lm_head_format", "kv_format", "untied_lm_head")]
 
 
 class RefLatConfig(C.Structure):
@@ -125,6 +125,11 @@ def lib():
         "ref_synth_fill": (None, [C.c_uint64, C.c_uint32, C.c_int64, C.c_float, F32P]),
         "ref_synth_tokens": (None, [C.c_uint64, C.c_uint32, C.c_int64, C.c_uint32, U32P]),
         "ref_model_create": (C.c_void_p, [C.POINTER(RefConfig)]),
+        "ref_rope_frequencies": (C.c_int, [C.c_int, C.c_double, C.c_int, C.c_int, C.c_double, C.c_int,
+                                           C.c_double, C.c_double, C.c_double, F32P, C.POINTER(C.c_float),
+                                           C.c_char_p, C.c_int]),
+        "ref_model_set_rope_scaling": (C.c_int, [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double,
+                                                 C.c_double, C.c_double, C.c_char_p, C.c_int]),
         "ref_model_free": (None, [C.c_void_p]),
         "ref_model_num_tensors": (C.c_int, [C.c_void_p]),
         "ref_model_tensor_info": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_int64),
@@ -373,9 +378,35 @@ def synth_tokens(seed, stream, n, vocab):
 
 def make_config(vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_heads, max_seq_len,
                 rope_theta=10000.0, norm_eps=1e-5, num_future_tokens=0, weight_format=W_F32,
-                lm_head_format=0, kv_format=KV_F32):
+                lm_head_format=0, kv_format=KV_F32, untied_lm_head=0):
     return RefConfig(vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_heads, max_seq_len,
-                     rope_theta, norm_eps, num_future_tokens, weight_format, lm_head_format, kv_format)
+                     rope_theta, norm_eps, num_future_tokens, weight_format, lm_head_format, kv_format,
+                     int(untied_lm_head))
+
+
+ROPE_METHODS = {None: 0, "none": 0, "yarn": 1, "ntk": 2, "linear": 3}
+
+
+def _rope_args(scaling):
+    """(method, factor, original_max_seq_len, beta_fast, beta_slow, attn_factor) of a mapping
+    with RopeScalingConfig's fields (config.rs:22-47 defaults: yarn, 32, 1, attn 1)."""
+    if scaling is None:
+        return (0, 0.0, 0, 0.0, 0.0, 0.0)
+    g = scaling.get if isinstance(scaling, dict) else (lambda k, d=None: getattr(scaling, k, d))
+    return (ROPE_METHODS[g("method", "yarn")], float(g("factor", 1.0)), int(g("original_max_seq_len", 0)),
+            float(g("beta_fast", 32.0)), float(g("beta_slow", 1.0)), float(g("attn_factor", 1.0)))
+
+
+def rope_frequencies(head_dim, theta, max_seq_len, scaling=None):
+    """inverse_frequencies_for_config (rope_scaling.rs:24-33): (inv_freq f32[hd/2], attn_factor);
+    ValueError with RopeScalingConfig::validate's message on a bad config."""
+    inv = np.zeros(max(head_dim // 2, 1), np.float32)
+    attn = C.c_float()
+    err = C.create_string_buffer(256)
+    r = lib().ref_rope_frequencies(head_dim, theta, max_seq_len, *_rope_args(scaling), inv, C.byref(attn), err, 256)
+    if r:
+        raise ValueError(err.value.decode())
+    return inv[: head_dim // 2], attn.value
 
 
 class Model:
@@ -388,6 +419,12 @@ class Model:
             st = lib().ref_model_init_synthetic(self.h, seed, std)
             if st:
                 raise ValueError(f"synthetic init failed: {st}")
+
+    def set_rope_scaling(self, scaling):
+        """RopeCache::from_config with cfg.rope_scaling = scaling (None: unscaled)."""
+        err = C.create_string_buffer(256)
+        if lib().ref_model_set_rope_scaling(self.h, *_rope_args(scaling), err, 256):
+            raise ValueError(err.value.decode())
 
     def close(self):
         if self.h:

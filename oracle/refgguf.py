@@ -160,10 +160,13 @@ def decode_tensor(enc, shape, payload):
 
 
 def model_config_json(vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_heads, max_seq_len,
-                      rope_theta=10000.0, norm_eps=1e-5, num_future_tokens=0, tie_embeddings=True):
+                      rope_theta=10000.0, norm_eps=1e-5, num_future_tokens=0, tie_embeddings=True,
+                      rope_scaling=None):
     """ModelConfig (core/src/config.rs:732-776) as serde_json writes it (optional fields omitted)."""
     cfg = {"vocab_size": vocab_size, "hidden_dim": hidden_dim, "ffn_dim": ffn_dim, "n_layers": n_layers,
            "n_heads": n_heads, "n_kv_heads": n_kv_heads, "max_seq_len": max_seq_len, "rope_theta": rope_theta}
+    if rope_scaling is not None:
+        cfg["rope_scaling"] = dict(rope_scaling)
     if num_future_tokens:
         cfg["mtp"] = {"num_future_tokens": num_future_tokens, "aux_loss_weight": 0.3}
     cfg["norm_eps"] = norm_eps

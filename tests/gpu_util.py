@@ -15,10 +15,12 @@ def rel_rows(got, want):
 def make_pair(seed=0, std=0.02, max_batch=1, max_rows=64, **kw):
     """Identical random-init weights in the oracle and on the device (f32 host values,
     quantised by each side's own codec)."""
-    rc = R.make_config(**kw)
+    tie = kw.pop("tie_embeddings", True)
+    rc = R.make_config(untied_lm_head=0 if tie else 1, **kw)
     ref = R.Model(rc)
-    mc = A.ModelConfig(**kw)
+    mc = A.ModelConfig(tie_embeddings=tie, **kw)
     hip = A.HipModel(mc, max_batch=max_batch, max_rows=max_rows)
+    assert [t[0] for t in hip.tensors()] == [t[0] for t in ref.tensors()]
     for i, (name, r, c, kind) in enumerate(ref.tensors()):
         raw = R.synth_fill(seed, i, r * c, std) if kind != R.T_NORM else np.ones(r * c, np.float32)
         ref.set(i, raw)

@@ -14,18 +14,19 @@ def rms(x, w, eps):
     return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w.reshape(-1)
 
 
-def rope(x, pos, theta):
-    # x [S, H, hd]
+def rope(x, pos, theta, rs=None):
+    # x [S, H, hd]; rs = (inverse frequencies, cos / sin factor) of a scaled RoPE
     hd = x.shape[-1]
     half = hd // 2
-    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
+    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd) if rs is None else np.asarray(rs[0], np.float64)
+    a = 1.0 if rs is None else float(rs[1])
     ang = pos[:, None] * inv[None, :]
-    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    c, s = a * np.cos(ang)[:, None, :], a * np.sin(ang)[:, None, :]
     x1, x2 = x[..., :half], x[..., half:]
     return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], -1)
 
 
-def block(W, pre, x, cfg, pos):
+def block(W, pre, x, cfg, pos, rs=None):
     H, nh, nkv = cfg.hidden_dim, cfg.n_heads, cfg.n_kv_heads
     hd = H // nh
     S = x.shape[0]
@@ -33,7 +34,7 @@ def block(W, pre, x, cfg, pos):
     q = (xn @ W[pre + "attn.wq.weight"].T).reshape(S, nh, hd)
     k = (xn @ W[pre + "attn.wk.weight"].T).reshape(S, nkv, hd)
     v = (xn @ W[pre + "attn.wv.weight"].T).reshape(S, nkv, hd)
-    q, k = rope(q, pos, cfg.rope_theta), rope(k, pos, cfg.rope_theta)
+    q, k = rope(q, pos, cfg.rope_theta, rs), rope(k, pos, cfg.rope_theta, rs)
     out = np.zeros((S, nh, hd))
     mask = np.tril(np.ones((S, S), bool))
     for h in range(nh):
@@ -50,13 +51,14 @@ def block(W, pre, x, cfg, pos):
     return x + (g / (1 + np.exp(-g)) * u) @ W[pre + "ffn.w_down.weight"].T
 
 
-def forward(W, cfg, ids):
-    """Full (uncached) forward over ids; returns logits [S, V] and normed hidden [S, H]."""
+def forward(W, cfg, ids, rs=None):
+    """Full (uncached) forward over ids; returns logits [S, V] and normed hidden [S, H].
+    rs: (inverse frequencies, cos / sin factor) of a scaled RoPE, None for the base one."""
     E = W["embedding.weight"]
     x = E[np.asarray(ids, np.int64)]
     pos = np.arange(len(ids), dtype=np.float64)
     for l in range(cfg.n_layers):
-        x = block(W, f"blocks.{l}.", x, cfg, pos)
+        x = block(W, f"blocks.{l}.", x, cfg, pos, rs)
     hn = rms(x, W["final_norm.weight"], cfg.norm_eps)
     return hn @ E.T, hn
 

@@ -20,6 +20,7 @@ int aarh_get_config(const aarh_ctx*, aarh_model_config*) { return AARH_ERR_CONFI
 int aarh_num_tensors(const aarh_ctx*) { return 0; }
 int aarh_tensor_info(const aarh_ctx*, int, char*, int, int64_t*, int64_t*, int32_t*) { return AARH_ERR_SHAPE; }
 int aarh_load_tensor_f32(aarh_ctx*, int, const float*, int64_t) { return AARH_ERR_CONFIG; }
+int aarh_set_rope_scaling(aarh_ctx*, const aarh_rope_scaling*) { return AARH_ERR_CONFIG; }
 }
 
 static std::vector<unsigned char> slurp(const std::string& p) {
@@ -81,14 +82,16 @@ int main(int argc, char** argv) {
             return 1;
         }
         aarh_model_config mc{};
-        if (gguf && aarh_gguf_config(p.c_str(), &mc) != AARH_OK) return 1;
+        aarh_rope_scaling rs{};
+        if (gguf && (aarh_gguf_config(p.c_str(), &mc) != AARH_OK || aarh_gguf_rope_scaling(p.c_str(), &rs) != AARH_OK))
+            return 1;
         // every truncation and a sweep of single-byte corruptions end in a status code
         const std::vector<unsigned char> b = slurp(p);
         const std::string q = tmp + "/mut" + (gguf ? ".gguf" : ".safetensors");
         for (size_t cut = 0; cut < b.size(); cut += (cut < 256 ? 1 : 97)) {
             spit(q, std::vector<unsigned char>(b.begin(), b.begin() + cut));
             read_all(q, gguf);
-            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc);
+            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs);
         }
         unsigned seed = 12345;
         for (int t = 0; t < 400; t++) {
@@ -99,7 +102,7 @@ int main(int argc, char** argv) {
             m[at] = (unsigned char)(seed >> 16);
             spit(q, m);
             read_all(q, gguf);
-            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc);
+            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs);
         }
     }
     printf("checkpoint reader sanitizer run: ok\n");

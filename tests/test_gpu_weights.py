@@ -122,8 +122,10 @@ def test_checkpoint_errors(tmp_path):
     base = G.model_config_json(**kw)
     with pytest.raises(A.ConfigError):  # a different model shape
         hip.load_gguf(gguf(dict(base, ffn_dim=768), vals, "a.gguf"))
-    with pytest.raises(A.UnsupportedError):  # untied LM head
+    with pytest.raises(A.ConfigError, match="tie_embeddings"):  # an untied head into a tied context
         hip.load_gguf(gguf(dict(base, tie_embeddings=False), vals, "b.gguf"))
+    with pytest.raises(A.CheckpointError, match="tie_embeddings"):  # serde requires the field
+        hip.load_gguf(gguf({k: v for k, v in base.items() if k != "tie_embeddings"}, vals, "b2.gguf"))
     with pytest.raises(A.UnsupportedError):  # a layer variant the device does not run
         hip.load_gguf(gguf(dict(base, moe={"num_experts": 4}), vals, "c.gguf"))
     short = {k: v for k, v in vals.items() if k != "blocks.0.ffn.w_up.weight"}
