@@ -182,6 +182,10 @@ def lib():
         "aarh_prof_get": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                     C.POINTER(C.c_int64)]),
         "aarh_lat_create": (C.c_int, [C.c_int, C.POINTER(_LatCfg), C.POINTER(_P)]),
+        "aarh_lat_get_config": (C.c_int, [_P, C.POINTER(_LatCfg)]),
+        "aarh_lat_load_gguf": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
+        "aarh_lat_load_safetensors": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int32)]),
+        "aarh_lat_gguf_config": (C.c_int, [C.c_char_p, C.POINTER(_LatCfg)]),
         "aarh_lat_destroy": (None, [_P]),
         "aarh_lat_last_error": (C.c_char_p, [_P]),
         "aarh_lat_num_tensors": (C.c_int, [_P]),
@@ -225,7 +229,8 @@ EXPORTED = ["aarh_create", "aarh_destroy", "aarh_last_error", "aarh_stream", "aa
             "aarh_lat_load_tensor_packed_i4", "aarh_packed_i4_params", "aarh_spec_session_begin",
             "aarh_spec_session_step", "aarh_spec_session_result", "aarh_spec_session_candidates",
             "aarh_spec_session_rng_offsets", "aarh_spec_session_set_rng_offsets", "aarh_spec_session_end",
-            "aarh_set_rope_scaling", "aarh_gguf_rope_scaling"]
+            "aarh_set_rope_scaling", "aarh_gguf_rope_scaling", "aarh_lat_get_config", "aarh_lat_load_gguf",
+            "aarh_lat_load_safetensors", "aarh_lat_gguf_config"]
 
 
 def _ptr(a):
@@ -1039,6 +1044,18 @@ class LatConfig:
     rope_theta: float = 10000.0
     norm_eps: float = 1e-5
 
+    @classmethod
+    def from_gguf(cls, path, **overrides):
+        """Latent shape from a GGUF v1 file's config (aarh_lat_gguf_config: MlaConfig::resolve,
+        MoE fine experts, the reference's config checks); formats from `overrides`."""
+        c = _LatCfg()
+        _host_check(lib().aarh_lat_gguf_config(os.fsencode(path), C.byref(c)))
+        kw = {f: getattr(c, f) for f in ("vocab_size", "hidden_dim", "n_layers", "n_heads", "max_seq_len",
+                                         "latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
+                                         "expert_dim", "n_shared", "rope_theta", "norm_eps")}
+        kw.update(overrides)
+        return cls(**kw)
+
 
 class HipLatModel:
     """Device copy of a latent-attention MoE decoder plus its latent cache slots."""
@@ -1093,6 +1110,18 @@ class HipLatModel:
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(lib().aarh_lat_init_synthetic(self.h, seed, std))
+
+    def load_gguf(self, path):
+        """Every tensor of an MLA + MoE GGUF v1 checkpoint (aarh_lat_load_gguf); returns the count."""
+        n = C.c_int32()
+        self._check(lib().aarh_lat_load_gguf(self.h, os.fsencode(path), C.byref(n)))
+        return n.value
+
+    def load_safetensors(self, path):
+        """Every tensor of an MLA + MoE safetensors checkpoint (aarh_lat_load_safetensors)."""
+        n = C.c_int32()
+        self._check(lib().aarh_lat_load_safetensors(self.h, os.fsencode(path), C.byref(n)))
+        return n.value
 
     def kv_len(self, slot=0):
         v = C.c_int32()

@@ -650,6 +650,11 @@ int prof_collect(Ctx* c) {
 
 }  // namespace
 
+namespace aarh {
+// Records a failure on a latent context for the checkpoint readers (weights.cpp).
+int lat_ctx_fail(aarh_lat_ctx* c, int code, const char* msg) { return fail(c, code, "%s", msg); }
+}  // namespace aarh
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -860,6 +865,12 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
         HIPCHK(c, hipHostMalloc((void**)&c->h_ids, M * 4, 0));
     }
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    return AARH_OK;
+}
+
+int aarh_lat_get_config(const aarh_lat_ctx* c, aarh_lat_config* out) {
+    if (!c || !out) return AARH_ERR_CONFIG;
+    *out = c->cfg;
     return AARH_OK;
 }
 

@@ -602,6 +602,8 @@ int stage_release(aarh_ctx* c, int slot) {
 namespace aarh {
 // Records a failure on a context for the library's other translation units (weights.cpp).
 int ctx_fail(aarh_ctx* c, int code, const char* msg) { return fail(c, code, "%s", msg); }
+// RopeScalingConfig::validate (config.rs:52-96) of a checkpoint config, for weights.cpp.
+int rope_scaling_check(int head_dim, int max_seq_len, const aarh_rope_scaling* s, std::string& err);
 }  // namespace aarh
 
 // ===========================================================================
@@ -832,6 +834,20 @@ int rope_frequencies(int hd, double theta, int max_seq_len, const aarh_rope_scal
     }
     return 0;
 }
+
+}  // namespace
+
+int aarh::rope_scaling_check(int head_dim, int max_seq_len, const aarh_rope_scaling* s, std::string& err) {
+    std::vector<float> inv;
+    float attn = 1.0f;
+    if (head_dim <= 0 || head_dim % 2) {
+        err = "RoPE head_dim must be non-zero and even";
+        return AARH_ERR_CONFIG;
+    }
+    return rope_frequencies(head_dim, 10000.0, max_seq_len, s, inv, &attn, err);
+}
+
+namespace {
 
 // cos / sin tables [positions][hd / 2] (rope.rs:43-72: angle pos * freq in f32, times the
 // attention factor) uploaded into the context's table buffers.

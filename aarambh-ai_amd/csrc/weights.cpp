@@ -8,6 +8,7 @@
 //
 // Built without floating-point contraction: q * scale + min is two roundings,
 // as in the reference (gguf_quant.rs:37-49).
+#include <algorithm>
 #include <cerrno>
 #include <cmath>
 #include <cstdarg>
@@ -518,14 +519,27 @@ struct Slot {
     bool loaded = false;
 };
 
-std::map<std::string, Slot> context_slots(aarh_ctx* ctx) {
+// The two context types (dense aarh_ctx, latent aarh_lat_ctx) behind one set of names.
+int num_tensors(aarh_ctx* c) { return aarh_num_tensors(c); }
+int num_tensors(aarh_lat_ctx* c) { return aarh_lat_num_tensors(c); }
+int tensor_info(aarh_ctx* c, int id, char* name, int cap, int64_t* r, int64_t* cc, int32_t* k) {
+    return aarh_tensor_info(c, id, name, cap, r, cc, k);
+}
+int tensor_info(aarh_lat_ctx* c, int id, char* name, int cap, int64_t* r, int64_t* cc, int32_t* k) {
+    return aarh_lat_tensor_info(c, id, name, cap, r, cc, k);
+}
+int load_f32(aarh_ctx* c, int id, const float* v, int64_t n) { return aarh_load_tensor_f32(c, id, v, n); }
+int load_f32(aarh_lat_ctx* c, int id, const float* v, int64_t n) { return aarh_lat_load_tensor_f32(c, id, v, n); }
+
+template <class Ctx>
+std::map<std::string, Slot> context_slots(Ctx* ctx) {
     std::map<std::string, Slot> m;
     char name[256];
-    const int n = aarh_num_tensors(ctx);
+    const int n = num_tensors(ctx);
     for (int id = 0; id < n; id++) {
         int64_t r = 0, c = 0;
         int32_t kind = 0;
-        if (aarh_tensor_info(ctx, id, name, sizeof(name), &r, &c, &kind) == AARH_OK) m[name] = Slot{id, r, c};
+        if (tensor_info(ctx, id, name, sizeof(name), &r, &c, &kind) == AARH_OK) m[name] = Slot{id, r, c};
     }
     return m;
 }
@@ -539,15 +553,23 @@ bool shape_matches(const std::vector<int64_t>& shape, const Slot& s) {
 
 }  // namespace
 
-// Set by the library's runtime (runtime.cpp): the context's error text.
+// Set by the library's runtimes (runtime.cpp, lat_runtime.cpp): the context's error text;
+// the RoPE scaling check of the dense runtime.
 namespace aarh {
 int ctx_fail(aarh_ctx* c, int code, const char* msg);
-}
+int lat_ctx_fail(aarh_lat_ctx* c, int code, const char* msg);
+int rope_scaling_check(int head_dim, int max_seq_len, const aarh_rope_scaling* s, std::string& err);
+}  // namespace aarh
 
 namespace {
 
 int fail_ctx(aarh_ctx* c, int code, const std::string& msg) {
     if (c) return aarh::ctx_fail(c, code, msg.c_str());
+    g_host_err = msg;
+    return code;
+}
+int fail_ctx(aarh_lat_ctx* c, int code, const std::string& msg) {
+    if (c) return aarh::lat_ctx_fail(c, code, msg.c_str());
     g_host_err = msg;
     return code;
 }
@@ -649,6 +671,314 @@ int check_gguf_config(aarh_ctx* c, const JVal& meta) {
     return aarh_set_rope_scaling(c, &rs);
 }
 
+// Unsigned integer field with a serde default: absent -> def; present and not a valid
+// non-negative integer -> false.
+bool opt_u32(const JVal* obj, const char* key, int64_t def, int64_t* out) {
+    const JVal* v = obj ? obj->get(key) : nullptr;
+    if (!v) {
+        *out = def;
+        return true;
+    }
+    return json_i64(v, out) && *out >= 0 && *out <= INT32_MAX;
+}
+
+// ModelConfig of an MLA + MoE checkpoint (config.rs:732-776) -> the latent context's shape
+// fields, with AarambhModel::validate_config's checks (model.rs:281-344) for the parts the
+// latent decoder has: MoeConfig::validate (config.rs:179-211), the attention schedule
+// (HybridAttentionSchedule::validate, :680-708, GatedDeltaNetConfig::resolve :470-518),
+// MlaConfig::resolve / validate (:558-612), RopeScalingConfig::validate (:52-96), and
+// dsa_config (DsaConfig::validate :239-258, then "does not select any sparse attention
+// layer", since no layer of an all-MLA schedule is full attention).  The latent context runs
+// MLA and MoE in every layer with a tied LM head: other layer mixes are UNSUPPORTED.  mtp
+// heads, if configured, are not part of the latent context and are ignored (as are qat,
+// training-only, model.rs:82-88).  Formats and sizing fields are left as the caller set them.
+int lat_config_from_json(const JVal& meta, aarh_lat_config* out, std::string& err) {
+    const JVal* cfg = meta.get("config");
+    if (!cfg || cfg->kind != JVal::OBJ) {
+        err = "GGUF metadata has no model config";
+        return AARH_ERR_CHECKPOINT;
+    }
+    int64_t vocab, hidden, ffn, layers, heads, kv_heads, max_seq;
+    const struct {
+        const char* key;
+        int64_t* dst;
+    } ints[] = {{"vocab_size", &vocab}, {"hidden_dim", &hidden}, {"ffn_dim", &ffn},        {"n_layers", &layers},
+                {"n_heads", &heads},    {"n_kv_heads", &kv_heads}, {"max_seq_len", &max_seq}};
+    for (const auto& f : ints)
+        if (!json_i64(cfg->get(f.key), f.dst) || *f.dst < 0 || *f.dst > INT32_MAX) {
+            err = std::string("GGUF config lacks a valid ") + f.key;
+            return AARH_ERR_CHECKPOINT;
+        }
+    const JVal* th = cfg->get("rope_theta");
+    const JVal* ep = cfg->get("norm_eps");
+    const JVal* tie = cfg->get("tie_embeddings");
+    if (!th || th->kind != JVal::NUM || !ep || ep->kind != JVal::NUM) {
+        err = "GGUF config lacks rope_theta / norm_eps";
+        return AARH_ERR_CHECKPOINT;
+    }
+    if (!tie || tie->kind != JVal::BOOL) {
+        err = "GGUF config lacks tie_embeddings";
+        return AARH_ERR_CHECKPOINT;
+    }
+    // validate_config (model.rs:283-313), head_dim == 64 aside (the benchmark shapes differ)
+    auto cfg_err = [&](const std::string& m) {
+        err = m;
+        return AARH_ERR_CONFIG;
+    };
+    if (vocab == 0) return cfg_err("vocab_size must be non-zero");
+    if (hidden == 0 || ffn == 0 || layers == 0) return cfg_err("hidden_dim, ffn_dim, and n_layers must be non-zero");
+    if (heads == 0 || kv_heads == 0) return cfg_err("n_heads and n_kv_heads must be non-zero");
+    if (max_seq == 0) return cfg_err("max_seq_len must be non-zero");
+    if (hidden % heads) return cfg_err("hidden_dim must be divisible by n_heads");
+    if (heads % kv_heads) return cfg_err("n_heads must be divisible by n_kv_heads");
+    aarh_rope_scaling rs;
+    int r = parse_rope_scaling(cfg, &rs, err);
+    if (r) return r;
+    if (rs.method != AARH_ROPE_NONE && (r = aarh::rope_scaling_check((int)(hidden / heads), (int)max_seq, &rs, err)))
+        return r;
+    // MoE (moe.validate, config.rs:179-211)
+    const JVal* moe = cfg->get("moe");
+    if (!moe || moe->kind == JVal::NUL) {
+        err = "the latent context runs a MoE FFN in every layer; the checkpoint config has no moe";
+        return AARH_ERR_UNSUPPORTED;
+    }
+    if (moe->kind != JVal::OBJ) {
+        err = "GGUF config moe is not an object";
+        return AARH_ERR_CHECKPOINT;
+    }
+    int64_t n_exp, top_k, exp_ffn, every_n, fine, n_shared;
+    if (!opt_u32(moe, "num_experts", 8, &n_exp) || !opt_u32(moe, "top_k", 2, &top_k) ||
+        !opt_u32(moe, "expert_ffn_dim", 0, &exp_ffn) || !opt_u32(moe, "every_n_layers", 2, &every_n) ||
+        !opt_u32(moe, "fine_grained_factor", 1, &fine) || !opt_u32(moe, "num_shared_experts", 0, &n_shared)) {
+        err = "GGUF config moe has a field that is not a valid count";
+        return AARH_ERR_CHECKPOINT;
+    }
+    double aux = 0.01;
+    if (const JVal* a = moe->get("aux_loss_weight")) {
+        if (a->kind != JVal::NUM) {
+            err = "GGUF config moe.aux_loss_weight is not a number";
+            return AARH_ERR_CHECKPOINT;
+        }
+        aux = a->num;
+    }
+    if (n_exp < 2) return cfg_err("moe.num_experts must be at least 2");
+    if (fine == 0) return cfg_err("moe.fine_grained_factor must be non-zero");
+    if (exp_ffn == 0 || exp_ffn % fine)
+        return cfg_err("moe.expert_ffn_dim " + std::to_string(exp_ffn) +
+                       " must be non-zero and divisible by fine_grained_factor " + std::to_string(fine));
+    const int64_t routed = n_exp * fine;
+    if (top_k == 0 || top_k > routed)
+        return cfg_err("moe.top_k must be in 1..=" + std::to_string(routed) + " for num_experts=" +
+                       std::to_string(n_exp) + " and fine_grained_factor=" + std::to_string(fine));
+    if (!(aux >= 0.0) || !std::isfinite(aux)) return cfg_err("moe.aux_loss_weight must be finite and non-negative");
+    if (every_n == 0) return cfg_err("moe.every_n_layers must be non-zero");
+    if (every_n > layers) return cfg_err("moe.every_n_layers does not select any model layer");
+    // what the latent context cannot hold is reported after the reference's own checks
+    std::string unsupported;
+    if (every_n != 1)
+        unsupported = "the latent context runs a MoE FFN in every layer; moe.every_n_layers " +
+                      std::to_string(every_n) + " leaves dense FFN layers";
+    // attention schedule with MLA in every layer
+    const JVal* sch = cfg->get("attention_schedule");
+    if (!sch || sch->kind == JVal::NUL) {
+        err = "the latent context runs MLA in every layer; the checkpoint config has no attention_schedule";
+        return AARH_ERR_UNSUPPORTED;
+    }
+    if (sch->kind != JVal::OBJ) {
+        err = "GGUF config attention_schedule is not an object";
+        return AARH_ERR_CHECKPOINT;
+    }
+    int64_t full_every;
+    if (!opt_u32(sch, "full_attention_every_n", 4, &full_every)) {
+        err = "GGUF config attention_schedule.full_attention_every_n is not a valid count";
+        return AARH_ERR_CHECKPOINT;
+    }
+    std::vector<bool> is_mla((size_t)layers, false);
+    if (const JVal* ml = sch->get("mla_layers")) {
+        if (ml->kind != JVal::ARR) {
+            err = "GGUF config attention_schedule.mla_layers is not an array";
+            return AARH_ERR_CHECKPOINT;
+        }
+        for (const JVal& v : ml->arr) {
+            int64_t l = 0;
+            if (!json_i64(&v, &l) || l < 0) {
+                err = "GGUF config attention_schedule.mla_layers holds a value that is not a layer index";
+                return AARH_ERR_CHECKPOINT;
+            }
+            if (l < layers) is_mla[(size_t)l] = true;
+        }
+    }
+    if (full_every == 0) return cfg_err("attention_schedule.full_attention_every_n must be non-zero");
+    bool all_mla = true, any_mla = false;
+    for (bool b : is_mla) all_mla = all_mla && b, any_mla = any_mla || b;
+    if (layers < 2 || !any_mla)
+        return cfg_err("attention_schedule must select at least one Gated DeltaNet or LatentMLA layer");
+    const JVal* mla = sch->get("mla");
+    if (!mla || mla->kind == JVal::NUL) return cfg_err("attention_schedule.mla must be set when mla_layers is non-empty");
+    if (mla->kind != JVal::OBJ) {
+        err = "GGUF config attention_schedule.mla is not an object";
+        return AARH_ERR_CHECKPOINT;
+    }
+    // GatedDeltaNetConfig::resolve + validate run for every schedule (config.rs:707)
+    {
+        const JVal* gd = sch->get("gated_deltanet");
+        if (gd && gd->kind != JVal::OBJ) {
+            err = "GGUF config attention_schedule.gated_deltanet is not an object";
+            return AARH_ERR_CHECKPOINT;
+        }
+        int64_t gh, gk, gv, conv, chunk;
+        if (!opt_u32(gd, "n_heads", 0, &gh) || !opt_u32(gd, "key_head_dim", 0, &gk) ||
+            !opt_u32(gd, "value_head_dim", 0, &gv) || !opt_u32(gd, "conv_kernel_size", 4, &conv) ||
+            !opt_u32(gd, "chunk_size", 64, &chunk)) {
+            err = "GGUF config attention_schedule.gated_deltanet has a field that is not a valid count";
+            return AARH_ERR_CHECKPOINT;
+        }
+        if (gh == 0) gh = std::max<int64_t>(heads / 2, 1);
+        if (gk == 0) gk = hidden * 3 / (4 * gh);
+        if (gv == 0) gv = gk * 2;
+        if (gh == 0 || gk == 0 || gv == 0)
+            return cfg_err("gated_deltanet head counts and dimensions must resolve to non-zero values");
+        if (conv < 2) return cfg_err("gated_deltanet.conv_kernel_size must be at least 2");
+        if (chunk < 16 || chunk > 256 || (chunk & (chunk - 1)))
+            return cfg_err("gated_deltanet.chunk_size must be a power of two in 16..=256");
+    }
+    if (!all_mla && unsupported.empty())
+        unsupported = "the latent context runs MLA in every layer; attention_schedule.mla_layers must list all " +
+                      std::to_string(layers) + " layers";
+    // MlaConfig::resolve (config.rs:558-587) and validate (:589-612)
+    int64_t latent, nope, rope, mheads, vdim;
+    if (!opt_u32(mla, "latent_dim", 512, &latent) || !opt_u32(mla, "nope_head_dim", 0, &nope) ||
+        !opt_u32(mla, "rope_head_dim", 16, &rope) || !opt_u32(mla, "n_heads", 0, &mheads) ||
+        !opt_u32(mla, "value_head_dim", 0, &vdim)) {
+        err = "GGUF config attention_schedule.mla has a field that is not a valid count";
+        return AARH_ERR_CHECKPOINT;
+    }
+    if (mheads == 0) mheads = heads;
+    if (nope == 0) nope = std::max<int64_t>(hidden / heads > rope ? hidden / heads - rope : 0, 8);
+    if (vdim == 0) vdim = nope;
+    if (latent == 0) return cfg_err("mla.latent_dim must be non-zero");
+    if (mheads == 0) return cfg_err("mla.n_heads must resolve to a non-zero value");
+    if (nope == 0) return cfg_err("mla.nope_head_dim must resolve to a non-zero value");
+    if (rope == 0 || rope % 2) return cfg_err("mla.rope_head_dim must be a positive even number");
+    if (vdim == 0) return cfg_err("mla.value_head_dim must resolve to a non-zero value");
+    // dsa_config: validate, then no layer of an all-MLA schedule is a sparse slot
+    if (const JVal* dsa = cfg->get("dsa_config"); dsa && dsa->kind != JVal::NUL) {
+        int64_t bs, tk, mn;
+        if (dsa->kind != JVal::OBJ || !opt_u32(dsa, "block_size", 64, &bs) || !opt_u32(dsa, "top_k_blocks", 16, &tk) ||
+            !opt_u32(dsa, "min_seq_len_for_sparsity", 2048, &mn)) {
+            err = "GGUF config dsa_config is not a valid object";
+            return AARH_ERR_CHECKPOINT;
+        }
+        if (bs < 16 || bs > 256 || (bs & (bs - 1))) return cfg_err("dsa.block_size must be a power of two in 16..=256");
+        if (tk == 0) return cfg_err("dsa.top_k_blocks must be non-zero");
+        if (mn < bs) return cfg_err("dsa.min_seq_len_for_sparsity must be at least dsa.block_size");
+        // Sparse slots are the schedule's full-attention layers that are not MLA layers
+        bool any_sparse = false;
+        for (int64_t l = 0; l < layers; l++) any_sparse = any_sparse || (!is_mla[(size_t)l] && l % full_every == 0);
+        if (!any_sparse) return cfg_err("dsa_config does not select any sparse attention layer");
+    }
+    if (!unsupported.empty()) {
+        err = unsupported;
+        return AARH_ERR_UNSUPPORTED;
+    }
+    if (!tie->b) {
+        err = "the latent context's LM head is tied to the embedding; the checkpoint has tie_embeddings false";
+        return AARH_ERR_UNSUPPORTED;
+    }
+    out->vocab_size = (int32_t)vocab;
+    out->hidden_dim = (int32_t)hidden;
+    out->n_layers = (int32_t)layers;
+    out->n_heads = (int32_t)mheads;
+    out->max_seq_len = (int32_t)max_seq;
+    out->rope_theta = (float)th->num;
+    out->norm_eps = (float)ep->num;
+    out->latent_dim = (int32_t)latent;
+    out->rope_dim = (int32_t)rope;
+    out->nope_dim = (int32_t)nope;
+    out->v_dim = (int32_t)vdim;
+    out->n_experts = (int32_t)routed;
+    out->top_k = (int32_t)top_k;
+    out->expert_dim = (int32_t)(exp_ffn / fine);
+    out->n_shared = (int32_t)n_shared;
+    return 0;
+}
+
+// The latent file's shape against the context's (as check_gguf_config for the dense context).
+int check_lat_gguf_config(aarh_lat_ctx* c, const JVal& meta) {
+    aarh_lat_config want{}, got{};
+    aarh_lat_get_config(c, &want);
+    std::string err;
+    int r = lat_config_from_json(meta, &got, err);
+    if (r) return fail_ctx(c, r, err);
+    const struct {
+        const char* key;
+        int32_t file, ctx;
+    } f[] = {{"vocab_size", got.vocab_size, want.vocab_size},  {"hidden_dim", got.hidden_dim, want.hidden_dim},
+             {"n_layers", got.n_layers, want.n_layers},        {"mla n_heads", got.n_heads, want.n_heads},
+             {"mla latent_dim", got.latent_dim, want.latent_dim}, {"mla rope_head_dim", got.rope_dim, want.rope_dim},
+             {"mla nope_head_dim", got.nope_dim, want.nope_dim}, {"mla value_head_dim", got.v_dim, want.v_dim},
+             {"routed experts", got.n_experts, want.n_experts}, {"moe top_k", got.top_k, want.top_k},
+             {"fine expert width", got.expert_dim, want.expert_dim},
+             {"moe num_shared_experts", got.n_shared, want.n_shared}};
+    for (const auto& x : f)
+        if (x.file != x.ctx)
+            return fail_ctx(c, AARH_ERR_CONFIG, std::string("checkpoint ") + x.key + " " + std::to_string(x.file) +
+                                                    " does not match the context's " + std::to_string(x.ctx));
+    if (got.rope_theta != want.rope_theta || got.norm_eps != want.norm_eps)
+        return fail_ctx(c, AARH_ERR_CONFIG, "checkpoint rope_theta / norm_eps do not match the context's configuration");
+    return 0;
+}
+
+// Every GGUF tensor the context names, decoded and uploaded; every context tensor required.
+template <class Ctx>
+int load_gguf_into(Ctx* c, Gguf& g, int32_t* out_loaded) {
+    auto slots = context_slots(c);
+    int loaded = 0, r;
+    std::string err;
+    std::vector<float> vals;
+    for (const GgufTensor& t : g.tensors) {
+        auto it = slots.find(t.name);
+        if (it == slots.end()) continue;  // tensors of other layer kinds (VarBuilder reads by name)
+        if (!shape_matches(t.shape, it->second))
+            return fail_ctx(c, AARH_ERR_SHAPE, "checkpoint tensor " + t.name + " has a shape the model does not expect");
+        if ((r = gguf_decode(g, t, vals, err))) return fail_ctx(c, r, err);
+        if ((r = load_f32(c, it->second.id, vals.data(), (int64_t)vals.size()))) return r;
+        it->second.loaded = true;
+        loaded++;
+    }
+    for (const auto& kv : slots)
+        if (!kv.second.loaded) return fail_ctx(c, AARH_ERR_CHECKPOINT, "checkpoint lacks tensor " + kv.first);
+    if (out_loaded) *out_loaded = loaded;
+    return AARH_OK;
+}
+
+template <class Ctx>
+int load_safetensors_into(Ctx* c, const char* path, int32_t* out_loaded) {
+    File file;
+    std::vector<StTensor> ts;
+    uint64_t data_off = 0;
+    std::string err;
+    int r = st_open(path, file, ts, &data_off, err);
+    if (r) return fail_ctx(c, r, err);
+    auto slots = context_slots(c);
+    int loaded = 0;
+    std::vector<float> vals;
+    for (const StTensor& t : ts) {
+        auto it = slots.find(t.name);
+        if (it == slots.end()) continue;
+        if (!shape_matches(t.shape, it->second))
+            return fail_ctx(c, AARH_ERR_SHAPE, "checkpoint tensor " + t.name + " has a shape the model does not expect");
+        if ((r = st_decode(file, data_off, t, vals, err))) return fail_ctx(c, r, err);
+        if ((r = load_f32(c, it->second.id, vals.data(), (int64_t)vals.size()))) return r;
+        it->second.loaded = true;
+        loaded++;
+    }
+    for (const auto& kv : slots)
+        if (!kv.second.loaded) return fail_ctx(c, AARH_ERR_CHECKPOINT, "checkpoint lacks tensor " + kv.first);
+    if (out_loaded) *out_loaded = loaded;
+    return AARH_OK;
+}
+
 // IEEE binary16 nearest value, ties to even (the conversion of a float to _Float16).
 uint16_t f32_to_f16_rne(float f) {
     uint32_t x;
@@ -678,49 +1008,39 @@ int aarh_load_gguf(aarh_ctx* c, const char* path, int32_t* out_loaded) {
     int r = gguf_open(path, g, err);
     if (r) return fail_ctx(c, r, err);
     if ((r = check_gguf_config(c, g.meta))) return r;
-    auto slots = context_slots(c);
-    int loaded = 0;
-    std::vector<float> vals;
-    for (const GgufTensor& t : g.tensors) {
-        auto it = slots.find(t.name);
-        if (it == slots.end()) continue;  // tensors of other layer kinds (VarBuilder reads by name)
-        if (!shape_matches(t.shape, it->second))
-            return fail_ctx(c, AARH_ERR_SHAPE, "checkpoint tensor " + t.name + " has a shape the model does not expect");
-        if ((r = gguf_decode(g, t, vals, err))) return fail_ctx(c, r, err);
-        if ((r = aarh_load_tensor_f32(c, it->second.id, vals.data(), (int64_t)vals.size()))) return r;
-        it->second.loaded = true;
-        loaded++;
-    }
-    for (const auto& kv : slots)
-        if (!kv.second.loaded) return fail_ctx(c, AARH_ERR_CHECKPOINT, "checkpoint lacks tensor " + kv.first);
-    if (out_loaded) *out_loaded = loaded;
-    return AARH_OK;
+    return load_gguf_into(c, g, out_loaded);
 }
 
 int aarh_load_safetensors(aarh_ctx* c, const char* path, int32_t* out_loaded) {
     if (!c || !path) return AARH_ERR_CONFIG;
-    File file;
-    std::vector<StTensor> ts;
-    uint64_t data_off = 0;
+    return load_safetensors_into(c, path, out_loaded);
+}
+
+int aarh_lat_load_gguf(aarh_lat_ctx* c, const char* path, int32_t* out_loaded) {
+    if (!c || !path) return AARH_ERR_CONFIG;
+    Gguf g;
     std::string err;
-    int r = st_open(path, file, ts, &data_off, err);
+    int r = gguf_open(path, g, err);
     if (r) return fail_ctx(c, r, err);
-    auto slots = context_slots(c);
-    int loaded = 0;
-    std::vector<float> vals;
-    for (const StTensor& t : ts) {
-        auto it = slots.find(t.name);
-        if (it == slots.end()) continue;
-        if (!shape_matches(t.shape, it->second))
-            return fail_ctx(c, AARH_ERR_SHAPE, "checkpoint tensor " + t.name + " has a shape the model does not expect");
-        if ((r = st_decode(file, data_off, t, vals, err))) return fail_ctx(c, r, err);
-        if ((r = aarh_load_tensor_f32(c, it->second.id, vals.data(), (int64_t)vals.size()))) return r;
-        it->second.loaded = true;
-        loaded++;
+    if ((r = check_lat_gguf_config(c, g.meta))) return r;
+    return load_gguf_into(c, g, out_loaded);
+}
+
+int aarh_lat_load_safetensors(aarh_lat_ctx* c, const char* path, int32_t* out_loaded) {
+    if (!c || !path) return AARH_ERR_CONFIG;
+    return load_safetensors_into(c, path, out_loaded);
+}
+
+int aarh_lat_gguf_config(const char* path, aarh_lat_config* out) {
+    if (!path || !out) {
+        g_host_err = "null path or config";
+        return AARH_ERR_CONFIG;
     }
-    for (const auto& kv : slots)
-        if (!kv.second.loaded) return fail_ctx(c, AARH_ERR_CHECKPOINT, "checkpoint lacks tensor " + kv.first);
-    if (out_loaded) *out_loaded = loaded;
+    Gguf g;
+    std::string err;
+    int r = gguf_open(path, g, err);
+    if (r) return fail_ctx((aarh_ctx*)nullptr, r, err);
+    if ((r = lat_config_from_json(g.meta, out, err))) return fail_ctx((aarh_ctx*)nullptr, r, err);
     return AARH_OK;
 }
 
@@ -812,9 +1132,9 @@ int aarh_gguf_config(const char* path, aarh_model_config* out) {
     Gguf g;
     std::string err;
     int r = gguf_open(path, g, err);
-    if (r) return fail_ctx(nullptr, r, err);
+    if (r) return fail_ctx((aarh_ctx*)nullptr, r, err);
     const JVal* cfg = g.meta.get("config");
-    if (!cfg || cfg->kind != JVal::OBJ) return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF metadata has no model config");
+    if (!cfg || cfg->kind != JVal::OBJ) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_CHECKPOINT, "GGUF metadata has no model config");
     const struct {
         const char* key;
         int32_t* dst;
@@ -824,17 +1144,17 @@ int aarh_gguf_config(const char* path, aarh_model_config* out) {
     for (const auto& fld : ints) {
         int64_t v = 0;
         if (!json_i64(cfg->get(fld.key), &v) || v < 0 || v > INT32_MAX)
-            return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, std::string("GGUF config lacks a valid ") + fld.key);
+            return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_CHECKPOINT, std::string("GGUF config lacks a valid ") + fld.key);
         *fld.dst = (int32_t)v;
     }
     const JVal* th = cfg->get("rope_theta");
     const JVal* ep = cfg->get("norm_eps");
     if (!th || th->kind != JVal::NUM || !ep || ep->kind != JVal::NUM)
-        return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks rope_theta / norm_eps");
+        return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks rope_theta / norm_eps");
     out->rope_theta = (float)th->num;
     out->norm_eps = (float)ep->num;
     const JVal* tie = cfg->get("tie_embeddings");
-    if (!tie || tie->kind != JVal::BOOL) return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks tie_embeddings");
+    if (!tie || tie->kind != JVal::BOOL) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_CHECKPOINT, "GGUF config lacks tie_embeddings");
     out->untied_lm_head = tie->b ? 0 : 1;
     out->num_future_tokens = 0;
     const JVal* mtp = cfg->get("mtp");
@@ -853,10 +1173,10 @@ int aarh_gguf_rope_scaling(const char* path, aarh_rope_scaling* out) {
     Gguf g;
     std::string err;
     int r = gguf_open(path, g, err);
-    if (r) return fail_ctx(nullptr, r, err);
+    if (r) return fail_ctx((aarh_ctx*)nullptr, r, err);
     const JVal* cfg = g.meta.get("config");
-    if (!cfg || cfg->kind != JVal::OBJ) return fail_ctx(nullptr, AARH_ERR_CHECKPOINT, "GGUF metadata has no model config");
-    if ((r = parse_rope_scaling(cfg, out, err))) return fail_ctx(nullptr, r, err);
+    if (!cfg || cfg->kind != JVal::OBJ) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_CHECKPOINT, "GGUF metadata has no model config");
+    if ((r = parse_rope_scaling(cfg, out, err))) return fail_ctx((aarh_ctx*)nullptr, r, err);
     return AARH_OK;
 }
 
@@ -869,7 +1189,7 @@ int aarh_gguf_read_tensor(const char* path, const char* name, float* out, int64_
     Gguf g;
     std::string err;
     int r = gguf_open(path, g, err);
-    if (r) return fail_ctx(nullptr, r, err);
+    if (r) return fail_ctx((aarh_ctx*)nullptr, r, err);
     for (const GgufTensor& t : g.tensors) {
         if (t.name != name) continue;
         const int64_t n = numel(t.shape);
@@ -879,13 +1199,13 @@ int aarh_gguf_read_tensor(const char* path, const char* name, float* out, int64_
             for (size_t d = 0; d < t.shape.size(); d++) out_shape[d] = t.shape[d];
         if (out_encoding) *out_encoding = t.enc;
         if (!out) return AARH_OK;
-        if (cap < n) return fail_ctx(nullptr, AARH_ERR_SHAPE, "output buffer too small for " + t.name);
+        if (cap < n) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_SHAPE, "output buffer too small for " + t.name);
         std::vector<float> vals;
-        if ((r = gguf_decode(g, t, vals, err))) return fail_ctx(nullptr, r, err);
+        if ((r = gguf_decode(g, t, vals, err))) return fail_ctx((aarh_ctx*)nullptr, r, err);
         memcpy(out, vals.data(), (size_t)n * 4);
         return AARH_OK;
     }
-    return fail_ctx(nullptr, AARH_ERR_SHAPE, std::string("no tensor ") + name + " in " + path);
+    return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_SHAPE, std::string("no tensor ") + name + " in " + path);
 }
 
 int aarh_safetensors_read_tensor(const char* path, const char* name, float* out, int64_t cap, int64_t* out_numel,
@@ -899,23 +1219,23 @@ int aarh_safetensors_read_tensor(const char* path, const char* name, float* out,
     uint64_t data_off = 0;
     std::string err;
     int r = st_open(path, file, ts, &data_off, err);
-    if (r) return fail_ctx(nullptr, r, err);
+    if (r) return fail_ctx((aarh_ctx*)nullptr, r, err);
     for (const StTensor& t : ts) {
         if (t.name != name) continue;
-        if (t.shape.size() > 8) return fail_ctx(nullptr, AARH_ERR_SHAPE, "tensor " + t.name + " has more than 8 dims");
+        if (t.shape.size() > 8) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_SHAPE, "tensor " + t.name + " has more than 8 dims");
         const int64_t n = numel(t.shape);
         if (out_numel) *out_numel = n;
         if (out_ndims) *out_ndims = (int32_t)t.shape.size();
         if (out_shape)
             for (size_t d = 0; d < t.shape.size(); d++) out_shape[d] = t.shape[d];
         if (!out) return AARH_OK;
-        if (cap < n) return fail_ctx(nullptr, AARH_ERR_SHAPE, "output buffer too small for " + t.name);
+        if (cap < n) return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_SHAPE, "output buffer too small for " + t.name);
         std::vector<float> vals;
-        if ((r = st_decode(file, data_off, t, vals, err))) return fail_ctx(nullptr, r, err);
+        if ((r = st_decode(file, data_off, t, vals, err))) return fail_ctx((aarh_ctx*)nullptr, r, err);
         memcpy(out, vals.data(), (size_t)n * 4);
         return AARH_OK;
     }
-    return fail_ctx(nullptr, AARH_ERR_SHAPE, std::string("no tensor ") + name + " in " + path);
+    return fail_ctx((aarh_ctx*)nullptr, AARH_ERR_SHAPE, std::string("no tensor ") + name + " in " + path);
 }
 
 }  // extern "C"

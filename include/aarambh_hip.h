@@ -389,6 +389,29 @@ int aarh_lat_num_tensors(const aarh_lat_ctx *ctx);
 int aarh_lat_tensor_info(const aarh_lat_ctx *ctx, int id, char *name, int name_cap, int64_t *rows,
                          int64_t *cols, int32_t *kind);
 int aarh_lat_load_tensor_f32(aarh_lat_ctx *ctx, int id, const float *host, int64_t numel);
+/* The configuration the latent context was created with. */
+int aarh_lat_get_config(const aarh_lat_ctx *ctx, aarh_lat_config *out);
+/* Checkpoints of an MLA + MoE model (AarambhModel::new over the checkpoint's VarBuilder,
+   model.rs:82-279: block_vb.pp("mla") per MLA layer, ffn.router / ffn.experts.{e} /
+   ffn.shared_experts.{s} per MoE layer), read and decoded as aarh_load_gguf /
+   aarh_load_safetensors do.  GGUF: the file's config is validated as
+   AarambhModel::validate_config does (model.rs:281-344: MoeConfig, the attention schedule
+   with its MLA and Gated DeltaNet settings, RopeScalingConfig, dsa_config; CONFIG with the
+   reference's message), then must describe what a latent context holds -- MLA in every
+   layer (attention_schedule.mla_layers = 0..n_layers), MoE in every layer
+   (moe.every_n_layers = 1) and a tied LM head (UNSUPPORTED otherwise) -- and match the
+   context's shape (CONFIG).  rope_scaling is validated but changes nothing, since MLA keeps
+   an unscaled RoPE cache (model.rs:1107-1116); mtp heads are not part of the latent
+   context and are not read.  Every context tensor must be present with its shape. */
+int aarh_lat_load_gguf(aarh_lat_ctx *ctx, const char *path, int32_t *out_loaded);
+int aarh_lat_load_safetensors(aarh_lat_ctx *ctx, const char *path, int32_t *out_loaded);
+/* A GGUF file's config resolved into the latent shape fields of *out (vocab_size,
+   hidden_dim, n_layers, n_heads = resolved MLA heads, max_seq_len, rope_theta, norm_eps,
+   latent/rope/nope/v widths from MlaConfig::resolve, n_experts = num_experts x
+   fine_grained_factor, top_k, expert_dim = expert_ffn_dim / fine_grained_factor,
+   n_shared = num_shared_experts); same checks and errors as aarh_lat_load_gguf's config
+   step, message in aarh_host_last_error.  Formats and sizing are left to the caller. */
+int aarh_lat_gguf_config(const char *path, aarh_lat_config *out);
 /* A PackedInt4Tensor (quant/src/types.rs:79-90) into an INT4 g128 tensor of the latent
    decoder (experts in expert_format, MLA projections and the router in attn_format);
    same rules, rounding and errors as aarh_load_tensor_packed_i4. */

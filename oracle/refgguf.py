@@ -174,6 +174,33 @@ def model_config_json(vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_h
     return cfg
 
 
+def lat_model_config_json(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, latent_dim, rope_dim, nope_dim,
+                          v_dim, n_experts, top_k, expert_dim, n_shared, rope_theta=10000.0, norm_eps=1e-5,
+                          fine_grained_factor=1, mla_heads=None, **_formats):
+    """ModelConfig of an MLA + MoE decoder (config.rs:732-776 with MoeConfig :99-130,
+    HybridAttentionSchedule :626-654 listing every layer in mla_layers, MlaConfig :529-556)
+    as serde_json writes it.  n_heads is the transformer's head count and, unless mla_heads
+    is given, the MLA head count too; n_experts routed fine experts come from
+    n_experts / fine_grained_factor coarse experts of width expert_dim * fine_grained_factor."""
+    assert n_experts % fine_grained_factor == 0
+    return {
+        "vocab_size": vocab_size, "hidden_dim": hidden_dim, "ffn_dim": 4 * hidden_dim, "n_layers": n_layers,
+        "n_heads": n_heads, "n_kv_heads": n_heads, "max_seq_len": max_seq_len, "rope_theta": rope_theta,
+        "moe": {"num_experts": n_experts // fine_grained_factor, "top_k": top_k,
+                "expert_ffn_dim": expert_dim * fine_grained_factor, "aux_loss_weight": 0.01, "every_n_layers": 1,
+                "fine_grained_factor": fine_grained_factor, "num_shared_experts": n_shared},
+        "attention_schedule": {
+            "full_attention_every_n": 4,
+            "gated_deltanet": {"n_heads": 0, "key_head_dim": 0, "value_head_dim": 0, "conv_kernel_size": 4,
+                               "chunk_size": 64},
+            "mla_layers": list(range(n_layers)),
+            "mla": {"latent_dim": latent_dim, "nope_head_dim": nope_dim, "rope_head_dim": rope_dim,
+                    "n_heads": n_heads if mla_heads is None else mla_heads, "value_head_dim": v_dim}},
+        "norm_eps": norm_eps,
+        "tie_embeddings": True,
+    }
+
+
 def save_gguf(path, config, fmt, tensors):
     """save_gguf (gguf.rs:47-72): magic, version, JSON metadata, tensors sorted by name,
     each with its shape, encoding byte and payload."""

@@ -14,6 +14,8 @@
 
 namespace aarh {
 int ctx_fail(aarh_ctx*, int code, const char*) { return code; }
+int lat_ctx_fail(aarh_lat_ctx*, int code, const char*) { return code; }
+int rope_scaling_check(int, int, const aarh_rope_scaling*, std::string&) { return 0; }
 }  // namespace aarh
 extern "C" {
 int aarh_get_config(const aarh_ctx*, aarh_model_config*) { return AARH_ERR_CONFIG; }
@@ -21,6 +23,10 @@ int aarh_num_tensors(const aarh_ctx*) { return 0; }
 int aarh_tensor_info(const aarh_ctx*, int, char*, int, int64_t*, int64_t*, int32_t*) { return AARH_ERR_SHAPE; }
 int aarh_load_tensor_f32(aarh_ctx*, int, const float*, int64_t) { return AARH_ERR_CONFIG; }
 int aarh_set_rope_scaling(aarh_ctx*, const aarh_rope_scaling*) { return AARH_ERR_CONFIG; }
+int aarh_lat_get_config(const aarh_lat_ctx*, aarh_lat_config*) { return AARH_ERR_CONFIG; }
+int aarh_lat_num_tensors(const aarh_lat_ctx*) { return 0; }
+int aarh_lat_tensor_info(const aarh_lat_ctx*, int, char*, int, int64_t*, int64_t*, int32_t*) { return AARH_ERR_SHAPE; }
+int aarh_lat_load_tensor_f32(aarh_lat_ctx*, int, const float*, int64_t) { return AARH_ERR_CONFIG; }
 }
 
 static std::vector<unsigned char> slurp(const std::string& p) {
@@ -83,6 +89,7 @@ int main(int argc, char** argv) {
         }
         aarh_model_config mc{};
         aarh_rope_scaling rs{};
+        aarh_lat_config lc{};
         if (gguf && (aarh_gguf_config(p.c_str(), &mc) != AARH_OK || aarh_gguf_rope_scaling(p.c_str(), &rs) != AARH_OK))
             return 1;
         // every truncation and a sweep of single-byte corruptions end in a status code
@@ -91,7 +98,8 @@ int main(int argc, char** argv) {
         for (size_t cut = 0; cut < b.size(); cut += (cut < 256 ? 1 : 97)) {
             spit(q, std::vector<unsigned char>(b.begin(), b.begin() + cut));
             read_all(q, gguf);
-            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs);
+            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs),
+                (void)aarh_lat_gguf_config(q.c_str(), &lc);
         }
         unsigned seed = 12345;
         for (int t = 0; t < 400; t++) {
@@ -102,7 +110,8 @@ int main(int argc, char** argv) {
             m[at] = (unsigned char)(seed >> 16);
             spit(q, m);
             read_all(q, gguf);
-            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs);
+            if (gguf) (void)aarh_gguf_config(q.c_str(), &mc), (void)aarh_gguf_rope_scaling(q.c_str(), &rs),
+                (void)aarh_lat_gguf_config(q.c_str(), &lc);
         }
     }
     printf("checkpoint reader sanitizer run: ok\n");

@@ -254,3 +254,71 @@ def test_lat_packed_int4_tensors_equal_device_quantisation():
     assert compare(lc, hc, [ref.kv(128).forward(ids, 0)], gaps, 7) == 1
     for m in (a, b, c):
         m.close()
+
+
+def lat_checkpoint(ref, seed):
+    """Named f32 tensors in the reference's checkpoint shapes (1-D norms) for a latent model."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, r, c, kind in ref.tensors():
+        if kind == R.T_NORM:
+            out[name] = (1 + 0.1 * rng.normal(size=c)).astype(np.float32)
+        else:
+            out[name] = rng.normal(0, 0.05, (r, c)).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("kind", ["gguf-Q4KM", "gguf-Q80", "safetensors-BF16"])
+def test_lat_checkpoint_into_context(tmp_path, kind):
+    """An MLA + MoE checkpoint (model.rs:161-210 names, config resolved by
+    aarh_lat_gguf_config) loaded by aarh_lat_load_gguf / aarh_lat_load_safetensors equals
+    the oracle holding the values the oracle's reader decodes from the same file."""
+    import refgguf as G
+    kw = small_kw()
+    fmts = {k: kw[k] for k in ("expert_format", "attn_format", "lm_head_format", "kv_format")}
+    ref = R.LatModel(R.make_lat_config(**kw))
+    vals = lat_checkpoint(ref, 31)
+    vals["mtp.heads.0.trunk_norm.weight"] = np.ones(256, np.float32)  # not a latent-context tensor: ignored
+    if kind.startswith("gguf"):
+        path = str(tmp_path / "m.gguf")
+        G.save_gguf(path, G.lat_model_config_json(**kw, fine_grained_factor=2), kind[5:], vals)
+        cfg = A.LatConfig.from_gguf(path, **fmts)
+        want = A.LatConfig(**kw)
+        assert np.float32(cfg.norm_eps) == np.float32(want.norm_eps)
+        assert cfg == A.LatConfig(**dict(kw, norm_eps=cfg.norm_eps))
+        _, dec = G.load_gguf_tensors(path)
+    else:
+        path = str(tmp_path / "m.safetensors")
+        G.save_safetensors(path, vals, "BF16")
+        cfg = A.LatConfig(**kw)
+        dec = G.safetensors_values(vals, "BF16")
+    hip = A.HipLatModel(cfg, max_batch=3, max_rows=96)
+    load = hip.load_gguf if kind.startswith("gguf") else hip.load_safetensors
+    assert load(path) == len(hip.tensors()) == len(ref.tensors())
+    for i, (name, *_r) in enumerate(ref.tensors()):
+        ref.set(i, dec[name])
+    B, P, K = 3, 20, 4
+    ids = R.synth_tokens(32, 1, B * (P + K), kw["vocab_size"]).reshape(B, P + K)
+    kvs = [ref.kv(128) for _ in range(B)]
+    gl, gh = hip.forward_with_cache_output(ids[:, :P], [0] * B)
+    checked = compare(gl, gh, [kvs[b].forward(ids[b, :P], 0) for b in range(B)], hip.router_gaps(), P)
+    gl, gh = hip.forward_with_cache_output(ids[:, P:], [P] * B)
+    checked += compare(gl, gh, [kvs[b].forward(ids[b, P:], P) for b in range(B)], hip.router_gaps(), K)
+    assert checked >= 3
+    if kind == "gguf-Q80":
+        other = A.HipLatModel(A.LatConfig(**dict(kw, n_experts=16)), max_batch=1, max_rows=32)
+        with pytest.raises(A.ConfigError, match="routed experts 8 does not match the context's 16"):
+            other.load_gguf(path)
+        other.close()
+        short = {k: v for k, v in vals.items() if k != "blocks.1.ffn.experts.3.w_up.weight"}
+        p2 = str(tmp_path / "short.gguf")
+        G.save_gguf(p2, G.lat_model_config_json(**kw), "Q80", short)
+        with pytest.raises(A.CheckpointError, match="experts.3.w_up"):
+            hip.load_gguf(p2)
+        p3 = str(tmp_path / "dense.gguf")
+        G.save_gguf(p3, G.model_config_json(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=2, n_heads=4,
+                                            n_kv_heads=4, max_seq_len=128), "Q80", vals)
+        with pytest.raises(A.UnsupportedError, match="no moe"):
+            hip.load_gguf(p3)
+    hip.close()
+    ref.close()
