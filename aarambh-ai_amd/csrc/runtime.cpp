@@ -1890,9 +1890,22 @@ int session_round(aarh_session* e) {
             e->htok[b] = hp[cap + b];
             e->hdraws[b] = hp[2 * cap + b];
             e->hstatus[b] = hp[3 * cap + b];
-            // sample_probabilities validates the proposal distribution (sampler.rs:142-152, 314-335)
-            if (!e->greedy && !e->finished[b] && hp[(size_t)(5 + K) * cap + b] != 0)
-                return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
+        }
+        // sample_probabilities validates the proposal distribution (sampler.rs:142-152, 314-335):
+        // the reference fails at the proposal, before this round's verify.  The flags arrive with
+        // the acceptance read-back, so the round's verify is undone first: every sequence is
+        // left as the proposal step found it (cache length, statistics, keystream position).
+        bool invalid = false;
+        for (int b = 0; b < nseq; b++)
+            invalid = invalid || (!e->greedy && !e->finished[b] && hp[(size_t)(5 + K) * cap + b] != 0);
+        if (invalid) {
+            for (int b = 0; b < nseq; b++) {
+                if (e->finished[b]) continue;
+                c->kv_len[b] = e->base[b];
+                e->stats[b].rounds--;
+                e->stats[b].target_decode_forwards--;
+            }
+            return fail(c, AARH_ERR_CONFIG, "proposal distribution is invalid (zero mass or does not sum to one)");
         }
         memcpy(e->hprops.data(), hp.data() + 4 * cap, (size_t)nseq * K * 4);
         count_proposals();

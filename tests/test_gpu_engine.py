@@ -139,6 +139,36 @@ def test_mtp_session_top_candidates_match_oracle():
     hip.close()
 
 
+def test_invalid_sampled_proposal_fails_at_the_proposal():
+    """An MTP head whose logits are all NaN makes its proposal distribution invalid
+    (sample_probabilities, sampler.rs:142-152, 314-335): the round fails with the
+    reference's message, and the session is left as the proposal step found it (the
+    reference fails before the verify forward, mtp_speculative.rs:169-209), so the cache
+    length, the statistics and the keystream position are those of the previous round."""
+    kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=704, n_layers=2, n_heads=8, n_kv_heads=2, max_seq_len=96,
+              num_future_tokens=3)
+    ref, hip = make_pair(seed=41, std=0.05, **kw)
+    names = [t[0] for t in hip.tensors()]
+    eng = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(3))
+    prompt = R.synth_tokens(41, 1, 12, 1024)
+    s = A.Sampler(greedy=False, temperature=0.8, seed=5)
+    sess = eng.session(prompt[None], 20, s, seeds=np.array([5], np.uint64))
+    sess.step(1)  # one good round
+    out = sess.result()[0]
+    st0, off0, kv0, n0 = out.speculative_stats, int(sess.rng_offsets()[0]), hip.kv_len(0), len(out.token_ids)
+    assert st0.rounds == 1 and kv0 == len(prompt) + n0
+    hip.load_f32(names.index("mtp.heads.1.output_norm.weight"), np.full(256, np.nan, np.float32))
+    with pytest.raises(A.ConfigError, match="proposal distribution is invalid"):
+        sess.step(1)
+    st1 = sess.result()[0].speculative_stats
+    assert (st1.rounds, st1.target_decode_forwards, st1.draft_tokens_proposed, st1.mtp_head_forwards) == \
+        (st0.rounds, st0.target_decode_forwards, st0.draft_tokens_proposed, st0.mtp_head_forwards)
+    assert int(sess.rng_offsets()[0]) == off0 and hip.kv_len(0) == kv0
+    assert len(sess.result()[0].token_ids) == n0
+    sess.close()
+    hip.close()
+
+
 def test_context_limit_and_engine_validation():
     kw = dict(vocab_size=1024, hidden_dim=256, ffn_dim=512, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=16,
               num_future_tokens=3)
