@@ -133,7 +133,7 @@ struct SelShared {
 struct AccShared {
     SelShared sel;
     SeqScan scan;
-    float red_f[ACC_WAVES];
+    float red_f[ACC_WAVES], red_g[ACC_WAVES];
     int red_k[ACC_WAVES], red_i[ACC_WAVES];
     unsigned n;
     unsigned is_last;
@@ -550,9 +550,15 @@ __device__ __forceinline__ int topk_band(float l, float mx, float rinv) {
 // max / min, one counting the logits of each band in the top quarter of the range, one
 // gathering the narrowest upper set of bands holding at least k logits (at most
 // TOPK_GATHER keys); ranking those keys gives the k-th key, and ranking the k survivors
-// by index puts them in keys[0..k) as topk_survivors leaves them.  Returns false (the
-// caller falls back to the radix select) on non-finite logits, a constant row, or when
-// no band set of at most TOPK_GATHER logits holds k.
+// by index puts them in keys[0..k) as topk_survivors leaves them.
+// Rows with a few logits far above the rest (an MTP head scores the token it was fed far
+// above every other) hold fewer than k logits in the top quarter.  The counting pass also
+// takes the largest logit below the top quarter, and a second counting pass bands the
+// rest of the row below that maximum; the gathered set is then the top-quarter logits
+// plus the narrowest upper set of second-level bands that completes k.  Both sets are
+// upper sets in logit value, so their union holds the k largest keys.
+// Returns false (the caller falls back to the radix select) on non-finite logits, a
+// constant row, or when no band set of at most TOPK_GATHER logits holds k.
 __device__ inline bool topk_fast_select(const float* row, int V, int k, float* buf, AccShared* sh, uint64_t* kkey) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     unsigned long long* keys = (unsigned long long*)buf;
@@ -591,33 +597,72 @@ __device__ inline bool topk_fast_select(const float* row, int V, int k, float* b
         return false;
     }
     const float rinv = 1.0f / R;
+    float below = -INFINITY;  // largest logit outside the top quarter
     rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
         const int b = valid ? topk_band(l, mx, rinv) : 0;
         if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
+        else if (valid) below = fmaxf(below, l);
     });
+    below = wave_max_f32(below);
+    if (lane == 0) sh->red_g[wid] = below;
     __syncthreads();
-    if (tid == 0) {
-        int pick = -1;
-        unsigned acc = 0, cnt = 0;
+    // pick: the lowest band of the narrowest upper set holding `need` logits; -1 when the
+    // counted bands hold fewer (top: their total), -2 when that set exceeds `room`
+    auto pick_band = [&](unsigned need, unsigned room) {
+        unsigned acc = 0;
         for (int b = 63; b >= 8; b--) {
             acc += sh->sel.hist[b];
-            if (acc >= (unsigned)k) {
-                pick = b;
-                cnt = acc;
-                break;
+            if (acc >= need) {
+                sh->sel.digit = acc <= room ? b : -2;
+                return;
             }
         }
-        sh->sel.digit = (pick >= 0 && cnt <= (unsigned)TOPK_GATHER) ? pick : -1;
+        sh->sel.digit = -1;
+        sh->sel.total = acc;
+    };
+    if (tid == 0) {
+        pick_band((unsigned)k, (unsigned)TOPK_GATHER);
         sh->n = 0;
     }
     __syncthreads();
-    const int band = sh->sel.digit;
-    if (band < 0) {
+    int band = sh->sel.digit;
+    if (band == -2) {
         __syncthreads();
         return false;
     }
+    // second level: the top quarter holds `top` < k logits; band the rest below its maximum
+    float mx1 = 0.0f, rinv1 = 0.0f;
+    int band1 = 64;
+    if (band == -1) {
+        const unsigned top = sh->sel.total;
+        mx1 = -INFINITY;
+        for (int w = 0; w < ACC_WAVES; w++) mx1 = fmaxf(mx1, sh->red_g[w]);
+        const float R1 = mx1 - mn;
+        __syncthreads();
+        if (!(R1 > 0.0f) || !isfinite(R1)) return false;
+        rinv1 = 1.0f / R1;
+        if (tid < 64) sh->sel.hist[tid] = 0u;
+        __syncthreads();
+        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+            const int b = (valid && topk_band(l, mx, rinv) < 8) ? topk_band(l, mx1, rinv1) : 0;
+            if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
+        });
+        __syncthreads();
+        if (tid == 0) pick_band((unsigned)k - top, (unsigned)TOPK_GATHER - top);
+        __syncthreads();
+        band1 = sh->sel.digit;
+        if (band1 < 0) {
+            __syncthreads();
+            return false;
+        }
+        band = 8;  // the whole top quarter
+    }
     const int c = min(gather_rare(
-                          row, V, [&](float l, int j) { return topk_band(l, mx, rinv) >= band; },
+                          row, V,
+                          [&](float l, int j) {
+                              const int b = topk_band(l, mx, rinv);
+                              return b >= band || (band1 < 64 && b < 8 && topk_band(l, mx1, rinv1) >= band1);
+                          },
                           [](float l, int j) { return (unsigned long long)logit_key(l, j); }, cand, TOPK_GATHER, sh),
                       TOPK_GATHER);
     // the k largest candidate keys, by rank; the k-th is the top-k cut

@@ -243,6 +243,38 @@ def test_top_k_top_p_variants_match_oracle(ctx, top_k, top_p):
         assert same.mean() >= 0.85
 
 
+@pytest.mark.parametrize("n_out", [1, 3, 49, 60])
+@pytest.mark.parametrize("top_p", [0.0, 0.9])
+def test_top_k_rows_with_outlier_logits(ctx, n_out, top_p):
+    """Rows where n_out logits sit far above a N(0, 0.7^2) bulk, as an MTP head scores
+    the token it was fed: with fewer than k = 50 outliers the top quarter of the range
+    holds fewer than k logits and the top-k cut lies in the bulk (the selection's second
+    banding level), with 60 it lies among the outliers.  Proposal draws (K = 0) and
+    acceptance with bonus bit-identical to the oracle except flagged draws."""
+    rng = np.random.default_rng(70 + n_out)
+    B, K, V = 8, 3, 32000
+    tgt = rng.normal(0, 0.7, (B, K + 1, V)).astype(np.float32)
+    drf = (tgt[:, :K] + rng.normal(0, 0.3, (B, K, V))).astype(np.float32)
+    for a in (tgt, drf):
+        for b in range(B):
+            for i in range(a.shape[1]):
+                idx = rng.choice(V, n_out, replace=False)
+                a[b, i, idx] = rng.uniform(12.0, 16.0, n_out).astype(np.float32)
+    s = R.sampler(temperature=0.7, top_k=50, top_p=top_p)
+    toks = np.zeros((B, K), np.uint32)
+    for b in range(B):
+        r = R.Rng(40_000 + b)
+        for i in range(K):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    out, ref = run_both(ctx, tgt, drf, toks, 0.7, True, seeds=np.arange(B, dtype=np.uint64) + 9, top_k=50,
+                        top_p=top_p)
+    assert_parity(out, ref, max_flag_frac=0.25)
+    # proposal draws: one row per sequence, sampling only
+    out, ref = run_both(ctx, drf[:, :1], np.zeros((B, 0, V), np.float32), np.zeros((B, 0), np.uint32), 0.7, True,
+                        seeds=np.arange(B, dtype=np.uint64) + 19, top_k=50, top_p=top_p)
+    assert_parity(out, ref, max_flag_frac=0.25)
+
+
 def test_top_k_keeps_lower_index_among_ties(ctx):
     """Stable total_cmp ranking: among equal logits at the top-k boundary the lower
     token ids are kept (sampler.rs:238-245), so the bonus draw can only land on them."""
