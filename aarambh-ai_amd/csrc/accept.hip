@@ -576,6 +576,7 @@ __device__ inline bool topk_fast_select(const float* row, int V, int k, float* b
             }
         }
     });
+
     mx = wave_max_f32(mx);
     mn = -wave_max_f32(-mn);
     nonfin = __any(nonfin) ? 1 : 0;
@@ -804,6 +805,8 @@ __device__ __forceinline__ void row_filter(const float* row, int V, float T, int
                 f.kkey = select_desc(kf, row, V, top_k, ~0ull, sh, &tot);
                 n = topk_survivors(row, V, f.kkey, (unsigned long long*)buf, sh);
             }
+            // survivors stay in buf[0 .. 2 n) (keys sorted by index) for a resolver in this workgroup
+            if (threadIdx.x == 0) sh->ib[6] = n;
             row_filter_topk(top_p, n, buf, sh, f, flags, status);
             return;
         }
@@ -927,14 +930,15 @@ __device__ __forceinline__ RowFilt rs_load_uniform(const uint32_t* w, float T) {
 // The resolver's draw on the compact top-k path.  wd == nullptr: the bonus draw from
 // the target row's distribution.  Otherwise the residual max(0, p - q), which is 0
 // outside the target row's top-k survivors: its exact mass, then its exact CDF.
+// have >= 0: the survivors of the target row are already in lds (this workgroup filtered it).
 __device__ __noinline__ void resolve_compact(const uint32_t* wt, const uint32_t* wd, const float* tl, const float* dl,
                                              int V, float T, float u, float* lds, AccShared* sh, SeqScan* cdf,
-                                             int* status) {
+                                             int* status, int have) {
     const int tid = threadIdx.x;
     unsigned long long* ckeys = (unsigned long long*)lds;
     float* cvals = lds + 2 * TOPK_FAST;
     const RowFilt ft = rs_load_uniform(wt, T);
-    const int n = topk_survivors(tl, V, ft.kkey, ckeys, sh);
+    const int n = have >= 0 ? have : topk_survivors(tl, V, ft.kkey, ckeys, sh);
     if (wd) {
         const RowFilt fd = rs_load_uniform(wd, T);
         for (int i = tid; i < n; i += ACC_THREADS) {
@@ -1006,9 +1010,25 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
     const float* drow0 = a.draft + (size_t)b * a.K * V;
     const float T = a.temperature;
 
+    // The resolution draws at most np + 1 uniforms (one per acceptance test, one resample),
+    // keystream words word .. word + np: lane d of wave 0 computes draw d (one ChaCha block
+    // each, in parallel) instead of thread 0 computing them one after another.
+    __shared__ float u_s[64];
+    const bool par_u = !a.greedy && np + 1 <= 64;
+    if (par_u && tid <= np) {
+        if (a.uniforms) {
+            u_s[tid] = a.uniforms[(size_t)b * (a.K + 1) + tid];
+        } else {
+            uint32_t key[8];
+            rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
+            u_s[tid] = rng_f32(key, (a.word_offsets ? a.word_offsets[b] : 0ull) + tid);
+        }
+    }
+    __syncthreads();
+
     if (tid == 0) {
         uint32_t key[8];
-        rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
+        if (!par_u) rng_key_from_seed(a.seeds ? a.seeds[b] : 0ull, key);
         const uint64_t word = a.word_offsets ? a.word_offsets[b] : 0ull;
         int draws = 0, acc = 0, rej = -1, status = 0;
         uint32_t flags = 0;
@@ -1039,7 +1059,9 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
                 rej = i;
                 break;
             }
-            const float u = a.uniforms ? a.uniforms[(size_t)b * (a.K + 1) + draws] : rng_f32(key, word + draws);
+            const float u = par_u       ? u_s[draws]
+                            : a.uniforms ? a.uniforms[(size_t)b * (a.K + 1) + draws]
+                                         : rng_f32(key, word + draws);
             draws++;
             const float ratio = p / q;
             float cl = ratio < 1.0f ? ratio : 1.0f;
@@ -1076,7 +1098,9 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
         else if (a.bonus) token = (int)rs_get(rs0 + np * ACC_RS_WORDS, RS_ARGMAX);
     } else if (status == 0 && (rej >= 0 || a.bonus)) {
         float u;
-        {
+        if (par_u) {
+            u = u_s[draws];
+        } else {
             uint32_t key[8];
             if (a.uniforms) {
                 u = a.uniforms[(size_t)b * (a.K + 1) + draws];
@@ -1088,9 +1112,11 @@ __global__ void __launch_bounds__(ACC_THREADS) __attribute__((amdgpu_waves_per_e
         SeqScan cdf = seq_scan_init();
         if (topk_compact(a.top_k, V)) {
             const int row = rej >= 0 ? rej : np;
+            // a one-row launch (a proposal draw) filtered that row in this workgroup
+            const int have = (rows_per_seq == 1 && rej < 0 && needed) ? sh.ib[6] : -1;
             resolve_compact(rs0 + row * ACC_RS_WORDS, rej >= 0 ? rsd0 + rej * ACC_RS_WORDS : nullptr,
                             trow0 + (size_t)row * V, rej >= 0 ? drow0 + (size_t)rej * V : nullptr, V, T, u, lds, &sh,
-                            &cdf, &status);
+                            &cdf, &status, have);
         } else if (rej >= 0) {
             // residual max(0, p - q): exact mass, then the exact CDF of r / mass
             const RowFilt ft = rs_load(rs0 + rej * ACC_RS_WORDS, T);
