@@ -41,7 +41,10 @@ static constexpr int TOPP_LDS_FLOATS = TOPP_PAGE * 3;  // page keys (8 B) + thei
 // order.  LDS: survivor keys (8 B), values (4 B) and top-p keys (8 B) per survivor.
 static constexpr int TOPK_FAST = 1024;
 static constexpr int TOPK_GATHER = 2048;  // candidate keys of the threshold selection (8 B each)
-static constexpr int TOPK_LDS_FLOATS = TOPK_FAST * 5 + TOPK_GATHER * 2;
+// The fast selection's candidate lists (value, index) follow: 1536 and 2048 entries.
+static constexpr int TOPK_LIST0 = TOPK_FAST * 5 + TOPK_GATHER * 2, TOPK_LIST0_CAP = 1536;
+static constexpr int TOPK_LIST1 = TOPK_LIST0 + 2 * TOPK_LIST0_CAP, TOPK_LIST1_CAP = 2048;
+static constexpr int TOPK_LDS_FLOATS = TOPK_LIST1 + 2 * TOPK_LIST1_CAP;  // 64 KiB
 __host__ __device__ __forceinline__ bool topk_compact(int top_k, int V) {
     return top_k > 0 && top_k < V && top_k <= TOPK_FAST;
 }
@@ -393,51 +396,16 @@ __device__ inline void block_sort_desc(unsigned long long* keys, int np2) {
 template <class P, class M>
 __device__ inline int gather_rare(const float* row, int V, const P& take, const M& make, unsigned long long* out,
                                   int cap, AccShared* sh) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    if (tid == 0) sh->n = 0;
+    if (threadIdx.x == 0) sh->n = 0;
     __syncthreads();
-    const bool vec = ((uintptr_t)row & 15) == 0;
-    for (int j0 = 0; j0 < V; j0 += 16 * ACC_THREADS) {
-        float l[16];
-        int jb[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            jb[q] = j0 + 4 * (q * ACC_THREADS + tid);
-            if (vec && jb[q] + 3 < V) {
-                const float4_t v = *(const float4_t*)(row + jb[q]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) l[4 * q + e] = v[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) l[4 * q + e] = jb[q] + e < V ? row[jb[q] + e] : 0.0f;
-            }
+    // each taken element claims a slot with one LDS atomic (taken elements are rare, and the
+    // callers rank the list by unique keys, so the slot order does not matter)
+    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+        if (valid && take(l, j)) {
+            const unsigned slot = atomicAdd(&sh->n, 1u);
+            if (slot < (unsigned)cap) out[slot] = make(l, j);
         }
-        uint32_t mask = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int j = jb[i >> 2] + (i & 3);
-            if (j < V && take(l[i], j)) mask |= 1u << i;
-        }
-        if (__ballot(mask != 0u) == 0ull) continue;  // wave-uniform
-        const int cnt = __popc(mask);
-        int incl = cnt;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int t = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += t;
-        }
-        const int total = __shfl(incl, 63, 64);
-        unsigned base = 0;
-        if (lane == 0) base = atomicAdd(&sh->n, (unsigned)total);
-        base = __builtin_amdgcn_readfirstlane(base);
-        unsigned slot = base + (unsigned)(incl - cnt);
-        while (mask) {
-            const int i = __ffs(mask) - 1;
-            mask &= mask - 1u;
-            if (slot < (unsigned)cap) out[slot] = make(l[i], jb[i >> 2] + (i & 3));
-            slot++;
-        }
-    }
+    });
     __syncthreads();
     const int n = (int)sh->n;
     __syncthreads();
@@ -546,24 +514,29 @@ __device__ __forceinline__ int topk_band(float l, float mx, float rinv) {
     return max(0, min(63, -4 * e - (int)((u >> 21) & 3u) - 1));
 }
 
-// Top-k selection for k <= TOPK_FAST without radix passes: one pass for the finite
-// max / min, one counting the logits of each band in the top quarter of the range, one
-// gathering the narrowest upper set of bands holding at least k logits (at most
-// TOPK_GATHER keys); ranking those keys gives the k-th key, and ranking the k survivors
-// by index puts them in keys[0..k) as topk_survivors leaves them.
+// Top-k selection for k <= TOPK_FAST without radix passes.  Bands: b(l) of topk_band
+// relative to the row's finite max / min, non-decreasing in l; the top quarter of the
+// range is b >= 8.  One pass takes the finite max / min; a second lists (value, index) of
+// every logit above thr, a threshold below which b < 8 is certain (a cheap compare per
+// logit; only the list gets banded), and the largest logit at or below thr.  From the list:
+// a histogram of the top-quarter bands and the narrowest upper set of bands holding at
+// least k logits (at most TOPK_GATHER); ranking those keys gives the k-th key, and
+// ranking the k survivors by index puts them in keys[0..k) as topk_survivors leaves them.
 // Rows with a few logits far above the rest (an MTP head scores the token it was fed far
-// above every other) hold fewer than k logits in the top quarter.  The counting pass also
-// takes the largest logit below the top quarter, and a second counting pass bands the
-// rest of the row below that maximum; the gathered set is then the top-quarter logits
-// plus the narrowest upper set of second-level bands that completes k.  Both sets are
-// upper sets in logit value, so their union holds the k largest keys.
+// above every other) hold fewer than k logits in the top quarter: a third pass lists the
+// logits in the top quarter of the range below those (up to the largest logit outside the
+// top quarter), bands them relative to it, and completes k from its narrowest upper set.
+// Both sets are upper sets in logit value, so their union holds the k largest keys.
 // Returns false (the caller falls back to the radix select) on non-finite logits, a
-// constant row, or when no band set of at most TOPK_GATHER logits holds k.
+// constant row, a range too narrow for the threshold's margin (R <= 0.01 |max|), a list
+// past its capacity, or when no band set of at most TOPK_GATHER logits holds k.
 __device__ inline bool topk_fast_select(const float* row, int V, int k, float* buf, AccShared* sh, uint64_t* kkey) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     unsigned long long* keys = (unsigned long long*)buf;
     unsigned long long* cand = (unsigned long long*)(buf + 5 * TOPK_FAST);
     unsigned long long* tmp = (unsigned long long*)(buf + 3 * TOPK_FAST);  // k <= TOPK_FAST entries
+    unsigned long long* list0 = (unsigned long long*)(buf + TOPK_LIST0);
+    unsigned long long* list1 = (unsigned long long*)(buf + TOPK_LIST1);
     float mx = -INFINITY, mn = INFINITY;
     int nonfin = 0;
     rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
@@ -576,7 +549,6 @@ __device__ inline bool topk_fast_select(const float* row, int V, int k, float* b
             }
         }
     });
-
     mx = wave_max_f32(mx);
     mn = -wave_max_f32(-mn);
     nonfin = __any(nonfin) ? 1 : 0;
@@ -585,30 +557,68 @@ __device__ inline bool topk_fast_select(const float* row, int V, int k, float* b
         sh->red_i[wid] = nonfin;
         sh->red_k[wid] = __float_as_int(mn);
     }
-    if (tid < 64) sh->sel.hist[tid] = 0u;
     __syncthreads();
     for (int w = 0; w < ACC_WAVES; w++) {
         mx = fmaxf(mx, sh->red_f[w]);
         mn = fminf(mn, __int_as_float(sh->red_k[w]));
         nonfin |= sh->red_i[w];
     }
-    const float R = mx - mn;
-    if (nonfin || !(R > 0.0f) || !isfinite(R)) {
-        __syncthreads();
-        return false;
-    }
-    const float rinv = 1.0f / R;
-    float below = -INFINITY;  // largest logit outside the top quarter
-    rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
-        const int b = valid ? topk_band(l, mx, rinv) : 0;
-        if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
-        else if (valid) below = fmaxf(below, l);
-    });
-    below = wave_max_f32(below);
-    if (lane == 0) sh->red_g[wid] = below;
     __syncthreads();
+    // A logit at or below top - 0.2501 range lies in band < 8 (relative to top) whatever the
+    // rounding of (top - l) / range: the 0.0001 range margin exceeds the rounding of top - l
+    // whenever range > 0.01 |top|.  -INFINITY: no such threshold.
+    auto skip_below = [](float top, float range) {
+        return range > 0.01f * fabsf(top) ? top - 0.2501f * range : -INFINITY;
+    };
+    const float R = mx - mn;
+    if (nonfin || !(R > 0.0f) || !isfinite(R)) return false;
+    const float rinv = 1.0f / R, thr = skip_below(mx, R);
+    if (thr == -INFINITY) return false;
+    // (value, index) of every logit with lo < l <= hi into out (cap entries); the largest
+    // logit at or below lo goes to *below_lo (-INFINITY for none); returns the count
+    auto list_pass = [&](float lo, float hi, unsigned long long* out, int cap, float* below_lo) {
+        if (tid == 0) sh->n = 0;
+        __syncthreads();
+        float bl = -INFINITY;
+        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
+            if (valid && l > lo && l <= hi) {
+                const unsigned slot = atomicAdd(&sh->n, 1u);
+                if (slot < (unsigned)cap)
+                    out[slot] = ((unsigned long long)__float_as_uint(l) << 32) | (unsigned long long)(uint32_t)j;
+            } else if (valid && l <= lo) {
+                bl = fmaxf(bl, l);
+            }
+        });
+        bl = wave_max_f32(bl);
+        if (lane == 0) sh->red_g[wid] = bl;
+        __syncthreads();
+        bl = -INFINITY;
+        for (int w = 0; w < ACC_WAVES; w++) bl = fmaxf(bl, sh->red_g[w]);
+        *below_lo = bl;
+        const int n = (int)sh->n;
+        __syncthreads();
+        return n;
+    };
+    auto ent_l = [](unsigned long long e) { return __uint_as_float((uint32_t)(e >> 32)); };
+    auto ent_j = [](unsigned long long e) { return (int)(uint32_t)e; };
+    // histogram of bands >= 8 of the listed logits (relative to top / tinv); returns through
+    // sh->red_g the largest listed logit in a band < 8
+    auto band_hist = [&](const unsigned long long* lst, int n, float top, float tinv) {
+        if (tid < 64) sh->sel.hist[tid] = 0u;
+        __syncthreads();
+        float bl = -INFINITY;
+        for (int i = tid; i < n; i += ACC_THREADS) {
+            const float l = ent_l(lst[i]);
+            const int b = topk_band(l, top, tinv);
+            if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
+            else bl = fmaxf(bl, l);
+        }
+        bl = wave_max_f32(bl);
+        if (lane == 0) sh->red_g[wid] = bl;
+        __syncthreads();
+    };
     // pick: the lowest band of the narrowest upper set holding `need` logits; -1 when the
-    // counted bands hold fewer (top: their total), -2 when that set exceeds `room`
+    // counted bands hold fewer (their total in sel.total), -2 when that set exceeds `room`
     auto pick_band = [&](unsigned need, unsigned room) {
         unsigned acc = 0;
         for (int b = 63; b >= 8; b--) {
@@ -621,51 +631,61 @@ __device__ inline bool topk_fast_select(const float* row, int V, int k, float* b
         sh->sel.digit = -1;
         sh->sel.total = acc;
     };
-    if (tid == 0) {
-        pick_band((unsigned)k, (unsigned)TOPK_GATHER);
-        sh->n = 0;
-    }
+
+    float below_lo;
+    const int n0 = list_pass(thr, INFINITY, list0, TOPK_LIST0_CAP, &below_lo);
+    if (n0 > TOPK_LIST0_CAP) return false;
+    band_hist(list0, n0, mx, rinv);
+    float below = below_lo;  // largest logit outside the top quarter
+    for (int w = 0; w < ACC_WAVES; w++) below = fmaxf(below, sh->red_g[w]);
+    if (tid == 0) pick_band((unsigned)k, (unsigned)TOPK_GATHER);
     __syncthreads();
-    int band = sh->sel.digit;
-    if (band == -2) {
+    const int band = sh->sel.digit;
+    const unsigned top = sh->sel.total;
+    __syncthreads();
+    if (band == -2) return false;
+    int c = 0;
+    if (band >= 8) {
+        // candidates: the listed logits in bands >= band
+        if (tid == 0) sh->n = 0;
         __syncthreads();
-        return false;
-    }
-    // second level: the top quarter holds `top` < k logits; band the rest below its maximum
-    float mx1 = 0.0f, rinv1 = 0.0f;
-    int band1 = 64;
-    if (band == -1) {
-        const unsigned top = sh->sel.total;
-        mx1 = -INFINITY;
-        for (int w = 0; w < ACC_WAVES; w++) mx1 = fmaxf(mx1, sh->red_g[w]);
-        const float R1 = mx1 - mn;
+        for (int i = tid; i < n0; i += ACC_THREADS) {
+            const unsigned long long e = list0[i];
+            if (topk_band(ent_l(e), mx, rinv) >= band) cand[atomicAdd(&sh->n, 1u)] = logit_key(ent_l(e), ent_j(e));
+        }
         __syncthreads();
+        c = (int)sh->n;
+        __syncthreads();
+    } else {
+        // second level below the top quarter: bands relative to its largest logit mx1
+        const float mx1 = below, R1 = mx1 - mn;
         if (!(R1 > 0.0f) || !isfinite(R1)) return false;
-        rinv1 = 1.0f / R1;
-        if (tid < 64) sh->sel.hist[tid] = 0u;
-        __syncthreads();
-        rows_foreach<1>(row, nullptr, V, [&](int j, float l, float, bool valid) {
-            const int b = (valid && topk_band(l, mx, rinv) < 8) ? topk_band(l, mx1, rinv1) : 0;
-            if (b >= 8) atomicAdd(&sh->sel.hist[b], 1u);
-        });
-        __syncthreads();
+        const float rinv1 = 1.0f / R1, thr1 = skip_below(mx1, R1);
+        if (thr1 == -INFINITY) return false;
+        float unused;
+        const int n1 = list_pass(thr1, mx1, list1, TOPK_LIST1_CAP, &unused);
+        if (n1 > TOPK_LIST1_CAP) return false;
+        band_hist(list1, n1, mx1, rinv1);
         if (tid == 0) pick_band((unsigned)k - top, (unsigned)TOPK_GATHER - top);
         __syncthreads();
-        band1 = sh->sel.digit;
-        if (band1 < 0) {
-            __syncthreads();
-            return false;
+        const int band1 = sh->sel.digit;
+        __syncthreads();
+        if (band1 < 0) return false;
+        // candidates: the top quarter (the logits above mx1) and the second-level set
+        if (tid == 0) sh->n = 0;
+        __syncthreads();
+        for (int i = tid; i < n0; i += ACC_THREADS) {
+            const unsigned long long e = list0[i];
+            if (ent_l(e) > mx1) cand[atomicAdd(&sh->n, 1u)] = logit_key(ent_l(e), ent_j(e));
         }
-        band = 8;  // the whole top quarter
+        for (int i = tid; i < n1; i += ACC_THREADS) {
+            const unsigned long long e = list1[i];
+            if (topk_band(ent_l(e), mx1, rinv1) >= band1) cand[atomicAdd(&sh->n, 1u)] = logit_key(ent_l(e), ent_j(e));
+        }
+        __syncthreads();
+        c = (int)sh->n;
+        __syncthreads();
     }
-    const int c = min(gather_rare(
-                          row, V,
-                          [&](float l, int j) {
-                              const int b = topk_band(l, mx, rinv);
-                              return b >= band || (band1 < 64 && b < 8 && topk_band(l, mx1, rinv1) >= band1);
-                          },
-                          [](float l, int j) { return (unsigned long long)logit_key(l, j); }, cand, TOPK_GATHER, sh),
-                      TOPK_GATHER);
     // the k largest candidate keys, by rank; the k-th is the top-k cut
     for (int i = tid; i < c; i += ACC_THREADS) {
         const unsigned long long key = cand[i];

@@ -275,6 +275,26 @@ def test_top_k_rows_with_outlier_logits(ctx, n_out, top_p):
     assert_parity(out, ref, max_flag_frac=0.25)
 
 
+@pytest.mark.parametrize("offset", [300.0, 1.0e4, -2.0e4])
+def test_top_k_rows_far_from_zero(ctx, offset):
+    """Logits offset far from zero with a range small against their magnitude: the band
+    thresholds round at the logits' own ulp, and the selection must still keep exactly
+    the top k (bit-identical draws to the oracle except flagged ones)."""
+    rng = np.random.default_rng(90)
+    B, K, V = 8, 3, 32000
+    tgt = (offset + rng.normal(0, 1.0, (B, K + 1, V))).astype(np.float32)
+    drf = (tgt[:, :K] + rng.normal(0, 0.3, (B, K, V))).astype(np.float32)
+    s = R.sampler(temperature=0.7, top_k=50, top_p=0.9)
+    toks = np.zeros((B, K), np.uint32)
+    for b in range(B):
+        r = R.Rng(50_000 + b)
+        for i in range(K):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    out, ref = run_both(ctx, tgt, drf, toks, 0.7, True, seeds=np.arange(B, dtype=np.uint64) + 29, top_k=50,
+                        top_p=0.9)
+    assert_parity(out, ref, max_flag_frac=0.25)
+
+
 def test_top_k_keeps_lower_index_among_ties(ctx):
     """Stable total_cmp ranking: among equal logits at the top-k boundary the lower
     token ids are kept (sampler.rs:238-245), so the bonus draw can only land on them."""
