@@ -305,10 +305,27 @@ def run_c2(args):
     alg = B * (2 * K + 1) * V * 4
     us = prof["ms"] * 1000.0 / max(prof["launches"], 1)
     acc = out["accept_len"].cpu().numpy()
+    # the same shape with the reference CLI's sampler (infer.rs:72-77: T 0.7, top-k 50, top-p 0.9);
+    # draft tokens from the draft's top-k / top-p set, as the engines propose them
+    s_cli = A.Sampler.top_k_top_p(0.7, top_k=50, top_p=0.9, seed=0)
+    pv, pi = torch.topk(torch.softmax(drf.reshape(-1, V) / 0.7, -1), 50, dim=-1)
+    keep = (torch.cumsum(pv, -1) - pv) < 0.9
+    pick = torch.multinomial(pv * keep, 1, generator=g)
+    toks_cli = torch.gather(pi, 1, pick).reshape(B, K).int()
+    for _ in range(3):
+        m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
+    m.prof_enable(True)
+    for _ in range(n):
+        m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
+    prof_cli = m.prof_get()["accept"]
+    m.prof_enable(False)
+    us_cli = prof_cli["ms"] * 1000.0 / max(prof_cli["launches"], 1)
     m.close()
     r = {"us_per_call": us, "alg_bytes": alg, "gbs": alg / (us * 1e-6) / 1e9, "hbm_frac": alg / (us * 1e-6) / 1e9 /
-         HBM_PEAK_GBS, "launches": prof["launches"], "mean_accept_len": float(acc.mean())}
-    print(f"# C2 sampled acceptance: {us:.2f} us per call, {r['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+         HBM_PEAK_GBS, "launches": prof["launches"], "mean_accept_len": float(acc.mean()),
+         "cli_sampler_us_per_call": us_cli}
+    print(f"# C2 sampled acceptance: {us:.2f} us per call, {r['gbs']:.0f} GB/s; with the CLI sampler "
+          f"(T 0.7, top-k 50, top-p 0.9) {us_cli:.2f} us", file=sys.stderr, flush=True)
     return r
 
 
