@@ -293,18 +293,21 @@ def run_c2(args):
     toks = torch.multinomial(torch.softmax(drf.reshape(-1, V) / 0.8, -1), 1, generator=g).reshape(B, K).int()
     seeds = torch.arange(B, device="cuda", dtype=torch.int64)
     s = A.Sampler.top_k_top_p(0.8, seed=0)
-    out = None
-    for _ in range(3):
-        out = m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
-    m.prof_enable(True)
+    which = getattr(args, "c2_sampler", "both")
     n = args.verify_iters * 5
-    for _ in range(n):
-        m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
-    prof = m.prof_get()["accept"]
-    m.prof_enable(False)
     alg = B * (2 * K + 1) * V * 4
-    us = prof["ms"] * 1000.0 / max(prof["launches"], 1)
-    acc = out["accept_len"].cpu().numpy()
+    us, acc, prof = float("nan"), np.zeros(1), {"launches": 0}
+    if which in ("both", "plain"):
+        out = None
+        for _ in range(3):
+            out = m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
+        m.prof_enable(True)
+        for _ in range(n):
+            m.accept_sample(tgt, drf, toks, s, True, seeds=seeds)
+        prof = m.prof_get()["accept"]
+        m.prof_enable(False)
+        us = prof["ms"] * 1000.0 / max(prof["launches"], 1)
+        acc = out["accept_len"].cpu().numpy()
     # the same shape with the reference CLI's sampler (infer.rs:72-77: T 0.7, top-k 50, top-p 0.9);
     # draft tokens from the draft's top-k / top-p set, as the engines propose them
     s_cli = A.Sampler.top_k_top_p(0.7, top_k=50, top_p=0.9, seed=0)
@@ -312,14 +315,16 @@ def run_c2(args):
     keep = (torch.cumsum(pv, -1) - pv) < 0.9
     pick = torch.multinomial(pv * keep, 1, generator=g)
     toks_cli = torch.gather(pi, 1, pick).reshape(B, K).int()
-    for _ in range(3):
-        m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
-    m.prof_enable(True)
-    for _ in range(n):
-        m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
-    prof_cli = m.prof_get()["accept"]
-    m.prof_enable(False)
-    us_cli = prof_cli["ms"] * 1000.0 / max(prof_cli["launches"], 1)
+    us_cli = float("nan")
+    if which in ("both", "cli"):
+        for _ in range(3):
+            m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
+        m.prof_enable(True)
+        for _ in range(n):
+            m.accept_sample(tgt, drf, toks_cli, s_cli, True, seeds=seeds)
+        prof_cli = m.prof_get()["accept"]
+        m.prof_enable(False)
+        us_cli = prof_cli["ms"] * 1000.0 / max(prof_cli["launches"], 1)
     m.close()
     r = {"us_per_call": us, "alg_bytes": alg, "gbs": alg / (us * 1e-6) / 1e9, "hbm_frac": alg / (us * 1e-6) / 1e9 /
          HBM_PEAK_GBS, "launches": prof["launches"], "mean_accept_len": float(acc.mean()),
@@ -620,6 +625,8 @@ def main():
     ap.add_argument("--workload", choices=["c4", "c5", "c2", "c3", "serve"], default="c4",
                     help="c4: the headline metric (default, with c2 / c3 / serve beside it); c5: the MLA + MoE "
                          "verify step; c2 / c3 / serve: only that measurement (profiling)")
+    ap.add_argument("--c2-sampler", choices=["both", "plain", "cli"], default="both",
+                    help="--workload c2: time the config's T 0.8 sampler, the reference CLI's, or both")
     ap.add_argument("--no-graphs", action="store_true",
                     help="serve workload: launch every forward directly instead of replaying captured graphs")
     ap.add_argument("--calibrate-copy", action="store_true",
