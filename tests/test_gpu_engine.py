@@ -40,6 +40,28 @@ def test_c1_config_greedy_mtp_bit_exact(replay):
     hip.close()
 
 
+def test_greedy_mtp_with_untied_head_and_yarn_rope():
+    """The MTP engine over a model with an untied LM head (model.rs:239-262, shared by the
+    MTP heads) and YaRN RoPE scaling (rope_scaling.rs:62-92): token ids and statistics
+    bit-exact against the oracle engine on the same model (f32, C1 widths, 3 heads)."""
+    kw = dict(vocab_size=4096, hidden_dim=256, ffn_dim=704, n_layers=2, n_heads=8, n_kv_heads=2, max_seq_len=256,
+              num_future_tokens=4)
+    ref, hip = make_pair(seed=3, std=0.05, max_batch=1, max_rows=64, tie_embeddings=False, **kw)
+    rs = dict(method="yarn", factor=4.0, original_max_seq_len=64, beta_fast=16.0, beta_slow=1.0, attn_factor=1.1)
+    ref.set_rope_scaling(rs)
+    hip.set_rope_scaling(A.RopeScaling(**rs))
+    prompt = R.synth_tokens(3, 0xC1, 48, 4096)
+    want, fin, stats, gap = ref.mtp_generate(prompt, 96, 4, R.sampler(greedy=True))
+    assert gap > 1e-5, f"oracle near-tie {gap}: parity would be flagged"
+    out = A.MtpSpeculativeEngine(hip, A.SpeculativeConfig(4)).generate(prompt, 96, A.Sampler.greedy_sampler())
+    assert out.token_ids == list(want)
+    got = out.speculative_stats
+    for k in ("rounds", "draft_tokens_proposed", "draft_tokens_accepted", "target_decode_forwards",
+              "mtp_head_forwards"):
+        assert getattr(got, k) == stats[k], (k, getattr(got, k), stats[k])
+    hip.close()
+
+
 def test_int4_batched_greedy_mtp_matches_oracle_per_round():
     """Four requests in lock-step: each request's committed tokens equal the oracle's
     up to its first near-tie round (top-2 gap below the INT4 logit tolerance); past it
