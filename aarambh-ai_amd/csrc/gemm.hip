@@ -10,11 +10,14 @@
 // layout: per (chunk, group, k-step, lane group) 16 hi entries then 16 lo);
 // INT4 / INT8 codes are exact in fp16, so products keep ~22 bits.
 //
-// Block: 8 waves = 2 (M) x 4 (N).  It covers MC = 2 * CPW row chunks (16 rows
-// each) x NT = 4 * TPW weight tiles (16 rows each) over a contiguous range of
-// 128-column groups (split-K).  Wave (wm, wn) owns CPW chunks x TPW tiles:
-// per group 8 * CPW * TPW MFMAs 16x16x32, with each INT4 weight word
-// dequantised once per wave for CPW chunks.
+// Block: 8 waves = WM (M) x WN = 8 / WM (N), WM = 2 or 1.  It covers MC = WM *
+// CPW row chunks (16 rows each) x NT = WN * TPW weight tiles (16 rows each) over
+// a contiguous range of 128-column groups (split-K).  Wave (wm, wn) owns CPW
+// chunks x TPW tiles: per group 8 * CPW * TPW MFMAs 16x16x32, with each INT4
+// weight word dequantised once per wave for CPW chunks.  At 32 rows and below
+// the 1 x 8 shape with both chunks in every wave dequantises each weight word
+// once for four MFMAs instead of two (the dequantisation is VALU work of the
+// same order as the MFMAs it feeds).
 //
 // Data movement: a ring of NS LDS stages, one 128-column group each, filled by
 // direct HBM/L2 -> LDS loads (buffer_load ... lds, no VGPRs): the activation
@@ -31,35 +34,41 @@
 
 namespace aarh {
 
-static constexpr int GM_WAVES = 8, GM_WM = 2, GM_WN = 4;
+static constexpr int GM_WAVES = 8;
 static constexpr int GM_LDS_BUDGET = 150 * 1024;  // dynamic LDS for the stage ring
 
-template <int FMT, int CPW, int TPW_>
+template <int FMT, int WM, int CPW, int TPW_>
 struct GmCfg {
     typedef FmtTraits<FMT> T;
+    static constexpr int WN = GM_WAVES / WM;                        // N-waves
     static constexpr int TPW = TPW_;                                // weight tiles per wave
-    static constexpr int NT = GM_WN * TPW;                          // weight tiles per block
-    static constexpr int MC = GM_WM * CPW;                          // row chunks per block
+    static constexpr int NT = WN * TPW;                             // weight tiles per block
+    static constexpr int MC = WM * CPW;                             // row chunks per block
     static constexpr int A_BYTES = MC * 8192;                       // hi + lo fragments of one group
     static constexpr int W_BYTES = NT * T::TILE_BYTES;
-    static constexpr int Z_BYTES = FMT == WF_INT4 ? 1024 : 0;      // one 64-lane load of scale/zero words
+    // scale/zero words of the block's tiles: one 64-lane load covers 16 tiles
+    static constexpr int Z_LOADS = FMT == WF_INT4 ? (NT + 15) / 16 : 0;
+    static constexpr int Z_BYTES = Z_LOADS * 1024;
     static constexpr int STAGE = A_BYTES + W_BYTES + Z_BYTES;
     // narrow 32-row blocks keep the ring small enough for two blocks per CU
-    static constexpr int BUDGET = (CPW == 1 && TPW <= 2) ? 76 * 1024 : GM_LDS_BUDGET;
+    static constexpr int BUDGET = (MC == 2 && NT <= 8) ? 76 * 1024 : GM_LDS_BUDGET;
     static constexpr int NS_RAW = BUDGET / STAGE;
     static constexpr int NS = NS_RAW < 2 ? 2 : (NS_RAW > 4 ? 4 : NS_RAW);
     static constexpr int A_PW = MC * 8 / GM_WAVES;                  // 1 KiB activation pieces per wave
     static constexpr int W_PIECES = W_BYTES / 1024;
     static constexpr int W_PW = (W_PIECES + GM_WAVES - 1) / GM_WAVES;  // 1 KiB weight pieces per wave
-    static constexpr int L = A_PW + W_PW + (FMT == WF_INT4 ? 1 : 0);  // loads per wave per stage
+    static constexpr int L = A_PW + W_PW + Z_LOADS;                 // loads per wave per stage
     static_assert(MC * 8 % GM_WAVES == 0, "activation pieces split over waves");
+    static_assert(WM * WN == GM_WAVES, "wave grid");
+    // the epilogue stages each wave's 16 CPW x (16 TPW + 4) f32 tile in the idle ring
+    static_assert(GM_WAVES * 16 * CPW * (16 * TPW + 4) * 4 <= NS * STAGE, "epilogue tile exceeds the ring");
     static_assert(NS * STAGE <= GM_LDS_BUDGET, "stage ring exceeds LDS");
 };
 
-template <int FMT, int EPI, int CPW, int TPW_>
+template <int FMT, int EPI, int WM, int CPW, int TPW_>
 __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, int gps) {
     typedef FmtTraits<FMT> T;
-    typedef GmCfg<FMT, CPW, TPW_> C;
+    typedef GmCfg<FMT, WM, CPW, TPW_> C;
     constexpr int TPW = C::TPW, NT = C::NT, MC = C::MC, NS = C::NS, LW = T::LANE_WORDS;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ float s_inv[MC * 16];
@@ -67,7 +76,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
 
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const int wm = wid / GM_WN, wn = wid % GM_WN;
+    const int wm = wid / C::WN, wn = wid % C::WN;
     const int G = a.K >> 7;
     const int ntiles = a.N >> 4;
     const int NB = (ntiles + NT - 1) / NT;
@@ -150,7 +159,9 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     // ---- stage loads: this wave's pieces of group g into ring slot st ----
     const __amdgpu_buffer_rsrc_t wr = coh_rsrc(a.w), fr = coh_rsrc(a.xf), zr = coh_rsrc(a.sz);
     constexpr int WP = T::TILE_BYTES / 1024;  // 1 KiB pieces per tile
-    const int z_tile = min(nb * NT + (lane >> 2), ntiles - 1);
+    int z_tile[C::Z_LOADS > 0 ? C::Z_LOADS : 1];
+#pragma unroll
+    for (int q = 0; q < C::Z_LOADS; q++) z_tile[q] = min(nb * NT + 16 * q + (lane >> 2), ntiles - 1);
     auto issue_stage = [&](int st, int g) {
         char* base = lds + st * C::STAGE;
 #pragma unroll
@@ -169,8 +180,10 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
             lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * 16 + sub * 1024,
                       (int)(((unsigned)nt * G + g) * T::TILE_BYTES));
         }
-        if (FMT == WF_INT4)
-            lds_dma16(zr, base + C::A_BYTES + C::W_BYTES, (int)(((unsigned)z_tile * G + g) * 64u + (lane & 3) * 16u), 0);
+#pragma unroll
+        for (int q = 0; q < C::Z_LOADS; q++)
+            lds_dma16(zr, base + C::A_BYTES + C::W_BYTES + q * 1024,
+                      (int)(((unsigned)z_tile[q] * G + g) * 64u + (lane & 3) * 16u), 0);
     };
 
     float4_t acc[CPW][TPW];
@@ -592,33 +605,34 @@ static int cu_count() {
     return cus;
 }
 
-template <int FMT, int EPI, int CPW, int TPW>
+template <int FMT, int EPI, int WM, int CPW, int TPW>
 static size_t ring_bytes() {
-    typedef GmCfg<FMT, CPW, TPW> C;
+    typedef GmCfg<FMT, WM, CPW, TPW> C;
     return (size_t)C::NS * C::STAGE;
 }
 
 // Resident blocks per CU of one configuration (dynamic LDS attribute set on first use).
-template <int FMT, int EPI, int CPW, int TPW>
+template <int FMT, int EPI, int WM, int CPW, int TPW>
 static int blocks_per_cu() {
     static int per_cu = 0;
     if (!per_cu) {
-        const size_t lds = ring_bytes<FMT, EPI, CPW, TPW>();
-        if (note_error(hipFuncSetAttribute((const void*)gemm_kernel<FMT, EPI, CPW, TPW>,
+        const size_t lds = ring_bytes<FMT, EPI, WM, CPW, TPW>();
+        if (note_error(hipFuncSetAttribute((const void*)gemm_kernel<FMT, EPI, WM, CPW, TPW>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)))
             return 0;
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemm_kernel<FMT, EPI, CPW, TPW>,
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)gemm_kernel<FMT, EPI, WM, CPW, TPW>,
                                                            GM_WAVES * 64, lds);
         per_cu = std::max(per_cu, 1);
     }
     return per_cu;
 }
 
-// Launch with CPW row chunks and TPW weight tiles per wave and S k-splits.
-template <int FMT, int EPI, int CPW, int TPW>
+// Launch with a WM x (8 / WM) wave grid, CPW row chunks and TPW weight tiles per
+// wave and S k-splits.
+template <int FMT, int EPI, int WM, int CPW, int TPW>
 static int launch_cfg(const GemvArgs& a, int S, hipStream_t stream) {
-    typedef GmCfg<FMT, CPW, TPW> C;
-    if (!blocks_per_cu<FMT, EPI, CPW, TPW>()) return 4;
+    typedef GmCfg<FMT, WM, CPW, TPW> C;
+    if (!blocks_per_cu<FMT, EPI, WM, CPW, TPW>()) return 4;
     const int G = a.K >> 7;
     const int NB = (a.N / 16 + C::NT - 1) / C::NT;
     const int MB = ((a.M + 15) / 16 + C::MC - 1) / C::MC;
@@ -627,99 +641,119 @@ static int launch_cfg(const GemvArgs& a, int S, hipStream_t stream) {
     const int gps = (G + S - 1) / S;
     S = (G + gps - 1) / gps;  // every split non-empty
     if (S > 1 && (!a.gcnt || NB * MB > 8192)) return 2;  // counters: 8192 per context
-    const size_t lds = ring_bytes<FMT, EPI, CPW, TPW>();
+    const size_t lds = ring_bytes<FMT, EPI, WM, CPW, TPW>();
     (void)hipGetLastError();
-    launch_timed(gemm_kernel<FMT, EPI, CPW, TPW>, dim3(NB * MB * S), dim3(GM_WAVES * 64), (uint32_t)lds, stream, a, S,
-                 gps);
+    launch_timed(gemm_kernel<FMT, EPI, WM, CPW, TPW>, dim3(NB * MB * S), dim3(GM_WAVES * 64), (uint32_t)lds, stream,
+                 a, S, gps);
     return note_error(hipGetLastError()) ? 4 : 0;
 }
 
-// Launch plan: row chunks per wave (CPW), weight tiles per wave (TPW) and k-splits (S).
+// Launch plan: block shape (wm = 2: 2 x 4 waves with cpw = 1 or 2; wm = 1: 1 x 8
+// waves with cpw = 2), weight tiles per wave (tpw) and k-splits (S).
 struct GmPlan {
-    int cpw, tpw, S;
+    int wm, cpw, tpw, S;
 };
 
 // Measured best plans for the projection shapes of the 7B-class decoder
 // (d_model 4096, 32 x 128 query heads, 8 kv heads, ffn 11008, INT4 g128; bf16
 // LM head over a 32000 vocabulary) at 32 / 64 / 128 rows (replay and MTP
-// batches; verify batches of 16 and 32 sequences x 4 rows).
+// batches; verify batches of 16 and 32 sequences x 4 rows).  At 128 rows the
+// 1 x 8 wave shape (four 32-row blocks per weight tile) took the batch-32 verify
+// step from 6.59 to 6.41 ms; at 32 rows it measured slower in the full model
+// (8.6 MB of weights per layer stream from HBM) than the 2 x 4 plans.
 struct GmTuned {
-    int fmt, N, K, plan[3][3];
+    int fmt, N, K;
+    GmPlan plan[3];
 };
 static constexpr GmTuned GM_TUNED[] = {
-    {WF_INT4, 6144, 4096, {{1, 2, 4}, {2, 2, 4}, {2, 2, 2}}},
-    {WF_INT4, 4096, 4096, {{1, 1, 4}, {2, 1, 4}, {2, 1, 2}}},
-    {WF_INT4, 22016, 4096, {{1, 3, 2}, {2, 3, 2}, {2, 3, 1}}},
-    {WF_INT4, 4096, 11008, {{1, 2, 8}, {2, 1, 4}, {2, 2, 4}}},
-    {WF_BF16, 32000, 4096, {{1, 2, 1}, {2, 2, 1}, {2, 2, 1}}},
+    {WF_INT4, 6144, 4096, {{2, 1, 2, 4}, {2, 2, 2, 4}, {1, 2, 1, 1}}},
+    {WF_INT4, 4096, 4096, {{2, 1, 1, 4}, {2, 2, 1, 4}, {1, 2, 1, 2}}},
+    {WF_INT4, 22016, 4096, {{2, 1, 3, 2}, {2, 2, 3, 2}, {1, 2, 3, 1}}},
+    {WF_INT4, 4096, 11008, {{2, 1, 2, 8}, {2, 2, 1, 4}, {1, 2, 1, 2}}},
+    {WF_BF16, 32000, 4096, {{2, 1, 2, 1}, {2, 2, 2, 1}, {2, 2, 2, 1}}},
 };
 
-template <int FMT, int EPI, int CPW>
+// Widest weight-tile count per wave whose stage ring fits the LDS budget.
+template <int FMT, int WM>
+static constexpr int max_tpw() {
+    return FMT == WF_BF16 ? (WM == 1 ? 1 : 2) : (WM == 1 && FMT == WF_INT8 ? 3 : 4);
+}
+
+template <int FMT, int EPI, int WM, int CPW>
 static int per_cu_of(int tpw) {
-    constexpr int T4 = FMT == WF_BF16 ? 2 : 4, T3 = FMT == WF_BF16 ? 2 : 3;
-    return tpw == T4 ? blocks_per_cu<FMT, EPI, CPW, T4>() : tpw == 3 ? blocks_per_cu<FMT, EPI, CPW, T3>()
-         : tpw == 2 ? blocks_per_cu<FMT, EPI, CPW, 2>() : blocks_per_cu<FMT, EPI, CPW, 1>();
+    constexpr int TM = max_tpw<FMT, WM>();
+    if constexpr (TM >= 4)
+        if (tpw >= 4) return blocks_per_cu<FMT, EPI, WM, CPW, 4>();
+    if constexpr (TM >= 3)
+        if (tpw >= 3) return blocks_per_cu<FMT, EPI, WM, CPW, 3>();
+    if constexpr (TM >= 2)
+        if (tpw >= 2) return blocks_per_cu<FMT, EPI, WM, CPW, 2>();
+    return blocks_per_cu<FMT, EPI, WM, CPW, 1>();
 }
 
 template <int FMT, int EPI>
-static int plan_capacity(int cpw, int tpw) {
-    const int per_cu = cpw == 2 ? per_cu_of<FMT, EPI, 2>(tpw) : per_cu_of<FMT, EPI, 1>(tpw);
+static int plan_capacity(int wm, int cpw, int tpw) {
+    const int per_cu = wm == 1 ? per_cu_of<FMT, EPI, 1, 2>(tpw)
+                     : cpw == 2 ? per_cu_of<FMT, EPI, 2, 2>(tpw) : per_cu_of<FMT, EPI, 2, 1>(tpw);
     return cu_count() * std::max(per_cu, 1);
 }
 
-// 64-row blocks above 32 rows, 32-row blocks otherwise.  Among the tile widths
-// (4, 3, 2, 1 weight tiles per wave; 2, 1 for BF16) and splits whose blocks fit one dispatch round, the plan fills the round best
-// (fill counted up to 2/3 of a one-block-per-CU round, 1/2 of a two-block one:
-// beyond that wider blocks measured faster than more of them), then uses the
-// fewest splits, then the widest tiles.
+// 64-row blocks above 32 rows, 32-row blocks otherwise (both block shapes).  Among
+// the tile widths (4, 3, 2, 1 weight tiles per wave; 2, 1 for BF16) and splits whose
+// blocks fit one dispatch round, the plan fills the round best (fill counted up to
+// 2/3 of a one-block-per-CU round, 1/2 of a two-block one: beyond that wider blocks
+// measured faster than more of them), then uses the fewest splits, then the widest
+// tiles, then the 2 x 4 shape.
 template <int FMT, int EPI>
 static GmPlan plan_gemm(const GemvArgs& a) {
-    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
     const int G = a.K >> 7, ntiles = a.N / 16, chunks = (a.M + 15) / 16;
     for (const GmTuned& t : GM_TUNED)
-        if (t.fmt == FMT && t.N == a.N && t.K == a.K) {
-            const int* p = t.plan[a.M <= 32 ? 0 : a.M <= 64 ? 1 : 2];
-            return {p[0], p[1], p[2]};
-        }
-    const int cpw = a.M > 32 ? 2 : 1;
-    GmPlan best{cpw, 1, 1};
+        if (t.fmt == FMT && t.N == a.N && t.K == a.K) return t.plan[a.M <= 32 ? 0 : a.M <= 64 ? 1 : 2];
+    GmPlan best{2, a.M > 32 ? 2 : 1, 1, 1};
     double bkey0 = -1.0;
     int bkey1 = 0, bkey2 = 0;
-    for (int tpw = T4; tpw >= 1; tpw--) {
-        const int cap = plan_capacity<FMT, EPI>(cpw, tpw);
-        const int units = ((ntiles + GM_WN * tpw - 1) / (GM_WN * tpw)) * ((chunks + GM_WM * cpw - 1) / (GM_WM * cpw));
-        for (int S = 1; S <= std::min(8, G); S++) {
-            const int gps = (G + S - 1) / S;
-            if ((G + gps - 1) / gps != S) continue;  // another S gives the same splits
-            const long long blocks = (long long)units * S;
-            if (blocks > cap) break;
-            const double fill = std::min((double)blocks / cap, cap > cu_count() ? 0.5 : 0.66);
-            const double key0 = std::floor(fill * 100.0 + 1e-9) / 100.0;
-            if (key0 > bkey0 || (key0 == bkey0 && (-S > bkey1 || (-S == bkey1 && tpw > bkey2)))) {
-                bkey0 = key0;
-                bkey1 = -S;
-                bkey2 = tpw;
-                best = {cpw, tpw, S};
+    for (int wm = 2; wm >= (a.M > 32 ? 2 : 1); wm--) {
+        const int cpw = wm == 1 || a.M > 32 ? 2 : 1, wn = GM_WAVES / wm;
+        for (int tpw = wm == 1 ? max_tpw<FMT, 1>() : max_tpw<FMT, 2>(); tpw >= 1; tpw--) {
+            const int cap = plan_capacity<FMT, EPI>(wm, cpw, tpw);
+            const int units = ((ntiles + wn * tpw - 1) / (wn * tpw)) * ((chunks + wm * cpw - 1) / (wm * cpw));
+            for (int S = 1; S <= std::min(8, G); S++) {
+                const int gps = (G + S - 1) / S;
+                if ((G + gps - 1) / gps != S) continue;  // another S gives the same splits
+                const long long blocks = (long long)units * S;
+                if (blocks > cap) break;
+                const double fill = std::min((double)blocks / cap, cap > cu_count() ? 0.5 : 0.66);
+                const double key0 = std::floor(fill * 100.0 + 1e-9) / 100.0;
+                const int key2 = wn * tpw;
+                if (key0 > bkey0 || (key0 == bkey0 && (-S > bkey1 || (-S == bkey1 && key2 > bkey2)))) {
+                    bkey0 = key0;
+                    bkey1 = -S;
+                    bkey2 = key2;
+                    best = {wm, cpw, tpw, S};
+                }
             }
         }
     }
     return best;
 }
 
+template <int FMT, int EPI, int WM, int CPW>
+static int launch_tpw(const GemvArgs& a, int tpw, int S, hipStream_t stream) {
+    constexpr int TM = max_tpw<FMT, WM>();
+    if constexpr (TM >= 4)
+        if (tpw >= 4) return launch_cfg<FMT, EPI, WM, CPW, 4>(a, S, stream);
+    if constexpr (TM >= 3)
+        if (tpw >= 3) return launch_cfg<FMT, EPI, WM, CPW, 3>(a, S, stream);
+    if constexpr (TM >= 2)
+        if (tpw >= 2) return launch_cfg<FMT, EPI, WM, CPW, 2>(a, S, stream);
+    return launch_cfg<FMT, EPI, WM, CPW, 1>(a, S, stream);
+}
+
 template <int FMT, int EPI>
 static int launch_plan(const GemvArgs& a, const GmPlan& p, hipStream_t stream) {
-    constexpr int T4 = FMT == WF_BF16 ? 2 : 4;
-    if constexpr (FMT != WF_BF16)
-        if (p.tpw == 3) return p.cpw == 2 ? launch_cfg<FMT, EPI, 2, 3>(a, p.S, stream)
-                                          : launch_cfg<FMT, EPI, 1, 3>(a, p.S, stream);
-    if (p.cpw == 2) {
-        if (p.tpw == T4) return launch_cfg<FMT, EPI, 2, T4>(a, p.S, stream);
-        if (p.tpw == 2) return launch_cfg<FMT, EPI, 2, 2>(a, p.S, stream);
-        return launch_cfg<FMT, EPI, 2, 1>(a, p.S, stream);
-    }
-    if (p.tpw == T4) return launch_cfg<FMT, EPI, 1, T4>(a, p.S, stream);
-    if (p.tpw == 2) return launch_cfg<FMT, EPI, 1, 2>(a, p.S, stream);
-    return launch_cfg<FMT, EPI, 1, 1>(a, p.S, stream);
+    if (p.wm == 1) return launch_tpw<FMT, EPI, 1, 2>(a, p.tpw, p.S, stream);
+    if (p.cpw == 2) return launch_tpw<FMT, EPI, 2, 2>(a, p.tpw, p.S, stream);
+    return launch_tpw<FMT, EPI, 2, 1>(a, p.tpw, p.S, stream);
 }
 
 template <int FMT, int EPI>
