@@ -85,7 +85,8 @@ class _LatCfg(C.Structure):
                [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
                [(n, C.c_int32) for n in ("latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
                                           "expert_dim", "n_shared", "expert_format", "attn_format",
-                                          "lm_head_format", "kv_format", "max_batch", "max_rows")]
+                                          "lm_head_format", "kv_format", "max_batch", "max_rows",
+                                          "untied_lm_head")]
 
 
 class _Sampler(C.Structure):
@@ -1043,16 +1044,19 @@ class LatConfig:
     kv_format: int = KV_F16
     rope_theta: float = 10000.0
     norm_eps: float = 1e-5
+    tie_embeddings: bool = True  # False: an lm_head.weight of its own (LmHead::untied_with_qat)
 
     @classmethod
     def from_gguf(cls, path, **overrides):
         """Latent shape from a GGUF v1 file's config (aarh_lat_gguf_config: MlaConfig::resolve,
-        MoE fine experts, the reference's config checks); formats from `overrides`."""
+        MoE fine experts, tie_embeddings, the reference's config checks); formats from
+        `overrides`."""
         c = _LatCfg()
         _host_check(lib().aarh_lat_gguf_config(os.fsencode(path), C.byref(c)))
         kw = {f: getattr(c, f) for f in ("vocab_size", "hidden_dim", "n_layers", "n_heads", "max_seq_len",
                                          "latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
                                          "expert_dim", "n_shared", "rope_theta", "norm_eps")}
+        kw["tie_embeddings"] = not c.untied_lm_head
         kw.update(overrides)
         return cls(**kw)
 
@@ -1065,7 +1069,7 @@ class HipLatModel:
         c = _LatCfg(cfg.vocab_size, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.max_seq_len, cfg.rope_theta,
                     cfg.norm_eps, cfg.latent_dim, cfg.rope_dim, cfg.nope_dim, cfg.v_dim, cfg.n_experts, cfg.top_k,
                     cfg.expert_dim, cfg.n_shared, cfg.expert_format, cfg.attn_format, cfg.lm_head_format,
-                    cfg.kv_format, max_batch, max_rows)
+                    cfg.kv_format, max_batch, max_rows, 0 if cfg.tie_embeddings else 1)
         h = _P()
         st = lib().aarh_lat_create(device, C.byref(c), C.byref(h))
         self.h = h

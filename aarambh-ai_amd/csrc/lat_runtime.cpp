@@ -44,7 +44,7 @@ struct LatLayer {
     _Float16 *upk_hi = nullptr, *upk_lo = nullptr, *upv_hi = nullptr, *upv_lo = nullptr;
 };
 
-enum LPart { L_EMBED, L_NORM, L_QP, L_KVA, L_KRP, L_UPK, L_UPV, L_OP, L_ROUTER, L_GATE, L_UP, L_DOWN };
+enum LPart { L_EMBED, L_NORM, L_QP, L_KVA, L_KRP, L_UPK, L_UPV, L_OP, L_ROUTER, L_GATE, L_UP, L_DOWN, L_LMHEAD };
 
 struct LSlot {
     std::string name;
@@ -511,6 +511,8 @@ void build_slots(Ctx* c) {
         }
     }
     add("final_norm.weight", 1, H, AARH_T_NORM, L_NORM, -1, -1, &c->final_norm);
+    // LmHead::untied_with_qat (model.rs:239-248): its own [vocab, hidden] weight after final_norm
+    if (c->cfg.untied_lm_head) add("lm_head.weight", c->V, H, AARH_T_EMBED, L_LMHEAD, -1, -1, nullptr);
 }
 
 int ensure_staging(Ctx* c, size_t elems) {
@@ -564,6 +566,16 @@ int place_staging(Ctx* c, int id) {
             HIPCHK(c, hipMemcpyAsync(c->embed, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
         } else {
             KCHK(c, launch_to_bf16(c->staging, (uint16_t*)c->embed, n, c->stream));
+            if (!c->cfg.untied_lm_head)
+                KCHK(c, launch_quantise_tiled(c->staging, c->V, c->H, WF_BF16, c->lm.w, nullptr, nullptr, 0, c->V, 0,
+                                              c->stream));
+        }
+        return 0;
+    }
+    if (s.part == L_LMHEAD) {
+        if (c->embed_fmt == WF_F32) {
+            HIPCHK(c, hipMemcpyAsync(c->lm.w, c->staging, n * 4, hipMemcpyDeviceToDevice, c->stream));
+        } else {
             KCHK(c, launch_quantise_tiled(c->staging, c->V, c->H, WF_BF16, c->lm.w, nullptr, nullptr, 0, c->V, 0,
                                           c->stream));
         }
@@ -755,7 +767,8 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
         return fail(c, AARH_ERR_UNSUPPORTED, "at most 64 routed and 72 total experts");
     if (c->H / 128 > 16 || c->D / 128 > 16) return fail(c, AARH_ERR_UNSUPPORTED, "hidden / expert width above 2048");
     if (g.expert_format < AARH_W_BF16 || g.expert_format > AARH_W_INT4_G128 || g.attn_format < 0 ||
-        g.attn_format > AARH_W_INT4_G128 || (g.lm_head_format != 0 && g.lm_head_format != 1))
+        g.attn_format > AARH_W_INT4_G128 || (g.lm_head_format != 0 && g.lm_head_format != 1) ||
+        (g.untied_lm_head != 0 && g.untied_lm_head != 1))
         return fail(c, AARH_ERR_CONFIG, "unknown or unsupported weight format (experts: bf16, int8, int4)");
     if (g.kv_format != AARH_KV_F16) return fail(c, AARH_ERR_UNSUPPORTED, "the latent cache is fp16 (AARH_KV_F16)");
     if (g.max_rows > 256) return fail(c, AARH_ERR_UNSUPPORTED, "max_rows must be <= 256");
@@ -774,7 +787,12 @@ int aarh_lat_create(int device, const aarh_lat_config* cfg, aarh_lat_ctx** out) 
         c->lm.fmt = WF_F32;
         c->lm.N = c->V;
         c->lm.K = c->H;
-        c->lm.w = (uint8_t*)c->embed;
+        if (!g.untied_lm_head) {
+            c->lm.w = (uint8_t*)c->embed;  // row-major f32 weights are shared
+        } else {
+            if (dalloc(c, &c->lm.w, weight_bytes(WF_F32, c->V, c->H))) return AARH_ERR_DEVICE;
+            HIPCHK(c, hipMemset(c->lm.w, 0, weight_bytes(WF_F32, c->V, c->H)));
+        }
     } else if ((r = alloc_tensor(c, c->lm, WF_BF16, c->V, c->H))) {
         return r;
     }

@@ -689,7 +689,8 @@ bool opt_u32(const JVal* obj, const char* key, int64_t def, int64_t* out) {
 // MlaConfig::resolve / validate (:558-612), RopeScalingConfig::validate (:52-96), and
 // dsa_config (DsaConfig::validate :239-258, then "does not select any sparse attention
 // layer", since no layer of an all-MLA schedule is full attention).  The latent context runs
-// MLA and MoE in every layer with a tied LM head: other layer mixes are UNSUPPORTED.  mtp
+// MLA and MoE in every layer (other layer mixes are UNSUPPORTED), with a tied or untied LM
+// head as tie_embeddings says.  mtp
 // heads, if configured, are not part of the latent context and are ignored (as are qat,
 // training-only, model.rs:82-88).  Formats and sizing fields are left as the caller set them.
 int lat_config_from_json(const JVal& meta, aarh_lat_config* out, std::string& err) {
@@ -881,10 +882,7 @@ int lat_config_from_json(const JVal& meta, aarh_lat_config* out, std::string& er
         err = unsupported;
         return AARH_ERR_UNSUPPORTED;
     }
-    if (!tie->b) {
-        err = "the latent context's LM head is tied to the embedding; the checkpoint has tie_embeddings false";
-        return AARH_ERR_UNSUPPORTED;
-    }
+    out->untied_lm_head = tie->b ? 0 : 1;  // LmHead::untied_with_qat (model.rs:239-248)
     out->vocab_size = (int32_t)vocab;
     out->hidden_dim = (int32_t)hidden;
     out->n_layers = (int32_t)layers;
@@ -926,6 +924,11 @@ int check_lat_gguf_config(aarh_lat_ctx* c, const JVal& meta) {
                                                     " does not match the context's " + std::to_string(x.ctx));
     if (got.rope_theta != want.rope_theta || got.norm_eps != want.norm_eps)
         return fail_ctx(c, AARH_ERR_CONFIG, "checkpoint rope_theta / norm_eps do not match the context's configuration");
+    if (got.untied_lm_head != want.untied_lm_head)
+        return fail_ctx(c, AARH_ERR_CONFIG, std::string("checkpoint tie_embeddings ") +
+                                                (got.untied_lm_head ? "false" : "true") +
+                                                " does not match the context's LM head (" +
+                                                (want.untied_lm_head ? "untied" : "tied") + ")");
     return 0;
 }
 

@@ -371,17 +371,21 @@ typedef struct {
     int32_t n_experts, top_k, expert_dim, n_shared;
     int32_t expert_format;  /* AARH_W_BF16 / INT8_ROW / INT4_G128: routed + shared experts */
     int32_t attn_format;    /* AARH_W_*: MLA projections and the router */
-    int32_t lm_head_format; /* AARH_W_F32 or AARH_W_BF16 (tied embedding) */
+    int32_t lm_head_format; /* AARH_W_F32 or AARH_W_BF16: the LM head (and the embedding) */
     int32_t kv_format;      /* AARH_KV_F16 (the latent cache is fp16) */
     int32_t max_batch;      /* cache sequence slots */
     int32_t max_rows;       /* max rows (sequences x tokens) per forward, <= 256 */
+    int32_t untied_lm_head; /* 0: the LM head reads the embedding (tie_embeddings); 1: its own
+                               lm_head.weight [vocab][hidden] after final_norm
+                               (LmHead::untied_with_qat, model.rs:239-248) */
 } aarh_lat_config;
 
 /* Context + weights (checkpoint names and order of the latent decoder, as
    AarambhModel::named_tensors writes them, model.rs:1053-1054, mla.rs:383-393,
    model.rs:944-1000: embedding, per layer blocks.{l}.norm1, blocks.{l}.mla.{q_proj,
    kv_a_proj, kv_a_norm, up_k, up_v, k_rope_proj, o_proj}, norm2, ffn.router,
-   ffn.experts.{e}.{w_gate,w_up,w_down}, ffn.shared_experts.{s}.{...}, then final_norm). */
+   ffn.experts.{e}.{w_gate,w_up,w_down}, ffn.shared_experts.{s}.{...}, then final_norm, then
+   lm_head when untied_lm_head). */
 int aarh_lat_create(int device, const aarh_lat_config *cfg, aarh_lat_ctx **out);
 void aarh_lat_destroy(aarh_lat_ctx *ctx);
 const char *aarh_lat_last_error(const aarh_lat_ctx *ctx);
@@ -399,8 +403,8 @@ int aarh_lat_get_config(const aarh_lat_ctx *ctx, aarh_lat_config *out);
    with its MLA and Gated DeltaNet settings, RopeScalingConfig, dsa_config; CONFIG with the
    reference's message), then must describe what a latent context holds -- MLA in every
    layer (attention_schedule.mla_layers = 0..n_layers), MoE in every layer
-   (moe.every_n_layers = 1) and a tied LM head (UNSUPPORTED otherwise) -- and match the
-   context's shape (CONFIG).  rope_scaling is validated but changes nothing, since MLA keeps
+   (moe.every_n_layers = 1), UNSUPPORTED otherwise -- and match the context's shape and
+   its untied_lm_head (tie_embeddings false: lm_head.weight is read; CONFIG otherwise).  rope_scaling is validated but changes nothing, since MLA keeps
    an unscaled RoPE cache (model.rs:1107-1116); mtp heads are not part of the latent
    context and are not read.  Every context tensor must be present with its shape. */
 int aarh_lat_load_gguf(aarh_lat_ctx *ctx, const char *path, int32_t *out_loaded);
@@ -409,7 +413,7 @@ int aarh_lat_load_safetensors(aarh_lat_ctx *ctx, const char *path, int32_t *out_
    hidden_dim, n_layers, n_heads = resolved MLA heads, max_seq_len, rope_theta, norm_eps,
    latent/rope/nope/v widths from MlaConfig::resolve, n_experts = num_experts x
    fine_grained_factor, top_k, expert_dim = expert_ffn_dim / fine_grained_factor,
-   n_shared = num_shared_experts); same checks and errors as aarh_lat_load_gguf's config
+   n_shared = num_shared_experts, untied_lm_head = !tie_embeddings); same checks and errors as aarh_lat_load_gguf's config
    step, message in aarh_host_last_error.  Formats and sizing are left to the caller. */
 int aarh_lat_gguf_config(const char *path, aarh_lat_config *out);
 /* A PackedInt4Tensor (quant/src/types.rs:79-90) into an INT4 g128 tensor of the latent

@@ -1941,7 +1941,7 @@ ref_lat *ref_lat_create(const ref_lat_config *c) {
     ref_lat *m = (ref_lat *)calloc(1, sizeof(ref_lat));
     m->cfg = *c;
     m->per_layer = X_FIXED + 3 * (c->n_experts + c->n_shared);
-    m->n_tensors = 2 + c->n_layers * m->per_layer;
+    m->n_tensors = 2 + c->n_layers * m->per_layer + (c->untied_lm_head ? 1 : 0);
     m->t = (ref_tensor *)calloc((size_t)m->n_tensors, sizeof(ref_tensor));
     int64_t H = c->hidden_dim, h = c->n_heads, D = c->expert_dim;
     char nm[96];
@@ -1973,6 +1973,8 @@ ref_lat *ref_lat_create(const ref_lat_config *c) {
         }
     }
     set_info(&m->t[lat_final_id(m)], "final_norm.weight", 1, H, REF_T_NORM);
+    /* LmHead::untied_with_qat (model.rs:239-248): a [vocab, hidden] head of its own */
+    if (c->untied_lm_head) set_info(&m->t[lat_final_id(m) + 1], "lm_head.weight", c->vocab_size, H, REF_T_EMBED);
     for (int i = 0; i < m->n_tensors; i++) {
         ref_tensor *t = &m->t[i];
         t->data = (float *)calloc((size_t)(t->rows * t->cols), sizeof(float));
@@ -2020,7 +2022,7 @@ int ref_lat_tensor_info(const ref_lat *m, int id, char *name, int name_cap, int6
 }
 
 /* Storage format of a tensor: experts in expert_format, MLA projections and the
-   router in attn_format, the tied embedding per lm_head_format. */
+   router in attn_format, the embedding and an untied head per lm_head_format. */
 static int lat_format(const ref_lat *m, int id) {
     const ref_tensor *t = &m->t[id];
     if (t->kind == REF_T_EMBED) return m->cfg.lm_head_format == 1 ? REF_W_BF16 : REF_W_F32;
@@ -2307,7 +2309,7 @@ int ref_lat_forward(const ref_lat *m, ref_lat_kv *kv, const uint32_t *ids, int S
     float *hn = (float *)malloc(sizeof(float) * (size_t)(S * H));
     rms_norm(x, S, H, m->t[lat_final_id(m)].data, c->norm_eps, hn);
     if (hidden) memcpy(hidden, hn, sizeof(float) * (size_t)(S * H));
-    if (logits) linear(hn, S, H, emb, V, logits, nt);
+    if (logits) linear(hn, S, H, c->untied_lm_head ? m->t[lat_final_id(m) + 1].data : emb, V, logits, nt);
     free(hn);
     free(x);
     return REF_OK;

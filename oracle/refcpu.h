@@ -191,6 +191,7 @@ typedef struct {
     int32_t attn_format;                             /* MLA projections and the router */
     int32_t lm_head_format;                          /* 0 f32, 1 bf16 */
     int32_t kv_format;                               /* latent cache: REF_KV_F32 or REF_KV_F16 */
+    int32_t untied_lm_head;                          /* 1: lm_head.weight after final_norm (model.rs:239-248) */
 } ref_lat_config;
 
 typedef struct ref_lat ref_lat;

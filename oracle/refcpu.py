@@ -59,7 +59,7 @@ class RefLatConfig(C.Structure):
                [("rope_theta", C.c_float), ("norm_eps", C.c_float)] + \
                [(n, C.c_int32) for n in ("latent_dim", "rope_dim", "nope_dim", "v_dim", "n_experts", "top_k",
                                           "expert_dim", "n_shared", "expert_format", "attn_format",
-                                          "lm_head_format", "kv_format")]
+                                          "lm_head_format", "kv_format", "untied_lm_head")]
 
 
 class RefSpecStats(C.Structure):
@@ -585,10 +585,10 @@ class KvCache:
 # ---------------- latent-attention MoE decoder (benchmark config 5) ----------------
 def make_lat_config(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, latent_dim, rope_dim, nope_dim, v_dim,
                     n_experts, top_k, expert_dim, n_shared, expert_format=W_F32, attn_format=W_F32,
-                    lm_head_format=0, kv_format=KV_F32, rope_theta=10000.0, norm_eps=1e-5):
+                    lm_head_format=0, kv_format=KV_F32, rope_theta=10000.0, norm_eps=1e-5, untied_lm_head=0):
     return RefLatConfig(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, rope_theta, norm_eps, latent_dim,
                         rope_dim, nope_dim, v_dim, n_experts, top_k, expert_dim, n_shared, expert_format,
-                        attn_format, lm_head_format, kv_format)
+                        attn_format, lm_head_format, kv_format, untied_lm_head)
 
 
 def topk_gating(logits, k):

@@ -176,7 +176,7 @@ def model_config_json(vocab_size, hidden_dim, ffn_dim, n_layers, n_heads, n_kv_h
 
 def lat_model_config_json(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len, latent_dim, rope_dim, nope_dim,
                           v_dim, n_experts, top_k, expert_dim, n_shared, rope_theta=10000.0, norm_eps=1e-5,
-                          fine_grained_factor=1, mla_heads=None, **_formats):
+                          fine_grained_factor=1, mla_heads=None, tie_embeddings=True, **_formats):
     """ModelConfig of an MLA + MoE decoder (config.rs:732-776 with MoeConfig :99-130,
     HybridAttentionSchedule :626-654 listing every layer in mla_layers, MlaConfig :529-556)
     as serde_json writes it.  n_heads is the transformer's head count and, unless mla_heads
@@ -197,7 +197,7 @@ def lat_model_config_json(vocab_size, hidden_dim, n_layers, n_heads, max_seq_len
             "mla": {"latent_dim": latent_dim, "nope_head_dim": nope_dim, "rope_head_dim": rope_dim,
                     "n_heads": n_heads if mla_heads is None else mla_heads, "value_head_dim": v_dim}},
         "norm_eps": norm_eps,
-        "tie_embeddings": True,
+        "tie_embeddings": tie_embeddings,
     }
 
 

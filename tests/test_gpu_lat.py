@@ -322,3 +322,62 @@ def test_lat_checkpoint_into_context(tmp_path, kind):
             hip.load_gguf(p3)
     hip.close()
     ref.close()
+
+
+def test_lat_untied_head_checkpoint(tmp_path):
+    """tie_embeddings false (LmHead::untied_with_qat, model.rs:239-248): the latent context
+    holds lm_head.weight after final_norm and reads it from a GGUF checkpoint.  Logits equal
+    the oracle's, and equal the final normed hidden state times the stored head (not the
+    embedding); a tied context rejects the file."""
+    import refgguf as G
+    kw = small_kw()
+    fmts = {k: kw[k] for k in ("expert_format", "attn_format", "lm_head_format", "kv_format")}
+    ref = R.LatModel(R.make_lat_config(**kw, untied_lm_head=1))
+    names = [t[0] for t in ref.tensors()]
+    assert names[-2:] == ["final_norm.weight", "lm_head.weight"]
+    vals = lat_checkpoint(ref, 37)
+    path = str(tmp_path / "untied.gguf")
+    G.save_gguf(path, G.lat_model_config_json(**kw, tie_embeddings=False), "Q80", vals)
+    cfg = A.LatConfig.from_gguf(path, **fmts)
+    assert cfg.tie_embeddings is False
+    hip = A.HipLatModel(cfg, max_batch=2, max_rows=64)
+    assert [t[0] for t in hip.tensors()] == names
+    assert hip.load_gguf(path) == len(names)
+    _, dec = G.load_gguf_tensors(path)
+    for i, name in enumerate(names):
+        ref.set(i, dec[name])
+    B, P = 2, 24
+    ids = R.synth_tokens(33, 1, B * P, kw["vocab_size"]).reshape(B, P)
+    kvs = [ref.kv(128) for _ in range(B)]
+    gl, gh = hip.forward_with_cache_output(ids, [0] * B)
+    assert compare(gl, gh, [kvs[b].forward(ids[b], 0) for b in range(B)], hip.router_gaps(), P) >= 1
+    head, emb = ref.get(len(names) - 1), ref.get(0)  # stored (bf16-rounded) values
+    for b in range(B):
+        via_head = gh[b].astype(np.float64) @ head.astype(np.float64).T
+        via_emb = gh[b].astype(np.float64) @ emb.astype(np.float64).T
+        assert rel_rows(gl[b], via_head).max() < TOL
+        assert rel_rows(gl[b], via_emb).max() > 0.5
+    tied = A.HipLatModel(A.LatConfig(**kw), max_batch=1, max_rows=32)
+    with pytest.raises(A.ConfigError, match=r"tie_embeddings false does not match the context's LM head \(tied\)"):
+        tied.load_gguf(path)
+    tied.close()
+    hip.close()
+    ref.close()
+
+
+def test_lat_untied_head_synthetic():
+    """Random init of an untied latent model (the head is the last tensor id on both sides)
+    against the oracle, bf16 and f32 heads."""
+    for lmfmt in (1, 0):
+        kw = small_kw(lm_head_format=lmfmt)
+        ref = R.LatModel(R.make_lat_config(**kw, untied_lm_head=1))
+        ref.init_synthetic(41, 0.05)
+        hip = A.HipLatModel(A.LatConfig(**kw, tie_embeddings=False), max_batch=2, max_rows=64)
+        hip.init_synthetic(41, 0.05)
+        B, P = 2, 16
+        ids = R.synth_tokens(43, 1, B * P, kw["vocab_size"]).reshape(B, P)
+        kvs = [ref.kv(128) for _ in range(B)]
+        gl, gh = hip.forward_with_cache_output(ids, [0] * B)
+        assert compare(gl, gh, [kvs[b].forward(ids[b], 0) for b in range(B)], hip.router_gaps(), P) >= 1
+        hip.close()
+        ref.close()

@@ -3,7 +3,8 @@
 schedule (:656-708), RopeScalingConfig::validate (:52-96), dsa_config (model.rs:316-337) and serde's
 field defaults, on GGUF files written by the oracle's encoder.  Pinned against the reference's own
 tests (config.rs:1110-1135) and, for each validation rule, the reference's message; configs a
-latent context cannot hold (MLA or MoE not in every layer, an untied head) are UNSUPPORTED."""
+latent context cannot hold (MLA or MoE not in every layer) are UNSUPPORTED; tie_embeddings false
+gives an untied head."""
 import copy
 
 import numpy as np
@@ -71,6 +72,12 @@ def test_bench_shape_and_fine_grained_subdivision(tmp_path):
     assert got.n_heads == 8
 
 
+def test_tie_embeddings_selects_the_head(tmp_path):
+    # LmHead::new (model.rs:239-248): tied reads the embedding, untied its own lm_head.weight
+    assert read(tmp_path, base()).tie_embeddings is True
+    assert read(tmp_path, base(tie_embeddings=False)).tie_embeddings is False
+
+
 def edit(path, value):
     cfg = base()
     node = cfg
@@ -117,7 +124,6 @@ def test_reference_validation_messages(tmp_path, path, value, msg):
 @pytest.mark.parametrize("path,value,match", [
     (("moe", "every_n_layers"), 2, "every_n_layers 2 leaves dense FFN layers"),
     (("attention_schedule", "mla_layers"), [1], "mla_layers must list all 2 layers"),
-    (("tie_embeddings",), False, "tie_embeddings false"),
     (("moe",), KeyError, "has no moe"),
     (("attention_schedule",), KeyError, "has no attention_schedule"),
 ])

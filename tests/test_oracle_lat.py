@@ -111,3 +111,28 @@ def test_synthetic_latent_cache_is_deterministic():
     a, _ = k1.forward(ids, 20)
     b, _ = k2.forward(ids, 20)
     assert np.array_equal(a, b)
+
+
+def test_untied_head_reads_lm_head():
+    """tie_embeddings false (LmHead::untied_with_qat, model.rs:239-248): lm_head.weight is the
+    tensor after final_norm and the logits are the final normed hidden state times it; the
+    embedding still feeds the input rows (same hidden state as the tied model)."""
+    tied = R.LatModel(tiny_lat())
+    untied = R.LatModel(tiny_lat(untied_lm_head=1))
+    names = [t[0] for t in untied.tensors()]
+    assert names[:-1] == [t[0] for t in tied.tensors()] and names[-1] == "lm_head.weight"
+    assert untied.tensors()[-1][1:3] == (97, 64)
+    synth(tied, 3)
+    synth(untied, 3)
+    kv_t, kv_u = tied.kv(48), untied.kv(48)
+    ids = np.array([5, 17, 96, 0, 41], np.uint32)
+    lt, ht = kv_t.forward(ids, 0)
+    lu, hu = kv_u.forward(ids, 0)
+    assert np.array_equal(ht, hu)  # everything before the head is shared
+    head = untied.get(len(names) - 1).astype(np.float64)
+    emb = untied.get(0).astype(np.float64)
+    assert rel(lu, hu.astype(np.float64) @ head.T) < 1e-5
+    assert rel(lt, ht.astype(np.float64) @ emb.T) < 1e-5
+    assert rel(lu, lt) > 0.1
+    tied.close()
+    untied.close()
