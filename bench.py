@@ -360,6 +360,7 @@ def run_c3(args):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_hbm_traffic.txt")
 TRAFFIC_PROFILE_B32 = os.path.join(ROOT, "profiles", "verify_c4_b32_hbm_traffic.txt")
 STATS_PROFILE = os.path.join(ROOT, "profiles", "verify_c4_b1_kernel_stats.txt")
+STATS_PROFILE_B32 = os.path.join(ROOT, "profiles", "verify_c4_b32_kernel_stats.txt")
 
 
 def measured_traffic(key="traffic_bytes_per_launch", path=None):
@@ -367,7 +368,8 @@ def measured_traffic(key="traffic_bytes_per_launch", path=None):
     launch of a kernel class from the --pmc summaries (FETCH_SIZE and WRITE_SIZE runs of
     this script, scaled by a plain-copy calibration: the INT4 GEMV and the decode attention
     of the batch-1 verify, the many-row INT4 GEMM of the batch-32 verify), or the mean
-    INT4 GEMV duration of the batch-1 kernel-trace summary."""
+    duration of the INT4 GEMV (batch 1) or 128-row INT4 GEMM (batch 32) launches of the
+    kernel-trace summaries."""
     try:
         for line in open(path or TRAFFIC_PROFILE):
             if line.startswith(key + " "):
@@ -575,7 +577,10 @@ def summarize_trace(path, title, cmd):
     """Text summary of a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv) for profiles/:
     per-kernel calls / total / mean / min / max, the verify-path kernels by workgroup
     count, and the mean duration of the INT4 GEMV launches (gemv_tile_kernel<3, ...>) as
-    `int4_gemv_avg_launch_us`, which bench.py quotes beside its own dispatch-timed figure."""
+    `int4_gemv_avg_launch_us`, and of the 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>:
+    the 1 x 8 wave shape with two 16-row chunks per wave, which the C4 plan table uses above
+    64 rows only) as `int4_gemm128_avg_launch_us`; bench.py quotes both beside its own
+    dispatch-timed figures."""
     import csv
     rows = list(csv.DictReader(open(path)))
     col = {k.lower(): k for k in rows[0].keys()} if rows else {}
@@ -605,6 +610,12 @@ def summarize_trace(path, title, cmd):
         n, t = sum(x[0] for x in g), sum(x[1] for x in g)
         out += ["", f"# all INT4 GEMV launches (gemv_tile_kernel<3, ...>): {n} dispatches, {t / 1e3:.3f} ms, mean "
                     f"{t / n:.3f} us", f"int4_gemv_avg_launch_us = {t / n:.3f}"]
+    g = [(n, t) for name, (n, t, _, _) in stats.items()
+         if name.startswith("void aarh::gemm_kernel<3,") and name.split("<")[1].split(",")[2:4] == [" 1", " 2"]]
+    if g:
+        n, t = sum(x[0] for x in g), sum(x[1] for x in g)
+        out += ["", f"# 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>): {n} dispatches, {t / 1e3:.3f} ms, "
+                    f"mean {t / n:.3f} us", f"int4_gemm128_avg_launch_us = {t / n:.3f}"]
     hot = [n for n in byname_wg if any(k in n for k in ("gemv_tile", "gemm_kernel", "attn", "accept", "candidates"))]
     if hot:
         out += ["", "# verify-path kernels: workgroups per launch"]
@@ -724,6 +735,12 @@ def main():
             "traffic": measured_traffic("gemm_traffic_bytes_per_launch", TRAFFIC_PROFILE_B32),
             "avg_launch_us": round(gm["avg_us"], 3),
         }
+        # the same launches' mean duration in the committed rocprofv3 kernel trace
+        prof_us = measured_traffic("int4_gemm128_avg_launch_us", STATS_PROFILE_B32)
+        if prof_us and gm["avg_us"]:
+            tf = gm["useful_tflops"] * gm["avg_us"] / prof_us
+            roof_gemm["profile"] = {"file": os.path.relpath(STATS_PROFILE_B32, ROOT), "avg_launch_us": prof_us,
+                                    "achieved": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu and 1 in res:
         try:
