@@ -210,7 +210,7 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // Method: while s stays inside one binade [2^e, 2^(e+1)), every partial sum
 // is an integer multiple of ulp(s), and fl(s + x) = s + ulp * RNE(x / ulp)
 // unless x / ulp has fraction exactly 1/2 (a tie, decided by parity).  So the
-// wave turns 256 elements at a time into integer increments, scans them, and
+// wave turns 512 elements at a time into integer increments, scans them, and
 // stops at the first element that leaves the binade or ties; that element is
 // added with a real f32 add and the scan restarts after it.
 // ---------------------------------------------------------------------------
@@ -248,7 +248,7 @@ __device__ __forceinline__ float readlane_f32(float x, int l) {
 // Elements added one at a time after the sum first becomes non-zero (see below).
 constexpr int SCAN_SCALAR = 64;
 __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, int gbase, SeqScan& st) {
-    constexpr int E = 16;  // consecutive elements per lane in the binade fast path (1024 per step)
+    constexpr int E = 8;  // consecutive elements per lane in the binade fast path (512 per step)
     const int lane = threadIdx.x & 63;
     float s = st.s;
     int pos = 0;
@@ -351,18 +351,36 @@ __device__ __forceinline__ void seq_scan_wave(const float* v, int n, float u, in
                 x[k] = (i >= pos && i < n) ? v[i] : 0.0f;
             }
         }
+        // r = RNE(c) for c = x / ulp.  An element is special when c is not a finite value
+        // in [0, 2^24) (its bit pattern, read as unsigned, is at or above that of 2^24:
+        // also negative values and NaN) or is a tie (|c - RNE(c)| == 1/2).  The lane
+        // tests both once over its E elements with vector max operations, and only a
+        // flagged lane marks its elements one by one (special elements become 2^24).
         int r[E];
         bool special = false;
         int lsum = 0;
+        float dmax = 0.0f;
+        uint32_t bmax = 0u;
 #pragma unroll
         for (int k = 0; k < E; k++) {
             const float c = ldexpf(x[k], sh);
-            const float a = floorf(c);
-            const float f = c - a;
-            const bool sp = !(c < 16777216.0f) || (f == 0.5f) || !(x[k] >= 0.0f);
-            r[k] = sp ? 16777216 : ((int)a + (f > 0.5f ? 1 : 0));
-            special |= sp;
+            const float rr = __builtin_rintf(c);
+            dmax = fmaxf(dmax, fabsf(c - rr));
+            bmax = max(bmax, __float_as_uint(c));
+            r[k] = (int)rr;
             lsum += r[k];
+        }
+        if (bmax >= 0x4B800000u || dmax == 0.5f) {
+            special = true;
+            lsum = 0;
+#pragma unroll
+            for (int k = 0; k < E; k++) {
+                const float c = ldexpf(x[k], sh);
+                const float rr = __builtin_rintf(c);
+                const bool sp = !(__float_as_uint(c) < 0x4B800000u) || (fabsf(c - rr) == 0.5f);
+                r[k] = sp ? 16777216 : (int)rr;
+                lsum += r[k];
+            }
         }
         if (special || lsum > 16777217) lsum = 16777217;  // past the binade anyway; keeps the scan in range
         const int incl = wave_incl_scan_dpp(lsum);

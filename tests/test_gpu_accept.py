@@ -124,6 +124,37 @@ def test_sampling_only_launch_is_inverse_cdf(ctx):
     assert np.all(out["draws"] == 1)
 
 
+def test_exact_sums_over_rounding_ties_and_wide_ranges(ctx):
+    """Rows built to stress the exact sequential f32 sums: logits on a 1/16 grid (a few
+    hundred distinct terms, each repeated, so a term that lands exactly halfway between
+    two floats of the running sum does so again and again and rounds by parity), and
+    logits spread over [-110, 0] (terms from 1 down
+    to subnormals, so the running sum crosses many binades with terms far below its
+    ulp).  Normalisers, residual masses and CDF walks must equal the oracle's
+    sequential loops: accepted lengths, tokens and draws identical except flagged."""
+    rng = np.random.default_rng(21)
+    B, K, V = 16, 4, 32000
+    tgt = np.empty((B, K + 1, V), np.float32)
+    tgt[:8] = np.round(rng.normal(0, 3, (8, K + 1, V)) * 16) / 16
+    tgt[8:] = -rng.uniform(0, 110, (8, K + 1, V))
+    drf = tgt[:, :K].copy()
+    drf[:, :, ::3] += np.round(rng.normal(0, 1, (B, K, (V + 2) // 3)) * 16).astype(np.float32) / 16
+    s = R.sampler(temperature=1.0)
+    toks = np.zeros((B, K), np.uint32)
+    for b in range(B):
+        r = R.Rng(500 + b)
+        for i in range(K):
+            toks[b, i] = R.sample_probabilities(s, r, R.probabilities(s, drf[b, i]))
+    out, ref = run_both(ctx, tgt, drf, toks, 1.0, True, seeds=np.arange(B, dtype=np.uint64) + 40)
+    assert_parity(out, ref, max_flag_frac=0.25)
+    assert np.array_equal(out["draws"], ref["draws"])
+    assert (ref["accept_len"] < K).any()
+    # sampling-only launches over the same target rows (the CDF walk over exact sums)
+    out, ref = run_both(ctx, tgt[:, :1], np.zeros((B, 0, V), np.float32), np.zeros((B, 0), np.uint32), 1.0, True,
+                        seeds=np.arange(B, dtype=np.uint64) + 90)
+    assert_parity(out, ref, max_flag_frac=0.25)
+
+
 def test_out_of_vocab_draft_token_rejects(ctx):
     tgt, drf, toks = c2_inputs(B=4, K=2, V=1024, seed=6)
     toks[:, 0] = 5000  # q = 0 -> rejected without a draw (speculative.rs:764-767)
