@@ -246,15 +246,18 @@ def test_many_row_gemm_variants(wfmt, lmfmt, nseq, S):
     hip.close()
 
 
-@pytest.mark.parametrize("wfmt,nseq,S", [(A.W_INT4_G128, 32, 1), (A.W_INT4_G128, 8, 4), (A.W_INT4_G128, 12, 4),
+@pytest.mark.parametrize("wfmt,nseq,S", [(A.W_INT4_G128, 32, 1), (A.W_INT4_G128, 8, 4), (A.W_INT4_G128, 5, 4),
+                                         (A.W_INT4_G128, 12, 4),
                                          (A.W_INT4_G128, 32, 4), (A.W_INT8_ROW, 32, 4), (A.W_INT8_ROW, 10, 4),
                                          (A.W_BF16, 32, 4)])
 def test_c4_width_gemm_plans(wfmt, nseq, S):
     """C4 projection widths (d_model 4096, ffn 11008, 32 query / 8 kv heads) at M = 32,
-    32, 48, 128 (INT4 g128), 128, 40 (INT8) and 128 (BF16) rows: the tuned INT4 GEMM
-    plans and the rule's plans for the other formats (32- and 64-row blocks, 1 to 4
-    weight tiles per wave, 1 to 8 k-splits) through a one-layer forward.  Logits and
-    hidden within 2e-3 of the f32 oracle."""
+    32, 20, 48, 128 (INT4 g128), 128, 40 (INT8) and 128 (BF16) rows: the tuned INT4 GEMM
+    plans (2 x 4 and 1 x 8 wave grids, the K-split mode of gate/up and down at 32 rows
+    and below, 20 rows leaving the second 16-row chunk partial) and the rule's plans for
+    the other formats (32- and 64-row blocks, 1 to 4 weight tiles per wave, 1 to 8
+    k-splits) through a one-layer forward.  Logits and hidden within 2e-3 of the f32
+    oracle."""
     kw = dict(vocab_size=2048, hidden_dim=4096, ffn_dim=11008, n_layers=1, n_heads=32, n_kv_heads=8,
               max_seq_len=64, weight_format=wfmt, kv_format=A.KV_INT8, lm_head_format=1)
     print("c4-width gemm", wfmt, nseq, S, flush=True)
