@@ -472,11 +472,11 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const int sc_voff = (lane & 15) * 4;
     auto issue = [&](char* st, int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int p = 0; p < 4; p++) lds_dma16(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+        for (int p = 0; p < 4; p++) lds_dma16<true>(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
 #pragma unroll
-        for (int p = 0; p < 4; p++) lds_dma16(vr, st + KVB + p * 1024, lane * 16 + p * 1024, t * AM_HD);
-        lds_dma4(ksr, st + 2 * KVB, sc_voff, t * 2);
-        lds_dma4(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
+        for (int p = 0; p < 4; p++) lds_dma16<true>(vr, st + KVB + p * 1024, lane * 16 + p * 1024, t * AM_HD);
+        lds_dma4<true>(ksr, st + 2 * KVB, sc_voff, t * 2);
+        lds_dma4<true>(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
     };
     // A wave whose two staged blocks hold no new position issues them first of all, so
     // their round trip overlaps the query loads and the append; the others issue after

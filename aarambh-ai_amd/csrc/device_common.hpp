@@ -481,34 +481,59 @@ __device__ inline SeqSum seq_sum_wave(const float* v, int n, float u) {
 // soff land at LDS address lds_base + 16 l (buffer_load_dwordx4 ... lds, base in
 // M0).  Written as inline asm so the compiler does not see an LDS write it would
 // guard with a conservative vmcnt(0) before every LDS read: the kernel counts
-// these loads itself.  M0 is restored before the statement ends.
+// these loads itself.  M0 is restored before the statement ends.  NT marks the load
+// non-temporal (data read once: a stream of weights or cache blocks).
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, const void* lds_dst, int voff, int soff) {
     const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
     int saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(base), "v"(voff), "s"(r), "s"(soff)
-        : "memory");
+    if constexpr (NT)
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, %4 offen nt lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(base), "v"(voff), "s"(r), "s"(soff)
+            : "memory");
+    else
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(base), "v"(voff), "s"(r), "s"(soff)
+            : "memory");
 }
 
 // One 256-byte wave load into LDS: lane l's 4 bytes land at lds_dst + 4 l.
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, const void* lds_dst, int voff, int soff) {
     const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
     int saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dword %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(base), "v"(voff), "s"(r), "s"(soff)
-        : "memory");
+    if constexpr (NT)
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dword %2, %3, %4 offen nt lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(base), "v"(voff), "s"(r), "s"(soff)
+            : "memory");
+    else
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dword %2, %3, %4 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(base), "v"(voff), "s"(r), "s"(soff)
+            : "memory");
 }
 
 // s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14), other counters unconstrained.
