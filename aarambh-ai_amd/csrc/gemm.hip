@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
             // pieces not a multiple of the waves: the extra loads repeat a piece (same bytes, same place)
             const int pi = (wid * C::W_PW + q) % C::W_PIECES, jj = pi / WP, sub = pi % WP;
             const int nt = min(nb * NT + jj, ntiles - 1);
-            lds_dma16(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * 16 + sub * 1024,
+            lds_dma16<true>(wr, base + C::A_BYTES + jj * T::TILE_BYTES + sub * 1024, lane * 16 + sub * 1024,
                       (int)(((unsigned)nt * G + g) * T::TILE_BYTES));
         }
 #pragma unroll
@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         for (int q = 0; q < 4; q++) {
             const int nt = ks_nt[(j0 + q) % (KS ? NT : 1)];
             w[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      wr, lane * 16, (int)(((unsigned)nt * G + g) * 1024u), 0));
+                                                      wr, lane * 16, (int)(((unsigned)nt * G + g) * 1024u), 2));
             z[q] = __builtin_amdgcn_raw_buffer_load_b32(zr, lr * 4, (int)(((unsigned)nt * G + g) * 64u), 0);
         }
     };
