@@ -25,55 +25,77 @@ static constexpr int AT_TOK = 64;       // tokens per LDS sub-block
 static constexpr int AT_MAXR = 32;      // query rows per workgroup
 static constexpr int AT_MAXHD = 128;
 
-// Append this launch's new K / V rows (positions pos0 .. kv_len-1, post-RoPE
-// f32 rows written by the QKV projection) that fall in [t_begin, t_end) to the
-// cache of (slot, kv head).  Every workgroup whose chunk covers a new position
-// writes it (identical bytes) before it reads the chunk, so no other launch
-// is needed.  INT8: per token, per kv head absmax scale (1.0 when <= eps) kept
-// as fp16, codes rounded from the f32 scale.  Returns with the writes visible
-// to the workgroup.
+// Append one new K / V row (position t of pos0 .. kv_len-1, post-RoPE f32 rows
+// written by the QKV projection) to the cache of (slot, kv head); one wave.
+// INT8: per token, per kv head absmax scale (1.0 when <= eps) kept as fp16,
+// codes rounded from the f32 scale.
+// The row's values for this lane (dims lane, lane + 64) are loaded by
+// load_kv_token so that several tokens' loads share one round trip.
+struct KvNew {
+    float v[2][2];  // [K / V][dim lane, lane + 64]
+};
+__device__ __forceinline__ KvNew load_kv_token(const AttnArgs& a, int seq, int kvh, int pos0, int t) {
+    const int lane = threadIdx.x & 63;
+    const int hd = a.hd, KD = a.n_kv * hd;
+    const size_t row = (size_t)seq * a.S + (t - pos0);
+    KvNew r;
+#pragma unroll
+    for (int which = 0; which < 2; which++) {
+        const float* src = a.knew + row * 2 * KD + (size_t)which * KD + (size_t)kvh * hd;
+        r.v[which][0] = lane < hd ? src[lane] : 0.f;
+        r.v[which][1] = lane + 64 < hd ? src[lane + 64] : 0.f;
+    }
+    return r;
+}
+__device__ __forceinline__ void store_kv_token(const AttnArgs& a, size_t hb, int t, const KvNew& nv) {
+    const int lane = threadIdx.x & 63;
+    const int hd = a.hd;
+#pragma unroll
+    for (int which = 0; which < 2; which++) {
+        const float v0 = nv.v[which][0], v1 = nv.v[which][1];
+        auto kdst = [&](int d) { return k_off(hb, t, d, a.cap, hd, a.kv_fmt); };
+        auto vdst = [&](int d) { return vt_off(hb, d, t, a.cap, hd, a.kv_fmt); };  // V^T
+        if (a.kv_fmt == KV_INT8) {
+            const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+            const float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
+            const int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.0f), 127.0f);
+            const int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
+            const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
+            if (which == 0) {
+                int8_t* kc = (int8_t*)a.kc;
+                if (lane < hd) kc[kdst(lane)] = q0;
+                if (lane + 64 < hd) kc[kdst(lane + 64)] = q1;
+                if (lane == 0) ((uint16_t*)a.ks)[hb * a.cap + t] = sh;
+            } else {
+                int8_t* vc = (int8_t*)a.vc;
+                if (lane < hd) vc[vdst(lane)] = q0;
+                if (lane + 64 < hd) vc[vdst(lane + 64)] = q1;
+                if (lane == 0) ((uint16_t*)a.vs)[hb * a.cap + t] = sh;
+            }
+        } else if (a.kv_fmt == KV_F16) {
+            _Float16* dst = (_Float16*)(which == 0 ? a.kc : a.vc);
+            if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = (_Float16)v0;
+            if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = (_Float16)v1;
+        } else {
+            float* dst = (float*)(which == 0 ? a.kc : a.vc);
+            if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = v0;
+            if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = v1;
+        }
+    }
+}
+__device__ __forceinline__ void append_kv_token(const AttnArgs& a, int seq, int kvh, size_t hb, int pos0, int t) {
+    store_kv_token(a, hb, t, load_kv_token(a, seq, kvh, pos0, t));
+}
+
+// Append this launch's new positions that fall in [t_begin, t_end), spread over the
+// workgroup's waves.  Every workgroup whose chunk covers a new position writes it
+// (identical bytes) before it reads the chunk, so no other launch is needed.
+// Returns with the writes visible to the workgroup.
 __device__ void append_new_kv(const AttnArgs& a, int seq, int kvh, size_t hb, int pos0, int t_begin, int t_end) {
     const int lo = max(t_begin, pos0);
     if (lo >= t_end) return;  // uniform over the workgroup
-    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-    const int hd = a.hd, KD = a.n_kv * hd;
-    for (int t = lo + wid; t < t_end; t += nw) {
-        const size_t row = (size_t)seq * a.S + (t - pos0);
-#pragma unroll
-        for (int which = 0; which < 2; which++) {
-            const float* src = a.knew + row * 2 * KD + (size_t)which * KD + (size_t)kvh * hd;
-            const float v0 = lane < hd ? src[lane] : 0.f;
-            const float v1 = lane + 64 < hd ? src[lane + 64] : 0.f;
-            auto kdst = [&](int d) { return k_off(hb, t, d, a.cap, hd, a.kv_fmt); };
-            auto vdst = [&](int d) { return vt_off(hb, d, t, a.cap, hd, a.kv_fmt); };  // V^T
-            if (a.kv_fmt == KV_INT8) {
-                const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
-                const float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
-                const int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.0f), 127.0f);
-                const int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
-                const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
-                if (which == 0) {
-                    int8_t* kc = (int8_t*)a.kc;
-                    if (lane < hd) kc[kdst(lane)] = q0;
-                    if (lane + 64 < hd) kc[kdst(lane + 64)] = q1;
-                    if (lane == 0) ((uint16_t*)a.ks)[hb * a.cap + t] = sh;
-                } else {
-                    int8_t* vc = (int8_t*)a.vc;
-                    if (lane < hd) vc[vdst(lane)] = q0;
-                    if (lane + 64 < hd) vc[vdst(lane + 64)] = q1;
-                    if (lane == 0) ((uint16_t*)a.vs)[hb * a.cap + t] = sh;
-                }
-            } else if (a.kv_fmt == KV_F16) {
-                _Float16* dst = (_Float16*)(which == 0 ? a.kc : a.vc);
-                if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = (_Float16)v0;
-                if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = (_Float16)v1;
-            } else {
-                float* dst = (float*)(which == 0 ? a.kc : a.vc);
-                if (lane < hd) dst[which == 0 ? kdst(lane) : vdst(lane)] = v0;
-                if (lane + 64 < hd) dst[which == 0 ? kdst(lane + 64) : vdst(lane + 64)] = v1;
-            }
-        }
-    }
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    for (int t = lo + wid; t < t_end; t += nw) append_kv_token(a, seq, kvh, hb, pos0, t);
     __threadfence_block();
     __syncthreads();
 }
@@ -308,6 +330,7 @@ __device__ __forceinline__ void lds_wave_sync() {
 static constexpr int AM_ROWS = 16;          // query rows per workgroup (one MFMA column tile)
 static constexpr int AM_HD = 128;
 static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
+static constexpr int AM_TAIL = AM_WAVES - 1;  // INT8 path: the wave that appends and reads the new positions
 static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
 static constexpr int AM_MAXCH = 32;         // chunks one merge combines
 static constexpr int AM_STAGE = 2 * 32 * AM_HD + 512;  // one INT8 block staged in LDS: K, V^T, scales
@@ -419,8 +442,9 @@ __device__ __forceinline__ void frag_out_pair(const XFrag& fo, int orow, int oco
 
 // Flash-decode attention on MFMA for head_dim 128 and fp16 / INT8 caches.
 // Workgroup = (sequence, kv head, tile of <= 16 query rows, token chunk), 8 waves;
-// wave w takes the chunk's 32-token blocks w, w+8, ... with the next block's
-// loads in flight while the current one computes.  Scores are computed
+// wave w takes the chunk's 32-token blocks w, w+8, ... (INT8: the blocks before the
+// new positions; the blocks holding new positions go to one wave, which appends
+// them) with the next block's loads in flight while the current one computes.  Scores are computed
 // transposed, S^T = K Q^T (A = K rows, B = Q^T as fp16 hi and lo halves), so the
 // MFMA result layout (lane = query row, 8 tokens per lane) is directly the B
 // operand of O^T = V^T P^T: no LDS round trip, and the row statistics live in
@@ -471,6 +495,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t ksr = coh_rsrc(a.ks + hb * a.cap), vsr = coh_rsrc(a.vs + hb * a.cap);
     const int sc_voff = (lane & 15) * 4;
     auto issue = [&](char* st, int t) __attribute__((always_inline)) {
+        t = __builtin_amdgcn_readfirstlane(t);  // wave-uniform: the loads take it as a scalar offset
 #pragma unroll
         for (int p = 0; p < 4; p++) lds_dma16<true>(kr, st + p * 1024, lane * 16 + p * 1024, t * AM_HD);
 #pragma unroll
@@ -478,18 +503,94 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         lds_dma4<true>(ksr, st + 2 * KVB, sc_voff, t * 2);
         lds_dma4<true>(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
     };
-    // A wave whose two staged blocks hold no new position issues them first of all, so
-    // their round trip overlaps the query loads and the append; the others issue after
-    // the append (which writes the new positions they read).
-    bool staged = false;
-    if constexpr (DMA) {
-        if (tb < t_end && max(tb, min(tb + STEP, t_last)) + 32 <= pos0) {
-            issue(st0, tb);
-            issue(st0 + AM_STAGE, min(tb + STEP, t_last));
-            staged = true;
+    // DMA schedule: the blocks wholly before the new positions ("old" blocks) go round
+    // robin to the eight waves; the blocks holding new positions ("tail" blocks) go to
+    // wave AM_TAIL, first in its list, and it hands as many of its last old blocks to
+    // waves 0, 1, ... as it has tail blocks.  The tail wave writes the new positions
+    // into its staged copy of a tail block (patch_tail) and stores the block back whole,
+    // so no wave waits for the cache append (a workgroup barrier after a byte-wise
+    // append held every wave until the appending waves' loads and stores came back).
+    // Wave wid's i-th block: tb_of(i); past its last block it re-reads that block.
+    const int tail_start = pos0 < t_end ? max(t_begin, pos0 & ~31) : t_end;
+    const int n_old = (tail_start - t_begin) >> 5, n_tail = (t_end - tail_start + 31) >> 5;
+    auto own_old = [&](int w) { return n_old > w ? (n_old - w + AM_WAVES - 1) / AM_WAVES : 0; };
+    const int t_old = own_old(AM_TAIL), n_moved = min(min(n_tail, t_old), AM_TAIL);
+    const int n_lead = wid == AM_TAIL ? n_tail : 0;                       // tail blocks first
+    const int n_first = wid == AM_TAIL ? t_old - n_moved : own_old(wid);  // strided old blocks
+    const int n_blk = n_lead + n_first + (wid != AM_TAIL && wid < n_moved ? 1 : 0);
+    auto tb_of = [&](int i) __attribute__((always_inline)) {
+        i = min(i, n_blk - 1);
+        if (i < n_lead) return tail_start + 32 * i;
+        i -= n_lead;
+        if (i < n_first) return t_begin + 32 * (wid + AM_WAVES * i);
+        return t_begin + 32 * (AM_TAIL + AM_WAVES * (t_old - n_moved + wid));  // handed over
+    };
+    // The cache append of tail block tb (positions max(tb, pos0) .. min(tb + 32, t_end) - 1,
+    // the bytes append_kv_token writes), made in the block's landed stage; the patched
+    // block then goes back to the cache whole, in the 16-byte runs the loads read.
+    // The first four new rows are loaded before any block (ahead of the block loads in
+    // the memory pipeline); later ones when their block is patched.
+    const int first_new = max(t_begin, pos0);
+    KvNew pre[4];
+    if (DMA && wid == AM_TAIL && n_tail > 0)
+#pragma unroll
+        for (int j = 0; j < 4; j++) pre[j] = load_kv_token(a, seq, kvh, pos0, min(first_new + j, t_end - 1));
+    auto patch_tail = [&](char* st, int tb) __attribute__((always_inline)) {
+        const int lo = max(tb, pos0), hi = min(tb + 32, t_end);
+        for (int t0 = lo; t0 < hi; t0 += 4) {
+            KvNew nv[4];
+            if (t0 == first_new) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) nv[j] = pre[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) nv[j] = load_kv_token(a, seq, kvh, pos0, min(t0 + j, hi - 1));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (t0 + j >= hi) break;
+                const int r = t0 + j - tb;
+#pragma unroll
+                for (int which = 0; which < 2; which++) {
+                    const float v0 = nv[j].v[which][0], v1 = nv[j].v[which][1];
+                    const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+                    const float sc = amax <= FLT_EPSILON ? 1.0f : amax / 127.0f;
+                    const int8_t q0 = (int8_t)fminf(fmaxf(roundf(v0 / sc), -127.0f), 127.0f);
+                    const int8_t q1 = (int8_t)fminf(fmaxf(roundf(v1 / sc), -127.0f), 127.0f);
+                    const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sc);
+                    if (which == 0) {
+                        st[k_off(0, r, lane, a.cap, AM_HD, KV_INT8)] = q0;
+                        st[k_off(0, r, lane + 64, a.cap, AM_HD, KV_INT8)] = q1;
+                        if (lane == 0) *(uint16_t*)(st + 2 * KVB + 2 * r) = sh;
+                    } else {
+                        st[KVB + vt_off(0, lane, r, a.cap, AM_HD, KV_INT8)] = q0;
+                        st[KVB + vt_off(0, lane + 64, r, a.cap, AM_HD, KV_INT8)] = q1;
+                        if (lane == 0) *(uint16_t*)(st + 2 * KVB + 256 + 2 * r) = sh;
+                    }
+                }
+            }
         }
+        uint8_t* kb = (uint8_t*)a.kc + (hb * a.cap + tb) * AM_HD;
+        uint8_t* vb = (uint8_t*)a.vc + (hb * a.cap + tb) * AM_HD;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            *(u32x4v_t*)(kb + p * 1024 + lane * 16) = *(const u32x4v_t*)(st + p * 1024 + lane * 16);
+            *(u32x4v_t*)(vb + p * 1024 + lane * 16) = *(const u32x4v_t*)(st + KVB + p * 1024 + lane * 16);
+        }
+        if (lane < 16) {
+            *(uint32_t*)((uint8_t*)((uint16_t*)a.ks + hb * a.cap + tb) + lane * 4) = *(const uint32_t*)(st + 2 * KVB + lane * 4);
+            *(uint32_t*)((uint8_t*)((uint16_t*)a.vs + hb * a.cap + tb) + lane * 4) =
+                *(const uint32_t*)(st + 2 * KVB + 256 + lane * 4);
+        }
+    };
+    if constexpr (DMA) {
+        if (n_blk > 0) {
+            issue(st0, tb_of(0));
+            issue(st0 + AM_STAGE, tb_of(1));
+        }
+    } else {
+        if (t_end > pos0) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
     }
-    if (t_end > pos0) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
 
     // ---- this lane's query row (lr): Q^T B operand, hi/lo, dims 32*lg + 8*kk + slot ----
     const bool row_ok = lr < R;
@@ -611,14 +712,12 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         // A block is copied to registers as soon as it lands and its stage is refilled
         // at once, so both stages stay in flight while the block is computed.
         constexpr int NL = 10;  // DMA loads per block
-        if (tb < t_end && !staged) {
-            issue(st0, tb);
-            issue(st0 + AM_STAGE, min(tb + STEP, t_last));
-        }
-        for (int i = 0; tb < t_end; i++, tb += STEP) {
+        for (int i = 0; i < n_blk; i++) {
+            tb = tb_of(i);
             char* cur_st = st0 + (i & 1) * AM_STAGE;
             wait_vmcnt<NL>();  // block i has landed; block i + 1 may still be in flight
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (i < n_lead) patch_tail(cur_st, tb);
             KvRaw<KVF> cur;
 #pragma unroll
             for (int ts = 0; ts < 2; ts++)
@@ -631,7 +730,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage has been read
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            issue(cur_st, min(tb + 2 * STEP, t_last));
+            issue(cur_st, tb_of(i + 2));
             block(cur);
         }
         wait_vmcnt<0>();
