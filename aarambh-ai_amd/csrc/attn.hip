@@ -331,6 +331,7 @@ static constexpr int AM_ROWS = 16;          // query rows per workgroup (one MFM
 static constexpr int AM_HD = 128;
 static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
 static constexpr int AM_TAIL = AM_WAVES - 1;  // INT8 path: the wave that appends and reads the new positions
+static constexpr int AM_HAND = 2;             // old blocks the tail wave hands over beyond its tail blocks
 static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
 static constexpr int AM_MAXCH = 32;         // chunks one merge combines
 static constexpr int AM_STAGE = 2 * 32 * AM_HD + 512;  // one INT8 block staged in LDS: K, V^T, scales
@@ -505,8 +506,10 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     };
     // DMA schedule: the blocks wholly before the new positions ("old" blocks) go round
     // robin to the eight waves; the blocks holding new positions ("tail" blocks) go to
-    // wave AM_TAIL, first in its list, and it hands as many of its last old blocks to
-    // waves 0, 1, ... as it has tail blocks.  The tail wave writes the new positions
+    // wave AM_TAIL, first in its list, and it hands its last n_tail + AM_HAND old blocks
+    // to wave 0 (the oldest wave of the workgroup, whose stream ends first: issue
+    // arbitration favours it, and timestamps put its stream's end 9 us before the
+    // others' at B = 32).  The tail wave writes the new positions
     // into its staged copy of a tail block (patch_tail) and stores the block back whole,
     // so no wave waits for the cache append (a workgroup barrier after a byte-wise
     // append held every wave until the appending waves' loads and stores came back).
@@ -514,16 +517,16 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     const int tail_start = pos0 < t_end ? max(t_begin, pos0 & ~31) : t_end;
     const int n_old = (tail_start - t_begin) >> 5, n_tail = (t_end - tail_start + 31) >> 5;
     auto own_old = [&](int w) { return n_old > w ? (n_old - w + AM_WAVES - 1) / AM_WAVES : 0; };
-    const int t_old = own_old(AM_TAIL), n_moved = min(min(n_tail, t_old), AM_TAIL);
+    const int t_old = own_old(AM_TAIL), n_moved = n_tail > 0 ? min(n_tail + AM_HAND, t_old) : 0;
     const int n_lead = wid == AM_TAIL ? n_tail : 0;                       // tail blocks first
     const int n_first = wid == AM_TAIL ? t_old - n_moved : own_old(wid);  // strided old blocks
-    const int n_blk = n_lead + n_first + (wid != AM_TAIL && wid < n_moved ? 1 : 0);
+    const int n_blk = n_lead + n_first + (wid == 0 ? n_moved : 0);
     auto tb_of = [&](int i) __attribute__((always_inline)) {
         i = min(i, n_blk - 1);
         if (i < n_lead) return tail_start + 32 * i;
         i -= n_lead;
         if (i < n_first) return t_begin + 32 * (wid + AM_WAVES * i);
-        return t_begin + 32 * (AM_TAIL + AM_WAVES * (t_old - n_moved + wid));  // handed over
+        return t_begin + 32 * (AM_TAIL + AM_WAVES * (t_old - n_moved + i - n_first));  // handed over
     };
     // The cache append of tail block tb (positions max(tb, pos0) .. min(tb + 32, t_end) - 1,
     // the bytes append_kv_token writes), made in the block's landed stage; the patched
