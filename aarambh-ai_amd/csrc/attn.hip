@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     // into its staged copy of a tail block (patch_tail) and stores the block back whole,
     // so no wave waits for the cache append (a workgroup barrier after a byte-wise
     // append held every wave until the appending waves' loads and stores came back).
-    // Wave wid's i-th block: tb_of(i); past its last block it re-reads that block.
+    // Wave wid's i-th block: tb_of(i); a wave issues no load past its last block.
     const int tail_start = pos0 < t_end ? max(t_begin, pos0 & ~31) : t_end;
     const int n_old = (tail_start - t_begin) >> 5, n_tail = (t_end - tail_start + 31) >> 5;
     auto own_old = [&](int w) { return n_old > w ? (n_old - w + AM_WAVES - 1) / AM_WAVES : 0; };
@@ -589,7 +589,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     if constexpr (DMA) {
         if (n_blk > 0) {
             issue(st0, tb_of(0));
-            issue(st0 + AM_STAGE, tb_of(1));
+            if (n_blk > 1) issue(st0 + AM_STAGE, tb_of(1));
         }
     } else {
         if (t_end > pos0) append_new_kv(a, seq, kvh, hb, pos0, t_begin, t_end);
@@ -718,7 +718,9 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         for (int i = 0; i < n_blk; i++) {
             tb = tb_of(i);
             char* cur_st = st0 + (i & 1) * AM_STAGE;
-            wait_vmcnt<NL>();  // block i has landed; block i + 1 may still be in flight
+            // block i has landed; block i + 1 (the only loads issued after it) may still be in flight
+            if (i + 1 < n_blk) wait_vmcnt<NL>();
+            else wait_vmcnt<0>();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             if (i < n_lead) patch_tail(cur_st, tb);
             KvRaw<KVF> cur;
@@ -733,7 +735,7 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage has been read
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            issue(cur_st, tb_of(i + 2));
+            if (i + 2 < n_blk) issue(cur_st, tb_of(i + 2));
             block(cur);
         }
         wait_vmcnt<0>();
