@@ -577,10 +577,10 @@ def summarize_trace(path, title, cmd):
     """Text summary of a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv) for profiles/:
     per-kernel calls / total / mean / min / max, the verify-path kernels by workgroup
     count, and the mean duration of the INT4 GEMV launches (gemv_tile_kernel<3, ...>) as
-    `int4_gemv_avg_launch_us`, and of the 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>:
-    the 1 x 8 wave shape with two 16-row chunks per wave, which the C4 plan table uses above
-    64 rows only) as `int4_gemm128_avg_launch_us`; bench.py quotes both beside its own
-    dispatch-timed figures."""
+    `int4_gemv_avg_launch_us`, and of the 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>
+    outside the K-split mode: the 1 x 8 wave shape with two 16-row chunks per wave, which the
+    C4 plan table uses above 64 rows only) as `int4_gemm128_avg_launch_us`; bench.py quotes
+    both beside its own dispatch-timed figures."""
     import csv
     rows = list(csv.DictReader(open(path)))
     col = {k.lower(): k for k in rows[0].keys()} if rows else {}
@@ -611,10 +611,11 @@ def summarize_trace(path, title, cmd):
         out += ["", f"# all INT4 GEMV launches (gemv_tile_kernel<3, ...>): {n} dispatches, {t / 1e3:.3f} ms, mean "
                     f"{t / n:.3f} us", f"int4_gemv_avg_launch_us = {t / n:.3f}"]
     g = [(n, t) for name, (n, t, _, _) in stats.items()
-         if name.startswith("void aarh::gemm_kernel<3,") and name.split("<")[1].split(",")[2:4] == [" 1", " 2"]]
+         if name.startswith("void aarh::gemm_kernel<3,") and name.split("<")[1].split(",")[2:4] == [" 1", " 2"]
+         and not name.rstrip().endswith("true>")]
     if g:
         n, t = sum(x[0] for x in g), sum(x[1] for x in g)
-        out += ["", f"# 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>): {n} dispatches, {t / 1e3:.3f} ms, "
+        out += ["", f"# 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *, false>): {n} dispatches, {t / 1e3:.3f} ms, "
                     f"mean {t / n:.3f} us", f"int4_gemm128_avg_launch_us = {t / n:.3f}"]
     hot = [n for n in byname_wg if any(k in n for k in ("gemv_tile", "gemm_kernel", "attn", "accept", "candidates"))]
     if hot:
