@@ -332,6 +332,7 @@ static constexpr int AM_HD = 128;
 static constexpr int AM_WAVES = 8;          // 512 threads; wave w takes 32-token blocks w, w+8, ...
 static constexpr int AM_TAIL = AM_WAVES - 1;  // INT8 path: the wave that appends and reads the new positions
 static constexpr int AM_HAND = 2;             // old blocks the tail wave hands over beyond its tail blocks
+static constexpr int AM_SOLO = 2;             // at most this many tail blocks go to the tail wave alone
 static constexpr int AM_REC = AM_HD + 4;    // partial record: m, l, pad, pad, o[hd]
 static constexpr int AM_MAXCH = 32;         // chunks one merge combines
 static constexpr int AM_STAGE = 2 * 32 * AM_HD + 512;  // one INT8 block staged in LDS: K, V^T, scales
@@ -505,25 +506,27 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
         lds_dma4<true>(vsr, st + 2 * KVB + 256, sc_voff, t * 2);
     };
     // DMA schedule: the blocks wholly before the new positions ("old" blocks) go round
-    // robin to the eight waves; the blocks holding new positions ("tail" blocks) go to
-    // wave AM_TAIL, first in its list, and it hands its last n_tail + AM_HAND old blocks
-    // to wave 0 (the oldest wave of the workgroup, whose stream ends first: issue
-    // arbitration favours it, and timestamps put its stream's end 9 us before the
-    // others' at B = 32).  The tail wave writes the new positions
-    // into its staged copy of a tail block (patch_tail) and stores the block back whole,
-    // so no wave waits for the cache append (a workgroup barrier after a byte-wise
-    // append held every wave until the appending waves' loads and stores came back).
-    // Wave wid's i-th block: tb_of(i); a wave issues no load past its last block.
+    // robin to the eight waves; the blocks holding new positions ("tail" blocks) come
+    // first in their wave's list, and that wave writes the new positions into its staged
+    // copy of the block (patch_tail) and stores the block back whole, so no wave waits
+    // for the cache append (a workgroup barrier after a byte-wise append held every wave
+    // until the appending waves' loads and stores came back).  One or two tail blocks
+    // (decode and verify) all go to wave AM_TAIL, which hands its last n_tail + AM_HAND
+    // old blocks to wave 0 (the oldest wave of the workgroup, whose stream ends first:
+    // issue arbitration favours it, and timestamps put its stream's end 9 us before the
+    // others' at B = 32).  More tail blocks (prompt chunks) go round robin like the old
+    // ones.  Wave wid's i-th block: tb_of(i); a wave issues no load past its last block.
     const int tail_start = pos0 < t_end ? max(t_begin, pos0 & ~31) : t_end;
     const int n_old = (tail_start - t_begin) >> 5, n_tail = (t_end - tail_start + 31) >> 5;
-    auto own_old = [&](int w) { return n_old > w ? (n_old - w + AM_WAVES - 1) / AM_WAVES : 0; };
-    const int t_old = own_old(AM_TAIL), n_moved = n_tail > 0 ? min(n_tail + AM_HAND, t_old) : 0;
-    const int n_lead = wid == AM_TAIL ? n_tail : 0;                       // tail blocks first
-    const int n_first = wid == AM_TAIL ? t_old - n_moved : own_old(wid);  // strided old blocks
+    auto own = [&](int n, int w) { return n > w ? (n - w + AM_WAVES - 1) / AM_WAVES : 0; };
+    const bool solo = n_tail <= AM_SOLO;
+    const int t_old = own(n_old, AM_TAIL), n_moved = solo && n_tail > 0 ? min(n_tail + AM_HAND, t_old) : 0;
+    const int n_lead = solo ? (wid == AM_TAIL ? n_tail : 0) : own(n_tail, wid);  // tail blocks first
+    const int n_first = solo && wid == AM_TAIL ? t_old - n_moved : own(n_old, wid);  // strided old blocks
     const int n_blk = n_lead + n_first + (wid == 0 ? n_moved : 0);
     auto tb_of = [&](int i) __attribute__((always_inline)) {
         i = min(i, n_blk - 1);
-        if (i < n_lead) return tail_start + 32 * i;
+        if (i < n_lead) return tail_start + 32 * (solo ? i : wid + AM_WAVES * i);
         i -= n_lead;
         if (i < n_first) return t_begin + 32 * (wid + AM_WAVES * i);
         return t_begin + 32 * (AM_TAIL + AM_WAVES * (t_old - n_moved + i - n_first));  // handed over
@@ -531,18 +534,20 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     // The cache append of tail block tb (positions max(tb, pos0) .. min(tb + 32, t_end) - 1,
     // the bytes append_kv_token writes), made in the block's landed stage; the patched
     // block then goes back to the cache whole, in the 16-byte runs the loads read.
-    // The first four new rows are loaded before any block (ahead of the block loads in
-    // the memory pipeline); later ones when their block is patched.
+    // The wave holding the first tail block loads the first four new rows before any
+    // block (ahead of the block loads in the memory pipeline); other rows are loaded
+    // when their block is patched.
     const int first_new = max(t_begin, pos0);
+    const bool has_first = n_lead > 0 && (solo || wid == 0);
     KvNew pre[4];
-    if (DMA && wid == AM_TAIL && n_tail > 0)
+    if (DMA && has_first)
 #pragma unroll
         for (int j = 0; j < 4; j++) pre[j] = load_kv_token(a, seq, kvh, pos0, min(first_new + j, t_end - 1));
     auto patch_tail = [&](char* st, int tb) __attribute__((always_inline)) {
         const int lo = max(tb, pos0), hi = min(tb + 32, t_end);
         for (int t0 = lo; t0 < hi; t0 += 4) {
             KvNew nv[4];
-            if (t0 == first_new) {
+            if (has_first && t0 == first_new) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) nv[j] = pre[j];
             } else {
