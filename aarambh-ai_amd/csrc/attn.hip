@@ -484,7 +484,8 @@ __global__ void __launch_bounds__(512) attn_mfma_kernel(AttnArgs a) {
     constexpr int STEP = 32 * AM_WAVES;
     int tb = t_begin + 32 * wid;
     const int t_chunk_last = (t_end - 1) & ~31;
-    // the wave's own last block (re-reads hit L1), or the chunk's last one for a wave without blocks
+    // register-ring path: the wave's own last block (re-reads hit L1), or the chunk's last one
+    // for a wave without blocks
     const int t_last = tb <= t_chunk_last ? tb + (t_chunk_last - tb) / STEP * STEP : t_chunk_last;
 
     // INT8 blocks stream into two LDS stages per wave with direct loads (no VGPRs held
