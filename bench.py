@@ -16,8 +16,8 @@ same rounds with the reference CLI's sampler (T 0.7, top-k 50, top-p 0.9) in
 `per_batch_sampled_cli`.  The verify
 step (K = 4 rows at offset 4096, repeated) is timed separately with per-kernel
 HIP events at dispatch level: the INT4 GEMV gives `roofline` (batch 1, HBM), the
-decode attention `roofline_attention` (batch 1, HBM) and the many-row GEMM
-`roofline_gemm` (batch 32, MFMA).  Also measured: the standalone sampled
+decode attention `roofline_attention` (batch 1, HBM) and `roofline_attention_b32`
+(batch 32, HBM), and the many-row GEMM `roofline_gemm` (batch 32, MFMA).  Also measured: the standalone sampled
 acceptance kernel of config 2 (32 x 4 x 32000, T = 0.8, HBM) and the config-3
 INT8 verify step at batch 1 and 16 (HBM).  `cpu_baseline` times the CPU oracle
 (restated reference CPU path, f32) on all host cores on a 2-layer slice of the
@@ -725,6 +725,17 @@ def main():
         "avg_launch_us": round(a1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(a1["alg_bytes_per_step"] / C4["n_layers"]),
     }
+    roof_att32 = None
+    if 32 in res:
+        a32 = res[32]["attention"]
+        roof_att32 = {
+            "kernel": "attn_mfma_kernel<INT8> (decode attention of the batch-32 verify step, 4096-token INT8 cache)",
+            "bound": "hbm", "achieved": round(a32["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(a32["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("attention_traffic_bytes_per_launch", TRAFFIC_PROFILE_B32),
+            "avg_launch_us": round(a32["avg_us"], 3),
+            "avg_alg_bytes_per_launch": round(a32["alg_bytes_per_step"] / C4["n_layers"]),
+        }
     roof_gemm = None
     if 32 in res:
         gm = res[32]["int4_proj"]
@@ -771,6 +782,7 @@ def main():
                                                                "hbm_frac")} for b, r in res.items()},
         "roofline": roof,
         "roofline_attention": roof_att,
+        "roofline_attention_b32": roof_att32,
         "roofline_gemm": roof_gemm,
         "c2_acceptance": c2,
         "c3_verify": {str(b): {k: v[k] for k in ("ms_wall", "alg_bytes", "hbm_gbs", "hbm_frac")}
