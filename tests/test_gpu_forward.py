@@ -327,6 +327,44 @@ def test_hd128_long_context_chunk_merge(kvfmt):
     hip.close()
 
 
+def test_hd128_int8_tail_blocks_and_cache_write_back():
+    """The INT8 decode attention writes the new positions into its staged copy of each
+    block that holds them and stores the block back whole.  New rows ending a block,
+    straddling two blocks and starting one (offsets 28, 29, 31, 1021), then a 64-row
+    prompt chunk over three blocks (rows spread over the waves, sixteen query tiles
+    storing the same blocks), and a second forward after each that reads the first
+    one's rows back from the cache: logits and hidden within 2e-3 of the oracle."""
+    kw = dict(vocab_size=2048, hidden_dim=512, ffn_dim=1024, n_layers=2, n_heads=4, n_kv_heads=1,
+              max_seq_len=1200, weight_format=A.W_INT4_G128, kv_format=A.KV_INT8, lm_head_format=1)
+    ref, hip = make_pair(seed=21, max_batch=4, max_rows=64, **kw)
+    lens = [28, 29, 31, 1021]
+    kvs = []
+    for b, L in enumerate(lens):
+        hip.kv_fill_synthetic(b, L, seed=80 + b)
+        kv = ref.kv(1200)
+        kv.fill_synthetic(80 + b, L)
+        kvs.append(kv)
+    for step in range(2):
+        ids = R.synth_tokens(21, 3 + step, 16, 2048).reshape(4, 4)
+        pos = [L + 4 * step for L in lens]
+        gl, gh = hip.forward_with_cache_output(ids, pos)
+        for b in range(4):
+            wl, wh = kvs[b].forward(ids[b], pos[b], nthreads=16)
+            assert rel_rows(gl[b], wl).max() < TOL, (step, pos[b], rel_rows(gl[b], wl).max())
+            assert rel_rows(gh[b], wh).max() < TOL, (step, pos[b], rel_rows(gh[b], wh).max())
+    # a 64-row prompt chunk at offset 20 (positions 20 .. 83: three blocks), then 4 rows at 84
+    hip.kv_fill_synthetic(0, 20, seed=90)
+    kv = ref.kv(1200)
+    kv.fill_synthetic(90, 20)
+    for S, L in ((64, 20), (4, 84)):
+        ids = R.synth_tokens(22, S, S, 2048).reshape(1, S)
+        gl, gh = hip.forward_with_cache_output(ids, [L], slots=[0])
+        wl, wh = kv.forward(ids[0], L, nthreads=16)
+        assert rel_rows(gl[0], wl).max() < TOL, (S, L, rel_rows(gl[0], wl).max())
+        assert rel_rows(gh[0], wh).max() < TOL, (S, L, rel_rows(gh[0], wh).max())
+    hip.close()
+
+
 @pytest.mark.parametrize("group", [128, 256, 512])
 def test_packed_int4_tensor_loads(group):
     """PackedInt4Tensor as the quant crate holds it (f32 scales / zeros, group_size):
