@@ -146,6 +146,35 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
         }
         __syncthreads();
     };
+    // K <= 4096 (one round of partials per lane), outside the K-split mode (whose
+    // registers are spoken for): the partials are loaded before the K loop and summed
+    // after it, so their round trip and the barrier stay off the loop's start (1/rms is
+    // needed only by the epilogue)
+    constexpr int RPW_INV = KS ? 1 : MC * 16 / GM_WAVES;
+    float inv_v[RPW_INV][4];
+    auto inv_load = [&]() {
+        const int nq = a.K >> 4;
+#pragma unroll
+        for (int k = 0; k < RPW_INV; k++) {
+            const int m = min(mb * MC * 16 + wid + GM_WAVES * k, a.M - 1);
+#pragma unroll
+            for (int u = 0; u < 4; u++) inv_v[k][u] = a.ssq_in[(size_t)m * a.ssq_ld + min(lane + 64 * u, nq - 1)];
+        }
+    };
+    auto inv_finish = [&]() {
+        const int nq = a.K >> 4;
+#pragma unroll
+        for (int k = 0; k < RPW_INV; k++) {
+            float t = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (lane + 64 * u < nq) t += inv_v[k][u];
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+            if (lane == 0) s_inv[wid + GM_WAVES * k] = 1.0f / sqrtf(t / (float)a.K + a.eps);
+        }
+        __syncthreads();
+    };
     if (EPI == EPI_STORE && a.hidden_out) {
         // final normed hidden state (model.rs:579-585): the NB * S blocks of this
         // M-block each write a slice of columns of its rows
@@ -339,7 +368,9 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     // the epilogue's 1/rms while the first stages are in flight (loads complete in
     // order, so its wait also covers those stages: the loop's first wait is then free)
     const bool norm_rows = a.norm_w && !(EPI == EPI_STORE && a.hidden_out);
-    if (norm_rows) compute_inv();
+    const bool inv_late = !KS && norm_rows && a.K <= 4096;
+    if (inv_late) inv_load();
+    else if (norm_rows) compute_inv();
     // rows and tiles of this wave's epilogue; QKV positions loaded up front
     const int row0 = (mb * MC + wm * CPW) * 16, tile0 = nb * NT + wn * TPW;
     int mrw[CPW][4];  // activation row, clamped into range
@@ -447,6 +478,7 @@ __global__ void __launch_bounds__(GM_WAVES * 64) gemm_kernel(GemvArgs a, int S, 
     }
     wait_vmcnt<0>();
     __syncthreads();  // every wave's stage loads have landed: the ring is free for the epilogue
+    if (inv_late) inv_finish();
 
     // ---- epilogue inputs that do not depend on this kernel's products: loaded in the
     //      same round trip as the split-K partials (after the arrival, which waits for
