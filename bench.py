@@ -577,10 +577,11 @@ def summarize_trace(path, title, cmd):
     """Text summary of a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv) for profiles/:
     per-kernel calls / total / mean / min / max, the verify-path kernels by workgroup
     count, and the mean duration of the INT4 GEMV launches (gemv_tile_kernel<3, ...>) as
-    `int4_gemv_avg_launch_us`, and of the 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>
+    `int4_gemv_avg_launch_us`, of the 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *>
     outside the K-split mode: the 1 x 8 wave shape with two 16-row chunks per wave, which the
-    C4 plan table uses above 64 rows only) as `int4_gemm128_avg_launch_us`; bench.py quotes
-    both beside its own dispatch-timed figures."""
+    C4 plan table uses above 64 rows only) as `int4_gemm128_avg_launch_us`, and of the
+    INT8-cache decode attention as `attention_avg_launch_us`; bench.py quotes them beside
+    its own dispatch-timed figures."""
     import csv
     rows = list(csv.DictReader(open(path)))
     col = {k.lower(): k for k in rows[0].keys()} if rows else {}
@@ -617,6 +618,11 @@ def summarize_trace(path, title, cmd):
         n, t = sum(x[0] for x in g), sum(x[1] for x in g)
         out += ["", f"# 128-row INT4 GEMM launches (gemm_kernel<3, *, 1, 2, *, false>): {n} dispatches, {t / 1e3:.3f} ms, "
                     f"mean {t / n:.3f} us", f"int4_gemm128_avg_launch_us = {t / n:.3f}"]
+    g = [(n, t) for name, (n, t, _, _) in stats.items() if name.startswith("void aarh::attn_mfma_kernel<2,")]
+    if g:
+        n, t = sum(x[0] for x in g), sum(x[1] for x in g)
+        out += ["", f"# INT8-cache decode attention launches (attn_mfma_kernel<2, ...>): {n} dispatches, "
+                    f"{t / 1e3:.3f} ms, mean {t / n:.3f} us", f"attention_avg_launch_us = {t / n:.3f}"]
     hot = [n for n in byname_wg if any(k in n for k in ("gemv_tile", "gemm_kernel", "attn", "accept", "candidates"))]
     if hot:
         out += ["", "# verify-path kernels: workgroups per launch"]
@@ -725,6 +731,17 @@ def main():
         "avg_launch_us": round(a1["avg_us"], 3),
         "avg_alg_bytes_per_launch": round(a1["alg_bytes_per_step"] / C4["n_layers"]),
     }
+    def att_profile(a, path):
+        """The same launches' mean duration in a committed rocprofv3 kernel trace summary."""
+        us = measured_traffic("attention_avg_launch_us", path)
+        if not us:
+            return None
+        gbs = a["alg_bytes_per_step"] / C4["n_layers"] / (us * 1e-6) / 1e9
+        return {"file": os.path.relpath(path, ROOT), "avg_launch_us": us, "achieved": round(gbs, 1),
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    prof = att_profile(a1, STATS_PROFILE)
+    if prof:
+        roof_att["profile"] = prof
     roof_att32 = None
     if 32 in res:
         a32 = res[32]["attention"]
@@ -736,6 +753,9 @@ def main():
             "avg_launch_us": round(a32["avg_us"], 3),
             "avg_alg_bytes_per_launch": round(a32["alg_bytes_per_step"] / C4["n_layers"]),
         }
+        prof = att_profile(a32, STATS_PROFILE_B32)
+        if prof:
+            roof_att32["profile"] = prof
     roof_gemm = None
     if 32 in res:
         gm = res[32]["int4_proj"]
